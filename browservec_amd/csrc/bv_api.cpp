@@ -1,0 +1,950 @@
+// Host runtime behind include/browservec_hip.h: device handles, index objects
+// holding their rows/codes in HBM, and the query pipelines that chain the
+// gfx950 kernels on one HIP stream per index.
+#include "../../include/browservec_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "bv_kernels.h"
+
+using namespace bvk;
+
+// ------------------------------------------------------------------ errors
+static thread_local std::string g_err;
+
+static int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+struct bv_device {
+    int ordinal = 0;
+    hipDeviceProp_t prop{};
+    bool lost = false;
+};
+
+static int hip_fail(bv_device *dev, hipError_t e, const char *what) {
+    if (e == hipErrorOutOfMemory) return fail(BV_E_OOM, "%s: out of device memory", what);
+    if (dev && (e == hipErrorIllegalAddress || e == hipErrorLaunchFailure || e == hipErrorECCNotCorrectable ||
+                e == hipErrorNoDevice))
+        dev->lost = true;
+    return fail(BV_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIPX(dev, expr, what)                        \
+    do {                                             \
+        hipError_t _e = (expr);                      \
+        if (_e != hipSuccess) return hip_fail((dev), _e, (what)); \
+    } while (0)
+
+// -------------------------------------------------------- device buffers
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+    // Grow to at least `bytes`, preserving the first `keep` bytes.
+    hipError_t ensure(size_t bytes, size_t keep, hipStream_t s, bool geometric = true) {
+        if (bytes <= cap) return hipSuccess;
+        size_t ncap = geometric ? std::max(bytes, cap + cap / 2) : bytes;
+        ncap = (ncap + 255) & ~size_t(255);
+        void *np = nullptr;
+        hipError_t e = hipMalloc(&np, ncap);
+        if (e != hipSuccess) return e;
+        if (p && keep) {
+            e = hipMemcpyAsync(np, p, keep, hipMemcpyDeviceToDevice, s);
+            if (e == hipSuccess) e = hipStreamSynchronize(s);
+            if (e != hipSuccess) {
+                (void)hipFree(np);
+                return e;
+            }
+        }
+        if (p) (void)hipFree(p);
+        p = np;
+        cap = ncap;
+        return hipSuccess;
+    }
+    template <class T> T *as() const { return (T *)p; }
+};
+
+struct HostBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    ~HostBuf() {
+        if (p) (void)hipHostFree(p);
+    }
+    hipError_t ensure(size_t bytes) {
+        if (bytes <= cap) return hipSuccess;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        size_t ncap = std::max(bytes, cap * 2);
+        hipError_t e = hipHostMalloc(&p, ncap, hipHostMallocDefault);
+        if (e != hipSuccess) {
+            cap = 0;
+            return e;
+        }
+        cap = ncap;
+        return hipSuccess;
+    }
+};
+
+// ------------------------------------------------------------------ index
+struct bv_index {
+    bv_device *dev = nullptr;
+    bv_index_desc d{};
+    uint32_t dim = 0, P = 0, words_per_row = 0, row_bytes = 0, units = 0;
+    int codec = -1;
+    bool quant = false;
+    uint64_t rows = 0;
+    hipStream_t stream = nullptr;
+
+    DevBuf raw;      // N x dim fp32 rows (flat corpus; quantized kinds: re-rank source)
+    DevBuf codes;    // N x row_bytes
+    DevBuf scales;   // N floats
+    DevBuf signs;    // rounds x P (+64 slack)
+    DevBuf slow;     // 1-bit sequential-sum counter
+
+    // per-call scratch
+    DevBuf qin, qrot, qscan, qscale, mask;
+    DevBuf partials, tickets, merged, merged_n;
+    DevBuf rr_scores, rr_rows, rr_tickets;
+    DevBuf out_rows, out_scores, out_n;
+    DevBuf cand, cand_n, dense;
+    HostBuf h_rows, h_scores, h_n;
+
+    uint32_t nprobe_override = 0;
+    double last_query_ms = 0, last_query_gpu_ms = 0;
+    uint64_t last_scanned = 0;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+
+    // kernel timing
+    bool timing = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> tev;
+    size_t tev_used = 0;
+    double scan_ms = 0;
+    uint64_t scan_launches = 0;
+};
+
+extern "C" const char *bv_last_error(void) { return g_err.c_str(); }
+extern "C" int bv_abi_version(void) { return BV_ABI_VERSION; }
+
+// ------------------------------------------------------------------ device
+extern "C" int bv_device_open(int ordinal, bv_device **out) {
+    if (!out) return fail(BV_E_INVALID, "out is null");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(BV_E_UNSUPPORTED, "no HIP device available");
+    if (ordinal < 0 || ordinal >= n) return fail(BV_E_INVALID, "device ordinal %d out of range (%d devices)", ordinal, n);
+    bv_device *d = new bv_device();
+    d->ordinal = ordinal;
+    e = hipSetDevice(ordinal);
+    if (e == hipSuccess) e = hipGetDeviceProperties(&d->prop, ordinal);
+    if (e != hipSuccess) {
+        delete d;
+        return fail(BV_E_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    }
+    *out = d;
+    return BV_OK;
+}
+
+extern "C" int bv_device_close(bv_device *dev) {
+    delete dev;
+    return BV_OK;
+}
+
+extern "C" int bv_device_is_lost(const bv_device *dev, int *lost) {
+    if (!dev || !lost) return fail(BV_E_INVALID, "null argument");
+    *lost = dev->lost ? 1 : 0;
+    return BV_OK;
+}
+
+extern "C" int bv_device_info(const bv_device *dev, char *name, uint32_t name_len, uint32_t *cu_count,
+                              uint64_t *hbm_bytes) {
+    if (!dev) return fail(BV_E_INVALID, "null device");
+    if (name && name_len) {
+        snprintf(name, name_len, "%s (%s)", dev->prop.name, dev->prop.gcnArchName);
+    }
+    if (cu_count) *cu_count = (uint32_t)dev->prop.multiProcessorCount;
+    if (hbm_bytes) *hbm_bytes = (uint64_t)dev->prop.totalGlobalMem;
+    return BV_OK;
+}
+
+// ------------------------------------------------------------------- index
+static uint32_t pad_to_pow2(uint32_t n) {
+    uint32_t p = 4;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+// mulberry32 / randomSigns / Rotator signs (src/quant/prng.ts:5-22,
+// src/quant/rotator.ts:44-58): computed once on the host per index.
+static uint32_t mb32_next(uint32_t &a) {
+    uint32_t s = a + 0x6d2b79f5u;
+    a = s;
+    uint32_t t = (s ^ (s >> 15)) * (1u | s);
+    t = (t + (t ^ (t >> 7)) * (61u | t)) ^ t;
+    return t ^ (t >> 14);
+}
+
+static void rotator_signs(uint32_t dim, uint32_t seed, uint32_t rounds, std::vector<float> &out) {
+    const uint32_t P = pad_to_pow2(dim);
+    out.assign((size_t)rounds * P + 64, 0.0f);
+    const double inv = 1.0 / std::sqrt((double)P);
+    for (uint32_t r = 0; r < rounds; r++) {
+        uint32_t a = seed ^ (uint32_t)(0x9e3779b9ull * (uint64_t)(r + 1));
+        for (uint32_t i = 0; i < P; i++) {
+            const double draw = (double)mb32_next(a) / 4294967296.0;
+            const double sgn = draw < 0.5 ? -1.0 : 1.0;
+            out[(size_t)r * P + i] = (float)(sgn * inv);
+        }
+    }
+}
+
+extern "C" int bv_index_create(bv_device *dev, const bv_index_desc *desc, bv_index **out) {
+    if (!dev || !desc || !out) return fail(BV_E_INVALID, "null argument");
+    if (desc->size < sizeof(bv_index_desc)) return fail(BV_E_INVALID, "bv_index_desc.size too small");
+    if (dev->lost) return fail(BV_E_DEVICE_LOST, "GPU device lost; re-create the store");
+    bv_index_desc d = *desc;
+    if (d.dim == 0) return fail(BV_E_INVALID, "dimension must be a positive integer, got %u", d.dim);
+    if (d.metric > BV_METRIC_L2) return fail(BV_E_INVALID, "unknown metric %u", d.metric);
+    if (d.kind > BV_KIND_IVFQUANT) return fail(BV_E_INVALID, "unknown index kind %u", d.kind);
+    const bool quant = d.kind == BV_KIND_QUANT || d.kind == BV_KIND_IVFQUANT;
+    if (d.bits != 0 && d.bits != 1 && d.bits != 4 && d.bits != 8)
+        return fail(BV_E_UNSUPPORTED, "quantBits %u not supported (ships 0, 1, 4, 8)", d.bits);
+    if (quant && d.bits == 0) return fail(BV_E_INVALID, "quantized index kinds need bits 1, 4 or 8");
+    if (!quant && d.bits != 0) return fail(BV_E_INVALID, "fp32 index kinds need bits 0");
+    // buildIndex's rejections (src/index.ts:124-141)
+    if ((d.kind == BV_KIND_IVF || d.kind == BV_KIND_IVFQUANT) && d.metric == BV_METRIC_L2)
+        return fail(BV_E_UNSUPPORTED, "IVF supports metric cosine/dot only (l2 is later work)");
+    if (d.kind == BV_KIND_QUANT && d.metric == BV_METRIC_L2)
+        return fail(BV_E_UNSUPPORTED,
+                    "quantized mode supports metric cosine/dot only (l2 quantization is later work)");
+    if (d.kind == BV_KIND_IVF || d.kind == BV_KIND_IVFQUANT)
+        return fail(BV_E_UNSUPPORTED, "IVF index kinds are not available in this build yet");
+    if (d.scorer == BV_SCORER_HAMMING && d.bits != 1)
+        return fail(BV_E_UNSUPPORTED, "the Hamming scorer needs 1-bit codes");
+    if (d.scorer == BV_SCORER_INT8SYM && d.bits != 8)
+        return fail(BV_E_UNSUPPORTED, "the int8 symmetric scorer needs int8 codes");
+    if (d.scorer > BV_SCORER_INT8SYM) return fail(BV_E_INVALID, "unknown scorer %u", d.scorer);
+    if (!d.has_seed) d.seed = 0x9e3779b9u;
+    if (d.rounds == 0) d.rounds = 2;
+
+    bv_index *x = new bv_index();
+    x->dev = dev;
+    x->d = d;
+    x->dim = d.dim;
+    x->quant = quant;
+    if (quant) {
+        x->P = pad_to_pow2(d.dim);
+        if (x->P > 4096) {
+            delete x;
+            return fail(BV_E_UNSUPPORTED, "quantized dimension %u (padded %u) exceeds 4096", d.dim, pad_to_pow2(d.dim));
+        }
+        const uint32_t per = d.bits == 8 ? 4 : d.bits == 4 ? 8 : 32;
+        x->words_per_row = x->P / per;
+        x->row_bytes = x->words_per_row * 4;
+        if (d.bits == 8) x->codec = d.scorer == BV_SCORER_INT8SYM ? C_I8S : C_Q8;
+        else if (d.bits == 4) x->codec = C_Q4;
+        else x->codec = d.scorer == BV_SCORER_HAMMING ? C_HAM : C_Q1A;
+        x->units = x->codec == C_Q1A ? x->row_bytes / 4 : x->row_bytes / 16;
+        if (x->row_bytes < 16 && x->codec != C_Q1A) {
+            delete x;
+            return fail(BV_E_UNSUPPORTED, "dimension %u too small for this code layout", d.dim);
+        }
+    } else {
+        x->P = d.dim;
+        x->row_bytes = d.dim * 4;
+        const bool l2 = d.metric == BV_METRIC_L2;
+        if (d.dim % 4 == 0) {
+            x->codec = l2 ? C_F32L2 : C_F32DOT;
+            x->units = d.dim / 4;
+        } else {
+            x->codec = l2 ? C_F32L2_S : C_F32DOT_S;
+            x->units = d.dim;
+        }
+    }
+    if (!scan_supported(x->codec, x->units)) {
+        int c = x->codec;
+        delete x;
+        return fail(BV_E_UNSUPPORTED, "dimension %u not supported by the scan kernels (codec %d)", d.dim, c);
+    }
+    hipError_t e = hipSetDevice(dev->ordinal);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreate(&x->ev0);
+    if (e == hipSuccess) e = hipEventCreate(&x->ev1);
+    if (e == hipSuccess && quant) {
+        std::vector<float> s;
+        rotator_signs(d.dim, d.seed, d.rounds, s);
+        e = x->signs.ensure(s.size() * 4, 0, x->stream, false);
+        if (e == hipSuccess) e = hipMemcpy(x->signs.p, s.data(), s.size() * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = x->slow.ensure(256, 0, x->stream, false);
+        if (e == hipSuccess) e = hipMemset(x->slow.p, 0, 256);
+    }
+    if (e != hipSuccess) {
+        int rc = hip_fail(dev, e, "bv_index_create");
+        delete x;
+        return rc;
+    }
+    *out = x;
+    return BV_OK;
+}
+
+extern "C" int bv_index_destroy(bv_index *idx) {
+    if (!idx) return BV_OK;
+    (void)hipSetDevice(idx->dev->ordinal);
+    if (idx->stream) (void)hipStreamSynchronize(idx->stream);
+    for (auto &pr : idx->tev) {
+        (void)hipEventDestroy(pr.first);
+        (void)hipEventDestroy(pr.second);
+    }
+    if (idx->ev0) (void)hipEventDestroy(idx->ev0);
+    if (idx->ev1) (void)hipEventDestroy(idx->ev1);
+    if (idx->stream) (void)hipStreamDestroy(idx->stream);
+    delete idx;
+    return BV_OK;
+}
+
+extern "C" int bv_index_size(const bv_index *idx, uint64_t *rows) {
+    if (!idx || !rows) return fail(BV_E_INVALID, "null argument");
+    *rows = idx->rows;
+    return BV_OK;
+}
+
+static int check_live(bv_index *idx) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    if (idx->dev->lost) return fail(BV_E_DEVICE_LOST, "GPU device lost; re-create the store");
+    hipError_t e = hipSetDevice(idx->dev->ordinal);
+    if (e != hipSuccess) return hip_fail(idx->dev, e, "hipSetDevice");
+    return BV_OK;
+}
+
+// Rotate+quantize rows [first, first+count) from the device row buffer.
+static int encode_range(bv_index *idx, uint64_t first, uint64_t count) {
+    EncodeArgs a{};
+    a.src = idx->raw.as<float>() + first * idx->dim;
+    a.rows = count;
+    a.dim = idx->dim;
+    a.P = idx->P;
+    a.signs = idx->signs.as<float>();
+    a.rounds = idx->d.rounds;
+    a.bits = idx->d.bits;
+    a.codes = idx->codes.as<uint32_t>() + first * idx->words_per_row;
+    a.scales = idx->scales.as<float>() + first;
+    a.slow_rows = idx->slow.as<uint32_t>();
+    HIPX(idx->dev, launch_encode(a, idx->stream), "encode kernel");
+    return BV_OK;
+}
+
+static int append_common(bv_index *idx, const float *data, bool device_src, uint64_t count) {
+    const uint64_t base = idx->rows, total = base + count;
+    const size_t rb = (size_t)idx->dim * 4;
+    HIPX(idx->dev, idx->raw.ensure(total * rb, base * rb, idx->stream), "row buffer");
+    HIPX(idx->dev,
+         hipMemcpyAsync(idx->raw.as<char>() + base * rb, data, count * rb,
+                        device_src ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, idx->stream),
+         "row upload");
+    if (idx->quant) {
+        HIPX(idx->dev, idx->codes.ensure(total * idx->row_bytes, base * idx->row_bytes, idx->stream), "code buffer");
+        HIPX(idx->dev, idx->scales.ensure(total * 4, base * 4, idx->stream), "scale buffer");
+        int rc = encode_range(idx, base, count);
+        if (rc) return rc;
+    }
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "append");
+    idx->rows = total;
+    return BV_OK;
+}
+
+extern "C" int bv_index_append(bv_index *idx, const float *data, uint64_t n_floats, uint64_t count) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (n_floats != count * idx->dim)
+        return fail(BV_E_INVALID, "expected %llu floats, got %llu", (unsigned long long)(count * idx->dim),
+                    (unsigned long long)n_floats);
+    if (count == 0) return BV_OK;
+    if (!data) return fail(BV_E_INVALID, "data is null");
+    if (idx->rows + count > 0xfffffffeull) return fail(BV_E_INVALID, "row count exceeds 2^32-2");
+    return append_common(idx, data, false, count);
+}
+
+extern "C" int bv_index_append_device(bv_index *idx, const float *d_data, uint64_t count) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (count == 0) return BV_OK;
+    if (!d_data) return fail(BV_E_INVALID, "data is null");
+    if (idx->rows + count > 0xfffffffeull) return fail(BV_E_INVALID, "row count exceeds 2^32-2");
+    return append_common(idx, d_data, true, count);
+}
+
+// ---------------------------------------------------------------- queries
+static uint32_t grid_for(uint64_t n, uint32_t *rows_per_wg) {
+    uint64_t g = (n + 255) / 256;
+    if (g < 1) g = 1;
+    if (g > (uint64_t)MAX_GRID) g = MAX_GRID;
+    uint64_t rpw = (n + g - 1) / g;
+    if (rpw < 1) rpw = 1;
+    g = (n + rpw - 1) / rpw;
+    if (g < 1) g = 1;
+    *rows_per_wg = (uint32_t)rpw;
+    return (uint32_t)g;
+}
+
+// Query transform for the scan: device-resident queries d_q (nq x dim) ->
+// qscan (per-codec layout), and for quantized kinds qrot (nq x P).
+static int prepare_queries(bv_index *idx, const float *d_q, uint32_t nq, const void **qscan, uint64_t *qstride) {
+    if (!idx->quant) {
+        *qscan = d_q;
+        *qstride = (uint64_t)idx->dim * 4;
+        return BV_OK;
+    }
+    const uint32_t P = idx->P;
+    HIPX(idx->dev, idx->qrot.ensure((size_t)nq * P * 4, 0, idx->stream), "query buffer");
+    EncodeArgs a{};
+    a.src = d_q;
+    a.rows = nq;
+    a.dim = idx->dim;
+    a.P = P;
+    a.signs = idx->signs.as<float>();
+    a.rounds = idx->d.rounds;
+    a.rotated = idx->qrot.as<float>();
+    switch (idx->codec) {
+    case C_Q8:
+        HIPX(idx->dev, idx->qscan.ensure((size_t)nq * P * 4, 0, idx->stream), "query buffer");
+        a.qdiv = idx->qscan.as<float>();
+        *qscan = idx->qscan.p;
+        *qstride = (uint64_t)P * 4;
+        break;
+    case C_Q4:
+    case C_Q1A:
+        *qscan = idx->qrot.p;
+        *qstride = (uint64_t)P * 4;
+        break;
+    case C_HAM:
+    case C_I8S: {
+        const uint32_t per = idx->codec == C_HAM ? 32 : 4;
+        const uint32_t W = P / per;
+        HIPX(idx->dev, idx->qscan.ensure((size_t)nq * W * 4, 0, idx->stream), "query buffer");
+        HIPX(idx->dev, idx->qscale.ensure((size_t)nq * 4, 0, idx->stream), "query buffer");
+        a.bits = idx->codec == C_HAM ? 1 : 8;
+        a.codes = idx->qscan.as<uint32_t>();
+        a.scales = idx->qscale.as<float>();  // the query's own scale is not used by integer scorers
+        *qscan = idx->qscan.p;
+        *qstride = (uint64_t)W * 4;
+        break;
+    }
+    default:
+        return fail(BV_E_STATE, "bad codec");
+    }
+    HIPX(idx->dev, launch_encode(a, idx->stream), "query rotate kernel");
+    return BV_OK;
+}
+
+static void timing_begin(bv_index *idx) {
+    if (!idx->timing) return;
+    if (idx->tev_used == idx->tev.size()) {
+        hipEvent_t a, b;
+        if (hipEventCreate(&a) != hipSuccess) return;
+        if (hipEventCreate(&b) != hipSuccess) return;
+        idx->tev.push_back({a, b});
+    }
+    (void)hipEventRecord(idx->tev[idx->tev_used].first, idx->stream);
+}
+static void timing_end(bv_index *idx) {
+    if (!idx->timing || idx->tev_used >= idx->tev.size()) return;
+    (void)hipEventRecord(idx->tev[idx->tev_used].second, idx->stream);
+    idx->tev_used++;
+}
+static void timing_collect(bv_index *idx) {
+    if (idx->tev_used == 0) return;
+    (void)hipStreamSynchronize(idx->stream);
+    for (size_t i = 0; i < idx->tev_used; i++) {
+        float ms = 0;
+        if (hipEventElapsedTime(&ms, idx->tev[i].first, idx->tev[i].second) == hipSuccess) idx->scan_ms += ms;
+        idx->scan_launches++;
+    }
+    idx->tev_used = 0;
+}
+
+// The device pipeline shared by every query entry point.
+//   d_q       : nq x dim device queries (original space)
+//   kprime    : candidates kept by the scan (the fetch)
+//   k_out     : results per query
+//   rerank    : re-rank the kprime candidates with f64 dotRow
+//   outputs   : device arrays [nq][k_out], [nq]
+static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
+                        const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores,
+                        uint32_t *d_n) {
+    const void *qscan = nullptr;
+    uint64_t qstride = 0;
+    int rc = prepare_queries(idx, d_q, nq, &qscan, &qstride);
+    if (rc) return rc;
+    uint32_t rpw = 0;
+    const uint64_t n = idx->rows;
+    const uint32_t grid = grid_for(n, &rpw);
+    HIPX(idx->dev, idx->partials.ensure((size_t)nq * grid * kprime * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
+    {
+        const size_t old = idx->tickets.cap;
+        HIPX(idx->dev, idx->tickets.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
+        if (idx->tickets.cap != old)
+            HIPX(idx->dev, hipMemsetAsync(idx->tickets.p, 0, idx->tickets.cap, idx->stream), "scratch");
+    }
+    ScanArgs a{};
+    a.codes = idx->quant ? idx->codes.p : idx->raw.p;
+    a.row_bytes = idx->row_bytes;
+    a.units = idx->units;
+    a.padded_dim = idx->P;
+    a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A) ? idx->scales.as<float>() : nullptr;
+    a.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
+    a.q = qscan;
+    a.q_stride = qstride;
+    a.mask = d_mask;
+    a.mask_bits = mask_bits;
+    a.n = n;
+    a.kprime = kprime;
+    a.rows_per_wg = rpw;
+    a.grid = grid;
+    a.partials = idx->partials.as<uint64_t>();
+    a.tickets = idx->tickets.as<uint32_t>();
+    a.merged = idx->merged.as<uint64_t>();
+    a.merged_n = idx->merged_n.as<uint32_t>();
+    if (!rerank) {
+        a.k_out = k_out;
+        a.out_rows = d_rows;
+        a.out_scores = d_scores;
+        a.out_n = d_n;
+    }
+    timing_begin(idx);
+    HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, idx->stream), "scan kernel");
+    timing_end(idx);
+    idx->last_scanned = n * nq;
+    if (rerank) {
+        HIPX(idx->dev, idx->rr_scores.ensure((size_t)nq * kprime * 4, 0, idx->stream), "scratch");
+        HIPX(idx->dev, idx->rr_rows.ensure((size_t)nq * kprime * 4, 0, idx->stream), "scratch");
+        const size_t old = idx->rr_tickets.cap;
+        HIPX(idx->dev, idx->rr_tickets.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
+        if (idx->rr_tickets.cap != old)
+            HIPX(idx->dev, hipMemsetAsync(idx->rr_tickets.p, 0, idx->rr_tickets.cap, idx->stream), "scratch");
+        RerankArgs r{};
+        r.rows = idx->raw.as<float>();
+        r.dim = idx->dim;
+        r.q = d_q;
+        r.q_stride = idx->dim;
+        r.merged = idx->merged.as<uint64_t>();
+        r.merged_n = idx->merged_n.as<uint32_t>();
+        r.kprime = kprime;
+        r.k_out = k_out;
+        r.rr_scores = idx->rr_scores.as<float>();
+        r.rr_rows = idx->rr_rows.as<uint32_t>();
+        r.tickets = idx->rr_tickets.as<uint32_t>();
+        r.out_rows = d_rows;
+        r.out_scores = d_scores;
+        r.out_n = d_n;
+        HIPX(idx->dev, launch_rerank(r, nq, idx->stream), "rerank kernel");
+    }
+    return BV_OK;
+}
+
+// Host entry: upload queries (+mask), run, download.
+static int host_query(bv_index *idx, const float *q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
+                      const uint32_t *mask, uint64_t mask_words, uint32_t *rows, float *scores, uint32_t *n_out) {
+    auto t0 = std::chrono::steady_clock::now();
+    if (idx->rows == 0 || k_out == 0) {
+        for (uint32_t i = 0; i < nq; i++) n_out[i] = 0;
+        idx->last_query_ms = 0;
+        idx->last_query_gpu_ms = 0;
+        return BV_OK;
+    }
+    const size_t qbytes = (size_t)nq * idx->dim * 4;
+    HIPX(idx->dev, idx->qin.ensure(qbytes, 0, idx->stream), "query buffer");
+    HIPX(idx->dev, hipEventRecord(idx->ev0, idx->stream), "event");
+    HIPX(idx->dev, hipMemcpyAsync(idx->qin.p, q, qbytes, hipMemcpyHostToDevice, idx->stream), "query upload");
+    const uint32_t *d_mask = nullptr;
+    uint64_t mask_bits = 0;
+    if (mask) {
+        HIPX(idx->dev, idx->mask.ensure(mask_words * 4, 0, idx->stream), "mask buffer");
+        HIPX(idx->dev, hipMemcpyAsync(idx->mask.p, mask, mask_words * 4, hipMemcpyHostToDevice, idx->stream),
+             "mask upload");
+        d_mask = idx->mask.as<uint32_t>();
+        mask_bits = mask_words * 32;
+    }
+    HIPX(idx->dev, idx->out_rows.ensure((size_t)nq * k_out * 4, 0, idx->stream), "output buffer");
+    HIPX(idx->dev, idx->out_scores.ensure((size_t)nq * k_out * 4, 0, idx->stream), "output buffer");
+    HIPX(idx->dev, idx->out_n.ensure((size_t)nq * 4, 0, idx->stream), "output buffer");
+    int rc = run_pipeline(idx, idx->qin.as<float>(), nq, kprime, k_out, rerank, d_mask, mask_bits,
+                          idx->out_rows.as<uint32_t>(), idx->out_scores.as<float>(), idx->out_n.as<uint32_t>());
+    if (rc) return rc;
+    HIPX(idx->dev, idx->h_rows.ensure((size_t)nq * k_out * 4), "pinned buffer");
+    HIPX(idx->dev, idx->h_scores.ensure((size_t)nq * k_out * 4), "pinned buffer");
+    HIPX(idx->dev, idx->h_n.ensure((size_t)nq * 4), "pinned buffer");
+    HIPX(idx->dev, hipMemcpyAsync(idx->h_rows.p, idx->out_rows.p, (size_t)nq * k_out * 4, hipMemcpyDeviceToHost,
+                                  idx->stream), "result download");
+    HIPX(idx->dev, hipMemcpyAsync(idx->h_scores.p, idx->out_scores.p, (size_t)nq * k_out * 4,
+                                  hipMemcpyDeviceToHost, idx->stream), "result download");
+    HIPX(idx->dev, hipMemcpyAsync(idx->h_n.p, idx->out_n.p, (size_t)nq * 4, hipMemcpyDeviceToHost, idx->stream),
+         "result download");
+    HIPX(idx->dev, hipEventRecord(idx->ev1, idx->stream), "event");
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "query");
+    timing_collect(idx);
+    float gms = 0;
+    (void)hipEventElapsedTime(&gms, idx->ev0, idx->ev1);
+    std::memcpy(rows, idx->h_rows.p, (size_t)nq * k_out * 4);
+    std::memcpy(scores, idx->h_scores.p, (size_t)nq * k_out * 4);
+    std::memcpy(n_out, idx->h_n.p, (size_t)nq * 4);
+    idx->last_query_gpu_ms = gms;
+    idx->last_query_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return BV_OK;
+}
+
+// Dense-score fallback for fetches beyond the fused top-k's capacity.
+static int host_query_dense(bv_index *idx, const float *q, uint32_t nq, uint32_t k, const uint32_t *mask,
+                            uint64_t mask_words, uint32_t *rows, float *scores, uint32_t *n_out);
+
+extern "C" int bv_index_query(bv_index *idx, const float *q, uint32_t k, uint32_t *rows, float *scores,
+                              uint32_t *n_out) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!q || !n_out || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
+    const uint32_t kk = (uint32_t)std::min<uint64_t>(k, idx->rows);
+    if (kk > (uint32_t)MAX_KPRIME) return host_query_dense(idx, q, 1, k, nullptr, 0, rows, scores, n_out);
+    return host_query(idx, q, 1, kk, kk, false, nullptr, 0, rows, scores, n_out);
+}
+
+extern "C" int bv_index_query_masked(bv_index *idx, const float *q, uint32_t k, const uint32_t *mask_words,
+                                     uint64_t n_words, uint32_t *rows, float *scores, uint32_t *n_out) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!q || !n_out || !mask_words || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
+    const uint64_t need = (idx->rows + 31) / 32;
+    if (n_words < need)
+        return fail(BV_E_INVALID, "mask has %llu words, need %llu for %llu rows", (unsigned long long)n_words,
+                    (unsigned long long)need, (unsigned long long)idx->rows);
+    const uint32_t kk = (uint32_t)std::min<uint64_t>(k, idx->rows);
+    if (kk > (uint32_t)MAX_KPRIME) return host_query_dense(idx, q, 1, k, mask_words, n_words, rows, scores, n_out);
+    return host_query(idx, q, 1, kk, kk, false, mask_words, n_words, rows, scores, n_out);
+}
+
+extern "C" int bv_index_query_batch(bv_index *idx, const float *queries, uint32_t nq, uint32_t k, uint32_t *rows,
+                                    float *scores, uint32_t *n_out) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (nq == 0) return BV_OK;
+    if (!queries || !n_out || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
+    const uint32_t kk = (uint32_t)std::min<uint64_t>(k, idx->rows);
+    if (kk > (uint32_t)MAX_KPRIME) {
+        std::vector<uint32_t> r(kk);
+        std::vector<float> s(kk);
+        for (uint32_t i = 0; i < nq; i++) {
+            rc = host_query_dense(idx, queries + (size_t)i * idx->dim, 1, k, nullptr, 0, rows + (size_t)i * k,
+                                  scores + (size_t)i * k, n_out + i);
+            if (rc) return rc;
+        }
+        return BV_OK;
+    }
+    // chunk to bound scratch
+    const uint32_t chunk = 64;
+    for (uint32_t s0 = 0; s0 < nq; s0 += chunk) {
+        const uint32_t m = std::min(chunk, nq - s0);
+        std::vector<uint32_t> r((size_t)m * kk);
+        std::vector<float> sc((size_t)m * kk);
+        rc = host_query(idx, queries + (size_t)s0 * idx->dim, m, kk, kk, false, nullptr, 0, r.data(), sc.data(),
+                        n_out + s0);
+        if (rc) return rc;
+        for (uint32_t i = 0; i < m; i++) {
+            std::memcpy(rows + (size_t)(s0 + i) * k, r.data() + (size_t)i * kk, (size_t)kk * 4);
+            std::memcpy(scores + (size_t)(s0 + i) * k, sc.data() + (size_t)i * kk, (size_t)kk * 4);
+        }
+    }
+    return BV_OK;
+}
+
+extern "C" int bv_index_set_nprobe(bv_index *idx, uint32_t nprobe) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    idx->nprobe_override = nprobe;
+    return BV_OK;
+}
+
+extern "C" int bv_index_search(bv_index *idx, const float *queries, uint32_t nq, uint32_t fetch, uint32_t k,
+                               uint32_t *rows, float *scores, uint32_t *n_out) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (nq == 0) return BV_OK;
+    if (!queries || !n_out || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
+    if (fetch && !idx->quant) return fail(BV_E_UNSUPPORTED, "re-rank needs a quantized index");
+    const uint32_t kk = (uint32_t)std::min<uint64_t>(k, idx->rows);
+    uint32_t fe = fetch ? (uint32_t)std::min<uint64_t>(std::max(fetch, kk), idx->rows) : 0;
+    if (fe > (uint32_t)MAX_KPRIME || kk > (uint32_t)MAX_KPRIME)
+        return fail(BV_E_UNSUPPORTED, "fetch %u exceeds the fused top-k limit %d", fe, MAX_KPRIME);
+    const uint32_t chunk = 64;
+    for (uint32_t s0 = 0; s0 < nq; s0 += chunk) {
+        const uint32_t m = std::min(chunk, nq - s0);
+        std::vector<uint32_t> r((size_t)m * std::max(kk, 1u));
+        std::vector<float> sc((size_t)m * std::max(kk, 1u));
+        rc = host_query(idx, queries + (size_t)s0 * idx->dim, m, fe ? fe : kk, kk, fe != 0, nullptr, 0, r.data(),
+                        sc.data(), n_out + s0);
+        if (rc) return rc;
+        for (uint32_t i = 0; i < m; i++) {
+            std::memcpy(rows + (size_t)(s0 + i) * k, r.data() + (size_t)i * kk, (size_t)kk * 4);
+            std::memcpy(scores + (size_t)(s0 + i) * k, sc.data() + (size_t)i * kk, (size_t)kk * 4);
+        }
+    }
+    return BV_OK;
+}
+
+extern "C" int bv_index_search_device(bv_index *idx, const float *d_queries, uint32_t nq, uint32_t fetch, uint32_t k,
+                                      uint32_t *d_rows, float *d_scores, uint32_t *d_n_out) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (nq == 0) return BV_OK;
+    if (!d_queries || !d_rows || !d_scores || !d_n_out) return fail(BV_E_INVALID, "null argument");
+    if (fetch && !idx->quant) return fail(BV_E_UNSUPPORTED, "re-rank needs a quantized index");
+    if (idx->rows == 0 || k == 0) return fail(BV_E_STATE, "empty index or k == 0");
+    const uint32_t kk = (uint32_t)std::min<uint64_t>(k, idx->rows);
+    const uint32_t fe = fetch ? (uint32_t)std::min<uint64_t>(std::max(fetch, kk), idx->rows) : 0;
+    if (fe > (uint32_t)MAX_KPRIME || kk > (uint32_t)MAX_KPRIME)
+        return fail(BV_E_UNSUPPORTED, "fetch %u exceeds the fused top-k limit %d", fe, MAX_KPRIME);
+    return run_pipeline(idx, d_queries, nq, fe ? fe : kk, kk, fe != 0, nullptr, 0, d_rows, d_scores, d_n_out);
+}
+
+extern "C" int bv_index_sync(bv_index *idx) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "sync");
+    return BV_OK;
+}
+
+extern "C" int bv_index_stream(bv_index *idx, void **stream) {
+    if (!idx || !stream) return fail(BV_E_INVALID, "null argument");
+    *stream = (void *)idx->stream;
+    return BV_OK;
+}
+
+extern "C" int bv_index_kernel_timing(bv_index *idx, int enable, double *scan_ms, uint64_t *scan_launches) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    timing_collect(idx);
+    if (enable) {
+        idx->timing = true;
+        idx->scan_ms = 0;
+        idx->scan_launches = 0;
+    } else {
+        idx->timing = false;
+    }
+    if (scan_ms) *scan_ms = idx->scan_ms;
+    if (scan_launches) *scan_launches = idx->scan_launches;
+    return BV_OK;
+}
+
+extern "C" int bv_index_rerank(bv_index *idx, const float *q, const uint32_t *cand, uint32_t n_cand, uint32_t k,
+                               uint32_t *rows, float *scores, uint32_t *n_out) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!q || !n_out || (n_cand && !cand) || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
+    if (n_cand > (uint32_t)MAX_KPRIME) return fail(BV_E_UNSUPPORTED, "at most %d re-rank candidates", MAX_KPRIME);
+    for (uint32_t i = 0; i < n_cand; i++)
+        if (cand[i] >= idx->rows) return fail(BV_E_INVALID, "candidate row %u out of range", cand[i]);
+    const uint32_t kk = std::min(k, n_cand);
+    if (kk == 0) {
+        *n_out = 0;
+        return BV_OK;
+    }
+    const size_t qb = (size_t)idx->dim * 4;
+    HIPX(idx->dev, idx->qin.ensure(qb, 0, idx->stream), "query buffer");
+    HIPX(idx->dev, hipMemcpyAsync(idx->qin.p, q, qb, hipMemcpyHostToDevice, idx->stream), "upload");
+    HIPX(idx->dev, idx->cand.ensure((size_t)n_cand * 4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, hipMemcpyAsync(idx->cand.p, cand, (size_t)n_cand * 4, hipMemcpyHostToDevice, idx->stream), "upload");
+    HIPX(idx->dev, idx->cand_n.ensure(4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, hipMemcpyAsync(idx->cand_n.p, &n_cand, 4, hipMemcpyHostToDevice, idx->stream), "upload");
+    HIPX(idx->dev, idx->rr_scores.ensure((size_t)n_cand * 4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->rr_rows.ensure((size_t)n_cand * 4, 0, idx->stream), "scratch");
+    {
+        const size_t old = idx->rr_tickets.cap;
+        HIPX(idx->dev, idx->rr_tickets.ensure(4, 0, idx->stream), "scratch");
+        if (idx->rr_tickets.cap != old)
+            HIPX(idx->dev, hipMemsetAsync(idx->rr_tickets.p, 0, idx->rr_tickets.cap, idx->stream), "scratch");
+    }
+    HIPX(idx->dev, idx->out_rows.ensure((size_t)kk * 4, 0, idx->stream), "output");
+    HIPX(idx->dev, idx->out_scores.ensure((size_t)kk * 4, 0, idx->stream), "output");
+    HIPX(idx->dev, idx->out_n.ensure(4, 0, idx->stream), "output");
+    RerankArgs r{};
+    r.rows = idx->raw.as<float>();
+    r.dim = idx->dim;
+    r.q = idx->qin.as<float>();
+    r.q_stride = idx->dim;
+    r.cand_rows = idx->cand.as<uint32_t>();
+    r.cand_n = idx->cand_n.as<uint32_t>();
+    r.kprime = n_cand;
+    r.k_out = kk;
+    r.rr_scores = idx->rr_scores.as<float>();
+    r.rr_rows = idx->rr_rows.as<uint32_t>();
+    r.tickets = idx->rr_tickets.as<uint32_t>();
+    r.out_rows = idx->out_rows.as<uint32_t>();
+    r.out_scores = idx->out_scores.as<float>();
+    r.out_n = idx->out_n.as<uint32_t>();
+    HIPX(idx->dev, launch_rerank(r, 1, idx->stream), "rerank kernel");
+    HIPX(idx->dev, hipMemcpyAsync(rows, idx->out_rows.p, (size_t)kk * 4, hipMemcpyDeviceToHost, idx->stream), "download");
+    HIPX(idx->dev, hipMemcpyAsync(scores, idx->out_scores.p, (size_t)kk * 4, hipMemcpyDeviceToHost, idx->stream),
+         "download");
+    HIPX(idx->dev, hipMemcpyAsync(n_out, idx->out_n.p, 4, hipMemcpyDeviceToHost, idx->stream), "download");
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "rerank");
+    return BV_OK;
+}
+
+// Dense scores of one query for every row (the scan's score for each row).
+static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uint64_t mask_words, float *out) {
+    const size_t qb = (size_t)idx->dim * 4;
+    HIPX(idx->dev, idx->qin.ensure(qb, 0, idx->stream), "query buffer");
+    HIPX(idx->dev, hipMemcpyAsync(idx->qin.p, q, qb, hipMemcpyHostToDevice, idx->stream), "upload");
+    HIPX(idx->dev, idx->dense.ensure(idx->rows * 4, 0, idx->stream), "scratch");
+    const void *qscan = nullptr;
+    uint64_t qstride = 0;
+    int rc = prepare_queries(idx, idx->qin.as<float>(), 1, &qscan, &qstride);
+    if (rc) return rc;
+    uint32_t rpw = 0;
+    const uint32_t grid = grid_for(idx->rows, &rpw);
+    HIPX(idx->dev, idx->partials.ensure((size_t)grid * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->merged.ensure(8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->merged_n.ensure(4, 0, idx->stream), "scratch");
+    {
+        const size_t old = idx->tickets.cap;
+        HIPX(idx->dev, idx->tickets.ensure(4, 0, idx->stream), "scratch");
+        if (idx->tickets.cap != old)
+            HIPX(idx->dev, hipMemsetAsync(idx->tickets.p, 0, idx->tickets.cap, idx->stream), "scratch");
+    }
+    const uint32_t *d_mask = nullptr;
+    if (mask) {
+        HIPX(idx->dev, idx->mask.ensure(mask_words * 4, 0, idx->stream), "mask buffer");
+        HIPX(idx->dev, hipMemcpyAsync(idx->mask.p, mask, mask_words * 4, hipMemcpyHostToDevice, idx->stream), "upload");
+        d_mask = idx->mask.as<uint32_t>();
+    }
+    ScanArgs a{};
+    a.codes = idx->quant ? idx->codes.p : idx->raw.p;
+    a.row_bytes = idx->row_bytes;
+    a.units = idx->units;
+    a.padded_dim = idx->P;
+    a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A) ? idx->scales.as<float>() : nullptr;
+    a.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
+    a.q = qscan;
+    a.q_stride = qstride;
+    a.mask = d_mask;
+    a.mask_bits = mask_words * 32;
+    a.n = idx->rows;
+    a.kprime = 1;
+    a.rows_per_wg = rpw;
+    a.grid = grid;
+    a.partials = idx->partials.as<uint64_t>();
+    a.tickets = idx->tickets.as<uint32_t>();
+    a.merged = idx->merged.as<uint64_t>();
+    a.merged_n = idx->merged_n.as<uint32_t>();
+    a.dense_out = idx->dense.as<float>();
+    HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, 1, idx->stream), "scan kernel");
+    HIPX(idx->dev, hipMemcpyAsync(out, idx->dense.p, idx->rows * 4, hipMemcpyDeviceToHost, idx->stream), "download");
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "dense scores");
+    return BV_OK;
+}
+
+static int host_query_dense(bv_index *idx, const float *q, uint32_t nq, uint32_t k, const uint32_t *mask,
+                            uint64_t mask_words, uint32_t *rows, float *scores, uint32_t *n_out) {
+    std::vector<float> s(idx->rows);
+    for (uint32_t i = 0; i < nq; i++) {
+        int rc = dense_scores(idx, q + (size_t)i * idx->dim, nullptr, 0, s.data());
+        if (rc) return rc;
+        std::vector<uint32_t> ids;
+        ids.reserve(idx->rows);
+        for (uint64_t r = 0; r < idx->rows; r++) {
+            if (mask && !((mask[r >> 5] >> (r & 31)) & 1u)) continue;
+            ids.push_back((uint32_t)r);
+        }
+        const size_t kk = std::min<size_t>(k, ids.size());
+        auto better = [&](uint32_t a, uint32_t b) {
+            float sa = s[a] + 0.0f, sb = s[b] + 0.0f;
+            return sa > sb || (sa == sb && a < b);
+        };
+        std::partial_sort(ids.begin(), ids.begin() + kk, ids.end(), better);
+        for (size_t j = 0; j < kk; j++) {
+            rows[(size_t)i * k + j] = ids[j];
+            scores[(size_t)i * k + j] = s[ids[j]] + 0.0f;
+        }
+        n_out[i] = (uint32_t)kk;
+    }
+    (void)mask_words;
+    return BV_OK;
+}
+
+// ------------------------------------------------------------ stats/exports
+extern "C" int bv_index_get_stats(bv_index *idx, bv_index_stats *out) {
+    if (!idx || !out) return fail(BV_E_INVALID, "null argument");
+    std::memset(out, 0, sizeof *out);
+    out->rows = idx->rows;
+    out->dim = idx->dim;
+    out->padded_dim = idx->quant ? idx->P : idx->dim;
+    out->words_per_row = idx->words_per_row;
+    out->bits = idx->d.bits;
+    uint32_t chunks = 1;
+    if (idx->d.chunk_rows && idx->rows) chunks = (uint32_t)((idx->rows + idx->d.chunk_rows - 1) / idx->d.chunk_rows);
+    out->chunk_count = chunks;
+    out->tuned_recall = -1.0f;
+    out->last_query_ms = idx->last_query_ms;
+    out->last_query_gpu_ms = idx->last_query_gpu_ms;
+    out->device_bytes = idx->raw.cap + idx->codes.cap + idx->scales.cap;
+    out->last_scanned_rows = idx->last_scanned;
+    return BV_OK;
+}
+
+extern "C" int bv_index_export_codes(bv_index *idx, uint64_t row0, uint64_t count, uint32_t *words, float *scales) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!idx->quant) return fail(BV_E_STATE, "not a quantized index");
+    if (row0 + count > idx->rows) return fail(BV_E_INVALID, "row range out of bounds");
+    if (count == 0) return BV_OK;
+    if (words)
+        HIPX(idx->dev, hipMemcpy(words, idx->codes.as<char>() + row0 * idx->row_bytes, count * idx->row_bytes,
+                                 hipMemcpyDeviceToHost), "download");
+    if (scales)
+        HIPX(idx->dev, hipMemcpy(scales, idx->scales.as<float>() + row0, count * 4, hipMemcpyDeviceToHost), "download");
+    return BV_OK;
+}
+
+extern "C" int bv_index_export_scores(bv_index *idx, const float *q, float *scores) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!q || !scores) return fail(BV_E_INVALID, "null argument");
+    if (idx->rows == 0) return BV_OK;
+    return dense_scores(idx, q, nullptr, 0, scores);
+}
+
+extern "C" int bv_index_export_rotated_query(bv_index *idx, const float *q, float *rotated) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!idx->quant) return fail(BV_E_STATE, "not a quantized index");
+    if (!q || !rotated) return fail(BV_E_INVALID, "null argument");
+    const size_t qb = (size_t)idx->dim * 4;
+    HIPX(idx->dev, idx->qin.ensure(qb, 0, idx->stream), "query buffer");
+    HIPX(idx->dev, hipMemcpyAsync(idx->qin.p, q, qb, hipMemcpyHostToDevice, idx->stream), "upload");
+    const void *qs = nullptr;
+    uint64_t st = 0;
+    rc = prepare_queries(idx, idx->qin.as<float>(), 1, &qs, &st);
+    if (rc) return rc;
+    HIPX(idx->dev, hipMemcpyAsync(rotated, idx->qrot.p, (size_t)idx->P * 4, hipMemcpyDeviceToHost, idx->stream),
+         "download");
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "rotate");
+    return BV_OK;
+}

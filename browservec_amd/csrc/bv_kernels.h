@@ -1,0 +1,97 @@
+// Launch interface between the host runtime (bv_api.cpp) and the gfx950
+// kernels (bv_kernels.hip).  Internal to libbrowservec_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bvk {
+
+// Code layouts the scan understands.
+enum CodecId : int {
+    C_F32DOT = 0,   // fp32 rows, dot / cosine        (16-byte units = 4 floats)
+    C_F32L2 = 1,    // fp32 rows, negative squared l2 (16-byte units)
+    C_Q8 = 2,       // int8 codes, asymmetric          (16-byte units = 16 codes)
+    C_Q4 = 3,       // int4 codes, asymmetric          (16-byte units = 32 codes)
+    C_Q1A = 4,      // 1-bit codes, asymmetric         (4-byte units = 32 codes)
+    C_HAM = 5,      // 1-bit codes, Hamming            (16-byte units = 128 bits)
+    C_I8S = 6,      // int8 codes x int8 query         (16-byte units)
+    C_F32DOT_S = 7, // fp32 rows, dim % 4 != 0         (4-byte units = 1 float)
+    C_F32L2_S = 8,
+    C_COUNT = 9
+};
+
+constexpr int SCAN_WG = 256;      // 4 waves
+constexpr int SCAN_CAP = 2048;    // LDS candidate keys per workgroup
+constexpr int MAX_KPRIME = 1024;  // largest fetch the fused top-k serves
+constexpr int MAX_GRID = 1024;    // workgroups per query
+
+struct ScanArgs {
+    const void *codes;        // row-major rows, row_bytes each
+    uint64_t row_bytes;
+    uint32_t units;           // units per row (W)
+    uint32_t padded_dim;      // P (Hamming similarity = P - 2*popcount)
+    const float *scales;      // per-row scale (quantized codecs) or null
+    float scale_mul;          // constant multiplier on the row scale (int4: f32(1/7))
+    const void *q;            // transformed queries, q_stride bytes apart
+    uint64_t q_stride;
+    const uint32_t *cand;     // indexed mode: row ids (null = rows 0..n-1)
+    const uint64_t *cand_off; // per-query offsets into cand (nq+1) or null
+    const uint32_t *mask;     // row filter bits (LSB-first) or null
+    uint64_t mask_bits;
+    uint64_t n;               // rows per query when cand_off is null
+    uint32_t kprime;          // per-query candidates kept
+    uint32_t rows_per_wg;
+    uint32_t grid;            // workgroups per query
+    uint64_t *partials;       // [nq][grid][kprime]
+    uint32_t *tickets;        // [nq], zero on entry, zeroed again on exit
+    uint64_t *merged;         // [nq][kprime] merged keys, descending
+    uint32_t *merged_n;       // [nq]
+    float *dense_out;         // optional: every row's score (query 0 only)
+    uint32_t k_out;           // when out_rows != null: decoded top-k_out
+    uint32_t *out_rows;       // [nq][k_out]
+    float *out_scores;
+    uint32_t *out_n;          // [nq]
+};
+
+struct EncodeArgs {
+    const float *src;         // rows x dim
+    uint64_t rows;
+    uint32_t dim;
+    uint32_t P;               // padToPow2(dim)
+    const float *signs;       // rounds x P
+    uint32_t rounds;
+    uint32_t bits;            // 8, 4, 1 (codes out) or 0 (no codes)
+    uint32_t *codes;          // rows x (P/per)
+    float *scales;            // rows
+    float *rotated;           // optional rows x P
+    float *qdiv;              // optional rows x P: rotated / 127 (int8 scan query)
+    uint32_t *slow_rows;      // counter of rows that took the sequential 1-bit sum
+};
+
+struct RerankArgs {
+    const float *rows;        // stored fp32 rows (original space), N x dim
+    uint32_t dim;
+    const float *q;           // queries (original space), q_stride floats apart
+    uint64_t q_stride;
+    const uint64_t *merged;   // [nq][kprime] candidate keys (row in low bits)
+    const uint32_t *merged_n; // [nq]
+    const uint32_t *cand_rows;// alternative: explicit candidate rows [nq][kprime]
+    const uint32_t *cand_n;   // [nq] counts for cand_rows
+    uint32_t kprime;
+    uint32_t k_out;
+    float *rr_scores;         // scratch [nq][kprime]
+    uint32_t *rr_rows;        // scratch [nq][kprime]
+    uint32_t *tickets;        // [nq]
+    uint32_t *out_rows;       // [nq][k_out]
+    float *out_scores;
+    uint32_t *out_n;
+};
+
+// Chooses the lane layout for a codec and row size; false if unsupported.
+bool scan_supported(int codec, uint32_t units);
+hipError_t launch_scan(int codec, uint32_t units, const ScanArgs &a, uint32_t nq, hipStream_t s);
+hipError_t launch_encode(const EncodeArgs &a, hipStream_t s);
+hipError_t launch_rerank(const RerankArgs &a, uint32_t nq, hipStream_t s);
+
+} // namespace bvk

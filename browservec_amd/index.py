@@ -1,0 +1,261 @@
+"""Index classes behind the reference's ``VectorIndex`` seam.
+
+``FlatIndex`` / ``QuantIndex`` mirror src/index/flat.ts:42-211 and
+src/index/quant.ts:21-258: same constructor knowledge (dim, metric, bits,
+seed, rounds, chunkRows), same ``size`` / ``append`` / ``query`` /
+``queryMasked`` / ``destroy`` surface and error messages, with every byte of
+corpus and every scan living on the MI355X through libbrowservec_hip.so.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib as L
+
+
+@dataclass(frozen=True)
+class FlatHit:
+    """One result (src/index/flat.ts:24-27): row id and score (higher = closer)."""
+
+    row: int
+    score: float
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class DeviceContext:
+    """The engine's DeviceContext (src/engine/device.ts:3-9) over a HIP device."""
+
+    def __init__(self, ordinal: int = 0):
+        self.lib = L.load()
+        h = ctypes.c_void_p()
+        L.check(self.lib.bv_device_open(ordinal, ctypes.byref(h)))
+        self.handle = h
+
+    @property
+    def lost(self) -> bool:
+        v = ctypes.c_int(0)
+        L.check(self.lib.bv_device_is_lost(self.handle, ctypes.byref(v)))
+        return bool(v.value)
+
+    def info(self) -> dict:
+        name = ctypes.create_string_buffer(256)
+        cu = ctypes.c_uint32()
+        hbm = ctypes.c_uint64()
+        L.check(self.lib.bv_device_info(self.handle, name, 256, ctypes.byref(cu), ctypes.byref(hbm)))
+        return {"name": name.value.decode(), "cu_count": cu.value, "hbm_bytes": hbm.value}
+
+    def destroy(self) -> None:
+        if self.handle:
+            self.lib.bv_device_close(self.handle)
+            self.handle = None
+
+
+class NativeIndex:
+    """Common native-index plumbing; subclasses fix the index kind."""
+
+    kind = L.KIND_FLAT
+
+    def __init__(self, ctx: DeviceContext, dim: int, metric: str = "cosine", bits: int = 0,
+                 seed: int | None = None, rounds: int = 2, chunk_rows: int | None = None,
+                 scorer: str = "asym", ivf: dict | None = None):
+        self.ctx = ctx
+        self.lib = ctx.lib
+        self.dim = int(dim)
+        self.metric = metric
+        self.bits = bits
+        d = L.IndexDesc()
+        d.size = ctypes.sizeof(L.IndexDesc)
+        d.kind = self.kind
+        d.dim = self.dim
+        if metric not in L.METRICS:
+            raise L.BVError(L.BV_E_INVALID, f"unknown metric {metric}")
+        d.metric = L.METRICS[metric]
+        d.bits = bits
+        d.scorer = L.SCORERS[scorer]
+        if seed is not None:
+            d.seed = seed & 0xFFFFFFFF
+            d.has_seed = 1
+        d.rounds = rounds
+        d.chunk_rows = chunk_rows or 0
+        d.target_recall = -1.0
+        ivf = ivf or {}
+        d.nlist = ivf.get("nlist") or 0
+        d.nprobe = ivf.get("nprobe") or 0
+        d.sample_size = ivf.get("sampleSize") or 0
+        d.train_size = ivf.get("trainSize") or 0
+        d.iters = ivf.get("iters") or 0
+        if ivf.get("seed") is not None:
+            d.ivf_seed = ivf["seed"] & 0xFFFFFFFF
+            d.has_ivf_seed = 1
+        if ivf.get("targetRecall") is not None:
+            d.target_recall = float(ivf["targetRecall"])
+        h = ctypes.c_void_p()
+        L.check(self.lib.bv_index_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)))
+        self.handle = h
+
+    # -- VectorIndex -------------------------------------------------------
+    @property
+    def size(self) -> int:
+        v = ctypes.c_uint64()
+        L.check(self.lib.bv_index_size(self.handle, ctypes.byref(v)))
+        return v.value
+
+    def append(self, data, count: int) -> None:
+        data = _f32(data).reshape(-1)
+        L.check(self.lib.bv_index_append(self.handle, _ptr(data), data.size, int(count)))
+
+    def query(self, q, k: int) -> list[FlatHit]:
+        q = _f32(q).reshape(-1)
+        rows = np.empty(max(k, 1), np.uint32)
+        scores = np.empty(max(k, 1), np.float32)
+        n = ctypes.c_uint32()
+        L.check(self.lib.bv_index_query(self.handle, _ptr(q), int(k), _ptr(rows), _ptr(scores), ctypes.byref(n)))
+        return [FlatHit(int(rows[i]), float(scores[i])) for i in range(n.value)]
+
+    def query_masked(self, q, k: int, mask_words) -> list[FlatHit]:
+        q = _f32(q).reshape(-1)
+        m = np.ascontiguousarray(mask_words, dtype=np.uint32)
+        rows = np.empty(max(k, 1), np.uint32)
+        scores = np.empty(max(k, 1), np.float32)
+        n = ctypes.c_uint32()
+        L.check(self.lib.bv_index_query_masked(self.handle, _ptr(q), int(k), _ptr(m), m.size, _ptr(rows),
+                                               _ptr(scores), ctypes.byref(n)))
+        return [FlatHit(int(rows[i]), float(scores[i])) for i in range(n.value)]
+
+    def query_batch(self, packed, n: int, k: int) -> list[list[FlatHit]]:
+        packed = _f32(packed).reshape(-1)
+        rows = np.empty((n, max(k, 1)), np.uint32)
+        scores = np.empty((n, max(k, 1)), np.float32)
+        cnt = np.empty(max(n, 1), np.uint32)
+        L.check(self.lib.bv_index_query_batch(self.handle, _ptr(packed), int(n), int(k), _ptr(rows),
+                                              _ptr(scores), _ptr(cnt)))
+        return [[FlatHit(int(rows[i, j]), float(scores[i, j])) for j in range(cnt[i])] for i in range(n)]
+
+    def destroy(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.bv_index_destroy(self.handle)
+            self.handle = None
+
+    # -- extras ------------------------------------------------------------
+    def set_nprobe(self, n: int | None) -> None:
+        L.check(self.lib.bv_index_set_nprobe(self.handle, int(n or 0)))
+
+    def search(self, queries, fetch: int, k: int):
+        """Approximate top-`fetch` then exact f64 re-rank to top-`k`, on the
+        device (BrowserVec.query's quantized path, src/index.ts:414-418).
+        Returns (rows[nq,k], scores[nq,k], counts[nq])."""
+        qs = _f32(queries).reshape(-1, self.dim)
+        nq = qs.shape[0]
+        rows = np.empty((nq, max(k, 1)), np.uint32)
+        scores = np.empty((nq, max(k, 1)), np.float32)
+        cnt = np.empty(max(nq, 1), np.uint32)
+        L.check(self.lib.bv_index_search(self.handle, _ptr(qs), nq, int(fetch), int(k), _ptr(rows), _ptr(scores),
+                                          _ptr(cnt)))
+        return rows[:, :k], scores[:, :k], cnt[:nq]
+
+    def rerank(self, q, cand, k: int) -> list[FlatHit]:
+        """BrowserVec.rerankExact on the device (src/index.ts:583-594)."""
+        q = _f32(q).reshape(-1)
+        c = np.ascontiguousarray(cand, dtype=np.uint32)
+        rows = np.empty(max(k, 1), np.uint32)
+        scores = np.empty(max(k, 1), np.float32)
+        n = ctypes.c_uint32()
+        L.check(self.lib.bv_index_rerank(self.handle, _ptr(q), _ptr(c), c.size, int(k), _ptr(rows), _ptr(scores),
+                                         ctypes.byref(n)))
+        return [FlatHit(int(rows[i]), float(scores[i])) for i in range(n.value)]
+
+    def stats(self) -> dict:
+        s = L.IndexStats()
+        L.check(self.lib.bv_index_get_stats(self.handle, ctypes.byref(s)))
+        return {f: getattr(s, f) for f, _ in L.IndexStats._fields_}
+
+    @property
+    def chunk_count(self) -> int:
+        return self.stats()["chunk_count"]
+
+    def export_scores(self, q) -> np.ndarray:
+        q = _f32(q).reshape(-1)
+        out = np.empty(self.size, np.float32)
+        L.check(self.lib.bv_index_export_scores(self.handle, _ptr(q), _ptr(out)))
+        return out
+
+    # device-resident entry points (pointers are integers, e.g. tensor.data_ptr())
+    def append_device(self, d_ptr: int, count: int) -> None:
+        L.check(self.lib.bv_index_append_device(self.handle, ctypes.c_void_p(d_ptr), int(count)))
+
+    def search_device(self, d_q: int, nq: int, fetch: int, k: int, d_rows: int, d_scores: int, d_n: int) -> None:
+        L.check(self.lib.bv_index_search_device(self.handle, ctypes.c_void_p(d_q), int(nq), int(fetch), int(k),
+                                                ctypes.c_void_p(d_rows), ctypes.c_void_p(d_scores),
+                                                ctypes.c_void_p(d_n)))
+
+    def sync(self) -> None:
+        L.check(self.lib.bv_index_sync(self.handle))
+
+    def stream_ptr(self) -> int:
+        s = ctypes.c_void_p()
+        L.check(self.lib.bv_index_stream(self.handle, ctypes.byref(s)))
+        return s.value or 0
+
+    def kernel_timing(self, enable: bool):
+        ms = ctypes.c_double()
+        n = ctypes.c_uint64()
+        L.check(self.lib.bv_index_kernel_timing(self.handle, 1 if enable else 0, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class FlatIndex(NativeIndex):
+    """Exact fp32 flat index (src/index/flat.ts:42-211)."""
+
+    kind = L.KIND_FLAT
+
+    def __init__(self, ctx, dim, metric="cosine", chunk_rows=None):
+        super().__init__(ctx, dim, metric, 0, chunk_rows=chunk_rows)
+
+
+class QuantIndex(NativeIndex):
+    """TurboQuant flat index (src/index/quant.ts:21-258): rotate + quantize on
+    the device at append; asymmetric scans (or the Hamming / int8 scorers)."""
+
+    kind = L.KIND_QUANT
+
+    def __init__(self, ctx, dim, seed=0x9E3779B9, rounds=2, bits=8, chunk_rows=None, scorer="asym",
+                 metric="cosine"):
+        super().__init__(ctx, dim, metric, bits, seed=seed, rounds=rounds, chunk_rows=chunk_rows, scorer=scorer)
+        st = self.stats()
+        self.padded_dim = st["padded_dim"]
+        self.words_per_row = st["words_per_row"]
+
+    @property
+    def ingest_mode(self) -> str:
+        """Where rotate+quantize runs; on this build always the device."""
+        return "device"
+
+    def export_codes(self, row0: int = 0, count: int | None = None):
+        count = self.size - row0 if count is None else count
+        words = np.empty((count, self.words_per_row), np.uint32)
+        scales = np.empty(count, np.float32)
+        L.check(self.lib.bv_index_export_codes(self.handle, row0, count, _ptr(words), _ptr(scales)))
+        return words, scales
+
+    def export_rotated_query(self, q) -> np.ndarray:
+        q = _f32(q).reshape(-1)
+        out = np.empty(self.padded_dim, np.float32)
+        L.check(self.lib.bv_index_export_rotated_query(self.handle, _ptr(q), _ptr(out)))
+        return out

@@ -1,0 +1,62 @@
+"""CPU checks of the drop-in boundary: the built library loads and exports
+every function include/browservec_hip.h declares (no GPU calls)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "browservec_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(bv_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_seam():
+    names = declared_functions()
+    for must in ("bv_device_open", "bv_index_create", "bv_index_append", "bv_index_query", "bv_index_query_masked",
+                 "bv_index_query_batch", "bv_index_rerank", "bv_index_search", "bv_index_destroy", "bv_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    from browservec_amd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("libbrowservec_hip.so is not built (python -m browservec_amd.build)")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # the Python binding covers the same set
+    assert set(declared_functions()) <= set(_lib.SIGNATURES)
+
+
+def test_no_device_error_path_is_clean():
+    """Without a GPU, opening a device fails with a status code and message,
+    never a crash or a silent CPU fallback."""
+    from browservec_amd import _lib
+    from browservec_amd.index import DeviceContext
+
+    try:
+        import torch
+
+        if torch.cuda.is_available():
+            pytest.skip("a GPU is present")
+    except Exception:
+        pass
+    with pytest.raises(_lib.BVError) as e:
+        DeviceContext(0)
+    assert e.value.code in (_lib.BV_E_UNSUPPORTED, _lib.BV_E_HIP, _lib.BV_E_INVALID)
+
+
+def test_struct_layouts_match_header():
+    from browservec_amd import _lib
+
+    assert ctypes.sizeof(_lib.IndexDesc) == 18 * 4
+    # IndexStats: u64 + 7*u32 + f32 + 3*f64 + 2*u64
+    assert ctypes.sizeof(_lib.IndexStats) == 8 + 8 * 4 + 3 * 8 + 2 * 8
