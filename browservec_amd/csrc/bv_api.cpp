@@ -125,7 +125,7 @@ struct bv_index {
 
     // per-call scratch
     DevBuf qin, qrot, qscan, qscale, mask;
-    DevBuf partials, tickets, merged, merged_n;
+    DevBuf qstate, wmax, cand_keys, merged, merged_n;
     DevBuf rr_scores, rr_rows, rr_tickets;
     DevBuf out_rows, out_scores, out_n;
     DevBuf cand, cand_n, dense;
@@ -407,6 +407,35 @@ static uint32_t grid_for(uint64_t n, uint32_t *rows_per_wg) {
     return (uint32_t)g;
 }
 
+// Scratch of the fused scan for nq queries: coordination state and wave
+// maxima must start zeroed (the kernel leaves them zeroed).
+static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kprime, ScanArgs &a) {
+    const size_t slots = (size_t)grid * (SCAN_WG / 64);
+    {
+        const size_t old = idx->qstate.cap;
+        HIPX(idx->dev, idx->qstate.ensure((size_t)nq * sizeof(QState), 0, idx->stream), "scratch");
+        if (idx->qstate.cap != old)
+            HIPX(idx->dev, hipMemsetAsync(idx->qstate.p, 0, idx->qstate.cap, idx->stream), "scratch");
+    }
+    {
+        const size_t old = idx->wmax.cap;
+        HIPX(idx->dev, idx->wmax.ensure((size_t)nq * slots * 8, 0, idx->stream), "scratch");
+        if (idx->wmax.cap != old) HIPX(idx->dev, hipMemsetAsync(idx->wmax.p, 0, idx->wmax.cap, idx->stream), "scratch");
+    }
+    const uint64_t ng = grid < (uint32_t)NGROUP ? grid : (uint32_t)NGROUP;
+    const uint64_t cap = ng * ((grid + ng - 1) / ng) * kprime;
+    HIPX(idx->dev, idx->cand_keys.ensure((size_t)nq * cap * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
+    a.qs = idx->qstate.as<QState>();
+    a.wmax = idx->wmax.as<uint64_t>();
+    a.cand_keys = idx->cand_keys.as<uint64_t>();
+    a.cand_cap = cap;
+    a.merged = idx->merged.as<uint64_t>();
+    a.merged_n = idx->merged_n.as<uint32_t>();
+    return BV_OK;
+}
+
 // Query transform for the scan: device-resident queries d_q (nq x dim) ->
 // qscan (per-codec layout), and for quantized kinds qrot (nq x P).
 static int prepare_queries(bv_index *idx, const float *d_q, uint32_t nq, const void **qscan, uint64_t *qstride) {
@@ -427,12 +456,21 @@ static int prepare_queries(bv_index *idx, const float *d_q, uint32_t nq, const v
     a.rotated = idx->qrot.as<float>();
     switch (idx->codec) {
     case C_Q8:
-        HIPX(idx->dev, idx->qscan.ensure((size_t)nq * P * 4, 0, idx->stream), "query buffer");
-        a.qdiv = idx->qscan.as<float>();
+    case C_Q4: {
+        const size_t st = level_stride(idx->codec, P);
+        HIPX(idx->dev, idx->qscan.ensure((size_t)nq * st, 0, idx->stream), "query buffer");
+        HIPX(idx->dev, launch_encode(a, idx->stream), "query rotate kernel");
+        LevelArgs la{};
+        la.qrot = idx->qrot.as<float>();
+        la.P = P;
+        la.codec = idx->codec;
+        la.out = idx->qscan.as<unsigned char>();
+        la.stride = st;
+        HIPX(idx->dev, launch_levels(la, nq, idx->stream), "query levels kernel");
         *qscan = idx->qscan.p;
-        *qstride = (uint64_t)P * 4;
-        break;
-    case C_Q4:
+        *qstride = st;
+        return BV_OK;
+    }
     case C_Q1A:
         *qscan = idx->qrot.p;
         *qstride = (uint64_t)P * 4;
@@ -499,16 +537,9 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
     uint32_t rpw = 0;
     const uint64_t n = idx->rows;
     const uint32_t grid = grid_for(n, &rpw);
-    HIPX(idx->dev, idx->partials.ensure((size_t)nq * grid * kprime * 8, 0, idx->stream), "scratch");
-    HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
-    HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
-    {
-        const size_t old = idx->tickets.cap;
-        HIPX(idx->dev, idx->tickets.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
-        if (idx->tickets.cap != old)
-            HIPX(idx->dev, hipMemsetAsync(idx->tickets.p, 0, idx->tickets.cap, idx->stream), "scratch");
-    }
     ScanArgs a{};
+    rc = scan_scratch(idx, nq, grid, kprime, a);
+    if (rc) return rc;
     a.codes = idx->quant ? idx->codes.p : idx->raw.p;
     a.row_bytes = idx->row_bytes;
     a.units = idx->units;
@@ -523,10 +554,6 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
     a.kprime = kprime;
     a.rows_per_wg = rpw;
     a.grid = grid;
-    a.partials = idx->partials.as<uint64_t>();
-    a.tickets = idx->tickets.as<uint32_t>();
-    a.merged = idx->merged.as<uint64_t>();
-    a.merged_n = idx->merged_n.as<uint32_t>();
     if (!rerank) {
         a.k_out = k_out;
         a.out_rows = d_rows;
@@ -820,15 +847,6 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     if (rc) return rc;
     uint32_t rpw = 0;
     const uint32_t grid = grid_for(idx->rows, &rpw);
-    HIPX(idx->dev, idx->partials.ensure((size_t)grid * 8, 0, idx->stream), "scratch");
-    HIPX(idx->dev, idx->merged.ensure(8, 0, idx->stream), "scratch");
-    HIPX(idx->dev, idx->merged_n.ensure(4, 0, idx->stream), "scratch");
-    {
-        const size_t old = idx->tickets.cap;
-        HIPX(idx->dev, idx->tickets.ensure(4, 0, idx->stream), "scratch");
-        if (idx->tickets.cap != old)
-            HIPX(idx->dev, hipMemsetAsync(idx->tickets.p, 0, idx->tickets.cap, idx->stream), "scratch");
-    }
     const uint32_t *d_mask = nullptr;
     if (mask) {
         HIPX(idx->dev, idx->mask.ensure(mask_words * 4, 0, idx->stream), "mask buffer");
@@ -836,6 +854,8 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
         d_mask = idx->mask.as<uint32_t>();
     }
     ScanArgs a{};
+    rc = scan_scratch(idx, 1, grid, 1, a);
+    if (rc) return rc;
     a.codes = idx->quant ? idx->codes.p : idx->raw.p;
     a.row_bytes = idx->row_bytes;
     a.units = idx->units;
@@ -850,10 +870,6 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     a.kprime = 1;
     a.rows_per_wg = rpw;
     a.grid = grid;
-    a.partials = idx->partials.as<uint64_t>();
-    a.tickets = idx->tickets.as<uint32_t>();
-    a.merged = idx->merged.as<uint64_t>();
-    a.merged_n = idx->merged_n.as<uint32_t>();
     a.dense_out = idx->dense.as<float>();
     HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, 1, idx->stream), "scan kernel");
     HIPX(idx->dev, hipMemcpyAsync(out, idx->dense.p, idx->rows * 4, hipMemcpyDeviceToHost, idx->stream), "download");

@@ -25,6 +25,22 @@ constexpr int SCAN_WG = 256;      // 4 waves
 constexpr int SCAN_CAP = 2048;    // LDS candidate keys per workgroup
 constexpr int MAX_KPRIME = 1024;  // largest fetch the fused top-k serves
 constexpr int MAX_GRID = 1024;    // workgroups per query
+constexpr int LOCAL_K = 16;       // best keys each workgroup keeps
+
+// Per-query coordination state of the fused scan (zero before first use;
+// the kernel leaves it zeroed).  Counters that many workgroups update sit in
+// NGROUP groups on separate 128-byte lines: a single hot address would
+// serialize every update.
+constexpr int NGROUP = 32;  // counter groups
+constexpr int CL = 32;      // u32 stride of one counter (128 bytes)
+struct QState {
+    unsigned long long tau;  // published bound: keys below it cannot be in the top-kprime
+    uint32_t top;            // groups whose workgroups have all finished
+    uint32_t fin;            // finishers (final selection + threshold helper)
+    uint32_t pad[28];
+    uint32_t done[NGROUP * CL];  // finished scanning workgroups per group
+    uint32_t cc[NGROUP * CL];    // keys flushed per group region
+};
 
 struct ScanArgs {
     const void *codes;        // row-major rows, row_bytes each
@@ -42,9 +58,11 @@ struct ScanArgs {
     uint64_t n;               // rows per query when cand_off is null
     uint32_t kprime;          // per-query candidates kept
     uint32_t rows_per_wg;
-    uint32_t grid;            // workgroups per query
-    uint64_t *partials;       // [nq][grid][kprime]
-    uint32_t *tickets;        // [nq], zero on entry, zeroed again on exit
+    uint32_t grid;            // scanning workgroups per query (one more runs the threshold helper)
+    QState *qs;               // [nq]
+    uint64_t *wmax;           // [nq][grid*4] per-wave running maxima (zero on entry and exit)
+    uint64_t *cand_keys;      // [nq][cand_cap] flushed candidate keys
+    uint64_t cand_cap;        // >= NGROUP regions of ceil(grid/NGROUP)*kprime keys
     uint64_t *merged;         // [nq][kprime] merged keys, descending
     uint32_t *merged_n;       // [nq]
     float *dense_out;         // optional: every row's score (query 0 only)
@@ -88,10 +106,20 @@ struct RerankArgs {
     uint32_t *out_n;
 };
 
+struct LevelArgs {
+    const float *qrot;        // nq x P rotated queries
+    uint32_t P;
+    int codec;                // C_Q8 or C_Q4
+    unsigned char *out;       // nq x stride bytes: packed levels + QLevelTail
+    uint64_t stride;
+};
+
 // Chooses the lane layout for a codec and row size; false if unsupported.
 bool scan_supported(int codec, uint32_t units);
 hipError_t launch_scan(int codec, uint32_t units, const ScanArgs &a, uint32_t nq, hipStream_t s);
 hipError_t launch_encode(const EncodeArgs &a, hipStream_t s);
 hipError_t launch_rerank(const RerankArgs &a, uint32_t nq, hipStream_t s);
+hipError_t launch_levels(const LevelArgs &a, uint32_t nq, hipStream_t s);
+size_t level_stride(int codec, uint32_t P);
 
 } // namespace bvk

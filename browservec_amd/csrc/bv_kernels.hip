@@ -43,143 +43,280 @@ __device__ __forceinline__ uint32_t key_row(uint64_t k) { return 0xffffffffu - (
 
 // ---------------------------------------------------------------- codecs --
 // Each codec: Unit (what one lane loads per unit), QT/QN (query registers per
-// unit), Acc (accumulator type), accumulate(), and score/ord finalisation.
+// unit), Acc/NA (NA accumulators per row), acc() adding one unit's
+// contribution, and Fin (per-query constants + score finalisation).
+//
+// int8 / int4 asymmetric scans use a three-level integer split of the rotated
+// fp32 query, q ~= s1*q1 + s2*q2 + s3*q3 with q1..q3 int8 (each level
+// quantizes the previous residual, so the residual is below 127^-3 of max|q|).
+// Every level's dot with the codes is an exact int32 from v_dot4_i32_i8;
+// the three are reduced across lanes exactly and combined once per row in
+// f64.  This replaces per-code int->float conversion + FMA, which left the
+// scan bound by VALU issue instead of HBM.
 template <int C> struct Codec;
 
 template <> struct Codec<C_F32DOT> {
     using Unit = uint4; using QT = float; using Acc = float;
-    static constexpr int QN = 4;
-    static __device__ __forceinline__ Acc acc(Unit u, const QT *q, Acc a) {
-        a = fmaf(__uint_as_float(u.x), q[0], a);
-        a = fmaf(__uint_as_float(u.y), q[1], a);
-        a = fmaf(__uint_as_float(u.z), q[2], a);
-        a = fmaf(__uint_as_float(u.w), q[3], a);
-        return a;
+    static constexpr int QN = 4, NA = 1;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
+        a[0] = fmaf(__uint_as_float(u.x), q[0], a[0]);
+        a[0] = fmaf(__uint_as_float(u.y), q[1], a[0]);
+        a[0] = fmaf(__uint_as_float(u.z), q[2], a[0]);
+        a[0] = fmaf(__uint_as_float(u.w), q[3], a[0]);
     }
-    static __device__ __forceinline__ float score(Acc a, float) { return a; }
 };
 template <> struct Codec<C_F32L2> {
     using Unit = uint4; using QT = float; using Acc = float;
-    static constexpr int QN = 4;
-    static __device__ __forceinline__ Acc acc(Unit u, const QT *q, Acc a) {
+    static constexpr int QN = 4, NA = 1;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
         float d0 = __uint_as_float(u.x) - q[0], d1 = __uint_as_float(u.y) - q[1];
         float d2 = __uint_as_float(u.z) - q[2], d3 = __uint_as_float(u.w) - q[3];
-        a = fmaf(d0, d0, a); a = fmaf(d1, d1, a); a = fmaf(d2, d2, a); a = fmaf(d3, d3, a);
-        return a;
+        a[0] = fmaf(d0, d0, a[0]); a[0] = fmaf(d1, d1, a[0]); a[0] = fmaf(d2, d2, a[0]); a[0] = fmaf(d3, d3, a[0]);
     }
-    static __device__ __forceinline__ float score(Acc a, float) { return -a; }
 };
 template <> struct Codec<C_F32DOT_S> {
     using Unit = uint32_t; using QT = float; using Acc = float;
-    static constexpr int QN = 1;
-    static __device__ __forceinline__ Acc acc(Unit u, const QT *q, Acc a) { return fmaf(__uint_as_float(u), q[0], a); }
-    static __device__ __forceinline__ float score(Acc a, float) { return a; }
+    static constexpr int QN = 1, NA = 1;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) { a[0] = fmaf(__uint_as_float(u), q[0], a[0]); }
 };
 template <> struct Codec<C_F32L2_S> {
     using Unit = uint32_t; using QT = float; using Acc = float;
-    static constexpr int QN = 1;
-    static __device__ __forceinline__ Acc acc(Unit u, const QT *q, Acc a) {
+    static constexpr int QN = 1, NA = 1;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
         float d = __uint_as_float(u) - q[0];
-        return fmaf(d, d, a);
+        a[0] = fmaf(d, d, a[0]);
     }
-    static __device__ __forceinline__ float score(Acc a, float) { return -a; }
 };
-// int8: q holds rotated/127 (the unpack4x8snorm scaling folded into the query).
+// int8 codes (16 per unit) x three int8 query levels: q[l*4 + d] holds the
+// level-l query bytes matching code dword d.
 template <> struct Codec<C_Q8> {
-    using Unit = uint4; using QT = float; using Acc = float;
-    static constexpr int QN = 16;
-    static __device__ __forceinline__ Acc acc(Unit u, const QT *q, Acc a) {
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            a = fmaf((float)(int32_t)((int32_t)(w[d] << 24) >> 24), q[4 * d + 0], a);
-            a = fmaf((float)(int32_t)((int32_t)(w[d] << 16) >> 24), q[4 * d + 1], a);
-            a = fmaf((float)(int32_t)((int32_t)(w[d] << 8) >> 24), q[4 * d + 2], a);
-            a = fmaf((float)((int32_t)w[d] >> 24), q[4 * d + 3], a);
-        }
-        return a;
-    }
-    static __device__ __forceinline__ float score(Acc a, float scale) { return a * scale; }
-};
-template <> struct Codec<C_Q4> {
-    using Unit = uint4; using QT = float; using Acc = float;
-    static constexpr int QN = 32;
-    static __device__ __forceinline__ Acc acc(Unit u, const QT *q, Acc a) {
+    using Unit = uint4; using QT = uint32_t; using Acc = int32_t;
+    static constexpr int QN = 12, NA = 3;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int d = 0; d < 4; ++d)
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                a = fmaf((float)((int32_t)(w[d] << (28 - 4 * j)) >> 28), q[8 * d + j], a);
-        return a;
+            for (int l = 0; l < 3; ++l) a[l] = __builtin_amdgcn_sdot4((int)w[d], (int)q[l * 4 + d], a[l], false);
     }
-    static __device__ __forceinline__ float score(Acc a, float scale) { return a * scale; }
+};
+// int4 codes (32 per unit).  Nibble n is carried as the byte u = n ^ 8
+// (= n + 8 in [0, 15]); sum n*q = sum u*q - 8*sum(q), the second term a
+// per-query integer.  q[l*8 + 2d] / q[l*8 + 2d + 1] hold the level-l query
+// bytes for the even / odd nibbles of code dword d.
+template <> struct Codec<C_Q4> {
+    using Unit = uint4; using QT = uint32_t; using Acc = int32_t;
+    static constexpr int QN = 24, NA = 3;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t x = w[d] ^ 0x88888888u;
+            const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int l = 0; l < 3; ++l) {
+                a[l] = __builtin_amdgcn_sdot4((int)lo, (int)q[l * 8 + 2 * d], a[l], false);
+                a[l] = __builtin_amdgcn_sdot4((int)hi, (int)q[l * 8 + 2 * d + 1], a[l], false);
+            }
+        }
+    }
 };
 template <> struct Codec<C_Q1A> {
     using Unit = uint32_t; using QT = float; using Acc = float;
-    static constexpr int QN = 32;
-    static __device__ __forceinline__ Acc acc(Unit u, const QT *q, Acc a) {
+    static constexpr int QN = 32, NA = 1;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
 #pragma unroll
-        for (int j = 0; j < 32; ++j) a += ((u >> j) & 1u) ? q[j] : -q[j];
-        return a;
+        for (int j = 0; j < 32; ++j) a[0] += ((u >> j) & 1u) ? q[j] : -q[j];
     }
-    static __device__ __forceinline__ float score(Acc a, float scale) { return a * scale; }
 };
 template <> struct Codec<C_HAM> {
     using Unit = uint4; using QT = uint32_t; using Acc = int32_t;
-    static constexpr int QN = 4;
-    static __device__ __forceinline__ Acc acc(Unit u, const QT *q, Acc a) {
-        return a + __popc(u.x ^ q[0]) + __popc(u.y ^ q[1]) + __popc(u.z ^ q[2]) + __popc(u.w ^ q[3]);
+    static constexpr int QN = 4, NA = 1;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
+        a[0] += __popc(u.x ^ q[0]) + __popc(u.y ^ q[1]) + __popc(u.z ^ q[2]) + __popc(u.w ^ q[3]);
     }
 };
 template <> struct Codec<C_I8S> {
     using Unit = uint4; using QT = uint32_t; using Acc = int32_t;
-    static constexpr int QN = 4;
-    static __device__ __forceinline__ Acc acc(Unit u, const QT *q, Acc a) {
-        a = __builtin_amdgcn_sdot4((int)u.x, (int)q[0], a, false);
-        a = __builtin_amdgcn_sdot4((int)u.y, (int)q[1], a, false);
-        a = __builtin_amdgcn_sdot4((int)u.z, (int)q[2], a, false);
-        a = __builtin_amdgcn_sdot4((int)u.w, (int)q[3], a, false);
-        return a;
+    static constexpr int QN = 4, NA = 1;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
+        a[0] = __builtin_amdgcn_sdot4((int)u.x, (int)q[0], a[0], false);
+        a[0] = __builtin_amdgcn_sdot4((int)u.y, (int)q[1], a[0], false);
+        a[0] = __builtin_amdgcn_sdot4((int)u.z, (int)q[2], a[0], false);
+        a[0] = __builtin_amdgcn_sdot4((int)u.w, (int)q[3], a[0], false);
     }
 };
 
 template <int C> struct IsInt { static constexpr bool v = (C == C_HAM || C == C_I8S); };
 
-// ------------------------------------------------------- wave reductions --
-// Transposing butterfly: lanes hold U partial sums (one per row group); after
-// log2(U) halving exchanges and log2(LPR/U) plain ones every lane holds the
-// full sum of row group bitrev(lane & (U-1)).
-template <int U, int LPR, typename T> struct XReduce {
-    static __device__ __forceinline__ T run(T (&v)[U], int lane) {
-#pragma unroll
-        for (int s = 0; (1 << s) < U; ++s) {
-            const int m = 1 << s;
-            const int n = U >> s;
-            const int h = n >> 1;
-            const bool hi = (lane & m) != 0;
-#pragma unroll
-            for (int j = 0; j < h; ++j) {
-                T send = hi ? v[j] : v[j + h];
-                T keep = hi ? v[j + h] : v[j];
-                v[j] = keep + __shfl_xor(send, m);
-            }
-        }
-#pragma unroll
-        for (int m = U; m < LPR; m <<= 1) v[0] += __shfl_xor(v[0], m);
-        return v[0];
+// Per-query constants stored after the query units (QLevelTail) and the
+// row-score finalisation.  `ord` is the order-preserving key word.
+struct QLevelTail {
+    double s[3];     // level scales (int8: already divided by 127)
+    int32_t sum[3];  // int4: sum of each level's query bytes
+    int32_t pad;
+};
+
+template <int C> struct Fin {
+    __device__ void load(const void *, uint32_t) {}
+    template <class Acc> __device__ __forceinline__ float score(const Acc *t, float scale, uint32_t &ord) const {
+        float sc;
+        if constexpr (C == C_F32L2 || C == C_F32L2_S) sc = -t[0];
+        else if constexpr (C == C_Q1A) sc = t[0] * scale;
+        else sc = t[0];
+        ord = ord_f32(sc);
+        return sc;
+    }
+};
+template <> struct Fin<C_HAM> {
+    int32_t P;
+    __device__ void load(const void *, uint32_t padded) { P = (int32_t)padded; }
+    __device__ __forceinline__ float score(const int32_t *t, float, uint32_t &ord) const {
+        const int32_t sim = P - 2 * t[0];
+        ord = ord_i32(sim);
+        return (float)sim;
+    }
+};
+template <> struct Fin<C_I8S> {
+    __device__ void load(const void *, uint32_t) {}
+    __device__ __forceinline__ float score(const int32_t *t, float, uint32_t &ord) const {
+        ord = ord_i32(t[0]);
+        return (float)t[0];
+    }
+};
+template <> struct Fin<C_Q8> {
+    double s0, s1, s2;
+    __device__ void load(const void *tail, uint32_t) {
+        const QLevelTail *q = (const QLevelTail *)tail;
+        s0 = q->s[0]; s1 = q->s[1]; s2 = q->s[2];
+    }
+    __device__ __forceinline__ float score(const int32_t *t, float scale, uint32_t &ord) const {
+        const double v = fma(s2, (double)t[2], fma(s1, (double)t[1], s0 * (double)t[0]));
+        const float sc = (float)(v * (double)scale);
+        ord = ord_f32(sc);
+        return sc;
+    }
+};
+template <> struct Fin<C_Q4> {
+    double s0, s1, s2;
+    int32_t c0, c1, c2;
+    __device__ void load(const void *tail, uint32_t) {
+        const QLevelTail *q = (const QLevelTail *)tail;
+        s0 = q->s[0]; s1 = q->s[1]; s2 = q->s[2];
+        c0 = 8 * q->sum[0]; c1 = 8 * q->sum[1]; c2 = 8 * q->sum[2];
+    }
+    __device__ __forceinline__ float score(const int32_t *t, float scale, uint32_t &ord) const {
+        const double v = fma(s2, (double)(t[2] - c2), fma(s1, (double)(t[1] - c1), s0 * (double)(t[0] - c0)));
+        const float sc = (float)(v * (double)scale);
+        ord = ord_f32(sc);
+        return sc;
     }
 };
 
-template <int U> __device__ __forceinline__ int bitrev_group(int p) {
-    int r = 0;
+// ------------------------------------------------------- wave reductions --
+// Cross-lane moves without LDS: DPP within 16-lane rows, and gfx950's
+// v_permlane{16,32}_swap across rows / halves.  All indices are compile-time.
+template <class T> __device__ __forceinline__ int as_i(T v) { return __builtin_bit_cast(int, v); }
+template <class T> __device__ __forceinline__ T from_i(int v) { return __builtin_bit_cast(T, v); }
+
+template <int CTRL, class T> __device__ __forceinline__ T dpp(T v) {
+    return from_i<T>(__builtin_amdgcn_update_dpp(0, as_i(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int DPP_XOR1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane ^ 7 within 8
+constexpr int DPP_MIRROR = 0x140;      // lane ^ 15 within 16
+constexpr int DPP_ROR8 = 0x128;        // lane ^ 8 within 16
+
+// v + (v of the partner lane that differs in lane bit B), for B = 0..5.
+template <int B, class T> __device__ __forceinline__ T plain_step(T v) {
+    if constexpr (B == 0) return v + dpp<DPP_XOR1>(v);
+    else if constexpr (B == 1) return v + dpp<DPP_XOR2>(v);
+    else if constexpr (B == 2) return v + dpp<DPP_HALF_MIRROR>(v);
+    else if constexpr (B == 3) return v + dpp<DPP_MIRROR>(v);
+    else if constexpr (B == 4) {
+        auto r = __builtin_amdgcn_permlane16_swap(as_i(v), as_i(v), false, false);
+        return from_i<T>(r[0]) + from_i<T>(r[1]);
+    } else {
+        auto r = __builtin_amdgcn_permlane32_swap(as_i(v), as_i(v), false, false);
+        return from_i<T>(r[0]) + from_i<T>(r[1]);
+    }
+}
+
+// One transposing exchange on lane bit B (5, 4 or 3): the lane with bit B
+// clear keeps rows [0,h) and the lane with it set keeps rows [h,2h); each
+// adds its partner's copy of the kept rows.
+template <int B, int H, class T> __device__ __forceinline__ void xpose_step(T *v, int lane) {
 #pragma unroll
-    for (int s = 0; (1 << s) < U; ++s)
-        if (p & (1 << s)) r |= (U >> (s + 1));
-    return r;
+    for (int j = 0; j < H; ++j) {
+        if constexpr (B == 5 || B == 4) {
+            auto r = (B == 5) ? __builtin_amdgcn_permlane32_swap(as_i(v[j]), as_i(v[j + H]), false, false)
+                              : __builtin_amdgcn_permlane16_swap(as_i(v[j]), as_i(v[j + H]), false, false);
+            v[j] = from_i<T>(r[0]) + from_i<T>(r[1]);
+        } else {
+            const bool hi = (lane >> B) & 1;
+            const T send = hi ? v[j] : v[j + H];
+            const T keep = hi ? v[j + H] : v[j];
+            v[j] = keep + dpp<DPP_ROR8>(send);
+        }
+    }
+}
+
+// Reduce U per-lane partials over an aligned group of LPR lanes.  Transposing
+// stages use lane bits log2(LPR)-1 downwards (one per halving of U); plain
+// stages cover the remaining low bits.  Afterwards every lane holds the full
+// sum of row group xrow<U, LPR>(lane); lanes with the low bits clear are the
+// distinct representatives.
+template <int U, int LPR> struct Lg {
+    static constexpr int lu = U == 1 ? 0 : U == 2 ? 1 : U == 4 ? 2 : 3;
+    static constexpr int ll = LPR == 4 ? 2 : LPR == 8 ? 3 : LPR == 16 ? 4 : LPR == 32 ? 5 : 6;
+    static constexpr int low = ll - lu;  // number of plain (low) bits
+};
+
+template <int U, int LPR, class T> __device__ __forceinline__ T xreduce(T (&v)[U], int lane) {
+    static_assert(Lg<U, LPR>::low >= 0, "U must not exceed LPR");
+    constexpr int ll = Lg<U, LPR>::ll;
+    if constexpr (U >= 2) xpose_step<ll - 1, U / 2>(v, lane);
+    if constexpr (U >= 4) xpose_step<ll - 2, U / 4>(v, lane);
+    if constexpr (U >= 8) xpose_step<ll - 3, U / 8>(v, lane);
+    T x = v[0];
+    constexpr int low = Lg<U, LPR>::low;
+    if constexpr (low > 0) x = plain_step<0>(x);
+    if constexpr (low > 1) x = plain_step<1>(x);
+    if constexpr (low > 2) x = plain_step<2>(x);
+    if constexpr (low > 3) x = plain_step<3>(x);
+    if constexpr (low > 4) x = plain_step<4>(x);
+    if constexpr (low > 5) x = plain_step<5>(x);
+    return x;
+}
+
+template <int U, int LPR> __device__ __forceinline__ int xrow(int lane) {
+    constexpr int ll = Lg<U, LPR>::ll;
+    int j = 0;
+    if constexpr (U >= 2) j += ((lane >> (ll - 1)) & 1) ? U / 2 : 0;
+    if constexpr (U >= 4) j += ((lane >> (ll - 2)) & 1) ? U / 4 : 0;
+    if constexpr (U >= 8) j += ((lane >> (ll - 3)) & 1) ? U / 8 : 0;
+    return j;
+}
+
+template <int U, int LPR> __device__ __forceinline__ bool xrep(int lane) {
+    return (lane & ((1 << Lg<U, LPR>::low) - 1)) == 0;
 }
 
 // ------------------------------------------------------- LDS top-k state --
+constexpr int SEL_BINS = 1024;  // histogram bins of the selection
+constexpr int SEL_TMP = 1024;   // gather buffer of the selection
+
+struct TopkLds {
+    uint64_t keys[SCAN_CAP];    // candidate keys
+    uint64_t tmp[SEL_TMP];      // selection gather buffer
+    uint32_t hist[SEL_BINS];
+    uint32_t red[16];           // cross-wave reduction slots
+    uint32_t ovl[SCAN_WG];      // workgroups to rescan (merge stage 3)
+    uint32_t cnt, cnt2, bstar, above, flag, last, grab;
+    uint64_t tau, gtau;
+};
+
 // Bitonic sort (descending) of keys[0, npow) by the whole workgroup.
 __device__ void bitonic_desc(uint64_t *keys, uint32_t npow) {
     const uint32_t tid = threadIdx.x, nt = blockDim.x;
@@ -188,11 +325,11 @@ __device__ void bitonic_desc(uint64_t *keys, uint32_t npow) {
             for (uint32_t i = tid; i < npow; i += nt) {
                 uint32_t ixj = i ^ j;
                 if (ixj > i) {
-                    uint64_t a = keys[i], b = keys[ixj];
+                    uint64_t x = keys[i], y = keys[ixj];
                     bool desc = (i & k) == 0;
-                    if (desc ? (a < b) : (a > b)) {
-                        keys[i] = b;
-                        keys[ixj] = a;
+                    if (desc ? (x < y) : (x > y)) {
+                        keys[i] = y;
+                        keys[ixj] = x;
                     }
                 }
             }
@@ -207,21 +344,136 @@ __device__ __forceinline__ uint32_t pow2_at_least(uint32_t n) {
     return p;
 }
 
-// Keep the best `kp` of keys[0, *cnt); tau becomes the kp-th best (or 0).
-// Must be called by the whole workgroup; cnt/tau live in LDS.
-__device__ void compact(uint64_t *keys, uint32_t *cnt, uint64_t *tau, uint32_t kp) {
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) v = max(v, (uint32_t)__shfl_xor((int)v, s));
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) v = min(v, (uint32_t)__shfl_xor((int)v, s));
+    return v;
+}
+
+// Keeps the best `kk` (>= 1) of L.keys[0, n) (unique, nonzero) in
+// L.keys[0, m), sorted descending, and returns m = min(n, kk).  Small inputs
+// are sorted outright; larger ones are binned by the score bits over their
+// actual range (1024 bins), the bin holding the kk-th key is located with a
+// suffix scan, and only keys from that bin upwards are gathered and sorted.
+// Whole workgroup; starts and ends with a barrier.
+__device__ __noinline__ uint32_t select_topk(TopkLds &L, uint32_t n, uint32_t kk) {
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nwaves = nt >> 6;
     __syncthreads();
-    const uint32_t n = *cnt;
-    const uint32_t npow = pow2_at_least(n);
-    for (uint32_t i = n + threadIdx.x; i < npow; i += blockDim.x) keys[i] = 0;
-    __syncthreads();
-    bitonic_desc(keys, npow);
-    if (threadIdx.x == 0) {
-        uint32_t m = n < kp ? n : kp;
-        *cnt = m;
-        *tau = (m == kp && kp > 0) ? keys[kp - 1] : 0;
+    if (n <= 256) {
+        // rank by counting: key i goes to slot #{keys greater than it}
+        uint64_t mine = 0;
+        uint32_t rank = 0;
+        if (tid < n) {
+            mine = L.keys[tid];
+            for (uint32_t j = 0; j < n; ++j) rank += L.keys[j] > mine ? 1u : 0u;
+        }
+        __syncthreads();
+        if (tid < n && rank < kk) L.keys[rank] = mine;
+        __syncthreads();
+        return n < kk ? n : kk;
     }
+    if (n <= kk) {
+        const uint32_t npow = pow2_at_least(n);
+        for (uint32_t i = n + tid; i < npow; i += nt) L.keys[i] = 0;
+        __syncthreads();
+        bitonic_desc(L.keys, npow);
+        return n;
+    }
+    // range of the high (score) words
+    uint32_t mx = 0, mn = 0xffffffffu;
+    for (uint32_t i = tid; i < n; i += nt) {
+        const uint32_t h = (uint32_t)(L.keys[i] >> 32);
+        mx = max(mx, h);
+        mn = min(mn, h);
+    }
+    mx = wave_max_u32(mx);
+    mn = wave_min_u32(mn);
+    if (lane == 0) {
+        L.red[wave] = mx;
+        L.red[8 + wave] = mn;
+    }
+    for (uint32_t b = tid; b < SEL_BINS; b += nt) L.hist[b] = 0;
     __syncthreads();
+    mx = 0;
+    mn = 0xffffffffu;
+    for (int w = 0; w < nwaves; ++w) {
+        mx = max(mx, L.red[w]);
+        mn = min(mn, L.red[8 + w]);
+    }
+    const uint32_t span = mx - mn;
+    uint32_t sh = 0;
+    while ((span >> sh) >= (uint32_t)SEL_BINS) ++sh;
+    for (uint32_t i = tid; i < n; i += nt)
+        atomicAdd(&L.hist[((uint32_t)(L.keys[i] >> 32) - mn) >> sh], 1u);
+    __syncthreads();
+    // b* = highest bin whose suffix count reaches kk (wave 0: 16 bins per lane)
+    if (wave == 0) {
+        constexpr int PER = SEL_BINS / 64;
+        uint32_t loc = 0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) loc += L.hist[lane * PER + j];
+        // inclusive suffix sum over lanes: T(l) = sum_{l' >= l} loc(l')
+        uint32_t T = loc;
+#pragma unroll
+        for (int s = 1; s < 64; s <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_down((int)T, s);
+            if (lane + s < 64) T += o;
+        }
+        const uint32_t Tnext = T - loc;  // suffix from the next lane up
+        if (Tnext < kk && T >= kk) {
+            uint32_t run = Tnext;
+            for (int j = PER - 1; j >= 0; --j) {
+                const uint32_t h = L.hist[lane * PER + j];
+                if (run + h >= kk) {
+                    L.bstar = lane * PER + j;
+                    L.above = run + h;  // keys in bins >= b*
+                    break;
+                }
+                run += h;
+            }
+        }
+    }
+    if (tid == 0) L.cnt2 = 0;
+    __syncthreads();
+    const uint32_t bstar = L.bstar, c = L.above;
+    if (c <= (uint32_t)SEL_TMP) {
+        for (uint32_t i = tid; i < n; i += nt) {
+            const uint64_t k = L.keys[i];
+            if ((((uint32_t)(k >> 32) - mn) >> sh) >= bstar) L.tmp[atomicAdd(&L.cnt2, 1u)] = k;
+        }
+        __syncthreads();
+        if (c <= nt) {
+            uint64_t mine = 0;
+            uint32_t rank = 0;
+            if (tid < c) {
+                mine = L.tmp[tid];
+                for (uint32_t j = 0; j < c; ++j) rank += L.tmp[j] > mine ? 1u : 0u;
+            }
+            __syncthreads();
+            if (tid < c && rank < kk) L.keys[rank] = mine;
+            __syncthreads();
+            return kk;
+        }
+        const uint32_t npow = pow2_at_least(c);
+        for (uint32_t i = c + tid; i < npow; i += nt) L.tmp[i] = 0;
+        __syncthreads();
+        bitonic_desc(L.tmp, npow);
+        for (uint32_t i = tid; i < kk; i += nt) L.keys[i] = L.tmp[i];
+        __syncthreads();
+        return kk;
+    }
+    // many keys share the k-th key's bin (ties): sort everything
+    const uint32_t npow = pow2_at_least(n);
+    for (uint32_t i = n + tid; i < npow; i += nt) L.keys[i] = 0;
+    __syncthreads();
+    bitonic_desc(L.keys, npow);
+    return kk;
 }
 
 // Wave-level append of keys for lanes where `take` holds.
@@ -240,182 +492,384 @@ __device__ __forceinline__ void wave_append(uint64_t *keys, uint32_t *cnt, bool 
 }
 
 // ------------------------------------------------------------ scan + top-k --
-template <int C, int LPR, int UPL>
-__global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
+// A unit slot past the end of a row (layouts whose lanes overhang the row)
+// must contribute nothing: zero query values do that for the dot-style codecs;
+// the l2 and Hamming codecs substitute a unit equal to the query itself.
+template <int C> struct Neutral {
+    template <class Unit, class QT> static __device__ __forceinline__ Unit get(Unit u, const QT *, bool ok) { return u; }
+};
+template <> struct Neutral<C_F32L2> {
+    static __device__ __forceinline__ uint4 get(uint4 u, const float *q, bool ok) {
+        return ok ? u : make_uint4(__float_as_uint(q[0]), __float_as_uint(q[1]), __float_as_uint(q[2]),
+                                   __float_as_uint(q[3]));
+    }
+};
+template <> struct Neutral<C_F32L2_S> {
+    static __device__ __forceinline__ uint32_t get(uint32_t u, const float *q, bool ok) {
+        return ok ? u : __float_as_uint(q[0]);
+    }
+};
+template <> struct Neutral<C_HAM> {
+    static __device__ __forceinline__ uint4 get(uint4 u, const uint32_t *q, bool ok) {
+        return ok ? u : make_uint4(q[0], q[1], q[2], q[3]);
+    }
+};
+
+// Rows are split across LPR lanes (each lane loads UPL 16-byte or 4-byte units
+// of a row; 64/LPR rows per load instruction).  Every step a wave issues all
+// U*UPL loads of its U row groups before any arithmetic, then reduces the
+// per-lane partial sums with the transposing butterfly.  IDX: rows come from
+// a candidate list (IVF probes) instead of being consecutive.
+// Per-lane constants of a scan: the query slice in registers and the
+// lane's place in the row layout.
+template <int C, int UPL> struct ScanRegs {
+    typename Codec<C>::QT qr[UPL][Codec<C>::QN];
+    bool uok[UPL];
+    uint32_t ucl[UPL];
+    Fin<C> fin;
+};
+
+// Compact the LDS buffer once it holds more than this many keys.
+constexpr uint32_t SCAN_TRIG = 256;
+
+template <int C, int LPR, int UPL> struct ScanShape {
+    static constexpr int U0 = UPL >= 4 ? 2 : (UPL >= 2 ? 4 : 8);
+    static constexpr int UMAX = LPR >= 64 ? 8 : LPR == 32 ? 4 : LPR == 16 ? 2 : 1;  // transposes on bits 5..3
+    static constexpr int U = U0 < UMAX ? U0 : UMAX;  // row groups per lane per step
+    static constexpr int G = 64 / LPR;               // rows per load instruction
+    static constexpr int WAVES = SCAN_WG / 64;
+    static constexpr int RPS = U * G;                // rows per wave step
+    static constexpr int GRAB_STEPS = 2;             // wave steps per work grab
+    static constexpr int GRAB_ROWS = WAVES * RPS * GRAB_STEPS;
+};
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+        const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), s) << 32) |
+                           (uint32_t)__shfl_xor((int)(uint32_t)v, s);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// Scans rows [r0, r1) (candidate slots when IDX): appends keys >= tau to
+// L.keys and folds every eligible key into the lane's running maximum `lmax`.
+// Rows are split across the workgroup's waves step by step.
+template <int C, int LPR, int UPL, bool IDX>
+__device__ __forceinline__ void scan_rows(const ScanArgs &a, const ScanRegs<C, UPL> &R, const uint32_t *cand,
+                                          uint64_t r0, uint64_t r1, uint64_t tau, TopkLds &L, uint64_t &lmax) {
     using CD = Codec<C>;
     using Unit = typename CD::Unit;
-    using QT = typename CD::QT;
     using Acc = typename CD::Acc;
-    constexpr int U = LPR < 8 ? LPR : 8;  // row groups per lane per step
-    constexpr int G = 64 / LPR;           // rows per load instruction
-    constexpr int WAVES = SCAN_WG / 64;
-    constexpr int RPS = U * G;            // rows per wave step
-
-    __shared__ uint64_t keys[SCAN_CAP];
-    __shared__ uint32_t cnt_s;
-    __shared__ uint64_t tau_s;
-    __shared__ uint32_t last_s;
-
-    const uint32_t qi = blockIdx.y;
+    using SH = ScanShape<C, LPR, UPL>;
+    constexpr int U = SH::U, G = SH::G, RPS = SH::RPS, WAVES = SH::WAVES;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int slot = lane / LPR, p = lane % LPR;
-
-    // query slice for the units this lane loads
-    QT qr[UPL][CD::QN];
-    const QT *qbase = (const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride);
-#pragma unroll
-    for (int t = 0; t < UPL; ++t) {
-        const uint32_t unit = p + LPR * t;
-#pragma unroll
-        for (int j = 0; j < CD::QN; ++j) qr[t][j] = unit < a.units ? qbase[unit * CD::QN + j] : (QT)0;
-    }
-
-    const uint32_t *cand = a.cand;
-    uint64_t n = a.n;
-    if (a.cand_off) {
-        cand = a.cand + a.cand_off[qi];
-        n = a.cand_off[qi + 1] - a.cand_off[qi];
-    }
-    const uint64_t r0 = (uint64_t)blockIdx.x * a.rows_per_wg;
-    const uint64_t r1 = r0 + a.rows_per_wg < n ? r0 + a.rows_per_wg : n;
-    const uint64_t span = r1 > r0 ? r1 - r0 : 0;
-    const uint32_t steps = (uint32_t)((span + RPS - 1) / RPS);
-    const uint32_t iters = (steps + WAVES - 1) / WAVES;
-    constexpr uint32_t period_rows = (uint32_t)(WAVES * RPS);
-    const uint32_t S = (SCAN_CAP / 2) / period_rows > 0 ? (SCAN_CAP / 2) / period_rows : 1;
-    const uint32_t kp = a.kprime;
-
-    if (tid == 0) {
-        cnt_s = 0;
-        tau_s = 0;
-    }
-    __syncthreads();
-    uint64_t tau = 0;
-    const int jrow = bitrev_group<U>(p & (U - 1));  // row group this lane ends up holding
-    const bool rep = p < U;
-
-    for (uint32_t it = 0; it < iters; ++it) {
-        const uint32_t step = it * WAVES + wave;
-        const uint64_t base = r0 + (uint64_t)step * RPS;
-        // scale / global row of the row this lane will hold after the reduction
-        const uint64_t myrow = base + (uint64_t)jrow * G + slot;
-        const bool myvalid = rep && myrow < r1;
-        uint32_t mygrow = 0;
-        float myscale = 1.0f;
-        if (myvalid) {
-            mygrow = cand ? cand[myrow] : (uint32_t)myrow;
-            if (a.scales) myscale = a.scales[mygrow] * a.scale_mul;
-        }
-        Acc acc[U];
+    const int slot = lane / LPR;
+    const char *codes = (const char *)a.codes;
+    const int jrow = xrow<U, LPR>(lane);
+    const bool rep = xrep<U, LPR>(lane);
+    for (uint64_t base = r0 + (uint64_t)wave * RPS; base < r1; base += (uint64_t)WAVES * RPS) {
+        Unit d[U][UPL];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            acc[u] = (Acc)0;
             const uint64_t row = base + (uint64_t)u * G + slot;
-            if (row < r1) {
-                const uint64_t grow = cand ? cand[row] : row;
-                const Unit *rp = (const Unit *)((const char *)a.codes + grow * a.row_bytes);
+            const uint64_t rc = row < r1 ? row : r1 - 1;
+            const uint64_t grow = IDX ? (uint64_t)cand[rc] : rc;
+            const Unit *rp = (const Unit *)(codes + grow * a.row_bytes);
 #pragma unroll
-                for (int t = 0; t < UPL; ++t) {
-                    const uint32_t unit = p + LPR * t;
-                    if (unit < a.units) acc[u] = CD::acc(rp[unit], qr[t], acc[u]);
-                }
-            }
+            for (int t = 0; t < UPL; ++t) d[u][t] = rp[R.ucl[t]];
         }
-        const Acc tot = XReduce<U, LPR, Acc>::run(acc, lane);
+        const uint64_t myrow = base + (uint64_t)jrow * G + slot;
+        const bool myvalid = rep && myrow < r1;
+        const uint64_t myrc = myrow < r1 ? myrow : r1 - 1;
+        const uint32_t mygrow = IDX ? cand[myrc] : (uint32_t)myrc;
+        const float myscale = a.scales ? a.scales[mygrow] * a.scale_mul : 1.0f;
+        Acc acc[CD::NA][U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            Acc a1[CD::NA];
+#pragma unroll
+            for (int m = 0; m < CD::NA; ++m) a1[m] = (Acc)0;
+#pragma unroll
+            for (int t = 0; t < UPL; ++t) CD::acc(Neutral<C>::get(d[u][t], R.qr[t], R.uok[t]), R.qr[t], a1);
+#pragma unroll
+            for (int m = 0; m < CD::NA; ++m) acc[m][u] = a1[m];
+        }
+        Acc tot[CD::NA];
+#pragma unroll
+        for (int m = 0; m < CD::NA; ++m) tot[m] = xreduce<U, LPR>(acc[m], lane);
         bool take = false;
         uint64_t key = 0;
         if (myvalid) {
             uint32_t ord;
-            float sc;
-            if constexpr (C == C_HAM) {
-                const int32_t sim = (int32_t)a.padded_dim - 2 * tot;
-                ord = ord_i32(sim);
-                sc = (float)sim;
-            } else if constexpr (C == C_I8S) {
-                ord = ord_i32(tot);
-                sc = (float)tot;
-            } else {
-                sc = CD::score(tot, myscale);
-                ord = ord_f32(sc);
-            }
-            if (a.dense_out && qi == 0) a.dense_out[myrow] = sc;
+            const float sc = R.fin.score(tot, myscale, ord);
+            if (a.dense_out && blockIdx.y == 0) a.dense_out[myrow] = sc;
             bool pass = true;
             if (a.mask) pass = mygrow < a.mask_bits && ((a.mask[mygrow >> 5] >> (mygrow & 31)) & 1u);
-            key = make_key(ord, mygrow);
-            take = pass && key > tau;
-        }
-        wave_append(keys, &cnt_s, take, key, lane);
-        if ((it + 1) % S == 0 || it + 1 == iters) {
-            __syncthreads();
-            if (it + 1 < iters && cnt_s > SCAN_CAP - S * period_rows) compact(keys, &cnt_s, &tau_s, kp);
-            __syncthreads();
-            tau = tau_s;
-        }
-    }
-    compact(keys, &cnt_s, &tau_s, kp);
-
-    // publish this workgroup's sorted top-kp
-    uint64_t *mine = a.partials + ((uint64_t)qi * a.grid + blockIdx.x) * kp;
-    const uint32_t have = cnt_s;
-    for (uint32_t j = tid; j < kp; j += SCAN_WG) mine[j] = j < have ? keys[j] : 0;
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last_s = atomicAdd(&a.tickets[qi], 1u) == a.grid - 1;
-    __syncthreads();
-    if (!last_s) return;
-    __threadfence();
-
-    // ---- last workgroup of this query: merge all partial lists --------------
-    const uint64_t *lists = a.partials + (uint64_t)qi * a.grid * kp;
-    if (tid == 0) {
-        cnt_s = 0;
-        tau_s = 0;
-    }
-    __syncthreads();
-    // stage 1: each list's best key
-    for (uint32_t g = tid; g < a.grid; g += SCAN_WG) {
-        const uint64_t k0 = __builtin_nontemporal_load(&lists[(uint64_t)g * kp]);
-        if (k0) keys[atomicAdd(&cnt_s, 1u)] = k0;
-    }
-    compact(keys, &cnt_s, &tau_s, kp);
-    tau = tau_s;
-    // stage 2: walk every list downwards while its keys beat tau
-    const uint32_t R = (SCAN_CAP / 2) / a.grid > 0 ? ((SCAN_CAP / 2) / a.grid < 8 ? (SCAN_CAP / 2) / a.grid : 8) : 1;
-    constexpr int MAXL = MAX_GRID / SCAN_WG;
-    bool alive[MAXL];
-#pragma unroll
-    for (int m = 0; m < MAXL; ++m) alive[m] = (uint32_t)(tid + m * SCAN_WG) < a.grid;
-    for (uint32_t j0 = 1; j0 < kp; j0 += R) {
-        bool any = false;
-#pragma unroll
-        for (int m = 0; m < MAXL; ++m) {
-            if (!alive[m]) continue;
-            const uint32_t g = tid + m * SCAN_WG;
-            for (uint32_t r = 0; r < R && j0 + r < kp; ++r) {
-                const uint64_t kk = __builtin_nontemporal_load(&lists[(uint64_t)g * kp + j0 + r]);
-                if (kk <= tau) {
-                    alive[m] = false;
-                    break;
-                }
-                keys[atomicAdd(&cnt_s, 1u)] = kk;
+            if (pass) {
+                key = make_key(ord, mygrow);
+                take = key >= tau;
+                lmax = key > lmax ? key : lmax;
             }
-            any = any || alive[m];
+        }
+        wave_append(L.keys, &L.cnt, take, key, lane);
+    }
+}
+
+// Publishes the wave's running maximum to wmax[slot] when it grew.
+__device__ __forceinline__ void publish_wave_max(uint64_t *wslot, uint64_t lmax, uint64_t &published, int lane) {
+    const uint64_t w = wave_max_u64(lmax);
+    if (w > published) {
+        published = w;
+        if (lane == 0) __hip_atomic_store(wslot, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Zeroes a query's coordination state and wave maxima (run by whichever of
+// the final selection and the helper finishes last).
+__device__ void reset_query(const ScanArgs &a, uint32_t qi) {
+    QState *qs = a.qs + qi;
+    uint64_t *wm = a.wmax + (uint64_t)qi * a.grid * (SCAN_WG / 64);
+    for (uint32_t i = threadIdx.x; i < a.grid * (SCAN_WG / 64); i += blockDim.x) wm[i] = 0;
+    for (uint32_t r = threadIdx.x; r < (uint32_t)NGROUP; r += blockDim.x) {
+        qs->done[r * CL] = 0;
+        qs->cc[r * CL] = 0;
+    }
+    if (threadIdx.x == 0) {
+        qs->tau = 0;
+        qs->top = 0;
+        qs->fin = 0;
+    }
+}
+
+__device__ __forceinline__ uint32_t group_size(uint32_t grid, uint32_t ng, uint32_t r) {
+    return grid / ng + (r < grid % ng ? 1u : 0u);
+}
+
+// Background threshold: the kprime-th best of the per-wave running maxima
+// is the key of a real row no better than the true kprime-th best, so every
+// scan may drop keys below it.  Recomputed until all scanning workgroups are
+// done; each round only gathers maxima at or above the previous bound (the
+// maxima only grow, so the new top-kprime is always among them).
+__device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
+    QState *qs = a.qs + qi;
+    const uint32_t nslots = a.grid * (SCAN_WG / 64);
+    const uint64_t *wm = a.wmax + (uint64_t)qi * nslots;
+    const uint32_t kp = a.kprime;
+    const uint32_t ng = a.grid < (uint32_t)NGROUP ? a.grid : (uint32_t)NGROUP;
+    const int tid = threadIdx.x;
+    if (kp > (uint32_t)SCAN_WG) return;  // the bound below ranks at most SCAN_WG keys
+    uint64_t th = 0;
+    for (int round = 0; round < (1 << 22); ++round) {
+        if (tid == 0) {
+            L.flag = __hip_atomic_load(&qs->top, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            L.cnt = 0;
         }
         __syncthreads();
-        if (cnt_s > SCAN_CAP / 2) compact(keys, &cnt_s, &tau_s, kp);
-        tau = tau_s;
-        if (!__syncthreads_or(any)) break;
+        const uint32_t top = L.flag;
+        // any SCAN_WG maxima at or above the current bound: the kp-th best of
+        // any set of real rows is a valid bound, and keeping only keys above
+        // the previous one makes it increase every round
+        for (uint32_t i0 = 0; i0 < nslots; i0 += 8 * SCAN_WG) {
+            uint64_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t i = i0 + j * SCAN_WG + tid;
+                v[j] = i < nslots ? __hip_atomic_load(&wm[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (v[j] != 0 && v[j] >= th) {
+                    const uint32_t slot = atomicAdd(&L.cnt, 1u);
+                    if (slot < (uint32_t)SCAN_WG) L.keys[slot] = v[j];
+                }
+            }
+        }
+        __syncthreads();
+        const uint32_t have = L.cnt < (uint32_t)SCAN_WG ? L.cnt : (uint32_t)SCAN_WG;
+        if (have >= kp) {
+            const uint32_t m = select_topk(L, have, kp);
+            const uint64_t t = L.keys[m - 1];
+            if (t > th) {
+                th = t;
+                if (tid == 0) atomicMax(&qs->tau, (unsigned long long)t);
+            }
+        }
+        __syncthreads();
+        if (top >= ng) break;
     }
-    compact(keys, &cnt_s, &tau_s, kp);
-    const uint32_t m = cnt_s;
+}
+
+// Fused scan + top-k (one launch per query batch).  Workgroups 0..grid-1
+// take row blocks round-robin (block b goes to workgroup b % grid), keep keys at or above the running threshold in LDS (compacting to
+// the best kprime), and publish their waves' running maxima.  Workgroup
+// `grid` is the threshold helper.  Each scanning workgroup finally flushes
+// its keys at or above the published threshold to a global array; the last
+// one to finish selects the best kprime from that array.
+template <int C, int LPR, int UPL, bool IDX>
+__global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
+    using CD = Codec<C>;
+    using QT = typename CD::QT;
+    using SH = ScanShape<C, LPR, UPL>;
+    __shared__ TopkLds L;
+
+    const uint32_t qi = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    QState *qs = a.qs + qi;
+    const uint32_t kp = a.kprime;
+
+    if (blockIdx.x == a.grid) {
+        threshold_helper(a, qi, L);
+        __syncthreads();
+        if (tid == 0) L.last = atomicAdd(&qs->fin, 1u) == 1;
+        __syncthreads();
+        if (L.last) reset_query(a, qi);
+        return;
+    }
+
+    const int p = lane % LPR;
+    ScanRegs<C, UPL> R;
+    const QT *qbase = (const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride);
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+        const uint32_t unit = p + LPR * t;
+        R.uok[t] = unit < a.units;
+        R.ucl[t] = R.uok[t] ? unit : a.units - 1;
+#pragma unroll
+        for (int j = 0; j < CD::QN; ++j) R.qr[t][j] = R.uok[t] ? qbase[unit * CD::QN + j] : (QT)0;
+    }
+    R.fin.load((const char *)qbase + (uint64_t)a.units * CD::QN * sizeof(QT), a.padded_dim);
+
+    const uint32_t *cand = a.cand;
+    uint64_t n = a.n;
+    if (IDX && a.cand_off) {
+        cand = a.cand + a.cand_off[qi];
+        n = a.cand_off[qi + 1] - a.cand_off[qi];
+    }
+    uint64_t *wslot = a.wmax + ((uint64_t)qi * a.grid + blockIdx.x) * SH::WAVES + wave;
+    uint64_t lmax = 0, published = 0;
+
+    if (tid == 0) {
+        L.cnt = 0;
+        L.tau = 0;
+    }
+    __syncthreads();
+    // grabs g, g + grid, g + 2*grid, ... of GRAB_ROWS rows each
+    for (uint64_t g = blockIdx.x;; g += a.grid) {
+        const uint64_t r0 = g * SH::GRAB_ROWS;
+        if (r0 >= n) break;
+        const uint64_t r1 = r0 + SH::GRAB_ROWS < n ? r0 + SH::GRAB_ROWS : n;
+        const uint64_t tau = L.tau;
+        uint64_t gt = 0;
+        if (tid == 0) gt = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        scan_rows<C, LPR, UPL, IDX>(a, R, cand, r0, r1, tau, L, lmax);
+        publish_wave_max(wslot, lmax, published, lane);
+        if (tid == 0) L.gtau = gt;
+        __syncthreads();
+        if (L.cnt > SCAN_TRIG) {
+            const uint32_t m = select_topk(L, L.cnt, kp);
+            if (tid == 0) {
+                L.cnt = m;
+                if (m == kp && L.keys[kp - 1] > L.tau) L.tau = L.keys[kp - 1];
+            }
+        }
+        if (tid == 0 && L.gtau > L.tau) L.tau = L.gtau;
+        __syncthreads();
+    }
+    // bound the flush to kprime keys, then flush those at or above the bound
+    if (L.cnt > kp) {
+        const uint32_t m = select_topk(L, L.cnt, kp);
+        if (tid == 0) L.cnt = m;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const uint64_t gt = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        L.gtau = gt > L.tau ? gt : L.tau;
+        L.cnt2 = 0;
+    }
+    __syncthreads();
+    const uint32_t have = L.cnt;
+    const uint64_t fl = L.gtau;
+    uint32_t myk = 0;
+    uint64_t mykeys[MAX_KPRIME / SCAN_WG];
+    for (uint32_t j = tid; j < have; j += SCAN_WG) {
+        const uint64_t k = L.keys[j];
+        if (k >= fl) mykeys[myk++] = k;
+    }
+    uint32_t off = 0;
+    if (myk) off = atomicAdd(&L.cnt2, myk);
+    __syncthreads();
+    const uint32_t ng = a.grid < (uint32_t)NGROUP ? a.grid : (uint32_t)NGROUP;
+    const uint32_t grp = blockIdx.x % ng;
+    const uint64_t region = (uint64_t)((a.grid + ng - 1) / ng) * kp;  // keys per group region
+    if (tid == 0) L.bstar = L.cnt2 ? atomicAdd(&qs->cc[grp * CL], L.cnt2) : 0;
+    __syncthreads();
+    uint64_t *ck = a.cand_keys + (uint64_t)qi * a.cand_cap + grp * region;
+    for (uint32_t j = 0; j < myk; ++j) ck[L.bstar + off + j] = mykeys[j];
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        // two-level ticket: the workgroup completing its group bumps `top`;
+        // the one completing `top` runs the final selection
+        bool last = false;
+        if (atomicAdd(&qs->done[grp * CL], 1u) == group_size(a.grid, ng, grp) - 1) {
+            __threadfence();
+            last = atomicAdd(&qs->top, 1u) == ng - 1;
+        }
+        L.last = last;
+    }
+    __syncthreads();
+    if (!L.last) return;
+    __threadfence();
+
+    // ---- last scanning workgroup: select the best kprime of the flushes ----
+    if (tid == 0) {
+        L.cnt = 0;
+        L.tau = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid < ng) L.ovl[tid] = __hip_atomic_load(&qs->cc[tid * CL], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (tid == 0) {
+        // exclusive prefix of the per-group counts in ovl[32..64]
+        uint32_t acc = 0;
+        for (uint32_t r = 0; r < ng; ++r) {
+            L.ovl[32 + r] = acc;
+            acc += (uint32_t)L.ovl[r];
+        }
+        L.ovl[32 + ng] = acc;
+    }
+    __syncthreads();
+    const uint64_t *ckq = a.cand_keys + (uint64_t)qi * a.cand_cap;
+    const uint32_t total = (uint32_t)L.ovl[32 + ng];
+    for (uint32_t c0 = 0; c0 < total; c0 += SCAN_CAP / 2) {
+        const uint64_t th = L.tau;
+        for (uint32_t i = c0 + tid; i < total && i < c0 + SCAN_CAP / 2; i += SCAN_WG) {
+            uint32_t r = 0;
+            while (r + 1 < ng && (uint32_t)L.ovl[32 + r + 1] <= i) ++r;
+            const uint64_t k = __builtin_nontemporal_load(&ckq[r * region + (i - (uint32_t)L.ovl[32 + r])]);
+            if (k >= th) L.keys[atomicAdd(&L.cnt, 1u)] = k;
+        }
+        __syncthreads();
+        if (L.cnt > (uint32_t)(SCAN_CAP / 2)) {
+            const uint32_t m = select_topk(L, L.cnt, kp);
+            if (tid == 0) {
+                L.cnt = m;
+                if (m == kp && L.keys[kp - 1] > L.tau) L.tau = L.keys[kp - 1];
+            }
+            __syncthreads();
+        }
+    }
+    const uint32_t m = select_topk(L, L.cnt, kp);
     uint64_t *outk = a.merged + (uint64_t)qi * kp;
-    for (uint32_t j = tid; j < kp; j += SCAN_WG) outk[j] = j < m ? keys[j] : 0;
+    for (uint32_t j = tid; j < kp; j += SCAN_WG) outk[j] = j < m ? L.keys[j] : 0;
     if (tid == 0) a.merged_n[qi] = m;
     if (a.out_rows) {
         const uint32_t ko = m < a.k_out ? m : a.k_out;
         for (uint32_t j = tid; j < ko; j += SCAN_WG) {
-            const uint64_t kk = keys[j];
+            const uint64_t kk = L.keys[j];
             a.out_rows[(uint64_t)qi * a.k_out + j] = key_row(kk);
             const uint32_t o = (uint32_t)(kk >> 32);
             a.out_scores[(uint64_t)qi * a.k_out + j] =
@@ -423,7 +877,10 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         }
         if (tid == 0) a.out_n[qi] = ko;
     }
-    if (tid == 0) a.tickets[qi] = 0;
+    __syncthreads();
+    if (tid == 0) L.last = atomicAdd(&qs->fin, 1u) == 1;
+    __syncthreads();
+    if (L.last) reset_query(a, qi);
 }
 
 // ---------------------------------------------------------------- encode --
@@ -570,6 +1027,76 @@ __global__ __launch_bounds__(128) void encode_rows(EncodeArgs a) {
     }
 }
 
+// ---------------------------------------------------------- query levels --
+// Splits each rotated query into three int8 levels (q ~= s1*q1 + s2*q2 +
+// s3*q3, each level quantizing the previous residual) and packs them in the
+// per-unit layout the int8 / int4 scan codecs read.  One wave per query.
+__global__ __launch_bounds__(64) void query_levels(LevelArgs a) {
+    extern __shared__ unsigned char lsm[];
+    const uint32_t P = a.P, qi = blockIdx.x;
+    const int lane = threadIdx.x;
+    signed char *lv = (signed char *)lsm;                   // 3 x P codes
+    double *rd = (double *)(lsm + ((3 * (size_t)P + 15) & ~(size_t)15));  // P residuals
+    const float *q = a.qrot + (uint64_t)qi * P;
+    for (uint32_t e = lane; e < P; e += 64) rd[e] = (double)q[e];
+    __syncthreads();
+    double sl[3];
+    int32_t sums[3];
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+        double m = 0.0;
+        for (uint32_t e = lane; e < P; e += 64) m = fmax(m, fabs(rd[e]));
+#pragma unroll
+        for (int sh = 1; sh < 64; sh <<= 1) m = fmax(m, __shfl_xor(m, sh));
+        const double sc = m > 0.0 ? m / 127.0 : 0.0;
+        int32_t sum = 0;
+        for (uint32_t e = lane; e < P; e += 64) {
+            double c = sc > 0.0 ? rint(rd[e] / sc) : 0.0;
+            c = c > 127.0 ? 127.0 : (c < -127.0 ? -127.0 : c);
+            rd[e] = fma(-sc, c, rd[e]);
+            lv[l * P + e] = (signed char)(int)c;
+            sum += (int)c;
+        }
+#pragma unroll
+        for (int sh = 1; sh < 64; sh <<= 1) sum += __shfl_xor(sum, sh);
+        sl[l] = sc;
+        sums[l] = sum;
+    }
+    __syncthreads();
+    unsigned char *out = a.out + (uint64_t)qi * a.stride;
+    uint32_t *w = (uint32_t *)out;
+    const unsigned char *lb = (const unsigned char *)lv;
+    uint32_t qwords;
+    if (a.codec == C_Q8) {
+        const uint32_t units = P / 16;
+        qwords = units * 12;
+        for (uint32_t i = lane; i < qwords; i += 64) {
+            const uint32_t u = i / 12, r = i % 12, l = r / 4, d = r % 4;
+            const uint32_t base = l * P + 16 * u + 4 * d;
+            w[i] = (uint32_t)lb[base] | ((uint32_t)lb[base + 1] << 8) | ((uint32_t)lb[base + 2] << 16) |
+                   ((uint32_t)lb[base + 3] << 24);
+        }
+    } else {  // C_Q4
+        const uint32_t units = P / 32;
+        qwords = units * 24;
+        for (uint32_t i = lane; i < qwords; i += 64) {
+            const uint32_t u = i / 24, r = i % 24, l = r / 8, d = (r % 8) / 2, h = r % 2;
+            const uint32_t base = l * P + 32 * u + 8 * d + h;
+            w[i] = (uint32_t)lb[base] | ((uint32_t)lb[base + 2] << 8) | ((uint32_t)lb[base + 4] << 16) |
+                   ((uint32_t)lb[base + 6] << 24);
+        }
+    }
+    if (lane == 0) {
+        QLevelTail *t = (QLevelTail *)(out + (uint64_t)qwords * 4);
+        const double div = a.codec == C_Q8 ? 127.0 : 1.0;
+        for (int l = 0; l < 3; ++l) {
+            t->s[l] = sl[l] / div;
+            t->sum[l] = sums[l];
+        }
+        t->pad = 0;
+    }
+}
+
 // ---------------------------------------------------------------- rerank --
 // One wave per candidate: stage the row and query in LDS, then four lanes run
 // Store.dotRow's four strided f64 accumulators (store.ts:114-130).  The last
@@ -683,7 +1210,10 @@ bool pick_layout(uint32_t units, Layout &L) {
 
 template <int C, int LPR, int UPL>
 hipError_t go(const ScanArgs &a, uint32_t nq, hipStream_t s) {
-    hipLaunchKernelGGL((scan_topk<C, LPR, UPL>), dim3(a.grid, nq), dim3(SCAN_WG), 0, s, a);
+    if (a.cand)
+        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, true>), dim3(a.grid + 1, nq), dim3(SCAN_WG), 0, s, a);
+    else
+        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, false>), dim3(a.grid + 1, nq), dim3(SCAN_WG), 0, s, a);
     return hipGetLastError();
 }
 
@@ -717,7 +1247,7 @@ bool scan_supported(int codec, uint32_t units) {
     Layout L;
     if (!pick_layout(units, L)) return false;
     // register budget: at most 64 query values per lane
-    static const int qn[C_COUNT] = {4, 4, 16, 32, 32, 4, 4, 1, 1};
+    static const int qn[C_COUNT] = {4, 4, 12, 24, 32, 4, 4, 1, 1};
     return codec >= 0 && codec < C_COUNT && L.upl * qn[codec] <= 64;
 }
 
@@ -757,6 +1287,18 @@ hipError_t launch_encode(const EncodeArgs &a, hipStream_t s) {
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_levels(const LevelArgs &a, uint32_t nq, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    const size_t lds = ((3 * (size_t)a.P + 15) & ~(size_t)15) + 8 * (size_t)a.P;
+    hipLaunchKernelGGL(query_levels, dim3(nq), dim3(64), lds, s, a);
+    return hipGetLastError();
+}
+
+size_t level_stride(int codec, uint32_t P) {
+    const size_t words = codec == C_Q8 ? (size_t)P / 16 * 12 : (size_t)P / 32 * 24;
+    return (words * 4 + sizeof(QLevelTail) + 63) & ~(size_t)63;
 }
 
 hipError_t launch_rerank(const RerankArgs &a, uint32_t nq, hipStream_t s) {

@@ -349,3 +349,33 @@ def test_browservec_api(ctx):
         st = db.stats()
         assert st["count"] == 999 and st["deleted"] == 1
         db.destroy()
+
+
+@pytest.mark.parametrize("bits", [8, 0])
+def test_topk_when_best_rows_share_a_workgroup(ctx, bits):
+    """The 300 best rows sit next to each other, so one workgroup holds far
+    more of the top-k than its local list keeps; the merge must rescan it and
+    still return the exact top-k of the device's scores."""
+    from browservec_amd import FlatIndex, QuantIndex
+
+    say("concentrated top-k", bits)
+    dim, n = 256, 100_000
+    rng = np.random.default_rng(8)
+    q = gaussian(1, dim, 81)[0]
+    data = gaussian(n, dim, 82)
+    near = q[None, :] + 0.02 * rng.standard_normal((300, dim)).astype(np.float32)
+    o.normalize_rows_store(near)
+    data[1000:1300] = near
+    idx = QuantIndex(ctx, dim, bits=8) if bits else FlatIndex(ctx, dim, "cosine")
+    idx.append(data, n)
+    dense = idx.export_scores(q)
+    for k in (100, 250, 17):
+        hits = idx.query(q, k)
+        er, es = o.topk_canonical(dense, k)
+        assert [h.row for h in hits] == er.tolist(), k
+    if bits:
+        rows, scores, cnt = idx.search(q[None], 200, 10)
+        exact = o.rerank_scores(data, q, rows[0])
+        assert np.array_equal(exact, scores[0])
+        assert set(rows[0].tolist()) <= set(range(1000, 1300))
+    idx.destroy()
