@@ -126,7 +126,7 @@ struct bv_index {
     // per-call scratch
     DevBuf qin, qrot, qscan, qscale, mask;
     DevBuf qstate, wmax, cand_keys, merged, merged_n;
-    DevBuf rr_scores, rr_rows, rr_tickets;
+    DevBuf rr_keys, rr_tickets;
     DevBuf out_rows, out_scores, out_n;
     DevBuf cand, cand_n, dense;
     HostBuf h_rows, h_scores, h_n;
@@ -395,15 +395,10 @@ extern "C" int bv_index_append_device(bv_index *idx, const float *d_data, uint64
 }
 
 // ---------------------------------------------------------------- queries
-static uint32_t grid_for(uint64_t n, uint32_t *rows_per_wg) {
-    uint64_t g = (n + 255) / 256;
+static uint32_t grid_for(uint64_t n) {
+    uint64_t g = (n + 255) / 256;  // at least 256 rows per workgroup
     if (g < 1) g = 1;
-    if (g > (uint64_t)MAX_GRID) g = MAX_GRID;
-    uint64_t rpw = (n + g - 1) / g;
-    if (rpw < 1) rpw = 1;
-    g = (n + rpw - 1) / rpw;
-    if (g < 1) g = 1;
-    *rows_per_wg = (uint32_t)rpw;
+    if (g > (uint64_t)SCAN_GRID) g = SCAN_GRID;
     return (uint32_t)g;
 }
 
@@ -423,7 +418,8 @@ static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kpri
         if (idx->wmax.cap != old) HIPX(idx->dev, hipMemsetAsync(idx->wmax.p, 0, idx->wmax.cap, idx->stream), "scratch");
     }
     const uint64_t ng = grid < (uint32_t)NGROUP ? grid : (uint32_t)NGROUP;
-    const uint64_t cap = ng * ((grid + ng - 1) / ng) * kprime;
+    const uint32_t wcap = scan_wcap(kprime);
+    const uint64_t cap = ng * ((grid + ng - 1) / ng) * (SCAN_WG / 64) * wcap;
     HIPX(idx->dev, idx->cand_keys.ensure((size_t)nq * cap * 8, 0, idx->stream), "scratch");
     HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
     HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
@@ -431,6 +427,7 @@ static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kpri
     a.wmax = idx->wmax.as<uint64_t>();
     a.cand_keys = idx->cand_keys.as<uint64_t>();
     a.cand_cap = cap;
+    a.wcap = wcap;
     a.merged = idx->merged.as<uint64_t>();
     a.merged_n = idx->merged_n.as<uint32_t>();
     return BV_OK;
@@ -534,9 +531,8 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
     uint64_t qstride = 0;
     int rc = prepare_queries(idx, d_q, nq, &qscan, &qstride);
     if (rc) return rc;
-    uint32_t rpw = 0;
     const uint64_t n = idx->rows;
-    const uint32_t grid = grid_for(n, &rpw);
+    const uint32_t grid = grid_for(n);
     ScanArgs a{};
     rc = scan_scratch(idx, nq, grid, kprime, a);
     if (rc) return rc;
@@ -552,7 +548,6 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
     a.mask_bits = mask_bits;
     a.n = n;
     a.kprime = kprime;
-    a.rows_per_wg = rpw;
     a.grid = grid;
     if (!rerank) {
         a.k_out = k_out;
@@ -565,8 +560,7 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
     timing_end(idx);
     idx->last_scanned = n * nq;
     if (rerank) {
-        HIPX(idx->dev, idx->rr_scores.ensure((size_t)nq * kprime * 4, 0, idx->stream), "scratch");
-        HIPX(idx->dev, idx->rr_rows.ensure((size_t)nq * kprime * 4, 0, idx->stream), "scratch");
+        HIPX(idx->dev, idx->rr_keys.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
         const size_t old = idx->rr_tickets.cap;
         HIPX(idx->dev, idx->rr_tickets.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
         if (idx->rr_tickets.cap != old)
@@ -580,8 +574,7 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
         r.merged_n = idx->merged_n.as<uint32_t>();
         r.kprime = kprime;
         r.k_out = k_out;
-        r.rr_scores = idx->rr_scores.as<float>();
-        r.rr_rows = idx->rr_rows.as<uint32_t>();
+        r.rr_keys = idx->rr_keys.as<uint64_t>();
         r.tickets = idx->rr_tickets.as<uint32_t>();
         r.out_rows = d_rows;
         r.out_scores = d_scores;
@@ -800,8 +793,7 @@ extern "C" int bv_index_rerank(bv_index *idx, const float *q, const uint32_t *ca
     HIPX(idx->dev, hipMemcpyAsync(idx->cand.p, cand, (size_t)n_cand * 4, hipMemcpyHostToDevice, idx->stream), "upload");
     HIPX(idx->dev, idx->cand_n.ensure(4, 0, idx->stream), "scratch");
     HIPX(idx->dev, hipMemcpyAsync(idx->cand_n.p, &n_cand, 4, hipMemcpyHostToDevice, idx->stream), "upload");
-    HIPX(idx->dev, idx->rr_scores.ensure((size_t)n_cand * 4, 0, idx->stream), "scratch");
-    HIPX(idx->dev, idx->rr_rows.ensure((size_t)n_cand * 4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->rr_keys.ensure((size_t)n_cand * 8, 0, idx->stream), "scratch");
     {
         const size_t old = idx->rr_tickets.cap;
         HIPX(idx->dev, idx->rr_tickets.ensure(4, 0, idx->stream), "scratch");
@@ -820,8 +812,7 @@ extern "C" int bv_index_rerank(bv_index *idx, const float *q, const uint32_t *ca
     r.cand_n = idx->cand_n.as<uint32_t>();
     r.kprime = n_cand;
     r.k_out = kk;
-    r.rr_scores = idx->rr_scores.as<float>();
-    r.rr_rows = idx->rr_rows.as<uint32_t>();
+    r.rr_keys = idx->rr_keys.as<uint64_t>();
     r.tickets = idx->rr_tickets.as<uint32_t>();
     r.out_rows = idx->out_rows.as<uint32_t>();
     r.out_scores = idx->out_scores.as<float>();
@@ -845,8 +836,7 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     uint64_t qstride = 0;
     int rc = prepare_queries(idx, idx->qin.as<float>(), 1, &qscan, &qstride);
     if (rc) return rc;
-    uint32_t rpw = 0;
-    const uint32_t grid = grid_for(idx->rows, &rpw);
+    const uint32_t grid = grid_for(idx->rows);
     const uint32_t *d_mask = nullptr;
     if (mask) {
         HIPX(idx->dev, idx->mask.ensure(mask_words * 4, 0, idx->stream), "mask buffer");
@@ -868,7 +858,6 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     a.mask_bits = mask_words * 32;
     a.n = idx->rows;
     a.kprime = 1;
-    a.rows_per_wg = rpw;
     a.grid = grid;
     a.dense_out = idx->dense.as<float>();
     HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, 1, idx->stream), "scan kernel");

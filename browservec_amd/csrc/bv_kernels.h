@@ -24,8 +24,16 @@ enum CodecId : int {
 constexpr int SCAN_WG = 256;      // 4 waves
 constexpr int SCAN_CAP = 2048;    // LDS candidate keys per workgroup
 constexpr int MAX_KPRIME = 1024;  // largest fetch the fused top-k serves
-constexpr int MAX_GRID = 1024;    // workgroups per query
-constexpr int LOCAL_K = 16;       // best keys each workgroup keeps
+constexpr int MAX_GRID = 1024;    // workgroups per query (bound of the wave-maxima scratch)
+constexpr int SCAN_GRID = 512;    // scanning workgroups per query for large row counts
+
+// Per-wave candidate list capacity of the fused scan for a fetch of kp:
+// twice kp plus room for one grab, at least 256 keys, a multiple of 64.
+inline uint32_t scan_wcap(uint32_t kp) {
+    uint32_t c = 2 * kp + 64;
+    if (c < 256) c = 256;
+    return (c + 63) & ~63u;
+}
 
 // Per-query coordination state of the fused scan (zero before first use;
 // the kernel leaves it zeroed).  Counters that many workgroups update sit in
@@ -57,12 +65,12 @@ struct ScanArgs {
     uint64_t mask_bits;
     uint64_t n;               // rows per query when cand_off is null
     uint32_t kprime;          // per-query candidates kept
-    uint32_t rows_per_wg;
+    uint32_t wcap;            // per-wave LDS list capacity, scan_wcap(kprime)
     uint32_t grid;            // scanning workgroups per query (one more runs the threshold helper)
     QState *qs;               // [nq]
     uint64_t *wmax;           // [nq][grid*4] per-wave running maxima (zero on entry and exit)
     uint64_t *cand_keys;      // [nq][cand_cap] flushed candidate keys
-    uint64_t cand_cap;        // >= NGROUP regions of ceil(grid/NGROUP)*kprime keys
+    uint64_t cand_cap;        // min(grid,NGROUP) regions of ceil(grid/NGROUP)*4*wcap keys
     uint64_t *merged;         // [nq][kprime] merged keys, descending
     uint32_t *merged_n;       // [nq]
     float *dense_out;         // optional: every row's score (query 0 only)
@@ -98,8 +106,7 @@ struct RerankArgs {
     const uint32_t *cand_n;   // [nq] counts for cand_rows
     uint32_t kprime;
     uint32_t k_out;
-    float *rr_scores;         // scratch [nq][kprime]
-    uint32_t *rr_rows;        // scratch [nq][kprime]
+    uint64_t *rr_keys;        // scratch [nq][kprime]: re-ranked (score, row) keys
     uint32_t *tickets;        // [nq]
     uint32_t *out_rows;       // [nq][k_out]
     float *out_scores;

@@ -312,7 +312,7 @@ struct TopkLds {
     uint64_t tmp[SEL_TMP];      // selection gather buffer
     uint32_t hist[SEL_BINS];
     uint32_t red[16];           // cross-wave reduction slots
-    uint32_t ovl[SCAN_WG];      // workgroups to rescan (merge stage 3)
+    uint32_t ovl[SCAN_WG];      // final selection: per-group flush counts, then their prefix
     uint32_t cnt, cnt2, bstar, above, flag, last, grab;
     uint64_t tau, gtau;
 };
@@ -355,6 +355,21 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     return v;
 }
 
+// #{keys in ks[0, n) greater than `mine`}; ks in LDS, read by every lane
+// alike (broadcast), 16 reads in flight per batch.
+__device__ __forceinline__ uint32_t count_greater(const uint64_t *ks, uint32_t n, uint64_t mine) {
+    uint32_t r = 0, j = 0;
+    for (; j + 16 <= n; j += 16) {
+        uint64_t v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = ks[j + u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) r += v[u] > mine ? 1u : 0u;
+    }
+    for (; j < n; ++j) r += ks[j] > mine ? 1u : 0u;
+    return r;
+}
+
 // Keeps the best `kk` (>= 1) of L.keys[0, n) (unique, nonzero) in
 // L.keys[0, m), sorted descending, and returns m = min(n, kk).  Small inputs
 // are sorted outright; larger ones are binned by the score bits over their
@@ -371,7 +386,7 @@ __device__ __noinline__ uint32_t select_topk(TopkLds &L, uint32_t n, uint32_t kk
         uint32_t rank = 0;
         if (tid < n) {
             mine = L.keys[tid];
-            for (uint32_t j = 0; j < n; ++j) rank += L.keys[j] > mine ? 1u : 0u;
+            rank = count_greater(L.keys, n, mine);
         }
         __syncthreads();
         if (tid < n && rank < kk) L.keys[rank] = mine;
@@ -453,7 +468,7 @@ __device__ __noinline__ uint32_t select_topk(TopkLds &L, uint32_t n, uint32_t kk
             uint32_t rank = 0;
             if (tid < c) {
                 mine = L.tmp[tid];
-                for (uint32_t j = 0; j < c; ++j) rank += L.tmp[j] > mine ? 1u : 0u;
+                rank = count_greater(L.tmp, c, mine);
             }
             __syncthreads();
             if (tid < c && rank < kk) L.keys[rank] = mine;
@@ -476,8 +491,11 @@ __device__ __noinline__ uint32_t select_topk(TopkLds &L, uint32_t n, uint32_t kk
     return kk;
 }
 
-// Wave-level append of keys for lanes where `take` holds.
-__device__ __forceinline__ void wave_append(uint64_t *keys, uint32_t *cnt, bool take, uint64_t key, int lane) {
+// Wave-level append to a shared LDS list: one atomic per wave.  Keys whose
+// slot would reach `cap` are dropped (callers size cap so that only the
+// threshold helper, which may use any subset, can hit it).
+__device__ __forceinline__ void wave_append(uint64_t *keys, uint32_t *cnt, uint32_t cap, bool take, uint64_t key,
+                                            int lane) {
     const uint64_t ball = __ballot(take);
     if (ball == 0) return;
     const uint32_t total = __popcll(ball);
@@ -486,12 +504,86 @@ __device__ __forceinline__ void wave_append(uint64_t *keys, uint32_t *cnt, bool 
     if (lane == leader) base = atomicAdd(cnt, total);
     base = __shfl(base, leader);
     if (take) {
-        const uint64_t below = ball & ((lane == 0) ? 0ull : (~0ull >> (64 - lane)));
-        keys[base + __popcll(below)] = key;
+        const uint32_t below =
+            __builtin_amdgcn_mbcnt_hi((uint32_t)(ball >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ball, 0u));
+        if (base + below < cap) keys[base + below] = key;
     }
 }
 
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+        const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), s) << 32) |
+                           (uint32_t)__shfl_xor((int)(uint32_t)v, s);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// ------------------------------------------------- per-wave candidate lists --
+// During the scan every wave owns a private list wk[0, wc) in LDS; wc is
+// wave-uniform, so appends need no atomics and no workgroup barriers.
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t ball) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(ball >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ball, 0u));
+}
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ void wave_push(uint64_t *wk, uint32_t &wc, bool take, uint64_t key) {
+    const uint64_t ball = __ballot(take);
+    if (take) wk[wc + lanes_below(ball)] = key;
+    wc += (uint32_t)__popcll(ball);
+}
+
+// Keeps the keys >= t of wk[0, wc) in place (order kept); returns the count.
+// Each 64-key chunk is read by the whole wave before any lane writes, and
+// writes land at or below the chunk, so the compaction is safe in place.
+__device__ uint32_t wave_filter(uint64_t *wk, uint32_t wc, uint64_t t, int lane) {
+    uint32_t out = 0;
+    for (uint32_t j = 0; j < wc; j += 64) {
+        const uint32_t i = j + lane;
+        const uint64_t k = i < wc ? wk[i] : 0;
+        wave_push(wk, out, i < wc && k >= t, k);
+    }
+    return out;
+}
+
+__device__ uint32_t wave_count_ge(const uint64_t *wk, uint32_t wc, uint64_t t, int lane) {
+    uint32_t c = 0;
+    for (uint32_t j = 0; j < wc; j += 64) {
+        const uint32_t i = j + lane;
+        c += (uint32_t)__popcll(__ballot(i < wc && wk[i] >= t));
+    }
+    return c;
+}
+
+// A bound t with kp <= #{keys >= t} <= target, for a list whose keys are all
+// >= lo and unique, with kp <= target < wc.  Bisection on the key value: the
+// count drops by at most one per unit step of t, so some t in (lo, max] has
+// exactly kp keys at or above it and the search always lands in the window.
+// Any such t is at most the kp-th best of the list, hence at most the
+// kp-th best of the whole scan: a valid pruning bound.
+__device__ uint64_t wave_bound(const uint64_t *wk, uint32_t wc, uint64_t lo, uint32_t kp, uint32_t target, int lane) {
+    uint64_t mx = 0;
+    for (uint32_t j = lane; j < wc; j += 64) mx = wk[j] > mx ? wk[j] : mx;
+    uint64_t hi = wave_max_u64(mx) + 1;  // nothing at or above hi
+    while (hi - lo > 1) {
+        const uint64_t mid = lo + ((hi - lo) >> 1);
+        const uint32_t c = wave_count_ge(wk, wc, mid, lane);
+        if (c < kp) hi = mid;
+        else if (c > target) lo = mid;
+        else return mid;
+    }
+    return lo;
+}
+
 // ------------------------------------------------------------ scan + top-k --
+constexpr uint32_t TAU_POLL = 4;  // grabs between reads of the shared bound
+
 // A unit slot past the end of a row (layouts whose lanes overhang the row)
 // must contribute nothing: zero query values do that for the dot-style codecs;
 // the l2 and Hamming codecs substitute a unit equal to the query itself.
@@ -515,11 +607,6 @@ template <> struct Neutral<C_HAM> {
     }
 };
 
-// Rows are split across LPR lanes (each lane loads UPL 16-byte or 4-byte units
-// of a row; 64/LPR rows per load instruction).  Every step a wave issues all
-// U*UPL loads of its U row groups before any arithmetic, then reduces the
-// per-lane partial sums with the transposing butterfly.  IDX: rows come from
-// a candidate list (IVF probes) instead of being consecutive.
 // Per-lane constants of a scan: the query slice in registers and the
 // lane's place in the row layout.
 template <int C, int UPL> struct ScanRegs {
@@ -529,9 +616,10 @@ template <int C, int UPL> struct ScanRegs {
     Fin<C> fin;
 };
 
-// Compact the LDS buffer once it holds more than this many keys.
-constexpr uint32_t SCAN_TRIG = 256;
-
+// Rows are split across LPR lanes (each lane loads UPL 16-byte or 4-byte units
+// of a row; 64/LPR rows per load instruction).  Every step a wave issues all
+// U*UPL loads of its U row groups before any arithmetic, then reduces the
+// per-lane partial sums with the transposing butterfly.
 template <int C, int LPR, int UPL> struct ScanShape {
     static constexpr int U0 = UPL >= 4 ? 2 : (UPL >= 2 ? 4 : 8);
     static constexpr int UMAX = LPR >= 64 ? 8 : LPR == 32 ? 4 : LPR == 16 ? 2 : 1;  // transposes on bits 5..3
@@ -541,81 +629,83 @@ template <int C, int LPR, int UPL> struct ScanShape {
     static constexpr int RPS = U * G;                // rows per wave step
     static constexpr int GRAB_STEPS = 2;             // wave steps per work grab
     static constexpr int GRAB_ROWS = WAVES * RPS * GRAB_STEPS;
+    static constexpr uint32_t WGRAB = RPS * GRAB_STEPS;  // keys one grab can add to a wave's list
 };
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), s) << 32) |
-                           (uint32_t)__shfl_xor((int)(uint32_t)v, s);
-        v = o > v ? o : v;
-    }
-    return v;
-}
+// One wave step: the U x UPL units each lane loads for RPS consecutive rows
+// (candidate slots when IDX), plus the scale and row id of the row whose
+// total this lane will hold after the reduction.
+template <int C, int LPR, int UPL> struct StepData {
+    typename Codec<C>::Unit d[ScanShape<C, LPR, UPL>::U][UPL];
+    float scale;
+    uint32_t grow;
+};
 
-// Scans rows [r0, r1) (candidate slots when IDX): appends keys >= tau to
-// L.keys and folds every eligible key into the lane's running maximum `lmax`.
-// Rows are split across the workgroup's waves step by step.
+// Issues the loads of the step covering rows [base, base + RPS), clipped to
+// lim (> 0): rows at or past lim load row lim-1 and are dropped later.
 template <int C, int LPR, int UPL, bool IDX>
-__device__ __forceinline__ void scan_rows(const ScanArgs &a, const ScanRegs<C, UPL> &R, const uint32_t *cand,
-                                          uint64_t r0, uint64_t r1, uint64_t tau, TopkLds &L, uint64_t &lmax) {
-    using CD = Codec<C>;
-    using Unit = typename CD::Unit;
-    using Acc = typename CD::Acc;
+__device__ __forceinline__ void load_step(const ScanArgs &a, const ScanRegs<C, UPL> &R, const uint32_t *cand,
+                                          uint64_t base, uint64_t lim, StepData<C, LPR, UPL> &S, int lane) {
+    using Unit = typename Codec<C>::Unit;
     using SH = ScanShape<C, LPR, UPL>;
-    constexpr int U = SH::U, G = SH::G, RPS = SH::RPS, WAVES = SH::WAVES;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    constexpr int U = SH::U, G = SH::G;
     const int slot = lane / LPR;
     const char *codes = (const char *)a.codes;
-    const int jrow = xrow<U, LPR>(lane);
-    const bool rep = xrep<U, LPR>(lane);
-    for (uint64_t base = r0 + (uint64_t)wave * RPS; base < r1; base += (uint64_t)WAVES * RPS) {
-        Unit d[U][UPL];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint64_t row = base + (uint64_t)u * G + slot;
-            const uint64_t rc = row < r1 ? row : r1 - 1;
-            const uint64_t grow = IDX ? (uint64_t)cand[rc] : rc;
-            const Unit *rp = (const Unit *)(codes + grow * a.row_bytes);
+    for (int u = 0; u < U; ++u) {
+        const uint64_t row = base + (uint64_t)u * G + slot;
+        const uint64_t rc = row < lim ? row : lim - 1;
+        const uint64_t grow = IDX ? (uint64_t)cand[rc] : rc;
+        const Unit *rp = (const Unit *)(codes + grow * a.row_bytes);
 #pragma unroll
-            for (int t = 0; t < UPL; ++t) d[u][t] = rp[R.ucl[t]];
-        }
-        const uint64_t myrow = base + (uint64_t)jrow * G + slot;
-        const bool myvalid = rep && myrow < r1;
-        const uint64_t myrc = myrow < r1 ? myrow : r1 - 1;
-        const uint32_t mygrow = IDX ? cand[myrc] : (uint32_t)myrc;
-        const float myscale = a.scales ? a.scales[mygrow] * a.scale_mul : 1.0f;
-        Acc acc[CD::NA][U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            Acc a1[CD::NA];
-#pragma unroll
-            for (int m = 0; m < CD::NA; ++m) a1[m] = (Acc)0;
-#pragma unroll
-            for (int t = 0; t < UPL; ++t) CD::acc(Neutral<C>::get(d[u][t], R.qr[t], R.uok[t]), R.qr[t], a1);
-#pragma unroll
-            for (int m = 0; m < CD::NA; ++m) acc[m][u] = a1[m];
-        }
-        Acc tot[CD::NA];
-#pragma unroll
-        for (int m = 0; m < CD::NA; ++m) tot[m] = xreduce<U, LPR>(acc[m], lane);
-        bool take = false;
-        uint64_t key = 0;
-        if (myvalid) {
-            uint32_t ord;
-            const float sc = R.fin.score(tot, myscale, ord);
-            if (a.dense_out && blockIdx.y == 0) a.dense_out[myrow] = sc;
-            bool pass = true;
-            if (a.mask) pass = mygrow < a.mask_bits && ((a.mask[mygrow >> 5] >> (mygrow & 31)) & 1u);
-            if (pass) {
-                key = make_key(ord, mygrow);
-                take = key >= tau;
-                lmax = key > lmax ? key : lmax;
-            }
-        }
-        wave_append(L.keys, &L.cnt, take, key, lane);
+        for (int t = 0; t < UPL; ++t) S.d[u][t] = rp[R.ucl[t]];
     }
+    const uint64_t myrow = base + (uint64_t)xrow<U, LPR>(lane) * G + slot;
+    const uint64_t myrc = myrow < lim ? myrow : lim - 1;
+    S.grow = IDX ? cand[myrc] : (uint32_t)myrc;
+    S.scale = a.scales ? a.scales[S.grow] * a.scale_mul : 1.0f;
+}
+
+// Scores a loaded step: pushes keys >= tau to the wave's list and folds
+// every eligible key into the lane's running maximum.
+template <int C, int LPR, int UPL>
+__device__ __forceinline__ void compute_step(const ScanArgs &a, const ScanRegs<C, UPL> &R,
+                                             const StepData<C, LPR, UPL> &S, uint64_t base, uint64_t lim,
+                                             uint64_t tau, uint64_t *wk, uint32_t &wc, uint64_t &lmax, int lane) {
+    using CD = Codec<C>;
+    using Acc = typename CD::Acc;
+    using SH = ScanShape<C, LPR, UPL>;
+    constexpr int U = SH::U, G = SH::G;
+    Acc acc[CD::NA][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        Acc a1[CD::NA];
+#pragma unroll
+        for (int m = 0; m < CD::NA; ++m) a1[m] = (Acc)0;
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) CD::acc(Neutral<C>::get(S.d[u][t], R.qr[t], R.uok[t]), R.qr[t], a1);
+#pragma unroll
+        for (int m = 0; m < CD::NA; ++m) acc[m][u] = a1[m];
+    }
+    Acc tot[CD::NA];
+#pragma unroll
+    for (int m = 0; m < CD::NA; ++m) tot[m] = xreduce<U, LPR>(acc[m], lane);
+    const uint64_t myrow = base + (uint64_t)xrow<U, LPR>(lane) * G + lane / LPR;
+    bool take = false;
+    uint64_t key = 0;
+    if (xrep<U, LPR>(lane) && myrow < lim) {
+        uint32_t ord;
+        const float sc = R.fin.score(tot, S.scale, ord);
+        if (a.dense_out && blockIdx.y == 0) a.dense_out[myrow] = sc;
+        bool pass = true;
+        if (a.mask) pass = S.grow < a.mask_bits && ((a.mask[S.grow >> 5] >> (S.grow & 31)) & 1u);
+        if (pass) {
+            key = make_key(ord, S.grow);
+            take = key >= tau;
+            lmax = key > lmax ? key : lmax;
+        }
+    }
+    wave_push(wk, wc, take, key);
 }
 
 // Publishes the wave's running maximum to wmax[slot] when it grew.
@@ -625,6 +715,27 @@ __device__ __forceinline__ void publish_wave_max(uint64_t *wslot, uint64_t lmax,
         published = w;
         if (lane == 0) __hip_atomic_store(wslot, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+// Cross-workgroup hand-off without cache-wide maintenance: data goes through
+// relaxed device-scope atomic stores and loads (write-through / coherent
+// accesses that never rely on a stale per-XCD L2 line), and the signalling
+// atomic is issued only after every prior access has completed.  A device
+// fence would instead write back and invalidate the whole L2 of the XCD,
+// stalling every workgroup still streaming through it.
+__device__ __forceinline__ void store_shared(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_shared(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T> __device__ __forceinline__ T load_shared(const T *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores_done() { __builtin_amdgcn_s_waitcnt(0); }
+
+__device__ __forceinline__ uint64_t load_tau(const QState *qs) {
+    return uniform_u64(__hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
 // Zeroes a query's coordination state and wave maxima (run by whichever of
@@ -648,19 +759,20 @@ __device__ __forceinline__ uint32_t group_size(uint32_t grid, uint32_t ng, uint3
     return grid / ng + (r < grid % ng ? 1u : 0u);
 }
 
-// Background threshold: the kprime-th best of the per-wave running maxima
+// Background threshold: the kprime-th best of any kprime or more wave maxima
 // is the key of a real row no better than the true kprime-th best, so every
-// scan may drop keys below it.  Recomputed until all scanning workgroups are
-// done; each round only gathers maxima at or above the previous bound (the
-// maxima only grow, so the new top-kprime is always among them).
+// scan may drop keys below it.  Each round gathers up to `cap` maxima at or
+// above the current bound (the maxima only grow, so the bound only rises)
+// and publishes the new kprime-th best.  Runs until every scanning workgroup
+// has finished.
 __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
     QState *qs = a.qs + qi;
     const uint32_t nslots = a.grid * (SCAN_WG / 64);
     const uint64_t *wm = a.wmax + (uint64_t)qi * nslots;
     const uint32_t kp = a.kprime;
     const uint32_t ng = a.grid < (uint32_t)NGROUP ? a.grid : (uint32_t)NGROUP;
-    const int tid = threadIdx.x;
-    if (kp > (uint32_t)SCAN_WG) return;  // the bound below ranks at most SCAN_WG keys
+    const uint32_t cap = kp <= (uint32_t)SCAN_WG ? (uint32_t)SCAN_WG : (uint32_t)SCAN_CAP;
+    const int tid = threadIdx.x, lane = tid & 63;
     uint64_t th = 0;
     for (int round = 0; round < (1 << 22); ++round) {
         if (tid == 0) {
@@ -669,9 +781,6 @@ __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
         }
         __syncthreads();
         const uint32_t top = L.flag;
-        // any SCAN_WG maxima at or above the current bound: the kp-th best of
-        // any set of real rows is a valid bound, and keeping only keys above
-        // the previous one makes it increase every round
         for (uint32_t i0 = 0; i0 < nslots; i0 += 8 * SCAN_WG) {
             uint64_t v[8];
 #pragma unroll
@@ -680,15 +789,10 @@ __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
                 v[j] = i < nslots ? __hip_atomic_load(&wm[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                if (v[j] != 0 && v[j] >= th) {
-                    const uint32_t slot = atomicAdd(&L.cnt, 1u);
-                    if (slot < (uint32_t)SCAN_WG) L.keys[slot] = v[j];
-                }
-            }
+            for (int j = 0; j < 8; ++j) wave_append(L.keys, &L.cnt, cap, v[j] != 0 && v[j] >= th, v[j], lane);
         }
         __syncthreads();
-        const uint32_t have = L.cnt < (uint32_t)SCAN_WG ? L.cnt : (uint32_t)SCAN_WG;
+        const uint32_t have = L.cnt < cap ? L.cnt : cap;
         if (have >= kp) {
             const uint32_t m = select_topk(L, have, kp);
             const uint64_t t = L.keys[m - 1];
@@ -703,17 +807,19 @@ __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
 }
 
 // Fused scan + top-k (one launch per query batch).  Workgroups 0..grid-1
-// take row blocks round-robin (block b goes to workgroup b % grid), keep keys at or above the running threshold in LDS (compacting to
-// the best kprime), and publish their waves' running maxima.  Workgroup
-// `grid` is the threshold helper.  Each scanning workgroup finally flushes
-// its keys at or above the published threshold to a global array; the last
-// one to finish selects the best kprime from that array.
+// take row blocks round-robin (block b goes to workgroup b % grid); each of
+// their waves keeps keys at or above its running bound in a private LDS list
+// and publishes its running maximum.  Workgroup `grid` is the threshold
+// helper.  At the end every wave flushes its keys at or above the freshest
+// bound to a global array; the last workgroup to finish selects the best
+// kprime of the flushes.  Dynamic LDS: max(sizeof(TopkLds), 4 * wcap * 8).
 template <int C, int LPR, int UPL, bool IDX>
 __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     using CD = Codec<C>;
     using QT = typename CD::QT;
     using SH = ScanShape<C, LPR, UPL>;
-    __shared__ TopkLds L;
+    extern __shared__ __align__(16) unsigned char scan_smem[];
+    TopkLds &L = *(TopkLds *)scan_smem;
 
     const uint32_t qi = blockIdx.y;
     const int tid = threadIdx.x;
@@ -752,78 +858,91 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     uint64_t *wslot = a.wmax + ((uint64_t)qi * a.grid + blockIdx.x) * SH::WAVES + wave;
     uint64_t lmax = 0, published = 0;
 
-    if (tid == 0) {
-        L.cnt = 0;
-        L.tau = 0;
-    }
-    __syncthreads();
-    // grabs g, g + grid, g + 2*grid, ... of GRAB_ROWS rows each
-    for (uint64_t g = blockIdx.x;; g += a.grid) {
-        const uint64_t r0 = g * SH::GRAB_ROWS;
-        if (r0 >= n) break;
-        const uint64_t r1 = r0 + SH::GRAB_ROWS < n ? r0 + SH::GRAB_ROWS : n;
-        const uint64_t tau = L.tau;
+    const uint32_t wcap = a.wcap;
+    uint64_t *wk = (uint64_t *)scan_smem + (size_t)wave * wcap;
+    const uint32_t trig = wcap - SH::WGRAB;       // compact when the list passes this
+    const uint32_t target = kp + (trig - kp) / 2;  // ... down to at most this many keys
+    uint32_t wc = 0;
+    uint64_t tau = 0;
+    // grabs g, g + grid, g + 2*grid, ... of GRAB_ROWS rows each; a wave
+    // covers two steps of every grab (rows wofs.. and wofs + half..)
+    static_assert(SH::GRAB_STEPS == 2, "two steps per grab");
+    using SD = StepData<C, LPR, UPL>;
+    constexpr bool PIPE = SH::U * UPL * (int)(sizeof(typename CD::Unit) / 4) <= 32;  // double-buffer the loads
+    const uint64_t wofs = (uint64_t)wave * SH::RPS, half = (uint64_t)SH::WAVES * SH::RPS;
+    const uint64_t gstride = (uint64_t)a.grid * SH::GRAB_ROWS;
+    SD A, B;
+    uint64_t r0 = (uint64_t)blockIdx.x * SH::GRAB_ROWS;
+    if (PIPE && r0 < n)
+        load_step<C, LPR, UPL, IDX>(a, R, cand, r0 + wofs, r0 + SH::GRAB_ROWS < n ? r0 + SH::GRAB_ROWS : n, A, lane);
+    for (uint32_t gi = 0; r0 < n; ++gi) {
+        const uint64_t lim = r0 + SH::GRAB_ROWS < n ? r0 + SH::GRAB_ROWS : n;
+        // read the shared bound every TAU_POLL grabs (waves staggered): it is
+        // one cache line that every wave of the grid would otherwise hammer
+        const bool poll = (gi + (uint32_t)wave) % TAU_POLL == 0;
         uint64_t gt = 0;
-        if (tid == 0) gt = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        scan_rows<C, LPR, UPL, IDX>(a, R, cand, r0, r1, tau, L, lmax);
+        if (poll) gt = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t nr0 = r0 + gstride;
+        if constexpr (PIPE) {
+            // the next step's loads are in flight while this one is scored
+            load_step<C, LPR, UPL, IDX>(a, R, cand, r0 + wofs + half, lim, B, lane);
+            compute_step<C, LPR, UPL>(a, R, A, r0 + wofs, lim, tau, wk, wc, lmax, lane);
+            if (nr0 < n)
+                load_step<C, LPR, UPL, IDX>(a, R, cand, nr0 + wofs, nr0 + SH::GRAB_ROWS < n ? nr0 + SH::GRAB_ROWS : n,
+                                            A, lane);
+            compute_step<C, LPR, UPL>(a, R, B, r0 + wofs + half, lim, tau, wk, wc, lmax, lane);
+        } else {
+            load_step<C, LPR, UPL, IDX>(a, R, cand, r0 + wofs, lim, A, lane);
+            compute_step<C, LPR, UPL>(a, R, A, r0 + wofs, lim, tau, wk, wc, lmax, lane);
+            load_step<C, LPR, UPL, IDX>(a, R, cand, r0 + wofs + half, lim, A, lane);
+            compute_step<C, LPR, UPL>(a, R, A, r0 + wofs + half, lim, tau, wk, wc, lmax, lane);
+        }
+        r0 = nr0;
         publish_wave_max(wslot, lmax, published, lane);
-        if (tid == 0) L.gtau = gt;
-        __syncthreads();
-        if (L.cnt > SCAN_TRIG) {
-            const uint32_t m = select_topk(L, L.cnt, kp);
-            if (tid == 0) {
-                L.cnt = m;
-                if (m == kp && L.keys[kp - 1] > L.tau) L.tau = L.keys[kp - 1];
+        if (poll) {
+            const uint64_t ugt = uniform_u64(gt);
+            tau = ugt > tau ? ugt : tau;
+        }
+        if (wc > trig) {
+            wc = wave_filter(wk, wc, tau, lane);
+            if (wc > target) {
+                const uint64_t t = wave_bound(wk, wc, tau, kp, target, lane);
+                wc = wave_filter(wk, wc, t, lane);
+                if (t > tau) {
+                    tau = t;
+                    if (lane == 0) atomicMax(&qs->tau, (unsigned long long)t);
+                }
             }
         }
-        if (tid == 0 && L.gtau > L.tau) L.tau = L.gtau;
-        __syncthreads();
     }
-    // bound the flush to kprime keys, then flush those at or above the bound
-    if (L.cnt > kp) {
-        const uint32_t m = select_topk(L, L.cnt, kp);
-        if (tid == 0) L.cnt = m;
-        __syncthreads();
+    // flush the keys at or above the freshest bound
+    {
+        const uint64_t gt = load_tau(qs);
+        tau = gt > tau ? gt : tau;
+        wc = wave_filter(wk, wc, tau, lane);
     }
-    if (tid == 0) {
-        const uint64_t gt = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        L.gtau = gt > L.tau ? gt : L.tau;
-        L.cnt2 = 0;
-    }
-    __syncthreads();
-    const uint32_t have = L.cnt;
-    const uint64_t fl = L.gtau;
-    uint32_t myk = 0;
-    uint64_t mykeys[MAX_KPRIME / SCAN_WG];
-    for (uint32_t j = tid; j < have; j += SCAN_WG) {
-        const uint64_t k = L.keys[j];
-        if (k >= fl) mykeys[myk++] = k;
-    }
-    uint32_t off = 0;
-    if (myk) off = atomicAdd(&L.cnt2, myk);
-    __syncthreads();
     const uint32_t ng = a.grid < (uint32_t)NGROUP ? a.grid : (uint32_t)NGROUP;
     const uint32_t grp = blockIdx.x % ng;
-    const uint64_t region = (uint64_t)((a.grid + ng - 1) / ng) * kp;  // keys per group region
-    if (tid == 0) L.bstar = L.cnt2 ? atomicAdd(&qs->cc[grp * CL], L.cnt2) : 0;
-    __syncthreads();
-    uint64_t *ck = a.cand_keys + (uint64_t)qi * a.cand_cap + grp * region;
-    for (uint32_t j = 0; j < myk; ++j) ck[L.bstar + off + j] = mykeys[j];
-    __threadfence();
+    const uint64_t region = a.cand_cap / ng;  // keys per group region
+    if (wc) {
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&qs->cc[grp * CL], wc);
+        base = __builtin_amdgcn_readfirstlane(base);
+        uint64_t *ck = a.cand_keys + (uint64_t)qi * a.cand_cap + grp * region + base;
+        for (uint32_t j = lane; j < wc; j += 64) store_shared(&ck[j], wk[j]);
+    }
+    wait_stores_done();
     __syncthreads();
     if (tid == 0) {
         // two-level ticket: the workgroup completing its group bumps `top`;
         // the one completing `top` runs the final selection
         bool last = false;
-        if (atomicAdd(&qs->done[grp * CL], 1u) == group_size(a.grid, ng, grp) - 1) {
-            __threadfence();
+        if (atomicAdd(&qs->done[grp * CL], 1u) == group_size(a.grid, ng, grp) - 1)
             last = atomicAdd(&qs->top, 1u) == ng - 1;
-        }
         L.last = last;
     }
     __syncthreads();
     if (!L.last) return;
-    __threadfence();
 
     // ---- last scanning workgroup: select the best kprime of the flushes ----
     if (tid == 0) {
@@ -837,23 +956,34 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         uint32_t acc = 0;
         for (uint32_t r = 0; r < ng; ++r) {
             L.ovl[32 + r] = acc;
-            acc += (uint32_t)L.ovl[r];
+            acc += L.ovl[r];
         }
         L.ovl[32 + ng] = acc;
     }
     __syncthreads();
     const uint64_t *ckq = a.cand_keys + (uint64_t)qi * a.cand_cap;
-    const uint32_t total = (uint32_t)L.ovl[32 + ng];
-    for (uint32_t c0 = 0; c0 < total; c0 += SCAN_CAP / 2) {
+    const uint32_t total = L.ovl[32 + ng];
+    constexpr uint32_t CHUNK = SCAN_CAP / 2;
+    for (uint32_t c0 = 0; c0 < total; c0 += CHUNK) {
         const uint64_t th = L.tau;
-        for (uint32_t i = c0 + tid; i < total && i < c0 + SCAN_CAP / 2; i += SCAN_WG) {
-            uint32_t r = 0;
-            while (r + 1 < ng && (uint32_t)L.ovl[32 + r + 1] <= i) ++r;
-            const uint64_t k = __builtin_nontemporal_load(&ckq[r * region + (i - (uint32_t)L.ovl[32 + r])]);
-            if (k >= th) L.keys[atomicAdd(&L.cnt, 1u)] = k;
+        const uint32_t c1 = c0 + CHUNK < total ? c0 + CHUNK : total;
+        for (uint32_t i0 = c0; i0 < c1; i0 += 4 * SCAN_WG) {
+            uint64_t v[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t i = i0 + j * SCAN_WG + tid;
+                v[j] = 0;
+                if (i < c1) {
+                    uint32_t r = 0;
+                    while (r + 1 < ng && L.ovl[32 + r + 1] <= i) ++r;
+                    v[j] = load_shared(&ckq[r * region + (i - L.ovl[32 + r])]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) wave_append(L.keys, &L.cnt, SCAN_CAP, v[j] != 0 && v[j] >= th, v[j], lane);
         }
         __syncthreads();
-        if (L.cnt > (uint32_t)(SCAN_CAP / 2)) {
+        if (L.cnt > CHUNK) {
             const uint32_t m = select_topk(L, L.cnt, kp);
             if (tid == 0) {
                 L.cnt = m;
@@ -1098,13 +1228,16 @@ __global__ __launch_bounds__(64) void query_levels(LevelArgs a) {
 }
 
 // ---------------------------------------------------------------- rerank --
-// One wave per candidate: stage the row and query in LDS, then four lanes run
-// Store.dotRow's four strided f64 accumulators (store.ts:114-130).  The last
-// wave of each query sorts the re-ranked scores and writes the top-k_out.
+// One wave per candidate.  The wave loads the row and query coalesced and
+// stages every exact f64 product x[i]*q[i] (exact: two 24-bit significands)
+// in LDS, transposed so that accumulator m's terms x[4j+m]*q[4j+m] are
+// contiguous.  Lanes 0..3 then run Store.dotRow's four strided f64 sums
+// (src/store/store.ts:114-130) in their original order (adding an exact
+// product rounds exactly like the reference's `acc += x*y`), and lane 0 adds
+// ((a0+a1)+a2)+a3 and the tail.  The last wave of each query ranks the
+// re-ranked keys and writes the top-k_out.  Dynamic LDS: 8 * (dim & ~3).
 __global__ __launch_bounds__(64) void rerank_topk(RerankArgs a) {
-    extern __shared__ float rsm[];
-    float *rowv = rsm;
-    float *qv = rsm + a.dim;
+    extern __shared__ __align__(16) double prod[];
     __shared__ uint64_t keys[MAX_KPRIME];
     __shared__ uint32_t last_s;
     const uint32_t qi = blockIdx.y, c = blockIdx.x;
@@ -1126,50 +1259,74 @@ __global__ __launch_bounds__(64) void rerank_topk(RerankArgs a) {
         }
     }
     if (have) {
-        const float *src = a.rows + (uint64_t)row * a.dim;
+        const uint32_t dim = a.dim, vec = dim & ~3u, nv = vec >> 2;
+        const float *src = a.rows + (uint64_t)row * dim;
         const float *qs = a.q + (uint64_t)qi * a.q_stride;
-        for (uint32_t i = lane; i < a.dim; i += 64) {
-            rowv[i] = src[i];
-            qv[i] = qs[i];
+        constexpr int B = 8;
+        for (uint32_t e0 = 0; e0 < vec; e0 += 64 * B) {
+            float xv[B], qv[B];
+#pragma unroll
+            for (int t = 0; t < B; ++t) {
+                const uint32_t e = e0 + t * 64 + lane;
+                xv[t] = e < vec ? src[e] : 0.0f;
+                qv[t] = e < vec ? qs[e] : 0.0f;
+            }
+#pragma unroll
+            for (int t = 0; t < B; ++t) {
+                const uint32_t e = e0 + t * 64 + lane;
+                if (e < vec) prod[(e & 3) * nv + (e >> 2)] = (double)xv[t] * (double)qv[t];
+            }
         }
         __syncthreads();
-        const uint32_t vec = a.dim & ~3u;
         double acc = 0.0;
         if (lane < 4) {
-            for (uint32_t i = lane; i < vec; i += 4) acc = fma((double)rowv[i], (double)qv[i], acc);
+            const double *pp = prod + (uint32_t)lane * nv;
+            uint32_t j = 0;
+            for (; j + 8 <= nv; j += 8) {
+                double t[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) t[u] = pp[j + u];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc = acc + t[u];
+            }
+            for (; j < nv; ++j) acc = acc + pp[j];
         }
         const double a1 = __shfl(acc, 1), a2 = __shfl(acc, 2), a3 = __shfl(acc, 3);
         if (lane == 0) {
             double s = acc + a1;
             s = s + a2;
             s = s + a3;
-            for (uint32_t i = vec; i < a.dim; ++i) s = fma((double)rowv[i], (double)qv[i], s);
-            a.rr_scores[(uint64_t)qi * a.kprime + c] = (float)s;
-            a.rr_rows[(uint64_t)qi * a.kprime + c] = row;
+            for (uint32_t i = vec; i < dim; ++i) s = fma((double)src[i], (double)qs[i], s);
+            store_shared(&a.rr_keys[(uint64_t)qi * a.kprime + c], make_key(ord_f32((float)s), row));
         }
     }
-    __threadfence();
+    wait_stores_done();
     __syncthreads();
     if (lane == 0) last_s = atomicAdd(&a.tickets[qi], 1u) == gridDim.x - 1;
     __syncthreads();
     if (!last_s) return;
-    __threadfence();
-    const uint32_t npow = pow2_at_least(m);
-    for (uint32_t j = lane; j < npow; j += 64) {
-        uint64_t kk = 0;
-        if (j < m) {
-            const float sc = __builtin_nontemporal_load(&a.rr_scores[(uint64_t)qi * a.kprime + j]);
-            const uint32_t rw = __builtin_nontemporal_load(&a.rr_rows[(uint64_t)qi * a.kprime + j]);
-            kk = make_key(ord_f32(sc), rw);
-        }
-        keys[j] = kk;
-    }
+    for (uint32_t j = lane; j < m; j += 64) keys[j] = load_shared(&a.rr_keys[(uint64_t)qi * a.kprime + j]);
     __syncthreads();
-    bitonic_desc(keys, npow);
     const uint32_t ko = m < a.k_out ? m : a.k_out;
-    for (uint32_t j = lane; j < ko; j += 64) {
-        a.out_rows[(uint64_t)qi * a.k_out + j] = key_row(keys[j]);
-        a.out_scores[(uint64_t)qi * a.k_out + j] = f32_from_ord((uint32_t)(keys[j] >> 32));
+    if (m <= 256) {
+        // rank by counting (keys are unique): key j goes to slot #{greater}
+        for (uint32_t j = lane; j < m; j += 64) {
+            const uint64_t kj = keys[j];
+            const uint32_t r = count_greater(keys, m, kj);
+            if (r < ko) {
+                a.out_rows[(uint64_t)qi * a.k_out + r] = key_row(kj);
+                a.out_scores[(uint64_t)qi * a.k_out + r] = f32_from_ord((uint32_t)(kj >> 32));
+            }
+        }
+    } else {
+        const uint32_t npow = pow2_at_least(m);
+        for (uint32_t j = m + lane; j < npow; j += 64) keys[j] = 0;
+        __syncthreads();
+        bitonic_desc(keys, npow);
+        for (uint32_t j = lane; j < ko; j += 64) {
+            a.out_rows[(uint64_t)qi * a.k_out + j] = key_row(keys[j]);
+            a.out_scores[(uint64_t)qi * a.k_out + j] = f32_from_ord((uint32_t)(keys[j] >> 32));
+        }
     }
     if (lane == 0) {
         a.out_n[qi] = ko;
@@ -1210,10 +1367,14 @@ bool pick_layout(uint32_t units, Layout &L) {
 
 template <int C, int LPR, int UPL>
 hipError_t go(const ScanArgs &a, uint32_t nq, hipStream_t s) {
+    // the per-wave lists must take a whole grab above the compaction target
+    if (a.wcap < 2 * a.kprime + ScanShape<C, LPR, UPL>::WGRAB || (a.wcap & 63)) return hipErrorInvalidValue;
+    size_t lds = (size_t)(SCAN_WG / 64) * a.wcap * sizeof(uint64_t);
+    if (lds < sizeof(TopkLds)) lds = sizeof(TopkLds);
     if (a.cand)
-        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, true>), dim3(a.grid + 1, nq), dim3(SCAN_WG), 0, s, a);
+        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, true>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, a);
     else
-        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, false>), dim3(a.grid + 1, nq), dim3(SCAN_WG), 0, s, a);
+        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, false>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, a);
     return hipGetLastError();
 }
 
@@ -1302,7 +1463,7 @@ size_t level_stride(int codec, uint32_t P) {
 }
 
 hipError_t launch_rerank(const RerankArgs &a, uint32_t nq, hipStream_t s) {
-    const size_t lds = sizeof(float) * 2 * (size_t)a.dim;
+    const size_t lds = sizeof(double) * (size_t)(a.dim & ~3u) + 16;
     hipLaunchKernelGGL(rerank_topk, dim3(a.kprime, nq), dim3(64), lds, s, a);
     return hipGetLastError();
 }
