@@ -632,6 +632,17 @@ template <int C, int LPR, int UPL> struct ScanShape {
     static constexpr uint32_t WGRAB = RPS * GRAB_STEPS;  // keys one grab can add to a wave's list
 };
 
+// Streaming loads of codes and scales are nontemporal: every byte is read
+// once per query, and keeping it out of the caches' normal allocation lets
+// the scan sustain a higher share of HBM bandwidth.
+typedef unsigned int nt_u4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const uint4 *p) {
+    const nt_u4 t = __builtin_nontemporal_load((const nt_u4 *)p);
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ uint32_t load_stream(const uint32_t *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ float load_stream(const float *p) { return __builtin_nontemporal_load(p); }
+
 // One wave step: the U x UPL units each lane loads for RPS consecutive rows
 // (candidate slots when IDX), plus the scale and row id of the row whose
 // total this lane will hold after the reduction.
@@ -658,12 +669,12 @@ __device__ __forceinline__ void load_step(const ScanArgs &a, const ScanRegs<C, U
         const uint64_t grow = IDX ? (uint64_t)cand[rc] : rc;
         const Unit *rp = (const Unit *)(codes + grow * a.row_bytes);
 #pragma unroll
-        for (int t = 0; t < UPL; ++t) S.d[u][t] = rp[R.ucl[t]];
+        for (int t = 0; t < UPL; ++t) S.d[u][t] = load_stream(rp + R.ucl[t]);
     }
     const uint64_t myrow = base + (uint64_t)xrow<U, LPR>(lane) * G + slot;
     const uint64_t myrc = myrow < lim ? myrow : lim - 1;
     S.grow = IDX ? cand[myrc] : (uint32_t)myrc;
-    S.scale = a.scales ? a.scales[S.grow] * a.scale_mul : 1.0f;
+    S.scale = a.scales ? load_stream(a.scales + S.grow) * a.scale_mul : 1.0f;
 }
 
 // Scores a loaded step: pushes keys >= tau to the wave's list and folds
