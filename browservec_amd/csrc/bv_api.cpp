@@ -404,7 +404,7 @@ static uint32_t grid_for(uint64_t n) {
 
 // Scratch of the fused scan for nq queries: coordination state and wave
 // maxima must start zeroed (the kernel leaves them zeroed).
-static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kprime, ScanArgs &a) {
+static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kprime, uint32_t rr_dim, ScanArgs &a) {
     const size_t slots = (size_t)grid * (SCAN_WG / 64);
     {
         const size_t old = idx->qstate.cap;
@@ -420,7 +420,7 @@ static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kpri
     const uint64_t ng = grid < (uint32_t)NGROUP ? grid : (uint32_t)NGROUP;
     const uint32_t wcap = scan_wcap(kprime);
     const uint64_t cap = ng * ((grid + ng - 1) / ng) * (SCAN_WG / 64) * wcap;
-    HIPX(idx->dev, idx->cand_keys.ensure((size_t)nq * cap * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->cand_keys.ensure((size_t)nq * cap * 16, 0, idx->stream), "scratch");
     HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
     HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
     a.qs = idx->qstate.as<QState>();
@@ -428,6 +428,7 @@ static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kpri
     a.cand_keys = idx->cand_keys.as<uint64_t>();
     a.cand_cap = cap;
     a.wcap = wcap;
+    a.wstride = wcap + ((rr_dim & ~3u) + 1) / 2 * 2;  // list + re-rank staging (doubles)
     a.merged = idx->merged.as<uint64_t>();
     a.merged_n = idx->merged_n.as<uint32_t>();
     return BV_OK;
@@ -527,14 +528,25 @@ static void timing_collect(bv_index *idx) {
 static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                         const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores,
                         uint32_t *d_n) {
-    const void *qscan = nullptr;
-    uint64_t qstride = 0;
-    int rc = prepare_queries(idx, d_q, nq, &qscan, &qstride);
-    if (rc) return rc;
+    ScanArgs a{};
+    int rc = BV_OK;
+    if (idx->quant && scan_prep_supported(idx->codec, idx->units, idx->P)) {
+        // the scan kernel rotates and transforms the fp32 queries itself
+        a.qraw = d_q;
+        a.qdim = idx->dim;
+        a.signs = idx->signs.as<float>();
+        a.rounds = idx->d.rounds;
+    } else {
+        const void *qscan = nullptr;
+        uint64_t qstride = 0;
+        rc = prepare_queries(idx, d_q, nq, &qscan, &qstride);
+        if (rc) return rc;
+        a.q = qscan;
+        a.q_stride = qstride;
+    }
     const uint64_t n = idx->rows;
     const uint32_t grid = grid_for(n);
-    ScanArgs a{};
-    rc = scan_scratch(idx, nq, grid, kprime, a);
+    rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a);
     if (rc) return rc;
     a.codes = idx->quant ? idx->codes.p : idx->raw.p;
     a.row_bytes = idx->row_bytes;
@@ -542,45 +554,26 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
     a.padded_dim = idx->P;
     a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A) ? idx->scales.as<float>() : nullptr;
     a.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
-    a.q = qscan;
-    a.q_stride = qstride;
     a.mask = d_mask;
     a.mask_bits = mask_bits;
     a.n = n;
     a.kprime = kprime;
     a.grid = grid;
-    if (!rerank) {
-        a.k_out = k_out;
-        a.out_rows = d_rows;
-        a.out_scores = d_scores;
-        a.out_n = d_n;
+    a.k_out = k_out;
+    a.out_rows = d_rows;
+    a.out_scores = d_scores;
+    a.out_n = d_n;
+    if (rerank) {
+        // the scan re-ranks its fetch exactly against the stored fp32 rows
+        a.rr_src = idx->raw.as<float>();
+        a.rr_dim = idx->dim;
+        a.rr_q = d_q;
+        a.rr_q_stride = idx->dim;
     }
     timing_begin(idx);
     HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, idx->stream), "scan kernel");
     timing_end(idx);
     idx->last_scanned = n * nq;
-    if (rerank) {
-        HIPX(idx->dev, idx->rr_keys.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
-        const size_t old = idx->rr_tickets.cap;
-        HIPX(idx->dev, idx->rr_tickets.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
-        if (idx->rr_tickets.cap != old)
-            HIPX(idx->dev, hipMemsetAsync(idx->rr_tickets.p, 0, idx->rr_tickets.cap, idx->stream), "scratch");
-        RerankArgs r{};
-        r.rows = idx->raw.as<float>();
-        r.dim = idx->dim;
-        r.q = d_q;
-        r.q_stride = idx->dim;
-        r.merged = idx->merged.as<uint64_t>();
-        r.merged_n = idx->merged_n.as<uint32_t>();
-        r.kprime = kprime;
-        r.k_out = k_out;
-        r.rr_keys = idx->rr_keys.as<uint64_t>();
-        r.tickets = idx->rr_tickets.as<uint32_t>();
-        r.out_rows = d_rows;
-        r.out_scores = d_scores;
-        r.out_n = d_n;
-        HIPX(idx->dev, launch_rerank(r, nq, idx->stream), "rerank kernel");
-    }
     return BV_OK;
 }
 
@@ -844,7 +837,7 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
         d_mask = idx->mask.as<uint32_t>();
     }
     ScanArgs a{};
-    rc = scan_scratch(idx, 1, grid, 1, a);
+    rc = scan_scratch(idx, 1, grid, 1, 0, a);
     if (rc) return rc;
     a.codes = idx->quant ? idx->codes.p : idx->raw.p;
     a.row_bytes = idx->row_bytes;

@@ -48,6 +48,7 @@ struct QState {
     uint32_t pad[28];
     uint32_t done[NGROUP * CL];  // finished scanning workgroups per group
     uint32_t cc[NGROUP * CL];    // keys flushed per group region
+    uint32_t dyn[NGROUP * CL];   // dynamic chunks taken per slice (may overshoot)
 };
 
 struct ScanArgs {
@@ -57,8 +58,12 @@ struct ScanArgs {
     uint32_t padded_dim;      // P (Hamming similarity = P - 2*popcount)
     const float *scales;      // per-row scale (quantized codecs) or null
     float scale_mul;          // constant multiplier on the row scale (int4: f32(1/7))
-    const void *q;            // transformed queries, q_stride bytes apart
+    const void *q;            // transformed queries, q_stride bytes apart (when qraw is null)
     uint64_t q_stride;
+    const float *qraw;        // quantized codecs: fp32 queries (nq x qdim) transformed in the kernel
+    uint32_t qdim;
+    const float *signs;       // rotation signs (rounds x padded_dim) for qraw
+    uint32_t rounds;
     const uint32_t *cand;     // indexed mode: row ids (null = rows 0..n-1)
     const uint64_t *cand_off; // per-query offsets into cand (nq+1) or null
     const uint32_t *mask;     // row filter bits (LSB-first) or null
@@ -66,15 +71,20 @@ struct ScanArgs {
     uint64_t n;               // rows per query when cand_off is null
     uint32_t kprime;          // per-query candidates kept
     uint32_t wcap;            // per-wave LDS list capacity, scan_wcap(kprime)
+    uint32_t wstride;         // u64 words of LDS per wave: wcap (+ dim & ~3 re-rank staging)
     uint32_t grid;            // scanning workgroups per query (one more runs the threshold helper)
     QState *qs;               // [nq]
     uint64_t *wmax;           // [nq][grid*4] per-wave running maxima (zero on entry and exit)
-    uint64_t *cand_keys;      // [nq][cand_cap] flushed candidate keys
-    uint64_t cand_cap;        // min(grid,NGROUP) regions of ceil(grid/NGROUP)*4*wcap keys
+    uint64_t *cand_keys;      // [nq][cand_cap][2] flushed (scan key, exact key) pairs
+    uint64_t cand_cap;        // pairs per query: min(grid,NGROUP) regions of ceil(grid/NGROUP)*4*wcap
     uint64_t *merged;         // [nq][kprime] merged keys, descending
     uint32_t *merged_n;       // [nq]
     float *dense_out;         // optional: every row's score (query 0 only)
-    uint32_t k_out;           // when out_rows != null: decoded top-k_out
+    const float *rr_src;      // re-rank: stored fp32 rows (N x rr_dim) or null for no re-rank
+    uint32_t rr_dim;
+    const float *rr_q;        // re-rank: fp32 queries, rr_q_stride floats apart
+    uint64_t rr_q_stride;
+    uint32_t k_out;           // when out_rows != null: top-k_out (by exact score when re-ranking)
     uint32_t *out_rows;       // [nq][k_out]
     float *out_scores;
     uint32_t *out_n;          // [nq]
@@ -91,7 +101,6 @@ struct EncodeArgs {
     uint32_t *codes;          // rows x (P/per)
     float *scales;            // rows
     float *rotated;           // optional rows x P
-    float *qdiv;              // optional rows x P: rotated / 127 (int8 scan query)
     uint32_t *slow_rows;      // counter of rows that took the sequential 1-bit sum
 };
 
@@ -128,5 +137,8 @@ hipError_t launch_encode(const EncodeArgs &a, hipStream_t s);
 hipError_t launch_rerank(const RerankArgs &a, uint32_t nq, hipStream_t s);
 hipError_t launch_levels(const LevelArgs &a, uint32_t nq, hipStream_t s);
 size_t level_stride(int codec, uint32_t P);
+size_t scan_query_lds(int codec, uint32_t P);
+// True when the scan for this codec / row layout transforms fp32 queries itself (ScanArgs::qraw).
+bool scan_prep_supported(int codec, uint32_t units, uint32_t P);
 
 } // namespace bvk

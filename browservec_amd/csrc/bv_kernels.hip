@@ -581,8 +581,388 @@ __device__ uint64_t wave_bound(const uint64_t *wk, uint32_t wc, uint64_t lo, uin
     return lo;
 }
 
+// ---------------------------------------------------------------- encode --
+// Wave-level building blocks shared by the row encoder and the query
+// transform inside the scan.  A wave holds one padded row; lane l holds
+// elements [l*E, l*E+E) (E = P/64, or E = 1 with P lanes when P < 64).
+
+// Rotator.rotateInto (src/quant/rotator.ts:61-70): per round, multiply by
+// the round's signs (f32), then the in-place FWHT with len = 1, 2, 4, ...
+// Butterflies within a lane first, then across lanes (partner = lane ^
+// (len / E)); every butterfly is the reference's f32 (u+v, u-v).
+template <int E>
+__device__ __forceinline__ void rotate_wave(const float *src, uint32_t dim, uint32_t P, const float *signs,
+                                            uint32_t rounds, float (&x)[E], int lane) {
+#pragma clang fp contract(off)
+    const uint32_t lanes_used = P / E;
+    const uint32_t e0 = lane * E;
+    const bool active = (uint32_t)lane < lanes_used;
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+        const uint32_t e = e0 + t;
+        x[t] = (active && e < dim) ? src[e] : 0.0f;
+    }
+    for (uint32_t r = 0; r < rounds; ++r) {
+        const float *s = signs + (size_t)r * P;
+#pragma unroll
+        for (int t = 0; t < E; ++t) x[t] = active ? x[t] * s[e0 + t] : 0.0f;
+#pragma unroll
+        for (int len = 1; len < E; len <<= 1) {
+#pragma unroll
+            for (int t = 0; t < E; ++t) {
+                if (!(t & len)) {
+                    const float u = x[t], w = x[t + len];
+                    x[t] = u + w;
+                    x[t + len] = u - w;
+                }
+            }
+        }
+        for (uint32_t m = 1; m < lanes_used; m <<= 1) {
+            const bool hi = (lane & m) != 0;
+#pragma unroll
+            for (int t = 0; t < E; ++t) {
+                const float y = __shfl_xor(x[t], (int)m);
+                x[t] = hi ? (y - x[t]) : (x[t] + y);
+            }
+        }
+    }
+}
+
+// quantizeRow8 / quantizeRow4 / quantizeRow1 of a rotated row held by the
+// wave (src/quant/codec.ts:22-154): codes packed LSB-first into `codes`
+// (P/4, P/8 or P/32 words) and, when `scale` is set, the row scale.
+// cbytes: P bytes and fbuf: 4P bytes of wave-private LDS.
+template <int E>
+__device__ void quantize_store_wave(const float (&x)[E], uint32_t P, uint32_t bits, unsigned char *cbytes,
+                                    float *fbuf, uint32_t *codes, float *scale, uint32_t *slow_rows, int lane) {
+#pragma clang fp contract(off)
+    const uint32_t lanes_used = P / E;
+    const uint32_t e0 = lane * E;
+    const bool active = (uint32_t)lane < lanes_used;
+    if (bits == 8 || bits == 4) {
+        float m = 0.0f;
+#pragma unroll
+        for (int t = 0; t < E; ++t) {
+            const float v = fabsf(x[t]);
+            if (v > m) m = v;  // NaN never wins, as `a > maxAbs` in JS
+        }
+#pragma unroll
+        for (int s = 1; s < 64; s <<= 1) {
+            const float o = __shfl_xor(m, s);
+            if (o > m) m = o;
+        }
+        const double sc = m > 0.0f ? (double)m : 1.0;
+        const double inv = 1.0 / sc;
+        const double levels = bits == 8 ? 127.0 : 7.0;
+#pragma unroll
+        for (int t = 0; t < E; ++t) {
+            double c = (double)x[t] * inv;
+            c = c < -1.0 ? -1.0 : (c > 1.0 ? 1.0 : c);
+            const double y = c * levels;
+            double rr = floor(y);
+            if (y - rr >= 0.5) rr += 1.0;  // Math.round: ties toward +infinity
+            if (rr < -levels) rr = -levels;
+            if (rr > levels) rr = levels;
+            const int code = (rr == rr) ? (int)rr : 0;  // NaN -> 0 (ToInt32)
+            if (active) cbytes[e0 + t] = (unsigned char)(code & (bits == 8 ? 0xff : 0xf));
+        }
+        if (scale && lane == 0) *scale = (float)sc;
+    } else {  // 1-bit: signs, and mean |x| as a sequential f64 sum
+#pragma unroll
+        for (int t = 0; t < E; ++t)
+            if (active) cbytes[e0 + t] = x[t] >= 0.0f ? 1 : 0;
+        if (scale) {
+            double s = 0.0;
+            int emin = 1 << 20;
+#pragma unroll
+            for (int t = 0; t < E; ++t) {
+                const float v = fabsf(x[t]);
+                s += (double)v;
+                if (v != 0.0f) {
+                    const uint32_t b = __float_as_uint(v);
+                    const int ex = (int)((b >> 23) & 0xffu);
+                    const int ue = ex ? ex - 150 : -149;  // exponent of the value's ulp
+                    emin = ue < emin ? ue : emin;
+                }
+            }
+#pragma unroll
+            for (int sh = 1; sh < 64; sh <<= 1) {
+                s += __shfl_xor(s, sh);
+                const int o = __shfl_xor(emin, sh);
+                emin = o < emin ? o : emin;
+            }
+            // Every partial sum (any order) is a multiple of 2^emin no larger
+            // than the total; below 2^(emin+52) all are exact in f64, so the
+            // tree sum equals the reference's sequential one.  Otherwise take
+            // the sequential sum literally.
+            const bool exact = (s == 0.0) || (s < ldexp(1.0, emin + 52));
+            if (!exact) {
+                if (active) {
+#pragma unroll
+                    for (int t = 0; t < E; ++t) fbuf[e0 + t] = x[t];
+                }
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                double seq = 0.0;
+                if (lane == 0) {
+                    for (uint32_t i = 0; i < P; ++i) seq += (double)fabsf(fbuf[i]);
+                    if (slow_rows) atomicAdd(slow_rows, 1u);
+                }
+                s = __shfl(seq, 0);
+            }
+            if (lane == 0) *scale = s > 0.0 ? (float)(s / (double)P) : 1.0f;
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    // pack: word g covers `per` consecutive codes
+    const uint32_t per = bits == 8 ? 4 : (bits == 4 ? 8 : 32);
+    const uint32_t W = P / per, sh = bits == 8 ? 8 : (bits == 4 ? 4 : 1);
+    for (uint32_t g = lane; g < W; g += 64) {
+        uint32_t w = 0;
+        for (uint32_t j = 0; j < per; ++j) w |= (uint32_t)cbytes[g * per + j] << (sh * j);
+        codes[g] = w;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+// One wave per row: rotate, optionally store the rotation, quantize + pack.
+template <int E>
+__global__ __launch_bounds__(128) void encode_rows(EncodeArgs a) {
+    extern __shared__ unsigned char smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t P = a.P;
+    unsigned char *cbytes = smem + (size_t)wave * (P + 4 * P);
+    float *fbuf = (float *)(cbytes + P);
+    const uint32_t lanes_used = P / E;
+    const uint32_t e0 = lane * E;
+    const bool active = (uint32_t)lane < lanes_used;
+    const uint64_t nwaves = (uint64_t)gridDim.x * (blockDim.x >> 6);
+    for (uint64_t row = (uint64_t)blockIdx.x * (blockDim.x >> 6) + wave; row < a.rows; row += nwaves) {
+        float x[E];
+        rotate_wave<E>(a.src + row * a.dim, a.dim, P, a.signs, a.rounds, x, lane);
+        if (a.rotated && active) {
+#pragma unroll
+            for (int t = 0; t < E; ++t) a.rotated[row * P + e0 + t] = x[t];
+        }
+        if (a.bits == 0) continue;
+        const uint32_t W = P / (a.bits == 8 ? 4 : (a.bits == 4 ? 8 : 32));
+        quantize_store_wave<E>(x, P, a.bits, cbytes, fbuf, a.codes + row * W, a.scales + row, a.slow_rows, lane);
+    }
+}
+
+// ---------------------------------------------------------- query levels --
+// Splits a rotated query into three int8 levels (q ~= s1*q1 + s2*q2 + s3*q3,
+// each level quantizing the previous residual in f64) and packs them in the
+// per-unit layout the int8 / int4 scan codecs read, followed by QLevelTail.
+// The wave holds the query as in rotate_wave; lv: 3P bytes of LDS.
+template <int E>
+__device__ void levels_wave(const float (&x)[E], uint32_t P, int codec, signed char *lv, unsigned char *out,
+                            int lane) {
+    const uint32_t lanes_used = P / E;
+    const uint32_t e0 = lane * E;
+    const bool active = (uint32_t)lane < lanes_used;
+    double rd[E];
+#pragma unroll
+    for (int t = 0; t < E; ++t) rd[t] = active ? (double)x[t] : 0.0;
+    double sl[3];
+    int32_t sums[3];
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+        double m = 0.0;
+#pragma unroll
+        for (int t = 0; t < E; ++t) m = fmax(m, fabs(rd[t]));
+#pragma unroll
+        for (int sh = 1; sh < 64; sh <<= 1) m = fmax(m, __shfl_xor(m, sh));
+        const double sc = m > 0.0 ? m / 127.0 : 0.0;
+        const double inv = sc > 0.0 ? 1.0 / sc : 0.0;
+        int32_t sum = 0;
+#pragma unroll
+        for (int t = 0; t < E; ++t) {
+            double c = rint(rd[t] * inv);
+            c = c > 127.0 ? 127.0 : (c < -127.0 ? -127.0 : c);
+            rd[t] = fma(-sc, c, rd[t]);  // exact residual bookkeeping in f64
+            if (active) lv[l * P + e0 + t] = (signed char)(int)c;
+            sum += (int)c;
+        }
+#pragma unroll
+        for (int sh = 1; sh < 64; sh <<= 1) sum += __shfl_xor(sum, sh);
+        sl[l] = sc;
+        sums[l] = sum;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    uint32_t *w = (uint32_t *)out;
+    const unsigned char *lb = (const unsigned char *)lv;
+    uint32_t qwords;
+    if (codec == C_Q8) {
+        const uint32_t units = P / 16;
+        qwords = units * 12;
+        for (uint32_t i = lane; i < qwords; i += 64) {
+            const uint32_t u = i / 12, r = i % 12, l = r / 4, d = r % 4;
+            const uint32_t base = l * P + 16 * u + 4 * d;
+            w[i] = (uint32_t)lb[base] | ((uint32_t)lb[base + 1] << 8) | ((uint32_t)lb[base + 2] << 16) |
+                   ((uint32_t)lb[base + 3] << 24);
+        }
+    } else {  // C_Q4
+        const uint32_t units = P / 32;
+        qwords = units * 24;
+        for (uint32_t i = lane; i < qwords; i += 64) {
+            const uint32_t u = i / 24, r = i % 24, l = r / 8, d = (r % 8) / 2, h = r % 2;
+            const uint32_t base = l * P + 32 * u + 8 * d + h;
+            w[i] = (uint32_t)lb[base] | ((uint32_t)lb[base + 2] << 8) | ((uint32_t)lb[base + 4] << 16) |
+                   ((uint32_t)lb[base + 6] << 24);
+        }
+    }
+    if (lane == 0) {
+        QLevelTail *t = (QLevelTail *)(out + (uint64_t)qwords * 4);
+        const double div = codec == C_Q8 ? 127.0 : 1.0;
+        for (int l = 0; l < 3; ++l) {
+            t->s[l] = sl[l] / div;
+            t->sum[l] = sums[l];
+        }
+        t->pad = 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+// Standalone level split of rotated queries (nq x P): one wave per query.
+template <int E>
+__global__ __launch_bounds__(64) void query_levels(LevelArgs a) {
+    extern __shared__ unsigned char lsm[];
+    const uint32_t P = a.P, qi = blockIdx.x;
+    const int lane = threadIdx.x;
+    const uint32_t lanes_used = P / E, e0 = lane * E;
+    float x[E];
+    const float *q = a.qrot + (uint64_t)qi * P;
+#pragma unroll
+    for (int t = 0; t < E; ++t) x[t] = (uint32_t)lane < lanes_used ? q[e0 + t] : 0.0f;
+    levels_wave<E>(x, P, a.codec, (signed char *)lsm, a.out + (uint64_t)qi * a.stride, lane);
+}
+
+// Bytes of the scan's per-query layout for codec C at padded dimension P.
+__host__ __device__ inline size_t query_layout_bytes(int codec, uint32_t P) {
+    switch (codec) {
+    case C_Q8: return ((size_t)P / 16 * 12 * 4 + sizeof(QLevelTail) + 63) & ~(size_t)63;
+    case C_Q4: return ((size_t)P / 32 * 24 * 4 + sizeof(QLevelTail) + 63) & ~(size_t)63;
+    case C_Q1A: return (size_t)P * 4;
+    case C_HAM: return ((size_t)P / 32 * 4 + 15) & ~(size_t)15;
+    case C_I8S: return ((size_t)P / 4 * 4 + 15) & ~(size_t)15;
+    default: return 0;
+    }
+}
+// LDS the in-scan query transform needs: layout + scratch.
+__host__ __device__ inline size_t query_prep_lds(int codec, uint32_t P) {
+    const size_t lay = query_layout_bytes(codec, P);
+    if (codec == C_Q8 || codec == C_Q4) return lay + 3 * (size_t)P;
+    if (codec == C_HAM || codec == C_I8S) return lay + 5 * (size_t)P;
+    return lay;
+}
+
+// The query transform of the quantized scans, done by one wave of every
+// scanning workgroup straight from the fp32 query: rotation, then the
+// codec's layout (int8 levels, rotated floats, or quantized query codes) in
+// LDS at `lds`.  Byte-identical to the standalone encode + levels kernels.
+template <int C, int E>
+__device__ __forceinline__ void prep_query_e(const ScanArgs &a, uint32_t qi, unsigned char *lds, int lane) {
+    const uint32_t P = a.padded_dim;
+    float x[E];
+    rotate_wave<E>(a.qraw + (uint64_t)qi * a.qdim, a.qdim, P, a.signs, a.rounds, x, lane);
+    const size_t lay = query_layout_bytes(C, P);
+    if constexpr (C == C_Q8 || C == C_Q4) {
+        levels_wave<E>(x, P, C, (signed char *)(lds + lay), lds, lane);
+    } else if constexpr (C == C_Q1A) {
+        const uint32_t lanes_used = P / E, e0 = lane * E;
+        float *f = (float *)lds;
+        if ((uint32_t)lane < lanes_used) {
+#pragma unroll
+            for (int t = 0; t < E; ++t) f[e0 + t] = x[t];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    } else if constexpr (C == C_HAM || C == C_I8S) {
+        unsigned char *cbytes = lds + lay;
+        quantize_store_wave<E>(x, P, C == C_HAM ? 1 : 8, cbytes, (float *)(cbytes + P), (uint32_t *)lds, nullptr,
+                               nullptr, lane);
+    }
+}
+
+// Codes per scan unit, and the padded dimension / elements per lane for
+// which a scan layout does its own query transform: the layout's full unit
+// count (LPR * UPL units), with at most 16 elements per lane so the
+// transform's registers stay below the scan loop's.
+template <int C> struct UnitCodes {
+    static constexpr int v = (C == C_Q8 || C == C_I8S) ? 16 : (C == C_Q4 || C == C_Q1A) ? 32 : (C == C_HAM) ? 128 : 0;
+};
+template <int C, int LPR, int UPL> struct PrepShape {
+    static constexpr int P = UnitCodes<C>::v * LPR * UPL;
+    static constexpr int E = P >= 64 ? P / 64 : 1;
+    static constexpr bool ok = UnitCodes<C>::v > 0 && P >= 64 && E <= 16;
+};
+
+// ------------------------------------------------------------ exact score --
+// Store.dotRow of one stored fp32 row with the fp32 query, by one wave
+// (src/store/store.ts:114-130): four f64 accumulators over the strided
+// elements 4j+m, combined as ((a0+a1)+a2)+a3, then the tail elements.  The
+// wave loads row and query coalesced and stages every exact product
+// x[i]*q[i] (two 24-bit significands fit a double) in `stage` (vec doubles,
+// wave-private LDS), transposed so that accumulator m's terms are
+// contiguous; lanes 0..3 then add them in the reference's order (adding an
+// exact product rounds exactly like the reference's `acc += x*y`).  Returns
+// the (score, row) key in every lane.
+__device__ uint64_t exact_key_wave(const float *src, const float *qs, uint32_t dim, uint32_t row, double *stage,
+                                   int lane) {
+    const uint32_t vec = dim & ~3u, nv = vec >> 2;
+    constexpr int B = 8;
+    for (uint32_t e0 = 0; e0 < vec; e0 += 64 * B) {
+        float xv[B], qv[B];
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+            const uint32_t e = e0 + t * 64 + lane;
+            xv[t] = e < vec ? src[e] : 0.0f;
+            qv[t] = e < vec ? qs[e] : 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+            const uint32_t e = e0 + t * 64 + lane;
+            if (e < vec) stage[(e & 3) * nv + (e >> 2)] = (double)xv[t] * (double)qv[t];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    double acc = 0.0;
+    if (lane < 4) {
+        const double *pp = stage + (uint32_t)lane * nv;
+        uint32_t j = 0;
+        for (; j + 8 <= nv; j += 8) {
+            double t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = pp[j + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = acc + t[u];
+        }
+        for (; j < nv; ++j) acc = acc + pp[j];
+    }
+    const double a1 = __shfl(acc, 1), a2 = __shfl(acc, 2), a3 = __shfl(acc, 3);
+    uint64_t key = 0;
+    if (lane == 0) {
+        double sum = acc + a1;
+        sum = sum + a2;
+        sum = sum + a3;
+        for (uint32_t i = vec; i < dim; ++i) sum = fma((double)src[i], (double)qs[i], sum);
+        key = make_key(ord_f32((float)sum), row);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // stage is free again
+    return uniform_u64(key);
+}
+
 // ------------------------------------------------------------ scan + top-k --
-constexpr uint32_t TAU_POLL = 4;  // grabs between reads of the shared bound
+constexpr uint32_t TAU_POLL = 4;     // step pairs between reads of the shared bound
+constexpr uint32_t STATIC_PCT = 80;  // share of the grabs assigned statically
+constexpr uint32_t DSTEPS = 4;       // steps per dynamically assigned chunk
 
 // A unit slot past the end of a row (layouts whose lanes overhang the row)
 // must contribute nothing: zero query values do that for the dot-style codecs;
@@ -758,6 +1138,7 @@ __device__ void reset_query(const ScanArgs &a, uint32_t qi) {
     for (uint32_t r = threadIdx.x; r < (uint32_t)NGROUP; r += blockDim.x) {
         qs->done[r * CL] = 0;
         qs->cc[r * CL] = 0;
+        qs->dyn[r * CL] = 0;
     }
     if (threadIdx.x == 0) {
         qs->tau = 0;
@@ -849,16 +1230,12 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
 
     const int p = lane % LPR;
     ScanRegs<C, UPL> R;
-    const QT *qbase = (const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride);
 #pragma unroll
     for (int t = 0; t < UPL; ++t) {
         const uint32_t unit = p + LPR * t;
         R.uok[t] = unit < a.units;
         R.ucl[t] = R.uok[t] ? unit : a.units - 1;
-#pragma unroll
-        for (int j = 0; j < CD::QN; ++j) R.qr[t][j] = R.uok[t] ? qbase[unit * CD::QN + j] : (QT)0;
     }
-    R.fin.load((const char *)qbase + (uint64_t)a.units * CD::QN * sizeof(QT), a.padded_dim);
 
     const uint32_t *cand = a.cand;
     uint64_t n = a.n;
@@ -870,45 +1247,151 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     uint64_t lmax = 0, published = 0;
 
     const uint32_t wcap = a.wcap;
-    uint64_t *wk = (uint64_t *)scan_smem + (size_t)wave * wcap;
+    uint64_t *wk = (uint64_t *)scan_smem + (size_t)wave * a.wstride;  // list, then re-rank staging
     const uint32_t trig = wcap - SH::WGRAB;       // compact when the list passes this
     const uint32_t target = kp + (trig - kp) / 2;  // ... down to at most this many keys
     uint32_t wc = 0;
     uint64_t tau = 0;
-    // grabs g, g + grid, g + 2*grid, ... of GRAB_ROWS rows each; a wave
-    // covers two steps of every grab (rows wofs.. and wofs + half..)
+    const uint32_t ng = a.grid < (uint32_t)NGROUP ? a.grid : (uint32_t)NGROUP;
+
+    // ---- a wave's stream of steps ----
+    // Static part: grabs g = blockIdx.x + gi*grid for gi < sgrabs, each wave
+    // taking two steps of every grab (rows wofs.. and wofs + half..).
+    // Dynamic part: rows [d0, n) in chunks of DSTEPS consecutive steps, handed
+    // out per wave from ng slices that each have their own counter; a wave
+    // whose slice runs dry moves to the slice with the most chunks left.  The
+    // dynamic part absorbs speed differences between XCDs.
     static_assert(SH::GRAB_STEPS == 2, "two steps per grab");
+    const uint64_t wofs = (uint64_t)wave * SH::RPS, half = (uint64_t)SH::WAVES * SH::RPS;
+    const uint64_t dch = (uint64_t)DSTEPS * SH::RPS;  // rows per dynamic chunk
+    const uint64_t ngrabs = (n + SH::GRAB_ROWS - 1) / SH::GRAB_ROWS;
+    const uint64_t sgrabs = ngrabs * STATIC_PCT / 100 / a.grid;  // full static grabs per workgroup
+    uint64_t d0 = sgrabs * a.grid * SH::GRAB_ROWS;
+    if (d0 > n) d0 = n;
+    const uint64_t nchunks = (n - d0 + dch - 1) / dch;
+    const uint64_t per = (nchunks + ng - 1) / ng;  // chunks per slice
+    auto slice_len = [&](uint32_t r) -> uint64_t {
+        const uint64_t lo = (uint64_t)r * per;
+        return lo >= nchunks ? 0 : (nchunks - lo < per ? nchunks - lo : per);
+    };
+    uint64_t gi = 0;
+    uint32_t sub = 0, ds = DSTEPS, slice = (blockIdx.x * SH::WAVES + wave) % ng, pend = 0;
+    bool dynamic = false, has_pend = false;
+    uint64_t c0 = 0, clim = 0;
+    // next dynamic chunk index, or ~0 when every slice is exhausted
+    auto take_chunk = [&]() -> uint64_t {
+        for (;;) {
+            uint32_t t;
+            if (has_pend) {
+                t = __builtin_amdgcn_readfirstlane(pend);
+                has_pend = false;
+            } else {
+                uint32_t v = 0;
+                if (lane == 0) v = atomicAdd(&qs->dyn[slice * CL], 1u);
+                t = __builtin_amdgcn_readfirstlane(v);
+            }
+            if (t < slice_len(slice)) {
+                if (lane == 0) pend = atomicAdd(&qs->dyn[slice * CL], 1u);  // next ticket in flight
+                has_pend = true;
+                return (uint64_t)slice * per + t;
+            }
+            // this slice is exhausted (its counter never drops): read every
+            // slice's counter at once and move to the one with most left
+            uint64_t rem = 0;
+            if ((uint32_t)lane < ng) {
+                const uint32_t c = load_shared(&qs->dyn[lane * CL]);
+                const uint64_t L = slice_len(lane);
+                rem = c < L ? L - c : 0;
+            }
+            const uint64_t best = wave_max_u64((rem << 32) | (uint32_t)lane);
+            if ((best >> 32) == 0) return ~0ull;
+            slice = (uint32_t)best;
+        }
+    };
+    auto next_step = [&](uint64_t &base, uint64_t &lim) -> bool {
+        if (!dynamic) {
+            while (gi < sgrabs) {
+                const uint64_t r0 = ((uint64_t)blockIdx.x + gi * a.grid) * SH::GRAB_ROWS;
+                base = r0 + wofs + (sub ? half : 0);
+                lim = r0 + SH::GRAB_ROWS < n ? r0 + SH::GRAB_ROWS : n;
+                if (++sub == 2) {
+                    sub = 0;
+                    ++gi;
+                }
+                if (base < lim) return true;
+            }
+            dynamic = true;
+        }
+        for (;;) {
+            if (ds < DSTEPS) {
+                base = c0 + (uint64_t)ds * SH::RPS;
+                ++ds;
+                if (base < clim) {
+                    lim = clim;
+                    return true;
+                }
+                ds = DSTEPS;
+            }
+            if (nchunks == 0) return false;
+            const uint64_t c = take_chunk();
+            if (c == ~0ull) return false;
+            c0 = d0 + c * dch;
+            clim = c0 + dch < n ? c0 + dch : n;
+            ds = 0;
+        }
+    };
+
     using SD = StepData<C, LPR, UPL>;
     constexpr bool PIPE = SH::U * UPL * (int)(sizeof(typename CD::Unit) / 4) <= 32;  // double-buffer the loads
-    const uint64_t wofs = (uint64_t)wave * SH::RPS, half = (uint64_t)SH::WAVES * SH::RPS;
-    const uint64_t gstride = (uint64_t)a.grid * SH::GRAB_ROWS;
     SD A, B;
-    uint64_t r0 = (uint64_t)blockIdx.x * SH::GRAB_ROWS;
-    if (PIPE && r0 < n)
-        load_step<C, LPR, UPL, IDX>(a, R, cand, r0 + wofs, r0 + SH::GRAB_ROWS < n ? r0 + SH::GRAB_ROWS : n, A, lane);
-    for (uint32_t gi = 0; r0 < n; ++gi) {
-        const uint64_t lim = r0 + SH::GRAB_ROWS < n ? r0 + SH::GRAB_ROWS : n;
-        // read the shared bound every TAU_POLL grabs (waves staggered): it is
-        // one cache line that every wave of the grid would otherwise hammer
-        const bool poll = (gi + (uint32_t)wave) % TAU_POLL == 0;
+    uint64_t ab = 0, al = 0, bb = 0, bl = 0;
+    bool ha = next_step(ab, al);
+    if (PIPE && ha) load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);  // needs no query yet
+
+    // the query slice: transformed here by wave 0 into LDS (while the first
+    // code loads are in flight), or read from a prepared global layout
+    const QT *qbase;
+    if (PrepShape<C, LPR, UPL>::ok && a.qraw) {
+        if constexpr (PrepShape<C, LPR, UPL>::ok) {
+            if (wave == 0) prep_query_e<C, PrepShape<C, LPR, UPL>::E>(a, qi, scan_smem, lane);
+        }
+        __syncthreads();
+        qbase = (const QT *)scan_smem;
+    } else {
+        qbase = (const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride);
+    }
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+#pragma unroll
+        for (int j = 0; j < CD::QN; ++j) R.qr[t][j] = R.uok[t] ? qbase[(p + LPR * t) * CD::QN + j] : (QT)0;
+    }
+    R.fin.load((const char *)qbase + (uint64_t)a.units * CD::QN * sizeof(QT), a.padded_dim);
+    if (a.qraw) __syncthreads();  // the LDS holding it becomes the waves' lists
+    for (uint32_t pi = 0; ha; ++pi) {
+        // read the shared bound every TAU_POLL step pairs (waves staggered):
+        // it is one cache line that every wave of the grid would otherwise hammer
+        const bool poll = (pi + (uint32_t)wave) % TAU_POLL == 0;
         uint64_t gt = 0;
         if (poll) gt = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint64_t nr0 = r0 + gstride;
         if constexpr (PIPE) {
             // the next step's loads are in flight while this one is scored
-            load_step<C, LPR, UPL, IDX>(a, R, cand, r0 + wofs + half, lim, B, lane);
-            compute_step<C, LPR, UPL>(a, R, A, r0 + wofs, lim, tau, wk, wc, lmax, lane);
-            if (nr0 < n)
-                load_step<C, LPR, UPL, IDX>(a, R, cand, nr0 + wofs, nr0 + SH::GRAB_ROWS < n ? nr0 + SH::GRAB_ROWS : n,
-                                            A, lane);
-            compute_step<C, LPR, UPL>(a, R, B, r0 + wofs + half, lim, tau, wk, wc, lmax, lane);
+            const bool hb = next_step(bb, bl);
+            if (hb) load_step<C, LPR, UPL, IDX>(a, R, cand, bb, bl, B, lane);
+            compute_step<C, LPR, UPL>(a, R, A, ab, al, tau, wk, wc, lmax, lane);
+            ha = hb && next_step(ab, al);
+            if (ha) load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
+            if (hb) compute_step<C, LPR, UPL>(a, R, B, bb, bl, tau, wk, wc, lmax, lane);
         } else {
-            load_step<C, LPR, UPL, IDX>(a, R, cand, r0 + wofs, lim, A, lane);
-            compute_step<C, LPR, UPL>(a, R, A, r0 + wofs, lim, tau, wk, wc, lmax, lane);
-            load_step<C, LPR, UPL, IDX>(a, R, cand, r0 + wofs + half, lim, A, lane);
-            compute_step<C, LPR, UPL>(a, R, A, r0 + wofs + half, lim, tau, wk, wc, lmax, lane);
+            load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
+            compute_step<C, LPR, UPL>(a, R, A, ab, al, tau, wk, wc, lmax, lane);
+            if (next_step(ab, al)) {
+                load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
+                compute_step<C, LPR, UPL>(a, R, A, ab, al, tau, wk, wc, lmax, lane);
+                ha = next_step(ab, al);
+            } else {
+                ha = false;
+            }
         }
-        r0 = nr0;
         publish_wave_max(wslot, lmax, published, lane);
         if (poll) {
             const uint64_t ugt = uniform_u64(gt);
@@ -932,15 +1415,34 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         tau = gt > tau ? gt : tau;
         wc = wave_filter(wk, wc, tau, lane);
     }
-    const uint32_t ng = a.grid < (uint32_t)NGROUP ? a.grid : (uint32_t)NGROUP;
+    // Flushed entries are (scan key, exact key) pairs; with re-ranking on,
+    // the wave scores its own candidates exactly here, while other waves of
+    // the grid are still scanning.
     const uint32_t grp = blockIdx.x % ng;
-    const uint64_t region = a.cand_cap / ng;  // keys per group region
+    const uint64_t region = a.cand_cap / ng;  // pairs per group region
     if (wc) {
         uint32_t base = 0;
         if (lane == 0) base = atomicAdd(&qs->cc[grp * CL], wc);
         base = __builtin_amdgcn_readfirstlane(base);
-        uint64_t *ck = a.cand_keys + (uint64_t)qi * a.cand_cap + grp * region + base;
-        for (uint32_t j = lane; j < wc; j += 64) store_shared(&ck[j], wk[j]);
+        uint64_t *ck = a.cand_keys + 2 * ((uint64_t)qi * a.cand_cap + grp * region + base);
+        if (a.rr_src) {
+            double *stage = (double *)(wk + wcap);
+            const float *rq = a.rr_q + (uint64_t)qi * a.rr_q_stride;
+            for (uint32_t j = 0; j < wc; ++j) {
+                const uint64_t k = wk[j];
+                const uint32_t row = key_row(k);
+                const uint64_t ek = exact_key_wave(a.rr_src + (uint64_t)row * a.rr_dim, rq, a.rr_dim, row, stage, lane);
+                if (lane == 0) {
+                    store_shared(&ck[2 * j], k);
+                    store_shared(&ck[2 * j + 1], ek);
+                }
+            }
+        } else {
+            for (uint32_t j = lane; j < wc; j += 64) {
+                store_shared(&ck[2 * j], wk[j]);
+                store_shared(&ck[2 * j + 1], 0ull);
+            }
+        }
     }
     wait_stores_done();
     __syncthreads();
@@ -972,7 +1474,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         L.ovl[32 + ng] = acc;
     }
     __syncthreads();
-    const uint64_t *ckq = a.cand_keys + (uint64_t)qi * a.cand_cap;
+    const uint64_t *ckq = a.cand_keys + 2 * (uint64_t)qi * a.cand_cap;
     const uint32_t total = L.ovl[32 + ng];
     constexpr uint32_t CHUNK = SCAN_CAP / 2;
     for (uint32_t c0 = 0; c0 < total; c0 += CHUNK) {
@@ -987,7 +1489,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
                 if (i < c1) {
                     uint32_t r = 0;
                     while (r + 1 < ng && L.ovl[32 + r + 1] <= i) ++r;
-                    v[j] = load_shared(&ckq[r * region + (i - L.ovl[32 + r])]);
+                    v[j] = load_shared(&ckq[2 * (r * region + (i - L.ovl[32 + r]))]);
                 }
             }
 #pragma unroll
@@ -1007,7 +1509,44 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     uint64_t *outk = a.merged + (uint64_t)qi * kp;
     for (uint32_t j = tid; j < kp; j += SCAN_WG) outk[j] = j < m ? L.keys[j] : 0;
     if (tid == 0) a.merged_n[qi] = m;
-    if (a.out_rows) {
+    if (a.rr_src) {
+        // the fetch set is every flushed pair whose scan key is at least the
+        // m-th best; rank its exact keys and keep the best k_out
+        const uint64_t T = m ? L.keys[m - 1] : ~0ull;
+        __syncthreads();
+        if (tid == 0) L.cnt2 = 0;
+        __syncthreads();
+        for (uint32_t i0 = 0; i0 < total; i0 += 4 * SCAN_WG) {
+            uint64_t v[4], e[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t i = i0 + j * SCAN_WG + tid;
+                v[j] = 0;
+                e[j] = 0;
+                if (i < total) {
+                    uint32_t r = 0;
+                    while (r + 1 < ng && L.ovl[32 + r + 1] <= i) ++r;
+                    const uint64_t slot = 2 * (r * region + (i - L.ovl[32 + r]));
+                    v[j] = load_shared(&ckq[slot]);
+                    e[j] = load_shared(&ckq[slot + 1]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) wave_append(L.tmp, &L.cnt2, SEL_TMP, v[j] != 0 && v[j] >= T, e[j], lane);
+        }
+        __syncthreads();
+        const uint32_t mm = L.cnt2 < (uint32_t)SEL_TMP ? L.cnt2 : (uint32_t)SEL_TMP;
+        const uint32_t ko = mm < a.k_out ? mm : a.k_out;
+        for (uint32_t j = tid; j < mm; j += SCAN_WG) {
+            const uint64_t ek = L.tmp[j];
+            const uint32_t r = count_greater(L.tmp, mm, ek);
+            if (r < ko) {
+                a.out_rows[(uint64_t)qi * a.k_out + r] = key_row(ek);
+                a.out_scores[(uint64_t)qi * a.k_out + r] = f32_from_ord((uint32_t)(ek >> 32));
+            }
+        }
+        if (tid == 0) a.out_n[qi] = ko;
+    } else if (a.out_rows) {
         const uint32_t ko = m < a.k_out ? m : a.k_out;
         for (uint32_t j = tid; j < ko; j += SCAN_WG) {
             const uint64_t kk = L.keys[j];
@@ -1024,229 +1563,10 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     if (L.last) reset_query(a, qi);
 }
 
-// ---------------------------------------------------------------- encode --
-// One wave per row.  Lane l holds elements [l*E, l*E+E) of the padded row.
-template <int E>
-__global__ __launch_bounds__(128) void encode_rows(EncodeArgs a) {
-#pragma clang fp contract(off)
-    extern __shared__ unsigned char smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t P = a.P;
-    unsigned char *cbytes = smem + (size_t)wave * (P + 4 * P);
-    float *fbuf = (float *)(cbytes + P);
-    const uint32_t lanes_used = P / E;  // 64, or P when P < 64
-    const uint32_t e0 = lane * E;
-    const bool active = (uint32_t)lane < lanes_used;
-    const uint64_t nwaves = (uint64_t)gridDim.x * (blockDim.x >> 6);
-
-    for (uint64_t row = (uint64_t)blockIdx.x * (blockDim.x >> 6) + wave; row < a.rows; row += nwaves) {
-        float x[E];
-        const float *src = a.src + row * a.dim;
-#pragma unroll
-        for (int t = 0; t < E; ++t) {
-            const uint32_t e = e0 + t;
-            x[t] = (active && e < a.dim) ? src[e] : 0.0f;
-        }
-        for (uint32_t r = 0; r < a.rounds; ++r) {
-            const float *s = a.signs + (size_t)r * P;
-#pragma unroll
-            for (int t = 0; t < E; ++t) x[t] = active ? x[t] * s[e0 + t] : 0.0f;
-            // stages len = 1, 2, ... < E inside the lane
-#pragma unroll
-            for (int len = 1; len < E; len <<= 1) {
-#pragma unroll
-                for (int t = 0; t < E; ++t) {
-                    if (!(t & len)) {
-                        const float u = x[t], w = x[t + len];
-                        x[t] = u + w;
-                        x[t + len] = u - w;
-                    }
-                }
-            }
-            // stages len >= E across lanes (partner = lane ^ (len / E))
-            for (uint32_t m = 1; m < lanes_used; m <<= 1) {
-                const bool hi = (lane & m) != 0;
-#pragma unroll
-                for (int t = 0; t < E; ++t) {
-                    const float y = __shfl_xor(x[t], (int)m);
-                    x[t] = hi ? (y - x[t]) : (x[t] + y);
-                }
-            }
-        }
-        if (a.rotated && active) {
-#pragma unroll
-            for (int t = 0; t < E; ++t) a.rotated[row * P + e0 + t] = x[t];
-        }
-        if (a.qdiv && active) {
-#pragma unroll
-            for (int t = 0; t < E; ++t) a.qdiv[row * P + e0 + t] = x[t] / 127.0f;
-        }
-        if (a.bits == 0) continue;
-
-        if (a.bits == 8 || a.bits == 4) {
-            float m = 0.0f;
-#pragma unroll
-            for (int t = 0; t < E; ++t) {
-                const float v = fabsf(x[t]);
-                if (v > m) m = v;  // NaN never wins, as `a > maxAbs` in JS
-            }
-#pragma unroll
-            for (int s = 1; s < 64; s <<= 1) {
-                const float o = __shfl_xor(m, s);
-                if (o > m) m = o;
-            }
-            const double scale = m > 0.0f ? (double)m : 1.0;
-            const double inv = 1.0 / scale;
-            const double levels = a.bits == 8 ? 127.0 : 7.0;
-#pragma unroll
-            for (int t = 0; t < E; ++t) {
-                double c = (double)x[t] * inv;
-                c = c < -1.0 ? -1.0 : (c > 1.0 ? 1.0 : c);
-                const double y = c * levels;
-                double rr = floor(y);
-                if (y - rr >= 0.5) rr += 1.0;  // Math.round: ties toward +infinity
-                if (rr < -levels) rr = -levels;
-                if (rr > levels) rr = levels;
-                const int code = (rr == rr) ? (int)rr : 0;  // NaN -> 0 (ToInt32)
-                if (active) cbytes[e0 + t] = (unsigned char)(code & (a.bits == 8 ? 0xff : 0xf));
-            }
-            if (lane == 0) a.scales[row] = (float)scale;
-        } else {  // 1-bit: signs, and mean |x| as a sequential f64 sum
-            double s = 0.0;
-            int emin = 1 << 20;
-#pragma unroll
-            for (int t = 0; t < E; ++t) {
-                const float v = fabsf(x[t]);
-                s += (double)v;
-                if (v != 0.0f) {
-                    const uint32_t b = __float_as_uint(v);
-                    const int ex = (int)((b >> 23) & 0xffu);
-                    const int ue = ex ? ex - 150 : -149;  // exponent of the value's ulp
-                    emin = ue < emin ? ue : emin;
-                }
-                if (active) cbytes[e0 + t] = x[t] >= 0.0f ? 1 : 0;
-            }
-#pragma unroll
-            for (int sh = 1; sh < 64; sh <<= 1) {
-                s += __shfl_xor(s, sh);
-                const int o = __shfl_xor(emin, sh);
-                emin = o < emin ? o : emin;
-            }
-            // Every partial sum (any order) is a multiple of 2^emin no larger
-            // than the total; below 2^(emin+52) all are exact in f64, so the
-            // tree sum equals the reference's sequential one.  Otherwise take
-            // the sequential sum literally.
-            const bool exact = (s == 0.0) || (s < ldexp(1.0, emin + 52));
-            if (!exact) {
-                if (active) {
-#pragma unroll
-                    for (int t = 0; t < E; ++t) fbuf[e0 + t] = x[t];
-                }
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-                double seq = 0.0;
-                if (lane == 0) {
-                    for (uint32_t i = 0; i < P; ++i) seq += (double)fabsf(fbuf[i]);
-                    if (a.slow_rows) atomicAdd(a.slow_rows, 1u);
-                }
-                s = __shfl(seq, 0);
-            }
-            if (lane == 0) a.scales[row] = s > 0.0 ? (float)(s / (double)P) : 1.0f;
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        // pack from LDS: word g covers `per` consecutive codes
-        const uint32_t per = a.bits == 8 ? 4 : (a.bits == 4 ? 8 : 32);
-        const uint32_t W = P / per, sh = a.bits == 8 ? 8 : (a.bits == 4 ? 4 : 1);
-        for (uint32_t g = lane; g < W; g += 64) {
-            uint32_t w = 0;
-            for (uint32_t j = 0; j < per; ++j) w |= (uint32_t)cbytes[g * per + j] << (sh * j);
-            a.codes[row * W + g] = w;
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    }
-}
-
-// ---------------------------------------------------------- query levels --
-// Splits each rotated query into three int8 levels (q ~= s1*q1 + s2*q2 +
-// s3*q3, each level quantizing the previous residual) and packs them in the
-// per-unit layout the int8 / int4 scan codecs read.  One wave per query.
-__global__ __launch_bounds__(64) void query_levels(LevelArgs a) {
-    extern __shared__ unsigned char lsm[];
-    const uint32_t P = a.P, qi = blockIdx.x;
-    const int lane = threadIdx.x;
-    signed char *lv = (signed char *)lsm;                   // 3 x P codes
-    double *rd = (double *)(lsm + ((3 * (size_t)P + 15) & ~(size_t)15));  // P residuals
-    const float *q = a.qrot + (uint64_t)qi * P;
-    for (uint32_t e = lane; e < P; e += 64) rd[e] = (double)q[e];
-    __syncthreads();
-    double sl[3];
-    int32_t sums[3];
-#pragma unroll
-    for (int l = 0; l < 3; ++l) {
-        double m = 0.0;
-        for (uint32_t e = lane; e < P; e += 64) m = fmax(m, fabs(rd[e]));
-#pragma unroll
-        for (int sh = 1; sh < 64; sh <<= 1) m = fmax(m, __shfl_xor(m, sh));
-        const double sc = m > 0.0 ? m / 127.0 : 0.0;
-        int32_t sum = 0;
-        for (uint32_t e = lane; e < P; e += 64) {
-            double c = sc > 0.0 ? rint(rd[e] / sc) : 0.0;
-            c = c > 127.0 ? 127.0 : (c < -127.0 ? -127.0 : c);
-            rd[e] = fma(-sc, c, rd[e]);
-            lv[l * P + e] = (signed char)(int)c;
-            sum += (int)c;
-        }
-#pragma unroll
-        for (int sh = 1; sh < 64; sh <<= 1) sum += __shfl_xor(sum, sh);
-        sl[l] = sc;
-        sums[l] = sum;
-    }
-    __syncthreads();
-    unsigned char *out = a.out + (uint64_t)qi * a.stride;
-    uint32_t *w = (uint32_t *)out;
-    const unsigned char *lb = (const unsigned char *)lv;
-    uint32_t qwords;
-    if (a.codec == C_Q8) {
-        const uint32_t units = P / 16;
-        qwords = units * 12;
-        for (uint32_t i = lane; i < qwords; i += 64) {
-            const uint32_t u = i / 12, r = i % 12, l = r / 4, d = r % 4;
-            const uint32_t base = l * P + 16 * u + 4 * d;
-            w[i] = (uint32_t)lb[base] | ((uint32_t)lb[base + 1] << 8) | ((uint32_t)lb[base + 2] << 16) |
-                   ((uint32_t)lb[base + 3] << 24);
-        }
-    } else {  // C_Q4
-        const uint32_t units = P / 32;
-        qwords = units * 24;
-        for (uint32_t i = lane; i < qwords; i += 64) {
-            const uint32_t u = i / 24, r = i % 24, l = r / 8, d = (r % 8) / 2, h = r % 2;
-            const uint32_t base = l * P + 32 * u + 8 * d + h;
-            w[i] = (uint32_t)lb[base] | ((uint32_t)lb[base + 2] << 8) | ((uint32_t)lb[base + 4] << 16) |
-                   ((uint32_t)lb[base + 6] << 24);
-        }
-    }
-    if (lane == 0) {
-        QLevelTail *t = (QLevelTail *)(out + (uint64_t)qwords * 4);
-        const double div = a.codec == C_Q8 ? 127.0 : 1.0;
-        for (int l = 0; l < 3; ++l) {
-            t->s[l] = sl[l] / div;
-            t->sum[l] = sums[l];
-        }
-        t->pad = 0;
-    }
-}
-
 // ---------------------------------------------------------------- rerank --
-// One wave per candidate.  The wave loads the row and query coalesced and
-// stages every exact f64 product x[i]*q[i] (exact: two 24-bit significands)
-// in LDS, transposed so that accumulator m's terms x[4j+m]*q[4j+m] are
-// contiguous.  Lanes 0..3 then run Store.dotRow's four strided f64 sums
-// (src/store/store.ts:114-130) in their original order (adding an exact
-// product rounds exactly like the reference's `acc += x*y`), and lane 0 adds
-// ((a0+a1)+a2)+a3 and the tail.  The last wave of each query ranks the
-// re-ranked keys and writes the top-k_out.  Dynamic LDS: 8 * (dim & ~3).
+// Re-rank of an explicit candidate list: one wave per candidate computes
+// Store.dotRow exactly (exact_key_wave); the last wave of each query ranks
+// the re-ranked keys and writes the top-k_out.  Dynamic LDS: 8 * (dim & ~3).
 __global__ __launch_bounds__(64) void rerank_topk(RerankArgs a) {
     extern __shared__ __align__(16) double prod[];
     __shared__ uint64_t keys[MAX_KPRIME];
@@ -1270,46 +1590,9 @@ __global__ __launch_bounds__(64) void rerank_topk(RerankArgs a) {
         }
     }
     if (have) {
-        const uint32_t dim = a.dim, vec = dim & ~3u, nv = vec >> 2;
-        const float *src = a.rows + (uint64_t)row * dim;
-        const float *qs = a.q + (uint64_t)qi * a.q_stride;
-        constexpr int B = 8;
-        for (uint32_t e0 = 0; e0 < vec; e0 += 64 * B) {
-            float xv[B], qv[B];
-#pragma unroll
-            for (int t = 0; t < B; ++t) {
-                const uint32_t e = e0 + t * 64 + lane;
-                xv[t] = e < vec ? src[e] : 0.0f;
-                qv[t] = e < vec ? qs[e] : 0.0f;
-            }
-#pragma unroll
-            for (int t = 0; t < B; ++t) {
-                const uint32_t e = e0 + t * 64 + lane;
-                if (e < vec) prod[(e & 3) * nv + (e >> 2)] = (double)xv[t] * (double)qv[t];
-            }
-        }
-        __syncthreads();
-        double acc = 0.0;
-        if (lane < 4) {
-            const double *pp = prod + (uint32_t)lane * nv;
-            uint32_t j = 0;
-            for (; j + 8 <= nv; j += 8) {
-                double t[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) t[u] = pp[j + u];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) acc = acc + t[u];
-            }
-            for (; j < nv; ++j) acc = acc + pp[j];
-        }
-        const double a1 = __shfl(acc, 1), a2 = __shfl(acc, 2), a3 = __shfl(acc, 3);
-        if (lane == 0) {
-            double s = acc + a1;
-            s = s + a2;
-            s = s + a3;
-            for (uint32_t i = vec; i < dim; ++i) s = fma((double)src[i], (double)qs[i], s);
-            store_shared(&a.rr_keys[(uint64_t)qi * a.kprime + c], make_key(ord_f32((float)s), row));
-        }
+        const uint64_t ek = exact_key_wave(a.rows + (uint64_t)row * a.dim, a.q + (uint64_t)qi * a.q_stride, a.dim, row,
+                                           prod, lane);
+        if (lane == 0) store_shared(&a.rr_keys[(uint64_t)qi * a.kprime + c], ek);
     }
     wait_stores_done();
     __syncthreads();
@@ -1380,8 +1663,15 @@ template <int C, int LPR, int UPL>
 hipError_t go(const ScanArgs &a, uint32_t nq, hipStream_t s) {
     // the per-wave lists must take a whole grab above the compaction target
     if (a.wcap < 2 * a.kprime + ScanShape<C, LPR, UPL>::WGRAB || (a.wcap & 63)) return hipErrorInvalidValue;
-    size_t lds = (size_t)(SCAN_WG / 64) * a.wcap * sizeof(uint64_t);
+    if (a.wstride < a.wcap || (a.rr_src && a.wstride < a.wcap + (a.rr_dim & ~3u))) return hipErrorInvalidValue;
+    size_t lds = (size_t)(SCAN_WG / 64) * a.wstride * sizeof(uint64_t);
     if (lds < sizeof(TopkLds)) lds = sizeof(TopkLds);
+    if (a.qraw) {
+        if (!PrepShape<C, LPR, UPL>::ok || a.padded_dim != (uint32_t)PrepShape<C, LPR, UPL>::P)
+            return hipErrorInvalidValue;
+        const size_t need = (query_prep_lds(C, a.padded_dim) + 15) & ~(size_t)15;
+        if (lds < need) lds = need;
+    }
     if (a.cand)
         hipLaunchKernelGGL((scan_topk<C, LPR, UPL, true>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, a);
     else
@@ -1463,15 +1753,36 @@ hipError_t launch_encode(const EncodeArgs &a, hipStream_t s) {
 
 hipError_t launch_levels(const LevelArgs &a, uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
-    const size_t lds = ((3 * (size_t)a.P + 15) & ~(size_t)15) + 8 * (size_t)a.P;
-    hipLaunchKernelGGL(query_levels, dim3(nq), dim3(64), lds, s, a);
+    const size_t lds = 3 * (size_t)a.P;
+    switch (a.P >= 64 ? a.P / 64 : 1) {
+    case 1: hipLaunchKernelGGL(query_levels<1>, dim3(nq), dim3(64), lds, s, a); break;
+    case 2: hipLaunchKernelGGL(query_levels<2>, dim3(nq), dim3(64), lds, s, a); break;
+    case 4: hipLaunchKernelGGL(query_levels<4>, dim3(nq), dim3(64), lds, s, a); break;
+    case 8: hipLaunchKernelGGL(query_levels<8>, dim3(nq), dim3(64), lds, s, a); break;
+    case 16: hipLaunchKernelGGL(query_levels<16>, dim3(nq), dim3(64), lds, s, a); break;
+    case 32: hipLaunchKernelGGL(query_levels<32>, dim3(nq), dim3(64), lds, s, a); break;
+    case 64: hipLaunchKernelGGL(query_levels<64>, dim3(nq), dim3(64), lds, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
-size_t level_stride(int codec, uint32_t P) {
-    const size_t words = codec == C_Q8 ? (size_t)P / 16 * 12 : (size_t)P / 32 * 24;
-    return (words * 4 + sizeof(QLevelTail) + 63) & ~(size_t)63;
+size_t level_stride(int codec, uint32_t P) { return query_layout_bytes(codec, P); }
+
+bool scan_prep_supported(int codec, uint32_t units, uint32_t P) {
+    Layout L;
+    if (!pick_layout(units, L)) return false;
+    int upc = 0;
+    switch (codec) {
+    case C_Q8: case C_I8S: upc = 16; break;
+    case C_Q4: case C_Q1A: upc = 32; break;
+    case C_HAM: upc = 128; break;
+    default: return false;
+    }
+    const uint32_t full = (uint32_t)upc * L.lpr * L.upl;
+    return P == full && P >= 64 && P / 64 <= 16;
 }
+size_t scan_query_lds(int codec, uint32_t P) { return query_prep_lds(codec, P); }
 
 hipError_t launch_rerank(const RerankArgs &a, uint32_t nq, hipStream_t s) {
     const size_t lds = sizeof(double) * (size_t)(a.dim & ~3u) + 16;
