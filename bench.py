@@ -122,7 +122,20 @@ def main():
     ap.add_argument("--batch-steps", type=int, default=8, help="timed batch-256 steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-only", action="store_true", help="build + a short timed loop (for rocprofv3)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 10 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+
+    if args.copy_calibration:
+        import torch
+
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": src.numel() * 4, "launches": 10}))
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU; the search path shards by rows across GPUs "
@@ -159,8 +172,15 @@ def main():
         return
     # kernel timing covered warmup + steps launches
     scan_avg_ms = scan_ms / max(launches, 1)
-    scan_bytes = args.rows * (row_bytes + 4)  # codes + scales per launch
+    # algorithmic bytes of the one launch per query: codes + scales + the
+    # fp32 rows of the re-ranked fetch
+    scan_bytes = args.rows * (row_bytes + 4) + args.fetch * args.dim * 4
     achieved = scan_bytes / (scan_avg_ms * 1e-3) / 1e9
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "scan_topk_q8_1Mx768_traffic.json")
+    if (args.rows, args.dim, args.bits, args.fetch) == (1_000_000, 768, 8, 100) and os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get("traffic_bytes")
 
     # ---- batch 256 ------------------------------------------------------------
     nb = min(256, args.queries)
@@ -206,7 +226,7 @@ def main():
                          f"({os.cpu_count()} logical CPUs visible)"}
         del xh
 
-    algo_bytes_q = args.rows * (row_bytes + 4) + args.fetch * args.dim * 4
+    algo_bytes_q = scan_bytes
     out = {
         "metric": METRIC,
         "value": round(qps_b1, 2),
@@ -225,9 +245,11 @@ def main():
                    "rows": args.rows, "dim": args.dim, "padded_dim": P, "bits": args.bits, "fetch": args.fetch,
                    "k": args.k, "queries": args.queries, "rotation_seed": "0x9e3779b9", "data_seed": hex(seed)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "scan_topk<C_Q8,64,1>", "kernel_avg_us": round(scan_avg_ms * 1e3, 2),
-                     "algorithmic_bytes_per_launch": scan_bytes},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "scan_topk<C_Q8,64,1> (query rotate+levels, scan, top-100, exact re-rank)",
+                     "kernel_avg_us": round(scan_avg_ms * 1e3, 2),
+                     "algorithmic_bytes_per_launch": scan_bytes,
+                     "traffic_source": "profiles/scan_topk_q8_1Mx768_traffic.md" if traffic else None},
         "cpu_baseline": cpu,
         "batch256_qps": round(qps_b256, 1),
         "recall_at_10": round(recall, 4),

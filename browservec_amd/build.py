@@ -50,6 +50,32 @@ def _compile(src: str, obj: str) -> None:
         sys.stderr.write(warn + "\n")
 
 
+NODE_INCLUDE = os.environ.get("BV_NODE_INCLUDE", "/usr/include/node")
+NAPI_SRC = os.path.join(HERE, "napi", "bv_napi.c")
+NAPI_OUT = os.path.join(LIBDIR, "browservec_napi.node")
+
+
+def build_napi(verbose: bool = True) -> str | None:
+    """The Node binding (N-API addon over the C ABI); skipped when the image
+    has no Node headers."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        if verbose:
+            print(f"skipped {NAPI_OUT}: no node_api.h under {NODE_INCLUDE}")
+        return None
+    tmp = NAPI_OUT + ".tmp"
+    cmd = ["gcc", "-O2", "-std=c11", "-Wall", "-Wno-unused-parameter", "-shared", "-fPIC",
+           "-DNODE_GYP_MODULE_NAME=browservec_napi", "-I", NODE_INCLUDE, NAPI_SRC, "-o", tmp,
+           "-L", LIBDIR, "-lbrowservec_hip", "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("gcc failed for the N-API addon")
+    os.replace(tmp, NAPI_OUT)
+    if verbose:
+        print(f"built {NAPI_OUT}")
+    return NAPI_OUT
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(LIBDIR, exist_ok=True)
     objdir = os.path.join(LIBDIR, "obj")
@@ -63,6 +89,7 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_napi(verbose)
     return LIB
 
 
