@@ -395,10 +395,16 @@ extern "C" int bv_index_append_device(bv_index *idx, const float *d_data, uint64
 }
 
 // ---------------------------------------------------------------- queries
-static uint32_t grid_for(uint64_t n) {
-    uint64_t g = (n + 255) / 256;  // at least 256 rows per workgroup
+// Scanning workgroups per query: at least 256 rows each, and at most
+// 2 * CUs - 1 so that the scanning workgroups plus the threshold helper fit
+// the device at two workgroups per CU whatever the kernel's register count.
+static uint32_t grid_for(const bv_index *idx, uint64_t n) {
+    uint64_t g = (n + 255) / 256;
+    const int cus = idx->dev->prop.multiProcessorCount > 0 ? idx->dev->prop.multiProcessorCount : 128;
+    uint64_t cap = 2 * (uint64_t)cus - 1;
+    if (cap > (uint64_t)SCAN_GRID) cap = SCAN_GRID;
+    if (g > cap) g = cap;
     if (g < 1) g = 1;
-    if (g > (uint64_t)SCAN_GRID) g = SCAN_GRID;
     return (uint32_t)g;
 }
 
@@ -545,7 +551,7 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
         a.q_stride = qstride;
     }
     const uint64_t n = idx->rows;
-    const uint32_t grid = grid_for(n);
+    const uint32_t grid = grid_for(idx, n);
     rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a);
     if (rc) return rc;
     a.codes = idx->quant ? idx->codes.p : idx->raw.p;
@@ -829,7 +835,7 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     uint64_t qstride = 0;
     int rc = prepare_queries(idx, idx->qin.as<float>(), 1, &qscan, &qstride);
     if (rc) return rc;
-    const uint32_t grid = grid_for(idx->rows);
+    const uint32_t grid = grid_for(idx, idx->rows);
     const uint32_t *d_mask = nullptr;
     if (mask) {
         HIPX(idx->dev, idx->mask.ensure(mask_words * 4, 0, idx->stream), "mask buffer");

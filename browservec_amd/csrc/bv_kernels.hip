@@ -308,7 +308,8 @@ constexpr int SEL_BINS = 1024;  // histogram bins of the selection
 constexpr int SEL_TMP = 1024;   // gather buffer of the selection
 
 struct TopkLds {
-    uint64_t keys[SCAN_CAP];    // candidate keys
+    uint64_t keys[SCAN_CAP];    // candidate keys (final selection with re-rank: scan keys in
+                                // [0, SCAN_CAP/2), their exact keys at the same index + SCAN_CAP/2)
     uint64_t tmp[SEL_TMP];      // selection gather buffer
     uint32_t hist[SEL_BINS];
     uint32_t red[16];           // cross-wave reduction slots
@@ -520,6 +521,26 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
+// wave_append for (key, companion) pairs stored at the same index.
+__device__ __forceinline__ void wave_append2(uint64_t *keys, uint64_t *comp, uint32_t *cnt, uint32_t cap, bool take,
+                                             uint64_t key, uint64_t c, int lane) {
+    const uint64_t ball = __ballot(take);
+    if (ball == 0) return;
+    const uint32_t total = __popcll(ball);
+    const int leader = __ffsll((unsigned long long)ball) - 1;
+    uint32_t base = 0;
+    if (lane == leader) base = atomicAdd(cnt, total);
+    base = __shfl(base, leader);
+    if (take) {
+        const uint32_t i = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(ball >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)ball, 0u));
+        if (i < cap) {
+            keys[i] = key;
+            comp[i] = c;
+        }
+    }
+}
+
 // ------------------------------------------------- per-wave candidate lists --
 // During the scan every wave owns a private list wk[0, wc) in LDS; wc is
 // wave-uniform, so appends need no atomics and no workgroup barriers.
@@ -590,22 +611,55 @@ __device__ uint64_t wave_bound(const uint64_t *wk, uint32_t wc, uint64_t lo, uin
 // the round's signs (f32), then the in-place FWHT with len = 1, 2, 4, ...
 // Butterflies within a lane first, then across lanes (partner = lane ^
 // (len / E)); every butterfly is the reference's f32 (u+v, u-v).
+// rotate_load issues every global read up front (the row and the signs of
+// the first two rounds) so they cost one memory round trip; rotate_apply
+// does the arithmetic.
+template <int E> struct RotIn {
+    float x[E];
+    float s[2][E];
+};
+
 template <int E>
-__device__ __forceinline__ void rotate_wave(const float *src, uint32_t dim, uint32_t P, const float *signs,
-                                            uint32_t rounds, float (&x)[E], int lane) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ void rotate_load(const float *src, uint32_t dim, uint32_t P, const float *signs,
+                                            uint32_t rounds, RotIn<E> &in, int lane) {
     const uint32_t lanes_used = P / E;
     const uint32_t e0 = lane * E;
     const bool active = (uint32_t)lane < lanes_used;
 #pragma unroll
     for (int t = 0; t < E; ++t) {
         const uint32_t e = e0 + t;
-        x[t] = (active && e < dim) ? src[e] : 0.0f;
+        in.x[t] = (active && e < dim) ? src[e] : 0.0f;
     }
-    for (uint32_t r = 0; r < rounds; ++r) {
-        const float *s = signs + (size_t)r * P;
 #pragma unroll
-        for (int t = 0; t < E; ++t) x[t] = active ? x[t] * s[e0 + t] : 0.0f;
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int t = 0; t < E; ++t) in.s[r][t] = (active && (uint32_t)r < rounds) ? signs[(size_t)r * P + e0 + t] : 0.0f;
+    }
+}
+
+template <int E>
+__device__ __forceinline__ void rotate_apply(RotIn<E> &in, uint32_t P, const float *signs, uint32_t rounds,
+                                             float (&x)[E], int lane) {
+#pragma clang fp contract(off)
+    const uint32_t lanes_used = P / E;
+    const uint32_t e0 = lane * E;
+    const bool active = (uint32_t)lane < lanes_used;
+#pragma unroll
+    for (int t = 0; t < E; ++t) x[t] = in.x[t];
+    for (uint32_t r = 0; r < rounds; ++r) {
+        float sg[E];
+        if (r == 0) {
+#pragma unroll
+            for (int t = 0; t < E; ++t) sg[t] = in.s[0][t];
+        } else if (r == 1) {
+#pragma unroll
+            for (int t = 0; t < E; ++t) sg[t] = in.s[1][t];
+        } else {
+#pragma unroll
+            for (int t = 0; t < E; ++t) sg[t] = signs[(size_t)r * P + e0 + t];
+        }
+#pragma unroll
+        for (int t = 0; t < E; ++t) x[t] = active ? x[t] * sg[t] : 0.0f;
 #pragma unroll
         for (int len = 1; len < E; len <<= 1) {
 #pragma unroll
@@ -626,6 +680,14 @@ __device__ __forceinline__ void rotate_wave(const float *src, uint32_t dim, uint
             }
         }
     }
+}
+
+template <int E>
+__device__ __forceinline__ void rotate_wave(const float *src, uint32_t dim, uint32_t P, const float *signs,
+                                            uint32_t rounds, float (&x)[E], int lane) {
+    RotIn<E> in;
+    rotate_load<E>(src, dim, P, signs, rounds, in, lane);
+    rotate_apply<E>(in, P, signs, rounds, x, lane);
 }
 
 // quantizeRow8 / quantizeRow4 / quantizeRow1 of a rotated row held by the
@@ -856,7 +918,11 @@ __host__ __device__ inline size_t query_layout_bytes(int codec, uint32_t P) {
 // LDS the in-scan query transform needs: layout + scratch.
 __host__ __device__ inline size_t query_prep_lds(int codec, uint32_t P) {
     const size_t lay = query_layout_bytes(codec, P);
-    if (codec == C_Q8 || codec == C_Q4) return lay + 3 * (size_t)P;
+    // the larger of the one-wave needs and the workgroup-wide ones
+    // (layout + xs + lv + reduction slots)
+    const size_t wg = ((lay + 15) & ~(size_t)15) + 4 * (size_t)P + 3 * (size_t)P + 12 * 8 + 12 * 4;
+    if (codec == C_Q8 || codec == C_Q4) return wg;
+    if (codec == C_Q1A) return wg;
     if (codec == C_HAM || codec == C_I8S) return lay + 5 * (size_t)P;
     return lay;
 }
@@ -866,10 +932,10 @@ __host__ __device__ inline size_t query_prep_lds(int codec, uint32_t P) {
 // codec's layout (int8 levels, rotated floats, or quantized query codes) in
 // LDS at `lds`.  Byte-identical to the standalone encode + levels kernels.
 template <int C, int E>
-__device__ __forceinline__ void prep_query_e(const ScanArgs &a, uint32_t qi, unsigned char *lds, int lane) {
+__device__ __forceinline__ void prep_query_e(const ScanArgs &a, RotIn<E> &in, unsigned char *lds, int lane) {
     const uint32_t P = a.padded_dim;
     float x[E];
-    rotate_wave<E>(a.qraw + (uint64_t)qi * a.qdim, a.qdim, P, a.signs, a.rounds, x, lane);
+    rotate_apply<E>(in, P, a.signs, a.rounds, x, lane);
     const size_t lay = query_layout_bytes(C, P);
     if constexpr (C == C_Q8 || C == C_Q4) {
         levels_wave<E>(x, P, C, (signed char *)(lds + lay), lds, lane);
@@ -900,6 +966,180 @@ template <int C, int LPR, int UPL> struct PrepShape {
     static constexpr int P = UnitCodes<C>::v * LPR * UPL;
     static constexpr int E = P >= 64 ? P / 64 : 1;
     static constexpr bool ok = UnitCodes<C>::v > 0 && P >= 64 && E <= 16;
+};
+
+// The same transform spread over the 4 waves of a workgroup, for the
+// int8 / int4 level split and the 1-bit asym layout at P = 256 * EP
+// (EP = 1, 2, 4).  Wave w holds the quarter [w*P/4, (w+1)*P/4) with EP
+// consecutive elements per lane: FWHT stages len < P/4 run in registers as
+// in rotate_apply, the last two (len = P/4, P/2) across waves through LDS.
+// Same butterflies in the same stage order, and the level split does the
+// same per-element f64 arithmetic with workgroup-wide exact max / sum, so
+// the bytes equal the one-wave transform's.  Every thread takes part (the
+// caller's barriers follow); LDS layout: [layout | xs: P floats | lv: 3P
+// bytes | 3 x 4 double + 3 x 4 int reduction slots].
+template <int EP> struct RotInWG {
+    float x[EP];
+    float s[2][EP];
+};
+
+__host__ __device__ inline size_t prep_wg_xs_offset(size_t lay) { return (lay + 15) & ~(size_t)15; }
+
+template <int EP>
+__device__ __forceinline__ void rotate_load_wg(const float *src, uint32_t dim, uint32_t P, const float *signs,
+                                               uint32_t rounds, RotInWG<EP> &in, int tid) {
+    const uint32_t e0 = (uint32_t)tid * EP;  // quarter of wave w starts at w*64*EP = (tid - lane)*EP
+#pragma unroll
+    for (int t = 0; t < EP; ++t) in.x[t] = e0 + t < dim ? src[e0 + t] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+#pragma unroll
+        for (int t = 0; t < EP; ++t) in.s[r][t] = (uint32_t)r < rounds ? signs[(size_t)r * P + e0 + t] : 0.0f;
+    }
+}
+
+template <int C, int EP>
+__device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in, unsigned char *lds, int tid) {
+#pragma clang fp contract(off)
+    const uint32_t P = a.padded_dim;  // == 256 * EP
+    const int lane = tid & 63, wave = tid >> 6;
+    const uint32_t e0 = (uint32_t)tid * EP;
+    const size_t lay = query_layout_bytes(C, P);
+    float *xs = (float *)(lds + prep_wg_xs_offset(lay));
+    float x[EP];
+#pragma unroll
+    for (int t = 0; t < EP; ++t) x[t] = in.x[t];
+    for (uint32_t r = 0; r < a.rounds; ++r) {
+        float sg[EP];
+        if (r == 0) {
+#pragma unroll
+            for (int t = 0; t < EP; ++t) sg[t] = in.s[0][t];
+        } else if (r == 1) {
+#pragma unroll
+            for (int t = 0; t < EP; ++t) sg[t] = in.s[1][t];
+        } else {
+#pragma unroll
+            for (int t = 0; t < EP; ++t) sg[t] = a.signs[(size_t)r * P + e0 + t];
+        }
+#pragma unroll
+        for (int t = 0; t < EP; ++t) x[t] = x[t] * sg[t];
+#pragma unroll
+        for (int len = 1; len < EP; len <<= 1) {
+#pragma unroll
+            for (int t = 0; t < EP; ++t) {
+                if (!(t & len)) {
+                    const float u = x[t], w = x[t + len];
+                    x[t] = u + w;
+                    x[t + len] = u - w;
+                }
+            }
+        }
+        for (int m = 1; m < 64; m <<= 1) {
+            const bool hi = (lane & m) != 0;
+#pragma unroll
+            for (int t = 0; t < EP; ++t) {
+                const float y = __shfl_xor(x[t], m);
+                x[t] = hi ? (y - x[t]) : (x[t] + y);
+            }
+        }
+        // stages len = P/4 and P/2 pair elements of different waves
+#pragma unroll
+        for (int t = 0; t < EP; ++t) xs[e0 + t] = x[t];
+        __syncthreads();
+        for (uint32_t len = P / 4; len < P; len <<= 1) {
+            for (uint32_t idx = tid; idx < P / 2; idx += SCAN_WG) {
+                const uint32_t i = (idx / len) * (2 * len) + idx % len, j = i + len;
+                const float u = xs[i], w = xs[j];
+                xs[i] = u + w;
+                xs[j] = u - w;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int t = 0; t < EP; ++t) x[t] = xs[e0 + t];
+        __syncthreads();  // xs is rewritten by the next round
+    }
+    if constexpr (C == C_Q1A) {
+        float *f = (float *)lds;
+#pragma unroll
+        for (int t = 0; t < EP; ++t) f[e0 + t] = x[t];
+        return;
+    } else {
+        signed char *lv = (signed char *)(xs + P);
+        double *redm = (double *)(lv + 3 * (size_t)P);  // [3][4]
+        int32_t *reds = (int32_t *)(redm + 12);         // [3][4]
+        double rd[EP];
+#pragma unroll
+        for (int t = 0; t < EP; ++t) rd[t] = (double)x[t];
+        double sl[3];
+#pragma unroll
+        for (int l = 0; l < 3; ++l) {
+            double m = 0.0;
+#pragma unroll
+            for (int t = 0; t < EP; ++t) m = fmax(m, fabs(rd[t]));
+#pragma unroll
+            for (int sh = 1; sh < 64; sh <<= 1) m = fmax(m, __shfl_xor(m, sh));
+            if (lane == 0) redm[l * 4 + wave] = m;
+            __syncthreads();
+            m = fmax(fmax(redm[l * 4 + 0], redm[l * 4 + 1]), fmax(redm[l * 4 + 2], redm[l * 4 + 3]));
+            const double sc = m > 0.0 ? m / 127.0 : 0.0;
+            const double inv = sc > 0.0 ? 1.0 / sc : 0.0;
+            int32_t sum = 0;
+#pragma unroll
+            for (int t = 0; t < EP; ++t) {
+                double c = rint(rd[t] * inv);
+                c = c > 127.0 ? 127.0 : (c < -127.0 ? -127.0 : c);
+                rd[t] = fma(-sc, c, rd[t]);
+                lv[l * P + e0 + t] = (signed char)(int)c;
+                sum += (int)c;
+            }
+#pragma unroll
+            for (int sh = 1; sh < 64; sh <<= 1) sum += __shfl_xor(sum, sh);
+            if (lane == 0) reds[l * 4 + wave] = sum;
+            sl[l] = sc;
+        }
+        __syncthreads();
+        uint32_t *w = (uint32_t *)lds;
+        const unsigned char *lb = (const unsigned char *)lv;
+        uint32_t qwords;
+        if constexpr (C == C_Q8) {
+            const uint32_t units = P / 16;
+            qwords = units * 12;
+            for (uint32_t i = tid; i < qwords; i += SCAN_WG) {
+                const uint32_t u = i / 12, r = i % 12, l = r / 4, d = r % 4;
+                const uint32_t base = l * P + 16 * u + 4 * d;
+                w[i] = (uint32_t)lb[base] | ((uint32_t)lb[base + 1] << 8) | ((uint32_t)lb[base + 2] << 16) |
+                       ((uint32_t)lb[base + 3] << 24);
+            }
+        } else {  // C_Q4
+            const uint32_t units = P / 32;
+            qwords = units * 24;
+            for (uint32_t i = tid; i < qwords; i += SCAN_WG) {
+                const uint32_t u = i / 24, r = i % 24, l = r / 8, d = (r % 8) / 2, h = r % 2;
+                const uint32_t base = l * P + 32 * u + 8 * d + h;
+                w[i] = (uint32_t)lb[base] | ((uint32_t)lb[base + 2] << 8) | ((uint32_t)lb[base + 4] << 16) |
+                       ((uint32_t)lb[base + 6] << 24);
+            }
+        }
+        if (tid == 0) {
+            QLevelTail *tl = (QLevelTail *)(lds + (size_t)qwords * 4);
+            const double div = C == C_Q8 ? 127.0 : 1.0;
+#pragma unroll
+            for (int l = 0; l < 3; ++l) {
+                tl->s[l] = sl[l] / div;
+                tl->sum[l] = reds[l * 4 + 0] + reds[l * 4 + 1] + reds[l * 4 + 2] + reds[l * 4 + 3];
+            }
+            tl->pad = 0;
+        }
+    }
+}
+
+// Which transform a scan layout uses: the workgroup-wide one for int8 /
+// int4 / 1-bit asym at P = 256, 512, 1024, else the one-wave one.
+template <int C, int LPR, int UPL> struct PrepWG {
+    static constexpr int P = UnitCodes<C>::v * LPR * UPL;
+    static constexpr bool ok = (C == C_Q8 || C == C_Q4 || C == C_Q1A) && (P == 256 || P == 512 || P == 1024);
+    static constexpr int EP = ok ? P / 256 : 1;
 };
 
 // ------------------------------------------------------------ exact score --
@@ -1345,15 +1585,33 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     constexpr bool PIPE = SH::U * UPL * (int)(sizeof(typename CD::Unit) / 4) <= 32;  // double-buffer the loads
     SD A, B;
     uint64_t ab = 0, al = 0, bb = 0, bl = 0;
+    // the query slice: transformed here by wave 0 into LDS, or read from a
+    // prepared global layout.  Wave 0 issues the query and sign reads before
+    // any code load, and transforms while the first code loads are in flight.
+    using PS = PrepShape<C, LPR, UPL>;
+    using PW = PrepWG<C, LPR, UPL>;
+    RotIn<(PS::ok && !PW::ok) ? PS::E : 1> rin;
+    RotInWG<PW::EP> rinw;
+    const bool prep = PS::ok && a.qraw != nullptr;
+    const float *qsrc = a.qraw + (uint64_t)qi * a.qdim;
+    if constexpr (PW::ok) {
+        if (prep) rotate_load_wg<PW::EP>(qsrc, a.qdim, a.padded_dim, a.signs, a.rounds, rinw, tid);
+    } else if constexpr (PS::ok) {
+        if (prep && wave == 0) rotate_load<PS::E>(qsrc, a.qdim, a.padded_dim, a.signs, a.rounds, rin, lane);
+    }
+    // the first two steps' code loads need no query: both go out before the
+    // query transform, so the memory system stays busy while it runs
     bool ha = next_step(ab, al);
-    if (PIPE && ha) load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);  // needs no query yet
+    if (PIPE && ha) load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
+    bool hb = PIPE && ha && next_step(bb, bl);
+    if (PIPE && hb) load_step<C, LPR, UPL, IDX>(a, R, cand, bb, bl, B, lane);
 
-    // the query slice: transformed here by wave 0 into LDS (while the first
-    // code loads are in flight), or read from a prepared global layout
     const QT *qbase;
-    if (PrepShape<C, LPR, UPL>::ok && a.qraw) {
-        if constexpr (PrepShape<C, LPR, UPL>::ok) {
-            if (wave == 0) prep_query_e<C, PrepShape<C, LPR, UPL>::E>(a, qi, scan_smem, lane);
+    if (prep) {
+        if constexpr (PW::ok) {
+            prep_query_wg<C, PW::EP>(a, rinw, scan_smem, tid);
+        } else if constexpr (PS::ok) {
+            if (wave == 0) prep_query_e<C, PS::E>(a, rin, scan_smem, lane);
         }
         __syncthreads();
         qbase = (const QT *)scan_smem;
@@ -1374,13 +1632,14 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         uint64_t gt = 0;
         if (poll) gt = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if constexpr (PIPE) {
-            // the next step's loads are in flight while this one is scored
-            const bool hb = next_step(bb, bl);
-            if (hb) load_step<C, LPR, UPL, IDX>(a, R, cand, bb, bl, B, lane);
+            // steps alternate between A and B; the other buffer's loads are
+            // in flight while one is scored
             compute_step<C, LPR, UPL>(a, R, A, ab, al, tau, wk, wc, lmax, lane);
             ha = hb && next_step(ab, al);
             if (ha) load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
             if (hb) compute_step<C, LPR, UPL>(a, R, B, bb, bl, tau, wk, wc, lmax, lane);
+            hb = ha && next_step(bb, bl);
+            if (hb) load_step<C, LPR, UPL, IDX>(a, R, cand, bb, bl, B, lane);
         } else {
             load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
             compute_step<C, LPR, UPL>(a, R, A, ab, al, tau, wk, wc, lmax, lane);
@@ -1477,6 +1736,68 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     const uint64_t *ckq = a.cand_keys + 2 * (uint64_t)qi * a.cand_cap;
     const uint32_t total = L.ovl[32 + ng];
     constexpr uint32_t CHUNK = SCAN_CAP / 2;
+    if (a.rr_src && total <= CHUNK) {
+        // Re-rank, common case: one pass gathers the (scan key, exact key)
+        // pairs at or above the bound; the fetch is the best kp scan keys,
+        // found by rank counting; its exact keys are ranked for the output.
+        const uint64_t th = L.tau;
+        for (uint32_t i0 = 0; i0 < total; i0 += 4 * SCAN_WG) {
+            uint64_t v[4], e[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t i = i0 + j * SCAN_WG + tid;
+                v[j] = 0;
+                e[j] = 0;
+                if (i < total) {
+                    uint32_t r = 0;
+                    while (r + 1 < ng && L.ovl[32 + r + 1] <= i) ++r;
+                    const uint64_t slot = 2 * (r * region + (i - L.ovl[32 + r]));
+                    v[j] = load_shared(&ckq[slot]);
+                    e[j] = load_shared(&ckq[slot + 1]);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                wave_append2(L.keys, L.keys + CHUNK, &L.cnt, CHUNK, v[j] != 0 && v[j] >= th, v[j], e[j], lane);
+        }
+        if (tid == 0) {
+            L.gtau = 0;
+            L.cnt2 = 0;
+        }
+        __syncthreads();
+        const uint32_t nk = L.cnt;
+        if (nk > kp) {
+            for (uint32_t j = tid; j < nk; j += SCAN_WG)
+                if (count_greater(L.keys, nk, L.keys[j]) == kp - 1) L.gtau = L.keys[j];
+        }
+        __syncthreads();
+        const uint64_t T = L.gtau;  // 0 when every gathered key is in the fetch
+        for (uint32_t j0 = 0; j0 < nk; j0 += SCAN_WG) {
+            const uint32_t j = j0 + tid;
+            const bool in = j < nk && L.keys[j] >= T;
+            wave_append(L.tmp, &L.cnt2, SEL_TMP, in, in ? L.keys[CHUNK + j] : 0ull, lane);
+        }
+        __syncthreads();
+        const uint32_t mm = L.cnt2;
+        const uint32_t ko = mm < a.k_out ? mm : a.k_out;
+        for (uint32_t j = tid; j < mm; j += SCAN_WG) {
+            const uint64_t ek = L.tmp[j];
+            const uint32_t r = count_greater(L.tmp, mm, ek);
+            if (r < ko) {
+                a.out_rows[(uint64_t)qi * a.k_out + r] = key_row(ek);
+                a.out_scores[(uint64_t)qi * a.k_out + r] = f32_from_ord((uint32_t)(ek >> 32));
+            }
+        }
+        if (tid == 0) {
+            a.out_n[qi] = ko;
+            a.merged_n[qi] = mm;
+        }
+        __syncthreads();
+        if (tid == 0) L.last = atomicAdd(&qs->fin, 1u) == 1;
+        __syncthreads();
+        if (L.last) reset_query(a, qi);
+        return;
+    }
     for (uint32_t c0 = 0; c0 < total; c0 += CHUNK) {
         const uint64_t th = L.tau;
         const uint32_t c1 = c0 + CHUNK < total ? c0 + CHUNK : total;
