@@ -108,6 +108,8 @@ SIGNATURES = {
     "bv_index_export_codes": [vp, u64, u64, vp, vp],
     "bv_index_export_scores": [vp, vp, vp],
     "bv_index_export_rotated_query": [vp, vp, vp],
+    "bv_index_build": [vp],
+    "bv_index_export_ivf": [vp, vp, vp, vp],
 }
 _RESTYPE = {"bv_last_error": ctypes.c_char_p}
 

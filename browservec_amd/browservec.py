@@ -17,7 +17,7 @@ from typing import Any, Callable
 import numpy as np
 
 from . import _lib as L
-from .index import DeviceContext, FlatHit, FlatIndex, NativeIndex, QuantIndex
+from .index import DeviceContext, FlatHit, FlatIndex, IVFIndex, IVFQuantIndex, NativeIndex, QuantIndex
 
 DEFAULT_SEED = 0x9E3779B9  # src/index.ts:71
 FILTER_CPU_SCAN_MAX = 4096  # src/index.ts:76
@@ -220,10 +220,10 @@ class BrowserVec:
 
         def make():
             if ann is not None:
-                from .ivf import IVFIndex, IVFQuantIndex  # noqa: F401 (IVF arrives with its kernels)
                 if quantBits:
-                    return IVFQuantIndex(ctx, dimension, seed, rounds, ann, quantBits, chunkRows)
-                return IVFIndex(ctx, dimension, metric, ann, chunkRows)
+                    return IVFQuantIndex(ctx, dimension, bits=quantBits, seed=seed, rounds=rounds, ivf=ann,
+                                         chunk_rows=chunkRows, metric=metric)
+                return IVFIndex(ctx, dimension, metric, ivf=ann, chunk_rows=chunkRows)
             if quantBits == 0:
                 return FlatIndex(ctx, dimension, metric, chunkRows)
             return QuantIndex(ctx, dimension, seed, rounds, quantBits, chunkRows, scorer=scorer, metric=metric)
@@ -312,7 +312,7 @@ class BrowserVec:
                 return []
             if len(match) <= FILTER_CPU_SCAN_MAX:
                 return self._query_rows_exact(q, match, k)
-            if hasattr(self.index, "query_masked") and not isinstance(self.index, _IVFBase):
+            if hasattr(self.index, "query_masked") and not getattr(self.index, "is_ivf", False):
                 mask = words
             else:
                 skip_rows = self.store.count - len(match)
@@ -442,6 +442,3 @@ class BrowserVec:
         self.index.destroy()
         self.ctx.destroy()
 
-
-class _IVFBase:  # marker for IVF indexes (over-fetch filter path, src/index.ts:389-394)
-    pass

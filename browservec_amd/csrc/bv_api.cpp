@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <functional>
 #include <chrono>
 #include <cmath>
 #include <cstdarg>
@@ -132,6 +133,20 @@ struct bv_index {
     HostBuf h_rows, h_scores, h_n;
 
     uint32_t nprobe_override = 0;
+
+    // IVF (IVFIndex / IVFQuantIndex): reservoir sample, centroids, CSR lists
+    bool ivf = false;
+    uint32_t sample_cap = 0, sample_dim = 0;  // sample rows: padded dim (quant) or dim (fp32)
+    uint64_t sample_filled = 0, sample_seen = 0;
+    uint32_t sample_rng = 0;
+    DevBuf sample;
+    uint64_t built_rows = ~0ull;              // rows covered by the current lists
+    uint32_t nlist = 0;
+    DevBuf centroids, list_off, list_rows;
+    std::vector<uint32_t> list_sizes_desc;    // host: list sizes, largest first
+    DevBuf ivf_idx, ivf_idx2, ivf_slot, ivf_assign, ivf_hist, ivf_base, ivf_totals, ivf_toff, ivf_trows;
+    DevBuf probe_scores, probes, cand_tot, cand_off;
+    double build_ms = 0;
     double last_query_ms = 0, last_query_gpu_ms = 0;
     uint64_t last_scanned = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
@@ -238,8 +253,8 @@ extern "C" int bv_index_create(bv_device *dev, const bv_index_desc *desc, bv_ind
     if (d.kind == BV_KIND_QUANT && d.metric == BV_METRIC_L2)
         return fail(BV_E_UNSUPPORTED,
                     "quantized mode supports metric cosine/dot only (l2 quantization is later work)");
-    if (d.kind == BV_KIND_IVF || d.kind == BV_KIND_IVFQUANT)
-        return fail(BV_E_UNSUPPORTED, "IVF index kinds are not available in this build yet");
+    if ((d.kind == BV_KIND_IVF || d.kind == BV_KIND_IVFQUANT) && d.nlist > IVF_MAX_NLIST)
+        return fail(BV_E_UNSUPPORTED, "nlist %u exceeds %u", d.nlist, IVF_MAX_NLIST);
     if (d.scorer == BV_SCORER_HAMMING && d.bits != 1)
         return fail(BV_E_UNSUPPORTED, "the Hamming scorer needs 1-bit codes");
     if (d.scorer == BV_SCORER_INT8SYM && d.bits != 8)
@@ -281,6 +296,14 @@ extern "C" int bv_index_create(bv_device *dev, const bv_index_desc *desc, bv_ind
             x->codec = l2 ? C_F32L2_S : C_F32DOT_S;
             x->units = d.dim;
         }
+    }
+    if (d.kind == BV_KIND_IVF || d.kind == BV_KIND_IVFQUANT) {
+        // src/index/ivf.ts:107-109, src/index/ivfquant.ts:112-124
+        x->ivf = true;
+        x->sample_cap = std::max<uint32_t>(1024, d.sample_size ? d.sample_size : 50000);
+        x->sample_dim = quant ? x->P : d.dim;
+        const uint32_t ivf_seed = d.has_ivf_seed ? d.ivf_seed : (quant ? d.seed : 0x51ed270bu);
+        x->sample_rng = quant ? (ivf_seed ^ 0x85ebca6bu) : ivf_seed;
     }
     if (!scan_supported(x->codec, x->units)) {
         int c = x->codec;
@@ -337,8 +360,73 @@ static int check_live(bv_index *idx) {
     return BV_OK;
 }
 
+// ------------------------------------------------------------------ IVF
+static double mb32_draw(uint32_t &a) { return (double)mb32_next(a) / 4294967296.0; }
+
+// Reservoir sampling of appended rows (src/index/ivfquant.ts:235-245,
+// src/index/ivf.ts:175-187): per row in order, the next free slot while the
+// sample is filling, else slot floor(rng() * (seen + 1)) when below the
+// capacity.  Only the last row written to a slot within the batch keeps it
+// (earlier ones would be overwritten in order).  Slots go to the device in
+// idx->ivf_slot (count ints); the sample buffer grows to the slots in use.
+static int ivf_reservoir(bv_index *idx, uint64_t count, std::vector<int32_t> &slots) {
+    slots.assign(count, -1);
+    for (uint64_t i = 0; i < count; ++i) {
+        if (idx->sample_filled < idx->sample_cap) {
+            slots[i] = (int32_t)idx->sample_filled++;
+        } else {
+            const uint64_t j = (uint64_t)std::floor(mb32_draw(idx->sample_rng) * (double)(idx->sample_seen + 1));
+            if (j < idx->sample_cap) slots[i] = (int32_t)j;
+        }
+        idx->sample_seen++;
+    }
+    std::vector<uint8_t> taken(idx->sample_cap, 0);
+    for (uint64_t i = count; i-- > 0;) {
+        if (slots[i] < 0) continue;
+        if (taken[slots[i]]) slots[i] = -1;
+        else taken[slots[i]] = 1;
+    }
+    const size_t rb = (size_t)idx->sample_dim * 4;
+    HIPX(idx->dev, idx->sample.ensure(idx->sample_filled * rb, idx->sample.cap, idx->stream), "sample buffer");
+    HIPX(idx->dev, idx->ivf_slot.ensure(count * 4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, hipMemcpyAsync(idx->ivf_slot.p, slots.data(), count * 4, hipMemcpyHostToDevice, idx->stream),
+         "upload");
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "upload");
+    idx->built_rows = ~0ull;  // lists are stale after any append (ivfquant.ts:462)
+    return BV_OK;
+}
+
+// fp32 IVF: the sampled rows themselves go to their slots.
+static int ivf_sample_raw(bv_index *idx, uint64_t base, const std::vector<int32_t> &slots) {
+    std::vector<uint32_t> src, dst;
+    for (size_t i = 0; i < slots.size(); ++i)
+        if (slots[i] >= 0) {
+            src.push_back((uint32_t)(base + i));
+            dst.push_back((uint32_t)slots[i]);
+        }
+    if (src.empty()) return BV_OK;
+    HIPX(idx->dev, idx->ivf_idx.ensure(src.size() * 4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->ivf_idx2.ensure(dst.size() * 4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, hipMemcpyAsync(idx->ivf_idx.p, src.data(), src.size() * 4, hipMemcpyHostToDevice, idx->stream),
+         "upload");
+    HIPX(idx->dev, hipMemcpyAsync(idx->ivf_idx2.p, dst.data(), dst.size() * 4, hipMemcpyHostToDevice, idx->stream),
+         "upload");
+    IvfCopyArgs c{};
+    c.src = idx->raw.as<float>();
+    c.src_stride = idx->dim;
+    c.src_idx = idx->ivf_idx.as<uint32_t>();
+    c.dst = idx->sample.as<float>();
+    c.dst_stride = idx->sample_dim;
+    c.dst_idx = idx->ivf_idx2.as<uint32_t>();
+    c.n = (uint32_t)src.size();
+    c.dim = idx->dim;
+    HIPX(idx->dev, ivf_launch_copy_rows(c, idx->stream), "sample copy");
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "sample copy");
+    return BV_OK;
+}
+
 // Rotate+quantize rows [first, first+count) from the device row buffer.
-static int encode_range(bv_index *idx, uint64_t first, uint64_t count) {
+static int encode_range(bv_index *idx, uint64_t first, uint64_t count, const int32_t *d_sample_slot = nullptr) {
     EncodeArgs a{};
     a.src = idx->raw.as<float>() + first * idx->dim;
     a.rows = count;
@@ -350,6 +438,10 @@ static int encode_range(bv_index *idx, uint64_t first, uint64_t count) {
     a.codes = idx->codes.as<uint32_t>() + first * idx->words_per_row;
     a.scales = idx->scales.as<float>() + first;
     a.slow_rows = idx->slow.as<uint32_t>();
+    if (d_sample_slot) {
+        a.sample_slot = d_sample_slot;
+        a.sample = idx->sample.as<float>();
+    }
     HIPX(idx->dev, launch_encode(a, idx->stream), "encode kernel");
     return BV_OK;
 }
@@ -362,10 +454,18 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
          hipMemcpyAsync(idx->raw.as<char>() + base * rb, data, count * rb,
                         device_src ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, idx->stream),
          "row upload");
+    std::vector<int32_t> slots;
+    if (idx->ivf) {
+        int rc = ivf_reservoir(idx, count, slots);
+        if (rc) return rc;
+    }
     if (idx->quant) {
         HIPX(idx->dev, idx->codes.ensure(total * idx->row_bytes, base * idx->row_bytes, idx->stream), "code buffer");
         HIPX(idx->dev, idx->scales.ensure(total * 4, base * 4, idx->stream), "scale buffer");
-        int rc = encode_range(idx, base, count);
+        int rc = encode_range(idx, base, count, idx->ivf ? idx->ivf_slot.as<int32_t>() : nullptr);
+        if (rc) return rc;
+    } else if (idx->ivf) {
+        int rc = ivf_sample_raw(idx, base, slots);
         if (rc) return rc;
     }
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "append");
@@ -392,6 +492,192 @@ extern "C" int bv_index_append_device(bv_index *idx, const float *d_data, uint64
     if (!d_data) return fail(BV_E_INVALID, "data is null");
     if (idx->rows + count > 0xfffffffeull) return fail(BV_E_INVALID, "row count exceeds 2^32-2");
     return append_common(idx, d_data, true, count);
+}
+
+// IVF build (src/index/ivfquant.ts:248-312, src/index/ivf.ts:191-259):
+// spherical k-means on the reservoir sample with device assignment and
+// device mean update (the host only draws the init / re-seed rows from
+// mulberry32, as the reference's trainer does), then every row is assigned
+// (by its codes for quantized kinds) and the CSR lists are built on the
+// device.
+static int ivf_build(bv_index *idx) {
+    auto t0 = std::chrono::steady_clock::now();
+    const uint64_t rows = idx->rows;
+    uint32_t nlist;
+    if (idx->d.nlist) {
+        nlist = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(idx->d.nlist, rows));
+    } else {
+        const uint64_t guess = (uint64_t)std::floor(std::sqrt((double)rows) + 0.5);
+        nlist = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(std::min<uint64_t>(4096, std::max<uint64_t>(16, guess)), rows));
+    }
+    const uint32_t seed = idx->d.has_ivf_seed ? idx->d.ivf_seed : 0x51ed270bu;
+    const uint32_t iters = idx->d.iters ? idx->d.iters : 8;
+    const uint32_t train = (uint32_t)std::min<uint64_t>(idx->sample_filled, idx->d.train_size ? idx->d.train_size : 16384);
+    if (train == 0) return fail(BV_E_STATE, "IVF build with an empty sample");
+    const uint32_t D = idx->sample_dim;
+    hipStream_t s = idx->stream;
+    HIPX(idx->dev, idx->centroids.ensure((size_t)nlist * D * 4, 0, s), "centroids");
+    const uint64_t nmax = std::max<uint64_t>(rows, train);
+    const uint32_t nblk = ivf_list_blocks(nmax);
+    HIPX(idx->dev, idx->ivf_assign.ensure(nmax * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_hist.ensure((size_t)std::max(nblk, 1u) * nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_base.ensure((size_t)std::max(nblk, 1u) * nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_totals.ensure((size_t)nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_toff.ensure(((size_t)nlist + 1) * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_trows.ensure((size_t)train * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_idx.ensure((size_t)nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_idx2.ensure((size_t)nlist * 4, 0, s), "scratch");
+
+    auto copy_rows = [&](const std::vector<uint32_t> &src, const std::vector<uint32_t> *dst) -> int {
+        if (src.empty()) return BV_OK;
+        HIPX(idx->dev, hipMemcpyAsync(idx->ivf_idx.p, src.data(), src.size() * 4, hipMemcpyHostToDevice, s), "upload");
+        if (dst)
+            HIPX(idx->dev, hipMemcpyAsync(idx->ivf_idx2.p, dst->data(), dst->size() * 4, hipMemcpyHostToDevice, s),
+                 "upload");
+        IvfCopyArgs c{};
+        c.src = idx->sample.as<float>();
+        c.src_stride = D;
+        c.src_idx = idx->ivf_idx.as<uint32_t>();
+        c.dst = idx->centroids.as<float>();
+        c.dst_stride = D;
+        c.dst_idx = dst ? idx->ivf_idx2.as<uint32_t>() : nullptr;
+        c.n = (uint32_t)src.size();
+        c.dim = D;
+        HIPX(idx->dev, ivf_launch_copy_rows(c, s), "centroid copy");
+        return BV_OK;
+    };
+    // randomInitCentroids (kmeans.ts:154-170)
+    {
+        uint32_t a = seed;
+        std::vector<uint32_t> pick(nlist);
+        for (uint32_t c = 0; c < nlist; ++c) pick[c] = (uint32_t)std::floor(mb32_draw(a) * (double)train);
+        int rc = copy_rows(pick, nullptr);
+        if (rc) return rc;
+        HIPX(idx->dev, ivf_launch_normalize(idx->centroids.as<float>(), nlist, D, D, s), "normalize");
+    }
+    IvfAssignArgs ta{};
+    ta.n = train;
+    ta.dim = D;
+    ta.rows = idx->sample.as<float>();
+    ta.row_stride = D;
+    ta.centroids = idx->centroids.as<float>();
+    ta.cen_stride = D;
+    ta.nlist = nlist;
+    ta.out = idx->ivf_assign.as<uint32_t>();
+    std::vector<uint32_t> toff(nlist + 1);
+    for (uint32_t it = 0; it < iters; ++it) {
+        HIPX(idx->dev, ivf_launch_assign(ta, 0, s), "assign kernel");
+        HIPX(idx->dev, ivf_launch_lists(ta.out, train, nlist, idx->ivf_hist.as<uint32_t>(), idx->ivf_base.as<uint32_t>(),
+                                        idx->ivf_totals.as<uint32_t>(), idx->ivf_toff.as<uint32_t>(),
+                                        idx->ivf_trows.as<uint32_t>(), s),
+             "list kernels");
+        HIPX(idx->dev, ivf_launch_means(idx->sample.as<float>(), D, D, idx->ivf_toff.as<uint32_t>(),
+                                        idx->ivf_trows.as<uint32_t>(), nlist, idx->centroids.as<float>(), D, s),
+             "mean kernel");
+        HIPX(idx->dev, hipMemcpyAsync(toff.data(), idx->ivf_toff.p, (nlist + 1) * 4, hipMemcpyDeviceToHost, s),
+             "download");
+        HIPX(idx->dev, hipStreamSynchronize(s), "k-means");
+        // empty clusters re-seeded in cluster order (kmeans.ts:195-199) with
+        // the trainer's per-iteration seed (kmeansTrainer.ts:97)
+        uint32_t a = seed + it + 1;
+        std::vector<uint32_t> src, dst;
+        for (uint32_t c = 0; c < nlist; ++c)
+            if (toff[c + 1] == toff[c]) {
+                src.push_back((uint32_t)std::floor(mb32_draw(a) * (double)train));
+                dst.push_back(c);
+            }
+        int rc = copy_rows(src, &dst);
+        if (rc) return rc;
+        HIPX(idx->dev, ivf_launch_normalize(idx->centroids.as<float>(), nlist, D, D, s), "normalize");
+    }
+    // final assignment of every row (ivfquant.ts:291-293: by its codes)
+    IvfAssignArgs fa = ta;
+    fa.n = rows;
+    if (idx->quant) {
+        fa.rows = nullptr;
+        fa.codes = idx->codes.as<uint32_t>();
+        fa.words_per_row = idx->words_per_row;
+        fa.scales = idx->scales.as<float>();
+    } else {
+        fa.rows = idx->raw.as<float>();
+        fa.row_stride = idx->dim;
+    }
+    HIPX(idx->dev, ivf_launch_assign(fa, idx->quant ? (int)idx->d.bits : 0, s), "assign kernel");
+    HIPX(idx->dev, idx->list_off.ensure(((size_t)nlist + 1) * 4, 0, s), "lists");
+    HIPX(idx->dev, idx->list_rows.ensure(std::max<uint64_t>(rows, 1) * 4, 0, s), "lists");
+    HIPX(idx->dev, ivf_launch_lists(fa.out, rows, nlist, idx->ivf_hist.as<uint32_t>(), idx->ivf_base.as<uint32_t>(),
+                                    idx->ivf_totals.as<uint32_t>(), idx->list_off.as<uint32_t>(),
+                                    idx->list_rows.as<uint32_t>(), s),
+         "list kernels");
+    std::vector<uint32_t> off(nlist + 1);
+    HIPX(idx->dev, hipMemcpyAsync(off.data(), idx->list_off.p, (nlist + 1) * 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "IVF build");
+    idx->list_sizes_desc.resize(nlist);
+    for (uint32_t c = 0; c < nlist; ++c) idx->list_sizes_desc[c] = off[c + 1] - off[c];
+    std::sort(idx->list_sizes_desc.begin(), idx->list_sizes_desc.end(), std::greater<uint32_t>());
+    idx->nlist = nlist;
+    idx->built_rows = rows;
+    idx->build_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    return BV_OK;
+}
+
+// nprobe for the next query (ivfquant.ts:159-162, 487-491): the per-query
+// override (consumed once), else the configured one, else 5% of nlist.
+static uint32_t ivf_resolve_nprobe(bv_index *idx) {
+    uint32_t n = idx->nprobe_override ? idx->nprobe_override
+                 : idx->d.nprobe      ? idx->d.nprobe
+                                      : (uint32_t)std::max<double>(1.0, std::floor(idx->nlist * 0.05 + 0.5));
+    idx->nprobe_override = 0;
+    n = std::max<uint32_t>(1, std::min<uint32_t>(n, idx->nlist));
+    return std::min<uint32_t>(n, IVF_MAX_NPROBE);
+}
+
+// Probes + gathered candidate lists for nq device queries (original space).
+// Returns the per-query candidate bound used to size the scan.
+static int ivf_candidates(bv_index *idx, const float *d_q, uint32_t nq, uint64_t *max_per_query) {
+    if (idx->built_rows != idx->rows) {
+        int rc = ivf_build(idx);
+        if (rc) return rc;
+    }
+    hipStream_t s = idx->stream;
+    const uint32_t nprobe = ivf_resolve_nprobe(idx);
+    const float *qrot = d_q;
+    if (idx->quant) {  // pickProbes scores the rotated query
+        HIPX(idx->dev, idx->qrot.ensure((size_t)nq * idx->P * 4, 0, s), "query buffer");
+        EncodeArgs e{};
+        e.src = d_q;
+        e.rows = nq;
+        e.dim = idx->dim;
+        e.P = idx->P;
+        e.signs = idx->signs.as<float>();
+        e.rounds = idx->d.rounds;
+        e.bits = 0;
+        e.rotated = idx->qrot.as<float>();
+        HIPX(idx->dev, launch_encode(e, s), "query rotate kernel");
+        qrot = idx->qrot.as<float>();
+    }
+    HIPX(idx->dev, idx->probe_scores.ensure((size_t)nq * idx->nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->probes.ensure((size_t)nq * nprobe * 4, 0, s), "scratch");
+    IvfProbeArgs pa{};
+    pa.centroids = idx->centroids.as<float>();
+    pa.nlist = idx->nlist;
+    pa.P = idx->sample_dim;
+    pa.qrot = qrot;
+    pa.scores = idx->probe_scores.as<float>();
+    pa.nprobe = nprobe;
+    pa.probes = idx->probes.as<uint32_t>();
+    HIPX(idx->dev, ivf_launch_probes(pa, nq, s), "probe kernels");
+    uint64_t per = 0;
+    for (uint32_t i = 0; i < nprobe && i < idx->list_sizes_desc.size(); ++i) per += idx->list_sizes_desc[i];
+    HIPX(idx->dev, idx->cand.ensure(std::max<uint64_t>(per * nq, 1) * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->cand_tot.ensure((size_t)nq * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->cand_off.ensure(((size_t)nq + 1) * 8, 0, s), "scratch");
+    HIPX(idx->dev, ivf_launch_gather(idx->probes.as<uint32_t>(), nq, nprobe, idx->list_off.as<uint32_t>(),
+                                     idx->list_rows.as<uint32_t>(), idx->cand_tot.as<uint64_t>(),
+                                     idx->cand_off.as<uint64_t>(), idx->cand.as<uint32_t>(), s),
+         "gather kernels");
+    *max_per_query = per;
+    return BV_OK;
 }
 
 // ---------------------------------------------------------------- queries
@@ -550,8 +836,14 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
         a.q = qscan;
         a.q_stride = qstride;
     }
-    const uint64_t n = idx->rows;
-    const uint32_t grid = grid_for(idx, n);
+    uint64_t n = idx->rows;
+    if (idx->ivf) {  // scan only the probed lists: indexed mode with per-query candidate ranges
+        rc = ivf_candidates(idx, d_q, nq, &n);
+        if (rc) return rc;
+        a.cand = idx->cand.as<uint32_t>();
+        a.cand_off = idx->cand_off.as<uint64_t>();
+    }
+    const uint32_t grid = grid_for(idx, std::max<uint64_t>(n, 1));
     rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a);
     if (rc) return rc;
     a.codes = idx->quant ? idx->codes.p : idx->raw.p;
@@ -867,6 +1159,7 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
 
 static int host_query_dense(bv_index *idx, const float *q, uint32_t nq, uint32_t k, const uint32_t *mask,
                             uint64_t mask_words, uint32_t *rows, float *scores, uint32_t *n_out) {
+    if (idx->ivf) return fail(BV_E_UNSUPPORTED, "IVF queries serve k <= %d", MAX_KPRIME);
     std::vector<float> s(idx->rows);
     for (uint32_t i = 0; i < nq; i++) {
         int rc = dense_scores(idx, q + (size_t)i * idx->dim, nullptr, 0, s.data());
@@ -906,9 +1199,17 @@ extern "C" int bv_index_get_stats(bv_index *idx, bv_index_stats *out) {
     if (idx->d.chunk_rows && idx->rows) chunks = (uint32_t)((idx->rows + idx->d.chunk_rows - 1) / idx->d.chunk_rows);
     out->chunk_count = chunks;
     out->tuned_recall = -1.0f;
+    if (idx->ivf && idx->nlist) {
+        out->nlist = idx->nlist;
+        const uint32_t saved = idx->nprobe_override;
+        out->nprobe = ivf_resolve_nprobe(idx);
+        idx->nprobe_override = saved;
+        out->build_ms = idx->build_ms;
+    }
     out->last_query_ms = idx->last_query_ms;
     out->last_query_gpu_ms = idx->last_query_gpu_ms;
-    out->device_bytes = idx->raw.cap + idx->codes.cap + idx->scales.cap;
+    out->device_bytes = idx->raw.cap + idx->codes.cap + idx->scales.cap + idx->sample.cap + idx->centroids.cap +
+                        idx->list_off.cap + idx->list_rows.cap;
     out->last_scanned_rows = idx->last_scanned;
     return BV_OK;
 }
@@ -950,5 +1251,31 @@ extern "C" int bv_index_export_rotated_query(bv_index *idx, const float *q, floa
     HIPX(idx->dev, hipMemcpyAsync(rotated, idx->qrot.p, (size_t)idx->P * 4, hipMemcpyDeviceToHost, idx->stream),
          "download");
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "rotate");
+    return BV_OK;
+}
+
+extern "C" int bv_index_build(bv_index *idx) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!idx->ivf) return BV_OK;
+    if (idx->rows == 0) return fail(BV_E_STATE, "IVF build needs rows");
+    if (idx->built_rows == idx->rows) return BV_OK;
+    return ivf_build(idx);
+}
+
+extern "C" int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *list_off, uint32_t *list_rows) {
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!idx->ivf) return fail(BV_E_STATE, "not an IVF index");
+    if (idx->built_rows != idx->rows) return fail(BV_E_STATE, "IVF lists are not built (bv_index_build)");
+    if (centroids)
+        HIPX(idx->dev, hipMemcpy(centroids, idx->centroids.p, (size_t)idx->nlist * idx->sample_dim * 4,
+                                 hipMemcpyDeviceToHost), "download");
+    if (list_off)
+        HIPX(idx->dev, hipMemcpy(list_off, idx->list_off.p, ((size_t)idx->nlist + 1) * 4, hipMemcpyDeviceToHost),
+             "download");
+    if (list_rows && idx->rows)
+        HIPX(idx->dev, hipMemcpy(list_rows, idx->list_rows.p, (size_t)idx->rows * 4, hipMemcpyDeviceToHost),
+             "download");
     return BV_OK;
 }

@@ -1,0 +1,458 @@
+// gfx950 kernels of the IVF path: k-means build, list construction, probes.
+//
+//   ivf_copy_rows        row gathers (centroid init / re-seed, reservoir)
+//   ivf_normalize_rows   normalizeRows (src/index/kmeans.ts:211-219)
+//   ivf_assign<L>        nearest-centroid argmax over a tiled fp32 product
+//                        (assign.ts / assignQ8.ts / assignQ4.ts / assignQ1.ts)
+//   ivf_block_hist, ivf_list_bases, ivf_scan_offsets, ivf_scatter
+//                        stable counting sort = the CSR lists
+//                        (src/index/ivfquant.ts:297-305)
+//   ivf_centroid_means   updateCentroids' f32 sums in row order + mean
+//                        (src/index/kmeans.ts:177-209)
+//   ivf_probe_scores     pickProbes' f64 four-way dot (ivfquant.ts:495-511)
+//   ivf_probe_select     top-nprobe of the probe scores, best first
+//   ivf_probe_totals, ivf_gather_lists
+//                        gatherCandidates (ivfquant.ts:513-527): the probed
+//                        lists concatenated in probe order
+#include "bv_kernels.h"
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bvk {
+
+namespace {
+
+__device__ __forceinline__ uint32_t ord_f32_i(float s) {
+    s = s + 0.0f;
+    uint32_t b = __float_as_uint(s);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+// larger = better: higher score, then lower index
+__device__ __forceinline__ uint64_t idx_key(float s, uint32_t c) {
+    return ((uint64_t)ord_f32_i(s) << 32) | (uint64_t)(0xffffffffu - c);
+}
+
+}  // namespace
+
+// dst[dst_idx ? dst_idx[j] : j] = src[src_idx[j]], rows of `dim` floats.
+__global__ __launch_bounds__(256) void ivf_copy_rows(IvfCopyArgs a) {
+    const uint32_t j = blockIdx.x;
+    if (j >= a.n) return;
+    const float *s = a.src + (uint64_t)a.src_idx[j] * a.src_stride;
+    float *d = a.dst + (uint64_t)(a.dst_idx ? a.dst_idx[j] : j) * a.dst_stride;
+    for (uint32_t i = threadIdx.x; i < a.dim; i += blockDim.x) d[i] = s[i];
+}
+
+// normalizeRows: s = sequential f64 sum of m*m (each product exact in f64),
+// inv = 1 / (sqrt(s) || 1), m = f32(m * inv).  One thread per row.
+__global__ __launch_bounds__(256) void ivf_normalize_rows(float *m, uint32_t rows, uint32_t dim, uint32_t stride) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    float *v = m + (uint64_t)r * stride;
+    double s = 0.0;
+    for (uint32_t i = 0; i < dim; ++i) s = fma((double)v[i], (double)v[i], s);
+    const double sq = sqrt(s);
+    const double inv = 1.0 / (sq != 0.0 ? sq : 1.0);
+    for (uint32_t i = 0; i < dim; ++i) v[i] = (float)((double)v[i] * inv);
+}
+
+// ---------------------------------------------------------------- assign --
+// Rows x centroids product in 128 x 128 tiles (256 threads, 8 x 8 outputs
+// each, fp32 fused multiply-add over the dimension in order), argmax per row
+// with the lowest centroid index winning ties.  The row loader dequantizes
+// codes exactly as the reference's assign kernels do before the product.
+constexpr int AT = 128;  // rows and centroids per tile
+constexpr int AK = 8;    // dimension chunk per LDS stage
+
+template <int BITS> struct RowLoader;
+template <> struct RowLoader<0> {  // fp32 rows
+    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i) {
+        return a.rows[r * a.row_stride + i];
+    }
+};
+template <> struct RowLoader<8> {  // unpack4x8snorm(b) * scale
+    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i) {
+        const uint32_t w = a.codes[r * a.words_per_row + (i >> 2)];
+        const int8_t b = (int8_t)((w >> (8 * (i & 3))) & 0xffu);
+        const float u = fmaxf((float)b / 127.0f, -1.0f);
+        return u * a.scales[r];
+    }
+};
+template <> struct RowLoader<4> {  // signed nibble * (scale * f32(1/7))
+    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i) {
+        const uint32_t w = a.codes[r * a.words_per_row + (i >> 3)];
+        const int32_t n = (int32_t)((w >> (4 * (i & 7))) & 0xfu);
+        const float inv7 = a.scales[r] * (1.0f / 7.0f);
+        return (float)(n - 16 * (n >> 3)) * inv7;
+    }
+};
+template <> struct RowLoader<1> {  // sign bits as +-1 (the scale multiplies the sum)
+    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i) {
+        const uint32_t w = a.codes[r * a.words_per_row + (i >> 5)];
+        return ((w >> (i & 31)) & 1u) ? 1.0f : -1.0f;
+    }
+};
+
+template <int BITS>
+__global__ __launch_bounds__(256) void ivf_assign(IvfAssignArgs a) {
+    __shared__ float As[AK][AT + 4];
+    __shared__ float Bs[AK][AT + 4];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const uint64_t r0 = (uint64_t)blockIdx.x * AT;
+    uint64_t best[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) best[i] = 0;
+    for (uint32_t c0 = 0; c0 < a.nlist; c0 += AT) {
+        float acc[8][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+        for (uint32_t k0 = 0; k0 < a.dim; k0 += AK) {
+            // stage AK x AT rows and centroids: 1024 values each, 4 per thread
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int e = tid + t * 256;
+                const int kk = e % AK, rr = e / AK;  // consecutive lanes read consecutive elements of a row
+                const uint32_t k = k0 + kk;
+                const uint64_t r = r0 + rr;
+                As[kk][rr] = (r < a.n && k < a.dim) ? RowLoader<BITS>::get(a, r, k) : 0.0f;
+                const uint32_t c = c0 + rr;
+                Bs[kk][rr] = (c < a.nlist && k < a.dim) ? a.centroids[(uint64_t)c * a.cen_stride + k] : 0.0f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int kk = 0; kk < AK; ++kk) {
+                float av[8], bv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) av[i] = As[kk][ty + 16 * i];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bv[j] = Bs[kk][tx + 16 * j];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+            }
+            __syncthreads();
+        }
+        // fold this tile into each row's running best
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint64_t b = best[i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t c = c0 + tx + 16 * j;
+                if (c < a.nlist) {
+                    const float s = BITS == 1 ? acc[i][j] * a.scales[(r0 + ty + 16 * i) < a.n ? r0 + ty + 16 * i : 0]
+                                              : acc[i][j];
+                    const uint64_t key = idx_key(s, c);
+                    b = key > b ? key : b;
+                }
+            }
+            best[i] = b;
+        }
+    }
+    // reduce over the 16 threads sharing each row (consecutive lanes)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        uint64_t b = best[i];
+#pragma unroll
+        for (int s = 1; s < 16; s <<= 1) {
+            const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(b >> 32), s) << 32) |
+                               (uint32_t)__shfl_xor((int)(uint32_t)b, s);
+            b = o > b ? o : b;
+        }
+        const uint64_t r = r0 + ty + 16 * i;
+        if (tx == 0 && r < a.n) a.out[r] = 0xffffffffu - (uint32_t)b;
+    }
+}
+
+// ----------------------------------------------------------------- lists --
+// Stable counting sort of rows by cluster: per-block histograms, per-cluster
+// running bases over the blocks, cluster offsets, then a scatter where each
+// row's rank inside its block counts the earlier rows of the same cluster.
+constexpr int LB = 1024;  // rows per block
+
+__global__ __launch_bounds__(256) void ivf_block_hist(const uint32_t *assign, uint64_t n, uint32_t nlist,
+                                                      uint32_t *hist) {
+    extern __shared__ uint32_t h[];
+    for (uint32_t c = threadIdx.x; c < nlist; c += blockDim.x) h[c] = 0;
+    __syncthreads();
+    const uint64_t r0 = (uint64_t)blockIdx.x * LB;
+    for (uint32_t j = threadIdx.x; j < LB; j += blockDim.x)
+        if (r0 + j < n) atomicAdd(&h[assign[r0 + j]], 1u);
+    __syncthreads();
+    for (uint32_t c = threadIdx.x; c < nlist; c += blockDim.x) hist[(uint64_t)blockIdx.x * nlist + c] = h[c];
+}
+
+// base[b][c] = sum of hist[b'][c] for b' < b; totals[c] = the full sum.
+__global__ __launch_bounds__(256) void ivf_list_bases(const uint32_t *hist, uint32_t nblk, uint32_t nlist,
+                                                      uint32_t *base, uint32_t *totals) {
+    const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= nlist) return;
+    uint32_t run = 0;
+    uint32_t b = 0;
+    for (; b + 8 <= nblk; b += 8) {
+        uint32_t h[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) h[u] = hist[(uint64_t)(b + u) * nlist + c];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            base[(uint64_t)(b + u) * nlist + c] = run;
+            run += h[u];
+        }
+    }
+    for (; b < nblk; ++b) {
+        base[(uint64_t)b * nlist + c] = run;
+        run += hist[(uint64_t)b * nlist + c];
+    }
+    totals[c] = run;
+}
+
+// offset[0] = 0, offset[c+1] = offset[c] + totals[c] (one workgroup).
+__global__ __launch_bounds__(256) void ivf_scan_offsets(const uint32_t *totals, uint32_t nlist, uint32_t *offset) {
+    __shared__ uint32_t part[256];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t per = (nlist + 255) / 256, c0 = tid * per;
+    uint32_t s = 0;
+    for (uint32_t c = c0; c < c0 + per && c < nlist; ++c) s += totals[c];
+    part[tid] = s;
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t run = 0;
+        for (int t = 0; t < 256; ++t) {
+            const uint32_t v = part[t];
+            part[t] = run;
+            run += v;
+        }
+        offset[nlist] = run;
+    }
+    __syncthreads();
+    uint32_t run = part[tid];
+    for (uint32_t c = c0; c < c0 + per && c < nlist; ++c) {
+        offset[c] = run;
+        run += totals[c];
+    }
+}
+
+__global__ __launch_bounds__(256) void ivf_scatter(const uint32_t *assign, uint64_t n, uint32_t nlist,
+                                                   const uint32_t *offset, const uint32_t *base, uint32_t *rows_out) {
+    __shared__ uint32_t cl[LB];
+    const uint64_t r0 = (uint64_t)blockIdx.x * LB;
+    for (uint32_t j = threadIdx.x; j < LB; j += blockDim.x) cl[j] = r0 + j < n ? assign[r0 + j] : 0xffffffffu;
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < LB; j += blockDim.x) {
+        if (r0 + j >= n) continue;
+        const uint32_t c = cl[j];
+        uint32_t rank = 0;
+        for (uint32_t i = 0; i < j; ++i) rank += cl[i] == c ? 1u : 0u;
+        rows_out[offset[c] + base[(uint64_t)blockIdx.x * nlist + c] + rank] = (uint32_t)(r0 + j);
+    }
+}
+
+// updateCentroids' mean: thread (c, i) adds column i of its cluster's rows in
+// row order in f32 (the reference's Float32Array `+=`), then stores
+// f32(sum * (1 / count)) with the reciprocal in f64.  Empty clusters are
+// left for the host's re-seed.
+__global__ __launch_bounds__(256) void ivf_centroid_means(const float *sample, uint32_t stride, uint32_t dim,
+                                                          const uint32_t *offset, const uint32_t *list_rows,
+                                                          uint32_t nlist, float *centroids, uint32_t cen_stride) {
+    const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t c = (uint32_t)(t / dim), i = (uint32_t)(t % dim);
+    if (c >= nlist) return;
+    const uint32_t b = offset[c], e = offset[c + 1];
+    if (b == e) return;
+    float s = 0.0f;
+    for (uint32_t j = b; j < e; ++j) s = s + sample[(uint64_t)list_rows[j] * stride + i];
+    const double inv = 1.0 / (double)(e - b);
+    centroids[(uint64_t)c * cen_stride + i] = (float)((double)s * inv);
+}
+
+// ---------------------------------------------------------------- probes --
+// pickProbes: four f64 accumulators over the strided elements 4j+m (each
+// product of two f32 exact in f64), a0 + a1 + a2 + a3, stored f32.  Four
+// lanes per centroid, 64 centroids per workgroup; grid (ceil(nlist/64), nq).
+__global__ __launch_bounds__(256) void ivf_probe_scores(IvfProbeArgs a) {
+    const uint32_t qi = blockIdx.y, g = threadIdx.x >> 2, m = threadIdx.x & 3;
+    const uint32_t c = blockIdx.x * 64 + g;
+    const float *rq = a.qrot + (uint64_t)qi * a.P;
+    const uint32_t vec = a.P & ~3u;
+    const float *cen = a.centroids + (uint64_t)(c < a.nlist ? c : 0) * a.P;
+    double acc = 0.0;
+    if (c < a.nlist)
+        for (uint32_t i = m; i < vec; i += 4) acc = fma((double)cen[i], (double)rq[i], acc);
+    const double a1 = __shfl_down(acc, 1, 4), a2 = __shfl_down(acc, 2, 4), a3 = __shfl_down(acc, 3, 4);
+    if (m == 0 && c < a.nlist) {
+        double s = ((acc + a1) + a2) + a3;
+        for (uint32_t i = vec; i < a.P; ++i) s = fma((double)cen[i], (double)rq[i], s);  // the fp32 IVF tail
+        a.scores[(uint64_t)qi * a.nlist + c] = (float)s;
+    }
+}
+
+// Best nprobe centroids of one query, best first (score desc, index asc).
+// One workgroup per query: a bisection on the 64-bit keys finds the
+// nprobe-th key (keys are unique), then the survivors are ranked.
+__global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
+    extern __shared__ uint64_t pk[];  // nlist keys
+    __shared__ uint32_t cnt_s[4];
+    __shared__ uint64_t sel[1024];
+    __shared__ uint32_t nsel;
+    const uint32_t qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *sc = a.scores + (uint64_t)qi * a.nlist;
+    for (uint32_t c = tid; c < a.nlist; c += 256) pk[c] = idx_key(sc[c], c);
+    if (tid == 0) nsel = 0;
+    __syncthreads();
+    const uint32_t np = a.nprobe < a.nlist ? a.nprobe : a.nlist;
+    uint64_t lo = 0, hi = ~0ull;  // count(>= lo) >= np > count(>= hi) (hi unreachable)
+    if (np < a.nlist) {
+        for (int it = 0; it < 64 && hi - lo > 1; ++it) {
+            const uint64_t mid = lo + ((hi - lo) >> 1);
+            uint32_t c = 0;
+            for (uint32_t j = tid; j < a.nlist; j += 256) c += pk[j] >= mid ? 1u : 0u;
+#pragma unroll
+            for (int s = 1; s < 64; s <<= 1) c += __shfl_xor(c, s);
+            if (lane == 0) cnt_s[wave] = c;
+            __syncthreads();
+            const uint32_t tot = cnt_s[0] + cnt_s[1] + cnt_s[2] + cnt_s[3];
+            __syncthreads();
+            if (tot >= np) lo = mid;
+            else hi = mid;
+        }
+    }
+    // keys >= lo: exactly np of them when np < nlist (unique keys), else all
+    for (uint32_t j = tid; j < a.nlist; j += 256)
+        if (pk[j] >= lo) {
+            const uint32_t s = atomicAdd(&nsel, 1u);
+            if (s < 1024) sel[s] = pk[j];
+        }
+    __syncthreads();
+    const uint32_t m = nsel < 1024 ? nsel : 1024;
+    for (uint32_t j = tid; j < m; j += 256) {
+        const uint64_t k = sel[j];
+        uint32_t r = 0;
+        for (uint32_t i = 0; i < m; ++i) r += sel[i] > k ? 1u : 0u;
+        if (r < np) a.probes[(uint64_t)qi * a.nprobe + r] = 0xffffffffu - (uint32_t)k;
+    }
+}
+
+// Candidates per query: the sizes of its probed lists.
+__global__ __launch_bounds__(256) void ivf_probe_totals(const uint32_t *probes, uint32_t nq, uint32_t nprobe,
+                                                        const uint32_t *offset, uint64_t *totals) {
+    const uint32_t qi = blockIdx.x * blockDim.x + threadIdx.x;
+    if (qi >= nq) return;
+    uint64_t t = 0;
+    for (uint32_t p = 0; p < nprobe; ++p) {
+        const uint32_t c = probes[(uint64_t)qi * nprobe + p];
+        t += offset[c + 1] - offset[c];
+    }
+    totals[qi] = t;
+}
+
+// cand_off[q] = sum of totals before q (one workgroup).
+__global__ __launch_bounds__(256) void ivf_cand_offsets(const uint64_t *totals, uint32_t nq, uint64_t *cand_off) {
+    __shared__ uint64_t part[256];
+    const uint32_t tid = threadIdx.x, per = (nq + 255) / 256, q0 = tid * per;
+    uint64_t s = 0;
+    for (uint32_t q = q0; q < q0 + per && q < nq; ++q) s += totals[q];
+    part[tid] = s;
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t run = 0;
+        for (int t = 0; t < 256; ++t) {
+            const uint64_t v = part[t];
+            part[t] = run;
+            run += v;
+        }
+        cand_off[nq] = run;
+    }
+    __syncthreads();
+    uint64_t run = part[tid];
+    for (uint32_t q = q0; q < q0 + per && q < nq; ++q) {
+        cand_off[q] = run;
+        run += totals[q];
+    }
+}
+
+// gatherCandidates: the probed lists in probe order, rows ascending within
+// a list.  One workgroup per query.
+__global__ __launch_bounds__(256) void ivf_gather_lists(const uint32_t *probes, uint32_t nprobe,
+                                                        const uint32_t *offset, const uint32_t *list_rows,
+                                                        const uint64_t *cand_off, uint32_t *cand) {
+    const uint32_t qi = blockIdx.x;
+    uint64_t w = cand_off[qi];
+    for (uint32_t p = 0; p < nprobe; ++p) {
+        const uint32_t c = probes[(uint64_t)qi * nprobe + p];
+        const uint32_t b = offset[c], e = offset[c + 1];
+        for (uint32_t j = threadIdx.x; j < e - b; j += blockDim.x) cand[w + j] = list_rows[b + j];
+        w += e - b;
+    }
+}
+
+// ------------------------------------------------------------- launchers --
+hipError_t ivf_launch_copy_rows(const IvfCopyArgs &a, hipStream_t s) {
+    if (a.n == 0) return hipSuccess;
+    hipLaunchKernelGGL(ivf_copy_rows, dim3(a.n), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t ivf_launch_normalize(float *m, uint32_t rows, uint32_t dim, uint32_t stride, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(ivf_normalize_rows, dim3((rows + 255) / 256), dim3(256), 0, s, m, rows, dim, stride);
+    return hipGetLastError();
+}
+
+hipError_t ivf_launch_assign(const IvfAssignArgs &a, int bits, hipStream_t s) {
+    if (a.n == 0) return hipSuccess;
+    const dim3 grid((uint32_t)((a.n + AT - 1) / AT));
+    switch (bits) {
+    case 0: hipLaunchKernelGGL(ivf_assign<0>, grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL(ivf_assign<8>, grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(ivf_assign<4>, grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL(ivf_assign<1>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+uint32_t ivf_list_blocks(uint64_t n) { return (uint32_t)((n + LB - 1) / LB); }
+
+hipError_t ivf_launch_lists(const uint32_t *assign, uint64_t n, uint32_t nlist, uint32_t *hist, uint32_t *base,
+                            uint32_t *totals, uint32_t *offset, uint32_t *rows_out, hipStream_t s) {
+    if (nlist == 0 || nlist > IVF_MAX_NLIST) return hipErrorInvalidValue;
+    const uint32_t nblk = ivf_list_blocks(n);
+    if (nblk) hipLaunchKernelGGL(ivf_block_hist, dim3(nblk), dim3(256), nlist * 4, s, assign, n, nlist, hist);
+    hipLaunchKernelGGL(ivf_list_bases, dim3((nlist + 255) / 256), dim3(256), 0, s, hist, nblk, nlist, base, totals);
+    hipLaunchKernelGGL(ivf_scan_offsets, dim3(1), dim3(256), 0, s, totals, nlist, offset);
+    if (nblk) hipLaunchKernelGGL(ivf_scatter, dim3(nblk), dim3(256), 0, s, assign, n, nlist, offset, base, rows_out);
+    return hipGetLastError();
+}
+
+hipError_t ivf_launch_means(const float *sample, uint32_t stride, uint32_t dim, const uint32_t *offset,
+                            const uint32_t *list_rows, uint32_t nlist, float *centroids, uint32_t cen_stride,
+                            hipStream_t s) {
+    const uint64_t t = (uint64_t)nlist * dim;
+    hipLaunchKernelGGL(ivf_centroid_means, dim3((uint32_t)((t + 255) / 256)), dim3(256), 0, s, sample, stride, dim,
+                       offset, list_rows, nlist, centroids, cen_stride);
+    return hipGetLastError();
+}
+
+hipError_t ivf_launch_probes(const IvfProbeArgs &a, uint32_t nq, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    if (a.nlist > IVF_MAX_NLIST || a.nprobe > IVF_MAX_NPROBE) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(ivf_probe_scores, dim3((a.nlist + 63) / 64, nq), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(ivf_probe_select, dim3(nq), dim3(256), (size_t)a.nlist * 8, s, a);
+    return hipGetLastError();
+}
+
+hipError_t ivf_launch_gather(const uint32_t *probes, uint32_t nq, uint32_t nprobe, const uint32_t *offset,
+                             const uint32_t *list_rows, uint64_t *totals, uint64_t *cand_off, uint32_t *cand,
+                             hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    hipLaunchKernelGGL(ivf_probe_totals, dim3((nq + 255) / 256), dim3(256), 0, s, probes, nq, nprobe, offset, totals);
+    hipLaunchKernelGGL(ivf_cand_offsets, dim3(1), dim3(256), 0, s, totals, nq, cand_off);
+    hipLaunchKernelGGL(ivf_gather_lists, dim3(nq), dim3(256), 0, s, probes, nprobe, offset, list_rows, cand_off, cand);
+    return hipGetLastError();
+}
+
+}  // namespace bvk

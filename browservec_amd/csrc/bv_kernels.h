@@ -101,6 +101,8 @@ struct EncodeArgs {
     uint32_t *codes;          // rows x (P/per)
     float *scales;            // rows
     float *rotated;           // optional rows x P
+    const int32_t *sample_slot; // optional per row: IVF reservoir slot or -1
+    float *sample;            // IVF reservoir (slots x P) when sample_slot is set
     uint32_t *slow_rows;      // counter of rows that took the sequential 1-bit sum
 };
 
@@ -129,6 +131,59 @@ struct LevelArgs {
     unsigned char *out;       // nq x stride bytes: packed levels + QLevelTail
     uint64_t stride;
 };
+
+// ---- IVF ------------------------------------------------------------------
+constexpr uint32_t IVF_MAX_NLIST = 4096;   // lists (the reference's automatic cap)
+constexpr uint32_t IVF_MAX_NPROBE = 1024;
+
+struct IvfCopyArgs {
+    const float *src;
+    uint64_t src_stride;
+    const uint32_t *src_idx;  // [n] source rows
+    float *dst;
+    uint64_t dst_stride;
+    const uint32_t *dst_idx;  // [n] destination rows, or null for 0..n-1
+    uint32_t n, dim;
+};
+
+struct IvfAssignArgs {
+    uint64_t n;               // rows to assign
+    uint32_t dim;             // product length (padded dim for codes)
+    const float *rows;        // fp32 rows (bits 0)
+    uint64_t row_stride;
+    const uint32_t *codes;    // codes (bits 8/4/1)
+    uint32_t words_per_row;
+    const float *scales;
+    const float *centroids;   // nlist x cen_stride
+    uint32_t cen_stride;
+    uint32_t nlist;
+    uint32_t *out;            // [n] nearest centroid
+};
+
+struct IvfProbeArgs {
+    const float *centroids;   // nlist x P
+    uint32_t nlist, P;
+    const float *qrot;        // nq x P queries in the centroids' space
+    float *scores;            // nq x nlist scratch
+    uint32_t nprobe;
+    uint32_t *probes;         // nq x nprobe, best first
+};
+
+hipError_t ivf_launch_copy_rows(const IvfCopyArgs &a, hipStream_t s);
+hipError_t ivf_launch_normalize(float *m, uint32_t rows, uint32_t dim, uint32_t stride, hipStream_t s);
+hipError_t ivf_launch_assign(const IvfAssignArgs &a, int bits, hipStream_t s);
+uint32_t ivf_list_blocks(uint64_t n);
+// hist/base: ivf_list_blocks(n) x nlist; totals: nlist; offset: nlist+1; rows_out: n.
+hipError_t ivf_launch_lists(const uint32_t *assign, uint64_t n, uint32_t nlist, uint32_t *hist, uint32_t *base,
+                            uint32_t *totals, uint32_t *offset, uint32_t *rows_out, hipStream_t s);
+hipError_t ivf_launch_means(const float *sample, uint32_t stride, uint32_t dim, const uint32_t *offset,
+                            const uint32_t *list_rows, uint32_t nlist, float *centroids, uint32_t cen_stride,
+                            hipStream_t s);
+hipError_t ivf_launch_probes(const IvfProbeArgs &a, uint32_t nq, hipStream_t s);
+// totals: nq; cand_off: nq+1; cand: capacity for every query's candidates.
+hipError_t ivf_launch_gather(const uint32_t *probes, uint32_t nq, uint32_t nprobe, const uint32_t *offset,
+                             const uint32_t *list_rows, uint64_t *totals, uint64_t *cand_off, uint32_t *cand,
+                             hipStream_t s);
 
 // Chooses the lane layout for a codec and row size; false if unsupported.
 bool scan_supported(int codec, uint32_t units);

@@ -808,6 +808,13 @@ __global__ __launch_bounds__(128) void encode_rows(EncodeArgs a) {
 #pragma unroll
             for (int t = 0; t < E; ++t) a.rotated[row * P + e0 + t] = x[t];
         }
+        if (a.sample_slot && active) {  // IVF reservoir: the rotated row goes to its sample slot
+            const int32_t slot = a.sample_slot[row];
+            if (slot >= 0) {
+#pragma unroll
+                for (int t = 0; t < E; ++t) a.sample[(uint64_t)slot * P + e0 + t] = x[t];
+            }
+        }
         if (a.bits == 0) continue;
         const uint32_t W = P / (a.bits == 8 ? 4 : (a.bits == 4 ? 8 : 32));
         quantize_store_wave<E>(x, P, a.bits, cbytes, fbuf, a.codes + row * W, a.scales + row, a.slow_rows, lane);

@@ -259,3 +259,43 @@ class QuantIndex(NativeIndex):
         out = np.empty(self.padded_dim, np.float32)
         L.check(self.lib.bv_index_export_rotated_query(self.handle, _ptr(q), _ptr(out)))
         return out
+
+
+class IVFIndex(NativeIndex):
+    """IVF over fp32 rows (src/index/ivf.ts:51): spherical k-means lists,
+    probes by exact dot with the centroids, scan of the probed lists."""
+
+    kind = L.KIND_IVF
+    is_ivf = True  # BrowserVec filters IVF queries by over-fetching (src/index.ts:389-394)
+
+    def __init__(self, ctx, dim, metric="cosine", ivf: dict | None = None, chunk_rows=None):
+        super().__init__(ctx, dim, metric, 0, chunk_rows=chunk_rows, ivf=ivf)
+
+    def build(self) -> None:
+        L.check(self.lib.bv_index_build(self.handle))
+
+    def export_ivf(self):
+        """(centroids [nlist, D], list offsets [nlist+1], list rows [rows])."""
+        self.build()
+        st = self.stats()
+        nlist = st["nlist"]
+        D = st["padded_dim"] if self.bits else self.dim
+        cen = np.empty((nlist, D), np.float32)
+        off = np.empty(nlist + 1, np.uint32)
+        rows = np.empty(max(self.size, 1), np.uint32)
+        L.check(self.lib.bv_index_export_ivf(self.handle, _ptr(cen), _ptr(off), _ptr(rows)))
+        return cen, off, rows[: self.size]
+
+
+class IVFQuantIndex(IVFIndex):
+    """IVF over TurboQuant codes (src/index/ivfquant.ts:33): k-means on the
+    rotated reservoir sample, rows assigned by their codes."""
+
+    kind = L.KIND_IVFQUANT
+
+    def __init__(self, ctx, dim, bits=8, seed=0x9E3779B9, rounds=2, ivf: dict | None = None, chunk_rows=None,
+                 metric="cosine"):
+        NativeIndex.__init__(self, ctx, dim, metric, bits, seed=seed, rounds=rounds, chunk_rows=chunk_rows, ivf=ivf)
+        st = self.stats()
+        self.padded_dim = st["padded_dim"]
+        self.words_per_row = st["words_per_row"]

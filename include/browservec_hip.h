@@ -196,6 +196,17 @@ int bv_index_export_scores(bv_index *idx, const float *q, float *scores);
 /* The device-rotated query (padded_dim floats), quantized kinds only. */
 int bv_index_export_rotated_query(bv_index *idx, const float *q, float *rotated);
 
+/* ---- IVF ------------------------------------------------------------------------ */
+/* IVFIndex / IVFQuantIndex build (src/index/ivf.ts:191-259,
+ * src/index/ivfquant.ts:248-312): k-means on the reservoir sample, final
+ * assignment, CSR lists.  Queries build on demand after appends, as the
+ * reference does; this entry builds now. */
+int bv_index_build(bv_index *idx);
+/* The built IVF state for parity checks: centroids (nlist x D floats, D =
+ * padded_dim for quantized kinds, dim for fp32), list offsets (nlist+1) and
+ * list rows (rows, ascending within a list).  Any pointer may be null. */
+int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *list_off, uint32_t *list_rows);
+
 #ifdef __cplusplus
 }
 #endif

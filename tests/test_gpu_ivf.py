@@ -1,0 +1,203 @@
+"""IVF parity on the device: the k-means build (reservoir, init, Lloyd
+iterations, final assignment, CSR lists) against the oracle's restatement of
+src/index/ivfquant.ts / ivf.ts / kmeans.ts, and IVF queries (probes, list
+gather, scan, exact re-rank) against the oracle pipeline."""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from tests.helpers import REL_TOL, clustered, gaussian, need_gpu, quant_magnitude, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    need_gpu()
+    from browservec_amd import DeviceContext
+
+    c = DeviceContext(0)
+    yield c
+    c.destroy()
+
+
+def dequant_f32(words, scales, bits, P):
+    """The device assignment's row values: unpack4x8snorm(b) * scale (int8),
+    signed nibble * (scale * f32(1/7)) (int4), f32 arithmetic throughout."""
+    n = words.shape[0]
+    if bits == 8:
+        b = words.view(np.uint8).reshape(n, -1)[:, :P].view(np.int8).astype(np.float32)
+        u = np.maximum(b / np.float32(127.0), np.float32(-1.0))
+        return (u * scales[:, None]).astype(np.float32)
+    w = words.astype(np.uint64)
+    shifts = np.arange(8, dtype=np.uint64) * 4
+    nib = ((w[:, :, None] >> shifts) & 0xF).astype(np.int32).reshape(n, -1)[:, :P]
+    sig = (nib - 16 * (nib >> 3)).astype(np.float32)
+    inv7 = (scales * (np.float32(1.0) / np.float32(7.0))).astype(np.float32)
+    return (sig * inv7[:, None]).astype(np.float32)
+
+
+def reference_build(data, dim, bits, ivf, seed=o.DEFAULT_SEED):
+    """The reference's IVF build restated on the oracle (test infrastructure)."""
+    n = data.shape[0]
+    quant = bits > 0
+    cap = max(1024, ivf.get("sampleSize") or 50000)
+    ivf_seed = ivf.get("seed")
+    if quant:
+        rseed = ((ivf_seed if ivf_seed is not None else seed) ^ 0x85EBCA6B) & 0xFFFFFFFF
+        words, scales, rot = o.encode(data, dim, bits, seed, want_rotated=True)
+        src = rot
+    else:
+        rseed = ivf_seed if ivf_seed is not None else o.IVF_SEED
+        words = scales = None
+        src = data
+    res = o.Reservoir(cap, rseed)
+    sample = np.zeros((cap, src.shape[1]), np.float32)
+    for i in range(n):
+        s = res.slot()
+        if s >= 0:
+            sample[s] = src[i]
+    filled = min(n, cap)
+    if ivf.get("nlist"):
+        nlist = max(1, min(ivf["nlist"], n))
+    else:
+        nlist = max(1, min(min(4096, max(16, int(np.floor(np.sqrt(n) + 0.5)))), n))
+    train = min(filled, ivf.get("trainSize") or 16384)
+    kseed = ivf_seed if ivf_seed is not None else o.IVF_SEED
+    iters = ivf.get("iters") or 8
+    T = np.ascontiguousarray(sample[:train])
+    cen = o.random_init_centroids(T, nlist, kseed)
+    for it in range(iters):
+        a = o.assign_f32(T, cen, order=1)
+        cen, _ = o.update_centroids(T, a, cen, (kseed + it + 1) & 0xFFFFFFFF)
+    if quant:
+        P = src.shape[1]
+        final = o.assign_f32(dequant_f32(words, scales, bits, P), cen, order=1)
+    else:
+        final = o.assign_f32(data, cen, order=1)
+    off, rows = o.build_csr(final, nlist)
+    return dict(cen=cen, off=off, rows=rows, final=final, words=words, scales=scales, nlist=nlist)
+
+
+CASES = [(8, 96, {"nlist": 24, "iters": 4}), (4, 128, {"nlist": 16, "iters": 3, "seed": 77}),
+         (0, 96, {"nlist": 20, "iters": 4}), (0, 100, {"iters": 2, "sampleSize": 1500, "trainSize": 1200})]
+
+
+@pytest.mark.parametrize("bits,dim,ivf", CASES)
+def test_ivf_build_matches_oracle(ctx, bits, dim, ivf):
+    from browservec_amd import IVFIndex, IVFQuantIndex
+
+    say("ivf build", bits, dim, ivf)
+    n = 6000
+    data = clustered(n, dim, 40, 0.08, seed=90 + bits)
+    idx = IVFQuantIndex(ctx, dim, bits=bits, ivf=ivf) if bits else IVFIndex(ctx, dim, ivf=ivf)
+    idx.append(data[:2500], 2500)  # two appends: the reservoir carries over
+    idx.append(data[2500:], n - 2500)
+    cen, off, rows = idx.export_ivf()
+    ref = reference_build(data, dim, bits, ivf)
+    assert cen.shape[0] == ref["nlist"]
+    assert np.array_equal(cen.view(np.uint32), ref["cen"].view(np.uint32)), "centroids differ"
+    assert np.array_equal(off.astype(np.int64), ref["off"].astype(np.int64)), "list offsets differ"
+    assert np.array_equal(rows.astype(np.int64), ref["rows"].astype(np.int64)), "list rows differ"
+    if bits:
+        # against the reference kernels' own dot4 order: equal except near-ties
+        P = cen.shape[1]
+        ref_assign = o.assign_quant(ref["words"], ref["scales"], P, bits, ref["cen"])
+        diff = np.nonzero(ref_assign != ref["final"])[0]
+        V = dequant_f32(ref["words"], ref["scales"], bits, P).astype(np.float64)
+        for r in diff:
+            s = V[r] @ ref["cen"].astype(np.float64).T
+            assert abs(s[ref_assign[r]] - s[ref["final"][r]]) <= 1e-5 * np.abs(V[r]).sum(), r
+    st = idx.stats()
+    assert st["nlist"] == ref["nlist"] and st["nprobe"] == max(1, int(np.floor(ref["nlist"] * 0.05 + 0.5)))
+    idx.destroy()
+
+
+@pytest.mark.parametrize("bits", [8, 0])
+def test_ivf_search_matches_oracle_pipeline(ctx, bits):
+    """Probes, gathered lists, scan and exact re-rank (ivfquant.ts:466-527)."""
+    from browservec_amd import IVFIndex, IVFQuantIndex
+
+    dim, n, nprobe, fetch = 96, 12000, 5, 40
+    ivf = {"nlist": 32, "iters": 3, "nprobe": nprobe}
+    say("ivf search", bits)
+    data = clustered(n, dim, 48, 0.1, seed=123 + bits)
+    idx = IVFQuantIndex(ctx, dim, bits=bits, ivf=ivf) if bits else IVFIndex(ctx, dim, ivf=ivf)
+    idx.append(data, n)
+    cen, off, lrows = idx.export_ivf()
+    qs = data[[5, 777, 11111]] + gaussian(3, dim, 7, normalize=False) * 0.05
+    qs = np.stack([o.normalize(q) for q in qs])
+    rows, scores, cnt = idx.search(qs, fetch, 10) if bits else (None, None, None)
+    flat_hits = [idx.query(q, 10) for q in qs]
+    for i, q in enumerate(qs):
+        rq = o.rotate(q, dim)[0] if bits else q
+        probes, _ = o.topk_canonical(o.probe_scores(cen, rq), nprobe)
+        cand = np.concatenate([lrows[off[c]:off[c + 1]] for c in probes]).astype(np.uint32)
+        if bits:
+            words, scales = idx_codes(idx)
+            approx = o.scan_quant(words, scales, rq, bits, cand=cand)
+            mag = quant_magnitude(words[cand], scales[cand], rq, bits)
+            # query(): the approximate top-10 of the probed lists by code score
+            got = np.array([h.row for h in flat_hits[i]])
+            assert set(got.tolist()) <= set(cand.tolist())
+            want, ws = o.topk_canonical(approx, 10, ids=cand)
+            kth = float(ws[-1])
+            pos = {int(r): j for j, r in enumerate(cand)}
+            for r in set(got.tolist()) ^ set(want.tolist()):
+                assert abs(float(approx[pos[r]]) - kth) <= 2 * REL_TOL * mag.max(), r
+            # search(): exact scores of rows from the probed lists
+            assert cnt[i] == 10 and set(rows[i].tolist()) <= set(cand.tolist())
+            exact = o.rerank_scores(data, q, rows[i])
+            assert np.array_equal(scores[i].view(np.uint32), exact.view(np.uint32))
+        else:
+            exact = o.scan_f32(data[cand], q)
+            want, ws = o.topk_canonical(exact, 10, ids=cand)
+            got = [h.row for h in flat_hits[i]]
+            kth = float(ws[-1])
+            pos = {int(r): j for j, r in enumerate(cand)}
+            for r in set(got) ^ set(want.tolist()):
+                assert abs(float(exact[pos[r]]) - kth) <= 1e-5, r
+    idx.destroy()
+
+
+def idx_codes(idx):
+    words = np.empty((idx.size, idx.words_per_row), np.uint32)
+    scales = np.empty(idx.size, np.float32)
+    from browservec_amd import _lib as L
+    from browservec_amd.index import _ptr
+
+    L.check(idx.lib.bv_index_export_codes(idx.handle, 0, idx.size, _ptr(words), _ptr(scales)))
+    return words, scales
+
+
+def test_ivf_masked_and_nprobe_override(ctx):
+    """Masked IVF scans keep only rows whose bit is set; a per-query nprobe
+    override is consumed by one query (ivfquant.ts:487-491)."""
+    from browservec_amd import IVFQuantIndex
+
+    dim, n = 64, 8000
+    say("ivf masked")
+    data = clustered(n, dim, 30, 0.1, seed=5)
+    idx = IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 20, "iters": 2, "nprobe": 4})
+    idx.append(data, n)
+    rng = np.random.default_rng(3)
+    keep = rng.random(n) < 0.4
+    words = np.zeros((n + 31) // 32, np.uint32)
+    for r in np.nonzero(keep)[0]:
+        words[r >> 5] |= np.uint32(1 << (int(r) & 31))
+    q = data[100]
+    hits = idx.query_masked(q, 10, words)
+    assert hits and all(keep[h.row] for h in hits)
+    idx.set_nprobe(20)  # every list: the masked query sees every kept row
+    hits_all = idx.query_masked(q, 10, words)
+    cen, off, lrows = idx.export_ivf()
+    words_c, scales = idx_codes(idx)
+    rq = o.rotate(q, dim)[0]
+    approx = o.scan_quant(words_c, scales, rq, 8)
+    approx[~keep] = -np.inf
+    want, _ = o.topk_canonical(approx, 10)
+    assert [h.row for h in hits_all][:5] == want[:5].tolist()
+    # the override was consumed: the next query uses nprobe 4 again
+    assert idx.stats()["nprobe"] == 4
+    idx.destroy()
