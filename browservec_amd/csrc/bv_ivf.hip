@@ -294,9 +294,9 @@ __global__ __launch_bounds__(256) void ivf_probe_scores(IvfProbeArgs a) {
 // One workgroup per query: a bisection on the 64-bit keys finds the
 // nprobe-th key (keys are unique), then the survivors are ranked.
 __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
-    extern __shared__ uint64_t pk[];  // nlist keys
+    extern __shared__ uint64_t pk[];  // nlist keys, then up to nlist selected keys
+    uint64_t *sel = pk + a.nlist;
     __shared__ uint32_t cnt_s[4];
-    __shared__ uint64_t sel[1024];
     __shared__ uint32_t nsel;
     const uint32_t qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *sc = a.scores + (uint64_t)qi * a.nlist;
@@ -322,12 +322,9 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
     }
     // keys >= lo: exactly np of them when np < nlist (unique keys), else all
     for (uint32_t j = tid; j < a.nlist; j += 256)
-        if (pk[j] >= lo) {
-            const uint32_t s = atomicAdd(&nsel, 1u);
-            if (s < 1024) sel[s] = pk[j];
-        }
+        if (pk[j] >= lo) sel[atomicAdd(&nsel, 1u)] = pk[j];
     __syncthreads();
-    const uint32_t m = nsel < 1024 ? nsel : 1024;
+    const uint32_t m = nsel;
     for (uint32_t j = tid; j < m; j += 256) {
         const uint64_t k = sel[j];
         uint32_t r = 0;
@@ -441,7 +438,7 @@ hipError_t ivf_launch_probes(const IvfProbeArgs &a, uint32_t nq, hipStream_t s) 
     if (nq == 0) return hipSuccess;
     if (a.nlist > IVF_MAX_NLIST || a.nprobe > IVF_MAX_NPROBE) return hipErrorInvalidValue;
     hipLaunchKernelGGL(ivf_probe_scores, dim3((a.nlist + 63) / 64, nq), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(ivf_probe_select, dim3(nq), dim3(256), (size_t)a.nlist * 8, s, a);
+    hipLaunchKernelGGL(ivf_probe_select, dim3(nq), dim3(256), (size_t)a.nlist * 16, s, a);
     return hipGetLastError();
 }
 

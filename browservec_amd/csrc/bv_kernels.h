@@ -134,7 +134,7 @@ struct LevelArgs {
 
 // ---- IVF ------------------------------------------------------------------
 constexpr uint32_t IVF_MAX_NLIST = 4096;   // lists (the reference's automatic cap)
-constexpr uint32_t IVF_MAX_NPROBE = 1024;
+constexpr uint32_t IVF_MAX_NPROBE = IVF_MAX_NLIST;
 
 struct IvfCopyArgs {
     const float *src;
