@@ -118,7 +118,8 @@ static uint32_t field_u32(napi_env env, napi_value obj, const char *name, uint32
     return x;
 }
 
-/* createIndex(dev, {kind, dim, metric, bits, scorer, seed, rounds, ...}) -> external */
+/* createIndex(dev, {kind, dim, metric, bits, scorer, seed, rounds, chunkRows,
+ *                   nlist, nprobe, sampleSize, trainSize, iters, ivfSeed}) -> external */
 static napi_value create_index(napi_env env, napi_callback_info info) {
     ARGS(2);
     bv_index_desc d;
@@ -133,6 +134,13 @@ static napi_value create_index(napi_env env, napi_callback_info info) {
     d.seed = field_u32(env, argv[1], "seed", 0);
     d.rounds = field_u32(env, argv[1], "rounds", 0);
     d.chunk_rows = field_u32(env, argv[1], "chunkRows", 0);
+    d.nlist = field_u32(env, argv[1], "nlist", 0);
+    d.nprobe = field_u32(env, argv[1], "nprobe", 0);
+    d.sample_size = field_u32(env, argv[1], "sampleSize", 0);
+    d.train_size = field_u32(env, argv[1], "trainSize", 0);
+    d.iters = field_u32(env, argv[1], "iters", 0);
+    d.has_ivf_seed = field_u32(env, argv[1], "hasIvfSeed", 0);
+    d.ivf_seed = field_u32(env, argv[1], "ivfSeed", 0);
     d.target_recall = -1.0f;
     bv_index *idx = NULL;
     int rc = bv_index_create((bv_device *)get_ptr(env, argv[0]), &d, &idx);
@@ -308,6 +316,9 @@ static napi_value stats(napi_env env, napi_callback_info info) {
     NUM("lastQueryMs", st.last_query_ms);
     NUM("lastQueryGpuMs", st.last_query_gpu_ms);
     NUM("deviceBytes", st.device_bytes);
+    NUM("nlist", st.nlist);
+    NUM("nprobe", st.nprobe);
+    NUM("buildMs", st.build_ms);
 #undef NUM
     return obj;
 }

@@ -49,8 +49,10 @@ class HipIndex {
     this.dim = dim;
     this.metric = metric || 'cosine';
     this.bits = bits;
+    const ivf = o.ivf || null;
+    this.isIvf = ivf !== null;
     this.handle = native.createIndex(ctx.handle, {
-      kind: bits ? KIND.quant : KIND.flat,
+      kind: ivf ? (bits ? KIND.ivfquant : KIND.ivf) : (bits ? KIND.quant : KIND.flat),
       dim: dim,
       metric: METRIC[this.metric],
       bits: bits,
@@ -59,6 +61,13 @@ class HipIndex {
       seed: o.seed === undefined ? 0 : o.seed >>> 0,
       rounds: o.rounds || 0,
       chunkRows: o.chunkRows || 0,
+      nlist: ivf && ivf.nlist ? ivf.nlist : 0,
+      nprobe: ivf && ivf.nprobe ? ivf.nprobe : 0,
+      sampleSize: ivf && ivf.sampleSize ? ivf.sampleSize : 0,
+      trainSize: ivf && ivf.trainSize ? ivf.trainSize : 0,
+      iters: ivf && ivf.iters ? ivf.iters : 0,
+      hasIvfSeed: ivf && ivf.seed !== undefined ? 1 : 0,
+      ivfSeed: ivf && ivf.seed !== undefined ? ivf.seed >>> 0 : 0,
     });
   }
   get size() {
@@ -100,6 +109,13 @@ class HipIndex {
   get chunkCount() {
     return native.stats(this.handle).chunkCount;
   }
+  // IVF getters (src/index.ts:718-748); 0 for flat kinds and before a build.
+  get nlist() {
+    return native.stats(this.handle).nlist;
+  }
+  get nprobe() {
+    return native.stats(this.handle).nprobe;
+  }
   stats() {
     return native.stats(this.handle);
   }
@@ -111,9 +127,12 @@ class HipIndex {
   }
 }
 
-// buildIndex (src/index.ts:105-142) for the kinds this library serves.
+// buildIndex (src/index.ts:105-142) for the kinds this library serves:
+// flat and quantized scans, and IVF over either.  HNSW is the reference's
+// CPU graph index and stays there.
 function buildIndex(ctx, dim, metric, quantBits, quant, ann, chunkRows) {
-  if (ann) throw new Error('IVF index kinds are not available in this build yet');
+  if (ann && ann.type === 'hnsw') throw new Error('HNSW indexes are not served by this library');
+  if (ann && metric === 'l2') throw new Error('IVF supports metric cosine/dot only (l2 is later work)');
   const q = quant || {};
   return new HipIndex(ctx, dim, metric, {
     bits: quantBits || 0,
@@ -121,6 +140,7 @@ function buildIndex(ctx, dim, metric, quantBits, quant, ann, chunkRows) {
     rounds: q.rounds,
     scorer: q.scorer,
     chunkRows: chunkRows,
+    ivf: ann || null,
   });
 }
 

@@ -78,7 +78,12 @@ const dim = %(dim)d, n = %(n)d, nq = %(nq)d;
   out.approx = await quant.query(qs.subarray(0, dim), 40);
   out.search = await quant.search(qs, nq, 40, 10);
   out.rerank = await quant.rerankExact(qs.subarray(0, dim), out.approx, 10);
-  flat.destroy(); quant.destroy(); ctx.destroy();
+  const ivf = m.buildIndex(ctx, dim, 'cosine', 8, {}, {nlist: 16, iters: 3, nprobe: 4});
+  ivf.append(rows, n);
+  out.ivf = await ivf.queryBatch(qs, nq, 10);
+  out.ivfStats = [ivf.nlist, ivf.nprobe];
+  try { m.buildIndex(ctx, dim, 'l2', 0, {}, {}); } catch (e) { out.ivfL2 = e.message; }
+  flat.destroy(); quant.destroy(); ivf.destroy(); ctx.destroy();
   console.log(JSON.stringify(out));
 })().catch((e) => { console.error(e.code, e.message); process.exit(3); });
 """
@@ -87,7 +92,7 @@ const dim = %(dim)d, n = %(n)d, nq = %(nq)d;
 @pytest.mark.gpu
 def test_node_results_equal_python_binding(tmp_path):
     need_gpu()
-    from browservec_amd import DeviceContext, FlatIndex, QuantIndex
+    from browservec_amd import DeviceContext, FlatIndex, IVFQuantIndex, QuantIndex
 
     dim, n, nq = 96, 3000, 4
     say("napi", dim, n, nq)
@@ -122,6 +127,14 @@ def test_node_results_equal_python_binding(tmp_path):
             assert [h["row"] for h in out["search"][i]] == rows[i, :cnt[i]].tolist()
             assert np.array_equal(np.float32([h["score"] for h in out["search"][i]]), scores[i, :cnt[i]])
         same(out["rerank"], quant.rerank(q[0], [h.row for h in py_approx], 10))
+        ivf = IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 16, "iters": 3, "nprobe": 4})
+        ivf.append(x, n)
+        py_ivf = ivf.query_batch(q, nq, 10)
+        for i in range(nq):
+            same(out["ivf"][i], py_ivf[i])
+        assert out["ivfStats"] == [16, 4]
+        assert out["ivfL2"] == "IVF supports metric cosine/dot only (l2 is later work)"
+        ivf.destroy()
         flat.destroy()
         quant.destroy()
     finally:
