@@ -17,7 +17,7 @@ LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libbrowservec_hip.so")
 ARCH = os.environ.get("BV_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["bv_kernels.hip", "bv_ivf.hip", "bv_api.cpp"]
+SOURCES = ["bv_kernels.hip", "bv_ivf.hip", "bv_mq.hip", "bv_api.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -130,7 +130,8 @@ struct bv_index {
     DevBuf rr_keys, rr_tickets;
     DevBuf out_rows, out_scores, out_n;
     DevBuf cand, cand_n, dense;
-    HostBuf h_rows, h_scores, h_n;
+    DevBuf mq_cand, mq_cnt, mq_tau, mq_flag;  // batched matrix-core scans
+    HostBuf h_rows, h_scores, h_n, h_flag;
 
     uint32_t nprobe_override = 0;
 
@@ -811,15 +812,10 @@ static void timing_collect(bv_index *idx) {
     idx->tev_used = 0;
 }
 
-// The device pipeline shared by every query entry point.
-//   d_q       : nq x dim device queries (original space)
-//   kprime    : candidates kept by the scan (the fetch)
-//   k_out     : results per query
-//   rerank    : re-rank the kprime candidates with f64 dotRow
-//   outputs   : device arrays [nq][k_out], [nq]
-static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
-                        const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores,
-                        uint32_t *d_n) {
+// The fused single-launch scan (one query per grid row): query transform,
+// scan, top-kprime and exact re-rank.
+static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
+                     const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
     ScanArgs a{};
     int rc = BV_OK;
     if (idx->quant && scan_prep_supported(idx->codec, idx->units, idx->P)) {
@@ -873,6 +869,154 @@ static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t k
     timing_end(idx);
     idx->last_scanned = n * nq;
     return BV_OK;
+}
+
+// ---------------------------------------------------------- batched scans
+// Query batches on an int8 index take the matrix-core path: a dense pass over
+// MQ_SAMPLE strided rows gives each query a pruning bound (its kprime-th best
+// sample key), a pass over all rows appends the keys at or above it, and the
+// best kprime per query go to the exact re-rank or straight to the output.
+// Keys are the single-query scan's keys, so results equal the same queries
+// run one at a time.  A query whose appended keys overflow their buffer (a
+// bound left loose by the sample) is re-run through the fused scan.
+constexpr uint32_t MQ_MIN_Q = 8;  // smallest batch for the matrix-core path
+
+static bool mq_eligible(const bv_index *idx, uint32_t nq, const uint32_t *d_mask) {
+    return !idx->ivf && !d_mask && idx->quant && idx->codec == C_Q8 && nq >= MQ_MIN_Q && idx->units >= 2 &&
+           (idx->units % 2) == 0 && idx->rows > 0;
+}
+
+static uint32_t mq_tiles(uint64_t n) {
+    const uint64_t t = (n + MQ_ROWS - 1) / MQ_ROWS;
+    return (uint32_t)((t + 7) & ~7ull);
+}
+
+static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
+                       uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
+    const void *qscan = nullptr;
+    uint64_t qstride = 0;
+    int rc = prepare_queries(idx, d_q, nq, &qscan, &qstride);
+    if (rc) return rc;
+    const uint64_t N = idx->rows;
+    const uint64_t S = std::min<uint64_t>(N, MQ_SAMPLE);
+    const bool one_pass = S == N;
+    // appended keys expected per query: about kprime * N / S; room for 4x that
+    uint64_t cap = one_pass ? N : std::max<uint64_t>(S, 4ull * kprime * ((N + S - 1) / S));
+    cap = std::min<uint64_t>(cap, N);
+    HIPX(idx->dev, idx->mq_cand.ensure((size_t)nq * cap * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->mq_cnt.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->mq_tau.ensure((size_t)nq * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->mq_flag.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
+
+    MqArgs m{};
+    m.codes = idx->codes.as<uint32_t>();
+    m.scales = idx->scales.as<float>();
+    m.W = idx->words_per_row;
+    m.units = idx->units;
+    m.qlev = (const unsigned char *)qscan;
+    m.qstride = qstride;
+    m.tail_off = idx->units * 48;  // 12 words per 16-code unit, then QLevelTail
+    m.nq = nq;
+    m.qblocks = (nq + MQ_QB - 1) / MQ_QB;
+    m.cand = idx->mq_cand.as<uint64_t>();
+    m.cnt = idx->mq_cnt.as<uint32_t>();
+    m.cap = cap;
+    MqSelArgs sa{};
+    sa.cand = m.cand;
+    sa.cnt = m.cnt;
+    sa.cap = cap;
+    sa.kk = kprime;
+
+    timing_begin(idx);
+    // sample pass: every key of logical rows i < S (physical row i * N/S)
+    m.n = S;
+    m.row_step = N / S;
+    m.tiles = mq_tiles(S);
+    m.tau = nullptr;
+    HIPX(idx->dev, hipMemsetD32Async((hipDeviceptr_t)idx->mq_cnt.p, (int)S, nq, idx->stream), "scratch");
+    HIPX(idx->dev, launch_mq_scan(m, idx->stream), "batched scan kernel");
+    if (!one_pass) {
+        sa.tau = idx->mq_tau.as<uint64_t>();
+        HIPX(idx->dev, launch_mq_select(sa, nq, idx->stream), "batched select kernel");
+        HIPX(idx->dev, hipMemsetAsync(idx->mq_cnt.p, 0, (size_t)nq * 4, idx->stream), "scratch");
+        m.n = N;
+        m.row_step = 1;
+        m.tiles = mq_tiles(N);
+        m.tau = idx->mq_tau.as<uint64_t>();
+        HIPX(idx->dev, launch_mq_scan(m, idx->stream), "batched scan kernel");
+        sa.tau = nullptr;
+    }
+    sa.merged = idx->merged.as<uint64_t>();
+    sa.merged_n = idx->merged_n.as<uint32_t>();
+    sa.overflow = idx->mq_flag.as<uint32_t>();
+    if (!rerank) {
+        sa.k_out = k_out;
+        sa.out_rows = d_rows;
+        sa.out_scores = d_scores;
+        sa.out_n = d_n;
+    }
+    HIPX(idx->dev, launch_mq_select(sa, nq, idx->stream), "batched select kernel");
+    if (rerank) {
+        HIPX(idx->dev, idx->rr_keys.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
+        {
+            const size_t old = idx->rr_tickets.cap;
+            HIPX(idx->dev, idx->rr_tickets.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
+            if (idx->rr_tickets.cap != old)
+                HIPX(idx->dev, hipMemsetAsync(idx->rr_tickets.p, 0, idx->rr_tickets.cap, idx->stream), "scratch");
+        }
+        RerankArgs r{};
+        r.rows = idx->raw.as<float>();
+        r.dim = idx->dim;
+        r.q = d_q;
+        r.q_stride = idx->dim;
+        r.merged = idx->merged.as<uint64_t>();
+        r.merged_n = idx->merged_n.as<uint32_t>();
+        r.kprime = kprime;
+        r.k_out = k_out;
+        r.rr_keys = idx->rr_keys.as<uint64_t>();
+        r.tickets = idx->rr_tickets.as<uint32_t>();
+        r.out_rows = d_rows;
+        r.out_scores = d_scores;
+        r.out_n = d_n;
+        HIPX(idx->dev, launch_rerank(r, nq, idx->stream), "rerank kernel");
+    }
+    timing_end(idx);
+    idx->last_scanned = (N + (one_pass ? 0 : S)) * nq;
+    // queries whose appended keys overflowed: the fused scan, one at a time
+    HIPX(idx->dev, idx->h_flag.ensure((size_t)nq * 4), "pinned buffer");
+    HIPX(idx->dev, hipMemcpyAsync(idx->h_flag.p, idx->mq_flag.p, (size_t)nq * 4, hipMemcpyDeviceToHost, idx->stream),
+         "flag download");
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "batched scan");
+    const uint32_t *flags = (const uint32_t *)idx->h_flag.p;
+    for (uint32_t i = 0; i < nq; i++) {
+        if (!flags[i]) continue;
+        rc = run_fused(idx, d_q + (size_t)i * idx->dim, 1, kprime, k_out, rerank, nullptr, 0,
+                       d_rows + (size_t)i * k_out, d_scores + (size_t)i * k_out, d_n + i);
+        if (rc) return rc;
+    }
+    return BV_OK;
+}
+
+// The device pipeline shared by every query entry point.
+//   d_q       : nq x dim device queries (original space)
+//   kprime    : candidates kept by the scan (the fetch)
+//   k_out     : results per query
+//   rerank    : re-rank the kprime candidates with f64 dotRow
+//   outputs   : device arrays [nq][k_out], [nq]
+static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
+                        const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores,
+                        uint32_t *d_n) {
+    if (mq_eligible(idx, nq, d_mask)) return run_batched(idx, d_q, nq, kprime, k_out, rerank, d_rows, d_scores, d_n);
+    return run_fused(idx, d_q, nq, kprime, k_out, rerank, d_mask, mask_bits, d_rows, d_scores, d_n);
+}
+
+// Queries per device call for query batches: the matrix-core path takes
+// large batches (its scratch is about 32 * kprime * N / MQ_SAMPLE bytes per
+// query); the fused scan's scratch is sized per query in flight.
+static uint32_t batch_chunk(const bv_index *idx, uint32_t nq) {
+    return mq_eligible(idx, nq, nullptr) ? 1024u : 64u;
 }
 
 // Host entry: upload queries (+mask), run, download.
@@ -972,7 +1116,7 @@ extern "C" int bv_index_query_batch(bv_index *idx, const float *queries, uint32_
         return BV_OK;
     }
     // chunk to bound scratch
-    const uint32_t chunk = 64;
+    const uint32_t chunk = batch_chunk(idx, nq);
     for (uint32_t s0 = 0; s0 < nq; s0 += chunk) {
         const uint32_t m = std::min(chunk, nq - s0);
         std::vector<uint32_t> r((size_t)m * kk);
@@ -1005,7 +1149,7 @@ extern "C" int bv_index_search(bv_index *idx, const float *queries, uint32_t nq,
     uint32_t fe = fetch ? (uint32_t)std::min<uint64_t>(std::max(fetch, kk), idx->rows) : 0;
     if (fe > (uint32_t)MAX_KPRIME || kk > (uint32_t)MAX_KPRIME)
         return fail(BV_E_UNSUPPORTED, "fetch %u exceeds the fused top-k limit %d", fe, MAX_KPRIME);
-    const uint32_t chunk = 64;
+    const uint32_t chunk = batch_chunk(idx, nq);
     for (uint32_t s0 = 0; s0 < nq; s0 += chunk) {
         const uint32_t m = std::min(chunk, nq - s0);
         std::vector<uint32_t> r((size_t)m * std::max(kk, 1u));

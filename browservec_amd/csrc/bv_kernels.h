@@ -186,6 +186,53 @@ hipError_t ivf_launch_gather(const uint32_t *probes, uint32_t nq, uint32_t nprob
                              hipStream_t s);
 
 // Chooses the lane layout for a codec and row size; false if unsupported.
+// Batched int8 scan on the matrix cores (bv_mq.hip).  One pass scores the
+// logical rows i < n (physical row i * row_step) against every query with
+// v_mfma_i32_32x32x32_i8 over the three int8 query levels, and either writes
+// every key densely (cand[q * cap + i]) or appends the keys at or above
+// tau[q] (counted in cnt[q]; keys past cap are dropped but still counted).
+constexpr int MQ_ROWS = 256;      // rows per workgroup tile (64 per wave)
+constexpr int MQ_QB = 64;         // queries per workgroup tile
+constexpr uint32_t MQ_SAMPLE = 16384;  // rows of the threshold sample
+struct MqArgs {
+    const uint32_t *codes;    // N x W words
+    const float *scales;      // N
+    uint32_t W;               // words per row
+    uint32_t units;           // 16-code units per row (even)
+    uint64_t n;               // logical rows in this pass
+    uint64_t row_step;        // physical row of logical row i = i * row_step
+    const unsigned char *qlev;// nq x qstride bytes: packed levels + QLevelTail
+    uint64_t qstride;
+    uint32_t tail_off;        // byte offset of QLevelTail in a query's layout
+    uint32_t nq;
+    uint32_t qblocks;         // ceil(nq / MQ_QB)
+    uint32_t tiles;           // ceil(n / MQ_ROWS) rounded up to a multiple of 8
+    const uint64_t *tau;      // [nq] append threshold (null: dense pass)
+    uint64_t *cand;           // [nq][cap]
+    uint32_t *cnt;            // [nq] appended keys (threshold pass)
+    uint64_t cap;
+};
+// Per query: the best kk keys of cand[q][0, min(cnt[q], cap)).  Outputs are
+// optional: tau = the kk-th best key (0 when there are kk or fewer), the
+// selected keys (merged, merged_n), overflow = cnt[q] > cap, and the selected
+// keys ranked into (rows, scores, n) for k_out results.
+struct MqSelArgs {
+    const uint64_t *cand;
+    const uint32_t *cnt;
+    uint64_t cap;
+    uint32_t kk;
+    uint64_t *tau;
+    uint64_t *merged;         // [nq][kk]
+    uint32_t *merged_n;
+    uint32_t *overflow;
+    uint32_t k_out;
+    uint32_t *out_rows;       // [nq][k_out]
+    float *out_scores;
+    uint32_t *out_n;
+};
+hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s);
+hipError_t launch_mq_select(const MqSelArgs &a, uint32_t nq, hipStream_t s);
+
 bool scan_supported(int codec, uint32_t units);
 hipError_t launch_scan(int codec, uint32_t units, const ScanArgs &a, uint32_t nq, hipStream_t s);
 hipError_t launch_encode(const EncodeArgs &a, hipStream_t s);

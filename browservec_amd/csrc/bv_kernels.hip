@@ -19,27 +19,12 @@
 // (higher score, then lower row), so a descending sort gives the canonical
 // (score desc, row asc) order and keys are unique per row.  Key 0 = empty.
 #include "bv_kernels.h"
+#include "bv_device.h"
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace bvk {
-
-// ------------------------------------------------------------------ keys --
-__device__ __forceinline__ uint32_t ord_f32(float s) {
-    s = s + 0.0f;  // -0 -> +0 (round-to-nearest keeps every other value)
-    uint32_t b = __float_as_uint(s);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-__device__ __forceinline__ float f32_from_ord(uint32_t o) {
-    uint32_t b = (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o;
-    return __uint_as_float(b);
-}
-__device__ __forceinline__ uint32_t ord_i32(int32_t s) { return (uint32_t)s ^ 0x80000000u; }
-__device__ __forceinline__ uint64_t make_key(uint32_t ord, uint32_t row) {
-    return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - row);
-}
-__device__ __forceinline__ uint32_t key_row(uint64_t k) { return 0xffffffffu - (uint32_t)k; }
 
 // ---------------------------------------------------------------- codecs --
 // Each codec: Unit (what one lane loads per unit), QT/QN (query registers per
@@ -149,13 +134,8 @@ template <> struct Codec<C_I8S> {
 
 template <int C> struct IsInt { static constexpr bool v = (C == C_HAM || C == C_I8S); };
 
-// Per-query constants stored after the query units (QLevelTail) and the
-// row-score finalisation.  `ord` is the order-preserving key word.
-struct QLevelTail {
-    double s[3];     // level scales (int8: already divided by 127)
-    int32_t sum[3];  // int4: sum of each level's query bytes
-    int32_t pad;
-};
+// Row-score finalisation from the per-query constants stored after the
+// query units (QLevelTail).  `ord` is the order-preserving key word.
 
 template <int C> struct Fin {
     __device__ void load(const void *, uint32_t) {}

@@ -1,0 +1,92 @@
+"""Query batches on the matrix-core int8 path against the same queries run one
+at a time through the fused single-query scan (src/index.ts:473-517: a
+batch must answer exactly as its queries would alone).  Keys are formed by
+the same f64 combine of exact int32 level dots in both paths, so rows and
+score bits must be identical, including re-ranked scores."""
+
+import numpy as np
+import pytest
+
+from oracle import oracle as o
+from tests.helpers import clustered, gaussian, need_gpu, say
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    need_gpu()
+    from browservec_amd import DeviceContext
+
+    c = DeviceContext(0)
+    yield c
+    c.destroy()
+
+
+def singles_equal(idx, qs, fetch, k):
+    rows, scores, cnt = idx.search(qs, fetch, k)
+    for i in range(qs.shape[0]):
+        r1, s1, c1 = idx.search(qs[i:i + 1], fetch, k)
+        assert cnt[i] == c1[0], i
+        assert np.array_equal(rows[i, :cnt[i]], r1[0, :c1[0]]), i
+        assert np.array_equal(scores[i, :cnt[i]].view(np.uint32), s1[0, :c1[0]].view(np.uint32)), i
+    return rows, scores, cnt
+
+
+@pytest.mark.parametrize("dim,n,nq", [(768, 40000, 70), (20, 20000, 9), (100, 3000, 64)])
+def test_batched_search_equals_singles(ctx, dim, n, nq):
+    from browservec_amd import QuantIndex
+
+    say("batched", dim, n, nq)
+    data = clustered(n, dim, 50, 0.1, seed=7 + dim)
+    idx = QuantIndex(ctx, dim, bits=8)
+    idx.append(data, n)
+    qs = data[np.arange(nq) * (n // nq)] + gaussian(nq, dim, 9, normalize=False) * 0.05
+    qs = np.stack([o.normalize(q) for q in qs]).astype(np.float32)
+    rows, scores, cnt = singles_equal(idx, qs, 100, 10)
+    # the re-ranked scores are Store.dotRow of the returned rows
+    for i in (0, nq - 1):
+        exact = o.rerank_scores(data, qs[i], rows[i, :cnt[i]])
+        assert np.array_equal(scores[i, :cnt[i]].view(np.uint32), exact.view(np.uint32))
+    batch = idx.query_batch(qs, nq, 20)
+    for i in range(nq):
+        assert batch[i] == idx.query(qs[i], 20), i
+    idx.destroy()
+
+
+def test_batched_large_fetch(ctx):
+    from browservec_amd import QuantIndex
+
+    dim, n, nq = 64, 40000, 16
+    say("batched fetch 1000")
+    data = gaussian(n, dim, 21)
+    idx = QuantIndex(ctx, dim, bits=8)
+    idx.append(data, n)
+    qs = gaussian(nq, dim, 22)
+    singles_equal(idx, qs, 1000, 10)
+    batch = idx.query_batch(qs, nq, 1000)
+    for i in (0, 7, 15):
+        assert batch[i] == idx.query(qs[i], 1000), i
+    idx.destroy()
+
+
+def test_batched_overflow_falls_back(ctx):
+    """Sampled rows (every second row here) all score low while the other
+    rows all sit next to the queries: the sample's bound admits every
+    unsampled row, the append buffer overflows, and those queries must still
+    answer exactly as alone."""
+    from browservec_amd import QuantIndex
+
+    dim, n, nq = 64, 40000, 8
+    say("batched overflow")
+    rng = np.random.default_rng(5)
+    qs = np.abs(gaussian(nq, dim, 31))  # queries in the positive orthant
+    qs /= np.linalg.norm(qs, axis=1, keepdims=True)
+    data = -np.abs(gaussian(n, dim, 32))  # even (sampled) rows: negative scores
+    odd = np.arange(1, n, 2)
+    near = np.abs(qs[odd % nq] + rng.standard_normal((odd.size, dim)).astype(np.float32) * 0.01)
+    data[odd] = near / np.linalg.norm(near, axis=1, keepdims=True)  # odd rows: scores near 1
+    idx = QuantIndex(ctx, dim, bits=8)
+    idx.append(data.astype(np.float32), n)
+    singles_equal(idx, qs.astype(np.float32), 100, 10)
+    idx.destroy()
