@@ -883,12 +883,15 @@ constexpr uint32_t MQ_MIN_Q = 8;  // smallest batch for the matrix-core path
 
 static bool mq_eligible(const bv_index *idx, uint32_t nq, const uint32_t *d_mask) {
     return !idx->ivf && !d_mask && idx->quant && idx->codec == C_Q8 && nq >= MQ_MIN_Q && idx->units >= 2 &&
-           (idx->units % 2) == 0 && idx->rows > 0;
+           (idx->units % 2) == 0 && idx->units / 2 <= MQ_MAX_STEPS && idx->rows > 0;
 }
 
-static uint32_t mq_tiles(uint64_t n) {
-    const uint64_t t = (n + MQ_ROWS - 1) / MQ_ROWS;
-    return (uint32_t)((t + 7) & ~7ull);
+// Workgroups per (XCD, query block) of the persistent batched scan: about
+// one workgroup per CU over the whole grid.
+static uint32_t mq_groups(const bv_index *idx, uint32_t qblocks) {
+    const int cus = idx->dev->prop.multiProcessorCount > 0 ? idx->dev->prop.multiProcessorCount : 256;
+    const uint32_t g = (uint32_t)cus / (8u * qblocks);
+    return g ? g : 1u;
 }
 
 static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
@@ -920,6 +923,7 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
     m.tail_off = idx->units * 48;  // 12 words per 16-code unit, then QLevelTail
     m.nq = nq;
     m.qblocks = (nq + MQ_QB - 1) / MQ_QB;
+    m.groups = mq_groups(idx, m.qblocks);
     m.cand = idx->mq_cand.as<uint64_t>();
     m.cnt = idx->mq_cnt.as<uint32_t>();
     m.cap = cap;
@@ -933,7 +937,6 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
     // sample pass: every key of logical rows i < S (physical row i * N/S)
     m.n = S;
     m.row_step = N / S;
-    m.tiles = mq_tiles(S);
     m.tau = nullptr;
     HIPX(idx->dev, hipMemsetD32Async((hipDeviceptr_t)idx->mq_cnt.p, (int)S, nq, idx->stream), "scratch");
     HIPX(idx->dev, launch_mq_scan(m, idx->stream), "batched scan kernel");
@@ -943,7 +946,6 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
         HIPX(idx->dev, hipMemsetAsync(idx->mq_cnt.p, 0, (size_t)nq * 4, idx->stream), "scratch");
         m.n = N;
         m.row_step = 1;
-        m.tiles = mq_tiles(N);
         m.tau = idx->mq_tau.as<uint64_t>();
         HIPX(idx->dev, launch_mq_scan(m, idx->stream), "batched scan kernel");
         sa.tau = nullptr;

@@ -191,8 +191,10 @@ hipError_t ivf_launch_gather(const uint32_t *probes, uint32_t nq, uint32_t nprob
 // v_mfma_i32_32x32x32_i8 over the three int8 query levels, and either writes
 // every key densely (cand[q * cap + i]) or appends the keys at or above
 // tau[q] (counted in cnt[q]; keys past cap are dropped but still counted).
-constexpr int MQ_ROWS = 256;      // rows per workgroup tile (64 per wave)
-constexpr int MQ_QB = 64;         // queries per workgroup tile
+constexpr int MQ_WAVES = 8;       // waves per workgroup (64 rows each)
+constexpr int MQ_ROWS = 512;      // rows per workgroup tile
+constexpr int MQ_QB = 32;         // queries per workgroup
+constexpr uint32_t MQ_MAX_STEPS = 32;  // 32-code steps per row (P <= 1024): levels resident in LDS
 constexpr uint32_t MQ_SAMPLE = 16384;  // rows of the threshold sample
 struct MqArgs {
     const uint32_t *codes;    // N x W words
@@ -206,7 +208,7 @@ struct MqArgs {
     uint32_t tail_off;        // byte offset of QLevelTail in a query's layout
     uint32_t nq;
     uint32_t qblocks;         // ceil(nq / MQ_QB)
-    uint32_t tiles;           // ceil(n / MQ_ROWS) rounded up to a multiple of 8
+    uint32_t groups;          // workgroups per (XCD, query block); tile stride = 8 * groups
     const uint64_t *tau;      // [nq] append threshold (null: dense pass)
     uint64_t *cand;           // [nq][cap]
     uint32_t *cnt;            // [nq] appended keys (threshold pass)

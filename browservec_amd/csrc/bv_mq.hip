@@ -28,6 +28,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
 
 // f64 combine of the three level dots, then the row scale: the arithmetic
 // of the single-query int8 scan's finalisation.
@@ -60,141 +62,233 @@ __device__ void sort_desc(uint64_t *keys, uint32_t npow) {
     }
 }
 
-}  // namespace
 
-// One workgroup = MQ_ROWS rows x MQ_QB queries; wave w takes rows
-// [64w, 64w + 64) of the tile against all MQ_QB queries as 2 x 2 blocks of
-// 32 x 32, three level accumulators each.  The K loop walks the row in
-// 32-code steps: lane l supplies 16 codes (unit 2s + l/32) of row l%32 as
-// the A operand and the same unit of query l%32's level bytes as the B
-// operand, so both operands pair the same codes.  Accumulator register r of
-// lane l holds row 8*(r/4) + 4*(l/32) + r%4, query l%32 of its block.
-__global__ __launch_bounds__(256) void mq_scan_q8(MqArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int h = lane >> 5, c = lane & 31;
-    // Dispatch is round robin over the 8 XCDs, so workgroups b, b+8, ... share
-    // an XCD.  The qblocks tiles of one row tile take consecutive slots on one
-    // XCD and read the same codes through its L2.
-    const uint32_t b = blockIdx.x, xcd = b & 7u, slot = b >> 3;
-    const uint32_t qb = slot % a.qblocks;
-    const uint64_t tile = (uint64_t)(slot / a.qblocks) * 8 + xcd;
-    const uint64_t t0 = tile * MQ_ROWS;
-    if (t0 >= a.n) return;
-    const uint64_t w0 = t0 + (uint64_t)wave * 64;
+// Per-query constants of the epilogue, in LDS: the level scales in f64
+// (exact keys) and in f32 with the level-3 bound (prefilter), and the bound
+// tau as a key and as an f32 score.
+struct MqQuery {
+    double s[3];
+    float s0f, s1f, e3;  // e3 = s2 * 127^2 * P >= |s2 * d2| for any row
+    float tau_score;     // -inf when tau is 0
+    uint64_t tau;
+};
 
-    const v4i *ap[2];
-#pragma unroll
-    for (int fr = 0; fr < 2; ++fr) {
-        uint64_t li = w0 + fr * 32 + c;
-        if (li >= a.n) li = a.n - 1;  // rows past the end load a valid row; their results are dropped
-        ap[fr] = (const v4i *)(a.codes + li * a.row_step * a.W) + h;
-    }
-    const v4i *bp[2];
-#pragma unroll
-    for (int fq = 0; fq < 2; ++fq) {
-        uint32_t q = qb * MQ_QB + fq * 32 + c;
-        if (q >= a.nq) q = a.nq - 1;
-        bp[fq] = (const v4i *)(a.qlev + (uint64_t)q * a.qstride) + h * 3;  // unit u, level l at u*3 + l
-    }
-
-    v16i acc[2][2][3];
-#pragma unroll
-    for (int fr = 0; fr < 2; ++fr)
-#pragma unroll
-        for (int fq = 0; fq < 2; ++fq)
-#pragma unroll
-            for (int l = 0; l < 3; ++l) acc[fr][fq][l] = v16i{};
-
-    const uint32_t S = a.units >> 1;
-    v4i A[2], B[2][3];
-#pragma unroll
-    for (int fr = 0; fr < 2; ++fr) A[fr] = ap[fr][0];
-#pragma unroll
-    for (int fq = 0; fq < 2; ++fq)
-#pragma unroll
-        for (int l = 0; l < 3; ++l) B[fq][l] = bp[fq][l];
-    for (uint32_t s = 0; s < S; ++s) {
-        const uint32_t sn = s + 1 < S ? s + 1 : s;  // the last step reloads its own operands
-        v4i An[2], Bn[2][3];
-#pragma unroll
-        for (int fr = 0; fr < 2; ++fr) An[fr] = ap[fr][2 * sn];
-#pragma unroll
-        for (int fq = 0; fq < 2; ++fq)
-#pragma unroll
-            for (int l = 0; l < 3; ++l) Bn[fq][l] = bp[fq][6 * sn + l];
-#pragma unroll
-        for (int fr = 0; fr < 2; ++fr)
-#pragma unroll
-            for (int fq = 0; fq < 2; ++fq)
-#pragma unroll
-                for (int l = 0; l < 3; ++l)
-                    acc[fr][fq][l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[fr], B[fq][l], acc[fr][fq][l], 0, 0, 0);
-#pragma unroll
-        for (int fr = 0; fr < 2; ++fr) A[fr] = An[fr];
-#pragma unroll
-        for (int fq = 0; fq < 2; ++fq)
-#pragma unroll
-            for (int l = 0; l < 3; ++l) B[fq][l] = Bn[fq][l];
-    }
-
-#pragma unroll
-    for (int fq = 0; fq < 2; ++fq) {
-        const uint32_t q = qb * MQ_QB + fq * 32 + c;
-        const bool qok = q < a.nq;
-        const uint32_t qq = qok ? q : a.nq - 1;
-        const QLevelTail *t = (const QLevelTail *)(a.qlev + (uint64_t)qq * a.qstride + a.tail_off);
-        const double s0 = t->s[0], s1 = t->s[1], s2 = t->s[2];
-        uint64_t *out = a.cand + (uint64_t)qq * a.cap;
-        if (!a.tau) {  // dense pass: key of logical row i at out[i]
-#pragma unroll
-            for (int fr = 0; fr < 2; ++fr)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const uint64_t li = w0 + fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (qok && li < a.n) {
-                        const uint64_t row = li * a.row_step;
-                        out[li] = q8_key(s0, s1, s2, acc[fr][fq][0][r], acc[fr][fq][1][r], acc[fr][fq][2][r],
-                                         a.scales[row], (uint32_t)row);
-                    }
-                }
-            continue;
-        }
-        const uint64_t tau = a.tau[qq];
-        uint32_t pass = 0;  // bit fr*16 + r: key at or above the bound
+// Keys of one wave's 64 rows x 32 queries from its accumulators: written
+// densely (logical row i at cand[q][i]) or appended when at or above tau[q].
+// Appending first checks an f32 upper bound of the score: the f32 sum of the
+// first two level terms, plus the level-3 bound e3 and 2^-20 of the terms'
+// magnitude (far above the f32 rounding of the sum and of the exact score),
+// times the row scale.  Only keys whose bound reaches tau_score get the exact
+// f64 combine.  sc: the scales of this wave's 64 rows (LDS).
+__device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3], uint64_t w0, uint32_t qb, int h,
+                                         int c, const MqQuery *mq, const float *sc) {
+    const bool full = w0 + 64 <= a.n;
+    const uint32_t q = qb * MQ_QB + c;
+    const bool qok = q < a.nq;
+    const uint32_t qq = qok ? q : a.nq - 1;
+    const MqQuery &Q = mq[c];
+    uint64_t *out = a.cand + (uint64_t)qq * a.cap;
+    if (!a.tau) {
 #pragma unroll
         for (int fr = 0; fr < 2; ++fr)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint64_t li = w0 + fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (qok && li < a.n) {
+                const uint32_t ri = fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const uint64_t li = w0 + ri;
+                if (qok && (full || li < a.n)) {
                     const uint64_t row = li * a.row_step;
-                    const uint64_t key = q8_key(s0, s1, s2, acc[fr][fq][0][r], acc[fr][fq][1][r],
-                                                acc[fr][fq][2][r], a.scales[row], (uint32_t)row);
-                    if (key >= tau) pass |= 1u << (fr * 16 + r);
+                    out[li] = q8_key(Q.s[0], Q.s[1], Q.s[2], acc[fr][0][r], acc[fr][1][r], acc[fr][2][r], sc[ri],
+                                     (uint32_t)row);
                 }
             }
-        // lanes c and c + 32 hold the same query: one reservation for both
-        const uint32_t mine = __popc(pass);
-        const uint32_t other = __shfl_xor(mine, 32);
-        uint32_t base = 0;
-        if (h == 0 && mine + other) base = atomicAdd(&a.cnt[qq], mine + other);
-        base = __shfl(base, c);
-        if (pass) {
-            uint64_t pos = (uint64_t)base + (h ? other : 0u);
+        return;
+    }
+    // f32 upper bounds of all 32 keys, branch-free; the lane's rows come in
+    // runs of four (r & 3), one 16-byte LDS read per run
+    uint32_t maybe = 0;
+#pragma unroll
+    for (int fr = 0; fr < 2; ++fr) {
+        float4 sv[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) sv[g] = *(const float4 *)&sc[fr * 32 + 8 * g + 4 * h];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float v4[4] = {sv[r >> 2].x, sv[r >> 2].y, sv[r >> 2].z, sv[r >> 2].w};
+            const float scale = v4[r & 3];
+            const float t0 = (float)acc[fr][0][r] * Q.s0f, t1 = (float)acc[fr][1][r] * Q.s1f;
+            const float upper = (t0 + t1) * scale + (Q.e3 + 0x1p-20f * (fabsf(t0) + fabsf(t1))) * fabsf(scale);
+            maybe |= (upper < Q.tau_score ? 0u : 1u) << (fr * 16 + r);
+        }
+    }
+    if (!qok) maybe = 0;
+    uint32_t pass = 0;  // bit fr*16 + r: key at or above the bound
+    if (__ballot(maybe != 0)) {
+#pragma unroll
+        for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t bit = 1u << (fr * 16 + r);
+                if (maybe & bit) {
+                    const uint32_t ri = fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const uint64_t li = w0 + ri;
+                    if (full || li < a.n) {
+                        const uint64_t key = q8_key(Q.s[0], Q.s[1], Q.s[2], acc[fr][0][r], acc[fr][1][r],
+                                                    acc[fr][2][r], sc[ri], (uint32_t)(li * a.row_step));
+                        if (key >= Q.tau) pass |= bit;
+                    }
+                }
+            }
+    }
+    if (!__ballot(pass != 0)) return;
+    // lanes c and c + 32 hold the same query: one reservation for both
+    const uint32_t mine = __popc(pass);
+    const uint32_t other = __shfl_xor(mine, 32);
+    uint32_t base = 0;
+    if (h == 0 && mine + other) base = atomicAdd(&a.cnt[qq], mine + other);
+    base = __shfl(base, c);
+    if (pass) {
+        uint64_t pos = (uint64_t)base + (h ? other : 0u);
+#pragma unroll
+        for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if (pass & (1u << (fr * 16 + r))) {
+                    const uint32_t ri = fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const uint64_t row = (w0 + ri) * a.row_step;
+                    if (pos < a.cap)
+                        out[pos] = q8_key(Q.s[0], Q.s[1], Q.s[2], acc[fr][0][r], acc[fr][1][r], acc[fr][2][r], sc[ri],
+                                          (uint32_t)row);
+                    ++pos;
+                }
+            }
+    }
+}
+
+}  // namespace
+
+// One workgroup = MQ_QB (32) queries, walking row tiles of MQ_ROWS (512)
+// rows with MQ_WAVES (8) waves, two per SIMD.  The queries' three int8
+// levels stay in LDS for the workgroup's lifetime (S steps x 3 levels x 1 KB,
+// 96 KB at P = 1024), laid out as MFMA B operands: block (s, l) holds, at
+// lane l's 16 bytes, unit 2s + l/32 of query l%32's level bytes.  Wave w
+// takes rows [64w, 64w + 64) of a tile as two 32-row A operands: lane l
+// supplies unit 2s + l/32 of row l%32, so both operands pair the same codes.
+// Accumulator register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4,
+// query l%32.  The codes of each wave's rows stream into a ring of D steps
+// of registers, loads running D steps ahead (into the next tile at a tile's
+// end), so the K loop needs no barrier.
+template <int S>
+__global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
+    constexpr int D = S < 8 ? S : 8;  // steps of codes in flight per wave
+    __shared__ v4i qlds[S][3][64];
+    __shared__ float srow[MQ_WAVES][64];
+    __shared__ MqQuery mq[MQ_QB];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane >> 5, c = lane & 31;
+    // Dispatch is round robin over the 8 XCDs, so workgroups b, b+8, ... share
+    // an XCD.  The qblocks workgroups of one group walk the same row tiles on
+    // one XCD and read the codes through its L2.
+    const uint32_t b = blockIdx.x, xcd = b & 7u, slot = b >> 3;
+    const uint32_t qb = slot % a.qblocks, grp = slot / a.qblocks;
+    const uint64_t tstride = 8ull * a.groups;
+    uint64_t tile = xcd + 8ull * grp;
+    if (tile * MQ_ROWS >= a.n) return;
+
+    // the block's query levels: 3S blocks of 1 KB, one wave instruction each
+    {
+        uint32_t q = qb * MQ_QB + c;
+        if (q >= a.nq) q = a.nq - 1;
+        const unsigned char *src = a.qlev + (uint64_t)q * a.qstride;
+        for (int blk = wave; blk < S * 3; blk += MQ_WAVES) {
+            const int st = blk / 3, lv = blk % 3;
+            const uint32_t u = 2 * st + h;
+            __builtin_amdgcn_global_load_lds((glb_void *)(src + ((uint64_t)u * 3 + lv) * 16),
+                                             (lds_void *)&qlds[st][lv][0], 16, 0, 0);
+        }
+    }
+    if (threadIdx.x < MQ_QB) {
+        uint32_t q = qb * MQ_QB + threadIdx.x;
+        if (q >= a.nq) q = a.nq - 1;
+        const QLevelTail *t = (const QLevelTail *)(a.qlev + (uint64_t)q * a.qstride + a.tail_off);
+        MqQuery &Q = mq[threadIdx.x];
+        Q.s[0] = t->s[0];
+        Q.s[1] = t->s[1];
+        Q.s[2] = t->s[2];
+        Q.s0f = (float)t->s[0];
+        Q.s1f = (float)t->s[1];
+        Q.e3 = (float)(fabs(t->s[2]) * 16129.0 * 16.0 * (double)a.units * 1.0000001);
+        Q.tau = a.tau ? a.tau[q] : 0ull;
+        Q.tau_score = Q.tau ? f32_from_ord((uint32_t)(Q.tau >> 32)) : -__builtin_inff();
+    }
+
+    auto row_ptrs = [&](uint64_t t, const v4i *(&ap)[2]) {
+        const uint64_t w0 = t * MQ_ROWS + (uint64_t)wave * 64;
+#pragma unroll
+        for (int fr = 0; fr < 2; ++fr) {
+            uint64_t li = w0 + fr * 32 + c;
+            if (li >= a.n) li = a.n - 1;  // rows past the end load a valid row; their results are dropped
+            ap[fr] = (const v4i *)(a.codes + li * a.row_step * a.W) + h;
+        }
+    };
+    auto row_scale = [&](uint64_t t) {
+        uint64_t li = t * MQ_ROWS + (uint64_t)wave * 64 + lane;
+        if (li >= a.n) li = a.n - 1;
+        return a.scales[li * a.row_step];
+    };
+    const v4i *ap[2];
+    row_ptrs(tile, ap);
+    v4i ring[D][2];
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+#pragma unroll
+        for (int fr = 0; fr < 2; ++fr) ring[j][fr] = ap[fr][2 * j];
+    float scale = row_scale(tile);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // query levels and constants are in LDS
+
+    for (;;) {  // row tiles
+        const uint64_t ntile = tile + tstride;
+        const bool more = ntile * MQ_ROWS < a.n;
+        const v4i *np[2];
+        row_ptrs(more ? ntile : tile, np);
+        v16i acc[2][3];
+#pragma unroll
+        for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+            for (int l = 0; l < 3; ++l) acc[fr][l] = v16i{};
+#pragma unroll
+        for (int st = 0; st < S; ++st) {
+            v4i A[2];
+#pragma unroll
+            for (int fr = 0; fr < 2; ++fr) A[fr] = ring[st % D][fr];
+            if (st + D < S) {
+#pragma unroll
+                for (int fr = 0; fr < 2; ++fr) ring[st % D][fr] = ap[fr][2 * (st + D)];
+            } else if (more) {
+#pragma unroll
+                for (int fr = 0; fr < 2; ++fr) ring[st % D][fr] = np[fr][2 * (st + D - S)];
+            }
+            v4i B[3];
+#pragma unroll
+            for (int l = 0; l < 3; ++l) B[l] = qlds[st][l][lane];
 #pragma unroll
             for (int fr = 0; fr < 2; ++fr)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    if (pass & (1u << (fr * 16 + r))) {
-                        const uint64_t li = w0 + fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                        const uint64_t row = li * a.row_step;
-                        if (pos < a.cap)
-                            out[pos] = q8_key(s0, s1, s2, acc[fr][fq][0][r], acc[fr][fq][1][r], acc[fr][fq][2][r],
-                                              a.scales[row], (uint32_t)row);
-                        ++pos;
-                    }
-                }
+                for (int l = 0; l < 3; ++l)
+                    acc[fr][l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[fr], B[l], acc[fr][l], 0, 0, 0);
         }
+        // this wave's 64 row scales, through wave-private LDS
+        srow[wave][lane] = scale;
+        if (more) scale = row_scale(ntile);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        epilogue(a, acc, tile * MQ_ROWS + (uint64_t)wave * 64, qb, h, c, mq, srow[wave]);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (!more) break;
+        ap[0] = np[0];
+        ap[1] = np[1];
+        tile = ntile;
     }
 }
 
@@ -295,12 +389,21 @@ __global__ __launch_bounds__(256) void mq_select(MqSelArgs a) {
 
 hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s) {
     if (a.n == 0 || a.nq == 0) return hipSuccess;
-    if ((a.units & 1u) || a.units == 0 || a.qblocks == 0 || (a.tiles & 7u) ||
-        (uint64_t)a.tiles * MQ_ROWS < a.n || (uint64_t)a.qblocks * MQ_QB < a.nq)
+    const uint32_t steps = a.units >> 1;
+    if ((a.units & 1u) || steps == 0 || steps > MQ_MAX_STEPS || (steps & (steps - 1)) || a.qblocks == 0 ||
+        a.groups == 0 || (uint64_t)a.qblocks * MQ_QB < a.nq)
         return hipErrorInvalidValue;
-    const uint64_t blocks = (uint64_t)a.tiles * a.qblocks;
+    const uint64_t blocks = 8ull * a.groups * a.qblocks;
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(mq_scan_q8, dim3((uint32_t)blocks), dim3(256), 0, s, a);
+    const dim3 g((uint32_t)blocks), wg(MQ_WAVES * 64);
+    switch (steps) {
+    case 1: hipLaunchKernelGGL(mq_scan_q8<1>, g, wg, 0, s, a); break;
+    case 2: hipLaunchKernelGGL(mq_scan_q8<2>, g, wg, 0, s, a); break;
+    case 4: hipLaunchKernelGGL(mq_scan_q8<4>, g, wg, 0, s, a); break;
+    case 8: hipLaunchKernelGGL(mq_scan_q8<8>, g, wg, 0, s, a); break;
+    case 16: hipLaunchKernelGGL(mq_scan_q8<16>, g, wg, 0, s, a); break;
+    default: hipLaunchKernelGGL(mq_scan_q8<32>, g, wg, 0, s, a); break;
+    }
     return hipGetLastError();
 }
 
