@@ -174,12 +174,17 @@ __device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3
 // takes rows [64w, 64w + 64) of a tile as two 32-row A operands: lane l
 // supplies unit 2s + l/32 of row l%32, so both operands pair the same codes.
 // Accumulator register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4,
-// query l%32.  The codes of each wave's rows stream into a ring of D steps
-// of registers, loads running D steps ahead (into the next tile at a tile's
-// end), so the K loop needs no barrier.
+// query l%32.  The codes of each wave's rows stream into two register
+// groups of G steps, loads running one group ahead (into the next tile at a
+// tile's end), so the K loop needs no barrier.
 template <int S>
 __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
-    constexpr int D = S < 8 ? S : 8;  // steps of codes in flight per wave
+    // Codes stream in groups of G steps: a group's loads are issued back to
+    // back one group ahead, so the G loads that read the same 128-byte line of
+    // a row (steps 4k .. 4k + 3 read line k) reach L1 together and share one
+    // fill.  Issued a step at a time, the lines of the 8 waves (64 KB per
+    // four steps) overflow the 32 KB L1 and are fetched up to four times.
+    constexpr int G = S < 4 ? S : 4;
     __shared__ v4i qlds[S][3][64];
     __shared__ float srow[MQ_WAVES][64];
     __shared__ MqQuery mq[MQ_QB];
@@ -237,11 +242,11 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
     };
     const v4i *ap[2];
     row_ptrs(tile, ap);
-    v4i ring[D][2];
+    v4i ring[2][G][2];  // [group parity][step in group][row half]
 #pragma unroll
-    for (int j = 0; j < D; ++j)
+    for (int j = 0; j < G; ++j)
 #pragma unroll
-        for (int fr = 0; fr < 2; ++fr) ring[j][fr] = ap[fr][2 * j];
+        for (int fr = 0; fr < 2; ++fr) ring[0][j][fr] = ap[fr][2 * j];
     float scale = row_scale(tile);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // query levels and constants are in LDS
@@ -258,16 +263,20 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
             for (int l = 0; l < 3; ++l) acc[fr][l] = v16i{};
 #pragma unroll
         for (int st = 0; st < S; ++st) {
+            const int gp = (st / G) & 1, j = st % G;
+            if (j == 0) {  // the next group: this tile's, or the next tile's first
+                const int ns = st + G;
+#pragma unroll
+                for (int jj = 0; jj < G; ++jj)
+#pragma unroll
+                    for (int fr = 0; fr < 2; ++fr) {
+                        if (ns < S) ring[gp ^ 1][jj][fr] = ap[fr][2 * (ns + jj)];
+                        else if (more) ring[gp ^ 1][jj][fr] = np[fr][2 * (ns - S + jj)];
+                    }
+            }
             v4i A[2];
 #pragma unroll
-            for (int fr = 0; fr < 2; ++fr) A[fr] = ring[st % D][fr];
-            if (st + D < S) {
-#pragma unroll
-                for (int fr = 0; fr < 2; ++fr) ring[st % D][fr] = ap[fr][2 * (st + D)];
-            } else if (more) {
-#pragma unroll
-                for (int fr = 0; fr < 2; ++fr) ring[st % D][fr] = np[fr][2 * (st + D - S)];
-            }
+            for (int fr = 0; fr < 2; ++fr) A[fr] = ring[gp][j][fr];
             v4i B[3];
 #pragma unroll
             for (int l = 0; l < 3; ++l) B[l] = qlds[st][l][lane];
@@ -276,6 +285,15 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
 #pragma unroll
                 for (int l = 0; l < 3; ++l)
                     acc[fr][l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[fr], B[l], acc[fr][l], 0, 0, 0);
+            // keep each step's loads in its step: the scheduler would otherwise
+            // sink the ring's loads next to their use and expose their latency
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr ((S / G) & 1) {  // one group per row: the next tile's first group is in half 1
+#pragma unroll
+            for (int j = 0; j < G; ++j)
+#pragma unroll
+                for (int fr = 0; fr < 2; ++fr) ring[0][j][fr] = ring[1][j][fr];
         }
         // this wave's 64 row scales, through wave-private LDS
         srow[wave][lane] = scale;
