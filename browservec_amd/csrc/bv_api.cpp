@@ -961,14 +961,7 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
     }
     HIPX(idx->dev, launch_mq_select(sa, nq, idx->stream), "batched select kernel");
     if (rerank) {
-        HIPX(idx->dev, idx->rr_keys.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
-        {
-            const size_t old = idx->rr_tickets.cap;
-            HIPX(idx->dev, idx->rr_tickets.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
-            if (idx->rr_tickets.cap != old)
-                HIPX(idx->dev, hipMemsetAsync(idx->rr_tickets.p, 0, idx->rr_tickets.cap, idx->stream), "scratch");
-        }
-        RerankArgs r{};
+        MqRerankArgs r{};
         r.rows = idx->raw.as<float>();
         r.dim = idx->dim;
         r.q = d_q;
@@ -977,12 +970,10 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
         r.merged_n = idx->merged_n.as<uint32_t>();
         r.kprime = kprime;
         r.k_out = k_out;
-        r.rr_keys = idx->rr_keys.as<uint64_t>();
-        r.tickets = idx->rr_tickets.as<uint32_t>();
         r.out_rows = d_rows;
         r.out_scores = d_scores;
         r.out_n = d_n;
-        HIPX(idx->dev, launch_rerank(r, nq, idx->stream), "rerank kernel");
+        HIPX(idx->dev, launch_mq_rerank(r, nq, idx->stream), "rerank kernel");
     }
     timing_end(idx);
     idx->last_scanned = (N + (one_pass ? 0 : S)) * nq;

@@ -232,7 +232,23 @@ struct MqSelArgs {
     float *out_scores;
     uint32_t *out_n;
 };
+// Exact re-rank of merged[q][0, merged_n[q]) against the stored fp32 rows,
+// then the top k_out (one workgroup per query).
+struct MqRerankArgs {
+    const float *rows;        // N x dim
+    uint32_t dim;
+    const float *q;           // queries, q_stride floats apart
+    uint64_t q_stride;
+    const uint64_t *merged;   // [nq][kprime] scan keys
+    const uint32_t *merged_n;
+    uint32_t kprime;
+    uint32_t k_out;
+    uint32_t *out_rows;       // [nq][k_out]
+    float *out_scores;
+    uint32_t *out_n;
+};
 hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s);
+hipError_t launch_mq_rerank(const MqRerankArgs &a, uint32_t nq, hipStream_t s);
 hipError_t launch_mq_select(const MqSelArgs &a, uint32_t nq, hipStream_t s);
 
 bool scan_supported(int codec, uint32_t units);

@@ -9,7 +9,8 @@
 //                dispatches + score buffers for query batches
 //                (src/engine/wgsl/distanceQ8.ts:56-82, src/index/quant.ts:178-245,
 //                src/index.ts:473-517).
-//   mq_select    exact 64-bit radix select of each query's best kk keys.
+//   mq_select    exact selection of each query's best kk keys.
+//   mq_rerank    exact f64 re-rank of the selected candidates, 16 per wave.
 //
 // A batch runs as: a dense pass over a strided sample of the rows, whose
 // kk-th best key per query is a valid pruning bound (it is the key of a real
@@ -310,99 +311,193 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
     }
 }
 
-// One workgroup per query.  The kk-th best key is found digit by digit
-// from the top (8 passes of 8 bits over the keys, a 256-bin histogram of
-// the keys that match the digits found so far); keys are unique, so exactly
-// kk keys are at or above it.
-__global__ __launch_bounds__(256) void mq_select(MqSelArgs a) {
-    __shared__ uint32_t hist[256];
-    __shared__ uint64_t sel[MAX_KPRIME];
-    __shared__ uint32_t s_digit, s_rem, s_cnt;
+// One workgroup per query.  The kk-th best key is found by binning the
+// keys over their actual range (2048 bins of a power-of-two width, so keys
+// concentrated in a few score octaves still spread over many bins) and
+// narrowing into the bin that holds it until the keys at or above that
+// bin's lower edge fit SEL_CAP; those are gathered and sorted.  Keys are
+// unique, so exactly kk keys are at or above the kk-th.
+constexpr int SEL_THREADS = 1024;
+constexpr int SEL_BINS = 2048;
+constexpr int SEL_CAP = 4096;
+
+__global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
+    __shared__ uint32_t hist[SEL_BINS];
+    __shared__ uint64_t sel[SEL_CAP];
+    __shared__ uint64_t red[2][SEL_THREADS / 64];
+    __shared__ uint32_t s_bin, s_excl, s_cnt;
     const uint32_t q = blockIdx.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const uint32_t total = a.cnt[q];
     const uint32_t n = (uint64_t)total < a.cap ? total : (uint32_t)a.cap;
     const uint64_t *keys = a.cand + (uint64_t)q * a.cap;
     const uint32_t kk = a.kk < n ? a.kk : n;
-    uint64_t T = 0;
+    uint64_t G = 0;  // keys >= G are gathered
     if (n > kk) {
-        uint64_t prefix = 0;
-        uint32_t rem = kk;  // rank of the wanted key from the top within the matching keys
-        for (int shift = 56; shift >= 0; shift -= 8) {
-            hist[tid] = 0;
+        uint64_t lo = ~0ull, hi = 0;
+        for (uint32_t i = tid; i < n; i += SEL_THREADS) {
+            const uint64_t k = keys[i];
+            lo = k < lo ? k : lo;
+            hi = k > hi ? k : hi;
+        }
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint64_t l2 = __shfl_xor(lo, o), h2 = __shfl_xor(hi, o);
+            lo = l2 < lo ? l2 : lo;
+            hi = h2 > hi ? h2 : hi;
+        }
+        if (lane == 0) {
+            red[0][wave] = lo;
+            red[1][wave] = hi;
+        }
+        __syncthreads();
+        lo = red[0][0];
+        hi = red[1][0];
+        for (int w = 1; w < SEL_THREADS / 64; ++w) {
+            lo = red[0][w] < lo ? red[0][w] : lo;
+            hi = red[1][w] > hi ? red[1][w] : hi;
+        }
+        uint32_t above = 0, rem = kk;  // keys above [lo, hi]; rank of the kk-th within [lo, hi]
+        for (;;) {
+            const uint64_t span = hi - lo;
+            const int shift = (span >> 11) ? 64 - __clzll((long long)(span >> 11)) : 0;  // (span >> shift) < 2048
+            for (uint32_t i = tid; i < SEL_BINS; i += SEL_THREADS) hist[i] = 0;
             __syncthreads();
-            const uint64_t hi_mask = shift == 56 ? 0ull : (~0ull << (shift + 8));
-            for (uint32_t i = tid; i < n; i += 256) {
+            for (uint32_t i = tid; i < n; i += SEL_THREADS) {
                 const uint64_t k = keys[i];
-                if ((k & hi_mask) == prefix) atomicAdd(&hist[(uint32_t)(k >> shift) & 255u], 1u);
+                if (k >= lo && k <= hi) atomicAdd(&hist[(uint32_t)((k - lo) >> shift)], 1u);
             }
             __syncthreads();
             if (wave == 0) {
-                // lane l holds digits 255-4l .. 252-4l; inclusive scan from the top
-                uint32_t c4[4], loc = 0;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    c4[j] = hist[255 - (4 * lane + j)];
-                    loc += c4[j];
-                }
+                // lane l holds bins 2047 - 32l - j (j < 32): counts from the top
+                uint32_t loc = 0;
+                for (int j = 0; j < 32; ++j) loc += hist[SEL_BINS - 1 - (32 * lane + j)];
                 uint32_t inc = loc;
 #pragma unroll
-                for (int off = 1; off < 64; off <<= 1) {
-                    const uint32_t v = __shfl_up(inc, off);
-                    if (lane >= off) inc += v;
+                for (int o = 1; o < 64; o <<= 1) {
+                    const uint32_t v = __shfl_up(inc, o);
+                    if (lane >= o) inc += v;
                 }
                 const uint32_t exc = inc - loc;
                 const uint64_t bal = __ballot(exc < rem && rem <= inc);
                 if (lane == __ffsll((unsigned long long)bal) - 1) {
-                    uint32_t accum = exc;
-                    for (int j = 0; j < 4; ++j) {
-                        if (accum + c4[j] >= rem) {
-                            s_digit = 255u - (uint32_t)(4 * lane + j);
-                            s_rem = rem - accum;
+                    uint32_t acc = exc;
+                    for (int j = 0; j < 32; ++j) {
+                        const uint32_t bin = SEL_BINS - 1 - (32 * lane + j);
+                        const uint32_t cb = hist[bin];
+                        if (acc + cb >= rem) {
+                            s_bin = bin;
+                            s_excl = acc;
+                            s_cnt = cb;
                             break;
                         }
-                        accum += c4[j];
+                        acc += cb;
                     }
                 }
             }
             __syncthreads();
-            prefix |= (uint64_t)s_digit << shift;
-            rem = s_rem;
+            const uint32_t bin = s_bin, excl = s_excl, cb = s_cnt;
             __syncthreads();
+            G = lo + ((uint64_t)bin << shift);
+            if (above + excl + cb <= (uint32_t)SEL_CAP || shift == 0) break;
+            above += excl;
+            rem -= excl;
+            lo = G;
+            const uint64_t top = G + ((1ull << shift) - 1);
+            hi = top < hi ? top : hi;
         }
-        T = prefix;
     }
     if (tid == 0) s_cnt = 0;
     __syncthreads();
-    for (uint32_t i = tid; i < n; i += 256) {
+    for (uint32_t i = tid; i < n; i += SEL_THREADS) {
         const uint64_t k = keys[i];
-        if (k >= T && k != 0) {
+        if (k >= G && k != 0) {
             const uint32_t p = atomicAdd(&s_cnt, 1u);
-            if (p < (uint32_t)MAX_KPRIME) sel[p] = k;
+            if (p < (uint32_t)SEL_CAP) sel[p] = k;
         }
     }
     __syncthreads();
-    const uint32_t m = s_cnt < kk ? s_cnt : kk;
+    const uint32_t got = s_cnt < (uint32_t)SEL_CAP ? s_cnt : (uint32_t)SEL_CAP;
+    uint32_t npow = 2;
+    while (npow < got) npow <<= 1;
+    for (uint32_t i = got + tid; i < npow; i += SEL_THREADS) sel[i] = 0;
+    __syncthreads();
+    sort_desc(sel, npow);
+    const uint32_t m = got < kk ? got : kk;
     if (tid == 0) {
-        if (a.tau) a.tau[q] = n > kk ? T : 0ull;
+        if (a.tau) a.tau[q] = n > kk ? sel[kk - 1] : 0ull;
         if (a.merged_n) a.merged_n[q] = m;
         if (a.overflow) a.overflow[q] = (uint64_t)total > a.cap ? 1u : 0u;
     }
     if (a.merged)
-        for (uint32_t i = tid; i < m; i += 256) a.merged[(uint64_t)q * a.kk + i] = sel[i];
+        for (uint32_t i = tid; i < m; i += SEL_THREADS) a.merged[(uint64_t)q * a.kk + i] = sel[i];
     if (a.out_rows) {
-        uint32_t npow = 2;
-        while (npow < m) npow <<= 1;
-        for (uint32_t i = m + tid; i < npow; i += 256) sel[i] = 0;
-        __syncthreads();
-        sort_desc(sel, npow);
         const uint32_t ko = m < a.k_out ? m : a.k_out;
-        for (uint32_t i = tid; i < ko; i += 256) {
+        for (uint32_t i = tid; i < ko; i += SEL_THREADS) {
             a.out_rows[(uint64_t)q * a.k_out + i] = key_row(sel[i]);
             a.out_scores[(uint64_t)q * a.k_out + i] = f32_from_ord((uint32_t)(sel[i] >> 32));
         }
         if (tid == 0) a.out_n[q] = ko;
     }
+}
+
+// Exact re-rank of each query's selected candidates (Store.dotRow,
+// src/store/store.ts:114-130) and the final top-k_out, one workgroup per
+// query.  Lane 4c + m of a wave runs accumulator m of candidate c: the f64
+// sum over elements 4j + m in order (each f32 x f32 product is exact in f64,
+// so fma adds it with the reference's single rounding); lanes 4c .. 4c + 3
+// then combine as ((a0 + a1) + a2) + a3 and add the tail elements in order.
+// Sixteen candidates per wave run at once.
+constexpr int RR_THREADS = 256;
+__global__ __launch_bounds__(RR_THREADS) void mq_rerank(MqRerankArgs a) {
+    extern __shared__ float qv[];  // the query, dim floats
+    __shared__ uint64_t ek[MAX_KPRIME];
+    const uint32_t q = blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const uint32_t dim = a.dim, vec = dim & ~3u;
+    const float *qs = a.q + (uint64_t)q * a.q_stride;
+    for (uint32_t i = tid; i < dim; i += RR_THREADS) qv[i] = qs[i];
+    __syncthreads();
+    const uint32_t m = a.merged_n[q];
+    const uint64_t *mk = a.merged + (uint64_t)q * a.kprime;
+    const int ci = lane >> 2, ai = lane & 3;
+    for (uint32_t c0 = (uint32_t)wave * 16; c0 < m; c0 += (RR_THREADS / 64) * 16) {
+        const uint32_t cand = c0 + ci;
+        const bool have = cand < m;
+        const uint32_t row = have ? key_row(mk[cand]) : 0u;
+        const float *x = a.rows + (uint64_t)row * dim;
+        double acc = 0.0;
+        uint32_t j = ai;
+        for (; j + 28 < vec; j += 32) {
+            float xv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) xv[u] = x[j + 4 * u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = fma((double)xv[u], (double)qv[j + 4 * u], acc);
+        }
+        for (; j < vec; j += 4) acc = fma((double)x[j], (double)qv[j], acc);
+        const double a1 = __shfl_down(acc, 1), a2 = __shfl_down(acc, 2), a3 = __shfl_down(acc, 3);
+        if (have && ai == 0) {
+            double sum = acc + a1;
+            sum = sum + a2;
+            sum = sum + a3;
+            for (uint32_t i = vec; i < dim; ++i) sum = fma((double)x[i], (double)qv[i], sum);
+            ek[cand] = make_key(ord_f32((float)sum), row);
+        }
+    }
+    __syncthreads();
+    // rank: key i goes to slot #{keys greater than it} (keys are unique)
+    const uint32_t ko = m < a.k_out ? m : a.k_out;
+    for (uint32_t i = tid; i < m; i += RR_THREADS) {
+        const uint64_t ki = ek[i];
+        uint32_t r = 0;
+        for (uint32_t j2 = 0; j2 < m; ++j2) r += ek[j2] > ki ? 1u : 0u;
+        if (r < ko) {
+            a.out_rows[(uint64_t)q * a.k_out + r] = key_row(ki);
+            a.out_scores[(uint64_t)q * a.k_out + r] = f32_from_ord((uint32_t)(ki >> 32));
+        }
+    }
+    if (tid == 0) a.out_n[q] = ko;
 }
 
 hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s) {
@@ -428,7 +523,15 @@ hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s) {
 hipError_t launch_mq_select(const MqSelArgs &a, uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
     if (a.kk == 0 || a.kk > (uint32_t)MAX_KPRIME) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(mq_select, dim3(nq), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(mq_select, dim3(nq), dim3(SEL_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_mq_rerank(const MqRerankArgs &a, uint32_t nq, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    if (a.kprime == 0 || a.kprime > (uint32_t)MAX_KPRIME || a.dim == 0 || (size_t)a.dim * 4 > 96 * 1024)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mq_rerank, dim3(nq), dim3(RR_THREADS), (size_t)a.dim * 4, s, a);
     return hipGetLastError();
 }
 
