@@ -882,8 +882,39 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
 constexpr uint32_t MQ_MIN_Q = 8;  // smallest batch for the matrix-core path
 
 static bool mq_eligible(const bv_index *idx, uint32_t nq, const uint32_t *d_mask) {
-    return !idx->ivf && !d_mask && idx->quant && idx->codec == C_Q8 && nq >= MQ_MIN_Q && idx->units >= 2 &&
-           (idx->units % 2) == 0 && idx->units / 2 <= MQ_MAX_STEPS && idx->rows > 0;
+    const uint32_t u16 = idx->P / 16;  // 16-code units per row
+    return !idx->ivf && !d_mask && idx->quant && (idx->codec == C_Q8 || idx->codec == C_Q4) && nq >= MQ_MIN_Q &&
+           u16 >= 2 && (u16 % 2) == 0 && u16 / 2 <= MQ_MAX_STEPS && idx->rows > 0;
+}
+
+// Rotated queries split into three int8 levels in the 16-code unit layout
+// the batched scan reads (int4 indexes: levels without the 1/127 scale).
+static int prepare_levels16(bv_index *idx, const float *d_q, uint32_t nq, const unsigned char **qlev,
+                            uint64_t *qstride) {
+    const uint32_t P = idx->P;
+    const int layout = idx->codec == C_Q4 ? C_Q4M : C_Q8;
+    const size_t st = level_stride(layout, P);
+    HIPX(idx->dev, idx->qrot.ensure((size_t)nq * P * 4, 0, idx->stream), "query buffer");
+    HIPX(idx->dev, idx->qscan.ensure((size_t)nq * st, 0, idx->stream), "query buffer");
+    EncodeArgs e{};
+    e.src = d_q;
+    e.rows = nq;
+    e.dim = idx->dim;
+    e.P = P;
+    e.signs = idx->signs.as<float>();
+    e.rounds = idx->d.rounds;
+    e.rotated = idx->qrot.as<float>();
+    HIPX(idx->dev, launch_encode(e, idx->stream), "query rotate kernel");
+    LevelArgs la{};
+    la.qrot = idx->qrot.as<float>();
+    la.P = P;
+    la.codec = layout;
+    la.out = idx->qscan.as<unsigned char>();
+    la.stride = st;
+    HIPX(idx->dev, launch_levels(la, nq, idx->stream), "query levels kernel");
+    *qlev = idx->qscan.as<unsigned char>();
+    *qstride = st;
+    return BV_OK;
 }
 
 // Workgroups per (XCD, query block) of the persistent batched scan: about
@@ -896,9 +927,9 @@ static uint32_t mq_groups(const bv_index *idx, uint32_t qblocks) {
 
 static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                        uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
-    const void *qscan = nullptr;
+    const unsigned char *qscan = nullptr;
     uint64_t qstride = 0;
-    int rc = prepare_queries(idx, d_q, nq, &qscan, &qstride);
+    int rc = prepare_levels16(idx, d_q, nq, &qscan, &qstride);
     if (rc) return rc;
     const uint64_t N = idx->rows;
     const uint64_t S = std::min<uint64_t>(N, MQ_SAMPLE);
@@ -917,10 +948,12 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
     m.codes = idx->codes.as<uint32_t>();
     m.scales = idx->scales.as<float>();
     m.W = idx->words_per_row;
-    m.units = idx->units;
-    m.qlev = (const unsigned char *)qscan;
+    m.units = idx->P / 16;
+    m.bits = idx->codec == C_Q4 ? 4 : 8;
+    m.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
+    m.qlev = qscan;
     m.qstride = qstride;
-    m.tail_off = idx->units * 48;  // 12 words per 16-code unit, then QLevelTail
+    m.tail_off = m.units * 48;  // 12 words per 16-code unit, then QLevelTail
     m.nq = nq;
     m.qblocks = (nq + MQ_QB - 1) / MQ_QB;
     m.groups = mq_groups(idx, m.qblocks);

@@ -18,7 +18,10 @@ enum CodecId : int {
     C_I8S = 6,      // int8 codes x int8 query         (16-byte units)
     C_F32DOT_S = 7, // fp32 rows, dim % 4 != 0         (4-byte units = 1 float)
     C_F32L2_S = 8,
-    C_COUNT = 9
+    C_COUNT = 9,
+    // query-level layout only (not a scan codec): int4 levels (no 1/127 scale)
+    // in the int8 16-code unit layout, for the batched matrix-core scan
+    C_Q4M = 16
 };
 
 constexpr int SCAN_WG = 256;      // 4 waves
@@ -200,10 +203,12 @@ struct MqArgs {
     const uint32_t *codes;    // N x W words
     const float *scales;      // N
     uint32_t W;               // words per row
-    uint32_t units;           // 16-code units per row (even)
+    uint32_t units;           // 16-code units per row (even), P / 16
     uint64_t n;               // logical rows in this pass
     uint64_t row_step;        // physical row of logical row i = i * row_step
-    const unsigned char *qlev;// nq x qstride bytes: packed levels + QLevelTail
+    int bits;                 // 8: int8 codes; 4: int4 codes (nibble n carried as n ^ 8)
+    float scale_mul;          // row scale multiplier (int4: f32(1/7))
+    const unsigned char *qlev;// nq x qstride bytes: packed levels (16-code units) + QLevelTail
     uint64_t qstride;
     uint32_t tail_off;        // byte offset of QLevelTail in a query's layout
     uint32_t nq;

@@ -845,7 +845,7 @@ __device__ void levels_wave(const float (&x)[E], uint32_t P, int codec, signed c
     uint32_t *w = (uint32_t *)out;
     const unsigned char *lb = (const unsigned char *)lv;
     uint32_t qwords;
-    if (codec == C_Q8) {
+    if (codec == C_Q8 || codec == C_Q4M) {
         const uint32_t units = P / 16;
         qwords = units * 12;
         for (uint32_t i = lane; i < qwords; i += 64) {
@@ -894,7 +894,8 @@ __global__ __launch_bounds__(64) void query_levels(LevelArgs a) {
 // Bytes of the scan's per-query layout for codec C at padded dimension P.
 __host__ __device__ inline size_t query_layout_bytes(int codec, uint32_t P) {
     switch (codec) {
-    case C_Q8: return ((size_t)P / 16 * 12 * 4 + sizeof(QLevelTail) + 63) & ~(size_t)63;
+    case C_Q8:
+    case C_Q4M: return ((size_t)P / 16 * 12 * 4 + sizeof(QLevelTail) + 63) & ~(size_t)63;
     case C_Q4: return ((size_t)P / 32 * 24 * 4 + sizeof(QLevelTail) + 63) & ~(size_t)63;
     case C_Q1A: return (size_t)P * 4;
     case C_HAM: return ((size_t)P / 32 * 4 + 15) & ~(size_t)15;
@@ -1184,6 +1185,38 @@ __device__ uint64_t exact_key_wave(const float *src, const float *qs, uint32_t d
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // stage is free again
     return uniform_u64(key);
+}
+
+// Store.dotRow of sixteen rows at once, four lanes per row: lane 4c + m
+// sums the exact products of elements 4j + m of row c in order (an exact
+// f32 x f32 product added by fma rounds like the reference's `acc += x*y`),
+// and lane 4c combines the four as ((a0 + a1) + a2) + a3 and adds the tail
+// elements in order.  x: this lane's row; every lane of the wave calls it.
+// Returns the (score, row) key in lanes 4c.
+__device__ __forceinline__ uint64_t exact_key_lanes4(const float *x, const float *qs, uint32_t dim, uint32_t row,
+                                                     int lane) {
+    const uint32_t vec = dim & ~3u;
+    const int m = lane & 3;
+    double acc = 0.0;
+    uint32_t j = m;
+    for (; j + 28 < vec; j += 32) {
+        float xv[8], qv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            xv[u] = x[j + 4 * u];
+            qv[u] = qs[j + 4 * u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fma((double)xv[u], (double)qv[u], acc);
+    }
+    for (; j < vec; j += 4) acc = fma((double)x[j], (double)qs[j], acc);
+    const double a1 = __shfl_down(acc, 1), a2 = __shfl_down(acc, 2), a3 = __shfl_down(acc, 3);
+    double sum = acc + a1;
+    sum = sum + a2;
+    sum = sum + a3;
+    if (m == 0)
+        for (uint32_t i = vec; i < dim; ++i) sum = fma((double)x[i], (double)qs[i], sum);
+    return make_key(ord_f32((float)sum), row);
 }
 
 // ------------------------------------------------------------ scan + top-k --
@@ -1672,13 +1705,14 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         base = __builtin_amdgcn_readfirstlane(base);
         uint64_t *ck = a.cand_keys + 2 * ((uint64_t)qi * a.cand_cap + grp * region + base);
         if (a.rr_src) {
-            double *stage = (double *)(wk + wcap);
             const float *rq = a.rr_q + (uint64_t)qi * a.rr_q_stride;
-            for (uint32_t j = 0; j < wc; ++j) {
-                const uint64_t k = wk[j];
-                const uint32_t row = key_row(k);
-                const uint64_t ek = exact_key_wave(a.rr_src + (uint64_t)row * a.rr_dim, rq, a.rr_dim, row, stage, lane);
-                if (lane == 0) {
+            for (uint32_t j0 = 0; j0 < wc; j0 += 16) {  // sixteen candidates per pass
+                const uint32_t j = j0 + (uint32_t)(lane >> 2);
+                const bool have = j < wc;
+                const uint64_t k = have ? wk[j] : 0ull;
+                const uint32_t row = have ? key_row(k) : 0u;  // absent candidates read row 0
+                const uint64_t ek = exact_key_lanes4(a.rr_src + (uint64_t)row * a.rr_dim, rq, a.rr_dim, row, lane);
+                if (have && (lane & 3) == 0) {
                     store_shared(&ck[2 * j], k);
                     store_shared(&ck[2 * j + 1], ek);
                 }

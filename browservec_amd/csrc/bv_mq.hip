@@ -1,14 +1,14 @@
 // Batched int8 scans on the gfx950 matrix cores.
 //
-//   mq_scan_q8   rows x queries x three int8 query levels on
+//   mq_scan      int8 / int4 rows x queries x three int8 query levels on
 //                v_mfma_i32_32x32x32_i8.  Every (row, query, level) dot is
 //                an exact int32, combined per (row, query) in f64 exactly as
 //                the single-query scan combines its three dots, so a batch
 //                produces the same keys as the same queries scanned one at a
-//                time.  Replaces the reference's per-query distanceQ8
-//                dispatches + score buffers for query batches
-//                (src/engine/wgsl/distanceQ8.ts:56-82, src/index/quant.ts:178-245,
-//                src/index.ts:473-517).
+//                time.  Replaces the reference's per-query distanceQ8 /
+//                distanceQ4 dispatches + score buffers for query batches
+//                (src/engine/wgsl/distanceQ8.ts:56-82, distanceQ4.ts:44-78,
+//                src/index/quant.ts:178-245, src/index.ts:473-517).
 //   mq_select    exact selection of each query's best kk keys.
 //   mq_rerank    exact f64 re-rank of the selected candidates, 16 per wave.
 //
@@ -23,6 +23,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace bvk {
 
 namespace {
@@ -33,12 +35,27 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
 
 // f64 combine of the three level dots, then the row scale: the arithmetic
-// of the single-query int8 scan's finalisation.
-__device__ __forceinline__ uint64_t q8_key(double s0, double s1, double s2, int32_t d0, int32_t d1, int32_t d2,
-                                           float scale, uint32_t row) {
+// of the single-query int8 / int4 scans' finalisation (d already corrected
+// for the int4 nibble offset).
+__device__ __forceinline__ uint64_t q_key(double s0, double s1, double s2, int32_t d0, int32_t d1, int32_t d2,
+                                          float scale, uint32_t row) {
     const double v = fma(s2, (double)d2, fma(s1, (double)d1, s0 * (double)d0));
     const float sc = (float)(v * (double)scale);
     return make_key(ord_f32(sc), row);
+}
+
+// 16 int4 codes (two words, nibble j of word g = code 8g + j) as 16 bytes
+// n ^ 8 in code order: the even and odd nibbles, interleaved by byte perms.
+__device__ __forceinline__ v4i unpack_q4(uint2 w) {
+    const uint32_t x0 = w.x ^ 0x88888888u, x1 = w.y ^ 0x88888888u;
+    const uint32_t e0 = x0 & 0x0f0f0f0fu, o0 = (x0 >> 4) & 0x0f0f0f0fu;
+    const uint32_t e1 = x1 & 0x0f0f0f0fu, o1 = (x1 >> 4) & 0x0f0f0f0fu;
+    v4i r;
+    r[0] = (int)__builtin_amdgcn_perm(o0, e0, 0x05010400u);
+    r[1] = (int)__builtin_amdgcn_perm(o0, e0, 0x07030602u);
+    r[2] = (int)__builtin_amdgcn_perm(o1, e1, 0x05010400u);
+    r[3] = (int)__builtin_amdgcn_perm(o1, e1, 0x07030602u);
+    return r;
 }
 
 // Descending bitonic sort of keys[0, npow) (npow a power of two), whole
@@ -69,10 +86,17 @@ __device__ void sort_desc(uint64_t *keys, uint32_t npow) {
 // tau as a key and as an f32 score.
 struct MqQuery {
     double s[3];
-    float s0f, s1f, e3;  // e3 = s2 * 127^2 * P >= |s2 * d2| for any row
+    int32_t c[3];        // int4: 8 * (sum of level l's bytes), the nibble offset's share; int8: 0
+    float s0f, s1f, e3;  // e3 >= |s2 * (d2 - c2)| for any row: s2 * 127 * max|code| * P
     float tau_score;     // -inf when tau is 0
     uint64_t tau;
 };
+
+// A level dot corrected for the int4 nibble offset (int8: as is).
+template <int BITS> __device__ __forceinline__ int32_t dq(int32_t d, int32_t c) {
+    if constexpr (BITS == 4) return d - c;
+    else return d;
+}
 
 // Keys of one wave's 64 rows x 32 queries from its accumulators: written
 // densely (logical row i at cand[q][i]) or appended when at or above tau[q].
@@ -81,6 +105,7 @@ struct MqQuery {
 // magnitude (far above the f32 rounding of the sum and of the exact score),
 // times the row scale.  Only keys whose bound reaches tau_score get the exact
 // f64 combine.  sc: the scales of this wave's 64 rows (LDS).
+template <int BITS>
 __device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3], uint64_t w0, uint32_t qb, int h,
                                          int c, const MqQuery *mq, const float *sc) {
     const bool full = w0 + 64 <= a.n;
@@ -98,7 +123,7 @@ __device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3
                 const uint64_t li = w0 + ri;
                 if (qok && (full || li < a.n)) {
                     const uint64_t row = li * a.row_step;
-                    out[li] = q8_key(Q.s[0], Q.s[1], Q.s[2], acc[fr][0][r], acc[fr][1][r], acc[fr][2][r], sc[ri],
+                    out[li] = q_key(Q.s[0], Q.s[1], Q.s[2], dq<BITS>(acc[fr][0][r], Q.c[0]), dq<BITS>(acc[fr][1][r], Q.c[1]), dq<BITS>(acc[fr][2][r], Q.c[2]), sc[ri],
                                      (uint32_t)row);
                 }
             }
@@ -116,7 +141,7 @@ __device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3
         for (int r = 0; r < 16; ++r) {
             const float v4[4] = {sv[r >> 2].x, sv[r >> 2].y, sv[r >> 2].z, sv[r >> 2].w};
             const float scale = v4[r & 3];
-            const float t0 = (float)acc[fr][0][r] * Q.s0f, t1 = (float)acc[fr][1][r] * Q.s1f;
+            const float t0 = (float)dq<BITS>(acc[fr][0][r], Q.c[0]) * Q.s0f, t1 = (float)dq<BITS>(acc[fr][1][r], Q.c[1]) * Q.s1f;
             const float upper = (t0 + t1) * scale + (Q.e3 + 0x1p-20f * (fabsf(t0) + fabsf(t1))) * fabsf(scale);
             maybe |= (upper < Q.tau_score ? 0u : 1u) << (fr * 16 + r);
         }
@@ -133,8 +158,8 @@ __device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3
                     const uint32_t ri = fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                     const uint64_t li = w0 + ri;
                     if (full || li < a.n) {
-                        const uint64_t key = q8_key(Q.s[0], Q.s[1], Q.s[2], acc[fr][0][r], acc[fr][1][r],
-                                                    acc[fr][2][r], sc[ri], (uint32_t)(li * a.row_step));
+                        const uint64_t key = q_key(Q.s[0], Q.s[1], Q.s[2], dq<BITS>(acc[fr][0][r], Q.c[0]), dq<BITS>(acc[fr][1][r], Q.c[1]),
+                                                    dq<BITS>(acc[fr][2][r], Q.c[2]), sc[ri], (uint32_t)(li * a.row_step));
                         if (key >= Q.tau) pass |= bit;
                     }
                 }
@@ -157,7 +182,7 @@ __device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3
                     const uint32_t ri = fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                     const uint64_t row = (w0 + ri) * a.row_step;
                     if (pos < a.cap)
-                        out[pos] = q8_key(Q.s[0], Q.s[1], Q.s[2], acc[fr][0][r], acc[fr][1][r], acc[fr][2][r], sc[ri],
+                        out[pos] = q_key(Q.s[0], Q.s[1], Q.s[2], dq<BITS>(acc[fr][0][r], Q.c[0]), dq<BITS>(acc[fr][1][r], Q.c[1]), dq<BITS>(acc[fr][2][r], Q.c[2]), sc[ri],
                                           (uint32_t)row);
                     ++pos;
                 }
@@ -178,8 +203,9 @@ __device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3
 // query l%32.  The codes of each wave's rows stream into two register
 // groups of G steps, loads running one group ahead (into the next tile at a
 // tile's end), so the K loop needs no barrier.
-template <int S>
-__global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
+template <int S, int BITS>
+__global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan(MqArgs a) {
+    using Code = typename std::conditional<BITS == 8, v4i, uint2>::type;  // 16 codes
     // Codes stream in groups of G steps: a group's loads are issued back to
     // back one group ahead, so the G loads that read the same 128-byte line of
     // a row (steps 4k .. 4k + 3 read line k) reach L1 together and share one
@@ -222,28 +248,30 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
         Q.s[2] = t->s[2];
         Q.s0f = (float)t->s[0];
         Q.s1f = (float)t->s[1];
-        Q.e3 = (float)(fabs(t->s[2]) * 16129.0 * 16.0 * (double)a.units * 1.0000001);
+#pragma unroll
+        for (int l = 0; l < 3; ++l) Q.c[l] = BITS == 4 ? 8 * t->sum[l] : 0;
+        Q.e3 = (float)(fabs(t->s[2]) * 127.0 * (BITS == 8 ? 127.0 : 8.0) * 16.0 * (double)a.units * 1.0000001);
         Q.tau = a.tau ? a.tau[q] : 0ull;
         Q.tau_score = Q.tau ? f32_from_ord((uint32_t)(Q.tau >> 32)) : -__builtin_inff();
     }
 
-    auto row_ptrs = [&](uint64_t t, const v4i *(&ap)[2]) {
+    auto row_ptrs = [&](uint64_t t, const Code *(&ap)[2]) {
         const uint64_t w0 = t * MQ_ROWS + (uint64_t)wave * 64;
 #pragma unroll
         for (int fr = 0; fr < 2; ++fr) {
             uint64_t li = w0 + fr * 32 + c;
             if (li >= a.n) li = a.n - 1;  // rows past the end load a valid row; their results are dropped
-            ap[fr] = (const v4i *)(a.codes + li * a.row_step * a.W) + h;
+            ap[fr] = (const Code *)(a.codes + li * a.row_step * a.W) + h;
         }
     };
     auto row_scale = [&](uint64_t t) {
         uint64_t li = t * MQ_ROWS + (uint64_t)wave * 64 + lane;
         if (li >= a.n) li = a.n - 1;
-        return a.scales[li * a.row_step];
+        return a.scales[li * a.row_step] * a.scale_mul;
     };
-    const v4i *ap[2];
+    const Code *ap[2];
     row_ptrs(tile, ap);
-    v4i ring[2][G][2];  // [group parity][step in group][row half]
+    Code ring[2][G][2];  // [group parity][step in group][row half]
 #pragma unroll
     for (int j = 0; j < G; ++j)
 #pragma unroll
@@ -255,7 +283,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
     for (;;) {  // row tiles
         const uint64_t ntile = tile + tstride;
         const bool more = ntile * MQ_ROWS < a.n;
-        const v4i *np[2];
+        const Code *np[2];
         row_ptrs(more ? ntile : tile, np);
         v16i acc[2][3];
 #pragma unroll
@@ -277,7 +305,10 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
             }
             v4i A[2];
 #pragma unroll
-            for (int fr = 0; fr < 2; ++fr) A[fr] = ring[gp][j][fr];
+            for (int fr = 0; fr < 2; ++fr) {
+                if constexpr (BITS == 8) A[fr] = ring[gp][j][fr];
+                else A[fr] = unpack_q4(ring[gp][j][fr]);
+            }
             v4i B[3];
 #pragma unroll
             for (int l = 0; l < 3; ++l) B[l] = qlds[st][l][lane];
@@ -301,7 +332,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_q8(MqArgs a) {
         if (more) scale = row_scale(ntile);
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        epilogue(a, acc, tile * MQ_ROWS + (uint64_t)wave * 64, qb, h, c, mq, srow[wave]);
+        epilogue<BITS>(a, acc, tile * MQ_ROWS + (uint64_t)wave * 64, qb, h, c, mq, srow[wave]);
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         if (!more) break;
@@ -504,19 +535,27 @@ hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s) {
     if (a.n == 0 || a.nq == 0) return hipSuccess;
     const uint32_t steps = a.units >> 1;
     if ((a.units & 1u) || steps == 0 || steps > MQ_MAX_STEPS || (steps & (steps - 1)) || a.qblocks == 0 ||
-        a.groups == 0 || (uint64_t)a.qblocks * MQ_QB < a.nq)
+        a.groups == 0 || (uint64_t)a.qblocks * MQ_QB < a.nq || (a.bits != 8 && a.bits != 4) ||
+        a.W * 32u != a.units * 16u * (uint32_t)a.bits)
         return hipErrorInvalidValue;
     const uint64_t blocks = 8ull * a.groups * a.qblocks;
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
     const dim3 g((uint32_t)blocks), wg(MQ_WAVES * 64);
+#define BV_MQ_CASE(ST)                                                                              \
+    case ST:                                                                                        \
+        if (a.bits == 8) hipLaunchKernelGGL((mq_scan<ST, 8>), g, wg, 0, s, a);                      \
+        else hipLaunchKernelGGL((mq_scan<ST, 4>), g, wg, 0, s, a);                                  \
+        break;
     switch (steps) {
-    case 1: hipLaunchKernelGGL(mq_scan_q8<1>, g, wg, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(mq_scan_q8<2>, g, wg, 0, s, a); break;
-    case 4: hipLaunchKernelGGL(mq_scan_q8<4>, g, wg, 0, s, a); break;
-    case 8: hipLaunchKernelGGL(mq_scan_q8<8>, g, wg, 0, s, a); break;
-    case 16: hipLaunchKernelGGL(mq_scan_q8<16>, g, wg, 0, s, a); break;
-    default: hipLaunchKernelGGL(mq_scan_q8<32>, g, wg, 0, s, a); break;
+        BV_MQ_CASE(1)
+        BV_MQ_CASE(2)
+        BV_MQ_CASE(4)
+        BV_MQ_CASE(8)
+        BV_MQ_CASE(16)
+        BV_MQ_CASE(32)
+    default: return hipErrorInvalidValue;
     }
+#undef BV_MQ_CASE
     return hipGetLastError();
 }
 

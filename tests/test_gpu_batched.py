@@ -1,5 +1,5 @@
-"""Query batches on the matrix-core int8 path against the same queries run one
-at a time through the fused single-query scan (src/index.ts:473-517: a
+"""Query batches on the matrix-core int8 / int4 path against the same queries
+run one at a time through the fused single-query scan (src/index.ts:473-517: a
 batch must answer exactly as its queries would alone).  Keys are formed by
 the same f64 combine of exact int32 level dots in both paths, so rows and
 score bits must be identical, including re-ranked scores."""
@@ -33,13 +33,14 @@ def singles_equal(idx, qs, fetch, k):
     return rows, scores, cnt
 
 
-@pytest.mark.parametrize("dim,n,nq", [(768, 40000, 70), (20, 20000, 9), (100, 3000, 64)])
-def test_batched_search_equals_singles(ctx, dim, n, nq):
+@pytest.mark.parametrize("bits,dim,n,nq", [(8, 768, 40000, 70), (8, 20, 20000, 9), (8, 100, 3000, 64),
+                                           (4, 1024, 40000, 40), (4, 100, 20000, 9)])
+def test_batched_search_equals_singles(ctx, bits, dim, n, nq):
     from browservec_amd import QuantIndex
 
-    say("batched", dim, n, nq)
+    say("batched", bits, dim, n, nq)
     data = clustered(n, dim, 50, 0.1, seed=7 + dim)
-    idx = QuantIndex(ctx, dim, bits=8)
+    idx = QuantIndex(ctx, dim, bits=bits)
     idx.append(data, n)
     qs = data[np.arange(nq) * (n // nq)] + gaussian(nq, dim, 9, normalize=False) * 0.05
     qs = np.stack([o.normalize(q) for q in qs]).astype(np.float32)
