@@ -122,6 +122,8 @@ def main():
     ap.add_argument("--batch-steps", type=int, default=8, help="timed batch-256 steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-only", action="store_true", help="build + a short timed loop (for rocprofv3)")
+    ap.add_argument("--profile-batch", action="store_true",
+                    help="build + timed batch-256 searches on the matrix-core path (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5"],
@@ -165,6 +167,13 @@ def main():
     build_s = time.perf_counter() - t0
     P = idx.padded_dim
     row_bytes = P * args.bits // 8
+
+    if args.profile_batch:
+        nb = min(256, args.queries)
+        el = timed_search(idx, q, args.queries, nb, args.batch_steps, 2, args.fetch, args.k, torch)
+        print(json.dumps({"qps_b256": args.batch_steps * nb / el, "batch_ms_avg": el / args.batch_steps * 1e3,
+                          "batches": args.batch_steps}))
+        return
 
     # ---- batch 1 ------------------------------------------------------------
     log("timing batch 1")
