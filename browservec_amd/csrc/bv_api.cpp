@@ -141,6 +141,10 @@ struct bv_index {
     uint64_t sample_filled = 0, sample_seen = 0;
     uint32_t sample_rng = 0;
     DevBuf sample;
+    std::vector<uint64_t> sample_row;         // corpus row held by each reservoir slot
+    uint32_t tuned_nprobe = 0;                // targetRecall tuning (0 = not tuned)
+    float tuned_recall = -1.0f;
+    DevBuf tune_q;
     uint64_t built_rows = ~0ull;              // rows covered by the current lists
     uint32_t nlist = 0;
     DevBuf centroids, list_off, list_rows;
@@ -370,7 +374,7 @@ static double mb32_draw(uint32_t &a) { return (double)mb32_next(a) / 4294967296.
 // capacity.  Only the last row written to a slot within the batch keeps it
 // (earlier ones would be overwritten in order).  Slots go to the device in
 // idx->ivf_slot (count ints); the sample buffer grows to the slots in use.
-static int ivf_reservoir(bv_index *idx, uint64_t count, std::vector<int32_t> &slots) {
+static int ivf_reservoir(bv_index *idx, uint64_t base, uint64_t count, std::vector<int32_t> &slots) {
     slots.assign(count, -1);
     for (uint64_t i = 0; i < count; ++i) {
         if (idx->sample_filled < idx->sample_cap) {
@@ -387,6 +391,9 @@ static int ivf_reservoir(bv_index *idx, uint64_t count, std::vector<int32_t> &sl
         if (taken[slots[i]]) slots[i] = -1;
         else taken[slots[i]] = 1;
     }
+    if (idx->sample_row.size() < idx->sample_filled) idx->sample_row.resize(idx->sample_filled);
+    for (uint64_t i = 0; i < count; ++i)
+        if (slots[i] >= 0) idx->sample_row[(uint32_t)slots[i]] = base + i;
     const size_t rb = (size_t)idx->sample_dim * 4;
     HIPX(idx->dev, idx->sample.ensure(idx->sample_filled * rb, idx->sample.cap, idx->stream), "sample buffer");
     HIPX(idx->dev, idx->ivf_slot.ensure(count * 4, 0, idx->stream), "scratch");
@@ -457,7 +464,7 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
          "row upload");
     std::vector<int32_t> slots;
     if (idx->ivf) {
-        int rc = ivf_reservoir(idx, count, slots);
+        int rc = ivf_reservoir(idx, base, count, slots);
         if (rc) return rc;
     }
     if (idx->quant) {
@@ -501,6 +508,118 @@ extern "C" int bv_index_append_device(bv_index *idx, const float *d_data, uint64
 // mulberry32, as the reference's trainer does), then every row is assigned
 // (by its codes for quantized kinds) and the CSR lists are built on the
 // device.
+static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
+                     const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores, uint32_t *d_n);
+
+// nprobe auto-tune for targetRecall (src/index/ivfTune.ts:31-61,
+// ivfquant.ts:322-344, ivf.ts:269-291), after a build, when no nprobe is
+// configured.  For up to 32 reservoir rows spread evenly over the sample
+// (pickTuneQueries), the top k+1 of every row by the index's own scores
+// (probing every list scores every row) and the probe rank of each hit's
+// list, skipping the first hit (the query row itself); chooseNprobe then
+// takes the smallest nprobe whose share of hits probed meets the target.
+// A sampled row's stored fp32 vector rotates to exactly its sample row, so
+// the queries go through the ordinary query path.
+static int ivf_tune(bv_index *idx, const uint32_t *d_assign) {
+    idx->tuned_nprobe = 0;
+    idx->tuned_recall = -1.0f;
+    if (!(idx->d.target_recall >= 0.0f) || idx->d.nprobe) return BV_OK;
+    const double target = std::min(1.0, std::max(0.0, (double)idx->d.target_recall));
+    const uint64_t rows = idx->rows;
+    const uint32_t nlist = idx->nlist;
+    const uint64_t kk = std::min<uint64_t>(10, rows ? rows - 1 : 0);
+    if (kk < 1 || nlist <= 1) {
+        idx->tuned_nprobe = 1;
+        idx->tuned_recall = 1.0f;
+        return BV_OK;
+    }
+    const uint32_t k1 = (uint32_t)kk + 1;
+    const uint64_t filled = idx->sample_filled;
+    const uint32_t nq = (uint32_t)std::min<uint64_t>(filled, 32);
+    hipStream_t s = idx->stream;
+    const size_t rb = (size_t)idx->dim * 4;
+    HIPX(idx->dev, idx->tune_q.ensure(std::max<size_t>((size_t)nq * rb, 4), 0, s), "scratch");
+    for (uint32_t i = 0; i < nq; ++i) {
+        const uint64_t r = idx->sample_row[(uint64_t)i * filled / nq];
+        HIPX(idx->dev, hipMemcpyAsync(idx->tune_q.as<char>() + i * rb, idx->raw.as<char>() + r * rb, rb,
+                                      hipMemcpyDeviceToDevice, s),
+             "tune queries");
+    }
+    const float *d_q = idx->tune_q.as<float>();
+    // the top k+1 over every row
+    HIPX(idx->dev, idx->out_rows.ensure((size_t)nq * k1 * 4, 0, s), "output buffer");
+    HIPX(idx->dev, idx->out_scores.ensure((size_t)nq * k1 * 4, 0, s), "output buffer");
+    HIPX(idx->dev, idx->out_n.ensure((size_t)nq * 4, 0, s), "output buffer");
+    idx->ivf = false;
+    int rc = run_fused(idx, d_q, nq, k1, k1, false, nullptr, 0, idx->out_rows.as<uint32_t>(),
+                       idx->out_scores.as<float>(), idx->out_n.as<uint32_t>());
+    idx->ivf = true;
+    if (rc) return rc;
+    // probe scores of the rotated queries against every centroid
+    const float *qrot = d_q;
+    if (idx->quant) {
+        HIPX(idx->dev, idx->qrot.ensure((size_t)nq * idx->P * 4, 0, s), "query buffer");
+        EncodeArgs e{};
+        e.src = d_q;
+        e.rows = nq;
+        e.dim = idx->dim;
+        e.P = idx->P;
+        e.signs = idx->signs.as<float>();
+        e.rounds = idx->d.rounds;
+        e.rotated = idx->qrot.as<float>();
+        HIPX(idx->dev, launch_encode(e, s), "query rotate kernel");
+        qrot = idx->qrot.as<float>();
+    }
+    HIPX(idx->dev, idx->probe_scores.ensure((size_t)nq * nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->probes.ensure((size_t)nq * 4, 0, s), "scratch");
+    IvfProbeArgs pa{};
+    pa.centroids = idx->centroids.as<float>();
+    pa.nlist = nlist;
+    pa.P = idx->sample_dim;
+    pa.qrot = qrot;
+    pa.scores = idx->probe_scores.as<float>();
+    pa.nprobe = 1;
+    pa.probes = idx->probes.as<uint32_t>();
+    HIPX(idx->dev, ivf_launch_probes(pa, nq, s), "probe kernels");
+    std::vector<uint32_t> gt((size_t)nq * k1), gtn(nq), assign(rows);
+    std::vector<float> ps((size_t)nq * nlist);
+    HIPX(idx->dev, hipMemcpyAsync(gt.data(), idx->out_rows.p, gt.size() * 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipMemcpyAsync(gtn.data(), idx->out_n.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipMemcpyAsync(ps.data(), idx->probe_scores.p, ps.size() * 4, hipMemcpyDeviceToHost, s),
+         "download");
+    HIPX(idx->dev, hipMemcpyAsync(assign.data(), d_assign, rows * 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "tune");
+    std::vector<uint32_t> hist(nlist, 0), order(nlist), rank(nlist);
+    uint64_t total = 0;
+    for (uint32_t q = 0; q < nq; ++q) {
+        const float *sc = ps.data() + (size_t)q * nlist;
+        for (uint32_t c = 0; c < nlist; ++c) order[c] = c;
+        std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) { return sc[x] > sc[y]; });
+        for (uint32_t r = 0; r < nlist; ++r) rank[order[r]] = r;
+        for (uint32_t h = 1; h < gtn[q]; ++h) {
+            hist[rank[assign[gt[(size_t)q * k1 + h]]]]++;
+            total++;
+        }
+    }
+    // chooseNprobe
+    uint32_t np = nlist;
+    double rec = 1.0;
+    if (total) {
+        uint64_t cum = 0;
+        for (uint32_t p = 1; p <= nlist; ++p) {
+            cum += hist[p - 1];
+            if ((double)cum / (double)total >= target) {
+                np = p;
+                rec = (double)cum / (double)total;
+                break;
+            }
+        }
+    }
+    idx->tuned_nprobe = np;
+    idx->tuned_recall = (float)rec;
+    return BV_OK;
+}
+
 static int ivf_build(bv_index *idx) {
     auto t0 = std::chrono::steady_clock::now();
     const uint64_t rows = idx->rows;
@@ -618,15 +737,19 @@ static int ivf_build(bv_index *idx) {
     std::sort(idx->list_sizes_desc.begin(), idx->list_sizes_desc.end(), std::greater<uint32_t>());
     idx->nlist = nlist;
     idx->built_rows = rows;
+    int rc = ivf_tune(idx, fa.out);
+    if (rc) return rc;
     idx->build_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     return BV_OK;
 }
 
 // nprobe for the next query (ivfquant.ts:159-162, 487-491): the per-query
-// override (consumed once), else the configured one, else 5% of nlist.
+// override (consumed once), else the configured one, else the tuned one,
+// else 5% of nlist.
 static uint32_t ivf_resolve_nprobe(bv_index *idx) {
     uint32_t n = idx->nprobe_override ? idx->nprobe_override
                  : idx->d.nprobe      ? idx->d.nprobe
+                 : idx->tuned_nprobe  ? idx->tuned_nprobe
                                       : (uint32_t)std::max<double>(1.0, std::floor(idx->nlist * 0.05 + 0.5));
     idx->nprobe_override = 0;
     n = std::max<uint32_t>(1, std::min<uint32_t>(n, idx->nlist));
@@ -1375,6 +1498,7 @@ extern "C" int bv_index_get_stats(bv_index *idx, bv_index_stats *out) {
         out->nprobe = ivf_resolve_nprobe(idx);
         idx->nprobe_override = saved;
         out->build_ms = idx->build_ms;
+        out->tuned_recall = idx->tuned_recall;
     }
     out->last_query_ms = idx->last_query_ms;
     out->last_query_gpu_ms = idx->last_query_gpu_ms;

@@ -118,8 +118,20 @@ static uint32_t field_u32(napi_env env, napi_value obj, const char *name, uint32
     return x;
 }
 
+static double field_f64(napi_env env, napi_value obj, const char *name, double dflt) {
+    bool has = false;
+    napi_value v;
+    double x = dflt;
+    if (napi_has_named_property(env, obj, name, &has) == napi_ok && has &&
+        napi_get_named_property(env, obj, name, &v) == napi_ok) {
+        napi_valuetype t;
+        if (napi_typeof(env, v, &t) == napi_ok && t == napi_number) napi_get_value_double(env, v, &x);
+    }
+    return x;
+}
+
 /* createIndex(dev, {kind, dim, metric, bits, scorer, seed, rounds, chunkRows,
- *                   nlist, nprobe, sampleSize, trainSize, iters, ivfSeed}) -> external */
+ *                   nlist, nprobe, sampleSize, trainSize, iters, ivfSeed, targetRecall}) -> external */
 static napi_value create_index(napi_env env, napi_callback_info info) {
     ARGS(2);
     bv_index_desc d;
@@ -141,7 +153,7 @@ static napi_value create_index(napi_env env, napi_callback_info info) {
     d.iters = field_u32(env, argv[1], "iters", 0);
     d.has_ivf_seed = field_u32(env, argv[1], "hasIvfSeed", 0);
     d.ivf_seed = field_u32(env, argv[1], "ivfSeed", 0);
-    d.target_recall = -1.0f;
+    d.target_recall = (float)field_f64(env, argv[1], "targetRecall", -1.0);
     bv_index *idx = NULL;
     int rc = bv_index_create((bv_device *)get_ptr(env, argv[0]), &d, &idx);
     if (rc) return throw_bv(env, rc);
@@ -319,6 +331,7 @@ static napi_value stats(napi_env env, napi_callback_info info) {
     NUM("nlist", st.nlist);
     NUM("nprobe", st.nprobe);
     NUM("buildMs", st.build_ms);
+    NUM("tunedRecall", st.tuned_recall);
 #undef NUM
     return obj;
 }

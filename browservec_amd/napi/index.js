@@ -68,6 +68,7 @@ class HipIndex {
       iters: ivf && ivf.iters ? ivf.iters : 0,
       hasIvfSeed: ivf && ivf.seed !== undefined ? 1 : 0,
       ivfSeed: ivf && ivf.seed !== undefined ? ivf.seed >>> 0 : 0,
+      targetRecall: ivf && ivf.targetRecall !== undefined ? ivf.targetRecall : -1,
     });
   }
   get size() {
@@ -115,6 +116,11 @@ class HipIndex {
   }
   get nprobe() {
     return native.stats(this.handle).nprobe;
+  }
+  // estimated recall@10 at the tuned nprobe; undefined unless tuning ran
+  get tunedRecall() {
+    const r = native.stats(this.handle).tunedRecall;
+    return r < 0 ? undefined : r;
   }
   stats() {
     return native.stats(this.handle);

@@ -54,10 +54,12 @@ def reference_build(data, dim, bits, ivf, seed=o.DEFAULT_SEED):
         src = data
     res = o.Reservoir(cap, rseed)
     sample = np.zeros((cap, src.shape[1]), np.float32)
+    sample_row = np.zeros(cap, np.int64)
     for i in range(n):
         s = res.slot()
         if s >= 0:
             sample[s] = src[i]
+            sample_row[s] = i
     filled = min(n, cap)
     if ivf.get("nlist"):
         nlist = max(1, min(ivf["nlist"], n))
@@ -77,7 +79,8 @@ def reference_build(data, dim, bits, ivf, seed=o.DEFAULT_SEED):
     else:
         final = o.assign_f32(data, cen, order=1)
     off, rows = o.build_csr(final, nlist)
-    return dict(cen=cen, off=off, rows=rows, final=final, words=words, scales=scales, nlist=nlist)
+    return dict(cen=cen, off=off, rows=rows, final=final, words=words, scales=scales, nlist=nlist,
+                src=src, filled=filled, sample_row=sample_row[:filled])
 
 
 CASES = [(8, 96, {"nlist": 24, "iters": 4}), (4, 128, {"nlist": 16, "iters": 3, "seed": 77}),
@@ -201,3 +204,54 @@ def test_ivf_masked_and_nprobe_override(ctx):
     # the override was consumed: the next query uses nprobe 4 again
     assert idx.stats()["nprobe"] == 4
     idx.destroy()
+
+
+def reference_tune(data, dim, bits, ref, target):
+    """ivfquant.ts:322-344 / ivf.ts:269-291 on the oracle: evenly spaced
+    reservoir rows as queries, the exhaustive top k+1 in the index's own
+    scores, the probe rank of each hit's list (first hit skipped),
+    chooseNprobe."""
+    n = data.shape[0]
+    k = min(10, n - 1)
+    ranks = []
+    for si in o.pick_tune_queries(ref["filled"], 32):
+        r = int(ref["sample_row"][si])
+        rq = ref["src"][r]  # the sample row: rotated (quantized kinds) or raw (fp32)
+        if bits:
+            scores = o.scan_quant(ref["words"], ref["scales"], rq, bits)
+        else:
+            scores = o.scan_f32(data, rq)
+        gt, _ = o.topk_canonical(scores, k + 1)
+        order, _ = o.topk_canonical(o.probe_scores(ref["cen"], rq), ref["nlist"])
+        rank = np.empty(ref["nlist"], np.int64)
+        rank[order] = np.arange(ref["nlist"])
+        ranks += [int(rank[ref["final"][g]]) for g in gt[1:]]
+    return o.choose_nprobe(ranks, ref["nlist"], target)
+
+
+@pytest.mark.parametrize("bits,target", [(8, 0.9), (0, 0.95), (4, 0.8)])
+def test_ivf_tune_matches_oracle(ctx, bits, target):
+    """targetRecall tuning (ivfTune.ts:31-61): the tuned nprobe and its
+    estimated recall equal the oracle's restatement of the reference's tune;
+    an explicit nprobe disables tuning."""
+    from browservec_amd import IVFIndex, IVFQuantIndex
+
+    dim, n = 96, 6000
+    ivf = {"nlist": 24, "iters": 4, "targetRecall": target}
+    say("ivf tune", bits, target)
+    data = clustered(n, dim, 40, 0.2, seed=31 + bits)
+    idx = IVFQuantIndex(ctx, dim, bits=bits, ivf=ivf) if bits else IVFIndex(ctx, dim, ivf=ivf)
+    idx.append(data, n)
+    idx.build()
+    ref = reference_build(data, dim, bits, ivf)
+    want_np, want_rec = reference_tune(data, dim, bits, ref, target)
+    st = idx.stats()
+    assert st["nprobe"] == want_np, (st["nprobe"], want_np, want_rec)
+    assert np.float32(st["tuned_recall"]) == np.float32(want_rec), (st["tuned_recall"], want_rec)
+    idx.destroy()
+    fixed_ivf = dict(ivf, nprobe=3)
+    fixed = IVFQuantIndex(ctx, dim, bits=bits, ivf=fixed_ivf) if bits else IVFIndex(ctx, dim, ivf=fixed_ivf)
+    fixed.append(data, n)
+    fixed.build()
+    assert fixed.stats()["nprobe"] == 3 and fixed.stats()["tuned_recall"] < 0
+    fixed.destroy()
