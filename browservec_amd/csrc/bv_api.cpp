@@ -1005,9 +1005,10 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
 constexpr uint32_t MQ_MIN_Q = 8;  // smallest batch for the matrix-core path
 
 static bool mq_eligible(const bv_index *idx, uint32_t nq, const uint32_t *d_mask) {
+    if (idx->ivf || d_mask || nq < MQ_MIN_Q || idx->rows == 0) return false;
+    if (!idx->quant) return idx->codec == C_F32DOT && mq_f32_supported(idx->dim);  // dot / cosine
     const uint32_t u16 = idx->P / 16;  // 16-code units per row
-    return !idx->ivf && !d_mask && idx->quant && (idx->codec == C_Q8 || idx->codec == C_Q4) && nq >= MQ_MIN_Q &&
-           u16 >= 2 && (u16 % 2) == 0 && u16 / 2 <= MQ_MAX_STEPS && idx->rows > 0;
+    return (idx->codec == C_Q8 || idx->codec == C_Q4) && u16 >= 2 && (u16 % 2) == 0 && u16 / 2 <= MQ_MAX_STEPS;
 }
 
 // Rotated queries split into three int8 levels in the 16-code unit layout
@@ -1050,10 +1051,13 @@ static uint32_t mq_groups(const bv_index *idx, uint32_t qblocks) {
 
 static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                        uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
-    const unsigned char *qscan = nullptr;
-    uint64_t qstride = 0;
-    int rc = prepare_levels16(idx, d_q, nq, &qscan, &qstride);
-    if (rc) return rc;
+    const unsigned char *qscan = (const unsigned char *)d_q;  // fp32 rows: the queries as they are
+    uint64_t qstride = (uint64_t)idx->dim * 4;
+    int rc = BV_OK;
+    if (idx->quant) {
+        rc = prepare_levels16(idx, d_q, nq, &qscan, &qstride);
+        if (rc) return rc;
+    }
     const uint64_t N = idx->rows;
     const uint64_t S = std::min<uint64_t>(N, MQ_SAMPLE);
     const bool one_pass = S == N;
@@ -1068,10 +1072,10 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
     HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
 
     MqArgs m{};
-    m.codes = idx->codes.as<uint32_t>();
+    m.codes = idx->quant ? idx->codes.as<uint32_t>() : idx->raw.as<uint32_t>();
     m.scales = idx->scales.as<float>();
-    m.W = idx->words_per_row;
-    m.units = idx->P / 16;
+    m.W = idx->quant ? idx->words_per_row : idx->dim;
+    m.units = idx->quant ? idx->P / 16 : idx->dim / 8;
     m.bits = idx->codec == C_Q4 ? 4 : 8;
     m.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
     m.qlev = qscan;
@@ -1095,7 +1099,8 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
     m.row_step = N / S;
     m.tau = nullptr;
     HIPX(idx->dev, hipMemsetD32Async((hipDeviceptr_t)idx->mq_cnt.p, (int)S, nq, idx->stream), "scratch");
-    HIPX(idx->dev, launch_mq_scan(m, idx->stream), "batched scan kernel");
+    HIPX(idx->dev, idx->quant ? launch_mq_scan(m, idx->stream) : launch_mq_scan_f32(m, idx->stream),
+         "batched scan kernel");
     if (!one_pass) {
         sa.tau = idx->mq_tau.as<uint64_t>();
         HIPX(idx->dev, launch_mq_select(sa, nq, idx->stream), "batched select kernel");
@@ -1103,7 +1108,8 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
         m.n = N;
         m.row_step = 1;
         m.tau = idx->mq_tau.as<uint64_t>();
-        HIPX(idx->dev, launch_mq_scan(m, idx->stream), "batched scan kernel");
+        HIPX(idx->dev, idx->quant ? launch_mq_scan(m, idx->stream) : launch_mq_scan_f32(m, idx->stream),
+         "batched scan kernel");
         sa.tau = nullptr;
     }
     sa.merged = idx->merged.as<uint64_t>();

@@ -253,6 +253,11 @@ struct MqRerankArgs {
     uint32_t *out_n;
 };
 hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s);
+// fp32 rows (dot / cosine): a.codes = the rows, a.W = dim, a.units = dim / 8,
+// a.qlev = fp32 queries (a.qstride bytes apart).  Dimensions 32 .. 1024 in
+// the set mq_f32_supported accepts (32 queries of up to 1024 floats stay in LDS).
+bool mq_f32_supported(uint32_t dim);
+hipError_t launch_mq_scan_f32(const MqArgs &a, hipStream_t s);
 hipError_t launch_mq_rerank(const MqRerankArgs &a, uint32_t nq, hipStream_t s);
 hipError_t launch_mq_select(const MqSelArgs &a, uint32_t nq, hipStream_t s);
 

@@ -31,6 +31,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
 
@@ -342,6 +343,155 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan(MqArgs a) {
     }
 }
 
+// fp32 rows x fp32 queries on v_mfma_f32_32x32x2f32 (dot / cosine): the
+// batched counterpart of the fp32 flat scan.  Same structure as mq_scan:
+// the block's 32 queries stay in LDS, each wave streams 64 rows.  Lane
+// l = 32h + c supplies, over the four MFMA steps of chunk t, elements
+// 8t + 4h .. 8t + 4h + 3 of row c (A) and of query c (B), one 16-byte load
+// each, so both operands pair the same elements.  The sum runs in the
+// matrix core's own order (the single-query scan adds in the reference's
+// order; the two agree to float rounding).  a.W = dim (floats per row),
+// a.units = dim / 8 chunks, a.qlev = the fp32 queries, a.qstride their
+// byte stride.
+template <int CHUNKS>
+__global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_f32(MqArgs a) {
+    constexpr int G = CHUNKS < 4 ? CHUNKS : 4;
+    __shared__ float4 qlds[CHUNKS][64];
+    __shared__ uint64_t qtau[MQ_QB];
+    __shared__ float qts[MQ_QB];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane >> 5, c = lane & 31;
+    const uint32_t b = blockIdx.x, xcd = b & 7u, slot = b >> 3;
+    const uint32_t qb = slot % a.qblocks, grp = slot / a.qblocks;
+    const uint64_t tstride = 8ull * a.groups;
+    uint64_t tile = xcd + 8ull * grp;
+    if (tile * MQ_ROWS >= a.n) return;
+    {
+        uint32_t q = qb * MQ_QB + c;
+        if (q >= a.nq) q = a.nq - 1;
+        const float *src = (const float *)(a.qlev + (uint64_t)q * a.qstride);
+        for (int t = wave; t < CHUNKS; t += MQ_WAVES)
+            __builtin_amdgcn_global_load_lds((glb_void *)(src + 8 * t + 4 * h), (lds_void *)&qlds[t][0], 16, 0, 0);
+    }
+    if (threadIdx.x < MQ_QB) {
+        uint32_t q = qb * MQ_QB + threadIdx.x;
+        if (q >= a.nq) q = a.nq - 1;
+        const uint64_t t = a.tau ? a.tau[q] : 0ull;
+        qtau[threadIdx.x] = t;
+        qts[threadIdx.x] = t ? f32_from_ord((uint32_t)(t >> 32)) : -__builtin_inff();
+    }
+    auto row_ptrs = [&](uint64_t t, const float4 *(&ap)[2]) {
+        const uint64_t w0 = t * MQ_ROWS + (uint64_t)wave * 64;
+#pragma unroll
+        for (int fr = 0; fr < 2; ++fr) {
+            uint64_t li = w0 + fr * 32 + c;
+            if (li >= a.n) li = a.n - 1;  // rows past the end load a valid row; their results are dropped
+            ap[fr] = (const float4 *)((const float *)a.codes + li * a.row_step * a.W + 4 * h);
+        }
+    };
+    const float4 *ap[2];
+    row_ptrs(tile, ap);
+    float4 ring[2][G][2];
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+        for (int fr = 0; fr < 2; ++fr) ring[0][j][fr] = ap[fr][2 * j];
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    const uint32_t q = qb * MQ_QB + c;
+    const bool qok = q < a.nq;
+    const uint32_t qq = qok ? q : a.nq - 1;
+    uint64_t *out = a.cand + (uint64_t)qq * a.cap;
+    for (;;) {
+        const uint64_t ntile = tile + tstride;
+        const bool more = ntile * MQ_ROWS < a.n;
+        const float4 *np[2];
+        row_ptrs(more ? ntile : tile, np);
+        v16f acc[2] = {v16f{}, v16f{}};
+#pragma unroll
+        for (int t = 0; t < CHUNKS; ++t) {
+            const int gp = (t / G) & 1, j = t % G;
+            if (j == 0) {
+                const int nt = t + G;
+#pragma unroll
+                for (int jj = 0; jj < G; ++jj)
+#pragma unroll
+                    for (int fr = 0; fr < 2; ++fr) {
+                        if (nt < CHUNKS) ring[gp ^ 1][jj][fr] = ap[fr][2 * (nt + jj)];
+                        else if (more) ring[gp ^ 1][jj][fr] = np[fr][2 * (nt - CHUNKS + jj)];
+                    }
+            }
+            const float4 B = qlds[t][lane];
+            const float bv[4] = {B.x, B.y, B.z, B.w};
+#pragma unroll
+            for (int fr = 0; fr < 2; ++fr) {
+                const float4 A = ring[gp][j][fr];
+                const float av[4] = {A.x, A.y, A.z, A.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[fr] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[e], bv[e], acc[fr], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr ((CHUNKS / G) & 1) {
+#pragma unroll
+            for (int j = 0; j < G; ++j)
+#pragma unroll
+                for (int fr = 0; fr < 2; ++fr) ring[0][j][fr] = ring[1][j][fr];
+        }
+        // keys: dense (logical row i at out[i]) or appended at or above tau
+        const uint64_t w0 = tile * MQ_ROWS + (uint64_t)wave * 64;
+        const bool full = w0 + 64 <= a.n;
+        if (!a.tau) {
+#pragma unroll
+            for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint64_t li = w0 + fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (qok && (full || li < a.n)) out[li] = make_key(ord_f32(acc[fr][r]), (uint32_t)(li * a.row_step));
+                }
+        } else {
+            const uint64_t tau = qtau[c];
+            const float ts = qts[c];
+            uint32_t pass = 0;
+#pragma unroll
+            for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float sc = acc[fr][r];
+                    if (!(sc < ts)) {
+                        const uint64_t li = w0 + fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                        if (qok && (full || li < a.n) && make_key(ord_f32(sc), (uint32_t)(li * a.row_step)) >= tau)
+                            pass |= 1u << (fr * 16 + r);
+                    }
+                }
+            if (__ballot(pass != 0)) {
+                const uint32_t mine = __popc(pass);
+                const uint32_t other = __shfl_xor(mine, 32);
+                uint32_t base = 0;
+                if (h == 0 && mine + other) base = atomicAdd(&a.cnt[qq], mine + other);
+                base = __shfl(base, c);
+                if (pass) {
+                    uint64_t pos = (uint64_t)base + (h ? other : 0u);
+#pragma unroll
+                    for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            if (pass & (1u << (fr * 16 + r))) {
+                                const uint64_t li = w0 + fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                                if (pos < a.cap) out[pos] = make_key(ord_f32(acc[fr][r]), (uint32_t)(li * a.row_step));
+                                ++pos;
+                            }
+                }
+            }
+        }
+        if (!more) break;
+        ap[0] = np[0];
+        ap[1] = np[1];
+        tile = ntile;
+    }
+}
+
 // One workgroup per query.  The kk-th best key is found by binning the
 // keys over their actual range (2048 bins of a power-of-two width, so keys
 // concentrated in a few score octaves still spread over many bins) and
@@ -556,6 +706,37 @@ hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s) {
     default: return hipErrorInvalidValue;
     }
 #undef BV_MQ_CASE
+    return hipGetLastError();
+}
+
+bool mq_f32_supported(uint32_t dim) {
+    switch (dim) {
+    case 32: case 64: case 96: case 128: case 192: case 256: case 384: case 512: case 768: case 1024: return true;
+    default: return false;
+    }
+}
+
+hipError_t launch_mq_scan_f32(const MqArgs &a, hipStream_t s) {
+    if (a.n == 0 || a.nq == 0) return hipSuccess;
+    if (!mq_f32_supported(a.W) || a.units * 8 != a.W || a.qblocks == 0 || a.groups == 0 ||
+        (uint64_t)a.qblocks * MQ_QB < a.nq)
+        return hipErrorInvalidValue;
+    const uint64_t blocks = 8ull * a.groups * a.qblocks;
+    if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+    const dim3 g((uint32_t)blocks), wg(MQ_WAVES * 64);
+    switch (a.units) {
+    case 4: hipLaunchKernelGGL(mq_scan_f32<4>, g, wg, 0, s, a); break;
+    case 8: hipLaunchKernelGGL(mq_scan_f32<8>, g, wg, 0, s, a); break;
+    case 12: hipLaunchKernelGGL(mq_scan_f32<12>, g, wg, 0, s, a); break;
+    case 16: hipLaunchKernelGGL(mq_scan_f32<16>, g, wg, 0, s, a); break;
+    case 24: hipLaunchKernelGGL(mq_scan_f32<24>, g, wg, 0, s, a); break;
+    case 32: hipLaunchKernelGGL(mq_scan_f32<32>, g, wg, 0, s, a); break;
+    case 48: hipLaunchKernelGGL(mq_scan_f32<48>, g, wg, 0, s, a); break;
+    case 64: hipLaunchKernelGGL(mq_scan_f32<64>, g, wg, 0, s, a); break;
+    case 96: hipLaunchKernelGGL(mq_scan_f32<96>, g, wg, 0, s, a); break;
+    case 128: hipLaunchKernelGGL(mq_scan_f32<128>, g, wg, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

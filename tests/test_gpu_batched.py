@@ -91,3 +91,36 @@ def test_batched_overflow_falls_back(ctx):
     idx.append(data.astype(np.float32), n)
     singles_equal(idx, qs.astype(np.float32), 100, 10)
     idx.destroy()
+
+
+@pytest.mark.parametrize("metric,dim,n,nq", [("cosine", 768, 40000, 40), ("dot", 96, 30000, 9),
+                                             ("cosine", 64, 5000, 33)])
+def test_batched_f32_within_tolerance(ctx, metric, dim, n, nq):
+    """fp32 batches on v_mfma_f32_32x32x2f32 sum in the matrix core's order,
+    not the reference's `acc = dot4 + acc`: every returned score is within
+    1e-5 of the oracle's fp32 score of that row (relative to |x||q|), and the
+    top-k rows equal the single-query scan's except near-ties at the cut."""
+    from browservec_amd import FlatIndex
+
+    say("batched f32", metric, dim, n, nq)
+    data = clustered(n, dim, 50, 0.15, seed=3 + dim)
+    if metric == "dot":
+        data = data * np.float32(1.5)
+    idx = FlatIndex(ctx, dim, metric)
+    idx.append(data, n)
+    qs = gaussian(nq, dim, 17 + dim)
+    k = 20
+    batch = idx.query_batch(qs, nq, k)
+    norms = np.linalg.norm(data.astype(np.float64), axis=1)
+    for i in range(nq):
+        exact = o.scan_f32(data, qs[i], metric)
+        mag = norms * np.linalg.norm(qs[i].astype(np.float64))
+        rows = np.array([h.row for h in batch[i]])
+        got = np.float64([h.score for h in batch[i]])
+        assert len(rows) == k
+        assert np.all(np.abs(got - exact[rows]) <= 1e-5 * mag[rows] + 1e-7), i
+        single = [h.row for h in idx.query(qs[i], k)]
+        kth = float(np.sort(exact)[-k])
+        for r in set(rows.tolist()) ^ set(single):
+            assert abs(float(exact[r]) - kth) <= 2e-5 * float(mag[r]) + 1e-7, (i, r)
+    idx.destroy()
