@@ -280,8 +280,20 @@ __global__ __launch_bounds__(256) void ivf_probe_scores(IvfProbeArgs a) {
     const uint32_t vec = a.P & ~3u;
     const float *cen = a.centroids + (uint64_t)(c < a.nlist ? c : 0) * a.P;
     double acc = 0.0;
-    if (c < a.nlist)
-        for (uint32_t i = m; i < vec; i += 4) acc = fma((double)cen[i], (double)rq[i], acc);
+    if (c < a.nlist) {
+        uint32_t i = m;
+        for (; i + 28 < vec; i += 32) {  // eight loads in flight, summed in element order
+            float cv[8], qv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                cv[u] = cen[i + 4 * u];
+                qv[u] = rq[i + 4 * u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = fma((double)cv[u], (double)qv[u], acc);
+        }
+        for (; i < vec; i += 4) acc = fma((double)cen[i], (double)rq[i], acc);
+    }
     const double a1 = __shfl_down(acc, 1, 4), a2 = __shfl_down(acc, 2, 4), a3 = __shfl_down(acc, 3, 4);
     if (m == 0 && c < a.nlist) {
         double s = ((acc + a1) + a2) + a3;
@@ -291,21 +303,54 @@ __global__ __launch_bounds__(256) void ivf_probe_scores(IvfProbeArgs a) {
 }
 
 // Best nprobe centroids of one query, best first (score desc, index asc).
-// One workgroup per query: a bisection on the 64-bit keys finds the
-// nprobe-th key (keys are unique), then the survivors are ranked.
+// One workgroup per query; keys are unique.  A bound: the np-th best of a
+// strided sample of 256 keys (at least np keys are at or above it, the
+// sample's own); the keys at or above it are gathered and ranked.  When
+// the bound admits too many keys (or np exceeds the sample), a bisection on
+// the 64-bit keys finds the np-th key instead.
+constexpr uint32_t PROBE_RANK_CAP = 1024;
 __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
     extern __shared__ uint64_t pk[];  // nlist keys, then up to nlist selected keys
     uint64_t *sel = pk + a.nlist;
+    __shared__ uint64_t smp[256];
     __shared__ uint32_t cnt_s[4];
     __shared__ uint32_t nsel;
+    __shared__ uint64_t s_bound;
     const uint32_t qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *sc = a.scores + (uint64_t)qi * a.nlist;
     for (uint32_t c = tid; c < a.nlist; c += 256) pk[c] = idx_key(sc[c], c);
-    if (tid == 0) nsel = 0;
+    if (tid == 0) {
+        nsel = 0;
+        s_bound = 0;
+    }
     __syncthreads();
     const uint32_t np = a.nprobe < a.nlist ? a.nprobe : a.nlist;
     uint64_t lo = 0, hi = ~0ull;  // count(>= lo) >= np > count(>= hi) (hi unreachable)
-    if (np < a.nlist) {
+    bool bisect = np < a.nlist;
+    if (bisect && a.nlist >= 512 && np <= 64) {
+        const uint32_t stride = a.nlist / 256;
+        smp[tid] = pk[tid * stride];
+        __syncthreads();
+        const uint64_t mine = smp[tid];
+        uint32_t r = 0;
+        for (uint32_t j = 0; j < 256; ++j) r += smp[j] > mine ? 1u : 0u;
+        if (r == np - 1) s_bound = mine;
+        __syncthreads();
+        const uint64_t bound = s_bound;
+        uint32_t c = 0;
+        for (uint32_t j = tid; j < a.nlist; j += 256) c += pk[j] >= bound ? 1u : 0u;
+#pragma unroll
+        for (int s = 1; s < 64; s <<= 1) c += __shfl_xor(c, s);
+        if (lane == 0) cnt_s[wave] = c;
+        __syncthreads();
+        const uint32_t tot = cnt_s[0] + cnt_s[1] + cnt_s[2] + cnt_s[3];
+        __syncthreads();
+        if (tot <= PROBE_RANK_CAP) {
+            lo = bound;  // rank the tot >= np keys at or above the bound below
+            bisect = false;
+        }
+    }
+    if (bisect) {
         for (int it = 0; it < 64 && hi - lo > 1; ++it) {
             const uint64_t mid = lo + ((hi - lo) >> 1);
             uint32_t c = 0;
@@ -372,18 +417,27 @@ __global__ __launch_bounds__(256) void ivf_cand_offsets(const uint64_t *totals, 
 }
 
 // gatherCandidates: the probed lists in probe order, rows ascending within
-// a list.  One workgroup per query.
+// a list.  One workgroup per (probed list, query): its position is the
+// query's offset plus the sizes of the lists probed before it.
 __global__ __launch_bounds__(256) void ivf_gather_lists(const uint32_t *probes, uint32_t nprobe,
                                                         const uint32_t *offset, const uint32_t *list_rows,
                                                         const uint64_t *cand_off, uint32_t *cand) {
-    const uint32_t qi = blockIdx.x;
-    uint64_t w = cand_off[qi];
-    for (uint32_t p = 0; p < nprobe; ++p) {
-        const uint32_t c = probes[(uint64_t)qi * nprobe + p];
-        const uint32_t b = offset[c], e = offset[c + 1];
-        for (uint32_t j = threadIdx.x; j < e - b; j += blockDim.x) cand[w + j] = list_rows[b + j];
-        w += e - b;
+    __shared__ uint64_t part[4];
+    const uint32_t p = blockIdx.x, qi = blockIdx.y, tid = threadIdx.x;
+    const uint32_t *pr = probes + (uint64_t)qi * nprobe;
+    uint64_t before = 0;
+    for (uint32_t i = tid; i < p; i += 256) {
+        const uint32_t c = pr[i];
+        before += offset[c + 1] - offset[c];
     }
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) before += __shfl_xor(before, s);
+    if ((tid & 63) == 0) part[tid >> 6] = before;
+    __syncthreads();
+    const uint64_t w = cand_off[qi] + part[0] + part[1] + part[2] + part[3];
+    const uint32_t c = pr[p];
+    const uint32_t b = offset[c], e = offset[c + 1];
+    for (uint32_t j = tid; j < e - b; j += 256) cand[w + j] = list_rows[b + j];
 }
 
 // ------------------------------------------------------------- launchers --
@@ -448,7 +502,8 @@ hipError_t ivf_launch_gather(const uint32_t *probes, uint32_t nq, uint32_t nprob
     if (nq == 0) return hipSuccess;
     hipLaunchKernelGGL(ivf_probe_totals, dim3((nq + 255) / 256), dim3(256), 0, s, probes, nq, nprobe, offset, totals);
     hipLaunchKernelGGL(ivf_cand_offsets, dim3(1), dim3(256), 0, s, totals, nq, cand_off);
-    hipLaunchKernelGGL(ivf_gather_lists, dim3(nq), dim3(256), 0, s, probes, nprobe, offset, list_rows, cand_off, cand);
+    hipLaunchKernelGGL(ivf_gather_lists, dim3(nprobe, nq), dim3(256), 0, s, probes, nprobe, offset, list_rows, cand_off,
+                       cand);
     return hipGetLastError();
 }
 
