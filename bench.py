@@ -266,6 +266,11 @@ def main():
                      "traffic_source": "profiles/scan_topk_q8_1Mx768_traffic.md" if traffic else None},
         "cpu_baseline": cpu,
         "batch256_qps": round(qps_b256, 1),
+        # the batch's dense int8 work (three query levels), over the whole
+        # batch pipeline time (levels, sample pass, full pass, selects, re-rank)
+        "batch256_int8_mfma": {"pops": round(2.0 * args.rows * nb * 3 * P * qps_b256 / nb / 1e15, 3),
+                               "peak": 5.0, "unit": "POP/s",
+                               "frac": round(2.0 * args.rows * nb * 3 * P * qps_b256 / nb / 1e15 / 5.0, 4)},
         "recall_at_10": round(recall, 4),
         "end_to_end_hbm_frac_b1": round(algo_bytes_q * qps_b1 / (HBM_PEAK_GBS * 1e9), 4),
         "latency_ms_sync_p50": round(lat_p50, 4),
