@@ -277,10 +277,28 @@ def main():
         "fp32_flat_cosine_batch_qps": round(flat_qps, 1),
         "build_s": round(build_s, 3),
         "device": info["name"],
+        "hbm_copy_gbs": round(copy_bandwidth(torch), 1),  # measured 1 GiB device copy, read + write
     }
     print(json.dumps(out))
     idx.destroy()
     ctx.destroy()
+
+
+def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
+    """Device-to-device copy of nbytes (read + write), timed with CUDA events:
+    the streaming ceiling of the card the run is on, in GB/s."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst
+    return gbs
 
 
 def time_batches(idx, q, nq_total, batch, steps, warmup, fetch, k, torch):
