@@ -1,4 +1,4 @@
-// Batched int8 scans on the gfx950 matrix cores.
+// Query batches on the gfx950 matrix cores.
 //
 //   mq_scan      int8 / int4 rows x queries x three int8 query levels on
 //                v_mfma_i32_32x32x32_i8.  Every (row, query, level) dot is
@@ -9,6 +9,9 @@
 //                distanceQ4 dispatches + score buffers for query batches
 //                (src/engine/wgsl/distanceQ8.ts:56-82, distanceQ4.ts:44-78,
 //                src/index/quant.ts:178-245, src/index.ts:473-517).
+//   mq_scan_f32  fp32 rows x fp32 queries (dot / cosine) on
+//                v_mfma_f32_32x32x2f32 (src/engine/wgsl/distance.ts:24-177,
+//                src/index/flat.ts:132-200 for query batches).
 //   mq_select    exact selection of each query's best kk keys.
 //   mq_rerank    exact f64 re-rank of the selected candidates, 16 per wave.
 //
@@ -199,7 +202,8 @@ __device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3
 // 96 KB at P = 1024), laid out as MFMA B operands: block (s, l) holds, at
 // lane l's 16 bytes, unit 2s + l/32 of query l%32's level bytes.  Wave w
 // takes rows [64w, 64w + 64) of a tile as two 32-row A operands: lane l
-// supplies unit 2s + l/32 of row l%32, so both operands pair the same codes.
+// supplies unit 2s + l/32 of row l%32 (int4 rows: that unit's 16 nibbles
+// unpacked to bytes n ^ 8), so both operands pair the same codes.
 // Accumulator register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4,
 // query l%32.  The codes of each wave's rows stream into two register
 // groups of G steps, loads running one group ahead (into the next tile at a
@@ -208,10 +212,11 @@ template <int S, int BITS>
 __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan(MqArgs a) {
     using Code = typename std::conditional<BITS == 8, v4i, uint2>::type;  // 16 codes
     // Codes stream in groups of G steps: a group's loads are issued back to
-    // back one group ahead, so the G loads that read the same 128-byte line of
-    // a row (steps 4k .. 4k + 3 read line k) reach L1 together and share one
-    // fill.  Issued a step at a time, the lines of the 8 waves (64 KB per
-    // four steps) overflow the 32 KB L1 and are fetched up to four times.
+    // back one group ahead, so the loads that read the same 128-byte line of
+    // a row (int8: steps 4k .. 4k + 3 read line k; int4: eight steps) reach
+    // L1 together and share one fill.  Issued a step at a time, the lines of
+    // the 8 waves (64 KB per four int8 steps) overflow the 32 KB L1 and are
+    // fetched up to four times.
     constexpr int G = S < 4 ? S : 4;
     __shared__ v4i qlds[S][3][64];
     __shared__ float srow[MQ_WAVES][64];
