@@ -148,7 +148,9 @@ int bv_index_query_masked(bv_index *idx, const float *q, uint32_t k, const uint3
                           uint64_t n_words, uint32_t *rows, float *scores, uint32_t *n_out);
 
 /* queryBatch (src/index.ts:499-501): nq queries (nq*dim floats); results
- * row-major [nq][k], n_out[nq].  Equal to looping bv_index_query. */
+ * row-major [nq][k], n_out[nq].  Equal to looping bv_index_query (8 or more
+ * queries on a flat fp32 dot/cosine index run on the matrix cores and agree
+ * with single queries to fp32 rounding: rows may differ at near-ties). */
 int bv_index_query_batch(bv_index *idx, const float *queries, uint32_t nq, uint32_t k, uint32_t *rows,
                          float *scores, uint32_t *n_out);
 
@@ -172,7 +174,9 @@ int bv_index_search(bv_index *idx, const float *queries, uint32_t nq, uint32_t f
 
 /* ---- device-resident variants (serving loops, benchmarks) ------------------ */
 /* Same as bv_index_search with every pointer in device memory; enqueued on
- * the index's stream and returns without waiting. */
+ * the index's stream and returns without waiting, except for batches of 8 or
+ * more queries on a flat int8/int4/fp32 index, which run on the matrix cores
+ * and wait once for the batch (one overflow flag per query is read back). */
 int bv_index_search_device(bv_index *idx, const float *d_queries, uint32_t nq, uint32_t fetch, uint32_t k,
                            uint32_t *d_rows, float *d_scores, uint32_t *d_n_out);
 /* Append rows that already live in device memory (count*dim floats). */
