@@ -124,3 +124,34 @@ def test_batched_f32_within_tolerance(ctx, metric, dim, n, nq):
         for r in set(rows.tolist()) ^ set(single):
             assert abs(float(exact[r]) - kth) <= 2e-5 * float(mag[r]) + 1e-7, (i, r)
     idx.destroy()
+
+
+@pytest.mark.parametrize("n", [1, 5, 300])
+def test_batched_tiny_corpus(ctx, n):
+    """Corpora smaller than one row tile: rows past the end are clamped on
+    load and dropped, k clamps to the row count, and batch results equal
+    single queries (int8) or agree within the fp32 tolerance."""
+    from browservec_amd import FlatIndex, QuantIndex
+
+    dim, nq = 64, 9
+    say("batched tiny", n)
+    data = gaussian(n, dim, 70 + n)
+    qs = gaussian(nq, dim, 71 + n)
+    quant = QuantIndex(ctx, dim, bits=8)
+    quant.append(data, n)
+    rows, scores, cnt = quant.search(qs, 8, 3)
+    for i in range(nq):
+        r1, s1, c1 = quant.search(qs[i:i + 1], 8, 3)
+        assert cnt[i] == c1[0] == min(3, n)
+        assert np.array_equal(rows[i, :cnt[i]], r1[0, :c1[0]])
+        assert np.array_equal(scores[i, :cnt[i]].view(np.uint32), s1[0, :c1[0]].view(np.uint32))
+    quant.destroy()
+    flat = FlatIndex(ctx, dim, "cosine")
+    flat.append(data, n)
+    batch = flat.query_batch(qs, nq, 4)
+    for i in range(nq):
+        exact = o.scan_f32(data, qs[i], "cosine")
+        assert len(batch[i]) == min(4, n)
+        for h in batch[i]:
+            assert abs(h.score - float(exact[h.row])) <= 1e-5 * float(np.linalg.norm(data[h.row])) + 1e-7
+    flat.destroy()
