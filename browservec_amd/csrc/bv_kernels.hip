@@ -85,10 +85,10 @@ template <> struct Codec<C_Q8> {
             for (int l = 0; l < 3; ++l) a[l] = __builtin_amdgcn_sdot4((int)w[d], (int)q[l * 4 + d], a[l], false);
     }
 };
-// int4 codes (32 per unit).  Nibble n is carried as the byte u = n ^ 8
-// (= n + 8 in [0, 15]); sum n*q = sum u*q - 8*sum(q), the second term a
-// per-query integer.  q[l*8 + 2d] / q[l*8 + 2d + 1] hold the level-l query
-// bytes for the even / odd nibbles of code dword d.
+// int4 codes (32 per unit).  Each signed nibble n is moved to the high half
+// of a byte, which reads as the int8 16 * n, so the level dots come out as
+// exact 16 * sum(n * q).  q[l*8 + 2d] / q[l*8 + 2d + 1] hold the level-l
+// query bytes for the even / odd nibbles of code dword d.
 template <> struct Codec<C_Q4> {
     using Unit = uint4; using QT = uint32_t; using Acc = int32_t;
     static constexpr int QN = 24, NA = 3;
@@ -96,8 +96,8 @@ template <> struct Codec<C_Q4> {
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-            const uint32_t x = w[d] ^ 0x88888888u;
-            const uint32_t lo = x & 0x0f0f0f0fu, hi = (x >> 4) & 0x0f0f0f0fu;
+            // each nibble in the high half of a byte: the signed byte is 16 * n
+            const uint32_t lo = (w[d] << 4) & 0xf0f0f0f0u, hi = w[d] & 0xf0f0f0f0u;
 #pragma unroll
             for (int l = 0; l < 3; ++l) {
                 a[l] = __builtin_amdgcn_sdot4((int)lo, (int)q[l * 8 + 2 * d], a[l], false);
@@ -179,14 +179,13 @@ template <> struct Fin<C_Q8> {
 };
 template <> struct Fin<C_Q4> {
     double s0, s1, s2;
-    int32_t c0, c1, c2;
     __device__ void load(const void *tail, uint32_t) {
         const QLevelTail *q = (const QLevelTail *)tail;
         s0 = q->s[0]; s1 = q->s[1]; s2 = q->s[2];
-        c0 = 8 * q->sum[0]; c1 = 8 * q->sum[1]; c2 = 8 * q->sum[2];
     }
+    // t[l] = 16 * sum(n * q_l) exactly: the shift recovers the level dot
     __device__ __forceinline__ float score(const int32_t *t, float scale, uint32_t &ord) const {
-        const double v = fma(s2, (double)(t[2] - c2), fma(s1, (double)(t[1] - c1), s0 * (double)(t[0] - c0)));
+        const double v = fma(s2, (double)(t[2] >> 4), fma(s1, (double)(t[1] >> 4), s0 * (double)(t[0] >> 4)));
         const float sc = (float)(v * (double)scale);
         ord = ord_f32(sc);
         return sc;
