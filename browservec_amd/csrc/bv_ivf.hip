@@ -272,32 +272,43 @@ __global__ __launch_bounds__(256) void ivf_centroid_means(const float *sample, u
 // ---------------------------------------------------------------- probes --
 // pickProbes: four f64 accumulators over the strided elements 4j+m (each
 // product of two f32 exact in f64), a0 + a1 + a2 + a3, stored f32.  Four
-// lanes per centroid, 64 centroids per workgroup; grid (ceil(nlist/64), nq).
-__global__ __launch_bounds__(256) void ivf_probe_scores(IvfProbeArgs a) {
+// lanes per centroid, 16 centroids per one-wave workgroup; grid
+// (ceil(nlist/16), nq).  The query sits in LDS and each lane keeps 32
+// centroid loads in flight, so a 768-dim dot is six round trips to memory.
+// P is at most PROBE_MAX_DIM (the scans' own limit: 4096 floats per row).
+constexpr uint32_t PROBE_MAX_DIM = 4096;
+__global__ __launch_bounds__(64) void ivf_probe_scores(IvfProbeArgs a) {
+    extern __shared__ float qs[];  // the query, P floats
     const uint32_t qi = blockIdx.y, g = threadIdx.x >> 2, m = threadIdx.x & 3;
-    const uint32_t c = blockIdx.x * 64 + g;
     const float *rq = a.qrot + (uint64_t)qi * a.P;
+    for (uint32_t i = threadIdx.x; i < a.P; i += 64) qs[i] = rq[i];
+    __syncthreads();
+    const uint32_t c = blockIdx.x * 16 + g;
     const uint32_t vec = a.P & ~3u;
     const float *cen = a.centroids + (uint64_t)(c < a.nlist ? c : 0) * a.P;
     double acc = 0.0;
     if (c < a.nlist) {
         uint32_t i = m;
-        for (; i + 28 < vec; i += 32) {  // eight loads in flight, summed in element order
-            float cv[8], qv[8];
+        for (; i + 124 < vec; i += 128) {  // summed in element order after the loads land
+            float cv[32];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                cv[u] = cen[i + 4 * u];
-                qv[u] = rq[i + 4 * u];
-            }
+            for (int u = 0; u < 32; ++u) cv[u] = cen[i + 4 * u];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc = fma((double)cv[u], (double)qv[u], acc);
+            for (int u = 0; u < 32; ++u) acc = fma((double)cv[u], (double)qs[i + 4 * u], acc);
         }
-        for (; i < vec; i += 4) acc = fma((double)cen[i], (double)rq[i], acc);
+        for (; i + 28 < vec; i += 32) {
+            float cv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) cv[u] = cen[i + 4 * u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = fma((double)cv[u], (double)qs[i + 4 * u], acc);
+        }
+        for (; i < vec; i += 4) acc = fma((double)cen[i], (double)qs[i], acc);
     }
     const double a1 = __shfl_down(acc, 1, 4), a2 = __shfl_down(acc, 2, 4), a3 = __shfl_down(acc, 3, 4);
     if (m == 0 && c < a.nlist) {
         double s = ((acc + a1) + a2) + a3;
-        for (uint32_t i = vec; i < a.P; ++i) s = fma((double)cen[i], (double)rq[i], s);  // the fp32 IVF tail
+        for (uint32_t i = vec; i < a.P; ++i) s = fma((double)cen[i], (double)qs[i], s);  // the fp32 IVF tail
         a.scores[(uint64_t)qi * a.nlist + c] = (float)s;
     }
 }
@@ -310,7 +321,7 @@ __global__ __launch_bounds__(256) void ivf_probe_scores(IvfProbeArgs a) {
 // the 64-bit keys finds the np-th key instead.
 constexpr uint32_t PROBE_RANK_CAP = 1024;
 __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
-    extern __shared__ uint64_t pk[];  // nlist keys, then up to nlist selected keys
+    extern __shared__ uint64_t pk[];  // nlist keys, then up to nlist + 16 selected keys
     uint64_t *sel = pk + a.nlist;
     __shared__ uint64_t smp[256];
     __shared__ uint32_t cnt_s[4];
@@ -318,6 +329,7 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
     __shared__ uint64_t s_bound;
     const uint32_t qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *sc = a.scores + (uint64_t)qi * a.nlist;
+#pragma unroll 8
     for (uint32_t c = tid; c < a.nlist; c += 256) pk[c] = idx_key(sc[c], c);
     if (tid == 0) {
         nsel = 0;
@@ -333,11 +345,13 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
         __syncthreads();
         const uint64_t mine = smp[tid];
         uint32_t r = 0;
+#pragma unroll 16
         for (uint32_t j = 0; j < 256; ++j) r += smp[j] > mine ? 1u : 0u;
         if (r == np - 1) s_bound = mine;
         __syncthreads();
         const uint64_t bound = s_bound;
         uint32_t c = 0;
+#pragma unroll 8
         for (uint32_t j = tid; j < a.nlist; j += 256) c += pk[j] >= bound ? 1u : 0u;
 #pragma unroll
         for (int s = 1; s < 64; s <<= 1) c += __shfl_xor(c, s);
@@ -369,47 +383,57 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
     for (uint32_t j = tid; j < a.nlist; j += 256)
         if (pk[j] >= lo) sel[atomicAdd(&nsel, 1u)] = pk[j];
     __syncthreads();
-    const uint32_t m = nsel;
+    // zeros pad the selection to a multiple of 16 (no key is 0: its low
+    // word is 0xffffffff - c with c < nlist), so the rank reads run 16 wide
+    const uint32_t m = nsel, mp = (m + 15) & ~15u;
+    if (m + tid < mp) sel[m + tid] = 0;
+    __syncthreads();
     for (uint32_t j = tid; j < m; j += 256) {
         const uint64_t k = sel[j];
         uint32_t r = 0;
-        for (uint32_t i = 0; i < m; ++i) r += sel[i] > k ? 1u : 0u;
+        for (uint32_t i = 0; i < mp; i += 16) {
+#pragma unroll
+            for (uint32_t u = 0; u < 16; ++u) r += sel[i + u] > k ? 1u : 0u;
+        }
         if (r < np) a.probes[(uint64_t)qi * a.nprobe + r] = 0xffffffffu - (uint32_t)k;
     }
 }
 
-// Candidates per query: the sizes of its probed lists.
+// Candidates per query: the sizes of its probed lists (one wave per query).
 __global__ __launch_bounds__(256) void ivf_probe_totals(const uint32_t *probes, uint32_t nq, uint32_t nprobe,
                                                         const uint32_t *offset, uint64_t *totals) {
-    const uint32_t qi = blockIdx.x * blockDim.x + threadIdx.x;
-    if (qi >= nq) return;
+    const uint32_t qi = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (qi >= nq) return;  // whole waves
     uint64_t t = 0;
-    for (uint32_t p = 0; p < nprobe; ++p) {
+    for (uint32_t p = lane; p < nprobe; p += 64) {
         const uint32_t c = probes[(uint64_t)qi * nprobe + p];
         t += offset[c + 1] - offset[c];
     }
-    totals[qi] = t;
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) t += __shfl_xor(t, s);
+    if (lane == 0) totals[qi] = t;
 }
 
-// cand_off[q] = sum of totals before q (one workgroup).
+// cand_off[q] = sum of totals before q (one workgroup): each thread sums a
+// run of queries, a scan over the 256 runs (within waves, then the four
+// wave totals) places them.
 __global__ __launch_bounds__(256) void ivf_cand_offsets(const uint64_t *totals, uint32_t nq, uint64_t *cand_off) {
-    __shared__ uint64_t part[256];
-    const uint32_t tid = threadIdx.x, per = (nq + 255) / 256, q0 = tid * per;
+    __shared__ uint64_t wsum[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t per = (nq + 255) / 256, q0 = tid * per;
     uint64_t s = 0;
     for (uint32_t q = q0; q < q0 + per && q < nq; ++q) s += totals[q];
-    part[tid] = s;
-    __syncthreads();
-    if (tid == 0) {
-        uint64_t run = 0;
-        for (int t = 0; t < 256; ++t) {
-            const uint64_t v = part[t];
-            part[t] = run;
-            run += v;
-        }
-        cand_off[nq] = run;
+    uint64_t x = s;  // inclusive scan within the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint64_t y = __shfl_up(x, d);
+        if (lane >= (uint32_t)d) x += y;
     }
+    if (lane == 63) wsum[wave] = x;
     __syncthreads();
-    uint64_t run = part[tid];
+    uint64_t run = x - s;
+    for (uint32_t w = 0; w < wave; ++w) run += wsum[w];
+    if (tid == 255) cand_off[nq] = run + s;
     for (uint32_t q = q0; q < q0 + per && q < nq; ++q) {
         cand_off[q] = run;
         run += totals[q];
@@ -490,9 +514,9 @@ hipError_t ivf_launch_means(const float *sample, uint32_t stride, uint32_t dim, 
 
 hipError_t ivf_launch_probes(const IvfProbeArgs &a, uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
-    if (a.nlist > IVF_MAX_NLIST || a.nprobe > IVF_MAX_NPROBE) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(ivf_probe_scores, dim3((a.nlist + 63) / 64, nq), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(ivf_probe_select, dim3(nq), dim3(256), (size_t)a.nlist * 16, s, a);
+    if (a.nlist > IVF_MAX_NLIST || a.nprobe > IVF_MAX_NPROBE || a.P > PROBE_MAX_DIM) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(ivf_probe_scores, dim3((a.nlist + 15) / 16, nq), dim3(64), (size_t)a.P * 4, s, a);
+    hipLaunchKernelGGL(ivf_probe_select, dim3(nq), dim3(256), ((size_t)a.nlist * 2 + 16) * 8, s, a);
     return hipGetLastError();
 }
 
@@ -500,7 +524,7 @@ hipError_t ivf_launch_gather(const uint32_t *probes, uint32_t nq, uint32_t nprob
                              const uint32_t *list_rows, uint64_t *totals, uint64_t *cand_off, uint32_t *cand,
                              hipStream_t s) {
     if (nq == 0) return hipSuccess;
-    hipLaunchKernelGGL(ivf_probe_totals, dim3((nq + 255) / 256), dim3(256), 0, s, probes, nq, nprobe, offset, totals);
+    hipLaunchKernelGGL(ivf_probe_totals, dim3((nq + 3) / 4), dim3(256), 0, s, probes, nq, nprobe, offset, totals);
     hipLaunchKernelGGL(ivf_cand_offsets, dim3(1), dim3(256), 0, s, totals, nq, cand_off);
     hipLaunchKernelGGL(ivf_gather_lists, dim3(nprobe, nq), dim3(256), 0, s, probes, nprobe, offset, list_rows, cand_off,
                        cand);

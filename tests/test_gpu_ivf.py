@@ -255,3 +255,55 @@ def test_ivf_tune_matches_oracle(ctx, bits, target):
     fixed.build()
     assert fixed.stats()["nprobe"] == 3 and fixed.stats()["tuned_recall"] < 0
     fixed.destroy()
+
+
+def probed_rows(cen, off, lrows, q, nprobe):
+    probes, _ = o.topk_canonical(o.probe_scores(cen, q), nprobe)
+    return set(np.concatenate([lrows[off[c]:off[c + 1]] for c in probes]).tolist())
+
+
+def test_ivf_probe_selection_many_lists(ctx):
+    """pickProbes at 1024 lists (ivfquant.ts:495-517): the sampled bound
+    (nprobe <= 64) and the bisection (nprobe > 64) both pick the oracle's
+    probe set.  k covers every candidate, so a query returns exactly the rows
+    of the lists it probed; single queries with a one-query override, then a
+    batch of 300 queries (more than one query per prefix run)."""
+    from browservec_amd import IVFIndex
+
+    dim, n = 32, 8192
+    say("ivf probes 1024 lists")
+    data = clustered(n, dim, 256, 0.2, seed=41)
+    idx = IVFIndex(ctx, dim, ivf={"nlist": 1024, "iters": 2, "nprobe": 48})
+    idx.append(data, n)
+    cen, off, lrows = idx.export_ivf()
+    assert cen.shape[0] == 1024
+    qs = gaussian(300, dim, 42)
+    for i, nprobe in enumerate([1, 16, 32, 64, 65, 80]):
+        want = probed_rows(cen, off, lrows, qs[i], nprobe)
+        assert len(want) <= 1024
+        idx.set_nprobe(nprobe)
+        got = {h.row for h in idx.query(qs[i], 1024)}
+        assert got == want, nprobe
+    batch = idx.query_batch(qs, qs.shape[0], 1024)
+    for i in range(qs.shape[0]):
+        want = probed_rows(cen, off, lrows, qs[i], 48)
+        assert len(want) <= 1024
+        assert {h.row for h in batch[i]} == want, i
+    idx.destroy()
+
+
+def test_ivf_probe_scores_widest_query(ctx):
+    """The widest query the scans serve (4096 floats) fills the probe
+    kernel's LDS staging; the probe set equals pickProbes'."""
+    from browservec_amd import IVFIndex
+
+    dim, n = 4096, 64
+    say("ivf probes dim 4096")
+    data = clustered(n, dim, 8, 0.3, seed=43)
+    idx = IVFIndex(ctx, dim, ivf={"nlist": 8, "iters": 2, "nprobe": 3})
+    idx.append(data, n)
+    cen, off, lrows = idx.export_ivf()
+    for i, q in enumerate(gaussian(3, dim, 44)):
+        got = {h.row for h in idx.query(q, n)}
+        assert got == probed_rows(cen, off, lrows, q, 3), i
+    idx.destroy()
