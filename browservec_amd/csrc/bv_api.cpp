@@ -790,12 +790,15 @@ static int ivf_candidates(bv_index *idx, const float *d_q, uint32_t nq, uint64_t
     pa.scores = idx->probe_scores.as<float>();
     pa.nprobe = nprobe;
     pa.probes = idx->probes.as<uint32_t>();
-    HIPX(idx->dev, ivf_launch_probes(pa, nq, s), "probe kernels");
     uint64_t per = 0;
     for (uint32_t i = 0; i < nprobe && i < idx->list_sizes_desc.size(); ++i) per += idx->list_sizes_desc[i];
     HIPX(idx->dev, idx->cand.ensure(std::max<uint64_t>(per * nq, 1) * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->cand_tot.ensure((size_t)nq * 8, 0, s), "scratch");
     HIPX(idx->dev, idx->cand_off.ensure(((size_t)nq + 1) * 8, 0, s), "scratch");
+    pa.offset = idx->list_off.as<uint32_t>();
+    pa.totals = idx->cand_tot.as<uint64_t>();
+    pa.cand_off = idx->cand_off.as<uint64_t>();
+    HIPX(idx->dev, ivf_launch_probes(pa, nq, s), "probe kernels");
     HIPX(idx->dev, ivf_launch_gather(idx->probes.as<uint32_t>(), nq, nprobe, idx->list_off.as<uint32_t>(),
                                      idx->list_rows.as<uint32_t>(), idx->cand_tot.as<uint64_t>(),
                                      idx->cand_off.as<uint64_t>(), idx->cand.as<uint32_t>(), s),

@@ -10,8 +10,9 @@
 //   ivf_centroid_means   updateCentroids' f32 sums in row order + mean
 //                        (src/index/kmeans.ts:177-209)
 //   ivf_probe_scores     pickProbes' f64 four-way dot (ivfquant.ts:495-511)
-//   ivf_probe_select     top-nprobe of the probe scores, best first
-//   ivf_probe_totals, ivf_gather_lists
+//   ivf_probe_select     top-nprobe of the probe scores, best first, and the
+//                        probed lists' total size
+//   ivf_cand_offsets, ivf_gather_lists
 //                        gatherCandidates (ivfquant.ts:513-527): the probed
 //                        lists concatenated in probe order
 #include "bv_kernels.h"
@@ -325,6 +326,7 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
     uint64_t *sel = pk + a.nlist;
     __shared__ uint64_t smp[256];
     __shared__ uint32_t cnt_s[4];
+    __shared__ uint64_t tot_s[4];
     __shared__ uint32_t nsel;
     __shared__ uint64_t s_bound;
     const uint32_t qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -388,6 +390,7 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
     const uint32_t m = nsel, mp = (m + 15) & ~15u;
     if (m + tid < mp) sel[m + tid] = 0;
     __syncthreads();
+    uint64_t size = 0;  // candidates in this thread's probed lists
     for (uint32_t j = tid; j < m; j += 256) {
         const uint64_t k = sel[j];
         uint32_t r = 0;
@@ -395,23 +398,26 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
 #pragma unroll
             for (uint32_t u = 0; u < 16; ++u) r += sel[i + u] > k ? 1u : 0u;
         }
-        if (r < np) a.probes[(uint64_t)qi * a.nprobe + r] = 0xffffffffu - (uint32_t)k;
+        if (r < np) {
+            const uint32_t c = 0xffffffffu - (uint32_t)k;
+            a.probes[(uint64_t)qi * a.nprobe + r] = c;
+            if (a.offset) size += a.offset[c + 1] - a.offset[c];
+        }
     }
-}
-
-// Candidates per query: the sizes of its probed lists (one wave per query).
-__global__ __launch_bounds__(256) void ivf_probe_totals(const uint32_t *probes, uint32_t nq, uint32_t nprobe,
-                                                        const uint32_t *offset, uint64_t *totals) {
-    const uint32_t qi = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (qi >= nq) return;  // whole waves
-    uint64_t t = 0;
-    for (uint32_t p = lane; p < nprobe; p += 64) {
-        const uint32_t c = probes[(uint64_t)qi * nprobe + p];
-        t += offset[c + 1] - offset[c];
-    }
+    if (a.offset) {  // the query's candidate count (gatherCandidates' total)
 #pragma unroll
-    for (int s = 1; s < 64; s <<= 1) t += __shfl_xor(t, s);
-    if (lane == 0) totals[qi] = t;
+        for (int s = 1; s < 64; s <<= 1) size += __shfl_xor(size, s);
+        if (lane == 0) tot_s[wave] = size;
+        __syncthreads();
+        if (tid == 0) {
+            const uint64_t t = tot_s[0] + tot_s[1] + tot_s[2] + tot_s[3];
+            a.totals[qi] = t;
+            if (gridDim.x == 1) {  // one query: its offsets need no prefix pass
+                a.cand_off[0] = 0;
+                a.cand_off[1] = t;
+            }
+        }
+    }
 }
 
 // cand_off[q] = sum of totals before q (one workgroup): each thread sums a
@@ -524,8 +530,7 @@ hipError_t ivf_launch_gather(const uint32_t *probes, uint32_t nq, uint32_t nprob
                              const uint32_t *list_rows, uint64_t *totals, uint64_t *cand_off, uint32_t *cand,
                              hipStream_t s) {
     if (nq == 0) return hipSuccess;
-    hipLaunchKernelGGL(ivf_probe_totals, dim3((nq + 3) / 4), dim3(256), 0, s, probes, nq, nprobe, offset, totals);
-    hipLaunchKernelGGL(ivf_cand_offsets, dim3(1), dim3(256), 0, s, totals, nq, cand_off);
+    if (nq > 1) hipLaunchKernelGGL(ivf_cand_offsets, dim3(1), dim3(256), 0, s, totals, nq, cand_off);
     hipLaunchKernelGGL(ivf_gather_lists, dim3(nprobe, nq), dim3(256), 0, s, probes, nprobe, offset, list_rows, cand_off,
                        cand);
     return hipGetLastError();

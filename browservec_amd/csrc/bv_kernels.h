@@ -170,6 +170,9 @@ struct IvfProbeArgs {
     float *scores;            // nq x nlist scratch
     uint32_t nprobe;
     uint32_t *probes;         // nq x nprobe, best first
+    const uint32_t *offset;   // list offsets (nlist + 1), or null: no totals
+    uint64_t *totals;         // nq: the probed lists' total size per query
+    uint64_t *cand_off;       // nq + 1 candidate offsets, written here when nq == 1
 };
 
 hipError_t ivf_launch_copy_rows(const IvfCopyArgs &a, hipStream_t s);
@@ -183,7 +186,8 @@ hipError_t ivf_launch_means(const float *sample, uint32_t stride, uint32_t dim, 
                             const uint32_t *list_rows, uint32_t nlist, float *centroids, uint32_t cen_stride,
                             hipStream_t s);
 hipError_t ivf_launch_probes(const IvfProbeArgs &a, uint32_t nq, hipStream_t s);
-// totals: nq; cand_off: nq+1; cand: capacity for every query's candidates.
+// totals: nq, as the probe launch wrote them; cand_off: nq+1 (the probe
+// launch wrote it when nq == 1); cand: capacity for every query's candidates.
 hipError_t ivf_launch_gather(const uint32_t *probes, uint32_t nq, uint32_t nprobe, const uint32_t *offset,
                              const uint32_t *list_rows, uint64_t *totals, uint64_t *cand_off, uint32_t *cand,
                              hipStream_t s);
