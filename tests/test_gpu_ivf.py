@@ -267,10 +267,11 @@ def test_ivf_probe_selection_many_lists(ctx):
     (nprobe <= 64) and the bisection (nprobe > 64) both pick the oracle's
     probe set.  k covers every candidate, so a query returns exactly the rows
     of the lists it probed; single queries with a one-query override, then a
-    batch of 300 queries (more than one query per prefix run)."""
+    batch of 300 queries (more than one query per prefix run; eight-query
+    probe tiles, the last one partial)."""
     from browservec_amd import IVFIndex
 
-    dim, n = 32, 8192
+    dim, n = 128, 8192
     say("ivf probes 1024 lists")
     data = clustered(n, dim, 256, 0.2, seed=41)
     idx = IVFIndex(ctx, dim, ivf={"nlist": 1024, "iters": 2, "nprobe": 48})
