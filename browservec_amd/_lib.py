@@ -88,6 +88,7 @@ SIGNATURES = {
     "bv_device_open": [ctypes.c_int, ctypes.POINTER(vp)],
     "bv_device_close": [vp],
     "bv_device_is_lost": [vp, ctypes.POINTER(ctypes.c_int)],
+    "bv_debug_inject": [vp, ctypes.c_int],
     "bv_device_info": [vp, ctypes.c_char_p, u32, ctypes.POINTER(u32), ctypes.POINTER(u64)],
     "bv_index_create": [vp, ctypes.POINTER(IndexDesc), ctypes.POINTER(vp)],
     "bv_index_destroy": [vp],
@@ -110,6 +111,7 @@ SIGNATURES = {
     "bv_index_export_rotated_query": [vp, vp, vp],
     "bv_index_build": [vp],
     "bv_index_export_ivf": [vp, vp, vp, vp],
+    "bv_index_export_probe_scores": [vp, vp, u32, vp],
 }
 _RESTYPE = {"bv_last_error": ctypes.c_char_p}
 

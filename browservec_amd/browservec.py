@@ -377,9 +377,37 @@ class BrowserVec:
         return self.index.rerank(q, [h.row for h in candidates], k)
 
     def query_batch(self, queries, k: int = 10, **opts) -> list[list[dict]]:
-        """queryBatch (src/index.ts:473-517): per-query results equal to
-        looping query() (the reference's flat/quant path is that loop)."""
-        return [self.query(q, k=k, **opts) for q in queries]
+        """queryBatch (src/index.ts:473-517).  The index's own batch is used
+        where the reference seam would offer one: a flat fp32 index, whose
+        batch returns exactly the single-query results.  Quantized and IVF
+        indexes (and filtered batches) loop query(), which re-ranks and
+        honours a per-query nprobe, as the reference's fallback loop does."""
+        if len(queries) == 0:
+            return []
+        if type(self.index) is not FlatIndex or opts.get("filter") is not None:
+            return [self.query(q, k=k, **opts) for q in queries]
+        packed = np.stack([self._prep_query(q) for q in queries])
+        deleted = self.store.deleted_count
+        k_eff = min(self.index.size, k + deleted)
+        t0 = time.perf_counter()
+        batch = self.index.query_batch(packed, len(queries), k_eff)
+        self.last_query_ms = (time.perf_counter() - t0) * 1e3
+        self.last_query_gpu_ms = self.index.stats()["last_query_gpu_ms"]
+        out = []
+        for hits in batch:
+            res = []
+            for h in hits:
+                if deleted and self.store.is_deleted(h.row):
+                    continue
+                e = self.store.by_row[h.row]
+                r = {"id": e.id, "score": h.score}
+                if e.metadata is not None:
+                    r["metadata"] = e.metadata
+                res.append(r)
+                if len(res) == k:
+                    break
+            out.append(res)
+        return out
 
     # ----------------------------------------------------------- mutation
     def delete(self, id: str) -> bool:

@@ -17,7 +17,12 @@ LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libbrowservec_hip.so")
 ARCH = os.environ.get("BV_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["bv_kernels.hip", "bv_ivf.hip", "bv_mq.hip", "bv_api.cpp"]
+# The fused scan's instantiations are split one codec per translation unit
+# (bv_scan_*.hip) so that they compile in parallel.
+SCAN_CODECS = ["f32dot", "f32l2", "q8", "q4", "q1a", "ham", "i8s", "f32dot_s", "f32l2_s"]
+SOURCES = (["bv_kernels.hip"] + [f"bv_scan_{c}.hip" for c in SCAN_CODECS] +
+           ["bv_ivf.hip", "bv_mq.hip", "bv_api.cpp"])
+HEADERS = ["bv_kernels.h", "bv_device.h", "bv_scan.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -76,13 +81,27 @@ def build_napi(verbose: bool = True) -> str | None:
     return NAPI_OUT
 
 
-def build(verbose: bool = True) -> str:
+def _stale(src: str, obj: str) -> bool:
+    """True when obj is missing or older than its source or a shared header."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [os.path.join(CSRC, src)] + [os.path.join(CSRC, h) for h in HEADERS]
+    deps.append(os.path.join(ROOT, "include", "browservec_hip.h"))
+    return any(os.path.getmtime(d) > t for d in deps if os.path.exists(d))
+
+
+def build(verbose: bool = True, incremental: bool = False) -> str:
+    """Compiles every source (incremental=True: only those older than their
+    inputs) and links the library and the Node addon."""
     os.makedirs(LIBDIR, exist_ok=True)
     objdir = os.path.join(LIBDIR, "obj")
     os.makedirs(objdir, exist_ok=True)
     objs = [os.path.join(objdir, s + ".o") for s in SOURCES]
-    with cf.ThreadPoolExecutor(len(SOURCES)) as ex:
-        list(ex.map(lambda so: _compile(*so), zip(SOURCES, objs)))
+    todo = [(s, o) for s, o in zip(SOURCES, objs) if not incremental or _stale(s, o)]
+    workers = max(1, min(len(todo), int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    with cf.ThreadPoolExecutor(workers) as ex:
+        list(ex.map(lambda so: _compile(*so), todo))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
     subprocess.run(cmd, check=True)
@@ -94,4 +113,4 @@ def build(verbose: bool = True) -> str:
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv)

@@ -37,6 +37,7 @@ struct bv_device {
     int ordinal = 0;
     hipDeviceProp_t prop{};
     bool lost = false;
+    bool inject_append_oom = false;  // bv_debug_inject: fail the next append's allocation
 };
 
 static int hip_fail(bv_device *dev, hipError_t e, const char *what) {
@@ -110,6 +111,9 @@ struct HostBuf {
 
 // ------------------------------------------------------------------ index
 struct bv_index {
+    // Calls on one index are serialized (the Node binding runs them on worker
+    // threads); the reference awaits them one at a time per store.
+    mutable std::recursive_mutex mu;
     bv_device *dev = nullptr;
     bv_index_desc d{};
     uint32_t dim = 0, P = 0, words_per_row = 0, row_bytes = 0, units = 0;
@@ -131,6 +135,9 @@ struct bv_index {
     DevBuf out_rows, out_scores, out_n;
     DevBuf cand, cand_n, dense;
     DevBuf mq_cand, mq_cnt, mq_tau, mq_flag;  // batched matrix-core scans
+    DevBuf rsq, rsq_max;                      // flat fp32: squared row norms and their maximum (float bits)
+    DevBuf mq_qsq, mq_slack, mq_rows;         // exact fp32 batches: query norms, slack, surviving rows
+    HostBuf h_cnt;
     HostBuf h_rows, h_scores, h_n, h_flag;
 
     uint32_t nprobe_override = 0;
@@ -144,7 +151,10 @@ struct bv_index {
     std::vector<uint64_t> sample_row;         // corpus row held by each reservoir slot
     uint32_t tuned_nprobe = 0;                // targetRecall tuning (0 = not tuned)
     float tuned_recall = -1.0f;
-    DevBuf tune_q;
+    // the tuner's own queries and outputs: a build may run inside a query
+    // call, so it must not touch that call's scratch or output buffers
+    DevBuf tune_q, tune_rot, tune_rows, tune_scores, tune_n;
+    DevBuf ivf_qrot;                          // probe-space queries of an IVF query
     uint64_t built_rows = ~0ull;              // rows covered by the current lists
     uint32_t nlist = 0;
     DevBuf centroids, list_off, list_rows;
@@ -195,6 +205,15 @@ extern "C" int bv_device_is_lost(const bv_device *dev, int *lost) {
     if (!dev || !lost) return fail(BV_E_INVALID, "null argument");
     *lost = dev->lost ? 1 : 0;
     return BV_OK;
+}
+
+extern "C" int bv_debug_inject(bv_device *dev, int what) {
+    if (!dev) return fail(BV_E_INVALID, "null device");
+    switch (what) {
+    case BV_INJECT_LOST: dev->lost = true; return BV_OK;
+    case BV_INJECT_APPEND_OOM: dev->inject_append_oom = true; return BV_OK;
+    default: return fail(BV_E_INVALID, "unknown injection %d", what);
+    }
 }
 
 extern "C" int bv_device_info(const bv_device *dev, char *name, uint32_t name_len, uint32_t *cu_count,
@@ -319,6 +338,10 @@ extern "C" int bv_index_create(bv_device *dev, const bv_index_desc *desc, bv_ind
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreate(&x->ev0);
     if (e == hipSuccess) e = hipEventCreate(&x->ev1);
+    if (e == hipSuccess && !quant && !x->ivf) {
+        e = x->rsq_max.ensure(256, 0, x->stream, false);
+        if (e == hipSuccess) e = hipMemset(x->rsq_max.p, 0, 256);
+    }
     if (e == hipSuccess && quant) {
         std::vector<float> s;
         rotator_signs(d.dim, d.seed, d.rounds, s);
@@ -352,6 +375,8 @@ extern "C" int bv_index_destroy(bv_index *idx) {
 }
 
 extern "C" int bv_index_size(const bv_index *idx, uint64_t *rows) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     if (!idx || !rows) return fail(BV_E_INVALID, "null argument");
     *rows = idx->rows;
     return BV_OK;
@@ -372,36 +397,45 @@ static double mb32_draw(uint32_t &a) { return (double)mb32_next(a) / 4294967296.
 // src/index/ivf.ts:175-187): per row in order, the next free slot while the
 // sample is filling, else slot floor(rng() * (seen + 1)) when below the
 // capacity.  Only the last row written to a slot within the batch keeps it
-// (earlier ones would be overwritten in order).  Slots go to the device in
-// idx->ivf_slot (count ints); the sample buffer grows to the slots in use.
-static int ivf_reservoir(bv_index *idx, uint64_t base, uint64_t count, std::vector<int32_t> &slots) {
-    slots.assign(count, -1);
+// (earlier ones would be overwritten in order).  The plan is drawn on a copy
+// of the sampler state; ivf_commit applies it once the append can no longer
+// fail, so a failed append leaves the sample as it was.
+struct ReservoirPlan {
+    uint64_t filled, seen;
+    uint32_t rng;
+    std::vector<int32_t> slots;
+};
+
+static void ivf_plan(const bv_index *idx, uint64_t count, ReservoirPlan &pl) {
+    pl.filled = idx->sample_filled;
+    pl.seen = idx->sample_seen;
+    pl.rng = idx->sample_rng;
+    pl.slots.assign(count, -1);
     for (uint64_t i = 0; i < count; ++i) {
-        if (idx->sample_filled < idx->sample_cap) {
-            slots[i] = (int32_t)idx->sample_filled++;
+        if (pl.filled < idx->sample_cap) {
+            pl.slots[i] = (int32_t)pl.filled++;
         } else {
-            const uint64_t j = (uint64_t)std::floor(mb32_draw(idx->sample_rng) * (double)(idx->sample_seen + 1));
-            if (j < idx->sample_cap) slots[i] = (int32_t)j;
+            const uint64_t j = (uint64_t)std::floor(mb32_draw(pl.rng) * (double)(pl.seen + 1));
+            if (j < idx->sample_cap) pl.slots[i] = (int32_t)j;
         }
-        idx->sample_seen++;
+        pl.seen++;
     }
     std::vector<uint8_t> taken(idx->sample_cap, 0);
     for (uint64_t i = count; i-- > 0;) {
-        if (slots[i] < 0) continue;
-        if (taken[slots[i]]) slots[i] = -1;
-        else taken[slots[i]] = 1;
+        if (pl.slots[i] < 0) continue;
+        if (taken[pl.slots[i]]) pl.slots[i] = -1;
+        else taken[pl.slots[i]] = 1;
     }
+}
+
+static void ivf_commit(bv_index *idx, uint64_t base, const ReservoirPlan &pl) {
+    idx->sample_filled = pl.filled;
+    idx->sample_seen = pl.seen;
+    idx->sample_rng = pl.rng;
     if (idx->sample_row.size() < idx->sample_filled) idx->sample_row.resize(idx->sample_filled);
-    for (uint64_t i = 0; i < count; ++i)
-        if (slots[i] >= 0) idx->sample_row[(uint32_t)slots[i]] = base + i;
-    const size_t rb = (size_t)idx->sample_dim * 4;
-    HIPX(idx->dev, idx->sample.ensure(idx->sample_filled * rb, idx->sample.cap, idx->stream), "sample buffer");
-    HIPX(idx->dev, idx->ivf_slot.ensure(count * 4, 0, idx->stream), "scratch");
-    HIPX(idx->dev, hipMemcpyAsync(idx->ivf_slot.p, slots.data(), count * 4, hipMemcpyHostToDevice, idx->stream),
-         "upload");
-    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "upload");
+    for (uint64_t i = 0; i < pl.slots.size(); ++i)
+        if (pl.slots[i] >= 0) idx->sample_row[(uint32_t)pl.slots[i]] = base + i;
     idx->built_rows = ~0ull;  // lists are stale after any append (ivfquant.ts:462)
-    return BV_OK;
 }
 
 // fp32 IVF: the sampled rows themselves go to their slots.
@@ -454,26 +488,56 @@ static int encode_range(bv_index *idx, uint64_t first, uint64_t count, const int
     return BV_OK;
 }
 
+// Append: every allocation happens first, so a failure (or an injected one)
+// leaves the index exactly as it was; then the rows are copied, the reservoir
+// plan is committed and the rows are encoded.
 static int append_common(bv_index *idx, const float *data, bool device_src, uint64_t count) {
     const uint64_t base = idx->rows, total = base + count;
     const size_t rb = (size_t)idx->dim * 4;
+    if (idx->dev->inject_append_oom) {
+        idx->dev->inject_append_oom = false;
+        return fail(BV_E_OOM, "row buffer: out of device memory");
+    }
+    ReservoirPlan plan;
+    if (idx->ivf) ivf_plan(idx, count, plan);
     HIPX(idx->dev, idx->raw.ensure(total * rb, base * rb, idx->stream), "row buffer");
+    if (idx->quant) {
+        HIPX(idx->dev, idx->codes.ensure(total * idx->row_bytes, base * idx->row_bytes, idx->stream), "code buffer");
+        HIPX(idx->dev, idx->scales.ensure(total * 4, base * 4, idx->stream), "scale buffer");
+    }
+    const bool norms = !idx->quant && !idx->ivf;  // flat fp32: the exact batch's error bound needs them
+    if (norms) HIPX(idx->dev, idx->rsq.ensure(total * 4, base * 4, idx->stream), "norm buffer");
+    if (idx->ivf) {
+        HIPX(idx->dev, idx->sample.ensure(plan.filled * (size_t)idx->sample_dim * 4, idx->sample.cap, idx->stream),
+             "sample buffer");
+        HIPX(idx->dev, idx->ivf_slot.ensure(count * 4, 0, idx->stream), "scratch");
+        if (!idx->quant) {  // fp32 kinds copy the sampled rows by index lists
+            size_t taken = 0;
+            for (int32_t s : plan.slots) taken += s >= 0;
+            HIPX(idx->dev, idx->ivf_idx.ensure(std::max<size_t>(taken, 1) * 4, 0, idx->stream), "scratch");
+            HIPX(idx->dev, idx->ivf_idx2.ensure(std::max<size_t>(taken, 1) * 4, 0, idx->stream), "scratch");
+        }
+    }
     HIPX(idx->dev,
          hipMemcpyAsync(idx->raw.as<char>() + base * rb, data, count * rb,
                         device_src ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, idx->stream),
          "row upload");
-    std::vector<int32_t> slots;
     if (idx->ivf) {
-        int rc = ivf_reservoir(idx, base, count, slots);
-        if (rc) return rc;
+        HIPX(idx->dev,
+             hipMemcpyAsync(idx->ivf_slot.p, plan.slots.data(), count * 4, hipMemcpyHostToDevice, idx->stream),
+             "upload");
+        ivf_commit(idx, base, plan);
     }
+    if (norms)
+        HIPX(idx->dev,
+             launch_row_sqnorms(idx->raw.as<float>() + base * idx->dim, count, idx->dim, idx->rsq.as<float>() + base,
+                                idx->rsq_max.as<uint32_t>(), idx->stream),
+             "norm kernel");
     if (idx->quant) {
-        HIPX(idx->dev, idx->codes.ensure(total * idx->row_bytes, base * idx->row_bytes, idx->stream), "code buffer");
-        HIPX(idx->dev, idx->scales.ensure(total * 4, base * 4, idx->stream), "scale buffer");
         int rc = encode_range(idx, base, count, idx->ivf ? idx->ivf_slot.as<int32_t>() : nullptr);
         if (rc) return rc;
     } else if (idx->ivf) {
-        int rc = ivf_sample_raw(idx, base, slots);
+        int rc = ivf_sample_raw(idx, base, plan.slots);
         if (rc) return rc;
     }
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "append");
@@ -482,6 +546,8 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
 }
 
 extern "C" int bv_index_append(bv_index *idx, const float *data, uint64_t n_floats, uint64_t count) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (n_floats != count * idx->dim)
@@ -494,6 +560,8 @@ extern "C" int bv_index_append(bv_index *idx, const float *data, uint64_t n_floa
 }
 
 extern "C" int bv_index_append_device(bv_index *idx, const float *d_data, uint64_t count) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (count == 0) return BV_OK;
@@ -547,18 +615,18 @@ static int ivf_tune(bv_index *idx, const uint32_t *d_assign) {
     }
     const float *d_q = idx->tune_q.as<float>();
     // the top k+1 over every row
-    HIPX(idx->dev, idx->out_rows.ensure((size_t)nq * k1 * 4, 0, s), "output buffer");
-    HIPX(idx->dev, idx->out_scores.ensure((size_t)nq * k1 * 4, 0, s), "output buffer");
-    HIPX(idx->dev, idx->out_n.ensure((size_t)nq * 4, 0, s), "output buffer");
+    HIPX(idx->dev, idx->tune_rows.ensure((size_t)nq * k1 * 4, 0, s), "output buffer");
+    HIPX(idx->dev, idx->tune_scores.ensure((size_t)nq * k1 * 4, 0, s), "output buffer");
+    HIPX(idx->dev, idx->tune_n.ensure((size_t)nq * 4, 0, s), "output buffer");
     idx->ivf = false;
-    int rc = run_fused(idx, d_q, nq, k1, k1, false, nullptr, 0, idx->out_rows.as<uint32_t>(),
-                       idx->out_scores.as<float>(), idx->out_n.as<uint32_t>());
+    int rc = run_fused(idx, d_q, nq, k1, k1, false, nullptr, 0, idx->tune_rows.as<uint32_t>(),
+                       idx->tune_scores.as<float>(), idx->tune_n.as<uint32_t>());
     idx->ivf = true;
     if (rc) return rc;
     // probe scores of the rotated queries against every centroid
     const float *qrot = d_q;
     if (idx->quant) {
-        HIPX(idx->dev, idx->qrot.ensure((size_t)nq * idx->P * 4, 0, s), "query buffer");
+        HIPX(idx->dev, idx->tune_rot.ensure((size_t)nq * idx->P * 4, 0, s), "query buffer");
         EncodeArgs e{};
         e.src = d_q;
         e.rows = nq;
@@ -566,9 +634,9 @@ static int ivf_tune(bv_index *idx, const uint32_t *d_assign) {
         e.P = idx->P;
         e.signs = idx->signs.as<float>();
         e.rounds = idx->d.rounds;
-        e.rotated = idx->qrot.as<float>();
+        e.rotated = idx->tune_rot.as<float>();
         HIPX(idx->dev, launch_encode(e, s), "query rotate kernel");
-        qrot = idx->qrot.as<float>();
+        qrot = idx->tune_rot.as<float>();
     }
     HIPX(idx->dev, idx->probe_scores.ensure((size_t)nq * nlist * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->probes.ensure((size_t)nq * 4, 0, s), "scratch");
@@ -583,8 +651,8 @@ static int ivf_tune(bv_index *idx, const uint32_t *d_assign) {
     HIPX(idx->dev, ivf_launch_probes(pa, nq, s), "probe kernels");
     std::vector<uint32_t> gt((size_t)nq * k1), gtn(nq), assign(rows);
     std::vector<float> ps((size_t)nq * nlist);
-    HIPX(idx->dev, hipMemcpyAsync(gt.data(), idx->out_rows.p, gt.size() * 4, hipMemcpyDeviceToHost, s), "download");
-    HIPX(idx->dev, hipMemcpyAsync(gtn.data(), idx->out_n.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipMemcpyAsync(gt.data(), idx->tune_rows.p, gt.size() * 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipMemcpyAsync(gtn.data(), idx->tune_n.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s), "download");
     HIPX(idx->dev, hipMemcpyAsync(ps.data(), idx->probe_scores.p, ps.size() * 4, hipMemcpyDeviceToHost, s),
          "download");
     HIPX(idx->dev, hipMemcpyAsync(assign.data(), d_assign, rows * 4, hipMemcpyDeviceToHost, s), "download");
@@ -743,6 +811,14 @@ static int ivf_build(bv_index *idx) {
     return BV_OK;
 }
 
+// The lazy build of the reference's first query after an append
+// (ivfquant.ts:461-463).  Query entry points call it before they take any
+// scratch or output pointer: the build grows and reuses buffers.
+static int ensure_built(bv_index *idx) {
+    if (!idx->ivf || idx->rows == 0 || idx->built_rows == idx->rows) return BV_OK;
+    return ivf_build(idx);
+}
+
 // nprobe for the next query (ivfquant.ts:159-162, 487-491): the per-query
 // override (consumed once), else the configured one, else the tuned one,
 // else 5% of nlist.
@@ -759,15 +835,13 @@ static uint32_t ivf_resolve_nprobe(bv_index *idx) {
 // Probes + gathered candidate lists for nq device queries (original space).
 // Returns the per-query candidate bound used to size the scan.
 static int ivf_candidates(bv_index *idx, const float *d_q, uint32_t nq, uint64_t *max_per_query) {
-    if (idx->built_rows != idx->rows) {
-        int rc = ivf_build(idx);
-        if (rc) return rc;
-    }
+    // every query entry point builds before it takes any buffer pointer
+    if (idx->built_rows != idx->rows) return fail(BV_E_STATE, "IVF lists are stale");
     hipStream_t s = idx->stream;
     const uint32_t nprobe = ivf_resolve_nprobe(idx);
     const float *qrot = d_q;
     if (idx->quant) {  // pickProbes scores the rotated query
-        HIPX(idx->dev, idx->qrot.ensure((size_t)nq * idx->P * 4, 0, s), "query buffer");
+        HIPX(idx->dev, idx->ivf_qrot.ensure((size_t)nq * idx->P * 4, 0, s), "query buffer");
         EncodeArgs e{};
         e.src = d_q;
         e.rows = nq;
@@ -776,9 +850,9 @@ static int ivf_candidates(bv_index *idx, const float *d_q, uint32_t nq, uint64_t
         e.signs = idx->signs.as<float>();
         e.rounds = idx->d.rounds;
         e.bits = 0;
-        e.rotated = idx->qrot.as<float>();
+        e.rotated = idx->ivf_qrot.as<float>();
         HIPX(idx->dev, launch_encode(e, s), "query rotate kernel");
-        qrot = idx->qrot.as<float>();
+        qrot = idx->ivf_qrot.as<float>();
     }
     HIPX(idx->dev, idx->probe_scores.ensure((size_t)nq * idx->nlist * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->probes.ensure((size_t)nq * nprobe * 4, 0, s), "scratch");
@@ -1009,7 +1083,11 @@ constexpr uint32_t MQ_MIN_Q = 8;  // smallest batch for the matrix-core path
 
 static bool mq_eligible(const bv_index *idx, uint32_t nq, const uint32_t *d_mask) {
     if (idx->ivf || d_mask || nq < MQ_MIN_Q || idx->rows == 0) return false;
-    if (!idx->quant) return idx->codec == C_F32DOT && mq_f32_supported(idx->dim);  // dot / cosine
+    // fp32: dot / cosine / l2 above the sample size (smaller corpora: one fused
+    // launch for the whole batch is already exact and cheap)
+    if (!idx->quant)
+        return (idx->codec == C_F32DOT || idx->codec == C_F32L2) && mq_f32_supported(idx->dim) &&
+               idx->rows > MQ_SAMPLE;
     const uint32_t u16 = idx->P / 16;  // 16-code units per row
     return (idx->codec == C_Q8 || idx->codec == C_Q4) && u16 >= 2 && (u16 % 2) == 0 && u16 / 2 <= MQ_MAX_STEPS;
 }
@@ -1052,8 +1130,119 @@ static uint32_t mq_groups(const bv_index *idx, uint32_t qblocks) {
     return g ? g : 1u;
 }
 
+// fp32 batches, exactly equal to single queries.  The matrix-core scan is a
+// prefilter: a dense pass over MQ_SAMPLE strided rows gives each query a
+// bound (its kprime-th best sample score), a pass over every row keeps the
+// ids of the rows whose matrix-core score reaches the bound minus the
+// slack 2E (E bounds the difference between a matrix-core score and the
+// single-query scan's), and the fused scan re-scores exactly those rows in
+// indexed mode with the single-query arithmetic and selects the top-k of the
+// same keys.  A query whose kept rows overflow their buffer runs the fused
+// scan over every row.
+static int run_batched_f32(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out,
+                           uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
+    const uint64_t N = idx->rows, S = MQ_SAMPLE;  // N > S (mq_eligible)
+    const bool l2 = idx->codec == C_F32L2;
+    uint64_t cap = std::max<uint64_t>(S, 4ull * kprime * ((N + S - 1) / S));
+    cap = std::min<uint64_t>(cap, N);
+    hipStream_t s = idx->stream;
+    HIPX(idx->dev, idx->mq_cand.ensure((size_t)nq * std::max<uint64_t>(cap, S) * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_rows.ensure((size_t)nq * cap * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_cnt.ensure((size_t)nq * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_tau.ensure((size_t)nq * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_qsq.ensure((size_t)nq * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_slack.ensure((size_t)nq * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->h_cnt.ensure((size_t)nq * 4), "pinned buffer");
+
+    timing_begin(idx);
+    HIPX(idx->dev,
+         launch_mq_f32_qconst(d_q, nq, idx->dim, idx->rsq_max.as<uint32_t>(), l2 ? 1 : 0, idx->mq_qsq.as<float>(),
+                              idx->mq_slack.as<float>(), s),
+         "query norm kernel");
+    MqArgs m{};
+    m.codes = idx->raw.as<uint32_t>();
+    m.W = idx->dim;
+    m.units = idx->dim / 8;
+    m.qlev = (const unsigned char *)d_q;
+    m.qstride = (uint64_t)idx->dim * 4;
+    m.nq = nq;
+    m.qblocks = (nq + MQ_QB - 1) / MQ_QB;
+    m.groups = mq_groups(idx, m.qblocks);
+    m.cand = idx->mq_cand.as<uint64_t>();
+    m.cnt = idx->mq_cnt.as<uint32_t>();
+    m.cap = std::max<uint64_t>(cap, S);
+    m.l2 = l2 ? 1 : 0;
+    m.rsq = idx->rsq.as<float>();
+    m.qsq = idx->mq_qsq.as<float>();
+    m.slack = idx->mq_slack.as<float>();
+    // sample pass: every (approximate) key of logical rows i < S
+    m.n = S;
+    m.row_step = N / S;
+    HIPX(idx->dev, hipMemsetD32Async((hipDeviceptr_t)idx->mq_cnt.p, (int)S, nq, s), "scratch");
+    HIPX(idx->dev, launch_mq_scan_f32(m, s), "batched scan kernel");
+    MqSelArgs sa{};
+    sa.cand = m.cand;
+    sa.cnt = m.cnt;
+    sa.cap = m.cap;
+    sa.kk = kprime;
+    sa.tau = idx->mq_tau.as<uint64_t>();
+    HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+    // full pass: ids of every row that can rank
+    HIPX(idx->dev, hipMemsetAsync(idx->mq_cnt.p, 0, (size_t)nq * 4, s), "scratch");
+    m.n = N;
+    m.row_step = 1;
+    m.tau = idx->mq_tau.as<uint64_t>();
+    m.cap = cap;
+    m.rows_out = idx->mq_rows.as<uint32_t>();
+    HIPX(idx->dev, launch_mq_scan_f32(m, s), "batched scan kernel");
+    HIPX(idx->dev, hipMemcpyAsync(idx->h_cnt.p, idx->mq_cnt.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s),
+         "count download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "batched scan");
+    const uint32_t *cnt = (const uint32_t *)idx->h_cnt.p;
+    uint64_t most = 1;
+    for (uint32_t i = 0; i < nq; i++) most = std::max<uint64_t>(most, std::min<uint64_t>(cnt[i], cap));
+    // exact re-score of the kept rows: the fused scan in indexed mode
+    ScanArgs a{};
+    const uint32_t grid = grid_for(idx, most);
+    int rc = scan_scratch(idx, nq, grid, kprime, 0, a);
+    if (rc) return rc;
+    a.codes = idx->raw.p;
+    a.row_bytes = idx->row_bytes;
+    a.units = idx->units;
+    a.padded_dim = idx->P;
+    a.scale_mul = 1.0f;
+    a.q = d_q;
+    a.q_stride = (uint64_t)idx->dim * 4;
+    a.cand = idx->mq_rows.as<uint32_t>();
+    a.cand_n = idx->mq_cnt.as<uint32_t>();
+    a.cand_stride = cap;
+    a.n = cap;
+    a.kprime = kprime;
+    a.grid = grid;
+    a.k_out = k_out;
+    a.out_rows = d_rows;
+    a.out_scores = d_scores;
+    a.out_n = d_n;
+    HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, s), "scan kernel");
+    timing_end(idx);
+    uint64_t scanned = N + S;
+    for (uint32_t i = 0; i < nq; i++) scanned += std::min<uint64_t>(cnt[i], cap);
+    idx->last_scanned = scanned;
+    // queries whose kept rows overflowed: the fused scan over every row
+    std::vector<uint32_t> over;
+    for (uint32_t i = 0; i < nq; i++)
+        if (cnt[i] > cap) over.push_back(i);
+    for (uint32_t i : over) {
+        rc = run_fused(idx, d_q + (size_t)i * idx->dim, 1, kprime, k_out, false, nullptr, 0,
+                       d_rows + (size_t)i * k_out, d_scores + (size_t)i * k_out, d_n + i);
+        if (rc) return rc;
+    }
+    return BV_OK;
+}
+
 static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                        uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
+    if (!idx->quant) return run_batched_f32(idx, d_q, nq, kprime, k_out, d_rows, d_scores, d_n);
     const unsigned char *qscan = (const unsigned char *)d_q;  // fp32 rows: the queries as they are
     uint64_t qstride = (uint64_t)idx->dim * 4;
     int rc = BV_OK;
@@ -1187,6 +1376,8 @@ static int host_query(bv_index *idx, const float *q, uint32_t nq, uint32_t kprim
         idx->last_query_gpu_ms = 0;
         return BV_OK;
     }
+    int rc = ensure_built(idx);
+    if (rc) return rc;
     const size_t qbytes = (size_t)nq * idx->dim * 4;
     HIPX(idx->dev, idx->qin.ensure(qbytes, 0, idx->stream), "query buffer");
     HIPX(idx->dev, hipEventRecord(idx->ev0, idx->stream), "event");
@@ -1203,8 +1394,8 @@ static int host_query(bv_index *idx, const float *q, uint32_t nq, uint32_t kprim
     HIPX(idx->dev, idx->out_rows.ensure((size_t)nq * k_out * 4, 0, idx->stream), "output buffer");
     HIPX(idx->dev, idx->out_scores.ensure((size_t)nq * k_out * 4, 0, idx->stream), "output buffer");
     HIPX(idx->dev, idx->out_n.ensure((size_t)nq * 4, 0, idx->stream), "output buffer");
-    int rc = run_pipeline(idx, idx->qin.as<float>(), nq, kprime, k_out, rerank, d_mask, mask_bits,
-                          idx->out_rows.as<uint32_t>(), idx->out_scores.as<float>(), idx->out_n.as<uint32_t>());
+    rc = run_pipeline(idx, idx->qin.as<float>(), nq, kprime, k_out, rerank, d_mask, mask_bits,
+                      idx->out_rows.as<uint32_t>(), idx->out_scores.as<float>(), idx->out_n.as<uint32_t>());
     if (rc) return rc;
     HIPX(idx->dev, idx->h_rows.ensure((size_t)nq * k_out * 4), "pinned buffer");
     HIPX(idx->dev, idx->h_scores.ensure((size_t)nq * k_out * 4), "pinned buffer");
@@ -1234,6 +1425,8 @@ static int host_query_dense(bv_index *idx, const float *q, uint32_t nq, uint32_t
 
 extern "C" int bv_index_query(bv_index *idx, const float *q, uint32_t k, uint32_t *rows, float *scores,
                               uint32_t *n_out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (!q || !n_out || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
@@ -1244,6 +1437,8 @@ extern "C" int bv_index_query(bv_index *idx, const float *q, uint32_t k, uint32_
 
 extern "C" int bv_index_query_masked(bv_index *idx, const float *q, uint32_t k, const uint32_t *mask_words,
                                      uint64_t n_words, uint32_t *rows, float *scores, uint32_t *n_out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (!q || !n_out || !mask_words || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
@@ -1258,6 +1453,8 @@ extern "C" int bv_index_query_masked(bv_index *idx, const float *q, uint32_t k, 
 
 extern "C" int bv_index_query_batch(bv_index *idx, const float *queries, uint32_t nq, uint32_t k, uint32_t *rows,
                                     float *scores, uint32_t *n_out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (nq == 0) return BV_OK;
@@ -1292,12 +1489,16 @@ extern "C" int bv_index_query_batch(bv_index *idx, const float *queries, uint32_
 
 extern "C" int bv_index_set_nprobe(bv_index *idx, uint32_t nprobe) {
     if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
+    if (!idx) return fail(BV_E_INVALID, "null index");
     idx->nprobe_override = nprobe;
     return BV_OK;
 }
 
 extern "C" int bv_index_search(bv_index *idx, const float *queries, uint32_t nq, uint32_t fetch, uint32_t k,
                                uint32_t *rows, float *scores, uint32_t *n_out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (nq == 0) return BV_OK;
@@ -1325,6 +1526,8 @@ extern "C" int bv_index_search(bv_index *idx, const float *queries, uint32_t nq,
 
 extern "C" int bv_index_search_device(bv_index *idx, const float *d_queries, uint32_t nq, uint32_t fetch, uint32_t k,
                                       uint32_t *d_rows, float *d_scores, uint32_t *d_n_out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (nq == 0) return BV_OK;
@@ -1335,10 +1538,14 @@ extern "C" int bv_index_search_device(bv_index *idx, const float *d_queries, uin
     const uint32_t fe = fetch ? (uint32_t)std::min<uint64_t>(std::max(fetch, kk), idx->rows) : 0;
     if (fe > (uint32_t)MAX_KPRIME || kk > (uint32_t)MAX_KPRIME)
         return fail(BV_E_UNSUPPORTED, "fetch %u exceeds the fused top-k limit %d", fe, MAX_KPRIME);
+    rc = ensure_built(idx);
+    if (rc) return rc;
     return run_pipeline(idx, d_queries, nq, fe ? fe : kk, kk, fe != 0, nullptr, 0, d_rows, d_scores, d_n_out);
 }
 
 extern "C" int bv_index_sync(bv_index *idx) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "sync");
@@ -1346,12 +1553,16 @@ extern "C" int bv_index_sync(bv_index *idx) {
 }
 
 extern "C" int bv_index_stream(bv_index *idx, void **stream) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     if (!idx || !stream) return fail(BV_E_INVALID, "null argument");
     *stream = (void *)idx->stream;
     return BV_OK;
 }
 
 extern "C" int bv_index_kernel_timing(bv_index *idx, int enable, double *scan_ms, uint64_t *scan_launches) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     if (!idx) return fail(BV_E_INVALID, "null index");
     timing_collect(idx);
     if (enable) {
@@ -1368,6 +1579,8 @@ extern "C" int bv_index_kernel_timing(bv_index *idx, int enable, double *scan_ms
 
 extern "C" int bv_index_rerank(bv_index *idx, const float *q, const uint32_t *cand, uint32_t n_cand, uint32_t k,
                                uint32_t *rows, float *scores, uint32_t *n_out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (!q || !n_out || (n_cand && !cand) || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
@@ -1490,6 +1703,8 @@ static int host_query_dense(bv_index *idx, const float *q, uint32_t nq, uint32_t
 
 // ------------------------------------------------------------ stats/exports
 extern "C" int bv_index_get_stats(bv_index *idx, bv_index_stats *out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     if (!idx || !out) return fail(BV_E_INVALID, "null argument");
     std::memset(out, 0, sizeof *out);
     out->rows = idx->rows;
@@ -1518,6 +1733,8 @@ extern "C" int bv_index_get_stats(bv_index *idx, bv_index_stats *out) {
 }
 
 extern "C" int bv_index_export_codes(bv_index *idx, uint64_t row0, uint64_t count, uint32_t *words, float *scales) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (!idx->quant) return fail(BV_E_STATE, "not a quantized index");
@@ -1532,6 +1749,8 @@ extern "C" int bv_index_export_codes(bv_index *idx, uint64_t row0, uint64_t coun
 }
 
 extern "C" int bv_index_export_scores(bv_index *idx, const float *q, float *scores) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (!q || !scores) return fail(BV_E_INVALID, "null argument");
@@ -1540,6 +1759,8 @@ extern "C" int bv_index_export_scores(bv_index *idx, const float *q, float *scor
 }
 
 extern "C" int bv_index_export_rotated_query(bv_index *idx, const float *q, float *rotated) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (!idx->quant) return fail(BV_E_STATE, "not a quantized index");
@@ -1558,6 +1779,8 @@ extern "C" int bv_index_export_rotated_query(bv_index *idx, const float *q, floa
 }
 
 extern "C" int bv_index_build(bv_index *idx) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (!idx->ivf) return BV_OK;
@@ -1566,7 +1789,55 @@ extern "C" int bv_index_build(bv_index *idx) {
     return ivf_build(idx);
 }
 
+extern "C" int bv_index_export_probe_scores(bv_index *idx, const float *queries, uint32_t nq, float *scores) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!idx->ivf) return fail(BV_E_STATE, "not an IVF index");
+    if (nq == 0) return BV_OK;
+    if (!queries || !scores) return fail(BV_E_INVALID, "null argument");
+    if (idx->rows == 0) return fail(BV_E_STATE, "IVF build needs rows");
+    rc = ensure_built(idx);
+    if (rc) return rc;
+    hipStream_t s = idx->stream;
+    const size_t qb = (size_t)nq * idx->dim * 4;
+    HIPX(idx->dev, idx->qin.ensure(qb, 0, s), "query buffer");
+    HIPX(idx->dev, hipMemcpyAsync(idx->qin.p, queries, qb, hipMemcpyHostToDevice, s), "upload");
+    const float *qrot = idx->qin.as<float>();
+    if (idx->quant) {
+        HIPX(idx->dev, idx->ivf_qrot.ensure((size_t)nq * idx->P * 4, 0, s), "query buffer");
+        EncodeArgs e{};
+        e.src = idx->qin.as<float>();
+        e.rows = nq;
+        e.dim = idx->dim;
+        e.P = idx->P;
+        e.signs = idx->signs.as<float>();
+        e.rounds = idx->d.rounds;
+        e.rotated = idx->ivf_qrot.as<float>();
+        HIPX(idx->dev, launch_encode(e, s), "query rotate kernel");
+        qrot = idx->ivf_qrot.as<float>();
+    }
+    HIPX(idx->dev, idx->probe_scores.ensure((size_t)nq * idx->nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->probes.ensure((size_t)nq * 4, 0, s), "scratch");
+    IvfProbeArgs pa{};
+    pa.centroids = idx->centroids.as<float>();
+    pa.nlist = idx->nlist;
+    pa.P = idx->sample_dim;
+    pa.qrot = qrot;
+    pa.scores = idx->probe_scores.as<float>();
+    pa.nprobe = 1;
+    pa.probes = idx->probes.as<uint32_t>();
+    HIPX(idx->dev, ivf_launch_probes(pa, nq, s), "probe kernels");
+    HIPX(idx->dev, hipMemcpyAsync(scores, idx->probe_scores.p, (size_t)nq * idx->nlist * 4, hipMemcpyDeviceToHost, s),
+         "download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "probe scores");
+    return BV_OK;
+}
+
 extern "C" int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *list_off, uint32_t *list_rows) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
     if (!idx->ivf) return fail(BV_E_STATE, "not an IVF index");

@@ -69,6 +69,8 @@ struct ScanArgs {
     uint32_t rounds;
     const uint32_t *cand;     // indexed mode: row ids (null = rows 0..n-1)
     const uint64_t *cand_off; // per-query offsets into cand (nq+1) or null
+    const uint32_t *cand_n;   // or: per-query counts, query q's ids at cand + q * cand_stride
+    uint64_t cand_stride;
     const uint32_t *mask;     // row filter bits (LSB-first) or null
     uint64_t mask_bits;
     uint64_t n;               // rows per query when cand_off is null
@@ -222,7 +224,26 @@ struct MqArgs {
     uint64_t *cand;           // [nq][cap]
     uint32_t *cnt;            // [nq] appended keys (threshold pass)
     uint64_t cap;
+    // fp32 rows only.  l2: score 2 x.q - |x|^2 - |q|^2 (rsq per row, qsq per
+    // query) instead of x.q.  rows_out: the threshold pass appends the ids of
+    // rows whose score reaches tau's score minus slack[q] ([nq][cap] u32)
+    // instead of keys: a superset of the rows that can rank in the exact scan.
+    int l2;
+    const float *rsq;
+    const float *qsq;
+    const float *slack;
+    uint32_t *rows_out;
 };
+// Per-row squared norms of fp32 rows (f64 sums rounded to f32) and, in
+// *max_bits, the largest of them (float bits, rounded up; rsq >= 0 so the
+// bits order like the values).
+hipError_t launch_row_sqnorms(const float *rows, uint64_t n, uint32_t dim, float *rsq, uint32_t *max_bits,
+                              hipStream_t s);
+// Per-query constants of the exact fp32 batch: qsq = |q|^2 and the slack
+// 2E, where E bounds |matrix-core score - single-query score| for every row:
+// dot 3(dim+2)u |x|max |q|, l2 4(dim+4)u (|x|max + |q|)^2 (u = 2^-24).
+hipError_t launch_mq_f32_qconst(const float *q, uint32_t nq, uint32_t dim, const uint32_t *max_bits, int l2,
+                                float *qsq, float *slack, hipStream_t s);
 // Per query: the best kk keys of cand[q][0, min(cnt[q], cap)).  Outputs are
 // optional: tau = the kk-th best key (0 when there are kk or fewer), the
 // selected keys (merged, merged_n), overflow = cnt[q] > cap, and the selected

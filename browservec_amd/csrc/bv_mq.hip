@@ -9,9 +9,13 @@
 //                distanceQ4 dispatches + score buffers for query batches
 //                (src/engine/wgsl/distanceQ8.ts:56-82, distanceQ4.ts:44-78,
 //                src/index/quant.ts:178-245, src/index.ts:473-517).
-//   mq_scan_f32  fp32 rows x fp32 queries (dot / cosine) on
+//   mq_scan_f32  fp32 rows x fp32 queries (dot / cosine / l2) on
 //                v_mfma_f32_32x32x2f32 (src/engine/wgsl/distance.ts:24-177,
-//                src/index/flat.ts:132-200 for query batches).
+//                src/index/flat.ts:132-200 for query batches).  Its scores
+//                are within a proven bound of the single-query scan's, and
+//                serve as a prefilter: the rows that can rank are re-scored
+//                by the single-query scan's own arithmetic, so a batch
+//                returns exactly the single-query results.
 //   mq_select    exact selection of each query's best kk keys.
 //   mq_rerank    exact f64 re-rank of the selected candidates, 16 per wave.
 //
@@ -61,6 +65,15 @@ __device__ __forceinline__ v4i unpack_q4(uint2 w) {
     r[3] = (int)__builtin_amdgcn_perm(o1, e1, 0x07030602u);
     return r;
 }
+
+// The next float above / below a finite x (bit steps; +-0 go to the
+// smallest subnormal of the right sign).
+__device__ __forceinline__ float next_up(float x) {
+    const uint32_t b = __float_as_uint(x);
+    if ((b & 0x7fffffffu) == 0) return __uint_as_float(1u);
+    return __uint_as_float((b & 0x80000000u) ? b - 1 : b + 1);
+}
+__device__ __forceinline__ float next_down(float x) { return -next_up(-x); }
 
 // Descending bitonic sort of keys[0, npow) (npow a power of two), whole
 // workgroup.
@@ -348,22 +361,32 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan(MqArgs a) {
     }
 }
 
-// fp32 rows x fp32 queries on v_mfma_f32_32x32x2f32 (dot / cosine): the
-// batched counterpart of the fp32 flat scan.  Same structure as mq_scan:
-// the block's 32 queries stay in LDS, each wave streams 64 rows.  Lane
-// l = 32h + c supplies, over the four MFMA steps of chunk t, elements
-// 8t + 4h .. 8t + 4h + 3 of row c (A) and of query c (B), one 16-byte load
-// each, so both operands pair the same elements.  The sum runs in the
-// matrix core's own order (the single-query scan adds in the reference's
-// order; the two agree to float rounding).  a.W = dim (floats per row),
-// a.units = dim / 8 chunks, a.qlev = the fp32 queries, a.qstride their
-// byte stride.
+// fp32 rows x fp32 queries on v_mfma_f32_32x32x2f32: the batched
+// counterpart of the fp32 flat scan.  Same structure as mq_scan: the block's
+// 32 queries stay in LDS, each wave streams 64 rows.  Lane l = 32h + c
+// supplies, over the four MFMA steps of chunk t, elements 8t + 4h .. 8t +
+// 4h + 3 of row c (A) and of query c (B), one 16-byte load each, so both
+// operands pair the same elements.  The sum runs in the matrix core's own
+// order, so a score differs from the single-query scan's by rounding only:
+// at most E (launch_mq_f32_qconst) for every row.  l2 scores are
+// 2 x.q - |x|^2 - |q|^2 from the rows' and queries' squared norms.
+// a.W = dim (floats per row), a.units = dim / 8 chunks, a.qlev = the fp32
+// queries, a.qstride their byte stride.
+//
+// Passes: dense (every key of logical row i at cand[q][i]); threshold with
+// keys (append keys at or above tau[q]); threshold with row ids (rows_out:
+// append every row whose score reaches tau's score minus slack[q], which
+// keeps every row the exact scan can rank: a row in the exact top-kk has
+// single-query score >= the kk-th best single-query score >= tau's score
+// - E, hence matrix-core score >= tau's score - 2E).
 template <int CHUNKS>
 __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_f32(MqArgs a) {
     constexpr int G = CHUNKS < 4 ? CHUNKS : 4;
     __shared__ float4 qlds[CHUNKS][64];
     __shared__ uint64_t qtau[MQ_QB];
     __shared__ float qts[MQ_QB];
+    __shared__ float qn2[MQ_QB];
+    __shared__ float rn2[MQ_WAVES][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = lane >> 5, c = lane & 31;
     const uint32_t b = blockIdx.x, xcd = b & 7u, slot = b >> 3;
@@ -383,8 +406,21 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_f32(MqArgs a) {
         if (q >= a.nq) q = a.nq - 1;
         const uint64_t t = a.tau ? a.tau[q] : 0ull;
         qtau[threadIdx.x] = t;
-        qts[threadIdx.x] = t ? f32_from_ord((uint32_t)(t >> 32)) : -__builtin_inff();
+        float ts = t ? f32_from_ord((uint32_t)(t >> 32)) : -__builtin_inff();
+        if (a.rows_out && t) {
+            // tau's score minus the slack, rounded down
+            const float r = (float)((double)ts - (double)a.slack[q]);
+            ts = next_down(r);
+        }
+        qts[threadIdx.x] = ts;
+        qn2[threadIdx.x] = a.l2 ? a.qsq[q] : 0.0f;
     }
+    auto row_sq = [&](uint64_t t) {
+        uint64_t li = t * MQ_ROWS + (uint64_t)wave * 64 + lane;
+        if (li >= a.n) li = a.n - 1;
+        return a.rsq[li * a.row_step];
+    };
+    float rsq_next = a.l2 ? row_sq(tile) : 0.0f;
     auto row_ptrs = [&](uint64_t t, const float4 *(&ap)[2]) {
         const uint64_t w0 = t * MQ_ROWS + (uint64_t)wave * 64;
 #pragma unroll
@@ -444,10 +480,60 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_f32(MqArgs a) {
 #pragma unroll
                 for (int fr = 0; fr < 2; ++fr) ring[0][j][fr] = ring[1][j][fr];
         }
-        // keys: dense (logical row i at out[i]) or appended at or above tau
+        // l2: the score from the dot and the squared norms (this wave's 64
+        // rows' norms through wave-private LDS)
+        if (a.l2) {
+            rn2[wave][lane] = rsq_next;
+            if (more) rsq_next = row_sq(ntile);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            const float qs2 = qn2[c];
+#pragma unroll
+            for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float x2 = rn2[wave][fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3)];
+                    acc[fr][r] = 2.0f * acc[fr][r] - x2 - qs2;
+                }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        }
+        // keys: dense (logical row i at out[i]), appended at or above tau, or
+        // row ids appended at or above the slackened bound
         const uint64_t w0 = tile * MQ_ROWS + (uint64_t)wave * 64;
         const bool full = w0 + 64 <= a.n;
-        if (!a.tau) {
+        if (a.rows_out) {
+            const float ts = qts[c];
+            uint32_t pass = 0;
+#pragma unroll
+            for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint64_t li = w0 + fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    // a NaN score passes: the exact scan ranks it as it ranks any key
+                    if (qok && (full || li < a.n) && !(acc[fr][r] < ts)) pass |= 1u << (fr * 16 + r);
+                }
+            if (__ballot(pass != 0)) {
+                const uint32_t mine = __popc(pass);
+                const uint32_t other = __shfl_xor(mine, 32);
+                uint32_t base = 0;
+                if (h == 0 && mine + other) base = atomicAdd(&a.cnt[qq], mine + other);
+                base = __shfl(base, c);
+                if (pass) {
+                    uint32_t *ro = a.rows_out + (uint64_t)qq * a.cap;
+                    uint64_t pos = (uint64_t)base + (h ? other : 0u);
+#pragma unroll
+                    for (int fr = 0; fr < 2; ++fr)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            if (pass & (1u << (fr * 16 + r))) {
+                                const uint64_t li = w0 + fr * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                                if (pos < a.cap) ro[pos] = (uint32_t)(li * a.row_step);
+                                ++pos;
+                            }
+                }
+            }
+        } else if (!a.tau) {
 #pragma unroll
             for (int fr = 0; fr < 2; ++fr)
 #pragma unroll
@@ -684,6 +770,69 @@ __global__ __launch_bounds__(RR_THREADS) void mq_rerank(MqRerankArgs a) {
         }
     }
     if (tid == 0) a.out_n[q] = ko;
+}
+
+namespace {
+
+// One wave per row: f64 sum of squares in element order, rounded to f32.
+__global__ __launch_bounds__(256) void row_sqnorms(const float *rows, uint64_t n, uint32_t dim, float *rsq,
+                                                   uint32_t *max_bits) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t nw = (uint64_t)gridDim.x * 4;
+    uint32_t mx = 0;
+    for (uint64_t r = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < n; r += nw) {
+        const float *x = rows + r * dim;
+        double s = 0.0;
+        for (uint32_t i = lane; i < dim; i += 64) s = fma((double)x[i], (double)x[i], s);
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
+        if (lane == 0) {
+            rsq[r] = (float)s;
+            // the bound uses a value no smaller than any row's: round up
+            const float up = next_up((float)s);
+            const uint32_t b = __float_as_uint(up);
+            mx = b > mx ? b : mx;
+        }
+    }
+    if (lane == 0 && mx) atomicMax(max_bits, mx);
+}
+
+// One wave per query: |q|^2 and the slack 2E of the exact fp32 batch.
+__global__ __launch_bounds__(64) void mq_f32_qconst(const float *q, uint32_t dim, const uint32_t *max_bits, int l2,
+                                                    float *qsq, float *slack) {
+    const int lane = threadIdx.x;
+    const float *x = q + (uint64_t)blockIdx.x * dim;
+    double s = 0.0;
+    for (uint32_t i = lane; i < dim; i += 64) s = fma((double)x[i], (double)x[i], s);
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
+    if (lane == 0) {
+        const double u = 0x1p-24;
+        const double xn = sqrt((double)__uint_as_float(*max_bits)) * (1.0 + 0x1p-20);
+        const double qn = sqrt(s) * (1.0 + 0x1p-20);
+        const double e = l2 ? 4.0 * (dim + 4) * u * (xn + qn) * (xn + qn) : 3.0 * (dim + 2) * u * xn * qn;
+        qsq[blockIdx.x] = (float)s;
+        // 2E plus room for the subnormal products a matrix core may flush
+        slack[blockIdx.x] = (float)((2.0 * e + dim * 0x1p-126) * (1.0 + 0x1p-10));
+    }
+}
+
+}  // namespace
+
+hipError_t launch_row_sqnorms(const float *rows, uint64_t n, uint32_t dim, float *rsq, uint32_t *max_bits,
+                              hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    uint64_t blocks = (n + 3) / 4;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(row_sqnorms, dim3((uint32_t)blocks), dim3(256), 0, s, rows, n, dim, rsq, max_bits);
+    return hipGetLastError();
+}
+
+hipError_t launch_mq_f32_qconst(const float *q, uint32_t nq, uint32_t dim, const uint32_t *max_bits, int l2,
+                                float *qsq, float *slack, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    hipLaunchKernelGGL(mq_f32_qconst, dim3(nq), dim3(64), 0, s, q, dim, max_bits, l2, qsq, slack);
+    return hipGetLastError();
 }
 
 hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s) {

@@ -33,6 +33,13 @@ def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+def _check_len(a: np.ndarray, want: int) -> None:
+    """The library reads exactly `want` floats: refuse any other length before
+    a pointer reaches it (the reference's message, src/index/flat.ts:96-98)."""
+    if a.size != want:
+        raise L.BVError(L.BV_E_INVALID, f"expected {want} floats, got {a.size}")
+
+
 class DeviceContext:
     """The engine's DeviceContext (src/engine/device.ts:3-9) over a HIP device."""
 
@@ -54,6 +61,11 @@ class DeviceContext:
         hbm = ctypes.c_uint64()
         L.check(self.lib.bv_device_info(self.handle, name, 256, ctypes.byref(cu), ctypes.byref(hbm)))
         return {"name": name.value.decode(), "cu_count": cu.value, "hbm_bytes": hbm.value}
+
+    def debug_inject(self, what: str) -> None:
+        """Force the device-lost state ('lost') or a failed allocation on the
+        next append ('append_oom') from the host; no device work happens."""
+        L.check(self.lib.bv_debug_inject(self.handle, {"lost": 1, "append_oom": 2}[what]))
 
     def destroy(self) -> None:
         if self.handle:
@@ -117,6 +129,7 @@ class NativeIndex:
 
     def query(self, q, k: int) -> list[FlatHit]:
         q = _f32(q).reshape(-1)
+        _check_len(q, self.dim)
         rows = np.empty(max(k, 1), np.uint32)
         scores = np.empty(max(k, 1), np.float32)
         n = ctypes.c_uint32()
@@ -125,6 +138,7 @@ class NativeIndex:
 
     def query_masked(self, q, k: int, mask_words) -> list[FlatHit]:
         q = _f32(q).reshape(-1)
+        _check_len(q, self.dim)
         m = np.ascontiguousarray(mask_words, dtype=np.uint32)
         rows = np.empty(max(k, 1), np.uint32)
         scores = np.empty(max(k, 1), np.float32)
@@ -135,6 +149,7 @@ class NativeIndex:
 
     def query_batch(self, packed, n: int, k: int) -> list[list[FlatHit]]:
         packed = _f32(packed).reshape(-1)
+        _check_len(packed, int(n) * self.dim)
         rows = np.empty((n, max(k, 1)), np.uint32)
         scores = np.empty((n, max(k, 1)), np.float32)
         cnt = np.empty(max(n, 1), np.uint32)
@@ -155,7 +170,10 @@ class NativeIndex:
         """Approximate top-`fetch` then exact f64 re-rank to top-`k`, on the
         device (BrowserVec.query's quantized path, src/index.ts:414-418).
         Returns (rows[nq,k], scores[nq,k], counts[nq])."""
-        qs = _f32(queries).reshape(-1, self.dim)
+        qs = _f32(queries)
+        if qs.size % self.dim:
+            _check_len(qs, (qs.size // self.dim + 1) * self.dim)
+        qs = qs.reshape(-1, self.dim)
         nq = qs.shape[0]
         rows = np.empty((nq, max(k, 1)), np.uint32)
         scores = np.empty((nq, max(k, 1)), np.float32)
@@ -167,6 +185,7 @@ class NativeIndex:
     def rerank(self, q, cand, k: int) -> list[FlatHit]:
         """BrowserVec.rerankExact on the device (src/index.ts:583-594)."""
         q = _f32(q).reshape(-1)
+        _check_len(q, self.dim)
         c = np.ascontiguousarray(cand, dtype=np.uint32)
         rows = np.empty(max(k, 1), np.uint32)
         scores = np.empty(max(k, 1), np.float32)
@@ -186,6 +205,7 @@ class NativeIndex:
 
     def export_scores(self, q) -> np.ndarray:
         q = _f32(q).reshape(-1)
+        _check_len(q, self.dim)
         out = np.empty(self.size, np.float32)
         L.check(self.lib.bv_index_export_scores(self.handle, _ptr(q), _ptr(out)))
         return out
@@ -244,8 +264,9 @@ class QuantIndex(NativeIndex):
 
     @property
     def ingest_mode(self) -> str:
-        """Where rotate+quantize runs; on this build always the device."""
-        return "device"
+        """ingestMode (src/index/quant.ts:115-118): where rotate+quantize ran,
+        'pending' before the first append."""
+        return "device" if self.size else "pending"
 
     def export_codes(self, row0: int = 0, count: int | None = None):
         count = self.size - row0 if count is None else count
@@ -256,6 +277,7 @@ class QuantIndex(NativeIndex):
 
     def export_rotated_query(self, q) -> np.ndarray:
         q = _f32(q).reshape(-1)
+        _check_len(q, self.dim)
         out = np.empty(self.padded_dim, np.float32)
         L.check(self.lib.bv_index_export_rotated_query(self.handle, _ptr(q), _ptr(out)))
         return out
@@ -274,6 +296,12 @@ class IVFIndex(NativeIndex):
     def build(self) -> None:
         L.check(self.lib.bv_index_build(self.handle))
 
+    @property
+    def train_mode(self) -> str:
+        """trainMode (src/index/ivf.ts:133-135): where the k-means mean update
+        ran, 'pending' before a build."""
+        return "device" if self.stats()["nlist"] else "pending"
+
     def export_ivf(self):
         """(centroids [nlist, D], list offsets [nlist+1], list rows [rows])."""
         self.build()
@@ -285,6 +313,16 @@ class IVFIndex(NativeIndex):
         rows = np.empty(max(self.size, 1), np.uint32)
         L.check(self.lib.bv_index_export_ivf(self.handle, _ptr(cen), _ptr(off), _ptr(rows)))
         return cen, off, rows[: self.size]
+
+    def export_probe_scores(self, queries) -> np.ndarray:
+        """pickProbes' score of every centroid for each query, [nq, nlist]."""
+        qs = _f32(queries)
+        _check_len(qs, qs.size // self.dim * self.dim if qs.size else self.dim)
+        qs = qs.reshape(-1, self.dim)
+        self.build()
+        out = np.empty((qs.shape[0], self.stats()["nlist"]), np.float32)
+        L.check(self.lib.bv_index_export_probe_scores(self.handle, _ptr(qs), qs.shape[0], _ptr(out)))
+        return out
 
 
 class IVFQuantIndex(IVFIndex):
@@ -299,3 +337,7 @@ class IVFQuantIndex(IVFIndex):
         st = self.stats()
         self.padded_dim = st["padded_dim"]
         self.words_per_row = st["words_per_row"]
+
+    @property
+    def ingest_mode(self) -> str:
+        return "device" if self.size else "pending"

@@ -2,10 +2,18 @@
  * N-API binding of libbrowservec_hip.so for Node (the reference's host
  * runtime).  It exposes the C ABI of include/browservec_hip.h one call per
  * function; index.js builds the reference's VectorIndex seam
- * (src/index/flat.ts:24-40) on top of it.  Failed calls throw an Error whose
- * message is bv_last_error(), as the reference throws `new Error(msg)`.
- * Calls are synchronous: the device work of one call is a few hundred
- * microseconds, below the cost of a thread-pool hop.
+ * (src/index/flat.ts:24-40) on top of it.
+ *
+ * Calls that do device work (append, build, every query) run as
+ * napi_async_work on libuv's thread pool and return a Promise, so a 4M-row
+ * append or an IVF build does not block the event loop; the library
+ * serializes calls on one index.  Input typed arrays are held by references
+ * until the work completes, and results are written straight into typed
+ * arrays created before the work is queued.  A failed call rejects (or, for
+ * the synchronous calls, throws) an Error whose message is bv_last_error()
+ * and whose `code` is the BV_E_* name, as the reference throws
+ * `new Error(msg)`.  Query lengths are checked here against the index
+ * dimension before any pointer reaches the library.
  */
 #define NAPI_VERSION 3
 #include <node_api.h>
@@ -24,16 +32,29 @@
         }                                                                \
     } while (0)
 
+static const char *code_name(int rc) {
+    static const char *names[] = {"BV_OK", "BV_E_INVALID", "BV_E_UNSUPPORTED", "BV_E_DEVICE_LOST",
+                                  "BV_E_OOM", "BV_E_HIP", "BV_E_STATE"};
+    if (rc > 0 && rc < (int)(sizeof names / sizeof names[0])) return names[rc];
+    return "BV_E_UNKNOWN";
+}
+
 static napi_value throw_bv(napi_env env, int rc) {
-    static const char *names[] = {"BV_OK",          "BV_E_INVALID", "BV_E_UNSUPPORTED", "BV_E_DEVICE_LOST",
-                                  "BV_E_OOM",       "BV_E_HIP",     "BV_E_STATE"};
     const char *msg = bv_last_error();
-    char code[24];
-    if (rc > 0 && rc < (int)(sizeof names / sizeof names[0])) snprintf(code, sizeof code, "%s", names[rc]);
-    else snprintf(code, sizeof code, "BV_E_%d", rc);
-    napi_throw_error(env, code, msg && *msg ? msg : "browservec_hip call failed");
+    napi_throw_error(env, code_name(rc), msg && *msg ? msg : "browservec_hip call failed");
     return NULL;
 }
+
+/* An index handle: the library object plus its (immutable) dimension, so
+ * lengths are checked without a library call.  `pending` counts queued
+ * device calls; destroy() on a handle with calls in flight marks it dead and
+ * the last call's completion destroys the index (all on the main thread). */
+typedef struct {
+    bv_index *idx;
+    uint32_t dim;
+    uint32_t pending;
+    int dead;
+} index_handle;
 
 static void *get_ptr(napi_env env, napi_value v) {
     void *p = NULL;
@@ -41,6 +62,11 @@ static void *get_ptr(napi_env env, napi_value v) {
     if (napi_typeof(env, v, &t) != napi_ok || t != napi_external) return NULL;
     napi_get_value_external(env, v, &p);
     return p;
+}
+
+static index_handle *get_index(napi_env env, napi_value v) {
+    index_handle *h = (index_handle *)get_ptr(env, v);
+    return h && h->idx && !h->dead ? h : NULL;
 }
 
 static int get_u32(napi_env env, napi_value v, uint32_t *out) {
@@ -76,6 +102,138 @@ static napi_value new_typed(napi_env env, napi_typedarray_type t, size_t n, size
         return NULL;                                                             \
     }
 
+static napi_value length_error(napi_env env, size_t want, size_t got) {
+    char msg[96];
+    snprintf(msg, sizeof msg, "expected %zu floats, got %zu", want, got);
+    napi_throw_type_error(env, NULL, msg);
+    return NULL;
+}
+
+/* ---- asynchronous device calls --------------------------------------------- */
+typedef enum { OP_APPEND, OP_QUERY, OP_QUERY_MASKED, OP_QUERY_BATCH, OP_SEARCH, OP_RERANK, OP_BUILD } op_kind;
+
+typedef struct {
+    napi_async_work work;
+    napi_deferred deferred;
+    op_kind op;
+    index_handle *h;
+    bv_index *idx;
+    napi_ref keep[3];   /* input arrays and the index handle, held until completion */
+    napi_ref result;    /* result object (queries), or NULL */
+    const float *data;
+    size_t n_floats;
+    uint64_t count;
+    const uint32_t *aux; /* mask words or candidate rows */
+    size_t n_aux;
+    uint32_t nq, k, fetch;
+    uint32_t *rows, *counts;
+    float *scores;
+    int rc;
+    char msg[512];
+} job;
+
+static void job_execute(napi_env env, void *data) {
+    (void)env;
+    job *j = (job *)data;
+    switch (j->op) {
+    case OP_APPEND: j->rc = bv_index_append(j->idx, j->data, j->n_floats, j->count); break;
+    case OP_QUERY: j->rc = bv_index_query(j->idx, j->data, j->k, j->rows, j->scores, j->counts); break;
+    case OP_QUERY_MASKED:
+        j->rc = bv_index_query_masked(j->idx, j->data, j->k, j->aux, j->n_aux, j->rows, j->scores, j->counts);
+        break;
+    case OP_QUERY_BATCH: j->rc = bv_index_query_batch(j->idx, j->data, j->nq, j->k, j->rows, j->scores, j->counts); break;
+    case OP_SEARCH:
+        j->rc = bv_index_search(j->idx, j->data, j->nq, j->fetch, j->k, j->rows, j->scores, j->counts);
+        break;
+    case OP_RERANK:
+        j->rc = bv_index_rerank(j->idx, j->data, j->aux, (uint32_t)j->n_aux, j->k, j->rows, j->scores, j->counts);
+        break;
+    case OP_BUILD: j->rc = bv_index_build(j->idx); break;
+    }
+    /* the message is thread-local: copy it on this thread */
+    if (j->rc) snprintf(j->msg, sizeof j->msg, "%s", bv_last_error());
+}
+
+static void job_complete(napi_env env, napi_status status, void *data) {
+    job *j = (job *)data;
+    napi_value v;
+    if (status != napi_ok && !j->rc) {
+        j->rc = BV_E_STATE;
+        snprintf(j->msg, sizeof j->msg, "async work was cancelled");
+    }
+    if (j->rc) {
+        napi_value msg, code, err;
+        napi_create_string_utf8(env, j->msg[0] ? j->msg : "browservec_hip call failed", NAPI_AUTO_LENGTH, &msg);
+        napi_create_string_utf8(env, code_name(j->rc), NAPI_AUTO_LENGTH, &code);
+        napi_create_error(env, code, msg, &err);
+        napi_reject_deferred(env, j->deferred, err);
+    } else {
+        if (j->result) napi_get_reference_value(env, j->result, &v);
+        else napi_get_undefined(env, &v);
+        napi_resolve_deferred(env, j->deferred, v);
+    }
+    for (int i = 0; i < 3; ++i)
+        if (j->keep[i]) napi_delete_reference(env, j->keep[i]);
+    if (j->result) napi_delete_reference(env, j->result);
+    napi_delete_async_work(env, j->work);
+    index_handle *h = j->h;
+    free(j);
+    if (--h->pending == 0 && h->dead && h->idx) {
+        bv_index_destroy(h->idx);
+        h->idx = NULL;
+    }
+}
+
+/* Queues the job and returns its promise.  `handle` (the index external)
+ * stays referenced until completion, so the index outlives the work. */
+static napi_value queue(napi_env env, job *j, napi_value handle, const char *name) {
+    napi_value promise, res;
+    if (napi_create_reference(env, handle, 1, &j->keep[2]) != napi_ok ||
+        napi_create_promise(env, &j->deferred, &promise) != napi_ok ||
+        napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &res) != napi_ok ||
+        napi_create_async_work(env, NULL, res, job_execute, job_complete, j, &j->work) != napi_ok ||
+        napi_queue_async_work(env, j->work) != napi_ok) {
+        for (int i = 0; i < 3; ++i)
+            if (j->keep[i]) napi_delete_reference(env, j->keep[i]);
+        if (j->result) napi_delete_reference(env, j->result);
+        free(j);
+        napi_throw_error(env, NULL, "could not queue the device call");
+        return NULL;
+    }
+    j->h->pending++;
+    return promise;
+}
+
+static job *new_job(napi_env env, op_kind op, index_handle *h) {
+    (void)env;
+    job *j = (job *)calloc(1, sizeof(job));
+    if (j) {
+        j->op = op;
+        j->h = h;
+        j->idx = h->idx;
+    }
+    return j;
+}
+
+/* Result object {rows: Uint32Array, scores: Float32Array, counts: Uint32Array},
+ * referenced by the job until it completes. */
+static int job_result(napi_env env, job *j, size_t nq, size_t k) {
+    napi_value r, s, c, obj;
+    r = new_typed(env, napi_uint32_array, nq * k, 4, (void **)&j->rows);
+    s = new_typed(env, napi_float32_array, nq * k, 4, (void **)&j->scores);
+    c = new_typed(env, napi_uint32_array, nq, 4, (void **)&j->counts);
+    if (!r || !s || !c || napi_create_object(env, &obj) != napi_ok) return 0;
+    napi_set_named_property(env, obj, "rows", r);
+    napi_set_named_property(env, obj, "scores", s);
+    napi_set_named_property(env, obj, "counts", c);
+    return napi_create_reference(env, obj, 1, &j->result) == napi_ok;
+}
+
+static int keep(napi_env env, job *j, int slot, napi_value v) {
+    return napi_create_reference(env, v, 1, &j->keep[slot]) == napi_ok;
+}
+
+/* ---- device ------------------------------------------------------------------ */
 /* openDevice(ordinal) -> external */
 static napi_value open_device(napi_env env, napi_callback_info info) {
     ARGS(1);
@@ -106,6 +264,16 @@ static napi_value device_lost(napi_env env, napi_callback_info info) {
     return out;
 }
 
+/* debugInject(dev, what): host-side failure flags (BV_INJECT_*). */
+static napi_value debug_inject(napi_env env, napi_callback_info info) {
+    ARGS(2);
+    uint32_t what = 0;
+    get_u32(env, argv[1], &what);
+    int rc = bv_debug_inject((bv_device *)get_ptr(env, argv[0]), (int)what);
+    if (rc) return throw_bv(env, rc);
+    return NULL;
+}
+
 static uint32_t field_u32(napi_env env, napi_value obj, const char *name, uint32_t dflt) {
     bool has = false;
     napi_value v;
@@ -128,6 +296,16 @@ static double field_f64(napi_env env, napi_value obj, const char *name, double d
         if (napi_typeof(env, v, &t) == napi_ok && t == napi_number) napi_get_value_double(env, v, &x);
     }
     return x;
+}
+
+/* The handle's finalizer: an index the script dropped without destroy(); calls in
+ * flight hold a reference to the handle, so none is pending here. */
+static void index_finalize(napi_env env, void *data, void *hint) {
+    (void)env;
+    (void)hint;
+    index_handle *h = (index_handle *)data;
+    if (h->idx) bv_index_destroy(h->idx);
+    free(h);
 }
 
 /* createIndex(dev, {kind, dim, metric, bits, scorer, seed, rounds, chunkRows,
@@ -157,162 +335,194 @@ static napi_value create_index(napi_env env, napi_callback_info info) {
     bv_index *idx = NULL;
     int rc = bv_index_create((bv_device *)get_ptr(env, argv[0]), &d, &idx);
     if (rc) return throw_bv(env, rc);
+    index_handle *h = (index_handle *)calloc(1, sizeof *h);
+    if (!h) {
+        bv_index_destroy(idx);
+        napi_throw_error(env, "BV_E_OOM", "out of host memory");
+        return NULL;
+    }
+    h->idx = idx;
+    h->dim = d.dim;
     napi_value out;
-    CALL(env, napi_create_external(env, idx, NULL, NULL, &out));
+    CALL(env, napi_create_external(env, h, index_finalize, NULL, &out));
     return out;
 }
 
 static napi_value destroy_index(napi_env env, napi_callback_info info) {
     ARGS(1);
-    int rc = bv_index_destroy((bv_index *)get_ptr(env, argv[0]));
+    index_handle *h = get_index(env, argv[0]);
+    if (!h) return NULL;
+    h->dead = 1;
+    if (h->pending) return NULL;  /* the last call in flight destroys it */
+    int rc = bv_index_destroy(h->idx);
+    h->idx = NULL;
     if (rc) return throw_bv(env, rc);
     return NULL;
 }
 
 static napi_value index_size(napi_env env, napi_callback_info info) {
     ARGS(1);
+    index_handle *h = get_index(env, argv[0]);
     uint64_t rows = 0;
-    int rc = bv_index_size((const bv_index *)get_ptr(env, argv[0]), &rows);
+    int rc = bv_index_size(h ? h->idx : NULL, &rows);
     if (rc) return throw_bv(env, rc);
     napi_value out;
     CALL(env, napi_create_double(env, (double)rows, &out));
     return out;
 }
 
-/* append(idx, Float32Array data, count) */
+/* append(idx, Float32Array data, count) -> Promise<void> */
 static napi_value append(napi_env env, napi_callback_info info) {
     ARGS(3);
+    index_handle *h = get_index(env, argv[0]);
     size_t n = 0;
     const float *data = (const float *)get_typed(env, argv[1], napi_float32_array, &n);
     uint32_t count = 0;
-    if (!data || !get_u32(env, argv[2], &count)) {
+    if (!h || !data || !get_u32(env, argv[2], &count)) {
         napi_throw_type_error(env, NULL, "append(idx, Float32Array, count)");
         return NULL;
     }
-    int rc = bv_index_append((bv_index *)get_ptr(env, argv[0]), data, n, count);
-    if (rc) return throw_bv(env, rc);
-    return NULL;
+    /* the reference's check and message (src/index/flat.ts:96-98) */
+    if (n != (size_t)count * h->dim) {
+        char msg[96];
+        snprintf(msg, sizeof msg, "expected %zu floats, got %zu", (size_t)count * h->dim, n);
+        napi_throw_error(env, "BV_E_INVALID", msg);
+        return NULL;
+    }
+    job *j = new_job(env, OP_APPEND, h);
+    if (!j || !keep(env, j, 0, argv[1])) {
+        free(j);
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    j->data = data;
+    j->n_floats = n;
+    j->count = count;
+    return queue(env, j, argv[0], "browservec.append");
 }
 
-/* Result object {rows: Uint32Array, scores: Float32Array, counts: Uint32Array}. */
-static napi_value result(napi_env env, size_t nq, size_t k, uint32_t **rows, float **scores, uint32_t **counts,
-                         napi_value *r, napi_value *s, napi_value *c) {
-    *r = new_typed(env, napi_uint32_array, nq * k, 4, (void **)rows);
-    *s = new_typed(env, napi_float32_array, nq * k, 4, (void **)scores);
-    *c = new_typed(env, napi_uint32_array, nq, 4, (void **)counts);
-    if (!*r || !*s || !*c) return NULL;
-    napi_value obj;
-    if (napi_create_object(env, &obj) != napi_ok) return NULL;
-    napi_set_named_property(env, obj, "rows", *r);
-    napi_set_named_property(env, obj, "scores", *s);
-    napi_set_named_property(env, obj, "counts", *c);
-    return obj;
+/* build(idx) -> Promise<void>: the IVF build now (queries build on demand). */
+static napi_value build(napi_env env, napi_callback_info info) {
+    ARGS(1);
+    index_handle *h = get_index(env, argv[0]);
+    if (!h) {
+        napi_throw_type_error(env, NULL, "build(idx)");
+        return NULL;
+    }
+    job *j = new_job(env, OP_BUILD, h);
+    if (!j) {
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    return queue(env, j, argv[0], "browservec.build");
 }
 
-/* query(idx, Float32Array q, k) / queryMasked(idx, q, k, Uint32Array mask) */
+/* query(idx, Float32Array q, k) / queryMasked(idx, q, k, Uint32Array mask) -> Promise<result> */
 static napi_value query_common(napi_env env, napi_callback_info info, int masked) {
     size_t argc = 4;
     napi_value argv[4];
     CALL(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
     size_t qn = 0, mn = 0;
+    index_handle *h = argc > 0 ? get_index(env, argv[0]) : NULL;
     const float *q = argc > 1 ? (const float *)get_typed(env, argv[1], napi_float32_array, &qn) : NULL;
     uint32_t k = 0;
     const uint32_t *mask = NULL;
     if (masked && argc > 3) mask = (const uint32_t *)get_typed(env, argv[3], napi_uint32_array, &mn);
-    if (!q || argc < 3 || !get_u32(env, argv[2], &k) || (masked && !mask)) {
+    if (!h || !q || argc < 3 || !get_u32(env, argv[2], &k) || (masked && !mask)) {
         napi_throw_type_error(env, NULL, masked ? "queryMasked(idx, Float32Array, k, Uint32Array)"
                                                 : "query(idx, Float32Array, k)");
         return NULL;
     }
-    uint32_t *rows, *counts;
-    float *scores;
-    napi_value r, s, c;
-    napi_value obj = result(env, 1, k, &rows, &scores, &counts, &r, &s, &c);
-    if (!obj) return NULL;
-    bv_index *idx = (bv_index *)get_ptr(env, argv[0]);
-    int rc = masked ? bv_index_query_masked(idx, q, k, mask, mn, rows, scores, counts)
-                    : bv_index_query(idx, q, k, rows, scores, counts);
-    if (rc) return throw_bv(env, rc);
-    return obj;
+    if (qn != h->dim) return length_error(env, h->dim, qn);
+    job *j = new_job(env, masked ? OP_QUERY_MASKED : OP_QUERY, h);
+    if (!j || !keep(env, j, 0, argv[1]) || (masked && !keep(env, j, 1, argv[3])) || !job_result(env, j, 1, k)) {
+        free(j);
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    j->data = q;
+    j->k = k;
+    j->aux = mask;
+    j->n_aux = mn;
+    return queue(env, j, argv[0], "browservec.query");
 }
 static napi_value query(napi_env env, napi_callback_info info) { return query_common(env, info, 0); }
 static napi_value query_masked(napi_env env, napi_callback_info info) { return query_common(env, info, 1); }
 
-/* queryBatch(idx, Float32Array packed, n, k) */
-static napi_value query_batch(napi_env env, napi_callback_info info) {
-    ARGS(4);
+/* queryBatch(idx, Float32Array packed, n, k) / search(idx, packed, n, fetch, k) -> Promise<result> */
+static napi_value batch_common(napi_env env, napi_callback_info info, int with_fetch) {
+    size_t argc = 5;
+    napi_value argv[5];
+    CALL(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
     size_t qn = 0;
-    const float *q = (const float *)get_typed(env, argv[1], napi_float32_array, &qn);
-    uint32_t nq = 0, k = 0;
-    if (!q || !get_u32(env, argv[2], &nq) || !get_u32(env, argv[3], &k)) {
-        napi_throw_type_error(env, NULL, "queryBatch(idx, Float32Array, n, k)");
-        return NULL;
-    }
-    uint32_t *rows, *counts;
-    float *scores;
-    napi_value r, s, c;
-    napi_value obj = result(env, nq, k, &rows, &scores, &counts, &r, &s, &c);
-    if (!obj) return NULL;
-    int rc = bv_index_query_batch((bv_index *)get_ptr(env, argv[0]), q, nq, k, rows, scores, counts);
-    if (rc) return throw_bv(env, rc);
-    return obj;
-}
-
-/* search(idx, Float32Array queries, n, fetch, k): top-fetch by code score, exact re-rank to k */
-static napi_value search(napi_env env, napi_callback_info info) {
-    ARGS(5);
-    size_t qn = 0;
-    const float *q = (const float *)get_typed(env, argv[1], napi_float32_array, &qn);
+    index_handle *h = argc > 0 ? get_index(env, argv[0]) : NULL;
+    const float *q = argc > 1 ? (const float *)get_typed(env, argv[1], napi_float32_array, &qn) : NULL;
     uint32_t nq = 0, fetch = 0, k = 0;
-    if (!q || !get_u32(env, argv[2], &nq) || !get_u32(env, argv[3], &fetch) || !get_u32(env, argv[4], &k)) {
-        napi_throw_type_error(env, NULL, "search(idx, Float32Array, n, fetch, k)");
+    const size_t need = with_fetch ? 5 : 4;
+    if (!h || !q || argc < need || !get_u32(env, argv[2], &nq) ||
+        (with_fetch && !get_u32(env, argv[3], &fetch)) || !get_u32(env, argv[need - 1], &k)) {
+        napi_throw_type_error(env, NULL, with_fetch ? "search(idx, Float32Array, n, fetch, k)"
+                                                    : "queryBatch(idx, Float32Array, n, k)");
         return NULL;
     }
-    uint32_t *rows, *counts;
-    float *scores;
-    napi_value r, s, c;
-    napi_value obj = result(env, nq, k, &rows, &scores, &counts, &r, &s, &c);
-    if (!obj) return NULL;
-    int rc = bv_index_search((bv_index *)get_ptr(env, argv[0]), q, nq, fetch, k, rows, scores, counts);
-    if (rc) return throw_bv(env, rc);
-    return obj;
+    if (qn != (size_t)nq * h->dim) return length_error(env, (size_t)nq * h->dim, qn);
+    job *j = new_job(env, with_fetch ? OP_SEARCH : OP_QUERY_BATCH, h);
+    if (!j || !keep(env, j, 0, argv[1]) || !job_result(env, j, nq, k)) {
+        free(j);
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    j->data = q;
+    j->nq = nq;
+    j->fetch = fetch;
+    j->k = k;
+    return queue(env, j, argv[0], with_fetch ? "browservec.search" : "browservec.queryBatch");
 }
+static napi_value query_batch(napi_env env, napi_callback_info info) { return batch_common(env, info, 0); }
+static napi_value search(napi_env env, napi_callback_info info) { return batch_common(env, info, 1); }
 
-/* rerank(idx, Float32Array q, Uint32Array candidates, k) */
+/* rerank(idx, Float32Array q, Uint32Array candidates, k) -> Promise<result> */
 static napi_value rerank(napi_env env, napi_callback_info info) {
     ARGS(4);
     size_t qn = 0, cn = 0;
+    index_handle *h = get_index(env, argv[0]);
     const float *q = (const float *)get_typed(env, argv[1], napi_float32_array, &qn);
     const uint32_t *cand = (const uint32_t *)get_typed(env, argv[2], napi_uint32_array, &cn);
     uint32_t k = 0;
-    if (!q || !cand || !get_u32(env, argv[3], &k)) {
+    if (!h || !q || !cand || !get_u32(env, argv[3], &k)) {
         napi_throw_type_error(env, NULL, "rerank(idx, Float32Array, Uint32Array, k)");
         return NULL;
     }
-    uint32_t *rows, *counts;
-    float *scores;
-    napi_value r, s, c;
-    napi_value obj = result(env, 1, k, &rows, &scores, &counts, &r, &s, &c);
-    if (!obj) return NULL;
-    int rc = bv_index_rerank((bv_index *)get_ptr(env, argv[0]), q, cand, (uint32_t)cn, k, rows, scores, counts);
-    if (rc) return throw_bv(env, rc);
-    return obj;
+    if (qn != h->dim) return length_error(env, h->dim, qn);
+    job *j = new_job(env, OP_RERANK, h);
+    if (!j || !keep(env, j, 0, argv[1]) || !keep(env, j, 1, argv[2]) || !job_result(env, j, 1, k)) {
+        free(j);
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    j->data = q;
+    j->aux = cand;
+    j->n_aux = cn;
+    j->k = k;
+    return queue(env, j, argv[0], "browservec.rerank");
 }
 
 static napi_value set_nprobe(napi_env env, napi_callback_info info) {
     ARGS(2);
+    index_handle *h = get_index(env, argv[0]);
     uint32_t n = 0;
     get_u32(env, argv[1], &n);
-    int rc = bv_index_set_nprobe((bv_index *)get_ptr(env, argv[0]), n);
+    int rc = bv_index_set_nprobe(h ? h->idx : NULL, n);
     if (rc) return throw_bv(env, rc);
     return NULL;
 }
 
 static napi_value stats(napi_env env, napi_callback_info info) {
     ARGS(1);
+    index_handle *h = get_index(env, argv[0]);
     bv_index_stats st;
     memset(&st, 0, sizeof st);
-    int rc = bv_index_get_stats((bv_index *)get_ptr(env, argv[0]), &st);
+    int rc = bv_index_get_stats(h ? h->idx : NULL, &st);
     if (rc) return throw_bv(env, rc);
     napi_value obj, v;
     CALL(env, napi_create_object(env, &obj));
@@ -349,11 +559,12 @@ static napi_value init(napi_env env, napi_value exports) {
         const char *name;
         napi_callback fn;
     } fns[] = {
-        {"openDevice", open_device},   {"closeDevice", close_device}, {"deviceLost", device_lost},
-        {"createIndex", create_index}, {"destroyIndex", destroy_index}, {"size", index_size},
-        {"append", append},            {"query", query},              {"queryMasked", query_masked},
-        {"queryBatch", query_batch},   {"search", search},            {"rerank", rerank},
-        {"setNprobe", set_nprobe},     {"stats", stats},              {"lastError", last_error},
+        {"openDevice", open_device},   {"closeDevice", close_device},   {"deviceLost", device_lost},
+        {"debugInject", debug_inject}, {"createIndex", create_index},   {"destroyIndex", destroy_index},
+        {"size", index_size},          {"append", append},              {"build", build},
+        {"query", query},              {"queryMasked", query_masked},   {"queryBatch", query_batch},
+        {"search", search},            {"rerank", rerank},              {"setNprobe", set_nprobe},
+        {"stats", stats},              {"lastError", last_error},
     };
     for (size_t i = 0; i < sizeof fns / sizeof fns[0]; ++i) {
         napi_value f;
@@ -363,6 +574,10 @@ static napi_value init(napi_env env, napi_value exports) {
     napi_value v;
     napi_create_uint32(env, (uint32_t)bv_abi_version(), &v);
     napi_set_named_property(env, exports, "abiVersion", v);
+    napi_create_uint32(env, BV_INJECT_LOST, &v);
+    napi_set_named_property(env, exports, "INJECT_LOST", v);
+    napi_create_uint32(env, BV_INJECT_APPEND_OOM, &v);
+    napi_set_named_property(env, exports, "INJECT_APPEND_OOM", v);
     return exports;
 }
 

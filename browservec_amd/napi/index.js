@@ -2,9 +2,23 @@
 // Node host side of the MI355X search path: the reference's VectorIndex seam
 // (src/index/flat.ts:24-40) and DeviceContext (src/engine/device.ts:3-9)
 // implemented over libbrowservec_hip.so through the N-API addon
-// (bv_napi.c).  A reference build swaps its WebGPU FlatIndex / QuantIndex
-// for HipIndex inside buildIndex (src/index.ts:105-142); BrowserVec and
-// everything above the seam stay as they are.
+// (bv_napi.c).  A reference build swaps its WebGPU FlatIndex / QuantIndex /
+// IVFIndex / IVFQuantIndex for these classes inside buildIndex
+// (src/index.ts:105-142); BrowserVec and everything above the seam stay as
+// they are.
+//
+// Each class carries exactly the duck-typed members its reference
+// counterpart has, because BrowserVec picks its code path by their presence
+// (src/index.ts:389-394, 477-481, 718-748):
+//   - queryMasked on flat and quantized indexes only (IVF filters go through
+//     BrowserVec's exact scan or over-fetch, as in the reference);
+//   - queryBatch on flat fp32 indexes only, whose batches return exactly the
+//     single-query results; quantized and IVF batches stay BrowserVec's loop
+//     of query(), which re-ranks and honours a per-query nprobe;
+//   - setNprobe / nlist / nprobe / tunedRecall / trainMode on IVF kinds,
+//     ingestMode on quantized kinds, chunkCount everywhere.
+// search() (approximate top-fetch + exact re-rank in one device call) and
+// rerankExact() are extras a caller may use explicitly.
 const path = require('path');
 
 const native = require(path.join(__dirname, '..', 'lib', 'browservec_napi.node'));
@@ -20,6 +34,11 @@ class HipDeviceContext {
   }
   get lost() {
     return this.handle === null || native.deviceLost(this.handle);
+  }
+  // Test hook: force the device-lost state (or a failed allocation on the
+  // next append) from the host; no device work happens.
+  debugInject(what) {
+    native.debugInject(this.handle, what === 'lost' ? native.INJECT_LOST : native.INJECT_APPEND_OOM);
   }
   destroy() {
     if (this.handle !== null) {
@@ -40,22 +59,25 @@ function f32(a) {
   return a instanceof Float32Array ? a : Float32Array.from(a);
 }
 
-// FlatIndex (src/index/flat.ts:42) and QuantIndex (src/index/quant.ts:21)
-// on the device: same members, same results order (score desc, row asc).
+function batchHits(res, n, k) {
+  const out = [];
+  for (let i = 0; i < n; i++) out.push(toHits(res, i, k));
+  return out;
+}
+
+// Members every index kind has (VectorIndex plus chunkCount and the extras).
 class HipIndex {
-  constructor(ctx, dim, metric, opts) {
+  constructor(ctx, dim, metric, kind, opts) {
     const o = opts || {};
-    const bits = o.bits || 0;
+    const ivf = o.ivf || null;
     this.dim = dim;
     this.metric = metric || 'cosine';
-    this.bits = bits;
-    const ivf = o.ivf || null;
-    this.isIvf = ivf !== null;
+    this.bits = o.bits || 0;
     this.handle = native.createIndex(ctx.handle, {
-      kind: ivf ? (bits ? KIND.ivfquant : KIND.ivf) : (bits ? KIND.quant : KIND.flat),
+      kind: kind,
       dim: dim,
       metric: METRIC[this.metric],
-      bits: bits,
+      bits: this.bits,
       scorer: SCORER[o.scorer || 'asym'],
       hasSeed: o.seed === undefined ? 0 : 1,
       seed: o.seed === undefined ? 0 : o.seed >>> 0,
@@ -74,53 +96,27 @@ class HipIndex {
   get size() {
     return native.size(this.handle);
   }
-  // append(data, count): `data` holds count*dim prepared floats.
+  // append(data, count): `data` holds count*dim prepared floats; the rows
+  // are copied and encoded on the device off the event loop (await it, as
+  // BrowserVec awaits the reference's async appends).
   append(data, count) {
-    native.append(this.handle, f32(data), count);
+    return native.append(this.handle, f32(data), count);
   }
   query(q, k) {
-    return Promise.resolve(toHits(native.query(this.handle, f32(q), k), 0, k));
-  }
-  queryMasked(q, k, maskWords) {
-    const m = maskWords instanceof Uint32Array ? maskWords : Uint32Array.from(maskWords);
-    return Promise.resolve(toHits(native.queryMasked(this.handle, f32(q), k, m), 0, k));
-  }
-  queryBatch(packed, n, k) {
-    const res = native.queryBatch(this.handle, f32(packed), n, k);
-    const out = [];
-    for (let i = 0; i < n; i++) out.push(toHits(res, i, k));
-    return Promise.resolve(out);
+    return native.query(this.handle, f32(q), k).then((res) => toHits(res, 0, k));
   }
   // BrowserVec.query's quantized path in one device call: approximate
   // top-`fetch`, exact Store.dotRow re-rank to k (src/index.ts:402-421).
   search(packed, n, fetch, k) {
-    const res = native.search(this.handle, f32(packed), n, fetch, k);
-    const out = [];
-    for (let i = 0; i < n; i++) out.push(toHits(res, i, k));
-    return Promise.resolve(out);
+    return native.search(this.handle, f32(packed), n, fetch, k).then((res) => batchHits(res, n, k));
   }
   // rerankExact (src/index.ts:583-594) against the rows kept on the device.
   rerankExact(q, candidates, k) {
     const rows = Uint32Array.from(candidates.map(function (h) { return h.row; }));
-    return Promise.resolve(toHits(native.rerank(this.handle, f32(q), rows, k), 0, k));
-  }
-  setNprobe(n) {
-    native.setNprobe(this.handle, n || 0);
+    return native.rerank(this.handle, f32(q), rows, k).then((res) => toHits(res, 0, k));
   }
   get chunkCount() {
     return native.stats(this.handle).chunkCount;
-  }
-  // IVF getters (src/index.ts:718-748); 0 for flat kinds and before a build.
-  get nlist() {
-    return native.stats(this.handle).nlist;
-  }
-  get nprobe() {
-    return native.stats(this.handle).nprobe;
-  }
-  // estimated recall@10 at the tuned nprobe; undefined unless tuning ran
-  get tunedRecall() {
-    const r = native.stats(this.handle).tunedRecall;
-    return r < 0 ? undefined : r;
   }
   stats() {
     return native.stats(this.handle);
@@ -133,21 +129,102 @@ class HipIndex {
   }
 }
 
-// buildIndex (src/index.ts:105-142) for the kinds this library serves:
-// flat and quantized scans, and IVF over either.  HNSW is the reference's
-// CPU graph index and stays there.
-function buildIndex(ctx, dim, metric, quantBits, quant, ann, chunkRows) {
-  if (ann && ann.type === 'hnsw') throw new Error('HNSW indexes are not served by this library');
-  if (ann && metric === 'l2') throw new Error('IVF supports metric cosine/dot only (l2 is later work)');
-  const q = quant || {};
-  return new HipIndex(ctx, dim, metric, {
-    bits: quantBits || 0,
-    seed: q.seed,
-    rounds: q.rounds,
-    scorer: q.scorer,
-    chunkRows: chunkRows,
-    ivf: ann || null,
-  });
+function queryMasked(q, k, maskWords) {
+  const m = maskWords instanceof Uint32Array ? maskWords : Uint32Array.from(maskWords);
+  return native.queryMasked(this.handle, f32(q), k, m).then((res) => toHits(res, 0, k));
 }
 
-module.exports = { HipDeviceContext, HipIndex, buildIndex, native, abiVersion: native.abiVersion };
+// FlatIndex (src/index/flat.ts:42): exact fp32 scans.
+class HipFlatIndex extends HipIndex {
+  constructor(ctx, dim, metric, opts) {
+    super(ctx, dim, metric, KIND.flat, Object.assign({}, opts, { bits: 0 }));
+  }
+  queryMasked(q, k, maskWords) {
+    return queryMasked.call(this, q, k, maskWords);
+  }
+  // One device call for the batch; every query's rows and score bits equal
+  // those of query() on the same vector.
+  queryBatch(packed, n, k) {
+    return native.queryBatch(this.handle, f32(packed), n, k).then((res) => batchHits(res, n, k));
+  }
+}
+
+// QuantIndex (src/index/quant.ts:21): rotate + quantize on the device.
+class HipQuantIndex extends HipIndex {
+  constructor(ctx, dim, metric, opts) {
+    super(ctx, dim, metric, KIND.quant, opts);
+  }
+  queryMasked(q, k, maskWords) {
+    return queryMasked.call(this, q, k, maskWords);
+  }
+  // where rotate + quantize runs (src/index/quant.ts:115-118): on the device
+  get ingestMode() {
+    return this.size > 0 ? 'device' : 'pending';
+  }
+}
+
+// IVFIndex (src/index/ivf.ts:51) / IVFQuantIndex (src/index/ivfquant.ts:33).
+class HipIvfIndex extends HipIndex {
+  constructor(ctx, dim, metric, opts) {
+    super(ctx, dim, metric, (opts && opts.bits) ? KIND.ivfquant : KIND.ivf, opts);
+  }
+  setNprobe(n) {
+    native.setNprobe(this.handle, n || 0);
+  }
+  // The build now (queries after an append build on demand, ivfquant.ts:461).
+  build() {
+    return native.build(this.handle);
+  }
+  // IVF getters (src/index.ts:718-748); 0 before a build.
+  get nlist() {
+    return native.stats(this.handle).nlist;
+  }
+  get nprobe() {
+    return native.stats(this.handle).nprobe;
+  }
+  // estimated recall@10 at the tuned nprobe; undefined unless tuning ran
+  get tunedRecall() {
+    const r = native.stats(this.handle).tunedRecall;
+    return r < 0 ? undefined : r;
+  }
+  // where the k-means mean update ran (src/index/ivf.ts:133-135)
+  get trainMode() {
+    return native.stats(this.handle).nlist > 0 ? 'device' : 'pending';
+  }
+}
+
+class HipIvfQuantIndex extends HipIvfIndex {
+  get ingestMode() {
+    return this.size > 0 ? 'device' : 'pending';
+  }
+}
+
+// buildIndex (src/index.ts:105-142) for the kinds this library serves:
+// flat and quantized scans, and IVF over either, with the reference's
+// rejections and messages.  HNSW is the reference's CPU graph index and
+// stays there.
+function buildIndex(ctx, dim, metric, quantBits, quant, ann, chunkRows) {
+  const bits = quantBits || 0;
+  const q = quant || {};
+  const opts = { bits: bits, seed: q.seed, rounds: q.rounds, scorer: q.scorer, chunkRows: chunkRows, ivf: ann || null };
+  if (ann && ann.type === 'hnsw') throw new Error('HNSW indexes are not served by this library');
+  if (ann) {
+    if (metric === 'l2') throw new Error('IVF supports metric cosine/dot only (l2 is later work)');
+    if (bits === 8 || bits === 4 || bits === 1) return new HipIvfQuantIndex(ctx, dim, metric, opts);
+    if (bits === 0) return new HipIvfIndex(ctx, dim, metric, opts);
+    throw new Error(`quantBits ${bits} not supported with ann`);
+  }
+  if (bits === 0) return new HipFlatIndex(ctx, dim, metric, opts);
+  if (bits === 8 || bits === 4 || bits === 1) {
+    if (metric === 'l2') {
+      throw new Error('quantized mode supports metric cosine/dot only (l2 quantization is later work)');
+    }
+    return new HipQuantIndex(ctx, dim, metric, opts);
+  }
+  throw new Error(`quantBits ${bits} not supported (ships 0, 1, 4, 8)`);
+}
+
+module.exports = {
+  HipDeviceContext, HipIndex, HipFlatIndex, HipQuantIndex, HipIvfIndex, HipIvfQuantIndex, buildIndex,
+  native, abiVersion: native.abiVersion,
+};

@@ -120,6 +120,14 @@ int bv_device_open(int ordinal, bv_device **out);
 int bv_device_close(bv_device *dev);
 /* DeviceContext.lost (device.ts:68-76). */
 int bv_device_is_lost(const bv_device *dev, int *lost);
+/* Failure injection for tests of the error paths.  The reference's device
+ * loss comes from the browser (GPUDevice.lost sets DeviceContext.lost,
+ * src/engine/device.ts:68-76; queries then throw "GPU device lost; re-create
+ * the store", src/index/flat.ts:137); these host-side flags force the same
+ * conditions without touching the GPU. */
+#define BV_INJECT_LOST 1       /* mark the device lost: every later call fails with BV_E_DEVICE_LOST */
+#define BV_INJECT_APPEND_OOM 2 /* the next append fails as if a device allocation failed; the index is unchanged */
+int bv_debug_inject(bv_device *dev, int what);
 /* Device name, compute-unit count and HBM size. */
 int bv_device_info(const bv_device *dev, char *name, uint32_t name_len, uint32_t *cu_count, uint64_t *hbm_bytes);
 
@@ -210,6 +218,11 @@ int bv_index_build(bv_index *idx);
  * padded_dim for quantized kinds, dim for fp32), list offsets (nlist+1) and
  * list rows (rows, ascending within a list).  Any pointer may be null. */
 int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *list_off, uint32_t *list_rows);
+/* pickProbes' scores (src/index/ivfquant.ts:495-509: the f64 4-way strided
+ * dot of the rotated query with every centroid, stored as f32) for nq
+ * queries: scores[nq][nlist].  Batches of 8 or more run the batched probe
+ * kernel, fewer the single-query one; both give the same bits. */
+int bv_index_export_probe_scores(bv_index *idx, const float *queries, uint32_t nq, float *scores);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,16 @@ topk_ref / merge_partials    topk.test.ts KATs + full sort on random input;
 topk_canonical               full sort by (score desc, row asc)
 kmeans pieces                kmeans.test.ts KATs (updateCentroids ->
                              [1,1,10,10], normalizeRows([3,4,0,0]))
+random_init_centroids        JS-engine vectors of the rows picked
+                             (Math.floor(rng() * count), seeds up to 4096 lists)
+update_centroids             JS-engine Float32Array run on a sample whose
+                             sequential f32 sums differ from f64 sums, with an
+                             empty cluster re-seeded and normalizeRows after
+Reservoir                    JS-engine slot sequences; first cap slots are the
+                             identity, admission probability cap/(i+1) and
+                             final inclusion cap/n within 5 sd over 6000 seeds
+assign_f32 (order 1)         brute-force argmax; the AVX2 path equals the
+                             scalar fmaf chain (order 2), ties included
 choose_nprobe / pick_tune    ivfTune.test.ts tables
 probe_scores                 long double brute force within 1 ulp f32
 ===========================  =================================================
@@ -416,7 +426,9 @@ def update_centroids(sample, assign, centroids, seed: int):
 
 def assign_f32(rows, centroids, order: int = 0) -> np.ndarray:
     """argmax-dot assignment (src/engine/wgsl/assign.ts:31-58); order 0 = the
-    reference kernel's dot4 groups, 1 = one sequential FMA chain."""
+    reference kernel's dot4 groups, 1 = one sequential FMA chain (vectorized
+    across centroids when the CPU has AVX2 + FMA), 2 = the same chain on the
+    scalar path."""
     rows, centroids = _f32(rows), _f32(centroids)
     out = np.empty(rows.shape[0], dtype=np.uint32)
     _lib.bvo_assign_f32(_p(rows, f32p), rows.shape[0], _p(centroids, f32p), centroids.shape[0], rows.shape[1],

@@ -10,6 +10,9 @@
 //   src/quant/codec.ts:22-154   quantizeRow / quantizeRow4 / quantizeRow1
 //   src/store/store.ts:114-217  dotRow, l2Row, normalizeInPlace
 //   src/index/flat.ts:217-239   topK (tie semantics)
+//   src/index/ivfquant.ts:114-124,235-245  the reservoir sampler's slots
+//   src/index/kmeans.ts:154-219 random init picks, the Float32Array mean
+//                               update, normalizeRows
 // The oracle (oracle/bv_oracle.c) must reproduce every value bit for bit.
 //
 // Usage: node tests/golden/make_js_vectors.js > tests/golden/js_vectors.json
@@ -259,5 +262,85 @@ out.topk = [
 var rs = uniformVec(200, 77, 3);
 for (var i = 0; i < 200; i += 3) rs[i] = rs[0];
 out.topk.push({ scores: Array.from(rs), k: 25, rows: selectTop(rs, 25).map(function (h) { return h.row; }) });
+
+// reservoir: the slot each appended row takes (-1: not sampled) for a
+// sampler of capacity `cap` seeded (seed ^ 0x85ebca6b) >>> 0
+function reservoirSlots(cap, seed, n) {
+  var rng = makeRng((seed ^ 0x85ebca6b) >>> 0);
+  var filled = 0, seen = 0, slots = [];
+  for (var i = 0; i < n; i++) {
+    if (filled < cap) {
+      slots.push(filled);
+      filled++;
+    } else {
+      var j = Math.floor(rng() * (seen + 1));
+      slots.push(j < cap ? j : -1);
+    }
+    seen++;
+  }
+  return slots;
+}
+out.reservoir = [[1024, 0x9e3779b9, 3000], [1024, 7, 5000], [1500, 0x51ed270b, 4000]].map(function (c) {
+  return { cap: c[0], seed: c[1] >>> 0, n: c[2], slots: reservoirSlots(c[0], c[1] >>> 0, c[2]) };
+});
+
+// random init: the sample row each centroid copies
+out.init_picks = [[0x51ed270b, 16, 1200], [77, 4096, 8192], [12345, 24, 6000]].map(function (c) {
+  var rng = makeRng(c[0]);
+  var picks = [];
+  for (var i = 0; i < c[1]; i++) picks.push(Math.floor(rng() * c[2]));
+  return { seed: c[0] >>> 0, nlist: c[1], count: c[2], picks: picks };
+});
+
+// mean update with Float32Array sums: values chosen so that the sequential
+// f32 sums differ from f64 sums (a large value absorbs small ones), plus an
+// empty cluster re-seeded from the sample, then normalizeRows
+function meanUpdate(sample, count, dim, assign, centroids, nlist, seed) {
+  var sums = new Float32Array(nlist * dim);
+  var counts = new Int32Array(nlist);
+  for (var r = 0; r < count; r++) {
+    var c = assign[r];
+    for (var i = 0; i < dim; i++) sums[c * dim + i] += sample[r * dim + i];
+    counts[c]++;
+  }
+  var rng = makeRng(seed);
+  for (var c2 = 0; c2 < nlist; c2++) {
+    if (counts[c2] === 0) {
+      var pick = Math.floor(rng() * count);
+      for (var i2 = 0; i2 < dim; i2++) centroids[c2 * dim + i2] = sample[pick * dim + i2];
+    } else {
+      var inv = 1 / counts[c2];
+      for (var i3 = 0; i3 < dim; i3++) centroids[c2 * dim + i3] = sums[c2 * dim + i3] * inv;
+    }
+  }
+  for (var r2 = 0; r2 < nlist; r2++) {
+    var s = 0;
+    for (var i4 = 0; i4 < dim; i4++) s += centroids[r2 * dim + i4] * centroids[r2 * dim + i4];
+    var iv = 1 / (Math.sqrt(s) || 1);
+    for (var i5 = 0; i5 < dim; i5++) centroids[r2 * dim + i5] *= iv;
+  }
+  return centroids;
+}
+(function () {
+  var dim = 4, nlist = 3, count = 9;
+  var sample = new Float32Array(count * dim);
+  var u = uniformVec(count * dim, 91, 1);
+  for (var i = 0; i < count * dim; i++) sample[i] = u[i];
+  // cluster 0: one large value followed by many small ones in each column
+  sample[0] = 16777216; sample[1] = 1; sample[2] = 3.0000002; sample[3] = -8388608;
+  for (var r = 1; r < 6; r++) { sample[r * dim] = 1; sample[r * dim + 1] = 1e-8; sample[r * dim + 2] = 1.1920929e-7; sample[r * dim + 3] = 0.75; }
+  var assign = new Uint32Array([0, 0, 0, 0, 0, 0, 2, 2, 0]);  // cluster 1 stays empty
+  var cen = new Float32Array(nlist * dim);
+  var before = f32bits(cen);
+  out.mean_update = { dim: dim, nlist: nlist, count: count, seed: 4242, sample: f32bits(sample),
+                      assign: Array.from(assign), centroids_in: before,
+                      centroids_out: f32bits(meanUpdate(sample, count, dim, assign, cen, nlist, 4242)) };
+  var s64 = 0;
+  for (var r3 = 0; r3 < count; r3++) if (assign[r3] === 0) s64 += sample[r3 * dim];
+  var acc = new Float32Array(1);
+  for (var r4 = 0; r4 < count; r4++) if (assign[r4] === 0) acc[0] += sample[r4 * dim];
+  out.mean_update.col0_f64_sum = s64;
+  out.mean_update.col0_f32_sum = acc[0];
+})();
 
 process.stdout.write(JSON.stringify(out));

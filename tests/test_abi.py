@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -60,3 +61,28 @@ def test_struct_layouts_match_header():
     assert ctypes.sizeof(_lib.IndexDesc) == 18 * 4
     # IndexStats: u64 + 7*u32 + f32 + 3*f64 + 2*u64
     assert ctypes.sizeof(_lib.IndexStats) == 8 + 8 * 4 + 3 * 8 + 2 * 8
+
+
+def test_query_lengths_are_checked_before_the_library():
+    """The Python binding refuses a query whose length is not the index
+    dimension (a short buffer would otherwise be read past its end); no
+    device is needed because the check runs before any library call."""
+    from browservec_amd import _lib as L
+    from browservec_amd.index import IVFIndex, NativeIndex
+
+    fake = NativeIndex.__new__(NativeIndex)
+    fake.dim = 8
+    fake.lib = None
+    fake.handle = None
+    for call in (lambda: fake.query(np.zeros(7, np.float32), 3),
+                 lambda: fake.query_masked(np.zeros(9, np.float32), 3, np.ones(1, np.uint32)),
+                 lambda: fake.query_batch(np.zeros(15, np.float32), 2, 3),
+                 lambda: fake.search(np.zeros(12, np.float32), 4, 3),
+                 lambda: fake.rerank(np.zeros(4, np.float32), [0, 1], 2)):
+        with pytest.raises(L.BVError) as e:
+            call()
+        assert e.value.code == L.BV_E_INVALID and "floats, got" in str(e.value)
+    fake_ivf = IVFIndex.__new__(IVFIndex)
+    fake_ivf.dim = 8
+    with pytest.raises(L.BVError):
+        fake_ivf.export_probe_scores(np.zeros(12, np.float32))

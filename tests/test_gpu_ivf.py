@@ -308,3 +308,52 @@ def test_ivf_probe_scores_widest_query(ctx):
         got = {h.row for h in idx.query(q, n)}
         assert got == probed_rows(cen, off, lrows, q, 3), i
     idx.destroy()
+
+
+def test_ivf_lazy_build_inside_a_query(ctx):
+    """The first query after an append builds the lists (ivfquant.ts:461)
+    and, with targetRecall and no nprobe, tunes nprobe before it scans.
+    Whatever entry point triggers that build (query, search, search_device),
+    its results equal those of an index built explicitly first, and the
+    tuned nprobe equals the oracle's."""
+    import torch
+
+    from browservec_amd import IVFQuantIndex
+
+    dim, n = 96, 6000
+    ivf = {"nlist": 24, "iters": 4, "targetRecall": 0.9}
+    say("ivf lazy build")
+    data = clustered(n, dim, 40, 0.2, seed=33)
+    qs = np.stack([o.normalize(q) for q in data[[3, 2000, 4500]] + gaussian(3, dim, 34, normalize=False) * 0.05])
+    qs = qs.astype(np.float32)
+
+    def fresh():
+        idx = IVFQuantIndex(ctx, dim, bits=8, ivf=ivf)
+        idx.append(data, n)
+        return idx
+
+    ref_idx = fresh()
+    ref_idx.build()
+    want_q = ref_idx.query(qs[0], 10)
+    want_rows, want_scores, want_cnt = ref_idx.search(qs, 40, 10)
+    ref = reference_build(data, dim, 8, ivf)
+    want_np, _ = reference_tune(data, dim, 8, ref, 0.9)
+    assert ref_idx.stats()["nprobe"] == want_np
+
+    a = fresh()
+    assert a.query(qs[0], 10) == want_q
+    assert a.stats()["nprobe"] == want_np
+    b = fresh()
+    rows, scores, cnt = b.search(qs, 40, 10)
+    assert np.array_equal(rows, want_rows) and np.array_equal(scores.view(np.uint32), want_scores.view(np.uint32))
+    c = fresh()
+    d_q = torch.from_numpy(qs).cuda()
+    d_rows = torch.empty(3, 10, dtype=torch.int32, device="cuda")
+    d_sc = torch.empty(3, 10, dtype=torch.float32, device="cuda")
+    d_n = torch.empty(3, dtype=torch.int32, device="cuda")
+    c.search_device(d_q.data_ptr(), 3, 40, 10, d_rows.data_ptr(), d_sc.data_ptr(), d_n.data_ptr())
+    c.sync()
+    assert np.array_equal(d_rows.cpu().numpy().view(np.uint32), want_rows)
+    assert np.array_equal(d_sc.cpu().numpy().view(np.uint32), want_scores.view(np.uint32))
+    for idx in (ref_idx, a, b, c):
+        idx.destroy()

@@ -27,18 +27,32 @@ def run_node(script: str, timeout: int = 120) -> subprocess.CompletedProcess:
 
 
 def test_addon_exports_the_seam():
+    """Each class carries the duck-typed members of its reference
+    counterpart, and no others that would change BrowserVec's path:
+    queryMasked only on flat / quantized (flat.ts:128, quant.ts:174),
+    queryBatch only on flat fp32 (whose batch equals single queries),
+    setNprobe and the IVF getters only on IVF (ivf.ts:123-150,
+    ivfquant.ts:151-212), ingestMode on quantized kinds."""
     r = run_node(f"""
 const m = require({json.dumps(MODULE)});
-const proto = Object.getOwnPropertyNames(m.HipIndex.prototype);
-console.log(JSON.stringify({{abi: m.abiVersion, proto: proto, native: Object.keys(m.native)}}));
+const has = (C) => ['size', 'append', 'query', 'queryMasked', 'queryBatch', 'setNprobe', 'destroy', 'search',
+  'rerankExact', 'chunkCount', 'nlist', 'nprobe', 'tunedRecall', 'trainMode', 'ingestMode', 'build']
+  .filter((k) => k in C.prototype);
+console.log(JSON.stringify({{abi: m.abiVersion, native: Object.keys(m.native),
+  flat: has(m.HipFlatIndex), quant: has(m.HipQuantIndex), ivf: has(m.HipIvfIndex),
+  ivfquant: has(m.HipIvfQuantIndex)}}));
 """)
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout.strip().splitlines()[-1])
     assert out["abi"] == 1
-    for member in ("size", "append", "query", "queryMasked", "queryBatch", "setNprobe", "destroy", "rerankExact",
-                   "search"):
-        assert member in out["proto"], member
-    for fn in ("openDevice", "createIndex", "append", "query", "queryMasked", "queryBatch", "search", "rerank"):
+    common = {"size", "append", "query", "destroy", "search", "rerankExact", "chunkCount"}
+    assert set(out["flat"]) == common | {"queryMasked", "queryBatch"}
+    assert set(out["quant"]) == common | {"queryMasked", "ingestMode"}
+    ivf = common | {"setNprobe", "nlist", "nprobe", "tunedRecall", "trainMode", "build"}
+    assert set(out["ivf"]) == ivf
+    assert set(out["ivfquant"]) == ivf | {"ingestMode"}
+    for fn in ("openDevice", "debugInject", "createIndex", "append", "build", "query", "queryMasked", "queryBatch",
+               "search", "rerank"):
         assert fn in out["native"], fn
 
 
@@ -70,20 +84,39 @@ const dim = %(dim)d, n = %(n)d, nq = %(nq)d;
   const ctx = new m.HipDeviceContext(0);
   const out = {};
   const flat = m.buildIndex(ctx, dim, 'cosine', 0);
-  flat.append(rows, n);
+  const pending = flat.append(rows, n);
+  out.appendIsPromise = pending instanceof Promise;
+  await pending;
   out.flatSize = flat.size;
   out.flat = await flat.queryBatch(qs, nq, 10);
+  try { await flat.query(qs.subarray(0, dim - 1), 5); } catch (e) { out.shortQuery = [e.constructor.name, e.message]; }
+  try { await flat.queryBatch(qs.subarray(0, dim * 2), 3, 5); } catch (e) { out.shortBatch = e.message; }
+  try { await flat.append(rows.subarray(0, dim + 1), 1); } catch (e) { out.badAppend = [e.code, e.message]; }
   const quant = m.buildIndex(ctx, dim, 'cosine', 8, {});
-  quant.append(rows, n);
+  out.ingestBefore = quant.ingestMode;
+  await quant.append(rows, n);
+  out.ingestAfter = quant.ingestMode;
   out.approx = await quant.query(qs.subarray(0, dim), 40);
   out.search = await quant.search(qs, nq, 40, 10);
   out.rerank = await quant.rerankExact(qs.subarray(0, dim), out.approx, 10);
   const ivf = m.buildIndex(ctx, dim, 'cosine', 8, {}, {nlist: 16, iters: 3, nprobe: 4});
-  ivf.append(rows, n);
-  out.ivf = await ivf.queryBatch(qs, nq, 10);
+  await ivf.append(rows, n);
+  out.trainBefore = ivf.trainMode;
+  out.ivf = [];
+  for (let i = 0; i < nq; i++) out.ivf.push(await ivf.query(qs.subarray(i * dim, (i + 1) * dim), 10));
+  out.trainAfter = ivf.trainMode;
   out.ivfStats = [ivf.nlist, ivf.nprobe];
   try { m.buildIndex(ctx, dim, 'l2', 0, {}, {}); } catch (e) { out.ivfL2 = e.message; }
-  flat.destroy(); quant.destroy(); ivf.destroy(); ctx.destroy();
+  // a destroy while a call is in flight: the call still completes
+  const q2 = quant.query(qs.subarray(0, dim), 5);
+  quant.destroy();
+  out.inflight = (await q2).length;
+  // the device-lost path, forced from the host
+  ctx.debugInject('lost');
+  out.lost = ctx.lost;
+  try { await flat.query(qs.subarray(0, dim), 5); } catch (e) { out.lostErr = [e.code, e.message]; }
+  out.sizeAfterLost = flat.size;
+  flat.destroy(); ivf.destroy(); ctx.destroy();
   console.log(JSON.stringify(out));
 })().catch((e) => { console.error(e.code, e.message); process.exit(3); });
 """
@@ -104,7 +137,16 @@ def test_node_results_equal_python_binding(tmp_path):
                                 "queries": json.dumps(str(tmp_path / "q.f32")), "dim": dim, "n": n, "nq": nq})
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout.strip().splitlines()[-1])
-    assert out["flatSize"] == n
+    assert out["flatSize"] == n and out["appendIsPromise"]
+    assert out["shortQuery"] == ["TypeError", f"expected {dim} floats, got {dim - 1}"]
+    assert out["shortBatch"] == f"expected {3 * dim} floats, got {2 * dim}"
+    assert out["badAppend"] == ["BV_E_INVALID", f"expected {dim} floats, got {dim + 1}"]
+    assert out["ingestBefore"] == "pending" and out["ingestAfter"] == "device"
+    assert out["trainBefore"] == "pending" and out["trainAfter"] == "device"
+    assert out["inflight"] == 5
+    assert out["lost"] is True
+    assert out["lostErr"] == ["BV_E_DEVICE_LOST", "GPU device lost; re-create the store"]
+    assert out["sizeAfterLost"] == n
 
     ctx = DeviceContext(0)
     try:
@@ -120,6 +162,7 @@ def test_node_results_equal_python_binding(tmp_path):
         py_flat = flat.query_batch(q, nq, 10)
         for i in range(nq):
             same(out["flat"][i], py_flat[i])
+            same(out["flat"][i], flat.query(q[i], 10))
         py_approx = quant.query(q[0], 40)
         same(out["approx"], py_approx)
         rows, scores, cnt = quant.search(q, 40, 10)
@@ -129,9 +172,8 @@ def test_node_results_equal_python_binding(tmp_path):
         same(out["rerank"], quant.rerank(q[0], [h.row for h in py_approx], 10))
         ivf = IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 16, "iters": 3, "nprobe": 4})
         ivf.append(x, n)
-        py_ivf = ivf.query_batch(q, nq, 10)
         for i in range(nq):
-            same(out["ivf"][i], py_ivf[i])
+            same(out["ivf"][i], ivf.query(q[i], 10))
         assert out["ivfStats"] == [16, 4]
         assert out["ivfL2"] == "IVF supports metric cosine/dot only (l2 is later work)"
         ivf.destroy()

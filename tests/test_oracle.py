@@ -375,12 +375,35 @@ def test_kmeans_known_answers():
     assert any(np.array_equal(c[1], seeds[i]) for i in range(2))
 
 
-def test_random_init_is_deterministic_row_picks():
-    sample = o.uniform_vectors(20, 4, 3)
-    a = o.random_init_centroids(sample, 3, 9)
-    assert np.array_equal(a, o.random_init_centroids(sample, 3, 9))
-    picks = np.floor(o.mulberry32_stream(9, 3) * 20).astype(int)
-    assert np.array_equal(a, o.normalize_rows(sample[picks]))
+def test_random_init_picks_match_js_engine(js):
+    """The rows randomInitCentroids copies (kmeans.ts:154-170), pinned by the
+    picks V8 computed: each sample row is a distinct unit vector (angle
+    2*pi*r/count), so the row behind every centroid is recoverable."""
+    for case in js["init_picks"]:
+        count, nlist = case["count"], case["nlist"]
+        ang = 2 * np.pi * np.arange(count) / count
+        sample = np.stack([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+        cen = o.random_init_centroids(sample, nlist, case["seed"])
+        got = np.argmax(cen.astype(np.float64) @ sample.astype(np.float64).T, axis=1)
+        assert got.tolist() == case["picks"], case["seed"]
+
+
+def test_update_centroids_matches_js_engine(js):
+    """updateCentroids (kmeans.ts:177-209) against V8's Float32Array run on a
+    sample whose sequential f32 column sums differ from the f64 sums (a large
+    value absorbs later small ones), with an empty cluster re-seeded from the
+    sample and normalizeRows after."""
+    m = js["mean_update"]
+    assert m["col0_f32_sum"] != m["col0_f64_sum"]  # the fixture separates the two
+    sample = bits_to_f32(m["sample"]).reshape(m["count"], m["dim"])
+    cen_in = bits_to_f32(m["centroids_in"]).reshape(m["nlist"], m["dim"])
+    got, counts = o.update_centroids(sample, np.array(m["assign"], np.uint32), cen_in, m["seed"])
+    assert np.array_equal(f32_bits(got).reshape(-1), np.asarray(m["centroids_out"], np.uint32))
+    assert counts.tolist() == [int(np.sum(np.array(m["assign"]) == c)) for c in range(m["nlist"])]
+    # an f64 accumulation gives a different centroid 0: the check separates them
+    f64 = sample[np.array(m["assign"]) == 0].astype(np.float64).sum(axis=0) / counts[0]
+    f64 = (f64 / np.linalg.norm(f64)).astype(np.float32)
+    assert not np.array_equal(f32_bits(f64), f32_bits(got[0]))
 
 
 def test_assign_argmax_lowest_index_wins():
@@ -394,6 +417,22 @@ def test_assign_argmax_lowest_index_wins():
     want = np.argmax(x.astype(np.float64) @ c.T.astype(np.float64), axis=1)
     assert np.array_equal(o.assign_f32(x, c, 0), want)
     assert np.array_equal(o.assign_f32(x, c, 1), want)
+
+
+def test_assign_vector_path_equals_scalar_chain():
+    """The AVX2 assignment (eight centroids per lane group, four groups in
+    flight) runs each lane's fmaf chain exactly as the scalar loop: equal
+    assignments, including ties between duplicated centroids and a centroid
+    count that leaves partial lane groups."""
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((300, 96)).astype(np.float32)
+    c = rng.standard_normal((37, 96)).astype(np.float32)
+    c[20] = c[3]
+    c[36] = c[3]
+    x[:10] = c[3]
+    a1 = o.assign_f32(x, c, 1)
+    assert np.array_equal(a1, o.assign_f32(x, c, 2))
+    assert np.all(a1[:10] == 3)
 
 
 def test_probe_scores_vs_long_double():
@@ -420,11 +459,40 @@ def test_csr_and_tuning_tables():
     assert len(set(p)) == 32 and p == sorted(p) and max(p) < 1000
 
 
-def test_reservoir_fill_then_replace():
-    res = o.Reservoir(4, 7)
-    slots = [res.slot() for _ in range(20)]
-    assert slots[:4] == [0, 1, 2, 3]
-    rng = o.mulberry32_stream(7, 16)
-    for i, s in enumerate(slots[4:]):
-        j = int(np.floor(rng[i] * (4 + i + 1)))
-        assert s == (j if j < 4 else -1)
+def test_reservoir_matches_js_engine(js):
+    """Slots of the IVF reservoir (ivfquant.ts:114-124, 235-245) pinned by
+    V8's run of the same recurrence (Math.floor of the f64 product)."""
+    for case in js["reservoir"]:
+        res = o.Reservoir(case["cap"], (case["seed"] ^ 0x85EBCA6B) & 0xFFFFFFFF)
+        assert [res.slot() for _ in range(case["n"])] == case["slots"], case["seed"]
+
+
+def test_reservoir_is_a_uniform_sample():
+    """What the mathematics fixes for reservoir sampling: the first `cap`
+    rows fill slots 0..cap-1 in order; row i >= cap is admitted with
+    probability cap/(i+1) (a `seen` for `seen + 1` slip gives cap/i, 1.0 at
+    i = cap); and after n rows every row is in the sample with probability
+    cap/n.  Frequencies over 6000 seeds must sit within 5 standard
+    deviations of those values."""
+    cap, n, trials = 8, 48, 6000
+    admit = np.zeros(n)
+    held = np.zeros(n)
+    for seed in range(trials):
+        res = o.Reservoir(cap, (seed * 2654435761) & 0xFFFFFFFF)
+        owner = [-1] * cap
+        for i in range(n):
+            s = res.slot()
+            if i < cap:
+                assert s == i
+            if s >= 0:
+                admit[i] += 1
+                owner[s] = i
+        for r in owner:
+            held[r] += 1
+    for i in range(cap, n):
+        p = cap / (i + 1)
+        sd = np.sqrt(p * (1 - p) / trials)
+        assert abs(admit[i] / trials - p) <= 5 * sd, (i, admit[i] / trials, p)
+    p = cap / n
+    sd = np.sqrt(p * (1 - p) / trials)
+    assert np.all(np.abs(held / trials - p) <= 5 * sd), held / trials
