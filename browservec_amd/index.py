@@ -210,6 +210,21 @@ class NativeIndex:
         L.check(self.lib.bv_index_export_scores(self.handle, _ptr(q), _ptr(out)))
         return out
 
+    # quantized kinds (QuantIndex, IVFQuantIndex): parity exports
+    def export_codes(self, row0: int = 0, count: int | None = None):
+        count = self.size - row0 if count is None else count
+        words = np.empty((count, self.words_per_row), np.uint32)
+        scales = np.empty(count, np.float32)
+        L.check(self.lib.bv_index_export_codes(self.handle, row0, count, _ptr(words), _ptr(scales)))
+        return words, scales
+
+    def export_rotated_query(self, q) -> np.ndarray:
+        q = _f32(q).reshape(-1)
+        _check_len(q, self.dim)
+        out = np.empty(self.padded_dim, np.float32)
+        L.check(self.lib.bv_index_export_rotated_query(self.handle, _ptr(q), _ptr(out)))
+        return out
+
     # device-resident entry points (pointers are integers, e.g. tensor.data_ptr())
     def append_device(self, d_ptr: int, count: int) -> None:
         L.check(self.lib.bv_index_append_device(self.handle, ctypes.c_void_p(d_ptr), int(count)))
@@ -267,21 +282,6 @@ class QuantIndex(NativeIndex):
         """ingestMode (src/index/quant.ts:115-118): where rotate+quantize ran,
         'pending' before the first append."""
         return "device" if self.size else "pending"
-
-    def export_codes(self, row0: int = 0, count: int | None = None):
-        count = self.size - row0 if count is None else count
-        words = np.empty((count, self.words_per_row), np.uint32)
-        scales = np.empty(count, np.float32)
-        L.check(self.lib.bv_index_export_codes(self.handle, row0, count, _ptr(words), _ptr(scales)))
-        return words, scales
-
-    def export_rotated_query(self, q) -> np.ndarray:
-        q = _f32(q).reshape(-1)
-        _check_len(q, self.dim)
-        out = np.empty(self.padded_dim, np.float32)
-        L.check(self.lib.bv_index_export_rotated_query(self.handle, _ptr(q), _ptr(out)))
-        return out
-
 
 class IVFIndex(NativeIndex):
     """IVF over fp32 rows (src/index/ivf.ts:51): spherical k-means lists,
