@@ -101,6 +101,7 @@ SIGNATURES = {
     "bv_index_rerank": [vp, vp, vp, u32, u32, vp, vp, vp],
     "bv_index_search": [vp, vp, u32, u32, u32, vp, vp, vp],
     "bv_index_search_device": [vp, vp, u32, u32, u32, vp, vp, vp],
+    "bv_index_search_device_noalloc": [vp, vp, u32, u32, u32, vp, vp, vp],
     "bv_index_append_device": [vp, vp, u64],
     "bv_index_sync": [vp],
     "bv_index_stream": [vp, ctypes.POINTER(vp)],

@@ -38,7 +38,29 @@ struct bv_device {
     hipDeviceProp_t prop{};
     bool lost = false;
     bool inject_append_oom = false;  // bv_debug_inject: fail the next append's allocation
+    void *scratch = nullptr;         // this GPU's copy of the no-allocation scratch array
 };
+
+// ------------------------------------------------- no-allocation scratch --
+// The fused scan's scratch for bv_index_search_device_noalloc lives in a
+// file-scope device array of BV_NOALLOC_SCRATCH_BYTES; every GPU the library
+// runs on holds its own copy until the process ends.  In host code `scratch`
+// names a host-side stand-in, never device memory: its device address comes
+// from hipGetSymbolAddress, resolved once per device with that device
+// current (bv_device_open) and used everywhere host code needs the array.
+static __device__ __align__(256) unsigned char scratch[BV_NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[256];  // per device ordinal; null until resolved
+
+static void *resolve_scratch(int ordinal) {
+    if (ordinal < 0 || ordinal >= 256) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[ordinal]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess) g_scratch_ptr[ordinal] = ptr;
+    }
+    return g_scratch_ptr[ordinal];
+}
 
 static int hip_fail(bv_device *dev, hipError_t e, const char *what) {
     if (e == hipErrorOutOfMemory) return fail(BV_E_OOM, "%s: out of device memory", what);
@@ -192,6 +214,7 @@ extern "C" int bv_device_open(int ordinal, bv_device **out) {
         delete d;
         return fail(BV_E_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
     }
+    d->scratch = resolve_scratch(ordinal);  // with this device current
     *out = d;
     return BV_OK;
 }
@@ -895,10 +918,46 @@ static uint32_t grid_for(const bv_index *idx, uint64_t n) {
     return (uint32_t)g;
 }
 
-// Scratch of the fused scan for nq queries: coordination state and wave
-// maxima must start zeroed (the kernel leaves them zeroed).
-static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kprime, uint32_t rr_dim, ScanArgs &a) {
+// Scratch of the fused scan for nq queries: per-query coordination state,
+// per-wave maxima (both must start zeroed; the kernel leaves them zeroed),
+// the flushed (scan key, exact key) pairs and the merged keys.  Byte offsets
+// from one base, 256-byte aligned.
+struct ScanLayout {
+    size_t qstate, wmax, cand_keys, merged, merged_n, total;
+    uint64_t cap;  // pairs per query
+    uint32_t wcap;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static ScanLayout scan_layout(uint32_t nq, uint32_t grid, uint32_t kprime) {
+    ScanLayout L{};
     const size_t slots = (size_t)grid * (SCAN_WG / 64);
+    const uint64_t ng = grid < (uint32_t)NGROUP ? grid : (uint32_t)NGROUP;
+    L.wcap = scan_wcap(kprime);
+    L.cap = ng * ((grid + ng - 1) / ng) * (SCAN_WG / 64) * L.wcap;
+    L.qstate = 0;
+    L.wmax = align256(L.qstate + (size_t)nq * sizeof(QState));
+    L.cand_keys = align256(L.wmax + (size_t)nq * slots * 8);
+    L.merged = align256(L.cand_keys + (size_t)nq * L.cap * 16);
+    L.merged_n = align256(L.merged + (size_t)nq * kprime * 8);
+    L.total = align256(L.merged_n + (size_t)nq * 4);
+    return L;
+}
+
+static void scan_bind(const ScanLayout &L, char *base, uint32_t rr_dim, ScanArgs &a) {
+    a.qs = (QState *)(base + L.qstate);
+    a.wmax = (uint64_t *)(base + L.wmax);
+    a.cand_keys = (uint64_t *)(base + L.cand_keys);
+    a.cand_cap = L.cap;
+    a.wcap = L.wcap;
+    a.wstride = L.wcap + ((rr_dim & ~3u) + 1) / 2 * 2;  // list + re-rank staging (doubles)
+    a.merged = (uint64_t *)(base + L.merged);
+    a.merged_n = (uint32_t *)(base + L.merged_n);
+}
+
+static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kprime, uint32_t rr_dim, ScanArgs &a) {
+    const ScanLayout L = scan_layout(nq, grid, kprime);
     {
         const size_t old = idx->qstate.cap;
         HIPX(idx->dev, idx->qstate.ensure((size_t)nq * sizeof(QState), 0, idx->stream), "scratch");
@@ -907,21 +966,18 @@ static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kpri
     }
     {
         const size_t old = idx->wmax.cap;
-        HIPX(idx->dev, idx->wmax.ensure((size_t)nq * slots * 8, 0, idx->stream), "scratch");
+        HIPX(idx->dev, idx->wmax.ensure(L.cand_keys - L.wmax, 0, idx->stream), "scratch");
         if (idx->wmax.cap != old) HIPX(idx->dev, hipMemsetAsync(idx->wmax.p, 0, idx->wmax.cap, idx->stream), "scratch");
     }
-    const uint64_t ng = grid < (uint32_t)NGROUP ? grid : (uint32_t)NGROUP;
-    const uint32_t wcap = scan_wcap(kprime);
-    const uint64_t cap = ng * ((grid + ng - 1) / ng) * (SCAN_WG / 64) * wcap;
-    HIPX(idx->dev, idx->cand_keys.ensure((size_t)nq * cap * 16, 0, idx->stream), "scratch");
+    HIPX(idx->dev, idx->cand_keys.ensure((size_t)nq * L.cap * 16, 0, idx->stream), "scratch");
     HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
     HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
     a.qs = idx->qstate.as<QState>();
     a.wmax = idx->wmax.as<uint64_t>();
     a.cand_keys = idx->cand_keys.as<uint64_t>();
-    a.cand_cap = cap;
-    a.wcap = wcap;
-    a.wstride = wcap + ((rr_dim & ~3u) + 1) / 2 * 2;  // list + re-rank staging (doubles)
+    a.cand_cap = L.cap;
+    a.wcap = L.wcap;
+    a.wstride = L.wcap + ((rr_dim & ~3u) + 1) / 2 * 2;  // list + re-rank staging (doubles)
     a.merged = idx->merged.as<uint64_t>();
     a.merged_n = idx->merged_n.as<uint32_t>();
     return BV_OK;
@@ -1012,6 +1068,35 @@ static void timing_collect(bv_index *idx) {
     idx->tev_used = 0;
 }
 
+// Arguments of the fused scan shared by every caller: the rows / codes, the
+// row count or candidate set, the fetch and the outputs.
+static void scan_common(const bv_index *idx, const float *d_q, uint64_t n, uint32_t grid, uint32_t kprime,
+                        uint32_t k_out, bool rerank, const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows,
+                        float *d_scores, uint32_t *d_n, ScanArgs &a) {
+    a.codes = idx->quant ? idx->codes.p : idx->raw.p;
+    a.row_bytes = idx->row_bytes;
+    a.units = idx->units;
+    a.padded_dim = idx->P;
+    a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A) ? idx->scales.as<float>() : nullptr;
+    a.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
+    a.mask = d_mask;
+    a.mask_bits = mask_bits;
+    a.n = n;
+    a.kprime = kprime;
+    a.grid = grid;
+    a.k_out = k_out;
+    a.out_rows = d_rows;
+    a.out_scores = d_scores;
+    a.out_n = d_n;
+    if (rerank) {
+        // the scan re-ranks its fetch exactly against the stored fp32 rows
+        a.rr_src = idx->raw.as<float>();
+        a.rr_dim = idx->dim;
+        a.rr_q = d_q;
+        a.rr_q_stride = idx->dim;
+    }
+}
+
 // The fused single-launch scan (one query per grid row): query transform,
 // scan, top-kprime and exact re-rank.
 static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
@@ -1042,28 +1127,7 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
     const uint32_t grid = grid_for(idx, std::max<uint64_t>(n, 1));
     rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a);
     if (rc) return rc;
-    a.codes = idx->quant ? idx->codes.p : idx->raw.p;
-    a.row_bytes = idx->row_bytes;
-    a.units = idx->units;
-    a.padded_dim = idx->P;
-    a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A) ? idx->scales.as<float>() : nullptr;
-    a.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
-    a.mask = d_mask;
-    a.mask_bits = mask_bits;
-    a.n = n;
-    a.kprime = kprime;
-    a.grid = grid;
-    a.k_out = k_out;
-    a.out_rows = d_rows;
-    a.out_scores = d_scores;
-    a.out_n = d_n;
-    if (rerank) {
-        // the scan re-ranks its fetch exactly against the stored fp32 rows
-        a.rr_src = idx->raw.as<float>();
-        a.rr_dim = idx->dim;
-        a.rr_q = d_q;
-        a.rr_q_stride = idx->dim;
-    }
+    scan_common(idx, d_q, n, grid, kprime, k_out, rerank, d_mask, mask_bits, d_rows, d_scores, d_n, a);
     timing_begin(idx);
     HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, idx->stream), "scan kernel");
     timing_end(idx);
@@ -1541,6 +1605,56 @@ extern "C" int bv_index_search_device(bv_index *idx, const float *d_queries, uin
     rc = ensure_built(idx);
     if (rc) return rc;
     return run_pipeline(idx, d_queries, nq, fe ? fe : kk, kk, fe != 0, nullptr, 0, d_rows, d_scores, d_n_out);
+}
+
+// bv_index_search_device without any device allocation: the fused scan on
+// every query, its scratch carved from this GPU's copy of `scratch` (used
+// through the address hipGetSymbolAddress gave, never through the name).
+// The coordination state and wave maxima are cleared by a fill kernel on
+// every call (the previous call may have laid the array out differently).
+extern "C" int bv_index_search_device_noalloc(bv_index *idx, const float *d_queries, uint32_t nq, uint32_t fetch,
+                                              uint32_t k, uint32_t *d_rows, float *d_scores, uint32_t *d_n_out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (nq == 0) return BV_OK;
+    if (!d_queries || !d_rows || !d_scores || !d_n_out) return fail(BV_E_INVALID, "null argument");
+    if (fetch && !idx->quant) return fail(BV_E_UNSUPPORTED, "re-rank needs a quantized index");
+    if (idx->rows == 0 || k == 0) return fail(BV_E_STATE, "empty index or k == 0");
+    if (idx->ivf)
+        return fail(BV_E_UNSUPPORTED, "IVF queries need list scratch and a possible build: use bv_index_search_device");
+    if (idx->quant && !scan_prep_supported(idx->codec, idx->units, idx->P))
+        return fail(BV_E_UNSUPPORTED, "this code layout needs a query buffer: use bv_index_search_device");
+    if (!idx->dev->scratch) return fail(BV_E_HIP, "the no-allocation scratch array has no device address");
+    const uint32_t kk = (uint32_t)std::min<uint64_t>(k, idx->rows);
+    const uint32_t fe = fetch ? (uint32_t)std::min<uint64_t>(std::max(fetch, kk), idx->rows) : 0;
+    if (fe > (uint32_t)MAX_KPRIME || kk > (uint32_t)MAX_KPRIME)
+        return fail(BV_E_UNSUPPORTED, "fetch %u exceeds the fused top-k limit %d", fe, MAX_KPRIME);
+    const uint32_t kprime = fe ? fe : kk;
+    const bool rerank = fe != 0;
+    const uint32_t grid = grid_for(idx, idx->rows);
+    const ScanLayout L = scan_layout(nq, grid, kprime);
+    if (L.total > (size_t)BV_NOALLOC_SCRATCH_BYTES)
+        return fail(BV_E_INVALID, "%u queries with fetch %u need %zu bytes of scratch; the limit is %zu", nq, kprime,
+                    L.total, (size_t)BV_NOALLOC_SCRATCH_BYTES);
+    char *base = (char *)idx->dev->scratch;
+    HIPX(idx->dev, launch_zero(base, L.cand_keys, idx->stream), "scratch clear");
+    ScanArgs a{};
+    if (idx->quant) {  // the scan rotates and transforms the fp32 queries itself
+        a.qraw = d_queries;
+        a.qdim = idx->dim;
+        a.signs = idx->signs.as<float>();
+        a.rounds = idx->d.rounds;
+    } else {
+        a.q = d_queries;
+        a.q_stride = (uint64_t)idx->dim * 4;
+    }
+    scan_bind(L, base, rerank ? idx->dim : 0, a);
+    scan_common(idx, d_queries, idx->rows, grid, kprime, kk, rerank, nullptr, 0, d_rows, d_scores, d_n_out, a);
+    HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, idx->stream), "scan kernel");
+    idx->last_scanned = idx->rows * nq;
+    return BV_OK;
 }
 
 extern "C" int bv_index_sync(bv_index *idx) {

@@ -286,6 +286,10 @@ hipError_t launch_mq_scan_f32(const MqArgs &a, hipStream_t s);
 hipError_t launch_mq_rerank(const MqRerankArgs &a, uint32_t nq, hipStream_t s);
 hipError_t launch_mq_select(const MqSelArgs &a, uint32_t nq, hipStream_t s);
 
+// Zeroes `bytes` (a multiple of 4) at p with a plain kernel (no memset node,
+// so the launch is safe to record in a captured graph).
+hipError_t launch_zero(void *p, size_t bytes, hipStream_t s);
+
 bool scan_supported(int codec, uint32_t units);
 hipError_t launch_scan(int codec, uint32_t units, const ScanArgs &a, uint32_t nq, hipStream_t s);
 hipError_t launch_encode(const EncodeArgs &a, hipStream_t s);

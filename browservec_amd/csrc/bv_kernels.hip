@@ -72,7 +72,22 @@ __global__ __launch_bounds__(64) void rerank_topk(RerankArgs a) {
     }
 }
 
+__global__ __launch_bounds__(256) void zero_words(uint32_t *p, uint64_t words) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride) p[i] = 0u;
+}
+
 }  // namespace
+
+hipError_t launch_zero(void *p, size_t bytes, hipStream_t s) {
+    if (bytes == 0) return hipSuccess;
+    if (bytes & 3) return hipErrorInvalidValue;
+    const uint64_t words = bytes / 4;
+    uint64_t blocks = (words + 255) / 256;
+    if (blocks > 2048) blocks = 2048;
+    hipLaunchKernelGGL(zero_words, dim3((uint32_t)blocks), dim3(256), 0, s, (uint32_t *)p, words);
+    return hipGetLastError();
+}
 
 
 bool scan_supported(int codec, uint32_t units) {

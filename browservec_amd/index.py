@@ -234,6 +234,13 @@ class NativeIndex:
                                                 ctypes.c_void_p(d_rows), ctypes.c_void_p(d_scores),
                                                 ctypes.c_void_p(d_n)))
 
+    def search_device_noalloc(self, d_q: int, nq: int, fetch: int, k: int, d_rows: int, d_scores: int,
+                              d_n: int) -> None:
+        """search_device without any device allocation (library-owned scratch)."""
+        L.check(self.lib.bv_index_search_device_noalloc(self.handle, ctypes.c_void_p(d_q), int(nq), int(fetch),
+                                                        int(k), ctypes.c_void_p(d_rows), ctypes.c_void_p(d_scores),
+                                                        ctypes.c_void_p(d_n)))
+
     def sync(self) -> None:
         L.check(self.lib.bv_index_sync(self.handle))
 

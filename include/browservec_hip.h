@@ -187,6 +187,21 @@ int bv_index_search(bv_index *idx, const float *queries, uint32_t nq, uint32_t f
  * and wait once for the batch (one overflow flag per query is read back). */
 int bv_index_search_device(bv_index *idx, const float *d_queries, uint32_t nq, uint32_t fetch, uint32_t k,
                            uint32_t *d_rows, float *d_scores, uint32_t *d_n_out);
+/* bv_index_search_device for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It has no counterpart in the reference.  Every query runs the
+ * fused single-query scan with its scratch in a library-owned array of
+ * BV_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; the call
+ * allocates nothing and launches only kernels (no memset or copy nodes).
+ * Serves flat indexes and quantized indexes whose scan transforms queries
+ * in-kernel (int8 / int4 / 1-bit / Hamming at padded dimensions 64..1024),
+ * not IVF.  BV_E_INVALID when nq, fetch and k need more scratch than the
+ * array holds (about 10.5 MB per query at 1M rows and fetch 100).  All calls
+ * on one GPU share the array: calls that overlap on that GPU (other streams,
+ * other threads, other indexes) race. */
+#define BV_NOALLOC_SCRATCH_BYTES (64u << 20)
+int bv_index_search_device_noalloc(bv_index *idx, const float *d_queries, uint32_t nq, uint32_t fetch, uint32_t k,
+                                   uint32_t *d_rows, float *d_scores, uint32_t *d_n_out);
 /* Append rows that already live in device memory (count*dim floats). */
 int bv_index_append_device(bv_index *idx, const float *d_data, uint64_t count);
 /* Wait for all work enqueued on the index's stream. */
