@@ -1,22 +1,31 @@
-"""Benchmark of the TurboQuant int8 search path on one MI355X.
+"""Benchmark of BrowserVec's search path on one MI355X.
 
-Workload (default): 1,000,000 x 768 fp32 rows from a mixture of 1024 Gaussian
-clusters (unit-norm centres, sigma 0.1), L2-normalized; rotated with the
-seeded randomized Hadamard transform to P=1024 and int8-quantized on the
-device; 256 queries = corpus rows + N(0, 0.05^2) noise, normalized.  One step
-= one query (batch 1): rotate, scan 1M codes with fused top-100, exact f64
-re-rank to top-10.  Inputs are resident in HBM before timing starts.
+Headline workload (`value`): 1,000,000 x 768 fp32 rows from a mixture of
+1024 Gaussian clusters (unit-norm centres, sigma 0.1), L2-normalized;
+rotated with the seeded randomized Hadamard transform to P=1024 and
+int8-quantized on the device; 256 queries = corpus rows + N(0, 0.05^2)
+noise, normalized.  One step = one query (batch 1): rotate, scan 1M codes
+with fused top-100, exact f64 re-rank to top-10.  Inputs are resident in HBM
+before timing starts.
 
 Prints one JSON line.  `value` is batch-1 queries/s over the timed steps.
-The line also carries batch-256 throughput, recall@10 against the exact fp32
-flat scan, the scan kernel's roofline position (HIP events on the index's
-stream) and the CPU baseline (the kernel.wat lane-order fp32 flat scan plus
-topK on one core, timed on this host).
+The line also carries, for the same workload, batch-256 throughput, recall@10
+against the exact fp32 flat scan, the scan kernel's roofline position (HIP
+events on the index's stream) and the CPU baseline (the kernel.wat
+lane-order fp32 flat scan plus topK on one core, timed on this host); and
+under "configs" the other workloads of the benchmark list, each with its own
+throughput, roofline, recall and CPU baseline:
+  c1  20,000 x 384 fp32 cosine, 100 queries: GPU top-10 ids vs the CPU scan
+  c2  1,000,000 x 768 fp32 flat dot / cosine / l2, batch 1 and 256
+  c4  4,000,000 x 1024 int4 and 1-bit (asym, Hamming), fetch 200 -> 10
+  c5  4,000,000 x 768 IVF int8, 4096 lists, 20 iterations, nprobe 32,
+      1024 queries, fetch 40 -> 10
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -29,6 +38,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+INT8_PEAK_POPS = 5.0
 METRIC = "queries/s at 1Mx768 int8 k=10 (batch 1 & 256); % HBM peak; recall@10"
 
 
@@ -37,6 +48,8 @@ def log(*a):
 
 
 def make_data(n, dim, nclusters, sigma, nq, qsigma, seed):
+    """Gaussian mixture (unit-norm centres + sigma N(0,1), rows normalized)
+    and noisy corpus rows as queries, generated on the device."""
     import torch
 
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -59,7 +72,6 @@ def make_data(n, dim, nclusters, sigma, nq, qsigma, seed):
 def timed_search(idx, d_q, nq_total, batch, steps, warmup, fetch, k, torch):
     """Runs `steps` timed search calls of `batch` queries each (cycling through
     the query set) after `warmup` untimed ones; returns seconds."""
-    dim = d_q.shape[1]
     rows = torch.empty(batch, k, dtype=torch.int32, device="cuda")
     scores = torch.empty(batch, k, dtype=torch.float32, device="cuda")
     cnt = torch.empty(batch, dtype=torch.int32, device="cuda")
@@ -81,9 +93,23 @@ def timed_search(idx, d_q, nq_total, batch, steps, warmup, fetch, k, torch):
     return time.perf_counter() - t0
 
 
-def cpu_baseline(x_host, q_host, budget_s=12.0):
+def qps(idx, q, nq_total, batch, steps, warmup, fetch, k, torch):
+    return steps * batch / timed_search(idx, q, nq_total, batch, steps, warmup, fetch, k, torch)
+
+
+def kernel_timed_b1(idx, q, nq_total, steps, fetch, k, torch):
+    """Batch-1 q/s and the scan kernel's mean duration (HIP events on the
+    index's stream around each launch of the timed steps)."""
+    timed_search(idx, q, nq_total, 1, max(steps // 10, 5), 0, fetch, k, torch)  # warmup, untimed
+    idx.kernel_timing(True)
+    el = timed_search(idx, q, nq_total, 1, steps, 0, fetch, k, torch)
+    ms, launches = idx.kernel_timing(False)
+    return steps / el, ms / max(launches, 1) * 1e3
+
+
+def cpu_baseline(x_host, q_host, metric="cosine", budget_s=12.0, min_q=3):
     """kernel.wat-order fp32 flat scan + topK (reference semantics) on one
-    core, over as many queries as fit the time budget (>= 4)."""
+    core, over as many queries as fit the time budget (at least min_q)."""
     from oracle import oracle as o
 
     cpus = None
@@ -96,10 +122,10 @@ def cpu_baseline(x_host, q_host, budget_s=12.0):
     t0 = time.perf_counter()
     try:
         while done < q_host.shape[0]:
-            s = o.wasm_scan(x_host, q_host[done])
+            s = o.wasm_scan(x_host, q_host[done], metric)
             o.topk_ref(s, 10)
             done += 1
-            if done >= 4 and time.perf_counter() - t0 > budget_s:
+            if done >= min_q and time.perf_counter() - t0 > budget_s:
                 break
     finally:
         if cpus:
@@ -108,6 +134,283 @@ def cpu_baseline(x_host, q_host, budget_s=12.0):
     return done / el, done, el
 
 
+def cpu_entry(x_host, q_host, metric, budget_s, what):
+    cqps, cn, cel = cpu_baseline(x_host, q_host, metric, budget_s)
+    n, dim = x_host.shape
+    return {"value": round(cqps, 3), "unit": "queries/s", "cores": 1, "kind": "port",
+            "sample": f"{cn} queries x {n:,} x {dim} fp32 {metric} flat scan in kernel.wat lane order + topK "
+                      f"k=10 ({what}), {cel:.1f} s on one core of {platform.processor() or 'host'} "
+                      f"({os.cpu_count()} logical CPUs visible)"}
+
+
+def hbm_roof(bytes_per_launch, kernel_us):
+    a = bytes_per_launch / (kernel_us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(a, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(a / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": int(bytes_per_launch),
+            "kernel_avg_us": round(kernel_us, 2)}
+
+
+def recall_vs_flat(ctx, x, q, rows_got, k, torch):
+    """recall@k of rows_got against the exact fp32 flat scan (whose batches
+    equal single queries)."""
+    from browservec_amd import FlatIndex
+
+    flat = FlatIndex(ctx, x.shape[1], "cosine")
+    flat.append_device(x.data_ptr(), x.shape[0])
+    nq = q.shape[0]
+    d_rows = torch.empty(nq, k, dtype=torch.int32, device="cuda")
+    d_sc = torch.empty(nq, k, dtype=torch.float32, device="cuda")
+    d_n = torch.empty(nq, dtype=torch.int32, device="cuda")
+    for s0 in range(0, nq, 256):
+        m = min(256, nq - s0)
+        flat.search_device(q[s0:s0 + m].data_ptr(), m, 0, k, d_rows[s0:].data_ptr(), d_sc[s0:].data_ptr(),
+                           d_n[s0:].data_ptr())
+    flat.sync()
+    truth = d_rows.cpu().numpy()
+    flat.destroy()
+    return float(np.mean([len(set(rows_got[i].tolist()) & set(truth[i].tolist())) / k for i in range(nq)]))
+
+
+def device_rows(idx, q, fetch, k, torch, chunk=256):
+    nq = q.shape[0]
+    d_rows = torch.empty(nq, k, dtype=torch.int32, device="cuda")
+    d_sc = torch.empty(nq, k, dtype=torch.float32, device="cuda")
+    d_n = torch.empty(nq, dtype=torch.int32, device="cuda")
+    for s0 in range(0, nq, chunk):
+        m = min(chunk, nq - s0)
+        idx.search_device(q[s0:s0 + m].data_ptr(), m, fetch, k, d_rows[s0:].data_ptr(), d_sc[s0:].data_ptr(),
+                          d_n[s0:].data_ptr())
+    idx.sync()
+    return d_rows.cpu().numpy()
+
+
+def free(torch):
+    import gc
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+# ------------------------------------------------------------------ configs --
+def bench_c1(ctx, torch):
+    """20,000 x 384 fp32 cosine, 100 queries: the GPU's top-10 ids against the
+    CPU baseline's (the kernel.wat lane-order scan + topK), all queries."""
+    from browservec_amd import FlatIndex
+    from oracle import oracle as o
+
+    n, dim, nq = 20_000, 384, 100
+    rng = np.random.default_rng(0xC1)
+    x = rng.standard_normal((n, dim)).astype(np.float32)
+    o.normalize_rows_store(x)
+    q = rng.standard_normal((nq, dim)).astype(np.float32)
+    o.normalize_rows_store(q)
+    idx = FlatIndex(ctx, dim, "cosine")
+    idx.append(x, n)
+    dq = torch.from_numpy(q).cuda()
+    b1 = qps(idx, dq, nq, 1, 200, 20, 0, 10, torch)
+    gpu = idx.query_batch(q, nq, 10)
+    t0 = time.perf_counter()
+    same = near = 0
+    for i in range(nq):
+        s = o.wasm_scan(x, q[i])
+        cpu_rows, _ = o.topk_ref(s, 10)
+        g = [h.row for h in gpu[i]]
+        if set(g) == set(cpu_rows.tolist()):
+            same += 1
+        else:  # a near-tie at the cut: the differing rows score within 1e-5 of the 10th
+            kth = float(np.sort(s)[-10])
+            if all(abs(float(s[r]) - kth) <= 1e-5 for r in set(g) ^ set(cpu_rows.tolist())):
+                near += 1
+    cpu_s = time.perf_counter() - t0
+    idx.destroy()
+    return {"workload": "20000x384 fp32 cosine flat, 100 queries, k=10",
+            "batch1_qps": round(b1, 1), "queries": nq, "top10_ids_equal_cpu": same,
+            "top10_ids_differ_only_at_near_ties": near,
+            "cpu_baseline": {"value": round(nq / cpu_s, 1), "unit": "queries/s", "cores": 1, "kind": "port",
+                             "sample": f"all {nq} queries, kernel.wat lane order + topK, {cpu_s:.2f} s"}}
+
+
+def bench_c2(ctx, torch, budget_s):
+    """1,000,000 x 768 fp32 flat scan, dot / cosine / l2, batch 1 and 256."""
+    from browservec_amd import FlatIndex
+
+    n, dim, nq, k = 1_000_000, 768, 256, 10
+    g = torch.Generator(device="cuda").manual_seed(0xB5EC0002)
+    x = torch.randn(n, dim, generator=g, device="cuda")
+    q = torch.randn(nq, dim, generator=g, device="cuda")
+    res = {}
+    cpu = {}
+    xh = None
+    for metric in ("dot", "cosine", "l2"):
+        if metric == "cosine":
+            xm, qm = (x / x.norm(dim=1, keepdim=True)).contiguous(), (q / q.norm(dim=1, keepdim=True)).contiguous()
+        else:
+            xm, qm = x, q
+        idx = FlatIndex(ctx, dim, metric)
+        idx.append_device(xm.data_ptr(), n)
+        b1, kus = kernel_timed_b1(idx, qm, nq, 200, 0, k, torch)
+        t256 = timed_search(idx, qm, nq, nq, 4, 1, 0, k, torch) / 4
+        flops = 2.0 * n * dim * nq
+        a = flops / t256 / 1e12
+        res[metric] = {"batch1_qps": round(b1, 1), "batch256_qps": round(nq / t256, 1),
+                       "roofline_b1": hbm_roof(n * dim * 4, kus),
+                       "roofline_b256": {"bound": "mfma", "achieved": round(a, 2), "peak": FP32_PEAK_TFLOPS,
+                                         "unit": "TFLOP/s", "frac": round(a / FP32_PEAK_TFLOPS, 4),
+                                         "algorithmic_flops_per_batch": flops,
+                                         "note": "whole batch pipeline: matrix-core prefilter + exact re-score"}}
+        idx.destroy()
+        if budget_s > 0:
+            xh = xm.cpu().numpy()
+            cpu[metric] = cpu_entry(xh, qm.cpu().numpy(), metric, budget_s, "batch 256 = 256 serial queries")
+            del xh
+        if metric == "cosine":
+            del xm, qm
+        free(torch)
+    del x, q
+    free(torch)
+    return {"workload": "1000000x768 fp32 N(0,1) flat scan (cosine: L2-normalized), 256 queries, k=10",
+            "metrics": res, "recall_at_10": 1.0,
+            "recall_note": "exact scan; batch rows and score bits equal single queries (tests)",
+            "cpu_baseline": cpu or None}
+
+
+def bench_c4(ctx, torch, budget_s):
+    """4,000,000 x 1024 int4 and 1-bit (asym and Hamming), fetch 200 -> 10."""
+    from browservec_amd import QuantIndex
+
+    n, dim, nq, fetch, k = 4_000_000, 1024, 256, 200, 10
+    x, q = make_data(n, dim, 1024, 0.1, nq, 0.05, 0xB5EC0004)
+    res = {}
+    for name, bits, scorer in (("int4", 4, "asym"), ("1bit_asym", 1, "asym"), ("1bit_hamming", 1, "hamming")):
+        idx = QuantIndex(ctx, dim, bits=bits, scorer=scorer)
+        t0 = time.perf_counter()
+        idx.append_device(x.data_ptr(), n)
+        idx.sync()
+        enc_s = time.perf_counter() - t0
+        b1, kus = kernel_timed_b1(idx, q, nq, 300, fetch, k, torch)
+        b256 = qps(idx, q, nq, nq, 3, 1, fetch, k, torch)
+        rows_q = device_rows(idx, q, fetch, k, torch)
+        rb = dim * bits // 8
+        res[name] = {"batch1_qps": round(b1, 1), "batch256_qps": round(b256, 1),
+                     "roofline_b1": hbm_roof(n * (rb + 4) + fetch * dim * 4, kus),
+                     "encode_s": round(enc_s, 3), "rows_q": rows_q}
+        idx.destroy()
+        free(torch)
+    for key in res:
+        res[key]["recall_at_10"] = round(recall_vs_flat(ctx, x, q, res[key].pop("rows_q"), k, torch), 4)
+    cpu = None
+    if budget_s > 0:
+        cpu = cpu_entry(x.cpu().numpy(), q[:16].cpu().numpy(), "cosine", budget_s,
+                        "the reference has no CPU quantized path")
+    del x, q
+    free(torch)
+    return {"workload": "4000000x1024 from a 1024-cluster mixture (sigma 0.1); int4 (512 B/row) and 1-bit "
+                        "(128 B/row) codes; fetch 200 -> exact f64 re-rank -> top-10; 256 noisy-row queries",
+            "codecs": res, "cpu_baseline": cpu}
+
+
+def bench_c5(ctx, torch, budget_s):
+    """IVF int8, 4,000,000 x 768, 4096 lists, 20 iterations, nprobe 32, fetch 40 -> 10."""
+    from browservec_amd import IVFQuantIndex
+
+    n, dim, nq, fetch, k, nprobe = 4_000_000, 768, 1024, 40, 10, 32
+    x, q = make_data(n, dim, 4096, 0.15, nq, 0.05, 0xB5EC0005)
+    idx = IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 4096, "iters": 20, "nprobe": nprobe})
+    t0 = time.perf_counter()
+    idx.append_device(x.data_ptr(), n)
+    idx.sync()
+    enc_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    idx.build()
+    build_s = time.perf_counter() - t0
+    st = idx.stats()
+    b1, kus = kernel_timed_b1(idx, q, nq, 500, fetch, k, torch)
+    bq = qps(idx, q, nq, nq, 3, 1, fetch, k, torch)
+    # rows each query scans: the sizes of its 32 probed lists (pickProbes'
+    # scores from the device, list offsets from the build), averaged
+    _, off, _ = idx.export_ivf()
+    sizes = np.diff(off.astype(np.int64))
+    ps = idx.export_probe_scores(q.cpu().numpy())
+    top = np.argpartition(-ps, nprobe - 1, axis=1)[:, :nprobe]
+    scanned = float(sizes[top].sum(axis=1).mean())
+    rows_q = device_rows(idx, q, fetch, k, torch, chunk=nq)
+    recall = recall_vs_flat(ctx, x, q, rows_q, k, torch)
+    # the same queries probing every list: the IVF scan then equals the
+    # exhaustive quantized scan, so this recall isolates the loss of the lists
+    qh = q[:64].cpu().numpy()
+    rows_all = []
+    for s0 in range(0, 64, 16):
+        idx.set_nprobe(st["nlist"])
+        r, _, _ = idx.search(qh[s0:s0 + 16], fetch, k)
+        rows_all.append(r)
+    recall_all = recall_vs_flat(ctx, x, q[:64].contiguous(), np.concatenate(rows_all), k, torch)
+    idx.destroy()
+    cpu = None
+    if budget_s > 0:
+        cpu = cpu_entry(x.cpu().numpy(), q[:16].cpu().numpy(), "cosine", budget_s,
+                        "the reference has no CPU IVF path")
+    del x, q
+    free(torch)
+    list_bytes = scanned * (1024 + 4 + 4)  # codes, scale and the candidate row id
+    return {"workload": "4000000x768 from a 4096-cluster mixture (sigma 0.15), IVF int8: 4096 lists, 20 Lloyd "
+                        "iterations on the 16384-row sample, nprobe 32, fetch 40 -> exact re-rank -> top-10, "
+                        "1024 noisy-row queries",
+            "batch1_qps": round(b1, 1), "batch1024_qps": round(bq, 1),
+            "roofline_b1_list_scan": dict(hbm_roof(list_bytes + fetch * dim * 4, kus),
+                                          avg_scanned_rows=round(scanned, 1)),
+            "recall_at_10": round(recall, 4), "recall_at_10_all_lists_64q": round(recall_all, 4),
+            "build_s": round(build_s, 3), "build_ms_device": round(st["build_ms"], 1), "encode_s": round(enc_s, 3),
+            "nlist": st["nlist"], "nprobe": nprobe, "cpu_baseline": cpu}
+
+
+def stream_ceiling(torch, nbytes=1 << 30, reps=20):
+    """Read-only streaming kernel (libbv_bench.so) over nbytes: plain and
+    nontemporal 16-byte loads, grid-stride or contiguous chunks per
+    workgroup, GB/s from CUDA events on torch's stream.  Returns the best
+    figure and the sweep."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "browservec_amd", "lib", "libbv_bench.so"))
+    lib.bvb_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_uint64, ctypes.c_void_p,
+                                    ctypes.c_uint32, ctypes.c_void_p]
+    buf = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    sink = torch.empty(4096 * 256, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    sweep = {}
+    for nt in (0, 1):
+        for chunk, blocks in ((0, 2048), (16 << 10, 512), (64 << 10, 512), (64 << 10, 1024), (256 << 10, 512),
+                              (64 << 10, 256)):
+            lib.bvb_stream_read(buf.data_ptr(), nbytes, nt, chunk, sink.data_ptr(), blocks, stream)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                lib.bvb_stream_read(buf.data_ptr(), nbytes, nt, chunk, sink.data_ptr(), blocks, stream)
+            e1.record()
+            torch.cuda.synchronize()
+            name = f"{'nontemporal' if nt else 'plain'} {'grid-stride' if not chunk else f'{chunk >> 10} KiB chunks'} x {blocks} wg"
+            sweep[name] = round(nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    del buf, sink
+    best = max(sweep, key=sweep.get)
+    return {"best_gbs": sweep[best], "best": best, "sweep": sweep}
+
+
+def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
+    """Device-to-device copy of nbytes (read + write), timed with CUDA events:
+    the streaming ceiling of the card the run is on, in GB/s."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst
+    return gbs
+
+
+# ------------------------------------------------------------------- main --
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,28 +424,17 @@ def main():
     ap.add_argument("--bits", type=int, default=8)
     ap.add_argument("--batch-steps", type=int, default=8, help="timed batch-256 steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--configs", default="c1,c2,c4,c5",
+                    help="extra workloads carried under 'configs' (comma list of c1,c2,c4,c5; '' for none)")
     ap.add_argument("--profile-only", action="store_true", help="build + a short timed loop (for rocprofv3)")
     ap.add_argument("--profile-batch", action="store_true",
                     help="build + timed batch-256 searches on the matrix-core path (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--config", default="c3", choices=["c2", "c3", "c4", "c5"],
-                    help="c3 (default): 1Mx768 int8 fetch 100; c2: 1Mx768 fp32 flat dot/cos/l2; "
-                         "c4: 4Mx1024 int4 + 1-bit fetch 200; c5: 4Mx768 IVF int8, 4096 lists, nprobe 32")
+    ap.add_argument("--stream-ceiling", action="store_true", help="only time the read-only streaming kernel")
+    ap.add_argument("--config", default=None, choices=["c1", "c2", "c4", "c5"],
+                    help="run one extra workload alone and print its object (for rocprofv3)")
     args = ap.parse_args()
-    if args.config != "c3":
-        return other_config(args)
-
-    if args.copy_calibration:
-        import torch
-
-        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(10):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_bytes_per_launch": src.numel() * 4, "launches": 10}))
-        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU; the search path shards by rows across GPUs "
@@ -152,13 +444,33 @@ def main():
 
     import torch
 
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": src.numel() * 4, "launches": 10}))
+        return
+    if args.stream_ceiling:
+        print(json.dumps({"stream_read_gbs": stream_ceiling(torch), "bytes_per_launch": 1 << 30}))
+        return
+
     from browservec_amd import DeviceContext, FlatIndex, QuantIndex
+
+    ctx = DeviceContext(0)
+    info = ctx.info()
+    budget = 0.0 if args.no_cpu_baseline else 6.0
+    if args.config:
+        fn = {"c1": lambda: bench_c1(ctx, torch), "c2": lambda: bench_c2(ctx, torch, budget),
+              "c4": lambda: bench_c4(ctx, torch, budget), "c5": lambda: bench_c5(ctx, torch, budget)}[args.config]
+        print(json.dumps({args.config: fn(), "device": info["name"]}))
+        ctx.destroy()
+        return
 
     seed = 0xB5EC0001
     log("generating data", args.rows, args.dim)
     x, q = make_data(args.rows, args.dim, 1024, 0.1, args.queries, 0.05, seed)
-    ctx = DeviceContext(0)
-    info = ctx.info()
 
     log("building int8 index")
     t0 = time.perf_counter()
@@ -227,18 +539,35 @@ def main():
     recall = float(np.mean([len(set(rows_q[i].tolist()) & set(truth[i].tolist())) / args.k
                             for i in range(args.queries)]))
     flat.destroy()
+    idx.destroy()
 
     # ---- CPU baseline -------------------------------------------------------------
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
         xh = x.cpu().numpy()
-        cqps, cn, cel = cpu_baseline(xh, qh)
+        cqps, cn, cel = cpu_baseline(xh, qh, "cosine", 12.0, 4)
         cpu = {"value": round(cqps, 3), "unit": "queries/s", "cores": 1, "kind": "port",
                "sample": f"{cn} queries x {args.rows:,} x {args.dim} fp32 cosine flat scan in kernel.wat lane "
                          f"order + topK k=10, {cel:.1f} s on one core of {platform.processor() or 'host'} "
                          f"({os.cpu_count()} logical CPUs visible)"}
         del xh
+    del x, q
+    free(torch)
+
+    configs = {}
+    for name in [c for c in args.configs.split(",") if c]:
+        log("config", name)
+        if name == "c1":
+            configs["c1_fp32_cosine_20kx384"] = bench_c1(ctx, torch)
+        elif name == "c2":
+            configs["c2_fp32_flat_1Mx768"] = bench_c2(ctx, torch, budget)
+        elif name == "c4":
+            configs["c4_int4_1bit_4Mx1024"] = bench_c4(ctx, torch, budget)
+        elif name == "c5":
+            configs["c5_ivf_int8_4Mx768"] = bench_c5(ctx, torch, budget)
+    log("streaming ceiling")
+    ceiling = stream_ceiling(torch)
 
     algo_bytes_q = scan_bytes
     out = {
@@ -269,8 +598,10 @@ def main():
         # the batch's dense int8 work (three query levels), over the whole
         # batch pipeline time (levels, sample pass, full pass, selects, re-rank)
         "batch256_int8_mfma": {"pops": round(2.0 * args.rows * nb * 3 * P * qps_b256 / nb / 1e15, 3),
-                               "peak": 5.0, "unit": "POP/s",
-                               "frac": round(2.0 * args.rows * nb * 3 * P * qps_b256 / nb / 1e15 / 5.0, 4)},
+                               "peak": INT8_PEAK_POPS, "unit": "POP/s",
+                               "frac": round(2.0 * args.rows * nb * 3 * P * qps_b256 / nb / 1e15 / INT8_PEAK_POPS, 4),
+                               "single_level_equivalent_frac":
+                                   round(2.0 * args.rows * nb * P * qps_b256 / nb / 1e15 / INT8_PEAK_POPS, 4)},
         "recall_at_10": round(recall, 4),
         "end_to_end_hbm_frac_b1": round(algo_bytes_q * qps_b1 / (HBM_PEAK_GBS * 1e9), 4),
         "latency_ms_sync_p50": round(lat_p50, 4),
@@ -278,156 +609,9 @@ def main():
         "build_s": round(build_s, 3),
         "device": info["name"],
         "hbm_copy_gbs": round(copy_bandwidth(torch), 1),  # measured 1 GiB device copy, read + write
+        "stream_read_gbs": ceiling,
+        "configs": configs,
     }
-    print(json.dumps(out))
-    idx.destroy()
-    ctx.destroy()
-
-
-def copy_bandwidth(torch, nbytes=1 << 30, reps=10):
-    """Device-to-device copy of nbytes (read + write), timed with CUDA events:
-    the streaming ceiling of the card the run is on, in GB/s."""
-    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
-    dst = torch.empty_like(src)
-    dst.copy_(src)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    e1.record()
-    torch.cuda.synchronize()
-    gbs = 2 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
-    del src, dst
-    return gbs
-
-
-def time_batches(idx, q, nq_total, batch, steps, warmup, fetch, k, torch):
-    el = timed_search(idx, q, nq_total, batch, steps, warmup, fetch, k, torch)
-    return steps * batch / el
-
-
-def recall_vs_flat(ctx, x, q, rows_got, k, torch):
-    from browservec_amd import FlatIndex
-
-    flat = FlatIndex(ctx, x.shape[1], "cosine")
-    flat.append_device(x.data_ptr(), x.shape[0])
-    nq = q.shape[0]
-    d_rows = torch.empty(nq, k, dtype=torch.int32, device="cuda")
-    d_sc = torch.empty(nq, k, dtype=torch.float32, device="cuda")
-    d_n = torch.empty(nq, dtype=torch.int32, device="cuda")
-    for s0 in range(0, nq, 64):
-        m = min(64, nq - s0)
-        flat.search_device(q[s0:s0 + m].data_ptr(), m, 0, k, d_rows[s0:].data_ptr(), d_sc[s0:].data_ptr(),
-                           d_n[s0:].data_ptr())
-    flat.sync()
-    truth = d_rows.cpu().numpy()
-    flat.destroy()
-    return float(np.mean([len(set(rows_got[i].tolist()) & set(truth[i].tolist())) / k for i in range(nq)]))
-
-
-def other_config(args):
-    """The other shapes of the reference's benchmark list, one JSON line each."""
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU", "n_gpus": args.gpus}))
-        sys.exit(2)
-    import torch
-
-    from browservec_amd import DeviceContext, FlatIndex, IVFQuantIndex, QuantIndex
-
-    ctx = DeviceContext(0)
-    info = ctx.info()
-    k = 10
-    out = {"unit": "queries/s", "n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-           "device": info["name"]}
-    if args.config == "c2":
-        n, dim, nq = 1_000_000, 768, 256
-        g = torch.Generator(device="cuda").manual_seed(0xB5EC0002)
-        x = torch.randn(n, dim, generator=g, device="cuda")
-        q = torch.randn(nq, dim, generator=g, device="cuda")
-        res = {}
-        for metric in ("dot", "cosine", "l2"):
-            xm, qm = (x / x.norm(dim=1, keepdim=True), q / q.norm(dim=1, keepdim=True)) if metric == "cosine" else (x, q)
-            xm, qm = xm.contiguous(), qm.contiguous()
-            idx = FlatIndex(ctx, dim, metric)
-            idx.append_device(xm.data_ptr(), n)
-            time_batches(idx, qm, nq, 1, 20, 0, 0, k, torch)  # warmup, outside the kernel timing
-            idx.kernel_timing(True)
-            b1 = time_batches(idx, qm, nq, 1, 200, 0, 0, k, torch)
-            ms, launches = idx.kernel_timing(False)
-            b256 = time_batches(idx, qm, nq, nq, 4, 1, 0, k, torch)
-            kus = ms / max(launches, 1) * 1e3
-            res[metric] = {"batch1_qps": round(b1, 1), "batch256_qps": round(b256, 1), "kernel_avg_us": round(kus, 1),
-                           "hbm_frac": round(n * dim * 4 / (kus * 1e-6) / 8e12, 4)}
-            idx.destroy()
-        out.update({"metric": "queries/s at 1Mx768 fp32 flat, k=10 (batch 1 & 256)", "value": res["cosine"]["batch1_qps"],
-                    "dtype": "f32", "data": "synthetic N(0,1) (cosine: L2-normalized) generated on device",
-                    "config": {"workload": "1000000x768 fp32 flat scan + top-10", "metrics": res}})
-    elif args.config == "c4":
-        n, dim, nq, fetch = 4_000_000, 1024, 256, 200
-        x, q = make_data(n, dim, 1024, 0.1, nq, 0.05, 0xB5EC0004)
-        res = {}
-        for name, bits, scorer in (("int4", 4, "asym"), ("1bit_asym", 1, "asym"), ("1bit_hamming", 1, "hamming")):
-            idx = QuantIndex(ctx, dim, bits=bits, scorer=scorer)
-            t0 = time.perf_counter()
-            idx.append_device(x.data_ptr(), n)
-            enc_s = time.perf_counter() - t0
-            time_batches(idx, q, nq, 1, 20, 0, fetch, k, torch)  # warmup, outside the kernel timing
-            idx.kernel_timing(True)
-            b1 = time_batches(idx, q, nq, 1, 300, 0, fetch, k, torch)
-            ms, launches = idx.kernel_timing(False)
-            b256 = time_batches(idx, q, nq, nq, 4, 1, fetch, k, torch)
-            rows_q, _, _ = idx.search(q.cpu().numpy(), fetch, k)
-            kus = ms / max(launches, 1) * 1e3
-            rb = dim * bits // 8
-            algo = n * (rb + 4) + fetch * dim * 4
-            res[name] = {
-                "batch1_qps": round(b1, 1), "batch256_qps": round(b256, 1), "kernel_avg_us": round(kus, 1),
-                "algorithmic_bytes_per_query": algo, "hbm_frac": round(algo / (kus * 1e-6) / 8e12, 4),
-                "encode_s": round(enc_s, 3), "rows_q": rows_q}
-            idx.destroy()
-        for key in res:
-            res[key]["recall_at_10"] = round(recall_vs_flat(ctx, x, q, res[key].pop("rows_q"), k, torch), 4)
-        out.update({"metric": "queries/s at 4Mx1024 int4 and 1-bit, fetch 200 -> exact re-rank -> k=10",
-                    "value": res["int4"]["batch1_qps"], "dtype": "int4/1-bit",
-                    "data": "synthetic: seeded 1024-cluster Gaussian mixture (sigma 0.1) generated on device",
-                    "config": {"workload": "4000000x1024 int4 / 1-bit asym scan + exact re-rank", "codecs": res}})
-    else:  # c5
-        n, dim, nq, fetch, nprobe = 4_000_000, 768, 1024, 40, 32
-        x, q = make_data(n, dim, 4096, 0.15, nq, 0.05, 0xB5EC0005)
-        ivf = {"nlist": 4096, "iters": 20, "nprobe": nprobe}
-        idx = IVFQuantIndex(ctx, dim, bits=8, ivf=ivf)
-        t0 = time.perf_counter()
-        idx.append_device(x.data_ptr(), n)
-        enc_s = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        idx.build()
-        build_s = time.perf_counter() - t0
-        st = idx.stats()
-        b1 = time_batches(idx, q, nq, 1, 500, 20, fetch, k, torch)
-        bq = time_batches(idx, q, nq, nq, 2, 1, fetch, k, torch)
-        qh = q.cpu().numpy()
-        rows_q, _, _ = idx.search(qh, fetch, k)
-        recall = recall_vs_flat(ctx, x, q, rows_q, k, torch)
-        # the same queries probing every list: the IVF scan then equals the
-        # exhaustive quantized scan, so this recall isolates the list loss
-        rows_all = []
-        for s0 in range(0, 64, 16):
-            idx.set_nprobe(st["nlist"])
-            r, _, _ = idx.search(qh[s0:s0 + 16], fetch, k)
-            rows_all.append(r)
-        recall_all = recall_vs_flat(ctx, x, q[:64].contiguous(), np.concatenate(rows_all), k, torch)
-        avg_list = n / st["nlist"]
-        out.update({"metric": "queries/s at 4Mx768 IVF int8 (4096 lists, nprobe 32), fetch 40 -> exact re-rank -> k=10",
-                    "value": round(b1, 1), "dtype": "int8",
-                    "data": "synthetic: seeded 4096-cluster Gaussian mixture (sigma 0.15) generated on device",
-                    "config": {"workload": "4000000x768 IVF int8, 20 Lloyd iterations on a 16384-row sample",
-                               "batch1_qps": round(b1, 1), "batch1024_qps": round(bq, 1),
-                               "recall_at_10": round(recall, 4),
-                               "recall_at_10_all_lists_64q": round(recall_all, 4), "build_s": round(build_s, 3),
-                               "build_ms_device": round(st["build_ms"], 1), "encode_s": round(enc_s, 3),
-                               "nlist": st["nlist"], "nprobe": nprobe,
-                               "avg_scanned_rows_per_query": round(avg_list * nprobe)}})
-        idx.destroy()
     print(json.dumps(out))
     ctx.destroy()
 

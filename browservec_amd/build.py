@@ -91,6 +91,23 @@ def _stale(src: str, obj: str) -> bool:
     return any(os.path.getmtime(d) > t for d in deps if os.path.exists(d))
 
 
+BENCH_SRC = "bench_stream.hip"
+BENCH_LIB = os.path.join(LIBDIR, "libbv_bench.so")
+
+
+def build_bench(verbose: bool = True) -> str:
+    """libbv_bench.so: the streaming-read ceiling kernel bench.py loads (not
+    part of the search library)."""
+    obj = os.path.join(LIBDIR, "obj", BENCH_SRC + ".o")
+    _compile(BENCH_SRC, obj)
+    tmp = BENCH_LIB + ".tmp"
+    subprocess.run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp, obj], check=True)
+    os.replace(tmp, BENCH_LIB)
+    if verbose:
+        print(f"built {BENCH_LIB}")
+    return BENCH_LIB
+
+
 def build(verbose: bool = True, incremental: bool = False) -> str:
     """Compiles every source (incremental=True: only those older than their
     inputs) and links the library and the Node addon."""
@@ -109,6 +126,8 @@ def build(verbose: bool = True, incremental: bool = False) -> str:
     if verbose:
         print(f"built {LIB}")
     build_napi(verbose)
+    if not incremental or _stale(BENCH_SRC, os.path.join(objdir, BENCH_SRC + ".o")):
+        build_bench(verbose)
     return LIB
 
 

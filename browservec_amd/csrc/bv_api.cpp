@@ -1754,7 +1754,8 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     HIPX(idx->dev, idx->dense.ensure(idx->rows * 4, 0, idx->stream), "scratch");
     const void *qscan = nullptr;
     uint64_t qstride = 0;
-    int rc = prepare_queries(idx, idx->qin.as<float>(), 1, &qscan, &qstride);
+    const bool in_kernel = idx->quant && scan_prep_supported(idx->codec, idx->units, idx->P);
+    int rc = in_kernel ? BV_OK : prepare_queries(idx, idx->qin.as<float>(), 1, &qscan, &qstride);
     if (rc) return rc;
     const uint32_t grid = grid_for(idx, idx->rows);
     const uint32_t *d_mask = nullptr;
@@ -1772,8 +1773,15 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     a.padded_dim = idx->P;
     a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A) ? idx->scales.as<float>() : nullptr;
     a.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
-    a.q = qscan;
-    a.q_stride = qstride;
+    if (in_kernel) {  // the scan rotates and transforms the fp32 query itself
+        a.qraw = idx->qin.as<float>();
+        a.qdim = idx->dim;
+        a.signs = idx->signs.as<float>();
+        a.rounds = idx->d.rounds;
+    } else {
+        a.q = qscan;
+        a.q_stride = qstride;
+    }
     a.mask = d_mask;
     a.mask_bits = mask_words * 32;
     a.n = idx->rows;

@@ -290,6 +290,99 @@ template <int U, int LPR> __device__ __forceinline__ bool xrep(int lane) {
     return (lane & ((1 << Lg<U, LPR>::low) - 1)) == 0;
 }
 
+// The value of lane ^ M (M = 1 .. 32) by DPP or a row / half swap, without
+// the LDS crossbar.  xor 4 within a 16-lane row: row_shl:4 for lanes with
+// bit 2 clear, row_shr:4 for the others (no lane reads outside its row).
+constexpr int DPP_ROW_SHL4 = 0x104;
+constexpr int DPP_ROW_SHR4 = 0x114;
+// Both moves of a pair run with every lane active, and one of the two
+// results is picked with integer masks: a select the compiler turned into a
+// branch would run each move with half the lanes disabled, and a move that
+// reads a disabled lane gets zero.
+__device__ __forceinline__ int pick_bits(int lo_val, int hi_val, bool hi) {
+    const int m = -(int)hi;  // all ones when hi
+    return lo_val ^ ((lo_val ^ hi_val) & m);
+}
+template <int M> __device__ __forceinline__ float lane_xor(float x, int lane) {
+    if constexpr (M == 1) return dpp<DPP_XOR1>(x);
+    else if constexpr (M == 2) return dpp<DPP_XOR2>(x);
+    else if constexpr (M == 4) {
+        const int up = as_i(dpp<DPP_ROW_SHL4>(x)), down = as_i(dpp<DPP_ROW_SHR4>(x));
+        return from_i<float>(pick_bits(up, down, (lane & 4) != 0));
+    } else if constexpr (M == 8) return dpp<DPP_ROR8>(x);
+    else {
+        // the swap returns two copies: lanes of the lower row / half find
+        // their partner in the second, the others in the first
+        auto r = (M == 16) ? __builtin_amdgcn_permlane16_swap(as_i(x), as_i(x), false, false)
+                           : __builtin_amdgcn_permlane32_swap(as_i(x), as_i(x), false, false);
+        return from_i<float>(pick_bits(r[1], r[0], (lane & M) != 0));
+    }
+}
+
+// One radix-2 FWHT stage across lanes (partner lane ^ M): the lane with bit
+// M clear holds the lower element u and keeps u + w, the other keeps u - w,
+// the reference's butterfly (src/quant/rotator.ts:24-36).
+template <int M, int E> __device__ __forceinline__ void fwht_xlane(float (&x)[E], int lane) {
+#pragma clang fp contract(off)
+    const bool hi = (lane & M) != 0;
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+        const float y = lane_xor<M>(x[t], lane);
+        x[t] = hi ? (y - x[t]) : (x[t] + y);
+    }
+}
+template <int E> __device__ __forceinline__ void fwht_xlane64(float (&x)[E], int lane) {
+    fwht_xlane<1>(x, lane);
+    fwht_xlane<2>(x, lane);
+    fwht_xlane<4>(x, lane);
+    fwht_xlane<8>(x, lane);
+    fwht_xlane<16>(x, lane);
+    fwht_xlane<32>(x, lane);
+}
+
+// Wave-wide f64 maximum (fmax: a NaN operand never wins) and i32 sum, in
+// every lane, through DPP / swaps on the 32-bit halves.
+__device__ __forceinline__ double wave_fmax_f64(double v) {
+#define BV_FMAX_STEP(GET)                                                        \
+    {                                                                            \
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);                      \
+        const uint32_t lo = GET((uint32_t)b), hi = GET((uint32_t)(b >> 32));     \
+        v = fmax(v, __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo));      \
+    }
+#define BV_DPP_GET(C) [](uint32_t w) { return dpp<C>(w); }
+    BV_FMAX_STEP(BV_DPP_GET(DPP_XOR1))
+    BV_FMAX_STEP(BV_DPP_GET(DPP_XOR2))
+    BV_FMAX_STEP(BV_DPP_GET(DPP_HALF_MIRROR))
+    BV_FMAX_STEP(BV_DPP_GET(DPP_MIRROR))
+#undef BV_DPP_GET
+#undef BV_FMAX_STEP
+    {
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        auto l = __builtin_amdgcn_permlane16_swap((int)(uint32_t)b, (int)(uint32_t)b, false, false);
+        auto h = __builtin_amdgcn_permlane16_swap((int)(uint32_t)(b >> 32), (int)(uint32_t)(b >> 32), false, false);
+        const double x = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[0] << 32) | (uint32_t)l[0]);
+        const double y = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[1] << 32) | (uint32_t)l[1]);
+        v = fmax(x, y);
+    }
+    {
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        auto l = __builtin_amdgcn_permlane32_swap((int)(uint32_t)b, (int)(uint32_t)b, false, false);
+        auto h = __builtin_amdgcn_permlane32_swap((int)(uint32_t)(b >> 32), (int)(uint32_t)(b >> 32), false, false);
+        const double x = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[0] << 32) | (uint32_t)l[0]);
+        const double y = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[1] << 32) | (uint32_t)l[1]);
+        v = fmax(x, y);
+    }
+    return v;
+}
+__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
+    v = plain_step<0>(v);
+    v = plain_step<1>(v);
+    v = plain_step<2>(v);
+    v = plain_step<3>(v);
+    v = plain_step<4>(v);
+    return plain_step<5>(v);
+}
+
 // ------------------------------------------------------- LDS top-k state --
 constexpr int SEL_BINS = 1024;  // histogram bins of the selection
 constexpr int SEL_TMP = 1024;   // gather buffer of the selection
@@ -498,14 +591,36 @@ __device__ __forceinline__ void wave_append(uint64_t *keys, uint32_t *cnt, uint3
     }
 }
 
+// The maximum over the wave, in every lane: DPP moves within 16-lane rows
+// (xor 1, xor 2, mirror within 8, mirror within 16) and row / half swaps,
+// each step pairing every lane with one whose range it has not seen.
+template <int CTRL> __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+template <bool HALF32> __device__ __forceinline__ uint64_t swap_max_u64(uint64_t v) {
+    const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+    auto a = HALF32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                    : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    auto b = HALF32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                    : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const uint64_t x = ((uint64_t)(uint32_t)b[0] << 32) | (uint32_t)a[0];
+    const uint64_t y = ((uint64_t)(uint32_t)b[1] << 32) | (uint32_t)a[1];
+    return x > y ? x : y;
+}
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), s) << 32) |
-                           (uint32_t)__shfl_xor((int)(uint32_t)v, s);
-        v = o > v ? o : v;
-    }
-    return v;
+    uint64_t o;
+    o = dpp_u64<DPP_XOR1>(v);
+    v = o > v ? o : v;
+    o = dpp_u64<DPP_XOR2>(v);
+    v = o > v ? o : v;
+    o = dpp_u64<DPP_HALF_MIRROR>(v);
+    v = o > v ? o : v;
+    o = dpp_u64<DPP_MIRROR>(v);
+    v = o > v ? o : v;
+    v = swap_max_u64<false>(v);
+    return swap_max_u64<true>(v);
 }
 
 // wave_append for (key, companion) pairs stored at the same index.
@@ -658,12 +773,16 @@ __device__ __forceinline__ void rotate_apply(RotIn<E> &in, uint32_t P, const flo
                 }
             }
         }
-        for (uint32_t m = 1; m < lanes_used; m <<= 1) {
-            const bool hi = (lane & m) != 0;
+        if (lanes_used == 64) {
+            fwht_xlane64<E>(x, lane);
+        } else {
+            for (uint32_t m = 1; m < lanes_used; m <<= 1) {
+                const bool hi = (lane & m) != 0;
 #pragma unroll
-            for (int t = 0; t < E; ++t) {
-                const float y = __shfl_xor(x[t], (int)m);
-                x[t] = hi ? (y - x[t]) : (x[t] + y);
+                for (int t = 0; t < E; ++t) {
+                    const float y = __shfl_xor(x[t], (int)m);
+                    x[t] = hi ? (y - x[t]) : (x[t] + y);
+                }
             }
         }
     }
@@ -829,8 +948,7 @@ __device__ void levels_wave(const float (&x)[E], uint32_t P, int codec, signed c
         double m = 0.0;
 #pragma unroll
         for (int t = 0; t < E; ++t) m = fmax(m, fabs(rd[t]));
-#pragma unroll
-        for (int sh = 1; sh < 64; sh <<= 1) m = fmax(m, __shfl_xor(m, sh));
+        m = wave_fmax_f64(m);
         const double sc = m > 0.0 ? m / 127.0 : 0.0;
         const double inv = sc > 0.0 ? 1.0 / sc : 0.0;
         int32_t sum = 0;
@@ -842,8 +960,7 @@ __device__ void levels_wave(const float (&x)[E], uint32_t P, int codec, signed c
             if (active) lv[l * P + e0 + t] = (signed char)(int)c;
             sum += (int)c;
         }
-#pragma unroll
-        for (int sh = 1; sh < 64; sh <<= 1) sum += __shfl_xor(sum, sh);
+        sum = wave_sum_i32(sum);
         sl[l] = sc;
         sums[l] = sum;
     }
@@ -1029,14 +1146,7 @@ __device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in
                 }
             }
         }
-        for (int m = 1; m < 64; m <<= 1) {
-            const bool hi = (lane & m) != 0;
-#pragma unroll
-            for (int t = 0; t < EP; ++t) {
-                const float y = __shfl_xor(x[t], m);
-                x[t] = hi ? (y - x[t]) : (x[t] + y);
-            }
-        }
+        fwht_xlane64<EP>(x, lane);
         // stages len = P/4 and P/2 pair elements of different waves
 #pragma unroll
         for (int t = 0; t < EP; ++t) xs[e0 + t] = x[t];
@@ -1072,8 +1182,7 @@ __device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in
             double m = 0.0;
 #pragma unroll
             for (int t = 0; t < EP; ++t) m = fmax(m, fabs(rd[t]));
-#pragma unroll
-            for (int sh = 1; sh < 64; sh <<= 1) m = fmax(m, __shfl_xor(m, sh));
+            m = wave_fmax_f64(m);
             if (lane == 0) redm[l * 4 + wave] = m;
             __syncthreads();
             m = fmax(fmax(redm[l * 4 + 0], redm[l * 4 + 1]), fmax(redm[l * 4 + 2], redm[l * 4 + 3]));
@@ -1088,8 +1197,7 @@ __device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in
                 lv[l * P + e0 + t] = (signed char)(int)c;
                 sum += (int)c;
             }
-#pragma unroll
-            for (int sh = 1; sh < 64; sh <<= 1) sum += __shfl_xor(sum, sh);
+            sum = wave_sum_i32(sum);
             if (lane == 0) reds[l * 4 + wave] = sum;
             sl[l] = sc;
         }
@@ -1276,7 +1384,7 @@ template <int C, int LPR, int UPL> struct ScanShape {
     static constexpr int RPS = U * G;                // rows per wave step
     static constexpr int GRAB_STEPS = 2;             // wave steps per work grab
     static constexpr int GRAB_ROWS = WAVES * RPS * GRAB_STEPS;
-    static constexpr uint32_t WGRAB = RPS * GRAB_STEPS;  // keys one grab can add to a wave's list
+    static constexpr uint32_t WGRAB = RPS * 2;       // keys one loop iteration (two steps) can add to a wave's list
 };
 
 // Streaming loads of codes and scales are nontemporal: every byte is read
@@ -1291,8 +1399,11 @@ __device__ __forceinline__ uint32_t load_stream(const uint32_t *p) { return __bu
 __device__ __forceinline__ float load_stream(const float *p) { return __builtin_nontemporal_load(p); }
 
 // One wave step: the U x UPL units each lane loads for RPS consecutive rows
-// (candidate slots when IDX), plus the scale and row id of the row whose
-// total this lane will hold after the reduction.
+// (candidate slots when IDX), plus the stored scale and row id of the row
+// whose total this lane will hold after the reduction.  The scale stays as
+// loaded until the step is scored: any arithmetic on it at load time would
+// make the wave wait for every load in flight (the load counter drains in
+// order), which leaves a single step in flight instead of two.
 template <int C, int LPR, int UPL> struct StepData {
     typename Codec<C>::Unit d[ScanShape<C, LPR, UPL>::U][UPL];
     float scale;
@@ -1321,7 +1432,7 @@ __device__ __forceinline__ void load_step(const ScanArgs &a, const ScanRegs<C, U
     const uint64_t myrow = base + (uint64_t)xrow<U, LPR>(lane) * G + slot;
     const uint64_t myrc = myrow < lim ? myrow : lim - 1;
     S.grow = IDX ? cand[myrc] : (uint32_t)myrc;
-    S.scale = a.scales ? load_stream(a.scales + S.grow) * a.scale_mul : 1.0f;
+    S.scale = a.scales ? load_stream(a.scales + S.grow) : 1.0f;
 }
 
 // Scores a loaded step: pushes keys >= tau to the wave's list and folds
@@ -1353,7 +1464,7 @@ __device__ __forceinline__ void compute_step(const ScanArgs &a, const ScanRegs<C
     uint64_t key = 0;
     if (xrep<U, LPR>(lane) && myrow < lim) {
         uint32_t ord;
-        const float sc = R.fin.score(tot, S.scale, ord);
+        const float sc = R.fin.score(tot, S.scale * a.scale_mul, ord);
         if (a.dense_out && blockIdx.y == 0) a.dense_out[myrow] = sc;
         bool pass = true;
         if (a.mask) pass = S.grow < a.mask_bits && ((a.mask[S.grow >> 5] >> (S.grow & 31)) & 1u);
@@ -1367,12 +1478,11 @@ __device__ __forceinline__ void compute_step(const ScanArgs &a, const ScanRegs<C
 }
 
 // Publishes the wave's running maximum to wmax[slot] when it grew.
-__device__ __forceinline__ void publish_wave_max(uint64_t *wslot, uint64_t lmax, uint64_t &published, int lane) {
-    const uint64_t w = wave_max_u64(lmax);
-    if (w > published) {
-        published = w;
-        if (lane == 0) __hip_atomic_store(wslot, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+// Publishes the wave's running maximum to wmax[slot] on every call, from
+// every lane (one line, one value): the scan loop issues the same memory
+// operations whatever the data, so that its waits stay exact.
+__device__ __forceinline__ void publish_wave_max(uint64_t *wslot, uint64_t lmax) {
+    __hip_atomic_store(wslot, wave_max_u64(lmax), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Cross-workgroup hand-off without cache-wide maintenance: data goes through
@@ -1514,7 +1624,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         n = a.cand_n[qi] < a.cand_stride ? a.cand_n[qi] : a.cand_stride;
     }
     uint64_t *wslot = a.wmax + ((uint64_t)qi * a.grid + blockIdx.x) * SH::WAVES + wave;
-    uint64_t lmax = 0, published = 0;
+    uint64_t lmax = 0;
 
     const uint32_t wcap = a.wcap;
     uint64_t *wk = (uint64_t *)scan_smem + (size_t)wave * a.wstride;  // list, then re-rank staging
@@ -1526,13 +1636,12 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
 
     // ---- a wave's stream of steps ----
     // Static part: grabs g = blockIdx.x + gi*grid for gi < sgrabs, each wave
-    // taking two steps of every grab (rows wofs.. and wofs + half..).
+    // taking GRAB_STEPS steps of every grab (rows wofs + s * wstep..).
     // Dynamic part: rows [d0, n) in chunks of DSTEPS consecutive steps, handed
     // out per wave from ng slices that each have their own counter; a wave
     // whose slice runs dry moves to the slice with the most chunks left.  The
     // dynamic part absorbs speed differences between XCDs.
-    static_assert(SH::GRAB_STEPS == 2, "two steps per grab");
-    const uint64_t wofs = (uint64_t)wave * SH::RPS, half = (uint64_t)SH::WAVES * SH::RPS;
+    const uint64_t wofs = (uint64_t)wave * SH::RPS, wstep = (uint64_t)SH::WAVES * SH::RPS;
     const uint64_t dch = (uint64_t)DSTEPS * SH::RPS;  // rows per dynamic chunk
     const uint64_t ngrabs = (n + SH::GRAB_ROWS - 1) / SH::GRAB_ROWS;
     const uint64_t sgrabs = ngrabs * STATIC_PCT / 100 / a.grid;  // full static grabs per workgroup
@@ -1582,9 +1691,9 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         if (!dynamic) {
             while (gi < sgrabs) {
                 const uint64_t r0 = ((uint64_t)blockIdx.x + gi * a.grid) * SH::GRAB_ROWS;
-                base = r0 + wofs + (sub ? half : 0);
+                base = r0 + wofs + (uint64_t)sub * wstep;
                 lim = r0 + SH::GRAB_ROWS < n ? r0 + SH::GRAB_ROWS : n;
-                if (++sub == 2) {
+                if (++sub == (uint32_t)SH::GRAB_STEPS) {
                     sub = 0;
                     ++gi;
                 }
@@ -1629,12 +1738,19 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     } else if constexpr (PS::ok) {
         if (prep && wave == 0) rotate_load<PS::E>(qsrc, a.qdim, a.padded_dim, a.signs, a.rounds, rin, lane);
     }
-    // the first two steps' code loads need no query: both go out before the
-    // query transform, so the memory system stays busy while it runs
-    bool ha = next_step(ab, al);
-    if (PIPE && ha) load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
+    // The first two steps' code loads need no query: both go out before the
+    // query transform, so the memory system stays busy while it runs.  Every
+    // step slot issues its loads whether or not the stream has a step for it
+    // (an idle slot loads the first row of the rows, a cached line, and is
+    // not scored), so every pass of the loop below issues the same memory
+    // operations and the load counter, which drains in order, lets a wave
+    // wait for exactly the step it scores while the other stays in flight.
+    // (A query with no rows issues no loads: the first row is not there.)
+    const bool any = n > 0;
+    bool ha = any && next_step(ab, al);
+    if (PIPE && any) load_step<C, LPR, UPL, IDX>(a, R, cand, ha ? ab : 0, ha ? al : 1, A, lane);
     bool hb = PIPE && ha && next_step(bb, bl);
-    if (PIPE && hb) load_step<C, LPR, UPL, IDX>(a, R, cand, bb, bl, B, lane);
+    if (PIPE && any) load_step<C, LPR, UPL, IDX>(a, R, cand, hb ? bb : 0, hb ? bl : 1, B, lane);
 
     const QT *qbase;
     if (prep) {
@@ -1655,21 +1771,32 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     }
     R.fin.load((const char *)qbase + (uint64_t)a.units * CD::QN * sizeof(QT), a.padded_dim);
     if (a.qraw) __syncthreads();  // the LDS holding it becomes the waves' lists
+    uint64_t gt = 0;      // what the previous pass read: the shared bound when it polled
+    bool polled = false;
     for (uint32_t pi = 0; ha; ++pi) {
-        // read the shared bound every TAU_POLL step pairs (waves staggered):
-        // it is one cache line that every wave of the grid would otherwise hammer
-        const bool poll = (pi + (uint32_t)wave) % TAU_POLL == 0;
-        uint64_t gt = 0;
-        if (poll) gt = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if constexpr (PIPE) {
             // steps alternate between A and B; the other buffer's loads are
             // in flight while one is scored
             compute_step<C, LPR, UPL>(a, R, A, ab, al, tau, wk, wc, lmax, lane);
-            ha = hb && next_step(ab, al);
-            if (ha) load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
+            const bool na = hb && next_step(ab, al);
+            load_step<C, LPR, UPL, IDX>(a, R, cand, na ? ab : 0, na ? al : 1, A, lane);
             if (hb) compute_step<C, LPR, UPL>(a, R, B, bb, bl, tau, wk, wc, lmax, lane);
-            hb = ha && next_step(bb, bl);
-            if (hb) load_step<C, LPR, UPL, IDX>(a, R, cand, bb, bl, B, lane);
+            if (polled) {  // the bound read in the previous pass, older than B's loads
+                const uint64_t ugt = uniform_u64(gt);
+                tau = ugt > tau ? ugt : tau;
+            }
+            // one store and one load per pass: the wave's maximum, and the
+            // shared bound every TAU_POLL passes (waves staggered; it is one
+            // line that every wave of the grid reads) or else the wave's own
+            // slot
+            publish_wave_max(wslot, lmax);
+            polled = (pi + (uint32_t)wave) % TAU_POLL == 0;
+            gt = __hip_atomic_load(polled ? (const uint64_t *)&qs->tau : (const uint64_t *)wslot, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            const bool nb = na && next_step(bb, bl);
+            load_step<C, LPR, UPL, IDX>(a, R, cand, nb ? bb : 0, nb ? bl : 1, B, lane);
+            ha = na;
+            hb = nb;
         } else {
             load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
             compute_step<C, LPR, UPL>(a, R, A, ab, al, tau, wk, wc, lmax, lane);
@@ -1680,11 +1807,9 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             } else {
                 ha = false;
             }
-        }
-        publish_wave_max(wslot, lmax, published, lane);
-        if (poll) {
-            const uint64_t ugt = uniform_u64(gt);
-            tau = ugt > tau ? ugt : tau;
+            publish_wave_max(wslot, lmax);
+            const uint64_t g = uniform_u64(__hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            tau = g > tau ? g : tau;
         }
         if (wc > trig) {
             wc = wave_filter(wk, wc, tau, lane);
