@@ -46,12 +46,12 @@ constexpr int NGROUP = 32;  // counter groups
 constexpr int CL = 32;      // u32 stride of one counter (128 bytes)
 struct QState {
     unsigned long long tau;  // published bound: keys below it cannot be in the top-kprime
-    uint32_t top;            // groups whose workgroups have all finished
+    uint32_t pad0[30];       // (every wave polls this line: the counters below live elsewhere)
+    uint32_t top;            // scanning workgroups that have finished
     uint32_t fin;            // finishers (final selection + threshold helper)
-    uint32_t pad[28];
-    uint32_t done[NGROUP * CL];  // finished scanning workgroups per group
+    uint32_t pad1[30];
     uint32_t cc[NGROUP * CL];    // keys flushed per group region
-    uint32_t dyn[NGROUP * CL];   // dynamic chunks taken per slice (may overshoot)
+    uint32_t dyn[NGROUP * CL];   // dynamic tickets taken per slice (may overshoot)
 };
 
 struct ScanArgs {

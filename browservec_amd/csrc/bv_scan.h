@@ -230,9 +230,12 @@ template <int B, class T> __device__ __forceinline__ T plain_step(T v) {
     }
 }
 
-// One transposing exchange on lane bit B (5, 4 or 3): the lane with bit B
-// clear keeps rows [0,h) and the lane with it set keeps rows [h,2h); each
-// adds its partner's copy of the kept rows.
+// One transposing exchange on lane bit B (0..5): the lane with bit B clear
+// keeps rows [0,h) and the lane with it set keeps rows [h,2h); each adds its
+// partner's copy of the kept rows.  The partner of bits 3..0 is a DPP lane
+// pattern that flips bit B (lane ^ 8, lane ^ 7 within 8, lane ^ 2, lane ^ 1):
+// any pairing that flips bit B and keeps the higher bits leaves the lanes
+// with bit B clear holding, between them, the whole group's sum.
 template <int B, int H, class T> __device__ __forceinline__ void xpose_step(T *v, int lane) {
 #pragma unroll
     for (int j = 0; j < H; ++j) {
@@ -241,10 +244,11 @@ template <int B, int H, class T> __device__ __forceinline__ void xpose_step(T *v
                               : __builtin_amdgcn_permlane16_swap(as_i(v[j]), as_i(v[j + H]), false, false);
             v[j] = from_i<T>(r[0]) + from_i<T>(r[1]);
         } else {
+            constexpr int CTRL = B == 3 ? DPP_ROR8 : B == 2 ? DPP_HALF_MIRROR : B == 1 ? DPP_XOR2 : DPP_XOR1;
             const bool hi = (lane >> B) & 1;
             const T send = hi ? v[j] : v[j + H];
             const T keep = hi ? v[j + H] : v[j];
-            v[j] = keep + dpp<DPP_ROR8>(send);
+            v[j] = keep + dpp<CTRL>(send);
         }
     }
 }
@@ -394,7 +398,7 @@ struct TopkLds {
     uint32_t hist[SEL_BINS];
     uint32_t red[16];           // cross-wave reduction slots
     uint32_t ovl[SCAN_WG];      // final selection: per-group flush counts, then their prefix
-    uint32_t cnt, cnt2, bstar, above, flag, last, grab;
+    uint32_t cnt, cnt2, bstar, above, flag, last, grab, over;
     uint64_t tau, gtau;
 };
 
@@ -1302,35 +1306,39 @@ __device__ uint64_t exact_key_wave(const float *src, const float *qs, uint32_t d
     return uniform_u64(key);
 }
 
-// Store.dotRow of sixteen rows at once, four lanes per row: lane 4c + m
-// sums the exact products of elements 4j + m of row c in order (an exact
-// f32 x f32 product added by fma rounds like the reference's `acc += x*y`),
-// and lane 4c combines the four as ((a0 + a1) + a2) + a3 and adds the tail
-// elements in order.  x: this lane's row; every lane of the wave calls it.
-// Returns the (score, row) key in lanes 4c.
-__device__ __forceinline__ uint64_t exact_key_lanes4(const float *x, const float *qs, uint32_t dim, uint32_t row,
-                                                     int lane) {
-    const uint32_t vec = dim & ~3u;
-    const int m = lane & 3;
-    double acc = 0.0;
-    uint32_t j = m;
-    for (; j + 28 < vec; j += 32) {
-        float xv[8], qv[8];
+// Store.dotRow (src/store/store.ts:114-129) of sixteen rows at once, four
+// lanes per row: lane 4c + m sums the exact products of elements 4j + m of
+// row c in order (an exact f32 x f32 product added by fma rounds like the
+// reference's `a_m += x*y` in f64), lane 4c combines the four as
+// ((a0 + a1) + a2) + a3 and adds the tail elements in order.  x: this lane's
+// row; every lane of the wave calls it; the key is valid in lanes 4c.
+// qd holds the query as doubles (LDS).  Each lane issues its row loads 64 at
+// a time ahead of the dependent FMA chain, so a row costs a few memory round
+// trips, not one per eight elements.
+template <int B>
+__device__ __forceinline__ void dot_chain(const float *x, const double *qd, uint32_t vec, uint32_t &j, double &acc) {
+    for (; j + 4 * (B - 1) < vec; j += 4 * B) {
+        float xv[B];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            xv[u] = x[j + 4 * u];
-            qv[u] = qs[j + 4 * u];
-        }
+        for (int u = 0; u < B; ++u) xv[u] = x[j + 4 * u];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc = fma((double)xv[u], (double)qv[u], acc);
+        for (int u = 0; u < B; ++u) acc = fma((double)xv[u], qd[j + 4 * u], acc);
     }
-    for (; j < vec; j += 4) acc = fma((double)x[j], (double)qs[j], acc);
+}
+__device__ __forceinline__ uint64_t exact_key_lanes4(const float *x, const double *qd, const float *q, uint32_t dim,
+                                                     uint32_t row, int lane) {
+    const uint32_t vec = dim & ~3u;
+    double acc = 0.0;
+    uint32_t j = (uint32_t)(lane & 3);
+    dot_chain<64>(x, qd, vec, j, acc);
+    dot_chain<16>(x, qd, vec, j, acc);
+    dot_chain<1>(x, qd, vec, j, acc);
     const double a1 = __shfl_down(acc, 1), a2 = __shfl_down(acc, 2), a3 = __shfl_down(acc, 3);
     double sum = acc + a1;
     sum = sum + a2;
     sum = sum + a3;
-    if (m == 0)
-        for (uint32_t i = vec; i < dim; ++i) sum = fma((double)x[i], (double)qs[i], sum);
+    if ((lane & 3) == 0)
+        for (uint32_t i = vec; i < dim; ++i) sum = fma((double)x[i], (double)q[i], sum);
     return make_key(ord_f32((float)sum), row);
 }
 
@@ -1377,7 +1385,10 @@ template <int C, int UPL> struct ScanRegs {
 // per-lane partial sums with the transposing butterfly.
 template <int C, int LPR, int UPL> struct ScanShape {
     static constexpr int U0 = UPL >= 4 ? 2 : (UPL >= 2 ? 4 : 8);
-    static constexpr int UMAX = LPR >= 64 ? 8 : LPR == 32 ? 4 : LPR == 16 ? 2 : 1;  // transposes on bits 5..3
+    // one transposing stage per halving of U (at most three), and at most 32
+    // rows per step so that a pass of two steps adds at most 64 keys to a
+    // wave's list (the list's slack beyond twice the fetch)
+    static constexpr int UMAX = LPR >= 16 ? 8 : LPR / 2;
     static constexpr int U = U0 < UMAX ? U0 : UMAX;  // row groups per lane per step
     static constexpr int G = 64 / LPR;               // rows per load instruction
     static constexpr int WAVES = SCAN_WG / 64;
@@ -1513,7 +1524,6 @@ __device__ void reset_query(const ScanArgs &a, uint32_t qi) {
     uint64_t *wm = a.wmax + (uint64_t)qi * a.grid * (SCAN_WG / 64);
     for (uint32_t i = threadIdx.x; i < a.grid * (SCAN_WG / 64); i += blockDim.x) wm[i] = 0;
     for (uint32_t r = threadIdx.x; r < (uint32_t)NGROUP; r += blockDim.x) {
-        qs->done[r * CL] = 0;
         qs->cc[r * CL] = 0;
         qs->dyn[r * CL] = 0;
     }
@@ -1522,10 +1532,6 @@ __device__ void reset_query(const ScanArgs &a, uint32_t qi) {
         qs->top = 0;
         qs->fin = 0;
     }
-}
-
-__device__ __forceinline__ uint32_t group_size(uint32_t grid, uint32_t ng, uint32_t r) {
-    return grid / ng + (r < grid % ng ? 1u : 0u);
 }
 
 // Background threshold: the kprime-th best of any kprime or more wave maxima
@@ -1571,7 +1577,7 @@ __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
             }
         }
         __syncthreads();
-        if (top >= ng) break;
+        if (top >= a.grid) break;
     }
 }
 
@@ -1637,28 +1643,39 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     // ---- a wave's stream of steps ----
     // Static part: grabs g = blockIdx.x + gi*grid for gi < sgrabs, each wave
     // taking GRAB_STEPS steps of every grab (rows wofs + s * wstep..).
-    // Dynamic part: rows [d0, n) in chunks of DSTEPS consecutive steps, handed
-    // out per wave from ng slices that each have their own counter; a wave
-    // whose slice runs dry moves to the slice with the most chunks left.  The
-    // dynamic part absorbs speed differences between XCDs.
+    // Dynamic part: the steps of rows [d0, n), cut into ng slices that each
+    // have their own ticket counter.  A slice hands out chunks of DSTEPS
+    // consecutive steps, then its last (steps % DSTEPS) steps one at a time.
+    // (Handing out more of a slice's end one step at a time evens out the
+    // waves' finish times but costs more than it gains: single scattered
+    // steps stream worse.)  A wave whose slice runs dry moves to the slice
+    // with the most tickets left.  The dynamic part absorbs speed differences between
+    // workgroups (older waves win memory arbitration) and XCDs.
     const uint64_t wofs = (uint64_t)wave * SH::RPS, wstep = (uint64_t)SH::WAVES * SH::RPS;
-    const uint64_t dch = (uint64_t)DSTEPS * SH::RPS;  // rows per dynamic chunk
     const uint64_t ngrabs = (n + SH::GRAB_ROWS - 1) / SH::GRAB_ROWS;
     const uint64_t sgrabs = ngrabs * STATIC_PCT / 100 / a.grid;  // full static grabs per workgroup
     uint64_t d0 = sgrabs * a.grid * SH::GRAB_ROWS;
     if (d0 > n) d0 = n;
-    const uint64_t nchunks = (n - d0 + dch - 1) / dch;
-    const uint64_t per = (nchunks + ng - 1) / ng;  // chunks per slice
-    auto slice_len = [&](uint32_t r) -> uint64_t {
+    const uint64_t nsd = (n - d0 + SH::RPS - 1) / SH::RPS;  // dynamic steps
+    const uint64_t per = (nsd + ng - 1) / ng;              // steps per slice
+    // a slice's step count, and its chunks of DSTEPS steps (the rest are
+    // single-step tickets)
+    auto slice_steps = [&](uint32_t r) -> uint64_t {
         const uint64_t lo = (uint64_t)r * per;
-        return lo >= nchunks ? 0 : (nchunks - lo < per ? nchunks - lo : per);
+        return lo >= nsd ? 0 : (nsd - lo < per ? nsd - lo : per);
+    };
+    auto big_chunks = [&](uint64_t ls) -> uint64_t { return ls / DSTEPS; };
+    auto slice_tickets = [&](uint32_t r) -> uint64_t {
+        const uint64_t ls = slice_steps(r), nb = big_chunks(ls);
+        return nb + (ls - nb * DSTEPS);
     };
     uint64_t gi = 0;
-    uint32_t sub = 0, ds = DSTEPS, slice = (blockIdx.x * SH::WAVES + wave) % ng, pend = 0;
+    uint32_t sub = 0, ds = 0, dlen = 0, slice = (blockIdx.x * SH::WAVES + wave) % ng, pend = 0;
     bool dynamic = false, has_pend = false;
     uint64_t c0 = 0, clim = 0;
-    // next dynamic chunk index, or ~0 when every slice is exhausted
-    auto take_chunk = [&]() -> uint64_t {
+    // takes the next dynamic ticket: its first row in c0 and end in clim;
+    // false when every slice is exhausted
+    auto take_chunk = [&]() -> bool {
         for (;;) {
             uint32_t t;
             if (has_pend) {
@@ -1669,21 +1686,27 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
                 if (lane == 0) v = atomicAdd(&qs->dyn[slice * CL], 1u);
                 t = __builtin_amdgcn_readfirstlane(v);
             }
-            if (t < slice_len(slice)) {
+            const uint64_t ls = slice_steps(slice), nb = big_chunks(ls);
+            if (t < nb + (ls - nb * DSTEPS)) {
                 if (lane == 0) pend = atomicAdd(&qs->dyn[slice * CL], 1u);  // next ticket in flight
                 has_pend = true;
-                return (uint64_t)slice * per + t;
+                const uint64_t st = t < nb ? (uint64_t)t * DSTEPS : nb * DSTEPS + (t - nb);
+                dlen = t < nb ? DSTEPS : 1;
+                c0 = d0 + ((uint64_t)slice * per + st) * SH::RPS;
+                const uint64_t e = c0 + (uint64_t)dlen * SH::RPS;
+                clim = e < n ? e : n;
+                return true;
             }
             // this slice is exhausted (its counter never drops): read every
             // slice's counter at once and move to the one with most left
             uint64_t rem = 0;
             if ((uint32_t)lane < ng) {
                 const uint32_t c = load_shared(&qs->dyn[lane * CL]);
-                const uint64_t L = slice_len(lane);
+                const uint64_t L = slice_tickets(lane);
                 rem = c < L ? L - c : 0;
             }
             const uint64_t best = wave_max_u64((rem << 32) | (uint32_t)lane);
-            if ((best >> 32) == 0) return ~0ull;
+            if ((best >> 32) == 0) return false;
             slice = (uint32_t)best;
         }
     };
@@ -1702,20 +1725,16 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             dynamic = true;
         }
         for (;;) {
-            if (ds < DSTEPS) {
+            if (ds < dlen) {
                 base = c0 + (uint64_t)ds * SH::RPS;
                 ++ds;
                 if (base < clim) {
                     lim = clim;
                     return true;
                 }
-                ds = DSTEPS;
+                ds = dlen;
             }
-            if (nchunks == 0) return false;
-            const uint64_t c = take_chunk();
-            if (c == ~0ull) return false;
-            c0 = d0 + c * dch;
-            clim = c0 + dch < n ? c0 + dch : n;
+            if (nsd == 0 || !take_chunk()) return false;
             ds = 0;
         }
     };
@@ -1823,73 +1842,92 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             }
         }
     }
-    // flush the keys at or above the freshest bound
-    {
-        const uint64_t gt = load_tau(qs);
-        tau = gt > tau ? gt : tau;
-        wc = wave_filter(wk, wc, tau, lane);
+    // Flush the keys at or above the wave's bound: the bound read by the last
+    // pass's poll, not a fresh read (one device round trip less at the end of
+    // the scan; the final selection filters by the freshest shared bound).
+    if constexpr (PIPE) {
+        if (polled) {
+            const uint64_t ugt = uniform_u64(gt);
+            tau = ugt > tau ? ugt : tau;
+        }
     }
+    wc = wave_filter(wk, wc, tau, lane);
     // Flushed entries are (scan key, exact key) pairs; with re-ranking on,
     // the wave scores its own candidates exactly here, while other waves of
-    // the grid are still scanning.
+    // the grid are still scanning.  The slot reservation is issued first and
+    // read only when the pairs are stored, so its round trip overlaps the
+    // re-rank's row loads.
     const uint32_t grp = blockIdx.x % ng;
     const uint64_t region = a.cand_cap / ng;  // pairs per group region
     if (wc) {
-        uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(&qs->cc[grp * CL], wc);
-        base = __builtin_amdgcn_readfirstlane(base);
-        uint64_t *ck = a.cand_keys + 2 * ((uint64_t)qi * a.cand_cap + grp * region + base);
+        uint32_t b0 = 0;
+        if (lane == 0) b0 = atomicAdd(&qs->cc[grp * CL], wc);
+        uint64_t *ck0 = a.cand_keys + 2 * ((uint64_t)qi * a.cand_cap + grp * region);
         if (a.rr_src) {
+            // the query as doubles in the wave's staging area behind its list
             const float *rq = a.rr_q + (uint64_t)qi * a.rr_q_stride;
+            double *qd = (double *)(wk + wcap);
+            const uint32_t vec = a.rr_dim & ~3u;
+            for (uint32_t i = (uint32_t)lane; i < vec; i += 64) qd[i] = (double)rq[i];
             for (uint32_t j0 = 0; j0 < wc; j0 += 16) {  // sixteen candidates per pass
                 const uint32_t j = j0 + (uint32_t)(lane >> 2);
                 const bool have = j < wc;
                 const uint64_t k = have ? wk[j] : 0ull;
                 const uint32_t row = have ? key_row(k) : 0u;  // absent candidates read row 0
-                const uint64_t ek = exact_key_lanes4(a.rr_src + (uint64_t)row * a.rr_dim, rq, a.rr_dim, row, lane);
+                const uint64_t ek = exact_key_lanes4(a.rr_src + (uint64_t)row * a.rr_dim, qd, rq, a.rr_dim, row, lane);
+                const uint32_t base = __builtin_amdgcn_readfirstlane(b0);
                 if (have && (lane & 3) == 0) {
-                    store_shared(&ck[2 * j], k);
-                    store_shared(&ck[2 * j + 1], ek);
+                    store_shared(&ck0[2 * (base + j)], k);
+                    store_shared(&ck0[2 * (base + j) + 1], ek);
                 }
             }
         } else {
+            const uint32_t base = __builtin_amdgcn_readfirstlane(b0);
             for (uint32_t j = lane; j < wc; j += 64) {
-                store_shared(&ck[2 * j], wk[j]);
-                store_shared(&ck[2 * j + 1], 0ull);
+                store_shared(&ck0[2 * (base + j)], wk[j]);
+                store_shared(&ck0[2 * (base + j) + 1], 0ull);
             }
         }
     }
     wait_stores_done();
     __syncthreads();
-    if (tid == 0) {
-        // two-level ticket: the workgroup completing its group bumps `top`;
-        // the one completing `top` runs the final selection
-        bool last = false;
-        if (atomicAdd(&qs->done[grp * CL], 1u) == group_size(a.grid, ng, grp) - 1)
-            last = atomicAdd(&qs->top, 1u) == ng - 1;
-        L.last = last;
-    }
+    // one ticket per workgroup: the last to finish runs the final selection
+    // (finishes are spread over the scan's last microseconds, so the single
+    // counter is not contended)
+    if (tid == 0) L.last = atomicAdd(&qs->top, 1u) == a.grid - 1;
     __syncthreads();
     if (!L.last) return;
 
     // ---- last scanning workgroup: select the best kprime of the flushes ----
+    // One round trip reads the bound, the per-group flush counts and the
+    // first SCAN_WG / ng pairs of every group region (groups rarely flush
+    // more); wave 0 turns the counts into their exclusive prefix.
+    const uint64_t *ckq = a.cand_keys + 2 * (uint64_t)qi * a.cand_cap;
+    const uint32_t spec = SCAN_WG / ng;
+    const uint32_t sg = tid % ng, ss = tid / ng;
+    const uint64_t sslot = 2 * ((uint64_t)sg * region + ss);
+    const uint64_t sv = load_shared(&ckq[sslot]), se = load_shared(&ckq[sslot + 1]);
     if (tid == 0) {
         L.cnt = 0;
-        L.tau = __hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        L.tau = load_shared(&qs->tau);
     }
-    if (tid < ng) L.ovl[tid] = __hip_atomic_load(&qs->cc[tid * CL], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (tid == 0) {
-        // exclusive prefix of the per-group counts in ovl[32..64]
-        uint32_t acc = 0;
-        for (uint32_t r = 0; r < ng; ++r) {
-            L.ovl[32 + r] = acc;
-            acc += L.ovl[r];
+    if (tid < 64) {
+        const uint32_t c = (uint32_t)tid < ng ? load_shared(&qs->cc[tid * CL]) : 0u;
+        uint32_t incl = c;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = __shfl_up(incl, d);
+            incl += lane >= d ? o : 0u;
         }
-        L.ovl[32 + ng] = acc;
+        const uint64_t over = __ballot(c > spec);
+        if ((uint32_t)tid < ng) {
+            L.ovl[tid] = c;
+            L.ovl[32 + tid] = incl - c;
+        }
+        if ((uint32_t)tid == ng - 1) L.ovl[32 + ng] = incl;
+        if (tid == 0) L.over = (uint32_t)over;
     }
     __syncthreads();
-    const uint64_t *ckq = a.cand_keys + 2 * (uint64_t)qi * a.cand_cap;
     const uint32_t total = L.ovl[32 + ng];
     constexpr uint32_t CHUNK = SCAN_CAP / 2;
     if (a.rr_src && total <= CHUNK) {
@@ -1897,24 +1935,20 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         // pairs at or above the bound; the fetch is the best kp scan keys,
         // found by rank counting; its exact keys are ranked for the output.
         const uint64_t th = L.tau;
-        for (uint32_t i0 = 0; i0 < total; i0 += 4 * SCAN_WG) {
-            uint64_t v[4], e[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t i = i0 + j * SCAN_WG + tid;
-                v[j] = 0;
-                e[j] = 0;
-                if (i < total) {
-                    uint32_t r = 0;
-                    while (r + 1 < ng && L.ovl[32 + r + 1] <= i) ++r;
-                    const uint64_t slot = 2 * (r * region + (i - L.ovl[32 + r]));
-                    v[j] = load_shared(&ckq[slot]);
-                    e[j] = load_shared(&ckq[slot + 1]);
+        const bool sok = ss < spec && ss < L.ovl[sg];  // (threads past ng * spec read no pair)
+        wave_append2(L.keys, L.keys + CHUNK, &L.cnt, CHUNK, sok && sv != 0 && sv >= th, sv, se, lane);
+        for (uint32_t over = L.over; over; over &= over - 1) {  // groups with more than spec pairs
+            const uint32_t r = (uint32_t)__builtin_ctz(over), c = L.ovl[r];
+            for (uint32_t i0 = spec; i0 < c; i0 += SCAN_WG) {
+                const uint32_t i = i0 + tid;
+                uint64_t v = 0, e = 0;
+                if (i < c) {
+                    const uint64_t slot = 2 * ((uint64_t)r * region + i);
+                    v = load_shared(&ckq[slot]);
+                    e = load_shared(&ckq[slot + 1]);
                 }
+                wave_append2(L.keys, L.keys + CHUNK, &L.cnt, CHUNK, v != 0 && v >= th, v, e, lane);
             }
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                wave_append2(L.keys, L.keys + CHUNK, &L.cnt, CHUNK, v[j] != 0 && v[j] >= th, v[j], e[j], lane);
         }
         if (tid == 0) {
             L.gtau = 0;
