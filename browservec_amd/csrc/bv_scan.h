@@ -1425,7 +1425,7 @@ template <int C, int LPR, int UPL> struct StepData {
 // lim (> 0): rows at or past lim load row lim-1 and are dropped later.
 template <int C, int LPR, int UPL, bool IDX>
 __device__ __forceinline__ void load_step(const ScanArgs &a, const ScanRegs<C, UPL> &R, const uint32_t *cand,
-                                          uint64_t base, uint64_t lim, StepData<C, LPR, UPL> &S, int lane) {
+                                          uint32_t base, uint32_t lim, StepData<C, LPR, UPL> &S, int lane) {
     using Unit = typename Codec<C>::Unit;
     using SH = ScanShape<C, LPR, UPL>;
     constexpr int U = SH::U, G = SH::G;
@@ -1433,15 +1433,15 @@ __device__ __forceinline__ void load_step(const ScanArgs &a, const ScanRegs<C, U
     const char *codes = (const char *)a.codes;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const uint64_t row = base + (uint64_t)u * G + slot;
-        const uint64_t rc = row < lim ? row : lim - 1;
-        const uint64_t grow = IDX ? (uint64_t)cand[rc] : rc;
+        const uint32_t row = base + (uint32_t)(u * G + slot);
+        const uint32_t rc = row < lim ? row : lim - 1;
+        const uint64_t grow = IDX ? (uint64_t)cand[rc] : (uint64_t)rc;
         const Unit *rp = (const Unit *)(codes + grow * a.row_bytes);
 #pragma unroll
         for (int t = 0; t < UPL; ++t) S.d[u][t] = load_stream(rp + R.ucl[t]);
     }
-    const uint64_t myrow = base + (uint64_t)xrow<U, LPR>(lane) * G + slot;
-    const uint64_t myrc = myrow < lim ? myrow : lim - 1;
+    const uint32_t myrow = base + (uint32_t)(xrow<U, LPR>(lane) * G + slot);
+    const uint32_t myrc = myrow < lim ? myrow : lim - 1;
     S.grow = IDX ? cand[myrc] : (uint32_t)myrc;
     S.scale = a.scales ? load_stream(a.scales + S.grow) : 1.0f;
 }
@@ -1450,7 +1450,7 @@ __device__ __forceinline__ void load_step(const ScanArgs &a, const ScanRegs<C, U
 // every eligible key into the lane's running maximum.
 template <int C, int LPR, int UPL>
 __device__ __forceinline__ void compute_step(const ScanArgs &a, const ScanRegs<C, UPL> &R,
-                                             const StepData<C, LPR, UPL> &S, uint64_t base, uint64_t lim,
+                                             const StepData<C, LPR, UPL> &S, uint32_t base, uint32_t lim,
                                              uint64_t tau, uint64_t *wk, uint32_t &wc, uint64_t &lmax, int lane) {
     using CD = Codec<C>;
     using Acc = typename CD::Acc;
@@ -1470,7 +1470,7 @@ __device__ __forceinline__ void compute_step(const ScanArgs &a, const ScanRegs<C
     Acc tot[CD::NA];
 #pragma unroll
     for (int m = 0; m < CD::NA; ++m) tot[m] = xreduce<U, LPR>(acc[m], lane);
-    const uint64_t myrow = base + (uint64_t)xrow<U, LPR>(lane) * G + lane / LPR;
+    const uint32_t myrow = base + (uint32_t)(xrow<U, LPR>(lane) * G + lane / LPR);
     bool take = false;
     uint64_t key = 0;
     if (xrep<U, LPR>(lane) && myrow < lim) {
@@ -1621,13 +1621,13 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     }
 
     const uint32_t *cand = a.cand;
-    uint64_t n = a.n;
+    uint32_t n = (uint32_t)a.n;  // row and candidate counts stay below 2^31 (checked at launch)
     if (IDX && a.cand_off) {
         cand = a.cand + a.cand_off[qi];
-        n = a.cand_off[qi + 1] - a.cand_off[qi];
+        n = (uint32_t)(a.cand_off[qi + 1] - a.cand_off[qi]);
     } else if (IDX && a.cand_n) {
         cand = a.cand + (uint64_t)qi * a.cand_stride;
-        n = a.cand_n[qi] < a.cand_stride ? a.cand_n[qi] : a.cand_stride;
+        n = a.cand_n[qi] < a.cand_stride ? a.cand_n[qi] : (uint32_t)a.cand_stride;
     }
     uint64_t *wslot = a.wmax + ((uint64_t)qi * a.grid + blockIdx.x) * SH::WAVES + wave;
     uint64_t lmax = 0;
@@ -1651,28 +1651,28 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     // steps stream worse.)  A wave whose slice runs dry moves to the slice
     // with the most tickets left.  The dynamic part absorbs speed differences between
     // workgroups (older waves win memory arbitration) and XCDs.
-    const uint64_t wofs = (uint64_t)wave * SH::RPS, wstep = (uint64_t)SH::WAVES * SH::RPS;
-    const uint64_t ngrabs = (n + SH::GRAB_ROWS - 1) / SH::GRAB_ROWS;
-    const uint64_t sgrabs = ngrabs * STATIC_PCT / 100 / a.grid;  // full static grabs per workgroup
-    uint64_t d0 = sgrabs * a.grid * SH::GRAB_ROWS;
+    const uint32_t wofs = (uint32_t)wave * SH::RPS, wstep = (uint32_t)SH::WAVES * SH::RPS;
+    const uint32_t ngrabs = (n + SH::GRAB_ROWS - 1) / SH::GRAB_ROWS;
+    const uint32_t sgrabs = (uint32_t)((uint64_t)ngrabs * STATIC_PCT / 100 / a.grid);  // full static grabs per workgroup
+    uint32_t d0 = sgrabs * a.grid * SH::GRAB_ROWS;
     if (d0 > n) d0 = n;
-    const uint64_t nsd = (n - d0 + SH::RPS - 1) / SH::RPS;  // dynamic steps
-    const uint64_t per = (nsd + ng - 1) / ng;              // steps per slice
+    const uint32_t nsd = (n - d0 + SH::RPS - 1) / SH::RPS;  // dynamic steps
+    const uint32_t per = (nsd + ng - 1) / ng;              // steps per slice
     // a slice's step count, and its chunks of DSTEPS steps (the rest are
     // single-step tickets)
-    auto slice_steps = [&](uint32_t r) -> uint64_t {
-        const uint64_t lo = (uint64_t)r * per;
+    auto slice_steps = [&](uint32_t r) -> uint32_t {
+        const uint32_t lo = r * per;
         return lo >= nsd ? 0 : (nsd - lo < per ? nsd - lo : per);
     };
-    auto big_chunks = [&](uint64_t ls) -> uint64_t { return ls / DSTEPS; };
-    auto slice_tickets = [&](uint32_t r) -> uint64_t {
-        const uint64_t ls = slice_steps(r), nb = big_chunks(ls);
+    auto big_chunks = [&](uint32_t ls) -> uint32_t { return ls / DSTEPS; };
+    auto slice_tickets = [&](uint32_t r) -> uint32_t {
+        const uint32_t ls = slice_steps(r), nb = big_chunks(ls);
         return nb + (ls - nb * DSTEPS);
     };
-    uint64_t gi = 0;
+    uint32_t gi = 0;
     uint32_t sub = 0, ds = 0, dlen = 0, slice = (blockIdx.x * SH::WAVES + wave) % ng, pend = 0;
     bool dynamic = false, has_pend = false;
-    uint64_t c0 = 0, clim = 0;
+    uint32_t c0 = 0, clim = 0;
     // takes the next dynamic ticket: its first row in c0 and end in clim;
     // false when every slice is exhausted
     auto take_chunk = [&]() -> bool {
@@ -1686,14 +1686,14 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
                 if (lane == 0) v = atomicAdd(&qs->dyn[slice * CL], 1u);
                 t = __builtin_amdgcn_readfirstlane(v);
             }
-            const uint64_t ls = slice_steps(slice), nb = big_chunks(ls);
+            const uint32_t ls = slice_steps(slice), nb = big_chunks(ls);
             if (t < nb + (ls - nb * DSTEPS)) {
                 if (lane == 0) pend = atomicAdd(&qs->dyn[slice * CL], 1u);  // next ticket in flight
                 has_pend = true;
-                const uint64_t st = t < nb ? (uint64_t)t * DSTEPS : nb * DSTEPS + (t - nb);
+                const uint32_t st = t < nb ? t * DSTEPS : nb * DSTEPS + (t - nb);
                 dlen = t < nb ? DSTEPS : 1;
-                c0 = d0 + ((uint64_t)slice * per + st) * SH::RPS;
-                const uint64_t e = c0 + (uint64_t)dlen * SH::RPS;
+                c0 = d0 + (slice * per + st) * SH::RPS;
+                const uint32_t e = c0 + dlen * SH::RPS;
                 clim = e < n ? e : n;
                 return true;
             }
@@ -1702,7 +1702,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             uint64_t rem = 0;
             if ((uint32_t)lane < ng) {
                 const uint32_t c = load_shared(&qs->dyn[lane * CL]);
-                const uint64_t L = slice_tickets(lane);
+                const uint64_t L = slice_tickets((uint32_t)lane);
                 rem = c < L ? L - c : 0;
             }
             const uint64_t best = wave_max_u64((rem << 32) | (uint32_t)lane);
@@ -1710,11 +1710,11 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             slice = (uint32_t)best;
         }
     };
-    auto next_step = [&](uint64_t &base, uint64_t &lim) -> bool {
+    auto next_step = [&](uint32_t &base, uint32_t &lim) -> bool {
         if (!dynamic) {
             while (gi < sgrabs) {
-                const uint64_t r0 = ((uint64_t)blockIdx.x + gi * a.grid) * SH::GRAB_ROWS;
-                base = r0 + wofs + (uint64_t)sub * wstep;
+                const uint32_t r0 = (blockIdx.x + gi * a.grid) * SH::GRAB_ROWS;
+                base = r0 + wofs + sub * wstep;
                 lim = r0 + SH::GRAB_ROWS < n ? r0 + SH::GRAB_ROWS : n;
                 if (++sub == (uint32_t)SH::GRAB_STEPS) {
                     sub = 0;
@@ -1726,7 +1726,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         }
         for (;;) {
             if (ds < dlen) {
-                base = c0 + (uint64_t)ds * SH::RPS;
+                base = c0 + ds * SH::RPS;
                 ++ds;
                 if (base < clim) {
                     lim = clim;
@@ -1742,7 +1742,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     using SD = StepData<C, LPR, UPL>;
     constexpr bool PIPE = SH::U * UPL * (int)(sizeof(typename CD::Unit) / 4) <= 32;  // double-buffer the loads
     SD A, B;
-    uint64_t ab = 0, al = 0, bb = 0, bl = 0;
+    uint32_t ab = 0, al = 0, bb = 0, bl = 0;
     // the query slice: transformed here by wave 0 into LDS, or read from a
     // prepared global layout.  Wave 0 issues the query and sign reads before
     // any code load, and transforms while the first code loads are in flight.
@@ -1765,13 +1765,28 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     // operations and the load counter, which drains in order, lets a wave
     // wait for exactly the step it scores while the other stays in flight.
     // (A query with no rows issues no loads: the first row is not there.)
+    // The query slice, when it comes prepared in global memory, is read
+    // before any code load: the load counter drains in order, so a read
+    // issued after the code loads would make the first score wait for all of
+    // them (and the compiler places that wait at the loop head, so every pass
+    // would wait for both steps).  A slice the kernel transforms itself is
+    // read from LDS after the transform.  Each read goes through a pointer of
+    // known address space.
+    auto read_query = [&](const QT *qb) {
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) {
+#pragma unroll
+            for (int j = 0; j < CD::QN; ++j) R.qr[t][j] = R.uok[t] ? qb[(p + LPR * t) * CD::QN + j] : (QT)0;
+        }
+        R.fin.load((const char *)qb + (uint64_t)a.units * CD::QN * sizeof(QT), a.padded_dim);
+    };
+    if (!prep) read_query((const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride));
     const bool any = n > 0;
     bool ha = any && next_step(ab, al);
     if (PIPE && any) load_step<C, LPR, UPL, IDX>(a, R, cand, ha ? ab : 0, ha ? al : 1, A, lane);
     bool hb = PIPE && ha && next_step(bb, bl);
     if (PIPE && any) load_step<C, LPR, UPL, IDX>(a, R, cand, hb ? bb : 0, hb ? bl : 1, B, lane);
 
-    const QT *qbase;
     if (prep) {
         if constexpr (PW::ok) {
             prep_query_wg<C, PW::EP>(a, rinw, scan_smem, tid);
@@ -1779,17 +1794,9 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             if (wave == 0) prep_query_e<C, PS::E>(a, rin, scan_smem, lane);
         }
         __syncthreads();
-        qbase = (const QT *)scan_smem;
-    } else {
-        qbase = (const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride);
+        read_query((const QT *)scan_smem);
+        __syncthreads();  // the LDS holding it becomes the waves' lists
     }
-#pragma unroll
-    for (int t = 0; t < UPL; ++t) {
-#pragma unroll
-        for (int j = 0; j < CD::QN; ++j) R.qr[t][j] = R.uok[t] ? qbase[(p + LPR * t) * CD::QN + j] : (QT)0;
-    }
-    R.fin.load((const char *)qbase + (uint64_t)a.units * CD::QN * sizeof(QT), a.padded_dim);
-    if (a.qraw) __syncthreads();  // the LDS holding it becomes the waves' lists
     uint64_t gt = 0;      // what the previous pass read: the shared bound when it polled
     bool polled = false;
     for (uint32_t pi = 0; ha; ++pi) {
@@ -2107,6 +2114,7 @@ template <int C, int LPR, int UPL>
 hipError_t go(const ScanArgs &a, uint32_t nq, hipStream_t s) {
     // the per-wave lists must take a whole grab above the compaction target
     if (a.wcap < 2 * a.kprime + ScanShape<C, LPR, UPL>::WGRAB || (a.wcap & 63)) return hipErrorInvalidValue;
+    if (a.n >= (1ull << 31)) return hipErrorInvalidValue;  // the kernel keeps row positions in 32 bits
     if (a.wstride < a.wcap || (a.rr_src && a.wstride < a.wcap + (a.rr_dim & ~3u))) return hipErrorInvalidValue;
     size_t lds = (size_t)(SCAN_WG / 64) * a.wstride * sizeof(uint64_t);
     if (lds < sizeof(TopkLds)) lds = sizeof(TopkLds);
