@@ -41,8 +41,18 @@ COMMON = [
 ]
 
 
+# The fused scan issues each atomic from one lane and reads its result later
+# (a prefetched work ticket, a slot reservation read after the re-rank's row
+# loads).  The backend's atomic optimizer would rewrite every such atomic into
+# a single-lane atomic plus an immediate broadcast of its result, which makes
+# the wave wait for the atomic's round trip on the spot.
+SCAN_FLAGS = ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]
+
+
 def _compile(src: str, obj: str) -> None:
     flags = list(COMMON)
+    if src.startswith("bv_scan_"):
+        flags += SCAN_FLAGS
     if src.endswith(".cpp"):
         flags = ["-x", "hip"] + flags
     cmd = [HIPCC] + flags + ["-c", os.path.join(CSRC, src), "-o", obj]

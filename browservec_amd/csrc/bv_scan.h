@@ -344,6 +344,52 @@ template <int E> __device__ __forceinline__ void fwht_xlane64(float (&x)[E], int
     fwht_xlane<32>(x, lane);
 }
 
+// The u64 of lane ^ M, by the same moves as lane_xor.
+template <int M> __device__ __forceinline__ uint64_t lane_xor_u64(uint64_t x, int lane) {
+    const float lo = lane_xor<M>(__builtin_bit_cast(float, (uint32_t)x), lane);
+    const float hi = lane_xor<M>(__builtin_bit_cast(float, (uint32_t)(x >> 32)), lane);
+    return ((uint64_t)__builtin_bit_cast(uint32_t, hi) << 32) | __builtin_bit_cast(uint32_t, lo);
+}
+
+// One compare-exchange stage (partner distance J, merge block size kk) of a
+// bitonic sort of 128 (key, payload) pairs held two per lane: element
+// lane + 64 s in k[s], v[s].  Keys are distinct; the sort is descending.
+template <int J>
+__device__ __forceinline__ void bitonic128_stage(uint64_t (&k)[2], uint64_t (&v)[2], int lane, uint32_t kk) {
+    uint64_t pk[2], pv[2];
+    if constexpr (J == 64) {
+        pk[0] = k[1]; pv[0] = v[1];
+        pk[1] = k[0]; pv[1] = v[0];
+    } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            pk[t] = lane_xor_u64<J>(k[t], lane);
+            pv[t] = lane_xor_u64<J>(v[t], lane);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const uint32_t e = (uint32_t)lane + 64u * t;
+        const bool lower = (e & J) == 0, desc = (e & kk) == 0;
+        const bool keep = (lower == desc) == (k[t] > pk[t]);  // keep the larger key iff lower == desc
+        k[t] = keep ? k[t] : pk[t];
+        v[t] = keep ? v[t] : pv[t];
+    }
+}
+// Sorts the 128 pairs descending by key (the whole wave takes part).
+__device__ __forceinline__ void bitonic128(uint64_t (&k)[2], uint64_t (&v)[2], int lane) {
+#pragma unroll
+    for (uint32_t kk = 2; kk <= 128; kk <<= 1) {
+        if (kk >= 128) bitonic128_stage<64>(k, v, lane, kk);
+        if (kk >= 64) bitonic128_stage<32>(k, v, lane, kk);
+        if (kk >= 32) bitonic128_stage<16>(k, v, lane, kk);
+        if (kk >= 16) bitonic128_stage<8>(k, v, lane, kk);
+        if (kk >= 8) bitonic128_stage<4>(k, v, lane, kk);
+        if (kk >= 4) bitonic128_stage<2>(k, v, lane, kk);
+        bitonic128_stage<1>(k, v, lane, kk);
+    }
+}
+
 // Wave-wide f64 maximum (fmax: a NaN operand never wins) and i32 sum, in
 // every lane, through DPP / swaps on the 32-bit halves.
 __device__ __forceinline__ double wave_fmax_f64(double v) {
@@ -1312,9 +1358,9 @@ __device__ uint64_t exact_key_wave(const float *src, const float *qs, uint32_t d
 // reference's `a_m += x*y` in f64), lane 4c combines the four as
 // ((a0 + a1) + a2) + a3 and adds the tail elements in order.  x: this lane's
 // row; every lane of the wave calls it; the key is valid in lanes 4c.
-// qd holds the query as doubles (LDS).  Each lane issues its row loads 64 at
-// a time ahead of the dependent FMA chain, so a row costs a few memory round
-// trips, not one per eight elements.
+// qd holds the query as doubles (LDS).  Each lane issues its row loads 192 at
+// a time ahead of the dependent FMA chain, so a row costs one memory round
+// trip up to dim 768 (a few beyond), not one per eight elements.
 template <int B>
 __device__ __forceinline__ void dot_chain(const float *x, const double *qd, uint32_t vec, uint32_t &j, double &acc) {
     for (; j + 4 * (B - 1) < vec; j += 4 * B) {
@@ -1330,7 +1376,7 @@ __device__ __forceinline__ uint64_t exact_key_lanes4(const float *x, const doubl
     const uint32_t vec = dim & ~3u;
     double acc = 0.0;
     uint32_t j = (uint32_t)(lane & 3);
-    dot_chain<64>(x, qd, vec, j, acc);
+    dot_chain<192>(x, qd, vec, j, acc);
     dot_chain<16>(x, qd, vec, j, acc);
     dot_chain<1>(x, qd, vec, j, acc);
     const double a1 = __shfl_down(acc, 1), a2 = __shfl_down(acc, 2), a3 = __shfl_down(acc, 3);
@@ -1555,7 +1601,9 @@ __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
             L.cnt = 0;
         }
         __syncthreads();
-        const uint32_t top = L.flag;
+        // every scanning workgroup has finished: nothing left to prune, and
+        // the launch completes only when this workgroup exits
+        if (L.flag >= a.grid) break;
         for (uint32_t i0 = 0; i0 < nslots; i0 += 8 * SCAN_WG) {
             uint64_t v[8];
 #pragma unroll
@@ -1577,7 +1625,6 @@ __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
             }
         }
         __syncthreads();
-        if (top >= a.grid) break;
     }
 }
 
@@ -1781,6 +1828,22 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         R.fin.load((const char *)qb + (uint64_t)a.units * CD::QN * sizeof(QT), a.padded_dim);
     };
     if (!prep) read_query((const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride));
+    // The fp32 query of the exact re-rank, read here too (dims up to 64 * RQ;
+    // lane l holds elements l + 64k) and staged as doubles behind the wave's
+    // list once the LDS is free, so the flush at the end of the scan starts
+    // with its row loads.
+    constexpr int RQ = 16;
+    const uint32_t rvec = a.rr_dim & ~3u;
+    const bool stage_q = a.rr_src != nullptr && rvec <= 64 * RQ;
+    float rqv[RQ];
+    if (stage_q) {
+        const float *rq = a.rr_q + (uint64_t)qi * a.rr_q_stride;
+#pragma unroll
+        for (int k = 0; k < RQ; ++k) {
+            const uint32_t i = (uint32_t)lane + 64u * k;
+            rqv[k] = rq[i < rvec ? i : rvec - 1];  // (clamped: every lane loads)
+        }
+    }
     const bool any = n > 0;
     bool ha = any && next_step(ab, al);
     if (PIPE && any) load_step<C, LPR, UPL, IDX>(a, R, cand, ha ? ab : 0, ha ? al : 1, A, lane);
@@ -1796,6 +1859,14 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         __syncthreads();
         read_query((const QT *)scan_smem);
         __syncthreads();  // the LDS holding it becomes the waves' lists
+    }
+    if (stage_q) {
+        double *qd = (double *)(wk + wcap);
+#pragma unroll
+        for (int k = 0; k < RQ; ++k) {
+            const uint32_t i = (uint32_t)lane + 64u * k;
+            if (i < rvec) qd[i] = (double)rqv[k];
+        }
     }
     uint64_t gt = 0;      // what the previous pass read: the shared bound when it polled
     bool polled = false;
@@ -1872,17 +1943,23 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         uint64_t *ck0 = a.cand_keys + 2 * ((uint64_t)qi * a.cand_cap + grp * region);
         if (a.rr_src) {
             // the query as doubles in the wave's staging area behind its list
+            // (staged before the scan when the dimension allows)
             const float *rq = a.rr_q + (uint64_t)qi * a.rr_q_stride;
             double *qd = (double *)(wk + wcap);
-            const uint32_t vec = a.rr_dim & ~3u;
-            for (uint32_t i = (uint32_t)lane; i < vec; i += 64) qd[i] = (double)rq[i];
+            if (!stage_q)
+                for (uint32_t i = (uint32_t)lane; i < rvec; i += 64) qd[i] = (double)rq[i];
             for (uint32_t j0 = 0; j0 < wc; j0 += 16) {  // sixteen candidates per pass
                 const uint32_t j = j0 + (uint32_t)(lane >> 2);
                 const bool have = j < wc;
                 const uint64_t k = have ? wk[j] : 0ull;
                 const uint32_t row = have ? key_row(k) : 0u;  // absent candidates read row 0
                 const uint64_t ek = exact_key_lanes4(a.rr_src + (uint64_t)row * a.rr_dim, qd, rq, a.rr_dim, row, lane);
-                const uint32_t base = __builtin_amdgcn_readfirstlane(b0);
+                // read the reservation only now: tied to the exact key, so the
+                // compiler cannot hoist the read (and its wait for the atomic)
+                // above the row loads
+                uint32_t bv = b0;
+                asm volatile("" : "+v"(bv) : "v"((uint32_t)ek));
+                const uint32_t base = __builtin_amdgcn_readfirstlane(bv);
                 if (have && (lane & 3) == 0) {
                     store_shared(&ck0[2 * (base + j)], k);
                     store_shared(&ck0[2 * (base + j) + 1], ek);
@@ -1963,6 +2040,47 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         }
         __syncthreads();
         const uint32_t nk = L.cnt;
+        if (nk <= 128) {
+            // Up to 128 pairs (the common case): wave 0 sorts them by scan
+            // key in registers, keeps the best kp (the fetch), and sorts the
+            // fetch's exact keys for the output.
+            if (wave == 0) {
+                uint64_t sk[2], ek[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const uint32_t e = (uint32_t)lane + 64u * t;
+                    sk[t] = e < nk ? L.keys[e] : 0ull;
+                    ek[t] = e < nk ? L.keys[CHUNK + e] : 0ull;
+                }
+                bitonic128(sk, ek, lane);
+                const uint32_t mm = nk < kp ? nk : kp;
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const uint32_t e = (uint32_t)lane + 64u * t;
+                    sk[t] = e < mm ? ek[t] : 0ull;  // the fetch's exact keys
+                    ek[t] = 0;
+                }
+                bitonic128(sk, ek, lane);
+                const uint32_t ko = mm < a.k_out ? mm : a.k_out;
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const uint32_t e = (uint32_t)lane + 64u * t;
+                    if (e < ko) {
+                        a.out_rows[(uint64_t)qi * a.k_out + e] = key_row(sk[t]);
+                        a.out_scores[(uint64_t)qi * a.k_out + e] = f32_from_ord((uint32_t)(sk[t] >> 32));
+                    }
+                }
+                if (lane == 0) {
+                    a.out_n[qi] = ko;
+                    a.merged_n[qi] = mm;
+                }
+            }
+            __syncthreads();
+            if (tid == 0) L.last = atomicAdd(&qs->fin, 1u) == 1;
+            __syncthreads();
+            if (L.last) reset_query(a, qi);
+            return;
+        }
         if (nk > kp) {
             for (uint32_t j = tid; j < nk; j += SCAN_WG)
                 if (count_greater(L.keys, nk, L.keys[j]) == kp - 1) L.gtau = L.keys[j];
