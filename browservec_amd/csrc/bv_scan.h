@@ -444,7 +444,7 @@ struct TopkLds {
     uint32_t hist[SEL_BINS];
     uint32_t red[16];           // cross-wave reduction slots
     uint32_t ovl[SCAN_WG];      // final selection: per-group flush counts, then their prefix
-    uint32_t cnt, cnt2, bstar, above, flag, last, grab, over;
+    uint32_t cnt, cnt2, bstar, above, flag, last, grab;
     uint64_t tau, gtau;
 };
 
@@ -1433,7 +1433,9 @@ template <int C, int LPR, int UPL> struct ScanShape {
     static constexpr int U0 = UPL >= 4 ? 2 : (UPL >= 2 ? 4 : 8);
     // one transposing stage per halving of U (at most three), and at most 32
     // rows per step so that a pass of two steps adds at most 64 keys to a
-    // wave's list (the list's slack beyond twice the fetch)
+    // wave's list (the list's slack beyond twice the fetch).  (64-row steps
+    // for the 8-lane layouts measured slower: 1-bit Hamming 0.31 vs 0.42 of
+    // HBM peak.)
     static constexpr int UMAX = LPR >= 16 ? 8 : LPR / 2;
     static constexpr int U = U0 < UMAX ? U0 : UMAX;  // row groups per lane per step
     static constexpr int G = 64 / LPR;               // rows per load instruction
@@ -2003,13 +2005,24 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             const uint32_t o = __shfl_up(incl, d);
             incl += lane >= d ? o : 0u;
         }
-        const uint64_t over = __ballot(c > spec);
+        // the pairs beyond the first spec of each group: their exclusive
+        // prefix in ovl[96..129) indexes one flat range for a parallel gather
+        const uint32_t ex = c > spec ? c - spec : 0u;
+        uint32_t xin = ex;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = __shfl_up(xin, d);
+            xin += lane >= d ? o : 0u;
+        }
         if ((uint32_t)tid < ng) {
             L.ovl[tid] = c;
             L.ovl[32 + tid] = incl - c;
+            L.ovl[96 + tid] = xin - ex;
         }
-        if ((uint32_t)tid == ng - 1) L.ovl[32 + ng] = incl;
-        if (tid == 0) L.over = (uint32_t)over;
+        if ((uint32_t)tid == ng - 1) {
+            L.ovl[32 + ng] = incl;
+            L.ovl[96 + ng] = xin;
+        }
     }
     __syncthreads();
     const uint32_t total = L.ovl[32 + ng];
@@ -2021,18 +2034,23 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         const uint64_t th = L.tau;
         const bool sok = ss < spec && ss < L.ovl[sg];  // (threads past ng * spec read no pair)
         wave_append2(L.keys, L.keys + CHUNK, &L.cnt, CHUNK, sok && sv != 0 && sv >= th, sv, se, lane);
-        for (uint32_t over = L.over; over; over &= over - 1) {  // groups with more than spec pairs
-            const uint32_t r = (uint32_t)__builtin_ctz(over), c = L.ovl[r];
-            for (uint32_t i0 = spec; i0 < c; i0 += SCAN_WG) {
-                const uint32_t i = i0 + tid;
-                uint64_t v = 0, e = 0;
-                if (i < c) {
-                    const uint64_t slot = 2 * ((uint64_t)r * region + i);
-                    v = load_shared(&ckq[slot]);
-                    e = load_shared(&ckq[slot + 1]);
+        // the rest of the groups that flushed more than spec pairs, all at once
+        const uint32_t xtot = L.ovl[96 + ng];
+        for (uint32_t i0 = 0; i0 < xtot; i0 += SCAN_WG) {
+            const uint32_t i = i0 + tid;
+            uint64_t v = 0, e = 0;
+            if (i < xtot) {
+                uint32_t lo = 0, hi = ng - 1;  // the group r with ovl[96 + r] <= i < ovl[96 + r + 1]
+                while (lo < hi) {
+                    const uint32_t mid = (lo + hi + 1) / 2;
+                    if (L.ovl[96 + mid] <= i) lo = mid;
+                    else hi = mid - 1;
                 }
-                wave_append2(L.keys, L.keys + CHUNK, &L.cnt, CHUNK, v != 0 && v >= th, v, e, lane);
+                const uint64_t slot = 2 * ((uint64_t)lo * region + spec + (i - L.ovl[96 + lo]));
+                v = load_shared(&ckq[slot]);
+                e = load_shared(&ckq[slot + 1]);
             }
+            wave_append2(L.keys, L.keys + CHUNK, &L.cnt, CHUNK, v != 0 && v >= th, v, e, lane);
         }
         if (tid == 0) {
             L.gtau = 0;
