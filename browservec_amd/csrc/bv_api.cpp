@@ -326,7 +326,9 @@ extern "C" int bv_index_create(bv_device *dev, const bv_index_desc *desc, bv_ind
         x->row_bytes = x->words_per_row * 4;
         if (d.bits == 8) x->codec = d.scorer == BV_SCORER_INT8SYM ? C_I8S : C_Q8;
         else if (d.bits == 4) x->codec = C_Q4;
-        else x->codec = d.scorer == BV_SCORER_HAMMING ? C_HAM : C_Q1A;
+        // 1-bit asymmetric: the bit-plane prefilter from P = 128 (one 16-byte
+        // unit per 128 codes), the plain fp32 sum below
+        else x->codec = d.scorer == BV_SCORER_HAMMING ? C_HAM : (x->P >= 128 ? C_Q1P : C_Q1A);
         x->units = x->codec == C_Q1A ? x->row_bytes / 4 : x->row_bytes / 16;
         if (x->row_bytes < 16 && x->codec != C_Q1A) {
             delete x;
@@ -1022,6 +1024,21 @@ static int prepare_queries(bv_index *idx, const float *d_q, uint32_t nq, const v
         *qscan = idx->qrot.p;
         *qstride = (uint64_t)P * 4;
         break;
+    case C_Q1P: {
+        const size_t st = level_stride(C_Q1P, P);
+        HIPX(idx->dev, idx->qscan.ensure((size_t)nq * st, 0, idx->stream), "query buffer");
+        HIPX(idx->dev, launch_encode(a, idx->stream), "query rotate kernel");
+        LevelArgs la{};
+        la.qrot = idx->qrot.as<float>();
+        la.P = P;
+        la.codec = C_Q1P;
+        la.out = idx->qscan.as<unsigned char>();
+        la.stride = st;
+        HIPX(idx->dev, launch_q1p_layout(la, nq, idx->stream), "query bit-plane kernel");
+        *qscan = idx->qscan.p;
+        *qstride = st;
+        return BV_OK;
+    }
     case C_HAM:
     case C_I8S: {
         const uint32_t per = idx->codec == C_HAM ? 32 : 4;
@@ -1077,7 +1094,7 @@ static void scan_common(const bv_index *idx, const float *d_q, uint64_t n, uint3
     a.row_bytes = idx->row_bytes;
     a.units = idx->units;
     a.padded_dim = idx->P;
-    a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A) ? idx->scales.as<float>() : nullptr;
+    a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A || idx->codec == C_Q1P) ? idx->scales.as<float>() : nullptr;
     a.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
     a.mask = d_mask;
     a.mask_bits = mask_bits;
@@ -1771,7 +1788,7 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     a.row_bytes = idx->row_bytes;
     a.units = idx->units;
     a.padded_dim = idx->P;
-    a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A) ? idx->scales.as<float>() : nullptr;
+    a.scales = (idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_Q1A || idx->codec == C_Q1P) ? idx->scales.as<float>() : nullptr;
     a.scale_mul = idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f;
     if (in_kernel) {  // the scan rotates and transforms the fp32 query itself
         a.qraw = idx->qin.as<float>();

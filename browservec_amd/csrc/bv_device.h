@@ -35,4 +35,14 @@ struct QLevelTail {
     int32_t pad;
 };
 
+// Tail of the 1-bit asymmetric bit-plane layout: the query's int8 level
+// (q ~= s1 * Q), sum |q - s1 * Q|, sum |q| and sum Q.
+struct Q1Tail {
+    double s1;
+    double rsum;
+    double qabs;
+    int32_t sumq;
+    int32_t pad;
+};
+
 }  // namespace bvk

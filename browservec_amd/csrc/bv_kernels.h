@@ -18,7 +18,10 @@ enum CodecId : int {
     C_I8S = 6,      // int8 codes x int8 query         (16-byte units)
     C_F32DOT_S = 7, // fp32 rows, dim % 4 != 0         (4-byte units = 1 float)
     C_F32L2_S = 8,
-    C_COUNT = 9,
+    C_Q1P = 9,      // 1-bit codes, asymmetric, scored through the query's int8
+                    // bit planes with an exact fp32 re-score near the bound
+                    // (16-byte units = 128 codes)
+    C_COUNT = 10,
     // query-level layout only (not a scan codec): int4 levels (no 1/127 scale)
     // in the int8 16-code unit layout, for the batched matrix-core scan
     C_Q4M = 16
@@ -77,6 +80,7 @@ struct ScanArgs {
     uint32_t kprime;          // per-query candidates kept
     uint32_t wcap;            // per-wave LDS list capacity, scan_wcap(kprime)
     uint32_t wstride;         // u64 words of LDS per wave: wcap (+ dim & ~3 re-rank staging)
+    uint32_t qf_off;          // C_Q1P: LDS byte offset of the fp32 query (set at launch)
     uint32_t grid;            // scanning workgroups per query (one more runs the threshold helper)
     QState *qs;               // [nq]
     uint64_t *wmax;           // [nq][grid*4] per-wave running maxima (zero on entry and exit)
@@ -295,6 +299,8 @@ hipError_t launch_scan(int codec, uint32_t units, const ScanArgs &a, uint32_t nq
 hipError_t launch_encode(const EncodeArgs &a, hipStream_t s);
 hipError_t launch_rerank(const RerankArgs &a, uint32_t nq, hipStream_t s);
 hipError_t launch_levels(const LevelArgs &a, uint32_t nq, hipStream_t s);
+// C_Q1P query layout (bit planes + Q1Tail + fp32 query) from rotated queries.
+hipError_t launch_q1p_layout(const LevelArgs &a, uint32_t nq, hipStream_t s);
 size_t level_stride(int codec, uint32_t P);
 size_t scan_query_lds(int codec, uint32_t P);
 // True when the scan for this codec / row layout transforms fp32 queries itself (ScanArgs::qraw).

@@ -94,7 +94,7 @@ bool scan_supported(int codec, uint32_t units) {
     Layout L;
     if (!pick_layout(units, L)) return false;
     // register budget: at most 64 query values per lane
-    static const int qn[C_COUNT] = {4, 4, 12, 24, 32, 4, 4, 1, 1};
+    static const int qn[C_COUNT] = {4, 4, 12, 24, 32, 4, 4, 1, 1, 32};
     return codec >= 0 && codec < C_COUNT && L.upl * qn[codec] <= 64;
 }
 
@@ -107,6 +107,7 @@ hipError_t launch_scan(int codec, uint32_t units, const ScanArgs &a, uint32_t nq
     case C_Q8: return scan_codec_q8(L.lpr, L.upl, a, nq, s);
     case C_Q4: return scan_codec_q4(L.lpr, L.upl, a, nq, s);
     case C_Q1A: return scan_codec_q1a(L.lpr, L.upl, a, nq, s);
+    case C_Q1P: return scan_codec_q1p(L.lpr, L.upl, a, nq, s);
     case C_HAM: return scan_codec_ham(L.lpr, L.upl, a, nq, s);
     case C_I8S: return scan_codec_i8s(L.lpr, L.upl, a, nq, s);
     case C_F32DOT_S: return scan_codec_f32dot_s(L.lpr, L.upl, a, nq, s);
@@ -154,6 +155,21 @@ hipError_t launch_levels(const LevelArgs &a, uint32_t nq, hipStream_t s) {
 
 size_t level_stride(int codec, uint32_t P) { return query_layout_bytes(codec, P); }
 
+hipError_t launch_q1p_layout(const LevelArgs &a, uint32_t nq, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    const size_t lds = a.P;
+    switch (a.P / 64) {
+    case 2: hipLaunchKernelGGL(query_q1p<2>, dim3(nq), dim3(64), lds, s, a); break;
+    case 4: hipLaunchKernelGGL(query_q1p<4>, dim3(nq), dim3(64), lds, s, a); break;
+    case 8: hipLaunchKernelGGL(query_q1p<8>, dim3(nq), dim3(64), lds, s, a); break;
+    case 16: hipLaunchKernelGGL(query_q1p<16>, dim3(nq), dim3(64), lds, s, a); break;
+    case 32: hipLaunchKernelGGL(query_q1p<32>, dim3(nq), dim3(64), lds, s, a); break;
+    case 64: hipLaunchKernelGGL(query_q1p<64>, dim3(nq), dim3(64), lds, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 bool scan_prep_supported(int codec, uint32_t units, uint32_t P) {
     Layout L;
     if (!pick_layout(units, L)) return false;
@@ -161,7 +177,7 @@ bool scan_prep_supported(int codec, uint32_t units, uint32_t P) {
     switch (codec) {
     case C_Q8: case C_I8S: upc = 16; break;
     case C_Q4: case C_Q1A: upc = 32; break;
-    case C_HAM: upc = 128; break;
+    case C_HAM: case C_Q1P: upc = 128; break;
     default: return false;
     }
     const uint32_t full = (uint32_t)upc * L.lpr * L.upl;

@@ -129,6 +129,24 @@ template <> struct Codec<C_HAM> {
         a[0] += __popc(u.x ^ q[0]) + __popc(u.y ^ q[1]) + __popc(u.z ^ q[2]) + __popc(u.w ^ q[3]);
     }
 };
+// 1-bit codes (128 per unit) against the query's int8 level Q held as bit
+// planes: q[p*4 + d] is bit p of Q for the 32 codes of code dword d (two's
+// complement, so plane 7 weighs -128).  The sum over the unit of
+// code_bit * Q is sum_p weight_p * popcount(code & plane_p), exact in int32.
+template <> struct Codec<C_Q1P> {
+    using Unit = uint4; using QT = uint32_t; using Acc = int32_t;
+    static constexpr int QN = 32, NA = 1;
+    static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int pl = 0; pl < 8; ++pl) {
+            int32_t c = 0;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) c += (int32_t)__popc(w[d] & q[pl * 4 + d]);
+            a[0] += pl == 7 ? -(c << 7) : (c << pl);
+        }
+    }
+};
 template <> struct Codec<C_I8S> {
     using Unit = uint4; using QT = uint32_t; using Acc = int32_t;
     static constexpr int QN = 4, NA = 1;
@@ -163,6 +181,19 @@ template <> struct Fin<C_HAM> {
         const int32_t sim = P - 2 * t[0];
         ord = ord_i32(sim);
         return (float)sim;
+    }
+};
+// The int8 level of the 1-bit asymmetric prefilter (the scan's exact
+// re-score uses the fp32 query; score() is not used).
+template <> struct Fin<C_Q1P> {
+    double s1, rsum, qabs;
+    int32_t sumq;
+    __device__ void load(const void *tail, uint32_t) {
+        const Q1Tail *q = (const Q1Tail *)tail;
+        s1 = q->s1;
+        rsum = q->rsum;
+        qabs = q->qabs;
+        sumq = q->sumq;
     }
 };
 template <> struct Fin<C_I8S> {
@@ -421,6 +452,40 @@ __device__ __forceinline__ double wave_fmax_f64(double v) {
         const double x = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[0] << 32) | (uint32_t)l[0]);
         const double y = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[1] << 32) | (uint32_t)l[1]);
         v = fmax(x, y);
+    }
+    return v;
+}
+// Wave-wide f64 sum in every lane (the same pairing as wave_fmax_f64; each
+// pair adds the same two values, so every lane ends with the same sum).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#define BV_SUM_STEP(GET)                                                         \
+    {                                                                            \
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);                      \
+        const uint32_t lo = GET((uint32_t)b), hi = GET((uint32_t)(b >> 32));     \
+        v = v + __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);           \
+    }
+#define BV_DPP_GET(C) [](uint32_t w) { return dpp<C>(w); }
+    BV_SUM_STEP(BV_DPP_GET(DPP_XOR1))
+    BV_SUM_STEP(BV_DPP_GET(DPP_XOR2))
+    BV_SUM_STEP(BV_DPP_GET(DPP_HALF_MIRROR))
+    BV_SUM_STEP(BV_DPP_GET(DPP_MIRROR))
+#undef BV_DPP_GET
+#undef BV_SUM_STEP
+    {
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        auto l = __builtin_amdgcn_permlane16_swap((int)(uint32_t)b, (int)(uint32_t)b, false, false);
+        auto h = __builtin_amdgcn_permlane16_swap((int)(uint32_t)(b >> 32), (int)(uint32_t)(b >> 32), false, false);
+        const double x = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[0] << 32) | (uint32_t)l[0]);
+        const double y = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[1] << 32) | (uint32_t)l[1]);
+        v = x + y;
+    }
+    {
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        auto l = __builtin_amdgcn_permlane32_swap((int)(uint32_t)b, (int)(uint32_t)b, false, false);
+        auto h = __builtin_amdgcn_permlane32_swap((int)(uint32_t)(b >> 32), (int)(uint32_t)(b >> 32), false, false);
+        const double x = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[0] << 32) | (uint32_t)l[0]);
+        const double y = __builtin_bit_cast(double, ((uint64_t)(uint32_t)h[1] << 32) | (uint32_t)l[1]);
+        v = x + y;
     }
     return v;
 }
@@ -1065,6 +1130,52 @@ __global__ __launch_bounds__(64) void query_levels(LevelArgs a) {
     levels_wave<E>(x, P, a.codec, (signed char *)lsm, a.out + (uint64_t)qi * a.stride, lane);
 }
 
+// C_Q1P bit planes from the query's int8 level Q (P signed bytes at lv):
+// word u*32 + pl*4 + d holds bit pl of Q for codes 128u + 32d .. +31 (bit b
+// = code 128u + 32d + b).  Threads tid, tid + nt, .. build one word each.
+__device__ __forceinline__ void q1p_planes(const signed char *lv, uint32_t P, uint32_t *out, uint32_t tid,
+                                           uint32_t nt) {
+    const uint32_t nw = P / 4;
+    for (uint32_t k = tid; k < nw; k += nt) {
+        const uint32_t u = k / 32, r = k % 32, pl = r / 4, d = r % 4;
+        const uint32_t *src = (const uint32_t *)(lv + 128 * u + 32 * d);
+        uint32_t bits = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t w = src[j] >> pl;  // bit pl of byte b now at bit 8b
+            bits |= ((w & 1u) | ((w >> 7) & 2u) | ((w >> 14) & 4u) | ((w >> 21) & 8u)) << (4 * j);
+        }
+        out[k] = bits;
+    }
+}
+
+// The int8 level of a rotated query for the 1-bit prefilter: q ~= s1 * Q with
+// s1 = max|q| / 127 and Q = rint(q / s1) (the rounding of the int8 level
+// split's first level); the lane's Q into lv, and its sums of |q - s1 * Q|,
+// |q| and Q.
+template <int E>
+__device__ __forceinline__ void q1p_level(const float (&x)[E], double s1, signed char *lv, uint32_t e0, double &rs,
+                                          double &qa, int32_t &sq) {
+    const double inv = s1 > 0.0 ? 1.0 / s1 : 0.0;
+    rs = 0.0;
+    qa = 0.0;
+    sq = 0;
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+        const double xd = (double)x[t];
+        double c = rint(xd * inv);
+        c = c > 127.0 ? 127.0 : (c < -127.0 ? -127.0 : c);
+        rs += fabs(fma(-s1, c, xd));
+        qa += fabs(xd);
+        sq += (int32_t)c;
+        lv[e0 + t] = (signed char)(int)c;
+    }
+}
+
+// C_Q1P layout: bit planes (P bytes: P/128 units x 32 words), Q1Tail at
+// byte P, the fp32 query at q1p_f_off(P).
+__host__ __device__ inline size_t q1p_f_off(uint32_t P) { return ((size_t)P + sizeof(Q1Tail) + 63) & ~(size_t)63; }
+
 // Bytes of the scan's per-query layout for codec C at padded dimension P.
 __host__ __device__ inline size_t query_layout_bytes(int codec, uint32_t P) {
     switch (codec) {
@@ -1072,6 +1183,7 @@ __host__ __device__ inline size_t query_layout_bytes(int codec, uint32_t P) {
     case C_Q4M: return ((size_t)P / 16 * 12 * 4 + sizeof(QLevelTail) + 63) & ~(size_t)63;
     case C_Q4: return ((size_t)P / 32 * 24 * 4 + sizeof(QLevelTail) + 63) & ~(size_t)63;
     case C_Q1A: return (size_t)P * 4;
+    case C_Q1P: return q1p_f_off(P) + (size_t)P * 4;
     case C_HAM: return ((size_t)P / 32 * 4 + 15) & ~(size_t)15;
     case C_I8S: return ((size_t)P / 4 * 4 + 15) & ~(size_t)15;
     default: return 0;
@@ -1084,9 +1196,50 @@ __host__ __device__ inline size_t query_prep_lds(int codec, uint32_t P) {
     // (layout + xs + lv + reduction slots)
     const size_t wg = ((lay + 15) & ~(size_t)15) + 4 * (size_t)P + 3 * (size_t)P + 12 * 8 + 12 * 4;
     if (codec == C_Q8 || codec == C_Q4) return wg;
-    if (codec == C_Q1A) return wg;
+    if (codec == C_Q1A || codec == C_Q1P) return wg;
     if (codec == C_HAM || codec == C_I8S) return lay + 5 * (size_t)P;
     return lay;
+}
+
+// The C_Q1P layout of one rotated query per workgroup of one wave (E = P/64
+// elements per lane): bit planes, Q1Tail and the fp32 query.
+template <int E>
+__global__ __launch_bounds__(64) void query_q1p(LevelArgs a) {
+    extern __shared__ unsigned char lsm[];  // P bytes: the int8 level
+    const uint32_t P = a.P, qi = blockIdx.x;
+    const int lane = threadIdx.x;
+    const uint32_t e0 = (uint32_t)lane * E;
+    const float *q = a.qrot + (uint64_t)qi * P;
+    unsigned char *out = a.out + (uint64_t)qi * a.stride;
+    float *qf = (float *)(out + q1p_f_off(P));
+    float x[E];
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+        x[t] = q[e0 + t];
+        qf[e0 + t] = x[t];
+    }
+    double m = 0.0;
+#pragma unroll
+    for (int t = 0; t < E; ++t) m = fmax(m, fabs((double)x[t]));
+    m = wave_fmax_f64(m);
+    const double s1 = m > 0.0 ? m / 127.0 : 0.0;
+    double rs, qa;
+    int32_t sq;
+    q1p_level<E>(x, s1, (signed char *)lsm, e0, rs, qa, sq);
+    rs = wave_sum_f64(rs);
+    qa = wave_sum_f64(qa);
+    sq = wave_sum_i32(sq);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    q1p_planes((const signed char *)lsm, P, (uint32_t *)out, (uint32_t)lane, 64);
+    if (lane == 0) {
+        Q1Tail *tl = (Q1Tail *)(out + P);
+        tl->s1 = s1;
+        tl->rsum = rs;
+        tl->qabs = qa;
+        tl->sumq = sq;
+        tl->pad = 0;
+    }
 }
 
 // The query transform of the quantized scans, done by one wave of every
@@ -1122,12 +1275,15 @@ __device__ __forceinline__ void prep_query_e(const ScanArgs &a, RotIn<E> &in, un
 // count (LPR * UPL units), with at most 16 elements per lane so the
 // transform's registers stay below the scan loop's.
 template <int C> struct UnitCodes {
-    static constexpr int v = (C == C_Q8 || C == C_I8S) ? 16 : (C == C_Q4 || C == C_Q1A) ? 32 : (C == C_HAM) ? 128 : 0;
+    static constexpr int v = (C == C_Q8 || C == C_I8S) ? 16 : (C == C_Q4 || C == C_Q1A) ? 32
+                             : (C == C_HAM || C == C_Q1P) ? 128 : 0;
 };
 template <int C, int LPR, int UPL> struct PrepShape {
     static constexpr int P = UnitCodes<C>::v * LPR * UPL;
     static constexpr int E = P >= 64 ? P / 64 : 1;
-    static constexpr bool ok = UnitCodes<C>::v > 0 && P >= 64 && E <= 16;
+    // (the bit-plane layout is built only by the workgroup-wide transform)
+    static constexpr bool ok = UnitCodes<C>::v > 0 && P >= 64 && E <= 16 &&
+                               (C != C_Q1P || P == 256 || P == 512 || P == 1024);
 };
 
 // The same transform spread over the 4 waves of a workgroup, for the
@@ -1219,6 +1375,45 @@ __device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in
 #pragma unroll
         for (int t = 0; t < EP; ++t) f[e0 + t] = x[t];
         return;
+    } else if constexpr (C == C_Q1P) {
+        // the fp32 query stays in LDS (at qf_off) for the scan's exact
+        // re-score; the int8 level goes to bit planes + Q1Tail at lds
+        float *qf = (float *)(lds + a.qf_off);
+#pragma unroll
+        for (int t = 0; t < EP; ++t) qf[e0 + t] = x[t];
+        signed char *lv = (signed char *)(xs + P);
+        double *red = (double *)(lv + P);       // [3][4]: max, sum |r|, sum |q|
+        int32_t *reds = (int32_t *)(red + 12);  // [4]: sum Q
+        double m = 0.0;
+#pragma unroll
+        for (int t = 0; t < EP; ++t) m = fmax(m, fabs((double)x[t]));
+        m = wave_fmax_f64(m);
+        if (lane == 0) red[wave] = m;
+        __syncthreads();
+        m = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
+        const double s1 = m > 0.0 ? m / 127.0 : 0.0;
+        double rs, qa;
+        int32_t sq;
+        q1p_level<EP>(x, s1, lv, e0, rs, qa, sq);
+        rs = wave_sum_f64(rs);
+        qa = wave_sum_f64(qa);
+        sq = wave_sum_i32(sq);
+        if (lane == 0) {
+            red[4 + wave] = rs;
+            red[8 + wave] = qa;
+            reds[wave] = sq;
+        }
+        __syncthreads();
+        q1p_planes(lv, P, (uint32_t *)lds, (uint32_t)tid, SCAN_WG);
+        if (tid == 0) {
+            Q1Tail *tl = (Q1Tail *)(lds + P);
+            tl->s1 = s1;
+            tl->rsum = ((red[4] + red[5]) + red[6]) + red[7];
+            tl->qabs = ((red[8] + red[9]) + red[10]) + red[11];
+            tl->sumq = reds[0] + reds[1] + reds[2] + reds[3];
+            tl->pad = 0;
+        }
+        return;
     } else {
         signed char *lv = (signed char *)(xs + P);
         double *redm = (double *)(lv + 3 * (size_t)P);  // [3][4]
@@ -1291,7 +1486,7 @@ __device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in
 // int4 / 1-bit asym at P = 256, 512, 1024, else the one-wave one.
 template <int C, int LPR, int UPL> struct PrepWG {
     static constexpr int P = UnitCodes<C>::v * LPR * UPL;
-    static constexpr bool ok = (C == C_Q8 || C == C_Q4 || C == C_Q1A) && (P == 256 || P == 512 || P == 1024);
+    static constexpr bool ok = (C == C_Q8 || C == C_Q4 || C == C_Q1A || C == C_Q1P) && (P == 256 || P == 512 || P == 1024);
     static constexpr int EP = ok ? P / 256 : 1;
 };
 
@@ -1423,6 +1618,7 @@ template <int C, int UPL> struct ScanRegs {
     bool uok[UPL];
     uint32_t ucl[UPL];
     Fin<C> fin;
+    const float *qf;  // C_Q1P: the fp32 query in LDS
 };
 
 // Rows are split across LPR lanes (each lane loads UPL 16-byte or 4-byte units
@@ -1497,9 +1693,9 @@ __device__ __forceinline__ void load_step(const ScanArgs &a, const ScanRegs<C, U
 // Scores a loaded step: pushes keys >= tau to the wave's list and folds
 // every eligible key into the lane's running maximum.
 template <int C, int LPR, int UPL>
-__device__ __forceinline__ void compute_step(const ScanArgs &a, const ScanRegs<C, UPL> &R,
-                                             const StepData<C, LPR, UPL> &S, uint32_t base, uint32_t lim,
-                                             uint64_t tau, uint64_t *wk, uint32_t &wc, uint64_t &lmax, int lane) {
+__device__ __forceinline__ void compute_step_gen(const ScanArgs &a, const ScanRegs<C, UPL> &R,
+                                                 const StepData<C, LPR, UPL> &S, uint32_t base, uint32_t lim,
+                                                 uint64_t tau, uint64_t *wk, uint32_t &wc, uint64_t &lmax, int lane) {
     using CD = Codec<C>;
     using Acc = typename CD::Acc;
     using SH = ScanShape<C, LPR, UPL>;
@@ -1536,7 +1732,120 @@ __device__ __forceinline__ void compute_step(const ScanArgs &a, const ScanRegs<C
     wave_push(wk, wc, take, key);
 }
 
-// Publishes the wave's running maximum to wmax[slot] when it grew.
+// C_Q1P: every row is scored through the int8 level's bit planes, an exact
+// integer T = sum over set code bits of Q.  A step in which some row's
+// bound on its exact score reaches the wave's bound is re-scored exactly
+// (the fp32 sum of +-q over the row's codes: each lane adds its units'
+// codes in order, then the transposing reduction; times the row scale), and
+// only exactly scored rows enter the list, so the keys are those of the
+// exact arithmetic.  Bound: the exact real sum is s1 * (2T - sum Q) + e with
+// |e| <= sum |q - s1 Q|, and the fp32 sum differs from it by at most 4e-5 *
+// sum |q| (up to 512 terms); the f64 bound takes a further 1e-6 margin.
+// The next float below a finite x (bit steps; +-0 go to the negative
+// smallest subnormal).
+__device__ __forceinline__ float float_below(float x) {
+    const uint32_t b = __float_as_uint(x);
+    if ((b & 0x7fffffffu) == 0) return __uint_as_float(0x80000001u);
+    return __uint_as_float((b & 0x80000000u) ? b + 1 : b - 1);
+}
+
+template <int LPR, int UPL>
+__device__ __forceinline__ void compute_step_q1p(const ScanArgs &a, const ScanRegs<C_Q1P, UPL> &R,
+                                                 const StepData<C_Q1P, LPR, UPL> &S, uint32_t base, uint32_t lim,
+                                                 uint64_t tau, uint64_t *wk, uint32_t &wc, uint64_t &lmax, int lane) {
+    using CD = Codec<C_Q1P>;
+    using SH = ScanShape<C_Q1P, LPR, UPL>;
+    constexpr int U = SH::U, G = SH::G;
+    int32_t acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        int32_t a1[1] = {0};
+#pragma unroll
+        for (int t = 0; t < UPL; ++t) CD::acc(S.d[u][t], R.qr[t], a1);  // (overhanging units: zero planes)
+        acc[u] = a1[0];
+    }
+    const int32_t T = xreduce<U, LPR>(acc, lane);
+    const uint32_t myrow = base + (uint32_t)(xrow<U, LPR>(lane) * G + lane / LPR);
+    const bool row_ok = xrep<U, LPR>(lane) && myrow < lim;
+    const float scale = S.scale * a.scale_mul;
+    const double hi =
+        (double)scale * (R.fin.s1 * (double)(2 * T - R.fin.sumq) + R.fin.rsum + 4e-5 * R.fin.qabs);
+    const double bound = hi + fabs(hi) * 1e-6;
+    const double tau_sc = (double)f32_from_ord((uint32_t)(tau >> 32));
+    const bool need = row_ok && (a.dense_out != nullptr || tau == 0 || !(bound < tau_sc));
+    bool pass = true;
+    if (a.mask && row_ok) pass = S.grow < a.mask_bits && ((a.mask[S.grow >> 5] >> (S.grow & 31)) & 1u);
+    // Every eligible row raises the wave's maximum by a lower bound of its
+    // exact key (rounded down), so the shared bound rises from the first
+    // steps on without waiting for exact re-scores: the kprime-th best of the
+    // published maxima is still at most the kprime-th best exact key.
+    if (row_ok && pass) {
+        double lo = (double)scale * (R.fin.s1 * (double)(2 * T - R.fin.sumq) - R.fin.rsum - 4e-5 * R.fin.qabs);
+        lo -= fabs(lo) * 1e-6;
+        if (lo == lo) {  // (not NaN)
+            float lf = (float)lo;
+            if ((double)lf > lo) lf = float_below(lf);
+            const uint64_t klo = make_key(ord_f32(lf), S.grow);
+            lmax = klo > lmax ? klo : lmax;
+        }
+    }
+    bool take = false;
+    uint64_t key = 0;
+    if (__ballot(need) != 0) {
+        // re-score only the row groups (u) that hold a row in need: after
+        // the transposing reduction lane l holds a row of group xrow(l)
+        const int xr = xrow<U, LPR>(lane);
+        const int pl = lane % LPR;
+        float ex[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float e = 0.0f;
+            if (__ballot(need && xr == u) == 0) {
+                ex[u] = e;
+                continue;
+            }
+#pragma unroll
+            for (int t = 0; t < UPL; ++t) {
+                if (!R.uok[t]) continue;
+                const float4 *q4 = (const float4 *)(R.qf + (size_t)(pl + LPR * t) * 128);
+                const uint32_t w[4] = {S.d[u][t].x, S.d[u][t].y, S.d[u][t].z, S.d[u][t].w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        const float4 qv = q4[d * 8 + c];
+                        const uint32_t b = w[d] >> (4 * c);
+                        e += (b & 1u) ? qv.x : -qv.x;
+                        e += (b & 2u) ? qv.y : -qv.y;
+                        e += (b & 4u) ? qv.z : -qv.z;
+                        e += (b & 8u) ? qv.w : -qv.w;
+                    }
+                }
+            }
+            ex[u] = e;
+        }
+        const float tot = xreduce<U, LPR>(ex, lane);
+        if (need) {
+            const float sc = tot * scale;
+            if (a.dense_out && blockIdx.y == 0) a.dense_out[myrow] = sc;
+            if (pass) {
+                key = make_key(ord_f32(sc), S.grow);
+                take = key >= tau;
+                lmax = key > lmax ? key : lmax;
+            }
+        }
+    }
+    wave_push(wk, wc, take, key);
+}
+
+template <int C, int LPR, int UPL>
+__device__ __forceinline__ void compute_step(const ScanArgs &a, const ScanRegs<C, UPL> &R,
+                                             const StepData<C, LPR, UPL> &S, uint32_t base, uint32_t lim,
+                                             uint64_t tau, uint64_t *wk, uint32_t &wc, uint64_t &lmax, int lane) {
+    if constexpr (C == C_Q1P) compute_step_q1p<LPR, UPL>(a, R, S, base, lim, tau, wk, wc, lmax, lane);
+    else compute_step_gen<C, LPR, UPL>(a, R, S, base, lim, tau, wk, wc, lmax, lane);
+}
+
 // Publishes the wave's running maximum to wmax[slot] on every call, from
 // every lane (one line, one value): the scan loop issues the same memory
 // operations whatever the data, so that its waits stay exact.
@@ -1830,6 +2139,16 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         R.fin.load((const char *)qb + (uint64_t)a.units * CD::QN * sizeof(QT), a.padded_dim);
     };
     if (!prep) read_query((const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride));
+    if constexpr (C == C_Q1P) {
+        // the fp32 query of the exact re-score, in LDS behind everything else
+        R.qf = (const float *)(scan_smem + a.qf_off);
+        if (!prep) {
+            const float *src = (const float *)((const char *)a.q + (uint64_t)qi * a.q_stride + q1p_f_off(a.padded_dim));
+            float *dst = (float *)(scan_smem + a.qf_off);
+            for (uint32_t i = (uint32_t)tid; i < a.padded_dim; i += SCAN_WG) dst[i] = src[i];
+            __syncthreads();
+        }
+    }
     // The fp32 query of the exact re-rank, read here too (dims up to 64 * RQ;
     // lane l holds elements l + 64k) and staged as doubles behind the wave's
     // list once the LDS is free, so the flush at the end of the scan starts
@@ -1889,7 +2208,9 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             // line that every wave of the grid reads) or else the wave's own
             // slot
             publish_wave_max(wslot, lmax);
-            polled = (pi + (uint32_t)wave) % TAU_POLL == 0;
+            // (the bit-plane scan polls every pass until a bound exists: its
+            // rows go through the exact re-score until then)
+            polled = (C == C_Q1P && tau == 0) || (pi + (uint32_t)wave) % TAU_POLL == 0;
             gt = __hip_atomic_load(polled ? (const uint64_t *)&qs->tau : (const uint64_t *)wslot, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             const bool nb = na && next_step(bb, bl);
@@ -2260,10 +2581,19 @@ hipError_t go(const ScanArgs &a, uint32_t nq, hipStream_t s) {
         const size_t need = (query_prep_lds(C, a.padded_dim) + 15) & ~(size_t)15;
         if (lds < need) lds = need;
     }
+    ScanArgs b = a;
+    if constexpr (C == C_Q1P) {
+        // the fp32 query for the exact re-score, behind the lists and the
+        // transform's scratch
+        lds = (lds + 15) & ~(size_t)15;
+        b.qf_off = (uint32_t)lds;
+        lds += (size_t)a.padded_dim * 4;
+    }
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
     if (a.cand)
-        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, true>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, a);
+        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, true>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, b);
     else
-        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, false>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, a);
+        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, false>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, b);
     return hipGetLastError();
 }
 
@@ -2308,6 +2638,7 @@ hipError_t scan_codec_f32l2(int lpr, int upl, const ScanArgs &a, uint32_t nq, hi
 hipError_t scan_codec_q8(int lpr, int upl, const ScanArgs &a, uint32_t nq, hipStream_t s);
 hipError_t scan_codec_q4(int lpr, int upl, const ScanArgs &a, uint32_t nq, hipStream_t s);
 hipError_t scan_codec_q1a(int lpr, int upl, const ScanArgs &a, uint32_t nq, hipStream_t s);
+hipError_t scan_codec_q1p(int lpr, int upl, const ScanArgs &a, uint32_t nq, hipStream_t s);
 hipError_t scan_codec_ham(int lpr, int upl, const ScanArgs &a, uint32_t nq, hipStream_t s);
 hipError_t scan_codec_i8s(int lpr, int upl, const ScanArgs &a, uint32_t nq, hipStream_t s);
 hipError_t scan_codec_f32dot_s(int lpr, int upl, const ScanArgs &a, uint32_t nq, hipStream_t s);

@@ -76,8 +76,12 @@ def test_encode_seed_and_rounds(ctx):
         idx.destroy()
 
 
+# 1-bit asym covers every layout path of the bit-plane scan: P = 128 (one
+# unit, query layout built by its own kernel), 512 and 1024 (built inside the
+# scan), 2048 (own kernel, 16 lanes per row); P = 64 keeps the plain fp32 sum
 SCAN_CASES = [(768, 8, "asym"), (384, 8, "asym"), (768, 4, "asym"), (1024, 4, "asym"), (768, 1, "asym"),
-              (1024, 1, "asym"), (1024, 1, "hamming"), (768, 8, "int8sym"), (2048, 8, "asym")]
+              (1024, 1, "asym"), (100, 1, "asym"), (400, 1, "asym"), (2000, 1, "asym"), (48, 1, "asym"),
+              (1024, 1, "hamming"), (768, 8, "int8sym"), (2048, 8, "asym")]
 
 
 @pytest.mark.parametrize("dim,bits,scorer", SCAN_CASES)
@@ -243,7 +247,7 @@ def test_masked_queries(ctx):
     words = np.zeros((n + 31) // 32, np.uint32)
     for r in np.nonzero(keep)[0]:
         words[r >> 5] |= np.uint32(1 << (r & 31))
-    for idx in (FlatIndex(ctx, dim, "cosine"), QuantIndex(ctx, dim, bits=8)):
+    for idx in (FlatIndex(ctx, dim, "cosine"), QuantIndex(ctx, dim, bits=8), QuantIndex(ctx, dim, bits=1)):
         idx.append(data, n)
         q = gaussian(1, dim, 32)[0]
         dense = idx.export_scores(q)
@@ -296,13 +300,14 @@ def test_edge_cases(ctx):
         i.destroy()
 
 
-def test_batch_equals_singles(ctx):
+@pytest.mark.parametrize("bits", [8, 1])
+def test_batch_equals_singles(ctx, bits):
     from browservec_amd import QuantIndex
 
-    say("batch")
+    say("batch", bits)
     dim = 256
     data = gaussian(4000, dim, 41)
-    idx = QuantIndex(ctx, dim, bits=8)
+    idx = QuantIndex(ctx, dim, bits=bits)
     idx.append(data, 4000)
     qs = gaussian(70, dim, 42)
     batch = idx.query_batch(qs, 70, 15)
