@@ -35,14 +35,16 @@ struct QLevelTail {
     int32_t pad;
 };
 
-// Tail of the 1-bit asymmetric bit-plane layout: the query's int8 level
-// (q ~= s1 * Q), sum |q - s1 * Q|, sum |q| and sum Q.
+// Tail of the 1-bit asymmetric bit-plane layout: the query's two levels
+// (q ~= s1 * Q1 + s2 * Q2, Q1 int8, Q2 int4), sum |q - s1 Q1 - s2 Q2|,
+// sum |q|, sum Q1 and sum Q2.
 struct Q1Tail {
     double s1;
+    double s2;
     double rsum;
     double qabs;
-    int32_t sumq;
-    int32_t pad;
+    int32_t sumq1;
+    int32_t sumq2;
 };
 
 }  // namespace bvk

@@ -18,9 +18,9 @@ enum CodecId : int {
     C_I8S = 6,      // int8 codes x int8 query         (16-byte units)
     C_F32DOT_S = 7, // fp32 rows, dim % 4 != 0         (4-byte units = 1 float)
     C_F32L2_S = 8,
-    C_Q1P = 9,      // 1-bit codes, asymmetric, scored through the query's int8
-                    // bit planes with an exact fp32 re-score near the bound
-                    // (16-byte units = 128 codes)
+    C_Q1P = 9,      // 1-bit codes, asymmetric, scored through the query's int8 +
+                    // int4 bit planes with an exact fp32 re-score near the
+                    // bound (16-byte units = 128 codes)
     C_COUNT = 10,
     // query-level layout only (not a scan codec): int4 levels (no 1/127 scale)
     // in the int8 16-code unit layout, for the batched matrix-core scan

@@ -94,7 +94,7 @@ bool scan_supported(int codec, uint32_t units) {
     Layout L;
     if (!pick_layout(units, L)) return false;
     // register budget: at most 64 query values per lane
-    static const int qn[C_COUNT] = {4, 4, 12, 24, 32, 4, 4, 1, 1, 32};
+    static const int qn[C_COUNT] = {4, 4, 12, 24, 32, 4, 4, 1, 1, Codec<C_Q1P>::QN};
     return codec >= 0 && codec < C_COUNT && L.upl * qn[codec] <= 64;
 }
 
@@ -157,7 +157,7 @@ size_t level_stride(int codec, uint32_t P) { return query_layout_bytes(codec, P)
 
 hipError_t launch_q1p_layout(const LevelArgs &a, uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
-    const size_t lds = a.P;
+    const size_t lds = 2 * (size_t)a.P;
     switch (a.P / 64) {
     case 2: hipLaunchKernelGGL(query_q1p<2>, dim3(nq), dim3(64), lds, s, a); break;
     case 4: hipLaunchKernelGGL(query_q1p<4>, dim3(nq), dim3(64), lds, s, a); break;

@@ -129,21 +129,25 @@ template <> struct Codec<C_HAM> {
         a[0] += __popc(u.x ^ q[0]) + __popc(u.y ^ q[1]) + __popc(u.z ^ q[2]) + __popc(u.w ^ q[3]);
     }
 };
-// 1-bit codes (128 per unit) against the query's int8 level Q held as bit
-// planes: q[p*4 + d] is bit p of Q for the 32 codes of code dword d (two's
-// complement, so plane 7 weighs -128).  The sum over the unit of
-// code_bit * Q is sum_p weight_p * popcount(code & plane_p), exact in int32.
+// 1-bit codes (128 per unit) against the query's two levels held as bit
+// planes: q[p*4 + d] is bit p of the int8 level Q1 for the 32 codes of code
+// dword d (p < 8), q[32 + p*4 + d] bit p of the int4 level Q2 (p < 4); both
+// two's complement, so the top plane weighs -128 / -8.  The sums over the
+// unit of code_bit * Q are sum_p weight_p * popcount(code & plane_p), exact
+// in int32.
+constexpr bool Q1P_L2 = false;  // the int4 residual level (else Q2 = 0; measured slower once the exact re-score is table-driven)
 template <> struct Codec<C_Q1P> {
     using Unit = uint4; using QT = uint32_t; using Acc = int32_t;
-    static constexpr int QN = 32, NA = 1;
+    static constexpr int QN = Q1P_L2 ? 48 : 32, NA = 2;
     static __device__ __forceinline__ void acc(Unit u, const QT *q, Acc *a) {
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-        for (int pl = 0; pl < 8; ++pl) {
+        for (int pl = 0; pl < QN / 4; ++pl) {
             int32_t c = 0;
 #pragma unroll
             for (int d = 0; d < 4; ++d) c += (int32_t)__popc(w[d] & q[pl * 4 + d]);
-            a[0] += pl == 7 ? -(c << 7) : (c << pl);
+            if (pl < 8) a[0] += pl == 7 ? -(c << 7) : (c << pl);
+            else a[1] += pl == 11 ? -(c << 3) : (c << (pl - 8));
         }
     }
 };
@@ -186,14 +190,16 @@ template <> struct Fin<C_HAM> {
 // The int8 level of the 1-bit asymmetric prefilter (the scan's exact
 // re-score uses the fp32 query; score() is not used).
 template <> struct Fin<C_Q1P> {
-    double s1, rsum, qabs;
-    int32_t sumq;
+    double s1, s2, rsum, qabs;
+    int32_t sumq1, sumq2;
     __device__ void load(const void *tail, uint32_t) {
         const Q1Tail *q = (const Q1Tail *)tail;
         s1 = q->s1;
+        s2 = q->s2;
         rsum = q->rsum;
         qabs = q->qabs;
-        sumq = q->sumq;
+        sumq1 = q->sumq1;
+        sumq2 = q->sumq2;
     }
 };
 template <> struct Fin<C_I8S> {
@@ -1130,51 +1136,87 @@ __global__ __launch_bounds__(64) void query_levels(LevelArgs a) {
     levels_wave<E>(x, P, a.codec, (signed char *)lsm, a.out + (uint64_t)qi * a.stride, lane);
 }
 
-// C_Q1P bit planes from the query's int8 level Q (P signed bytes at lv):
-// word u*32 + pl*4 + d holds bit pl of Q for codes 128u + 32d .. +31 (bit b
-// = code 128u + 32d + b).  Threads tid, tid + nt, .. build one word each.
+// C_Q1P bit planes from the query's levels (Q1 in lv[0, P), Q2 in lv[P, 2P),
+// signed bytes): word u*48 + p*4 + d holds bit p of Q1 (p < 8) or bit p - 8
+// of Q2 (p >= 8) for codes 128u + 32d .. +31 (bit b = code 128u + 32d + b).
+// Threads tid, tid + nt, .. build one word each.
 __device__ __forceinline__ void q1p_planes(const signed char *lv, uint32_t P, uint32_t *out, uint32_t tid,
                                            uint32_t nt) {
-    const uint32_t nw = P / 4;
+    constexpr uint32_t W = Codec<C_Q1P>::QN;  // words per unit
+    const uint32_t nw = P / 128 * W;
     for (uint32_t k = tid; k < nw; k += nt) {
-        const uint32_t u = k / 32, r = k % 32, pl = r / 4, d = r % 4;
-        const uint32_t *src = (const uint32_t *)(lv + 128 * u + 32 * d);
+        const uint32_t u = k / W, r = k % W, pl = r / 4, d = r % 4;
+        const signed char *lq = pl < 8 ? lv : lv + P;
+        const uint32_t sh = pl < 8 ? pl : pl - 8;
+        const uint32_t *src = (const uint32_t *)(lq + 128 * u + 32 * d);
         uint32_t bits = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const uint32_t w = src[j] >> pl;  // bit pl of byte b now at bit 8b
+            const uint32_t w = src[j] >> sh;  // bit sh of byte b now at bit 8b
             bits |= ((w & 1u) | ((w >> 7) & 2u) | ((w >> 14) & 4u) | ((w >> 21) & 8u)) << (4 * j);
         }
         out[k] = bits;
     }
 }
 
-// The int8 level of a rotated query for the 1-bit prefilter: q ~= s1 * Q with
-// s1 = max|q| / 127 and Q = rint(q / s1) (the rounding of the int8 level
-// split's first level); the lane's Q into lv, and its sums of |q - s1 * Q|,
-// |q| and Q.
+// The levels of a rotated query for the 1-bit prefilter: q ~= s1 * Q1 +
+// s2 * Q2 with s1 = max|q| / 127, Q1 = rint(q / s1) (the rounding of the
+// int8 level split's first level), s2 = s1 / 14 and Q2 = rint(r1 / s2) of
+// the residual r1 = q - s1 * Q1 (|r1| <= s1 / 2, so |Q2| <= 7).  The lane's
+// Q1 / Q2 go to lv[e] / lv[P + e]; it returns its sums of |q - s1 Q1 - s2 Q2|,
+// |q|, Q1 and Q2.
 template <int E>
-__device__ __forceinline__ void q1p_level(const float (&x)[E], double s1, signed char *lv, uint32_t e0, double &rs,
-                                          double &qa, int32_t &sq) {
+__device__ __forceinline__ void q1p_level(const float (&x)[E], double s1, uint32_t P, signed char *lv, uint32_t e0,
+                                          double &rs, double &qa, int32_t &sq1, int32_t &sq2) {
     const double inv = s1 > 0.0 ? 1.0 / s1 : 0.0;
+    const double s2 = s1 / 14.0, inv2 = s1 > 0.0 ? 14.0 / s1 : 0.0;
     rs = 0.0;
     qa = 0.0;
-    sq = 0;
+    sq1 = 0;
+    sq2 = 0;
 #pragma unroll
     for (int t = 0; t < E; ++t) {
         const double xd = (double)x[t];
         double c = rint(xd * inv);
         c = c > 127.0 ? 127.0 : (c < -127.0 ? -127.0 : c);
-        rs += fabs(fma(-s1, c, xd));
+        const double r1 = fma(-s1, c, xd);
+        double c2 = Q1P_L2 ? rint(r1 * inv2) : 0.0;
+        c2 = c2 > 7.0 ? 7.0 : (c2 < -7.0 ? -7.0 : c2);
+        rs += fabs(fma(-s2, c2, r1));
         qa += fabs(xd);
-        sq += (int32_t)c;
+        sq1 += (int32_t)c;
+        sq2 += (int32_t)c2;
         lv[e0 + t] = (signed char)(int)c;
+        lv[P + e0 + t] = (signed char)(int)c2;
     }
 }
 
-// C_Q1P layout: bit planes (P bytes: P/128 units x 32 words), Q1Tail at
-// byte P, the fp32 query at q1p_f_off(P).
-__host__ __device__ inline size_t q1p_f_off(uint32_t P) { return ((size_t)P + sizeof(Q1Tail) + 63) & ~(size_t)63; }
+// C_Q1P layout: bit planes (P/128 units x QN words), Q1Tail behind them,
+// the fp32 query at q1p_f_off(P).
+__host__ __device__ inline size_t q1p_tail_off(uint32_t P) { return (size_t)P / 128 * Codec<C_Q1P>::QN * 4; }
+__host__ __device__ inline size_t q1p_f_off(uint32_t P) { return (q1p_tail_off(P) + sizeof(Q1Tail) + 63) & ~(size_t)63; }
+
+// The exact re-score table of the C_Q1P scan (LDS): for every 4-code nibble
+// j of the query (codes 4j .. 4j+3) 16 fp32 entries, entry n =
+// ((s0 q0 + s1 q1) + s2 q2) + s3 q3 with s_k = +1 if bit k of n is set, else
+// -1.  Unit u's 32 nibbles start at u * Q1P_LUT_UNIT floats (the 16-float
+// pad spreads the units of a wave over the LDS banks).
+constexpr uint32_t Q1P_LUT_UNIT = 32 * 16 + 16;
+__host__ __device__ inline size_t q1p_lut_bytes(uint32_t P) { return (size_t)(P / 128) * Q1P_LUT_UNIT * 4; }
+// Builds the entries of nibbles j = tid, tid + nt, .. < P/4 from the fp32
+// query q (4 consecutive floats per nibble).
+__device__ __forceinline__ void q1p_lut_build(const float *q, uint32_t P, float *lut, uint32_t tid, uint32_t nt) {
+#pragma clang fp contract(off)
+    for (uint32_t j = tid; j < P / 4; j += nt) {
+        const float q0 = q[4 * j], q1 = q[4 * j + 1], q2 = q[4 * j + 2], q3 = q[4 * j + 3];
+        float *row = lut + (j / 32) * Q1P_LUT_UNIT + (j % 32) * 16;
+#pragma unroll
+        for (int n = 0; n < 16; ++n) {
+            const float a = (n & 1) ? q0 : -q0, b = (n & 2) ? q1 : -q1, c = (n & 4) ? q2 : -q2, d = (n & 8) ? q3 : -q3;
+            row[n] = ((a + b) + c) + d;
+        }
+    }
+}
 
 // Bytes of the scan's per-query layout for codec C at padded dimension P.
 __host__ __device__ inline size_t query_layout_bytes(int codec, uint32_t P) {
@@ -1205,7 +1247,7 @@ __host__ __device__ inline size_t query_prep_lds(int codec, uint32_t P) {
 // elements per lane): bit planes, Q1Tail and the fp32 query.
 template <int E>
 __global__ __launch_bounds__(64) void query_q1p(LevelArgs a) {
-    extern __shared__ unsigned char lsm[];  // P bytes: the int8 level
+    extern __shared__ unsigned char lsm[];  // 2P bytes: the two levels
     const uint32_t P = a.P, qi = blockIdx.x;
     const int lane = threadIdx.x;
     const uint32_t e0 = (uint32_t)lane * E;
@@ -1224,21 +1266,23 @@ __global__ __launch_bounds__(64) void query_q1p(LevelArgs a) {
     m = wave_fmax_f64(m);
     const double s1 = m > 0.0 ? m / 127.0 : 0.0;
     double rs, qa;
-    int32_t sq;
-    q1p_level<E>(x, s1, (signed char *)lsm, e0, rs, qa, sq);
+    int32_t sq1, sq2;
+    q1p_level<E>(x, s1, P, (signed char *)lsm, e0, rs, qa, sq1, sq2);
     rs = wave_sum_f64(rs);
     qa = wave_sum_f64(qa);
-    sq = wave_sum_i32(sq);
+    sq1 = wave_sum_i32(sq1);
+    sq2 = wave_sum_i32(sq2);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     q1p_planes((const signed char *)lsm, P, (uint32_t *)out, (uint32_t)lane, 64);
     if (lane == 0) {
-        Q1Tail *tl = (Q1Tail *)(out + P);
+        Q1Tail *tl = (Q1Tail *)(out + q1p_tail_off(P));
         tl->s1 = s1;
+        tl->s2 = Q1P_L2 ? s1 / 14.0 : 0.0;
         tl->rsum = rs;
         tl->qabs = qa;
-        tl->sumq = sq;
-        tl->pad = 0;
+        tl->sumq1 = sq1;
+        tl->sumq2 = sq2;
     }
 }
 
@@ -1376,14 +1420,13 @@ __device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in
         for (int t = 0; t < EP; ++t) f[e0 + t] = x[t];
         return;
     } else if constexpr (C == C_Q1P) {
-        // the fp32 query stays in LDS (at qf_off) for the scan's exact
-        // re-score; the int8 level goes to bit planes + Q1Tail at lds
-        float *qf = (float *)(lds + a.qf_off);
+        // the rotated query in xs for the exact re-score table (at qf_off);
+        // the levels go to bit planes + Q1Tail at lds
 #pragma unroll
-        for (int t = 0; t < EP; ++t) qf[e0 + t] = x[t];
-        signed char *lv = (signed char *)(xs + P);
-        double *red = (double *)(lv + P);       // [3][4]: max, sum |r|, sum |q|
-        int32_t *reds = (int32_t *)(red + 12);  // [4]: sum Q
+        for (int t = 0; t < EP; ++t) xs[e0 + t] = x[t];
+        signed char *lv = (signed char *)(xs + P);  // Q1, then Q2
+        double *red = (double *)(lv + 2 * P);   // [3][4]: max, sum |r|, sum |q|
+        int32_t *reds = (int32_t *)(red + 12);  // [2][4]: sum Q1, sum Q2
         double m = 0.0;
 #pragma unroll
         for (int t = 0; t < EP; ++t) m = fmax(m, fabs((double)x[t]));
@@ -1393,25 +1436,29 @@ __device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in
         m = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
         const double s1 = m > 0.0 ? m / 127.0 : 0.0;
         double rs, qa;
-        int32_t sq;
-        q1p_level<EP>(x, s1, lv, e0, rs, qa, sq);
+        int32_t sq1, sq2;
+        q1p_level<EP>(x, s1, P, lv, e0, rs, qa, sq1, sq2);
         rs = wave_sum_f64(rs);
         qa = wave_sum_f64(qa);
-        sq = wave_sum_i32(sq);
+        sq1 = wave_sum_i32(sq1);
+        sq2 = wave_sum_i32(sq2);
         if (lane == 0) {
             red[4 + wave] = rs;
             red[8 + wave] = qa;
-            reds[wave] = sq;
+            reds[wave] = sq1;
+            reds[4 + wave] = sq2;
         }
         __syncthreads();
         q1p_planes(lv, P, (uint32_t *)lds, (uint32_t)tid, SCAN_WG);
+        q1p_lut_build(xs, P, (float *)(lds + a.qf_off), (uint32_t)tid, SCAN_WG);
         if (tid == 0) {
-            Q1Tail *tl = (Q1Tail *)(lds + P);
+            Q1Tail *tl = (Q1Tail *)(lds + q1p_tail_off(P));
             tl->s1 = s1;
+            tl->s2 = Q1P_L2 ? s1 / 14.0 : 0.0;
             tl->rsum = ((red[4] + red[5]) + red[6]) + red[7];
             tl->qabs = ((red[8] + red[9]) + red[10]) + red[11];
-            tl->sumq = reds[0] + reds[1] + reds[2] + reds[3];
-            tl->pad = 0;
+            tl->sumq1 = reds[0] + reds[1] + reds[2] + reds[3];
+            tl->sumq2 = reds[4] + reds[5] + reds[6] + reds[7];
         }
         return;
     } else {
@@ -1618,7 +1665,7 @@ template <int C, int UPL> struct ScanRegs {
     bool uok[UPL];
     uint32_t ucl[UPL];
     Fin<C> fin;
-    const float *qf;  // C_Q1P: the fp32 query in LDS
+    const float *qf;  // C_Q1P: the exact re-score table in LDS
 };
 
 // Rows are split across LPR lanes (each lane loads UPL 16-byte or 4-byte units
@@ -1732,15 +1779,6 @@ __device__ __forceinline__ void compute_step_gen(const ScanArgs &a, const ScanRe
     wave_push(wk, wc, take, key);
 }
 
-// C_Q1P: every row is scored through the int8 level's bit planes, an exact
-// integer T = sum over set code bits of Q.  A step in which some row's
-// bound on its exact score reaches the wave's bound is re-scored exactly
-// (the fp32 sum of +-q over the row's codes: each lane adds its units'
-// codes in order, then the transposing reduction; times the row scale), and
-// only exactly scored rows enter the list, so the keys are those of the
-// exact arithmetic.  Bound: the exact real sum is s1 * (2T - sum Q) + e with
-// |e| <= sum |q - s1 Q|, and the fp32 sum differs from it by at most 4e-5 *
-// sum |q| (up to 512 terms); the f64 bound takes a further 1e-6 margin.
 // The next float below a finite x (bit steps; +-0 go to the negative
 // smallest subnormal).
 __device__ __forceinline__ float float_below(float x) {
@@ -1749,6 +1787,17 @@ __device__ __forceinline__ float float_below(float x) {
     return __uint_as_float((b & 0x80000000u) ? b + 1 : b - 1);
 }
 
+// C_Q1P: every row is scored through the levels' bit planes, exact integers
+// T1, T2 = sums of Q1, Q2 over the row's set code bits.  A row group in
+// which some row's bound on its exact score reaches the wave's bound is
+// re-scored exactly, and only exactly scored rows enter the list, so the
+// keys are those of the exact arithmetic: per unit the 32 nibble entries of
+// the re-score table (q1p_lut_build) added in order, the units in order,
+// then the transposing reduction, times the row scale.  Bound: the exact
+// real sum is s1 (2 T1 - sum Q1) + s2 (2 T2 - sum Q2) + e with
+// |e| <= sum |q - s1 Q1 - s2 Q2|, and the fp32 arithmetic differs from it by
+// at most 4e-5 * sum |q| (under 512 roundings); the f64 bound takes a
+// further 1e-6 margin.
 template <int LPR, int UPL>
 __device__ __forceinline__ void compute_step_q1p(const ScanArgs &a, const ScanRegs<C_Q1P, UPL> &R,
                                                  const StepData<C_Q1P, LPR, UPL> &S, uint32_t base, uint32_t lim,
@@ -1756,20 +1805,22 @@ __device__ __forceinline__ void compute_step_q1p(const ScanArgs &a, const ScanRe
     using CD = Codec<C_Q1P>;
     using SH = ScanShape<C_Q1P, LPR, UPL>;
     constexpr int U = SH::U, G = SH::G;
-    int32_t acc[U];
+    int32_t acc1[U], acc2[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        int32_t a1[1] = {0};
+        int32_t a1[2] = {0, 0};
 #pragma unroll
         for (int t = 0; t < UPL; ++t) CD::acc(S.d[u][t], R.qr[t], a1);  // (overhanging units: zero planes)
-        acc[u] = a1[0];
+        acc1[u] = a1[0];
+        acc2[u] = a1[1];
     }
-    const int32_t T = xreduce<U, LPR>(acc, lane);
+    const int32_t T1 = xreduce<U, LPR>(acc1, lane), T2 = xreduce<U, LPR>(acc2, lane);
+    // the levels' score of the row (without its scale)
+    const double lev = R.fin.s1 * (double)(2 * T1 - R.fin.sumq1) + R.fin.s2 * (double)(2 * T2 - R.fin.sumq2);
     const uint32_t myrow = base + (uint32_t)(xrow<U, LPR>(lane) * G + lane / LPR);
     const bool row_ok = xrep<U, LPR>(lane) && myrow < lim;
     const float scale = S.scale * a.scale_mul;
-    const double hi =
-        (double)scale * (R.fin.s1 * (double)(2 * T - R.fin.sumq) + R.fin.rsum + 4e-5 * R.fin.qabs);
+    const double hi = (double)scale * (lev + R.fin.rsum + 4e-5 * R.fin.qabs);
     const double bound = hi + fabs(hi) * 1e-6;
     const double tau_sc = (double)f32_from_ord((uint32_t)(tau >> 32));
     const bool need = row_ok && (a.dense_out != nullptr || tau == 0 || !(bound < tau_sc));
@@ -1780,7 +1831,7 @@ __device__ __forceinline__ void compute_step_q1p(const ScanArgs &a, const ScanRe
     // steps on without waiting for exact re-scores: the kprime-th best of the
     // published maxima is still at most the kprime-th best exact key.
     if (row_ok && pass) {
-        double lo = (double)scale * (R.fin.s1 * (double)(2 * T - R.fin.sumq) - R.fin.rsum - 4e-5 * R.fin.qabs);
+        double lo = (double)scale * (lev - R.fin.rsum - 4e-5 * R.fin.qabs);
         lo -= fabs(lo) * 1e-6;
         if (lo == lo) {  // (not NaN)
             float lf = (float)lo;
@@ -1807,19 +1858,12 @@ __device__ __forceinline__ void compute_step_q1p(const ScanArgs &a, const ScanRe
 #pragma unroll
             for (int t = 0; t < UPL; ++t) {
                 if (!R.uok[t]) continue;
-                const float4 *q4 = (const float4 *)(R.qf + (size_t)(pl + LPR * t) * 128);
+                const float *lt = R.qf + (size_t)(pl + LPR * t) * Q1P_LUT_UNIT;
                 const uint32_t w[4] = {S.d[u][t].x, S.d[u][t].y, S.d[u][t].z, S.d[u][t].w};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
 #pragma unroll
-                    for (int c = 0; c < 8; ++c) {
-                        const float4 qv = q4[d * 8 + c];
-                        const uint32_t b = w[d] >> (4 * c);
-                        e += (b & 1u) ? qv.x : -qv.x;
-                        e += (b & 2u) ? qv.y : -qv.y;
-                        e += (b & 4u) ? qv.z : -qv.z;
-                        e += (b & 8u) ? qv.w : -qv.w;
-                    }
+                    for (int c = 0; c < 8; ++c) e += lt[(d * 8 + c) * 16 + ((w[d] >> (4 * c)) & 15u)];
                 }
             }
             ex[u] = e;
@@ -2140,12 +2184,12 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     };
     if (!prep) read_query((const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride));
     if constexpr (C == C_Q1P) {
-        // the fp32 query of the exact re-score, in LDS behind everything else
+        // the exact re-score table, in LDS behind everything else (built by
+        // the query transform, or here from the prepared fp32 query)
         R.qf = (const float *)(scan_smem + a.qf_off);
         if (!prep) {
             const float *src = (const float *)((const char *)a.q + (uint64_t)qi * a.q_stride + q1p_f_off(a.padded_dim));
-            float *dst = (float *)(scan_smem + a.qf_off);
-            for (uint32_t i = (uint32_t)tid; i < a.padded_dim; i += SCAN_WG) dst[i] = src[i];
+            q1p_lut_build(src, a.padded_dim, (float *)(scan_smem + a.qf_off), (uint32_t)tid, SCAN_WG);
             __syncthreads();
         }
     }
@@ -2583,11 +2627,11 @@ hipError_t go(const ScanArgs &a, uint32_t nq, hipStream_t s) {
     }
     ScanArgs b = a;
     if constexpr (C == C_Q1P) {
-        // the fp32 query for the exact re-score, behind the lists and the
-        // transform's scratch
+        // the exact re-score table, behind the lists and the transform's
+        // scratch
         lds = (lds + 15) & ~(size_t)15;
         b.qf_off = (uint32_t)lds;
-        lds += (size_t)a.padded_dim * 4;
+        lds += q1p_lut_bytes(a.padded_dim);
     }
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     if (a.cand)
