@@ -592,7 +592,7 @@ def main():
                      "kernel": "scan_topk<C_Q8,64,1> (query rotate+levels, scan, top-100, exact re-rank)",
                      "kernel_avg_us": round(scan_avg_ms * 1e3, 2),
                      "algorithmic_bytes_per_launch": scan_bytes,
-                     "traffic_source": "profiles/scan_topk_q8_1Mx768_traffic.md" if traffic else None},
+                     "traffic_source": "profiles/scan_topk_q8_1Mx768.md" if traffic else None},
         "cpu_baseline": cpu,
         "batch256_qps": round(qps_b256, 1),
         # the batch's dense int8 work (three query levels), over the whole
