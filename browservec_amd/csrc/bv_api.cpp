@@ -604,7 +604,7 @@ extern "C" int bv_index_append_device(bv_index *idx, const float *d_data, uint64
 static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                      const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores, uint32_t *d_n);
 
-// nprobe auto-tune for targetRecall (src/index/ivfTune.ts:31-61,
+// nprobe auto-tune for targetRecall (src/index/ivfTune.ts:31-42,
 // ivfquant.ts:322-344, ivf.ts:269-291), after a build, when no nprobe is
 // configured.  For up to 32 reservoir rows spread evenly over the sample
 // (pickTuneQueries), the top k+1 of every row by the index's own scores

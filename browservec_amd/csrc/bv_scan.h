@@ -14,7 +14,7 @@
 //                  last-workgroup merge across the grid.  Replaces the
 //                  reference's distance kernels + score buffer + top-k kernel
 //                  + CPU merge (src/engine/wgsl/distance*.ts, topk.ts,
-//                  src/index/gpuTopk.ts:160-277).
+//                  src/index/gpuTopk.ts:160-189).
 //   rerank_topk    exact re-rank of the candidates with Store.dotRow's f64
 //                  arithmetic (src/store/store.ts:114-130), then the final
 //                  top-k (src/index.ts:583-594).

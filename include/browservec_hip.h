@@ -139,7 +139,7 @@ int bv_index_destroy(bv_index *idx);
 /* VectorIndex.size (flat.ts:31). */
 int bv_index_size(const bv_index *idx, uint64_t *rows);
 
-/* VectorIndex.append (flat.ts:37, quant.ts:368-380, ivfquant.ts:216-233):
+/* VectorIndex.append (flat.ts:37, quant.ts:129-140, ivfquant.ts:216-233):
  * `data` holds n_floats = count*dim prepared floats (normalized for cosine).
  * Quantized kinds rotate+quantize on the device. */
 int bv_index_append(bv_index *idx, const float *data, uint64_t n_floats, uint64_t count);
@@ -150,7 +150,7 @@ int bv_index_append(bv_index *idx, const float *data, uint64_t n_floats, uint64_
  * re-ranks, as BrowserVec.query does).  *n_out = min(k, rows). */
 int bv_index_query(bv_index *idx, const float *q, uint32_t k, uint32_t *rows, float *scores, uint32_t *n_out);
 
-/* queryMasked (flat.ts:128-130, quant.ts:413-415): rows whose bit (LSB-first,
+/* queryMasked (flat.ts:128-130, quant.ts:174-176): rows whose bit (LSB-first,
  * row r -> word r>>5) is clear never enter the top-k; *n_out may be < k. */
 int bv_index_query_masked(bv_index *idx, const float *q, uint32_t k, const uint32_t *mask_words,
                           uint64_t n_words, uint32_t *rows, float *scores, uint32_t *n_out);

@@ -320,8 +320,8 @@ EXPORT void bvo_rerank_scores(const float *rows, uint32_t dim, const float *q, c
 
 /* ------------------------------------------------------------------------ */
 /* a6-a9. Scan scores in the reference kernels' order                        */
-/* (src/engine/wgsl/distance.ts:24-44,147-191; distanceQ8.ts:247-257;        */
-/*  distanceQ4.ts:319-337; distanceQ1.ts:399-422).                           */
+/* (src/engine/wgsl/distance.ts:24-44,147-191; distanceQ8.ts:56-66;        */
+/*  distanceQ4.ts:44-62; distanceQ1.ts:44-67).                           */
 /* WGSL leaves the rounding inside dot() implementation-defined; this        */
 /* restatement fixes it as ((a0*b0 + a1*b1) + a2*b2) + a3*b3 with separate    */
 /* roundings, and accumulates acc = dot + acc in group order.                */
@@ -369,7 +369,7 @@ static inline float unpack_snorm8(uint32_t w, uint32_t j) {
 }
 
 /* int8 asymmetric scan; q is the rotated query (P floats). cand may be NULL
- * (flat) or list `rows` row ids (indexed mode, distanceQ8.ts:220-232). */
+ * (flat) or list `rows` row ids (indexed mode, distanceQ8.ts:17-40,79-84). */
 EXPORT void bvo_scan_q8(const uint32_t *codes, const float *scales, uint64_t rows, uint32_t P, const float *q,
                         const uint32_t *cand, float *out) {
     uint32_t W = P / 4;
@@ -604,7 +604,7 @@ EXPORT uint32_t bvo_topk_ref(const float *scores, uint32_t n, uint32_t k, uint32
     return len;
 }
 
-/* mergePartials (src/index/gpuTopk.ts:248-277): skips score <= -3.4e38 (f64
+/* mergePartials (src/index/gpuTopk.ts:160-189): skips score <= -3.4e38 (f64
  * compare) and row >= n, then the same selection as topK. */
 EXPORT uint32_t bvo_merge_partials(const float *scores, const uint32_t *prow, uint32_t count, uint32_t n,
                                    uint32_t k, uint32_t *rows, float *out_scores) {
@@ -813,8 +813,8 @@ EXPORT void bvo_assign_f32(const float *rows, uint32_t nrows, const float *centr
     }
 }
 
-/* Quantized assignment (assignQ8.ts:143-177, assignQ4.ts:212-249,
- * assignQ1.ts:284-325) in the reference kernels' order: the scale sits inside
+/* Quantized assignment (assignQ8.ts:29-65, assignQ4.ts:33-72,
+ * assignQ1.ts:33-76) in the reference kernels' order: the scale sits inside
  * the loop for int8/int4, after it for 1-bit. */
 EXPORT void bvo_assign_quant(const uint32_t *codes, const float *scales, uint32_t nrows, uint32_t P, uint32_t bits,
                              const float *centroids, uint32_t nlist, uint32_t *out) {

@@ -378,7 +378,7 @@ def topk_ref(scores, k: int):
 
 
 def merge_partials(scores, rows, n: int, k: int):
-    """mergePartials (src/index/gpuTopk.ts:248-277)."""
+    """mergePartials (src/index/gpuTopk.ts:160-189)."""
     scores, rows = _f32(scores), _u32(rows)
     m = max(min(k, n), 1)
     r = np.empty(m, dtype=np.uint32); s = np.empty(m, dtype=np.float32)

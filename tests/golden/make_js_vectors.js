@@ -225,6 +225,23 @@ var b4 = new Float32Array(64);
 b4[0] = -1;
 for (var i = 1; i < 64; i++) b4[i] = ((i % 2 ? -1 : 1) * ((i % 7) + 0.5)) / 7;
 codecInputs.push(f32bits(b4));
+// non-finite and subnormal rows: NaN never raises the max, an infinite max
+// scales every finite value to 0, NaN codes store as 0
+var nf = uniformVec(64, 5, 1);
+nf[3] = NaN; nf[17] = 1e-45; nf[40] = -3e-39;
+codecInputs.push(f32bits(nf));
+var inf = uniformVec(64, 6, 1);
+inf[9] = Infinity; inf[50] = NaN;
+codecInputs.push(f32bits(inf));
+var sub = new Float32Array(64);
+for (var i = 0; i < 64; i++) sub[i] = (i % 3 ? 1 : -1) * 1e-45 * (1 + (i % 11));
+sub[5] = 3e-39;
+codecInputs.push(f32bits(sub));
+codecInputs.push(f32bits(makeRotation(64, 0x9e3779b9, 2)(sub)));
+out.rotate.push({ dim: 64, seed: 0x9e3779b9, rounds: 2, vec_seed: -1, input: f32bits(sub),
+                  output: f32bits(makeRotation(64, 0x9e3779b9, 2)(sub)) });
+out.rotate.push({ dim: 64, seed: 0x9e3779b9, rounds: 2, vec_seed: -1, input: f32bits(inf),
+                  output: f32bits(makeRotation(64, 0x9e3779b9, 2)(inf)) });
 out.codec = codecInputs.map(function (bits) {
   var v = new Float32Array(new Uint32Array(bits).buffer);
   var r = { input: bits, q8: quant8(v), q4: null, q1: null };

@@ -231,7 +231,7 @@ def reference_tune(data, dim, bits, ref, target):
 
 @pytest.mark.parametrize("bits,target", [(8, 0.9), (0, 0.95), (4, 0.8)])
 def test_ivf_tune_matches_oracle(ctx, bits, target):
-    """targetRecall tuning (ivfTune.ts:31-61): the tuned nprobe and its
+    """targetRecall tuning (ivfTune.ts:31-42): the tuned nprobe and its
     estimated recall equal the oracle's restatement of the reference's tune;
     an explicit nprobe disables tuning."""
     from browservec_amd import IVFIndex, IVFQuantIndex

@@ -37,6 +37,15 @@ def _special_rows(dim):
     e = np.zeros(dim, np.float32)
     e[dim // 2] = -1.0
     rows.append(e)
+    d = np.full(dim, 3e-39, np.float32)  # subnormal coordinates
+    d[1::3] = -1e-45
+    rows.append(d)
+    n = np.linspace(-1, 1, dim, dtype=np.float32)
+    n[dim // 3] = np.nan  # NaN never raises the max; NaN codes store as 0
+    rows.append(n)
+    f = np.linspace(1, -1, dim, dtype=np.float32)
+    f[1] = np.inf  # infinite scale: finite coordinates code to 0
+    rows.append(f)
     return np.stack(rows)
 
 
