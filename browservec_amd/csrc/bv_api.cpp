@@ -159,6 +159,8 @@ struct bv_index {
     DevBuf mq_cand, mq_cnt, mq_tau, mq_flag;  // batched matrix-core scans
     DevBuf rsq, rsq_max;                      // flat fp32: squared row norms and their maximum (float bits)
     DevBuf mq_qsq, mq_slack, mq_rows;         // exact fp32 batches: query norms, slack, surviving rows
+    DevBuf cnorm, mq_rq, mq_up, mq_kept;       // flat int8 level-one batches: row code norms, query bounds, upper bounds, kept counts
+    DevBuf mq_bk, mq_bu, mq_bc;               // level-one batches: per-workgroup buckets (lower keys, upper bounds, lengths)
     HostBuf h_cnt;
     HostBuf h_rows, h_scores, h_n, h_flag;
 
@@ -532,6 +534,8 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
     }
     const bool norms = !idx->quant && !idx->ivf;  // flat fp32: the exact batch's error bound needs them
     if (norms) HIPX(idx->dev, idx->rsq.ensure(total * 4, base * 4, idx->stream), "norm buffer");
+    const bool code_norms = idx->codec == C_Q8 && !idx->ivf;  // flat int8: the level-one batch bound needs them
+    if (code_norms) HIPX(idx->dev, idx->cnorm.ensure(total * 4, base * 4, idx->stream), "norm buffer");
     if (idx->ivf) {
         HIPX(idx->dev, idx->sample.ensure(plan.filled * (size_t)idx->sample_dim * 4, idx->sample.cap, idx->stream),
              "sample buffer");
@@ -561,6 +565,11 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
     if (idx->quant) {
         int rc = encode_range(idx, base, count, idx->ivf ? idx->ivf_slot.as<int32_t>() : nullptr);
         if (rc) return rc;
+        if (code_norms)
+            HIPX(idx->dev,
+                 launch_row_code_norms(idx->codes.as<uint32_t>() + base * idx->words_per_row, count,
+                                       idx->words_per_row, idx->cnorm.as<float>() + base, idx->stream),
+                 "norm kernel");
     } else if (idx->ivf) {
         int rc = ivf_sample_raw(idx, base, plan.slots);
         if (rc) return rc;
@@ -1321,9 +1330,169 @@ static int run_batched_f32(bv_index *idx, const float *d_q, uint32_t nq, uint32_
     return BV_OK;
 }
 
+// int8 batches above the sample size, exactly equal to single queries.  The
+// matrix cores score every (row, query) on the query's first int8 level
+// alone (mq1_scan), which reads each code from HBM once per 256 queries and
+// does a third of the three-level work; the other two levels enter as a
+// bound, |c|_2 |R|_2 times the row scale.  A dense pass over MQ_SAMPLE
+// strided rows gives each query its kprime-th best lower-bound key (kprime
+// rows have exact keys at or above it); the pass over every row keeps the
+// rows whose upper bound reaches it, with their bounds; the kprime-th best
+// lower bound among those is a tighter bound, and only the rows whose upper
+// bound reaches it can be in the top kprime.  Those rows get their exact
+// keys with the single-query arithmetic (three exact level dots, f64
+// combine), and the best kprime of them are selected and re-ranked as a
+// single query's are.
+// A query whose kept rows overflow their buffer runs the fused scan over
+// every row.
+static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out,
+                          bool rerank, uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
+    const unsigned char *qlev = nullptr;
+    uint64_t qstride = 0;
+    int rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride);
+    if (rc) return rc;
+    const uint64_t N = idx->rows, S = MQ_SAMPLE;  // N > S (mq_eligible)
+    // rows kept per query: those within the bounds' width of the sample's
+    // bound, about 2-4x the kprime * N / S above it; room for 16x that
+    uint64_t cap = std::max<uint64_t>(4 * S, 16ull * kprime * ((N + S - 1) / S));
+    cap = std::min<uint64_t>(cap, N);
+    hipStream_t s = idx->stream;
+    const uint32_t qblocks = (nq + MQ1_QB - 1) / MQ1_QB;
+    const int cus = idx->dev->prop.multiProcessorCount > 0 ? idx->dev->prop.multiProcessorCount : 256;
+    const uint32_t nwg = std::min<uint32_t>(1024, std::max<uint32_t>(1, (uint32_t)cus / qblocks));
+    // each workgroup's bucket of a query: room for cap / nwg entries (the
+    // workgroups see evenly spread rows), at least 128
+    const uint32_t capw = (uint32_t)((std::max<uint64_t>(128, (cap + nwg - 1) / nwg) + 15) & ~15ull);
+    HIPX(idx->dev, idx->mq_cand.ensure((size_t)nq * std::max<uint64_t>(cap, S) * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_up.ensure((size_t)nq * cap * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_bk.ensure((size_t)nq * nwg * capw * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_bu.ensure((size_t)nq * nwg * capw * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_bc.ensure((size_t)nq * nwg * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_rows.ensure((size_t)nq * cap * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_cnt.ensure((size_t)nq * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_kept.ensure((size_t)nq * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_tau.ensure((size_t)nq * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_rq.ensure((size_t)nq * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->h_cnt.ensure((size_t)nq * 4), "pinned buffer");
+    HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, s), "scratch");
+    const uint32_t units16 = idx->P / 16;
+
+    timing_begin(idx);
+    HIPX(idx->dev, launch_mq1_qconst(qlev, qstride, units16, units16 * 48, nq, idx->mq_rq.as<float>(), s),
+         "query bound kernel");
+    Mq1Args m{};
+    m.codes = idx->codes.as<uint32_t>();
+    m.scales = idx->scales.as<float>();
+    m.cn = idx->cnorm.as<float>();
+    m.W = idx->words_per_row;
+    m.units = units16;
+    m.qlev = qlev;
+    m.qstride = qstride;
+    m.tail_off = units16 * 48;
+    m.rq = idx->mq_rq.as<float>();
+    m.nq = nq;
+    m.qblocks = qblocks;
+    m.groups = nwg;
+    m.nwg = nwg;
+    // sample pass: the lower-bound key of every logical row i < S
+    m.n = S;
+    m.row_step = N / S;
+    m.cand = idx->mq_cand.as<uint64_t>();
+    m.cap = S;
+    HIPX(idx->dev, hipMemsetD32Async((hipDeviceptr_t)idx->mq_cnt.p, (int)S, nq, s), "scratch");
+    HIPX(idx->dev, launch_mq1_scan(m, s), "batched scan kernel");
+    MqSelArgs sa{};
+    sa.cand = m.cand;
+    sa.cnt = idx->mq_cnt.as<uint32_t>();
+    sa.cap = S;
+    sa.kk = kprime;
+    sa.tau = idx->mq_tau.as<uint64_t>();
+    HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+    // full pass: every row whose upper bound reaches the sample's bound, into
+    // the workgroups' buckets, then one list per query
+    m.n = N;
+    m.row_step = 1;
+    m.tau = idx->mq_tau.as<uint64_t>();
+    m.cand = idx->mq_bk.as<uint64_t>();
+    m.up_out = idx->mq_bu.as<uint32_t>();
+    m.cnt = idx->mq_bc.as<uint32_t>();
+    m.cap = cap;
+    m.capw = capw;
+    HIPX(idx->dev, launch_mq1_scan(m, s), "batched scan kernel");
+    HIPX(idx->dev,
+         launch_mq1_compact(idx->mq_bk.as<uint64_t>(), idx->mq_bu.as<uint32_t>(), idx->mq_bc.as<uint32_t>(), nwg,
+                            capw, cap, idx->mq_cand.as<uint64_t>(), idx->mq_up.as<uint32_t>(),
+                            idx->mq_cnt.as<uint32_t>(), nq, s),
+         "batched compact kernel");
+    m.cand = idx->mq_cand.as<uint64_t>();
+    m.up_out = idx->mq_up.as<uint32_t>();
+    m.cnt = idx->mq_cnt.as<uint32_t>();
+    // the kprime-th best lower bound among the kept rows, and the rows whose
+    // upper bound reaches it
+    sa.cap = cap;
+    HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+    HIPX(idx->dev,
+         launch_mq1_keep(m.cand, m.up_out, m.cnt, cap, idx->mq_tau.as<uint64_t>(), idx->mq_rows.as<uint32_t>(),
+                         idx->mq_kept.as<uint32_t>(), nq, s),
+         "batched keep kernel");
+    // exact keys of those rows, the best kprime of them, and the re-rank
+    HIPX(idx->dev,
+         launch_mq1_exact(m.codes, m.W, m.scales, qlev, qstride, units16, idx->mq_rows.as<uint32_t>(),
+                          idx->mq_kept.as<uint32_t>(), cap, m.cand, nq, s),
+         "batched exact kernel");
+    MqSelArgs fa{};
+    fa.cand = m.cand;
+    fa.cnt = idx->mq_kept.as<uint32_t>();
+    fa.cap = cap;
+    fa.kk = kprime;
+    fa.merged = idx->merged.as<uint64_t>();
+    fa.merged_n = idx->merged_n.as<uint32_t>();
+    if (!rerank) {
+        fa.k_out = k_out;
+        fa.out_rows = d_rows;
+        fa.out_scores = d_scores;
+        fa.out_n = d_n;
+    }
+    HIPX(idx->dev, launch_mq_select(fa, nq, s), "batched select kernel");
+    if (rerank) {
+        MqRerankArgs r{};
+        r.rows = idx->raw.as<float>();
+        r.dim = idx->dim;
+        r.q = d_q;
+        r.q_stride = idx->dim;
+        r.merged = idx->merged.as<uint64_t>();
+        r.merged_n = idx->merged_n.as<uint32_t>();
+        r.kprime = kprime;
+        r.k_out = k_out;
+        r.out_rows = d_rows;
+        r.out_scores = d_scores;
+        r.out_n = d_n;
+        HIPX(idx->dev, launch_mq_rerank(r, nq, s), "rerank kernel");
+    }
+    timing_end(idx);
+    HIPX(idx->dev, hipMemcpyAsync(idx->h_cnt.p, idx->mq_cnt.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s),
+         "count download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "batched scan");
+    const uint32_t *cnt = (const uint32_t *)idx->h_cnt.p;
+    idx->last_scanned = (N + S) * nq;
+    // queries whose kept rows overflowed their buffer: the fused scan over every row
+    std::vector<uint32_t> over;
+    for (uint32_t i = 0; i < nq; i++)
+        if (cnt[i] > cap) over.push_back(i);
+    for (uint32_t i : over) {
+        rc = run_fused(idx, d_q + (size_t)i * idx->dim, 1, kprime, k_out, rerank, nullptr, 0,
+                       d_rows + (size_t)i * k_out, d_scores + (size_t)i * k_out, d_n + i);
+        if (rc) return rc;
+    }
+    return BV_OK;
+}
+
 static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                        uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
     if (!idx->quant) return run_batched_f32(idx, d_q, nq, kprime, k_out, d_rows, d_scores, d_n);
+    if (idx->codec == C_Q8 && idx->rows > MQ_SAMPLE)
+        return run_batched_q8(idx, d_q, nq, kprime, k_out, rerank, d_rows, d_scores, d_n);
     const unsigned char *qscan = (const unsigned char *)d_q;  // fp32 rows: the queries as they are
     uint64_t qstride = (uint64_t)idx->dim * 4;
     int rc = BV_OK;

@@ -281,6 +281,55 @@ struct MqRerankArgs {
     float *out_scores;
     uint32_t *out_n;
 };
+// Level-one prefilter of int8 batches (mq1_scan): MQ1_QB queries per
+// workgroup (32 per wave, in registers) scored on their first int8 level
+// alone against MQ1_ROWS-row tiles staged in LDS, with per-(row, query)
+// bounds from the row's code norm and the query's remaining levels.
+constexpr int MQ1_QB = 256;
+constexpr int MQ1_ROWS = 32;
+struct Mq1Args {
+    const uint32_t *codes;    // N x W words of int8 codes
+    const float *scales;      // N
+    const float *cn;          // N: |c|_2 of each row's codes, rounded up
+    uint32_t W;               // words per row
+    uint32_t units;           // 16-code units per row (even), P / 16
+    uint64_t n;               // logical rows in this pass
+    uint64_t row_step;        // physical row of logical row i = i * row_step
+    const unsigned char *qlev;// nq x qstride bytes: packed levels (16-code units) + QLevelTail
+    uint64_t qstride;
+    uint32_t tail_off;
+    const float *rq;          // [nq] bound of the query's levels two and three (launch_mq1_qconst)
+    uint32_t nq;
+    uint32_t qblocks;         // ceil(nq / MQ1_QB)
+    uint32_t groups;          // workgroups per query block (about one per CU in all)
+    uint32_t nwg;             // = groups (bucket count per query)
+    const uint64_t *tau;      // null: dense pass (lower-bound keys into cand); else [nq] bound keys
+    uint64_t *cand;           // dense: [nq][cap] lower-bound keys of logical rows;
+                              // threshold: [nq][nwg][capw] lower-bound keys of kept rows, per workgroup bucket
+    uint32_t *up_out;         // threshold: [nq][nwg][capw] order bits of the kept rows' upper bounds
+    uint32_t *cnt;            // threshold: [nq][nwg] bucket lengths (0xffffffff: overflowed)
+    uint64_t cap;
+    uint32_t capw;            // threshold: entries per bucket
+};
+// Per query: its buckets joined into lk / uo [nq][cap] and the length in
+// cnt[q] (0xffffffff when a bucket overflowed or the total exceeds cap).
+hipError_t launch_mq1_compact(const uint64_t *bk, const uint32_t *bu, const uint32_t *bc, uint32_t nwg,
+                              uint32_t capw, uint64_t cap, uint64_t *lk, uint32_t *uo, uint32_t *cnt, uint32_t nq,
+                              hipStream_t s);
+// Per query: the rows among cand[q][0, min(cnt[q], cap)) whose upper bound
+// (make_key(up[q][i], row)) reaches tau[q], into rows[q][...], their number
+// in kept[q].
+hipError_t launch_mq1_keep(const uint64_t *cand, const uint32_t *up, const uint32_t *cnt, uint64_t cap,
+                           const uint64_t *tau, uint32_t *rows, uint32_t *kept, uint32_t nq, hipStream_t s);
+// Per query: the exact key (the single-query scan's three-level f64
+// combine) of each of rows[q][0, kept[q]) into keys[q][...].
+hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scales, const unsigned char *qlev,
+                            uint64_t qstride, uint32_t units16, const uint32_t *rows, const uint32_t *kept,
+                            uint64_t cap, uint64_t *keys, uint32_t nq, hipStream_t s);
+hipError_t launch_row_code_norms(const uint32_t *codes, uint64_t n, uint32_t W, float *cn, hipStream_t s);
+hipError_t launch_mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32_t units, uint32_t tail_off,
+                             uint32_t nq, float *rq, hipStream_t s);
+hipError_t launch_mq1_scan(const Mq1Args &a, hipStream_t s);
 hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s);
 // fp32 rows (dot / cosine): a.codes = the rows, a.W = dim, a.units = dim / 8,
 // a.qlev = fp32 queries (a.qstride bytes apart).  Dimensions 32 .. 1024 in

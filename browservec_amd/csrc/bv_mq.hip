@@ -42,6 +42,10 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
 
+// s_waitcnt immediate waiting for vmcnt <= n (n < 64) only (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8 left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 // f64 combine of the three level dots, then the row scale: the arithmetic
 // of the single-query int8 / int4 scans' finalisation (d already corrected
 // for the int4 nibble offset).
@@ -207,6 +211,152 @@ __device__ __forceinline__ void epilogue(const MqArgs &a, const v16i (&acc)[2][3
     }
 }
 
+// Bounds of one (row, query) key from its level-one dot D alone.  The exact
+// key's score is f32(scale * (s0 D + s1 D1 + s2 D2)) and |s1 D1 + s2 D2| =
+// |sum_i c_i R_i| <= |c|_2 |R|_2 (Cauchy-Schwarz), so with av = s0 D and
+// bv = |c|_2 |R|_2 the score lies in scale * [av - bv, av + bv].  The extra
+// 2^-20 |av| (and the 2^-18 already in rq) are far above every f32 rounding
+// of the bound's own arithmetic and of the exact score.
+__device__ __forceinline__ float mq1_upper(int32_t d, float s0f, float nr_rq, float scale) {
+    const float av = (float)d * s0f;
+    return fmaf(fabsf(av), 0x1p-20f, av + nr_rq) * scale;
+}
+__device__ __forceinline__ float mq1_lower(int32_t d, float s0f, float nr_rq, float scale) {
+    const float av = (float)d * s0f;
+    return fmaf(-fabsf(av), 0x1p-20f, av - nr_rq) * scale;
+}
+
+// The threshold pass keeps its entries without device-scope atomics (they
+// are slow and serialize when many workgroups hit one query's counter, and
+// a returning atomic would also make a wave wait for its outstanding tile
+// loads).  Each tile's kept entries are staged in LDS by the wave that found
+// them (a wave-private region); the waves that issue no tile loads move them
+// to the workgroup's own bucket of each query, positions from LDS counters;
+// mq1_compact joins the buckets into one list per query afterwards.
+constexpr int MQ1_STAGE = 120;   // entries per wave per staging buffer
+constexpr int MQ1_LOADERS = 4;   // waves 0..3 issue the tile loads; 4..7 move staged entries
+struct Mq1Stage {
+    uint64_t lk[2][MQ_WAVES][MQ1_STAGE];   // lower-bound keys, in lane order
+    uint32_t uo[2][MQ_WAVES][MQ1_STAGE];   // order bits of the upper bounds
+    uint16_t lo[2][MQ_WAVES][64];          // first entry of each lane
+    uint16_t ln[2][MQ_WAVES][64];          // entries of each lane
+    uint8_t qovf[MQ1_QB];                  // a query's entries did not all fit
+};
+
+// Inclusive prefix sum over the wave's 64 lanes in VALU (DPP row shifts
+// within rows of 16, then the row broadcasts), no LDS traffic.
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
+}
+
+// Keys of one wave's 32 queries x the tile's MQ1_ROWS (32) rows.  Dense
+// pass: the lower-bound key of every (row, query) (a NaN bound as order 0,
+// below every key of the row).  Threshold pass: the rows whose upper bound
+// reaches the query's bound are staged (buffer sb) as (lower-bound key,
+// order bits of the upper bound; NaN: the largest).  Lane l holds query
+// l % 32 and, in accumulator register r, tile row 8(r/4) + 4(l/32) + r%4.
+// sc / cn: the tile rows' scales and code norms |c|_2 (LDS).
+__device__ __forceinline__ void mq1_epilogue(const Mq1Args &a, const v16i &acc, uint64_t t0, uint32_t q,
+                                             uint32_t qlocal, int h, float s0f, float rq, float tau_score,
+                                             const float *sc, const float *cn, Mq1Stage &st, int sb) {
+    // per-lane addresses are derived here, per tile: hoisted out of the tile
+    // loop they would stay live across the matrix loop
+    asm volatile("" : "+v"(q), "+v"(h));
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const bool qok = q < a.nq;
+    const bool full = t0 + MQ1_ROWS <= a.n;
+    // the lane's rows come in runs of four: one 16-byte LDS read per run
+    float sv[16], bv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const float4 s4 = *(const float4 *)&sc[8 * g + 4 * h];
+        const float4 n4 = *(const float4 *)&cn[8 * g + 4 * h];
+        sv[4 * g] = s4.x, sv[4 * g + 1] = s4.y, sv[4 * g + 2] = s4.z, sv[4 * g + 3] = s4.w;
+        bv[4 * g] = n4.x * rq, bv[4 * g + 1] = n4.y * rq, bv[4 * g + 2] = n4.z * rq, bv[4 * g + 3] = n4.w * rq;
+    }
+    auto row_of = [&](uint32_t r) { return 8 * (r >> 2) + 4 * (uint32_t)h + (r & 3); };
+    if (!a.tau) {
+        if (!qok) return;
+        uint64_t *out = a.cand + (uint64_t)q * a.cap;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint64_t li = t0 + row_of(r);
+            if (full || li < a.n) {
+                const float lo = mq1_lower(acc[r], s0f, bv[r], sv[r]);
+                out[li] = make_key(lo == lo ? ord_f32(lo) : 0u, (uint32_t)(li * a.row_step));
+            }
+        }
+        return;
+    }
+    uint32_t p = 0;  // bit r: the row can reach the query's bound
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const float up = mq1_upper(acc[r], s0f, bv[r], sv[r]);
+        p |= (!(up < tau_score) ? 1u : 0u) << r;  // NaN: kept
+    }
+    if (!full) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (t0 + row_of(r) >= a.n) p &= ~(1u << r);
+    }
+    if (!qok) p = 0;
+    // this wave's staging slots: an exclusive prefix of the lanes' counts (a
+    // wave-private region: no LDS atomic, which would wait for the tile loads)
+    const uint32_t mine = __popc(p);
+    const uint32_t incl = wave_incl_scan(mine);
+    st.lo[sb][wave][lane] = (uint16_t)(incl - mine);
+    st.ln[sb][wave][lane] = (uint16_t)mine;
+    if (!__builtin_amdgcn_readlane((int)incl, 63)) return;
+    uint32_t pos = incl - mine;
+    for (uint32_t m = p; m; m &= m - 1, ++pos) {
+        if (pos >= (uint32_t)MQ1_STAGE) {
+            st.qovf[qlocal] = 1;  // the query's list can no longer be complete: it falls back
+            break;
+        }
+        const uint32_t bit = __builtin_ctz(m);
+        int32_t d = 0;
+        float s_ = 0.0f, b_ = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if ((uint32_t)k == bit) d = acc[k], s_ = sv[k], b_ = bv[k];
+        const float lo = mq1_lower(d, s0f, b_, s_), up = mq1_upper(d, s0f, b_, s_);
+        st.lk[sb][wave][pos] = make_key(lo == lo ? ord_f32(lo) : 0u, (uint32_t)((t0 + row_of(bit)) * a.row_step));
+        st.uo[sb][wave][pos] = up == up ? ord_f32(up) : 0xffffffffu;
+    }
+}
+
+// Staged entries of buffer fb into this workgroup's bucket of each query.
+// Lane l of flushing wave f owns query f*64 + l of the block: its entries
+// were staged by wave (f*64 + l) / 32, lanes c and c + 32 (c = l % 32), and
+// its bucket length lives in the lane's register (len; ovf: it overflowed),
+// so no atomic is needed.
+__device__ __forceinline__ void mq1_flush(const Mq1Args &a, uint32_t qb, uint32_t wg, const Mq1Stage &st, int fb,
+                                          int f, int lane, uint32_t &len, bool &ovf) {
+    const uint32_t ql = (uint32_t)f * 64 + lane, w = ql / 32, c = ql % 32;
+    const uint64_t bucket = ((uint64_t)(qb * MQ1_QB + ql) * a.nwg + wg) * a.capw;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const uint32_t off = st.lo[fb][w][c + 32 * hh], n = st.ln[fb][w][c + 32 * hh];
+        for (uint32_t j = 0; j < n; ++j) {
+            const uint32_t i = off + j;
+            if (i >= (uint32_t)MQ1_STAGE) break;  // not staged (the query is marked)
+            if (len < a.capw) {
+                a.cand[bucket + len] = st.lk[fb][w][i];
+                a.up_out[bucket + len] = st.uo[fb][w][i];
+            } else {
+                ovf = true;
+            }
+            ++len;
+        }
+    }
+}
+
 }  // namespace
 
 // One workgroup = MQ_QB (32) queries, walking row tiles of MQ_ROWS (512)
@@ -359,6 +509,211 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan(MqArgs a) {
         ap[1] = np[1];
         tile = ntile;
     }
+}
+
+// Batched int8 prefilter on the first query level alone, on
+// v_mfma_i32_32x32x32_i8, one workgroup per CU.  Each of the 8 waves holds
+// one 32-query tile's level-one bytes in registers for the whole launch
+// (S x 16 bytes per lane: the B operand of every K step), so a workgroup
+// serves MQ1_QB = 256 queries and every code row is read from HBM once per
+// 256 queries, staged in LDS and read by all 8 waves.  Tiles of MQ1_ROWS
+// (32) rows rotate through four LDS buffers: three tiles stream in with
+// global_load_lds (issued by waves 0..3) while one is multiplied.  LDS rows
+// are one 16-byte unit longer than the codes, so the 32 rows an MFMA A
+// operand reads at one unit spread over the banks, and each step's reads sit
+// at a fixed offset from a per-lane base.  The matrix work is a third of a
+// three-level scan; keys are not formed here: each (row, query) gets the
+// bounds of mq1_upper / mq1_lower, the dense pass over a strided sample
+// writes lower-bound keys (whose kk-th best per query is a valid bound: kk
+// rows have exact keys at or above it), and the pass over every row keeps
+// the rows whose upper bound reaches it.
+template <int S>
+__global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan(Mq1Args a) {
+    constexpr uint32_t U = 2 * S;     // 16-byte units per row (<= 64)
+    constexpr uint32_t RS = U + 1;    // LDS row stride in units: one unit of padding
+    constexpr uint32_t PER_WAVE = MQ1_ROWS / MQ1_LOADERS;  // rows each loader wave loads per tile
+    // four buffers as separate LDS objects, each unrolled loop quarter naming
+    // its own, so the compiler can see that pending tile loads do not touch
+    // the rows being read
+    __shared__ v4i tb0[MQ1_ROWS * RS], tb1[MQ1_ROWS * RS], tb2[MQ1_ROWS * RS], tb3[MQ1_ROWS * RS];
+    __shared__ float sc0[MQ1_ROWS], sc1[MQ1_ROWS], sc2[MQ1_ROWS], sc3[MQ1_ROWS];
+    __shared__ float cs0[MQ1_ROWS], cs1[MQ1_ROWS], cs2[MQ1_ROWS], cs3[MQ1_ROWS];
+    __shared__ Mq1Stage stage;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane >> 5, c = lane & 31;
+    const uint64_t ntiles = (a.n + MQ1_ROWS - 1) / MQ1_ROWS;
+    const uint32_t qb = blockIdx.x % a.qblocks;
+    const uint32_t wg = blockIdx.x / a.qblocks;  // a.nwg workgroups per query block
+    const bool loader = wave < MQ1_LOADERS;
+    const bool thr = a.tau != nullptr;
+    for (uint32_t i = threadIdx.x; i < 2 * MQ_WAVES * 64; i += MQ_WAVES * 64)
+        stage.ln[i / (MQ_WAVES * 64)][(i / 64) % MQ_WAVES][i % 64] = 0;
+    if (threadIdx.x < MQ1_QB) stage.qovf[threadIdx.x] = 0;
+    uint32_t blen = 0;  // flushing lanes: the owned query's bucket length
+    bool bovf = false;
+    // this workgroup's tiles: wg, wg + nwg, ...
+    const uint64_t mine = wg < ntiles ? (ntiles - wg + a.nwg - 1) / a.nwg : 0;
+
+    // this wave's queries: level one (unit u of a query's packed levels:
+    // 48 bytes, level one first) as B operands, lane l: unit 2st + l/32
+    const uint32_t qlocal = (uint32_t)wave * 32 + c;
+    const uint32_t q = qb * MQ1_QB + qlocal;
+    const bool wave_live = qb * MQ1_QB + (uint32_t)wave * 32 < a.nq;
+    const uint32_t qc = q < a.nq ? q : a.nq - 1;
+    const unsigned char *qsrc = a.qlev + (uint64_t)qc * a.qstride;
+    v4i qreg[S];
+#pragma unroll
+    for (int st = 0; st < S; ++st) qreg[st] = *(const v4i *)(qsrc + (uint64_t)(2 * st + h) * 48);
+    const QLevelTail *qt = (const QLevelTail *)(qsrc + a.tail_off);
+    const float s0f = (float)qt->s[0];
+    const float rq = a.rq[qc];
+    const uint64_t tau = thr ? a.tau[qc] : 0ull;
+    const float tau_score = tau ? f32_from_ord((uint32_t)(tau >> 32)) : -__builtin_inff();
+
+    // tile k (the workgroup's k-th) into (tl, sc, cs) by the loader waves,
+    // one load instruction per row (lanes 0 .. U-1: the row's units in
+    // order), PER_WAVE rows each; the rows' scales and code norms by wave 0
+    // (one dword per lane, lanes 0 .. 31)
+    auto load_tile = [&](uint64_t k, v4i *tl, float *sc, float *cs) {
+        const uint64_t t = wg + k * a.nwg;
+        if ((uint32_t)lane < U) {
+#pragma unroll
+            for (uint32_t j = 0; j < PER_WAVE; ++j) {
+                const uint32_t r = (uint32_t)wave * PER_WAVE + j;
+                uint64_t li = t * MQ1_ROWS + r;
+                if (li >= a.n) li = a.n - 1;  // rows past the end load a valid row; their results are dropped
+                const v4i *src = (const v4i *)(a.codes + li * a.row_step * a.W) + lane;
+                __builtin_amdgcn_global_load_lds((glb_void *)src, (lds_void *)&tl[r * RS], 16, 0, 0);
+            }
+        }
+        if (wave == 0 && lane < MQ1_ROWS) {
+            uint64_t li = t * MQ1_ROWS + (uint32_t)lane;
+            if (li >= a.n) li = a.n - 1;
+            __builtin_amdgcn_global_load_lds((glb_void *)(a.scales + li * a.row_step), (lds_void *)sc, 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_void *)(a.cn + li * a.row_step), (lds_void *)cs, 4, 0, 0);
+        }
+    };
+    // tile k from (tl, sc, cs), staging into buffer k & 1, while tile k + 3
+    // streams into (ntl, nsc, ncs) and the previous tile's staged entries are
+    // moved to the buckets
+    auto run_tile = [&](uint64_t k, const v4i *tl, const float *sc, const float *cs, v4i *ntl, float *nsc,
+                        float *ncs) {
+        // this wave's loads of tile k have landed: the loads of the (up to
+        // two) later tiles issued after them may still run (vmcnt counts in
+        // issue order); the dense pass writes keys, so it waits for all
+        if (loader && thr) {
+            const uint64_t after = (mine - 1 - k) < 2 ? (mine - 1 - k) : 2;
+            if (wave == 0) {
+                if (after == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (PER_WAVE + 2)));
+                else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE + 2));
+                else __builtin_amdgcn_s_waitcnt(0);
+            } else {
+                if (after == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER_WAVE));
+                else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE));
+                else __builtin_amdgcn_s_waitcnt(0);
+            }
+        } else if (loader || !thr) {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        // every wave's loads have landed, and every wave is done with tile
+        // k - 1's buffers.  The barrier waits only for this wave's LDS
+        // operations: a workgroup fence on LDS would also wait for the later
+        // tiles' loads into LDS (and the flushing waves' bucket stores need
+        // not complete here); the memory clobber keeps every access on its
+        // side of it.
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (loader) {
+            if (k + 3 < mine) load_tile(k + 3, ntl, nsc, ncs);
+        } else if (thr) {
+            mq1_flush(a, qb, wg, stage, (int)((k + 1) & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+        }
+        if (wave_live) {
+            // two accumulators (even and odd K steps), so consecutive MFMAs
+            // do not wait on each other
+            v16i acc2[2] = {v16i{}, v16i{}};
+            // lane l reads row l%32, unit 2st + l/32: a fixed base plus a
+            // per-step constant
+            const v4i *A0 = tl + c * RS + h;
+            // A operands read PF steps ahead of their MFMA, so the LDS latency
+            // is hidden behind the matrix work
+            constexpr int PF = S < 4 ? S : 4;
+            v4i ar[PF];
+#pragma unroll
+            for (int st = 0; st < PF; ++st) ar[st] = A0[2 * st];
+#pragma unroll
+            for (int st = 0; st < S; ++st) {
+                const v4i x = ar[st % PF];
+                if (st + PF < S) ar[st % PF] = A0[2 * (st + PF)];
+                acc2[st & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x, qreg[st], acc2[st & 1], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);  // keep each step's read PF steps ahead
+            }
+            const v16i acc = acc2[0] + acc2[1];
+            mq1_epilogue(a, acc, (wg + k * a.nwg) * MQ1_ROWS, q, qlocal, h, s0f, rq, tau_score, sc, cs, stage,
+                         (int)(k & 1));
+        }
+    };
+
+    if (loader) {
+        if (mine > 0) load_tile(0, tb0, sc0, cs0);
+        if (mine > 1) load_tile(1, tb1, sc1, cs1);
+        if (mine > 2) load_tile(2, tb2, sc2, cs2);
+    }
+    for (uint64_t k = 0; k < mine; k += 4) {
+        run_tile(k, tb0, sc0, cs0, tb3, sc3, cs3);
+        if (k + 1 >= mine) break;
+        run_tile(k + 1, tb1, sc1, cs1, tb0, sc0, cs0);
+        if (k + 2 >= mine) break;
+        run_tile(k + 2, tb2, sc2, cs2, tb1, sc1, cs1);
+        if (k + 3 >= mine) break;
+        run_tile(k + 3, tb3, sc3, cs3, tb2, sc2, cs2);
+    }
+    if (thr) {  // the last tile's staged entries, then this workgroup's bucket lengths
+        __syncthreads();
+        if (!loader) {
+            if (mine) mq1_flush(a, qb, wg, stage, (int)((mine - 1) & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+            const uint32_t ql = (uint32_t)(wave - MQ1_LOADERS) * 64 + lane, qq = qb * MQ1_QB + ql;
+            if (qq < a.nq) a.cnt[(uint64_t)qq * a.nwg + wg] = bovf || stage.qovf[ql] ? 0xffffffffu : blen;
+        }
+    }
+}
+
+// One workgroup per query: the workgroups' buckets of the query joined into
+// one list (bucket order), and its length; a query with an overflowed
+// bucket or more than cap entries gets length 0xffffffff (it falls back).
+__global__ __launch_bounds__(256) void mq1_compact(const uint64_t *bk, const uint32_t *bu, const uint32_t *bc,
+                                                    uint32_t nwg, uint32_t capw, uint64_t cap, uint64_t *lk,
+                                                    uint32_t *uo, uint32_t *cnt) {
+    __shared__ uint32_t off[1025];
+    __shared__ uint32_t bad;
+    const uint32_t q = blockIdx.x, tid = threadIdx.x;
+    if (tid == 0) bad = 0;
+    __syncthreads();
+    // counts, then an exclusive prefix over the buckets (one thread per bucket; nwg <= 1024)
+    for (uint32_t w = tid; w < nwg; w += 256) {
+        const uint32_t c = bc[(uint64_t)q * nwg + w];
+        if (c > capw) bad = 1;
+        off[w + 1] = c > capw ? 0u : c;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        off[0] = 0;
+        for (uint32_t w = 0; w < nwg; ++w) off[w + 1] += off[w];
+    }
+    __syncthreads();
+    const uint32_t total = off[nwg];
+    if (bad || total > cap) {
+        if (tid == 0) cnt[q] = 0xffffffffu;
+        return;
+    }
+    for (uint32_t w = 0; w < nwg; ++w) {
+        const uint32_t n = off[w + 1] - off[w];
+        const uint64_t src = ((uint64_t)q * nwg + w) * capw, dst = (uint64_t)q * cap + off[w];
+        for (uint32_t i = tid; i < n; i += 256) {
+            lk[dst + i] = bk[src + i];
+            uo[dst + i] = bu[src + i];
+        }
+    }
+    if (tid == 0) cnt[q] = total;
 }
 
 // fp32 rows x fp32 queries on v_mfma_f32_32x32x2f32: the batched
@@ -817,7 +1172,188 @@ __global__ __launch_bounds__(64) void mq_f32_qconst(const float *q, uint32_t dim
     }
 }
 
+// One wave per row: |c|_2 of the int8 codes, rounded up to f32 (the exact
+// sum of squares from v_dot4 of each word with itself, below 2^24; f64
+// square root).
+__global__ __launch_bounds__(256) void row_code_norms(const uint32_t *codes, uint64_t n, uint32_t W, float *cn) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t nw = (uint64_t)gridDim.x * 4;
+    for (uint64_t r = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6); r < n; r += nw) {
+        const uint32_t *w = codes + r * W;
+        int acc = 0;
+        for (uint32_t i = lane; i < W; i += 64) acc = __builtin_amdgcn_sdot4((int)w[i], (int)w[i], acc, false);
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) acc += __shfl_xor(acc, o);
+        if (lane == 0) {
+            const double v = sqrt((double)acc);
+            float f = (float)v;
+            if ((double)f < v) f = next_up(f);
+            cn[r] = f;
+        }
+    }
+}
+
+// One wave per query: rq >= |R|_2 for R = s1 q1 + s2 q2, the part of the
+// query the level-one prefilter leaves out (f64 sum, 2^-18 added, rounded up
+// to f32).
+__global__ __launch_bounds__(64) void mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32_t units,
+                                                 uint32_t tail_off, float *rq) {
+    const int lane = threadIdx.x;
+    const unsigned char *src = qlev + (uint64_t)blockIdx.x * qstride;
+    const QLevelTail *t = (const QLevelTail *)(src + tail_off);
+    const double s1 = t->s[1], s2 = t->s[2];
+    double acc = 0.0;
+    for (uint32_t i = lane; i < units * 16; i += 64) {
+        const uint32_t u = i >> 4, j = i & 15;
+        const double r = fma(s2, (double)(int8_t)src[(u * 3 + 2) * 16 + j], s1 * (double)(int8_t)src[(u * 3 + 1) * 16 + j]);
+        acc = fma(r, r, acc);
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) acc += __shfl_xor(acc, o);
+    if (lane == 0) {
+        const double v = sqrt(acc) * (1.0 + 0x1p-18);
+        float f = (float)v;
+        if ((double)f < v) f = next_up(f);
+        rq[blockIdx.x] = f;
+    }
+}
+
+// One workgroup per query: the kept rows whose upper bound reaches tau[q]
+// (the kk-th best lower-bound key among them, so every row of the exact
+// top kk is among these).
+__global__ __launch_bounds__(1024) void mq1_keep(const uint64_t *cand, const uint32_t *up, const uint32_t *cnt,
+                                                  uint64_t cap, const uint64_t *tau, uint32_t *rows,
+                                                  uint32_t *kept) {
+    __shared__ uint32_t s_n;
+    const uint32_t q = blockIdx.x;
+    // an overflowed list (more rows than cap, or marked incomplete) keeps
+    // nothing: the query runs the single-query scan instead
+    const uint32_t n = (uint64_t)cnt[q] <= cap ? cnt[q] : 0u;
+    const uint64_t t = tau[q];
+    const uint64_t *lk = cand + (uint64_t)q * cap;
+    const uint32_t *uo = up + (uint64_t)q * cap;
+    uint32_t *out = rows + (uint64_t)q * cap;
+    if (threadIdx.x == 0) s_n = 0;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+        const uint32_t row = key_row(lk[i]);
+        if (make_key(uo[i], row) >= t) out[atomicAdd(&s_n, 1u)] = row;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) kept[q] = s_n;
+}
+
+// One workgroup per query: the exact key of every kept row, with the
+// single-query scan's arithmetic (three exact int32 level dots, f64
+// combine, row scale), into keys[q][i].  Sixteen lanes per row, four rows
+// per wave at a time: each load instruction reads 256 contiguous bytes of
+// four rows.
+__global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, uint32_t W, const float *scales,
+                                                   const unsigned char *qlev, uint64_t qstride, uint32_t units16,
+                                                   const uint32_t *rows, const uint32_t *kept, uint64_t cap,
+                                                   uint64_t *keys) {
+    __shared__ v4i ql[MQ_MAX_STEPS * 2 * 3];  // the query's packed levels: unit u, level l at 3u + l
+    const uint32_t q = blockIdx.x, tid = threadIdx.x;
+    const unsigned char *src = qlev + (uint64_t)q * qstride;
+    for (uint32_t i = tid; i < units16 * 3; i += 1024) ql[i] = ((const v4i *)src)[i];
+    const QLevelTail *t = (const QLevelTail *)(src + (uint64_t)units16 * 48);
+    const double s0 = t->s[0], s1 = t->s[1], s2 = t->s[2];
+    __syncthreads();
+    const uint32_t n = kept[q];
+    const uint32_t *rq = rows + (uint64_t)q * cap;
+    uint64_t *out = keys + (uint64_t)q * cap;
+    const int lane = tid & 63, l16 = lane & 15;
+    for (uint32_t i = tid >> 4; i < n; i += 64) {  // the 16 lanes of a row step together
+        const uint32_t row = rq[i];
+        const v4i *x = (const v4i *)(codes + (uint64_t)row * W);
+        int d0 = 0, d1 = 0, d2 = 0;
+        for (uint32_t u = l16; u < units16; u += 16) {
+            const v4i c = x[u];
+            const v4i a0 = ql[3 * u], a1 = ql[3 * u + 1], a2 = ql[3 * u + 2];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                d0 = __builtin_amdgcn_sdot4(c[w], a0[w], d0, false);
+                d1 = __builtin_amdgcn_sdot4(c[w], a1[w], d1, false);
+                d2 = __builtin_amdgcn_sdot4(c[w], a2[w], d2, false);
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+            d0 += __shfl_xor(d0, o);
+            d1 += __shfl_xor(d1, o);
+            d2 += __shfl_xor(d2, o);
+        }
+        if (l16 == 0) out[i] = q_key(s0, s1, s2, d0, d1, d2, scales[row], row);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scales, const unsigned char *qlev,
+                            uint64_t qstride, uint32_t units16, const uint32_t *rows, const uint32_t *kept,
+                            uint64_t cap, uint64_t *keys, uint32_t nq, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    if (units16 == 0 || units16 > MQ_MAX_STEPS * 2 || W != units16 * 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mq1_exact, dim3(nq), dim3(1024), 0, s, codes, W, scales, qlev, qstride, units16, rows, kept,
+                       cap, keys);
+    return hipGetLastError();
+}
+
+hipError_t launch_mq1_compact(const uint64_t *bk, const uint32_t *bu, const uint32_t *bc, uint32_t nwg,
+                              uint32_t capw, uint64_t cap, uint64_t *lk, uint32_t *uo, uint32_t *cnt, uint32_t nq,
+                              hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    if (nwg == 0 || nwg > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mq1_compact, dim3(nq), dim3(256), 0, s, bk, bu, bc, nwg, capw, cap, lk, uo, cnt);
+    return hipGetLastError();
+}
+
+hipError_t launch_mq1_keep(const uint64_t *cand, const uint32_t *up, const uint32_t *cnt, uint64_t cap,
+                           const uint64_t *tau, uint32_t *rows, uint32_t *kept, uint32_t nq, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    hipLaunchKernelGGL(mq1_keep, dim3(nq), dim3(1024), 0, s, cand, up, cnt, cap, tau, rows, kept);
+    return hipGetLastError();
+}
+
+hipError_t launch_row_code_norms(const uint32_t *codes, uint64_t n, uint32_t W, float *cn, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    uint64_t blocks = (n + 3) / 4;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(row_code_norms, dim3((uint32_t)blocks), dim3(256), 0, s, codes, n, W, cn);
+    return hipGetLastError();
+}
+
+hipError_t launch_mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32_t units, uint32_t tail_off,
+                             uint32_t nq, float *rq, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    hipLaunchKernelGGL(mq1_qconst, dim3(nq), dim3(64), 0, s, qlev, qstride, units, tail_off, rq);
+    return hipGetLastError();
+}
+
+hipError_t launch_mq1_scan(const Mq1Args &a, hipStream_t s) {
+    if (a.n == 0 || a.nq == 0) return hipSuccess;
+    const uint32_t steps = a.units >> 1;
+    if ((a.units & 1u) || steps == 0 || steps > MQ_MAX_STEPS || (steps & (steps - 1)) || a.qblocks == 0 ||
+        a.groups == 0 || (uint64_t)a.qblocks * MQ1_QB < a.nq || a.W * 2u != a.units * 8u ||
+        !a.cand || (a.tau && (!a.up_out || !a.cnt || a.capw == 0)) || a.nwg != a.groups)
+        return hipErrorInvalidValue;
+    const uint64_t blocks = (uint64_t)a.groups * a.qblocks;
+    if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+    const dim3 g((uint32_t)blocks), wg(MQ_WAVES * 64);
+#define BV_MQ1_CASE(ST)                                             \
+    case ST: hipLaunchKernelGGL((mq1_scan<ST>), g, wg, 0, s, a); break;
+    switch (steps) {
+        BV_MQ1_CASE(1)
+        BV_MQ1_CASE(2)
+        BV_MQ1_CASE(4)
+        BV_MQ1_CASE(8)
+        BV_MQ1_CASE(16)
+        BV_MQ1_CASE(32)
+    default: return hipErrorInvalidValue;
+    }
+#undef BV_MQ1_CASE
+    return hipGetLastError();
+}
 
 hipError_t launch_row_sqnorms(const float *rows, uint64_t n, uint32_t dim, float *rsq, uint32_t *max_bits,
                               hipStream_t s) {

@@ -56,6 +56,47 @@ def test_batched_search_equals_singles(ctx, bits, dim, n, nq):
     idx.destroy()
 
 
+def test_batched_int8_query_blocks_and_appends(ctx):
+    """int8 batches above the sample size score each row on the first query
+    level alone, 128 queries per workgroup, with a bound from the row's code
+    norm: 300 queries (three blocks, the last partial) over rows appended in
+    three calls (the norms of each append's rows), dot metric with rows of
+    varied norm, still equal to single queries."""
+    from browservec_amd import QuantIndex
+
+    dim, n, nq = 256, 60000, 300
+    say("batched int8 blocks/appends")
+    data = clustered(n, dim, 80, 0.1, seed=61)
+    data = data * np.random.default_rng(62).uniform(0.25, 4.0, (n, 1)).astype(np.float32)
+    idx = QuantIndex(ctx, dim, bits=8, metric="dot")
+    idx.append(data[:17000], 17000)
+    idx.append(data[17000:17001], 1)
+    idx.append(data[17001:], n - 17001)
+    qs = (data[np.arange(nq) * 199] + gaussian(nq, dim, 63, normalize=False) * 0.05).astype(np.float32)
+    singles_equal(idx, qs, 100, 10)
+    idx.destroy()
+
+
+def test_batched_int8_near_duplicates(ctx):
+    """Groups of eight rows within a small perturbation of each other: their
+    level-one bounds overlap the query's bound, so whole groups are kept and
+    the exact re-score must order them as single queries do."""
+    from browservec_amd import QuantIndex
+
+    dim, n, nq = 768, 40000, 24
+    say("batched int8 near-duplicates")
+    base = clustered(n // 8, dim, 40, 0.1, seed=64)
+    rng = np.random.default_rng(65)
+    data = np.repeat(base, 8, axis=0) + rng.standard_normal((n, dim)).astype(np.float32) * np.float32(1e-4)
+    data = np.stack([o.normalize(r) for r in data]).astype(np.float32)
+    idx = QuantIndex(ctx, dim, bits=8)
+    idx.append(data, n)
+    qs = (data[np.arange(nq) * 1601] + gaussian(nq, dim, 66, normalize=False) * 0.03).astype(np.float32)
+    qs = np.stack([o.normalize(q) for q in qs]).astype(np.float32)
+    singles_equal(idx, qs, 100, 10)
+    idx.destroy()
+
+
 def test_batched_large_fetch(ctx):
     from browservec_amd import QuantIndex
 
