@@ -1337,7 +1337,8 @@ static int run_batched_f32(bv_index *idx, const float *d_q, uint32_t nq, uint32_
 // bound, |c|_2 |R|_2 times the row scale.  A dense pass over MQ_SAMPLE
 // strided rows gives each query its kprime-th best lower-bound key (kprime
 // rows have exact keys at or above it); the pass over every row keeps the
-// rows whose upper bound reaches it, with their bounds; the kprime-th best
+// rows whose upper bound reaches it, with their bounds (in two parts, the
+// second under the bound the first part's rows give); the kprime-th best
 // lower bound among those is a tighter bound, and only the rows whose upper
 // bound reaches it can be in the top kprime.  Those rows get their exact
 // keys with the single-query arithmetic (three exact level dots, f64
@@ -1379,7 +1380,10 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     const uint32_t units16 = idx->P / 16;
 
     timing_begin(idx);
-    HIPX(idx->dev, launch_mq1_qconst(qlev, qstride, units16, units16 * 48, nq, idx->mq_rq.as<float>(), s),
+    // the query bounds, and the sample pass's key count per query
+    HIPX(idx->dev,
+         launch_mq1_qconst(qlev, qstride, units16, units16 * 48, nq, idx->mq_rq.as<float>(),
+                           idx->mq_cnt.as<uint32_t>(), (uint32_t)S, s),
          "query bound kernel");
     Mq1Args m{};
     m.codes = idx->codes.as<uint32_t>();
@@ -1400,7 +1404,6 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     m.row_step = N / S;
     m.cand = idx->mq_cand.as<uint64_t>();
     m.cap = S;
-    HIPX(idx->dev, hipMemsetD32Async((hipDeviceptr_t)idx->mq_cnt.p, (int)S, nq, s), "scratch");
     HIPX(idx->dev, launch_mq1_scan(m, s), "batched scan kernel");
     MqSelArgs sa{};
     sa.cand = m.cand;
@@ -1409,22 +1412,42 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     sa.kk = kprime;
     sa.tau = idx->mq_tau.as<uint64_t>();
     HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
-    // full pass: every row whose upper bound reaches the sample's bound, into
-    // the workgroups' buckets, then one list per query
-    m.n = N;
-    m.row_step = 1;
+    // the pass over every row keeps the rows whose upper bound reaches the
+    // bound, into the workgroups' buckets, then one list per query.  It runs
+    // in two parts: the first eighth of the rows, whose kept rows' kprime-th
+    // best lower bound (a bound for the same reason) is far tighter than the
+    // sample's, then the rest under the tighter of the two
+    const uint64_t NA = std::max<uint64_t>(MQ1_ROWS, N / 8 / MQ1_ROWS * MQ1_ROWS);
     m.tau = idx->mq_tau.as<uint64_t>();
-    m.cand = idx->mq_bk.as<uint64_t>();
     m.up_out = idx->mq_bu.as<uint32_t>();
     m.cnt = idx->mq_bc.as<uint32_t>();
     m.cap = cap;
     m.capw = capw;
-    HIPX(idx->dev, launch_mq1_scan(m, s), "batched scan kernel");
-    HIPX(idx->dev,
-         launch_mq1_compact(idx->mq_bk.as<uint64_t>(), idx->mq_bu.as<uint32_t>(), idx->mq_bc.as<uint32_t>(), nwg,
-                            capw, cap, idx->mq_cand.as<uint64_t>(), idx->mq_up.as<uint32_t>(),
-                            idx->mq_cnt.as<uint32_t>(), nq, s),
-         "batched compact kernel");
+    m.row_step = 1;
+    for (int part = 0; part < 2; ++part) {
+        const uint64_t r0 = part ? NA : 0, rn = part ? N - NA : NA;
+        if (rn == 0) break;
+        m.n = rn;
+        m.row_base = r0;
+        m.codes = idx->codes.as<uint32_t>() + r0 * idx->words_per_row;
+        m.scales = idx->scales.as<float>() + r0;
+        m.cn = idx->cnorm.as<float>() + r0;
+        m.cand = idx->mq_bk.as<uint64_t>();
+        HIPX(idx->dev, launch_mq1_scan(m, s), "batched scan kernel");
+        HIPX(idx->dev,
+             launch_mq1_compact(idx->mq_bk.as<uint64_t>(), idx->mq_bu.as<uint32_t>(), idx->mq_bc.as<uint32_t>(),
+                                nwg, capw, cap, idx->mq_cand.as<uint64_t>(), idx->mq_up.as<uint32_t>(),
+                                idx->mq_cnt.as<uint32_t>(), part > 0, nq, s),
+             "batched compact kernel");
+        if (part == 0) {  // the tighter bound
+            sa.cap = cap;
+            sa.tau_max = true;
+            HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+            sa.tau_max = false;
+        }
+    }
+    m.codes = idx->codes.as<uint32_t>();
+    m.scales = idx->scales.as<float>();
     m.cand = idx->mq_cand.as<uint64_t>();
     m.up_out = idx->mq_up.as<uint32_t>();
     m.cnt = idx->mq_cnt.as<uint32_t>();

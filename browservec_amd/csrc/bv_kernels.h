@@ -261,6 +261,7 @@ struct MqSelArgs {
     uint64_t *merged;         // [nq][kk]
     uint32_t *merged_n;
     uint32_t *overflow;
+    bool tau_max;             // tau[q] = max(tau[q], the kk-th best key)
     uint32_t k_out;
     uint32_t *out_rows;       // [nq][k_out]
     float *out_scores;
@@ -294,7 +295,8 @@ struct Mq1Args {
     uint32_t W;               // words per row
     uint32_t units;           // 16-code units per row (even), P / 16
     uint64_t n;               // logical rows in this pass
-    uint64_t row_step;        // physical row of logical row i = i * row_step
+    uint64_t row_step;        // logical row i reads row i * row_step of codes / scales / cn ...
+    uint64_t row_base;        // ... and is row row_base + i * row_step in the keys
     const unsigned char *qlev;// nq x qstride bytes: packed levels (16-code units) + QLevelTail
     uint64_t qstride;
     uint32_t tail_off;
@@ -311,11 +313,12 @@ struct Mq1Args {
     uint64_t cap;
     uint32_t capw;            // threshold: entries per bucket
 };
-// Per query: its buckets joined into lk / uo [nq][cap] and the length in
-// cnt[q] (0xffffffff when a bucket overflowed or the total exceeds cap).
+// Per query: its buckets joined into lk / uo [nq][cap] (after the list's
+// cnt[q] entries when append is set) and the length in cnt[q] (0xffffffff
+// when a bucket overflowed or the total exceeds cap).
 hipError_t launch_mq1_compact(const uint64_t *bk, const uint32_t *bu, const uint32_t *bc, uint32_t nwg,
-                              uint32_t capw, uint64_t cap, uint64_t *lk, uint32_t *uo, uint32_t *cnt, uint32_t nq,
-                              hipStream_t s);
+                              uint32_t capw, uint64_t cap, uint64_t *lk, uint32_t *uo, uint32_t *cnt, bool append,
+                              uint32_t nq, hipStream_t s);
 // Per query: the rows among cand[q][0, min(cnt[q], cap)) whose upper bound
 // (make_key(up[q][i], row)) reaches tau[q], into rows[q][...], their number
 // in kept[q].
@@ -328,7 +331,7 @@ hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scal
                             uint64_t cap, uint64_t *keys, uint32_t nq, hipStream_t s);
 hipError_t launch_row_code_norms(const uint32_t *codes, uint64_t n, uint32_t W, float *cn, hipStream_t s);
 hipError_t launch_mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32_t units, uint32_t tail_off,
-                             uint32_t nq, float *rq, hipStream_t s);
+                             uint32_t nq, float *rq, uint32_t *cnt, uint32_t cnt_value, hipStream_t s);
 hipError_t launch_mq1_scan(const Mq1Args &a, hipStream_t s);
 hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s);
 // fp32 rows (dot / cosine): a.codes = the rows, a.W = dim, a.units = dim / 8,

@@ -42,6 +42,24 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
 
+// A 16-byte (dwordx4) or 4-byte global load into LDS at lds + 16 * lane (4 *
+// lane), written as inline asm so that the compiler does not track it: it
+// would otherwise take every later LDS read as possibly racing with it and
+// wait for all outstanding LDS operations before each one.  The caller waits
+// for these loads itself (vmcnt) before the LDS is read.  They set M0, which
+// the compiler reserves and does not track across inline asm: no other code
+// in the kernels that use them keeps a value in M0.
+// lds: a wave-uniform LDS byte address (lds_addr), kept in an SGPR.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void *)p);
+}
+__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory");
+}
+
 // s_waitcnt immediate waiting for vmcnt <= n (n < 64) only (gfx9 encoding:
 // vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8 left at their maxima).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -289,7 +307,7 @@ __device__ __forceinline__ void mq1_epilogue(const Mq1Args &a, const v16i &acc, 
             const uint64_t li = t0 + row_of(r);
             if (full || li < a.n) {
                 const float lo = mq1_lower(acc[r], s0f, bv[r], sv[r]);
-                out[li] = make_key(lo == lo ? ord_f32(lo) : 0u, (uint32_t)(li * a.row_step));
+                out[li] = make_key(lo == lo ? ord_f32(lo) : 0u, (uint32_t)(a.row_base + li * a.row_step));
             }
         }
         return;
@@ -326,7 +344,8 @@ __device__ __forceinline__ void mq1_epilogue(const Mq1Args &a, const v16i &acc, 
         for (int k = 0; k < 16; ++k)
             if ((uint32_t)k == bit) d = acc[k], s_ = sv[k], b_ = bv[k];
         const float lo = mq1_lower(d, s0f, b_, s_), up = mq1_upper(d, s0f, b_, s_);
-        st.lk[sb][wave][pos] = make_key(lo == lo ? ord_f32(lo) : 0u, (uint32_t)((t0 + row_of(bit)) * a.row_step));
+        st.lk[sb][wave][pos] =
+            make_key(lo == lo ? ord_f32(lo) : 0u, (uint32_t)(a.row_base + (t0 + row_of(bit)) * a.row_step));
         st.uo[sb][wave][pos] = up == up ? ord_f32(up) : 0xffffffffu;
     }
 }
@@ -576,21 +595,21 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan(Mq1Args a) {
     // (one dword per lane, lanes 0 .. 31)
     auto load_tile = [&](uint64_t k, v4i *tl, float *sc, float *cs) {
         const uint64_t t = wg + k * a.nwg;
+        const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+        const uint32_t lb = lds_addr(&tl[wv * PER_WAVE * RS]);
         if ((uint32_t)lane < U) {
 #pragma unroll
             for (uint32_t j = 0; j < PER_WAVE; ++j) {
-                const uint32_t r = (uint32_t)wave * PER_WAVE + j;
-                uint64_t li = t * MQ1_ROWS + r;
+                uint64_t li = t * MQ1_ROWS + wv * PER_WAVE + j;
                 if (li >= a.n) li = a.n - 1;  // rows past the end load a valid row; their results are dropped
-                const v4i *src = (const v4i *)(a.codes + li * a.row_step * a.W) + lane;
-                __builtin_amdgcn_global_load_lds((glb_void *)src, (lds_void *)&tl[r * RS], 16, 0, 0);
+                lds_dma16((const v4i *)(a.codes + li * a.row_step * a.W) + lane, lb + j * RS * 16);
             }
         }
-        if (wave == 0 && lane < MQ1_ROWS) {
+        if (wv == 0 && lane < MQ1_ROWS) {
             uint64_t li = t * MQ1_ROWS + (uint32_t)lane;
             if (li >= a.n) li = a.n - 1;
-            __builtin_amdgcn_global_load_lds((glb_void *)(a.scales + li * a.row_step), (lds_void *)sc, 4, 0, 0);
-            __builtin_amdgcn_global_load_lds((glb_void *)(a.cn + li * a.row_step), (lds_void *)cs, 4, 0, 0);
+            lds_dma4(a.scales + li * a.row_step, lds_addr(sc));
+            lds_dma4(a.cn + li * a.row_step, lds_addr(cs));
         }
     };
     // tile k from (tl, sc, cs), staging into buffer k & 1, while tile k + 3
@@ -678,37 +697,58 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan(Mq1Args a) {
 }
 
 // One workgroup per query: the workgroups' buckets of the query joined into
-// one list (bucket order), and its length; a query with an overflowed
-// bucket or more than cap entries gets length 0xffffffff (it falls back).
-__global__ __launch_bounds__(256) void mq1_compact(const uint64_t *bk, const uint32_t *bu, const uint32_t *bc,
-                                                    uint32_t nwg, uint32_t capw, uint64_t cap, uint64_t *lk,
-                                                    uint32_t *uo, uint32_t *cnt) {
+// one list (bucket order; appended after the list's cnt[q] entries when
+// append is set), and its length; a query with an overflowed bucket or more
+// than cap entries gets length 0xffffffff (it falls back).
+__global__ __launch_bounds__(1024) void mq1_compact(const uint64_t *bk, const uint32_t *bu, const uint32_t *bc,
+                                                     uint32_t nwg, uint32_t capw, uint64_t cap, uint64_t *lk,
+                                                     uint32_t *uo, uint32_t *cnt, int append) {
     __shared__ uint32_t off[1025];
+    __shared__ uint32_t wsum[16];
     __shared__ uint32_t bad;
     const uint32_t q = blockIdx.x, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const uint32_t base = append ? cnt[q] : 0u;  // entries already in the list
+    if ((uint64_t)base > cap) return;             // already overflowed
     if (tid == 0) bad = 0;
     __syncthreads();
-    // counts, then an exclusive prefix over the buckets (one thread per bucket; nwg <= 1024)
-    for (uint32_t w = tid; w < nwg; w += 256) {
-        const uint32_t c = bc[(uint64_t)q * nwg + w];
-        if (c > capw) bad = 1;
-        off[w + 1] = c > capw ? 0u : c;
+    // bucket lengths (one thread per bucket; nwg <= 1024) and their exclusive
+    // prefix: within each wave, then across the waves
+    uint32_t c = 0;
+    if (tid < nwg) {
+        c = bc[(uint64_t)q * nwg + tid];
+        if (c > capw) {
+            bad = 1;
+            c = 0;
+        }
+    }
+    uint32_t incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int w = 0; w < wave; ++w) before += wsum[w];
+    if (tid < nwg) off[tid] = before + incl - c;
+    if (tid == 1023) {
+        uint32_t t = 0;
+        for (int w = 0; w < 16; ++w) t += wsum[w];
+        off[nwg] = t;
     }
     __syncthreads();
-    if (tid == 0) {
-        off[0] = 0;
-        for (uint32_t w = 0; w < nwg; ++w) off[w + 1] += off[w];
-    }
-    __syncthreads();
-    const uint32_t total = off[nwg];
+    const uint32_t total = base + off[nwg];
     if (bad || total > cap) {
         if (tid == 0) cnt[q] = 0xffffffffu;
         return;
     }
-    for (uint32_t w = 0; w < nwg; ++w) {
+    // wave v copies buckets v, v + 16, ...
+    for (uint32_t w = wave; w < nwg; w += 16) {
         const uint32_t n = off[w + 1] - off[w];
-        const uint64_t src = ((uint64_t)q * nwg + w) * capw, dst = (uint64_t)q * cap + off[w];
-        for (uint32_t i = tid; i < n; i += 256) {
+        const uint64_t src = ((uint64_t)q * nwg + w) * capw, dst = (uint64_t)q * cap + base + off[w];
+        for (uint32_t i = lane; i < n; i += 64) {
             lk[dst + i] = bk[src + i];
             uo[dst + i] = bu[src + i];
         }
@@ -1052,7 +1092,10 @@ __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
     sort_desc(sel, npow);
     const uint32_t m = got < kk ? got : kk;
     if (tid == 0) {
-        if (a.tau) a.tau[q] = n > kk ? sel[kk - 1] : 0ull;
+        if (a.tau) {
+            const uint64_t t = n > kk ? sel[kk - 1] : 0ull;
+            a.tau[q] = a.tau_max && a.tau[q] > t ? a.tau[q] : t;
+        }
         if (a.merged_n) a.merged_n[q] = m;
         if (a.overflow) a.overflow[q] = (uint64_t)total > a.cap ? 1u : 0u;
     }
@@ -1075,7 +1118,7 @@ __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
 // so fma adds it with the reference's single rounding); lanes 4c .. 4c + 3
 // then combine as ((a0 + a1) + a2) + a3 and add the tail elements in order.
 // Sixteen candidates per wave run at once.
-constexpr int RR_THREADS = 256;
+constexpr int RR_THREADS = 1024;
 __global__ __launch_bounds__(RR_THREADS) void mq_rerank(MqRerankArgs a) {
     extern __shared__ float qv[];  // the query, dim floats
     __shared__ uint64_t ek[MAX_KPRIME];
@@ -1095,6 +1138,14 @@ __global__ __launch_bounds__(RR_THREADS) void mq_rerank(MqRerankArgs a) {
         const float *x = a.rows + (uint64_t)row * dim;
         double acc = 0.0;
         uint32_t j = ai;
+        // 32 of the lane's elements loaded at once, then summed in order
+        for (; j + 124 < vec; j += 128) {
+            float xv[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) xv[u] = x[j + 4 * u];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) acc = fma((double)xv[u], (double)qv[j + 4 * u], acc);
+        }
         for (; j + 28 < vec; j += 32) {
             float xv[8];
 #pragma unroll
@@ -1195,9 +1246,9 @@ __global__ __launch_bounds__(256) void row_code_norms(const uint32_t *codes, uin
 
 // One wave per query: rq >= |R|_2 for R = s1 q1 + s2 q2, the part of the
 // query the level-one prefilter leaves out (f64 sum, 2^-18 added, rounded up
-// to f32).
+// to f32); cnt[q] = cnt_value when cnt is set (the dense pass's key count).
 __global__ __launch_bounds__(64) void mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32_t units,
-                                                 uint32_t tail_off, float *rq) {
+                                                 uint32_t tail_off, float *rq, uint32_t *cnt, uint32_t cnt_value) {
     const int lane = threadIdx.x;
     const unsigned char *src = qlev + (uint64_t)blockIdx.x * qstride;
     const QLevelTail *t = (const QLevelTail *)(src + tail_off);
@@ -1215,6 +1266,7 @@ __global__ __launch_bounds__(64) void mq1_qconst(const unsigned char *qlev, uint
         float f = (float)v;
         if ((double)f < v) f = next_up(f);
         rq[blockIdx.x] = f;
+        if (cnt) cnt[blockIdx.x] = cnt_value;
     }
 }
 
@@ -1248,42 +1300,66 @@ __global__ __launch_bounds__(1024) void mq1_keep(const uint64_t *cand, const uin
 // combine, row scale), into keys[q][i].  Sixteen lanes per row, four rows
 // per wave at a time: each load instruction reads 256 contiguous bytes of
 // four rows.
-__global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, uint32_t W, const float *scales,
-                                                   const unsigned char *qlev, uint64_t qstride, uint32_t units16,
+// Sum over the 16 lanes of a DPP row, in every lane of the row.
+__device__ __forceinline__ int row16_sum(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false);  // row_ror:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x124, 0xf, 0xf, false);  // row_ror:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x122, 0xf, 0xf, false);  // row_ror:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x121, 0xf, 0xf, false);  // row_ror:1
+    return x;
+}
+
+template <int UNITS>
+__global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, const float *scales,
+                                                   const unsigned char *qlev, uint64_t qstride,
                                                    const uint32_t *rows, const uint32_t *kept, uint64_t cap,
                                                    uint64_t *keys) {
-    __shared__ v4i ql[MQ_MAX_STEPS * 2 * 3];  // the query's packed levels: unit u, level l at 3u + l
+    constexpr int PER = UNITS < 16 ? 1 : UNITS / 16;  // units per lane (lanes >= UNITS idle when UNITS < 16)
+    constexpr uint32_t W = UNITS * 4;
+    __shared__ v4i ql[UNITS * 3];  // the query's packed levels: unit u, level l at 3u + l
     const uint32_t q = blockIdx.x, tid = threadIdx.x;
     const unsigned char *src = qlev + (uint64_t)q * qstride;
-    for (uint32_t i = tid; i < units16 * 3; i += 1024) ql[i] = ((const v4i *)src)[i];
-    const QLevelTail *t = (const QLevelTail *)(src + (uint64_t)units16 * 48);
+    for (uint32_t i = tid; i < UNITS * 3; i += 1024) ql[i] = ((const v4i *)src)[i];
+    const QLevelTail *t = (const QLevelTail *)(src + (uint64_t)UNITS * 48);
     const double s0 = t->s[0], s1 = t->s[1], s2 = t->s[2];
     __syncthreads();
     const uint32_t n = kept[q];
     const uint32_t *rq = rows + (uint64_t)q * cap;
     uint64_t *out = keys + (uint64_t)q * cap;
-    const int lane = tid & 63, l16 = lane & 15;
-    for (uint32_t i = tid >> 4; i < n; i += 64) {  // the 16 lanes of a row step together
-        const uint32_t row = rq[i];
-        const v4i *x = (const v4i *)(codes + (uint64_t)row * W);
-        int d0 = 0, d1 = 0, d2 = 0;
-        for (uint32_t u = l16; u < units16; u += 16) {
-            const v4i c = x[u];
-            const v4i a0 = ql[3 * u], a1 = ql[3 * u + 1], a2 = ql[3 * u + 2];
+    const int l16 = tid & 15;
+    // the 16 lanes of a DPP row take one row; two rows per step in flight
+    for (uint32_t i = tid >> 4; i < n; i += 128) {
+        const uint32_t i2 = i + 64 < n ? i + 64 : i;
+        const uint32_t ra = rq[i], rb = rq[i2];
+        const v4i *xa = (const v4i *)(codes + (uint64_t)ra * W), *xb = (const v4i *)(codes + (uint64_t)rb * W);
+        v4i ca[PER], cb[PER];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int u = l16 + 16 * j;
+            ca[j] = u < UNITS ? xa[u] : v4i{};
+            cb[j] = u < UNITS ? xb[u] : v4i{};
+        }
+        const float sa = scales[ra], sb = scales[rb];
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int u = l16 + 16 * j;
+            if (u >= UNITS) continue;
+            const v4i q0 = ql[3 * u], q1 = ql[3 * u + 1], q2 = ql[3 * u + 2];
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                d0 = __builtin_amdgcn_sdot4(c[w], a0[w], d0, false);
-                d1 = __builtin_amdgcn_sdot4(c[w], a1[w], d1, false);
-                d2 = __builtin_amdgcn_sdot4(c[w], a2[w], d2, false);
+                a0 = __builtin_amdgcn_sdot4(ca[j][w], q0[w], a0, false);
+                a1 = __builtin_amdgcn_sdot4(ca[j][w], q1[w], a1, false);
+                a2 = __builtin_amdgcn_sdot4(ca[j][w], q2[w], a2, false);
+                b0 = __builtin_amdgcn_sdot4(cb[j][w], q0[w], b0, false);
+                b1 = __builtin_amdgcn_sdot4(cb[j][w], q1[w], b1, false);
+                b2 = __builtin_amdgcn_sdot4(cb[j][w], q2[w], b2, false);
             }
         }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            d0 += __shfl_xor(d0, o);
-            d1 += __shfl_xor(d1, o);
-            d2 += __shfl_xor(d2, o);
-        }
-        if (l16 == 0) out[i] = q_key(s0, s1, s2, d0, d1, d2, scales[row], row);
+        a0 = row16_sum(a0), a1 = row16_sum(a1), a2 = row16_sum(a2);
+        b0 = row16_sum(b0), b1 = row16_sum(b1), b2 = row16_sum(b2);
+        if (l16 == 0) out[i] = q_key(s0, s1, s2, a0, a1, a2, sa, ra);
+        if (l16 == 1 && i2 != i) out[i2] = q_key(s0, s1, s2, b0, b1, b2, sb, rb);
     }
 }
 
@@ -1293,18 +1369,30 @@ hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scal
                             uint64_t qstride, uint32_t units16, const uint32_t *rows, const uint32_t *kept,
                             uint64_t cap, uint64_t *keys, uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
-    if (units16 == 0 || units16 > MQ_MAX_STEPS * 2 || W != units16 * 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(mq1_exact, dim3(nq), dim3(1024), 0, s, codes, W, scales, qlev, qstride, units16, rows, kept,
-                       cap, keys);
+    if (W != units16 * 4) return hipErrorInvalidValue;
+#define BV_EX_CASE(U)                                                                                         \
+    case U: hipLaunchKernelGGL(mq1_exact<U>, dim3(nq), dim3(1024), 0, s, codes, scales, qlev, qstride, rows, \
+                               kept, cap, keys); break;
+    switch (units16) {
+        BV_EX_CASE(2)
+        BV_EX_CASE(4)
+        BV_EX_CASE(8)
+        BV_EX_CASE(16)
+        BV_EX_CASE(32)
+        BV_EX_CASE(64)
+    default: return hipErrorInvalidValue;
+    }
+#undef BV_EX_CASE
     return hipGetLastError();
 }
 
 hipError_t launch_mq1_compact(const uint64_t *bk, const uint32_t *bu, const uint32_t *bc, uint32_t nwg,
-                              uint32_t capw, uint64_t cap, uint64_t *lk, uint32_t *uo, uint32_t *cnt, uint32_t nq,
-                              hipStream_t s) {
+                              uint32_t capw, uint64_t cap, uint64_t *lk, uint32_t *uo, uint32_t *cnt, bool append,
+                              uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
     if (nwg == 0 || nwg > 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(mq1_compact, dim3(nq), dim3(256), 0, s, bk, bu, bc, nwg, capw, cap, lk, uo, cnt);
+    hipLaunchKernelGGL(mq1_compact, dim3(nq), dim3(1024), 0, s, bk, bu, bc, nwg, capw, cap, lk, uo, cnt,
+                       append ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -1324,9 +1412,9 @@ hipError_t launch_row_code_norms(const uint32_t *codes, uint64_t n, uint32_t W, 
 }
 
 hipError_t launch_mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32_t units, uint32_t tail_off,
-                             uint32_t nq, float *rq, hipStream_t s) {
+                             uint32_t nq, float *rq, uint32_t *cnt, uint32_t cnt_value, hipStream_t s) {
     if (nq == 0) return hipSuccess;
-    hipLaunchKernelGGL(mq1_qconst, dim3(nq), dim3(64), 0, s, qlev, qstride, units, tail_off, rq);
+    hipLaunchKernelGGL(mq1_qconst, dim3(nq), dim3(64), 0, s, qlev, qstride, units, tail_off, rq, cnt, cnt_value);
     return hipGetLastError();
 }
 
