@@ -113,6 +113,8 @@ SIGNATURES = {
     "bv_index_build": [vp],
     "bv_index_export_ivf": [vp, vp, vp, vp],
     "bv_index_export_probe_scores": [vp, vp, u32, vp],
+    "bv_index_save_section": [vp, vp, u64, vp],
+    "bv_index_load_section": [vp, vp, u64, u64, vp, u64],
 }
 _RESTYPE = {"bv_last_error": ctypes.c_char_p}
 

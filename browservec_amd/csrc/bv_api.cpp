@@ -2166,6 +2166,262 @@ extern "C" int bv_index_export_probe_scores(bv_index *idx, const float *queries,
     return BV_OK;
 }
 
+// ------------------------------------------------------------ index section
+// A snapshot section holding what a load would otherwise re-derive: the
+// codes and scales (re-encoded from the rows and the fixed seed,
+// src/index.ts:673-700) and the IVF state (reservoir, centroids, CSR lists,
+// tuned nprobe; rebuilt on the first query after a load).  It sits beside
+// the reference snapshot's fp32 rows, as the HNSW graph section does
+// (src/persist/format.ts:1-22).  Little-endian; blocks 8-byte aligned.
+namespace {
+constexpr uint32_t SECTION_MAGIC = 0x58495642u;  // "BVIX"
+constexpr uint32_t SECTION_VERSION = 1;
+struct SectionHeader {
+    uint32_t magic, version, header_bytes, reserved;
+    uint32_t kind, dim, metric, bits, scorer, seed, rounds;
+    uint32_t nlist_desc, sample_size, train_size, iters, ivf_seed, has_ivf_seed;
+    float target_recall;
+    uint64_t count;
+    uint32_t P, words_per_row, nlist, built;
+    uint64_t built_rows;
+    uint32_t sample_cap, sample_dim;
+    uint64_t sample_filled, sample_seen;
+    uint32_t sample_rng, tuned_nprobe;
+    float tuned_recall;
+    uint32_t pad;
+};
+static_assert(sizeof(SectionHeader) % 8 == 0, "section header alignment");
+
+inline uint64_t pad8(uint64_t n) { return (n + 7) & ~7ull; }
+
+SectionHeader section_header(const bv_index *idx) {
+    SectionHeader h{};
+    h.magic = SECTION_MAGIC;
+    h.version = SECTION_VERSION;
+    h.header_bytes = sizeof(SectionHeader);
+    h.kind = idx->d.kind;
+    h.dim = idx->d.dim;
+    h.metric = idx->d.metric;
+    h.bits = idx->d.bits;
+    h.scorer = idx->d.scorer;
+    h.seed = idx->d.seed;
+    h.rounds = idx->d.rounds;
+    h.nlist_desc = idx->d.nlist;
+    h.sample_size = idx->d.sample_size;
+    h.train_size = idx->d.train_size;
+    h.iters = idx->d.iters;
+    h.ivf_seed = idx->d.ivf_seed;
+    h.has_ivf_seed = idx->d.has_ivf_seed;
+    h.target_recall = idx->d.target_recall;
+    h.count = idx->rows;
+    h.P = idx->P;
+    h.words_per_row = idx->words_per_row;
+    h.nlist = idx->nlist;
+    h.built = idx->ivf && idx->rows && idx->built_rows == idx->rows ? 1u : 0u;
+    h.built_rows = h.built ? idx->built_rows : 0;
+    h.sample_cap = idx->sample_cap;
+    h.sample_dim = idx->sample_dim;
+    h.sample_filled = idx->sample_filled;
+    h.sample_seen = idx->sample_seen;
+    h.sample_rng = idx->sample_rng;
+    h.tuned_nprobe = idx->tuned_nprobe;
+    h.tuned_recall = idx->tuned_recall;
+    return h;
+}
+
+// Block sizes in section order: scales, codes (quantized kinds); reservoir
+// rows, reservoir row ids (IVF); centroids, list offsets, list rows (built IVF).
+std::vector<uint64_t> section_blocks(const SectionHeader &h, bool quant, bool ivf, uint32_t row_bytes) {
+    std::vector<uint64_t> b;
+    if (quant) {
+        b.push_back(h.count * 4);
+        b.push_back(h.count * row_bytes);
+    }
+    if (ivf) {
+        b.push_back(h.sample_filled * h.sample_dim * 4);
+        b.push_back(h.sample_filled * 8);
+        if (h.built) {
+            b.push_back((uint64_t)h.nlist * h.sample_dim * 4);
+            b.push_back(((uint64_t)h.nlist + 1) * 4);
+            b.push_back(h.built_rows * 4);
+        }
+    }
+    return b;
+}
+
+uint64_t section_bytes(const std::vector<uint64_t> &blocks) {
+    uint64_t n = sizeof(SectionHeader);
+    for (uint64_t b : blocks) n += pad8(b);
+    return n;
+}
+}  // namespace
+
+extern "C" int bv_index_save_section(bv_index *idx, void *buf, uint64_t cap, uint64_t *size) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!size) return fail(BV_E_INVALID, "null argument");
+    const SectionHeader h = section_header(idx);
+    const std::vector<uint64_t> blocks = section_blocks(h, idx->quant, idx->ivf, idx->row_bytes);
+    const uint64_t total = section_bytes(blocks);
+    *size = total;
+    if (!buf || cap < total) return BV_OK;
+    unsigned char *out = (unsigned char *)buf;
+    std::memset(out, 0, total);
+    std::memcpy(out, &h, sizeof(h));
+    uint64_t at = sizeof(h);
+    std::vector<const void *> src;
+    if (idx->quant) {
+        src.push_back(idx->scales.p);
+        src.push_back(idx->codes.p);
+    }
+    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "save");
+    size_t bi = 0;
+    for (; bi < src.size(); ++bi) {
+        if (blocks[bi]) HIPX(idx->dev, hipMemcpy(out + at, src[bi], blocks[bi], hipMemcpyDeviceToHost), "download");
+        at += pad8(blocks[bi]);
+    }
+    if (idx->ivf) {
+        if (blocks[bi])
+            HIPX(idx->dev, hipMemcpy(out + at, idx->sample.p, blocks[bi], hipMemcpyDeviceToHost), "download");
+        at += pad8(blocks[bi++]);
+        if (blocks[bi]) std::memcpy(out + at, idx->sample_row.data(), blocks[bi]);
+        at += pad8(blocks[bi++]);
+        if (h.built) {
+            const void *dsrc[3] = {idx->centroids.p, idx->list_off.p, idx->list_rows.p};
+            for (int j = 0; j < 3; ++j, ++bi) {
+                if (blocks[bi])
+                    HIPX(idx->dev, hipMemcpy(out + at, dsrc[j], blocks[bi], hipMemcpyDeviceToHost), "download");
+                at += pad8(blocks[bi]);
+            }
+        }
+    }
+    return BV_OK;
+}
+
+extern "C" int bv_index_load_section(bv_index *idx, const float *data, uint64_t n_floats, uint64_t count,
+                                     const void *section, uint64_t bytes) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (!section || (count && !data)) return fail(BV_E_INVALID, "null argument");
+    if (idx->rows) return fail(BV_E_STATE, "a section loads into an empty index");
+    if (n_floats != count * idx->dim)
+        return fail(BV_E_INVALID, "expected %llu floats, got %llu", (unsigned long long)(count * idx->dim),
+                    (unsigned long long)n_floats);
+    SectionHeader h{};
+    if (bytes < sizeof(h)) return fail(BV_E_INVALID, "index section truncated (%llu bytes)", (unsigned long long)bytes);
+    std::memcpy(&h, section, sizeof(h));
+    if (h.magic != SECTION_MAGIC || h.header_bytes != sizeof(h)) return fail(BV_E_INVALID, "not an index section");
+    if (h.version != SECTION_VERSION) return fail(BV_E_UNSUPPORTED, "index section version %u", h.version);
+    const SectionHeader mine = section_header(idx);
+    if (h.kind != mine.kind || h.dim != mine.dim || h.metric != mine.metric || h.bits != mine.bits ||
+        h.scorer != mine.scorer || h.seed != mine.seed || h.rounds != mine.rounds || h.nlist_desc != mine.nlist_desc ||
+        h.sample_size != mine.sample_size || h.train_size != mine.train_size || h.iters != mine.iters ||
+        h.ivf_seed != mine.ivf_seed || h.has_ivf_seed != mine.has_ivf_seed || h.P != mine.P ||
+        h.words_per_row != mine.words_per_row || h.sample_cap != mine.sample_cap || h.sample_dim != mine.sample_dim ||
+        std::memcmp(&h.target_recall, &mine.target_recall, 4) != 0)
+        return fail(BV_E_INVALID, "the index section was saved from an index with a different configuration");
+    if (h.count != count)
+        return fail(BV_E_INVALID, "the index section holds %llu rows, got %llu", (unsigned long long)h.count,
+                    (unsigned long long)count);
+    if (idx->ivf && (h.sample_filled > h.sample_cap || h.sample_filled > h.count || h.sample_seen < h.sample_filled ||
+                     (h.built && (h.built_rows != h.count || h.nlist == 0 || h.nlist > IVF_MAX_NLIST))))
+        return fail(BV_E_INVALID, "index section: inconsistent IVF state");
+    const std::vector<uint64_t> blocks = section_blocks(h, idx->quant, idx->ivf, idx->row_bytes);
+    if (bytes != section_bytes(blocks))
+        return fail(BV_E_INVALID, "index section has %llu bytes, expected %llu", (unsigned long long)bytes,
+                    (unsigned long long)section_bytes(blocks));
+    const unsigned char *in = (const unsigned char *)section;
+    std::vector<uint64_t> at(blocks.size());
+    uint64_t pos = sizeof(h);
+    for (size_t j = 0; j < blocks.size(); ++j) {
+        at[j] = pos;
+        pos += pad8(blocks[j]);
+    }
+    if (idx->ivf && h.built) {  // the lists must be a valid CSR over the rows
+        const uint32_t *off = (const uint32_t *)(in + at[blocks.size() - 2]);
+        const uint32_t *lr = (const uint32_t *)(in + at[blocks.size() - 1]);
+        if (off[0] != 0 || off[h.nlist] != h.built_rows) return fail(BV_E_INVALID, "index section: bad list offsets");
+        for (uint32_t c = 0; c < h.nlist; ++c)
+            if (off[c + 1] < off[c]) return fail(BV_E_INVALID, "index section: bad list offsets");
+        for (uint64_t r = 0; r < h.built_rows; ++r)
+            if (lr[r] >= h.count) return fail(BV_E_INVALID, "index section: list row out of range");
+    }
+    if (idx->ivf) {
+        const uint64_t *sr = (const uint64_t *)(in + at[idx->quant ? 3 : 1]);
+        for (uint64_t j = 0; j < h.sample_filled; ++j)
+            if (sr[j] >= h.count) return fail(BV_E_INVALID, "index section: reservoir row out of range");
+    }
+    // every allocation first, so a failure leaves the index empty
+    const size_t rb = (size_t)idx->dim * 4;
+    hipStream_t s = idx->stream;
+    HIPX(idx->dev, idx->raw.ensure(std::max<uint64_t>(count, 1) * rb, 0, s), "row buffer");
+    const bool norms = !idx->quant && !idx->ivf;
+    const bool code_norms = idx->codec == C_Q8 && !idx->ivf;
+    if (norms) HIPX(idx->dev, idx->rsq.ensure(std::max<uint64_t>(count, 1) * 4, 0, s), "norm buffer");
+    if (code_norms) HIPX(idx->dev, idx->cnorm.ensure(std::max<uint64_t>(count, 1) * 4, 0, s), "norm buffer");
+    if (idx->quant) {
+        HIPX(idx->dev, idx->scales.ensure(std::max<uint64_t>(count, 1) * 4, 0, s), "scale buffer");
+        HIPX(idx->dev, idx->codes.ensure(std::max<uint64_t>(count, 1) * idx->row_bytes, 0, s), "code buffer");
+    }
+    if (idx->ivf) {
+        HIPX(idx->dev, idx->sample.ensure(std::max<uint64_t>(h.sample_filled, 1) * idx->sample_dim * 4, 0, s),
+             "sample buffer");
+        if (h.built) {
+            HIPX(idx->dev, idx->centroids.ensure((size_t)h.nlist * idx->sample_dim * 4, 0, s), "centroids");
+            HIPX(idx->dev, idx->list_off.ensure(((size_t)h.nlist + 1) * 4, 0, s), "lists");
+            HIPX(idx->dev, idx->list_rows.ensure(std::max<uint64_t>(h.built_rows, 1) * 4, 0, s), "lists");
+        }
+    }
+    if (count) HIPX(idx->dev, hipMemcpyAsync(idx->raw.p, data, count * rb, hipMemcpyHostToDevice, s), "row upload");
+    size_t bi = 0;
+    if (idx->quant) {
+        HIPX(idx->dev, hipMemcpyAsync(idx->scales.p, in + at[0], blocks[0], hipMemcpyHostToDevice, s), "upload");
+        HIPX(idx->dev, hipMemcpyAsync(idx->codes.p, in + at[1], blocks[1], hipMemcpyHostToDevice, s), "upload");
+        bi = 2;
+    }
+    if (norms)
+        HIPX(idx->dev, launch_row_sqnorms(idx->raw.as<float>(), count, idx->dim, idx->rsq.as<float>(),
+                                          idx->rsq_max.as<uint32_t>(), s),
+             "norm kernel");
+    if (code_norms)
+        HIPX(idx->dev, launch_row_code_norms(idx->codes.as<uint32_t>(), count, idx->words_per_row,
+                                             idx->cnorm.as<float>(), s),
+             "norm kernel");
+    if (idx->ivf) {
+        if (blocks[bi])
+            HIPX(idx->dev, hipMemcpyAsync(idx->sample.p, in + at[bi], blocks[bi], hipMemcpyHostToDevice, s),
+                 "upload");
+        ++bi;
+        const uint64_t *sr = (const uint64_t *)(in + at[bi++]);
+        idx->sample_row.assign(sr, sr + h.sample_filled);
+        idx->sample_filled = h.sample_filled;
+        idx->sample_seen = h.sample_seen;
+        idx->sample_rng = h.sample_rng;
+        idx->tuned_nprobe = h.tuned_nprobe;
+        idx->tuned_recall = h.tuned_recall;
+        if (h.built) {
+            void *dst[3] = {idx->centroids.p, idx->list_off.p, idx->list_rows.p};
+            for (int j = 0; j < 3; ++j, ++bi)
+                if (blocks[bi])
+                    HIPX(idx->dev, hipMemcpyAsync(dst[j], in + at[bi], blocks[bi], hipMemcpyHostToDevice, s),
+                         "upload");
+            const uint32_t *off = (const uint32_t *)(in + at[bi - 2]);
+            idx->nlist = h.nlist;
+            idx->list_sizes_desc.resize(h.nlist);
+            for (uint32_t c = 0; c < h.nlist; ++c) idx->list_sizes_desc[c] = off[c + 1] - off[c];
+            std::sort(idx->list_sizes_desc.begin(), idx->list_sizes_desc.end(), std::greater<uint32_t>());
+            idx->built_rows = h.built_rows;
+        }
+    }
+    HIPX(idx->dev, hipStreamSynchronize(s), "load");
+    idx->rows = count;
+    return BV_OK;
+}
+
 extern "C" int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *list_off, uint32_t *list_rows) {
     if (!idx) return fail(BV_E_INVALID, "null index");
     std::lock_guard<std::recursive_mutex> lock(idx->mu);

@@ -225,6 +225,21 @@ class NativeIndex:
         L.check(self.lib.bv_index_export_rotated_query(self.handle, _ptr(q), _ptr(out)))
         return out
 
+    def save_section(self) -> bytes:
+        """The index section of a snapshot: codes, scales and IVF state, so a
+        load skips re-encoding and re-training."""
+        size = ctypes.c_uint64(0)
+        L.check(self.lib.bv_index_save_section(self.handle, None, 0, ctypes.byref(size)))
+        buf = np.empty(size.value, np.uint8)
+        L.check(self.lib.bv_index_save_section(self.handle, _ptr(buf), size.value, ctypes.byref(size)))
+        return buf.tobytes()
+
+    def load_section(self, data, count: int, section: bytes) -> None:
+        """Fills this empty index from a snapshot's rows and a saved section."""
+        data = _f32(data).reshape(-1)
+        sec = np.frombuffer(section, np.uint8)
+        L.check(self.lib.bv_index_load_section(self.handle, _ptr(data), data.size, int(count), _ptr(sec), sec.size))
+
     # device-resident entry points (pointers are integers, e.g. tensor.data_ptr())
     def append_device(self, d_ptr: int, count: int) -> None:
         L.check(self.lib.bv_index_append_device(self.handle, ctypes.c_void_p(d_ptr), int(count)))

@@ -110,7 +110,9 @@ static napi_value length_error(napi_env env, size_t want, size_t got) {
 }
 
 /* ---- asynchronous device calls --------------------------------------------- */
-typedef enum { OP_APPEND, OP_QUERY, OP_QUERY_MASKED, OP_QUERY_BATCH, OP_SEARCH, OP_RERANK, OP_BUILD } op_kind;
+typedef enum {
+    OP_APPEND, OP_QUERY, OP_QUERY_MASKED, OP_QUERY_BATCH, OP_SEARCH, OP_RERANK, OP_BUILD, OP_SAVE, OP_LOAD
+} op_kind;
 
 typedef struct {
     napi_async_work work;
@@ -128,6 +130,9 @@ typedef struct {
     uint32_t nq, k, fetch;
     uint32_t *rows, *counts;
     float *scores;
+    const void *section;  /* loadSection input */
+    void *saved;          /* saveSection output (malloc'd; copied to JS on completion) */
+    uint64_t section_size;
     int rc;
     char msg[512];
 } job;
@@ -149,6 +154,23 @@ static void job_execute(napi_env env, void *data) {
         j->rc = bv_index_rerank(j->idx, j->data, j->aux, (uint32_t)j->n_aux, j->k, j->rows, j->scores, j->counts);
         break;
     case OP_BUILD: j->rc = bv_index_build(j->idx); break;
+    case OP_SAVE: {
+        uint64_t size = 0;
+        j->rc = bv_index_save_section(j->idx, NULL, 0, &size);
+        if (j->rc) break;
+        j->saved = malloc(size ? size : 1);
+        if (!j->saved) {
+            j->rc = BV_E_OOM;
+            snprintf(j->msg, sizeof j->msg, "out of host memory");
+            return;
+        }
+        j->section_size = size;
+        j->rc = bv_index_save_section(j->idx, j->saved, size, &size);
+        break;
+    }
+    case OP_LOAD:
+        j->rc = bv_index_load_section(j->idx, j->data, j->n_floats, j->count, j->section, j->section_size);
+        break;
     }
     /* the message is thread-local: copy it on this thread */
     if (j->rc) snprintf(j->msg, sizeof j->msg, "%s", bv_last_error());
@@ -167,11 +189,25 @@ static void job_complete(napi_env env, napi_status status, void *data) {
         napi_create_string_utf8(env, code_name(j->rc), NAPI_AUTO_LENGTH, &code);
         napi_create_error(env, code, msg, &err);
         napi_reject_deferred(env, j->deferred, err);
+    } else if (j->op == OP_SAVE) {
+        void *dst = NULL;
+        napi_value ab;
+        if (napi_create_arraybuffer(env, j->section_size, &dst, &ab) == napi_ok &&
+            napi_create_typedarray(env, napi_uint8_array, j->section_size, ab, 0, &v) == napi_ok) {
+            memcpy(dst, j->saved, j->section_size);
+            napi_resolve_deferred(env, j->deferred, v);
+        } else {
+            napi_value msg, err;
+            napi_create_string_utf8(env, "out of memory for the index section", NAPI_AUTO_LENGTH, &msg);
+            napi_create_error(env, NULL, msg, &err);
+            napi_reject_deferred(env, j->deferred, err);
+        }
     } else {
         if (j->result) napi_get_reference_value(env, j->result, &v);
         else napi_get_undefined(env, &v);
         napi_resolve_deferred(env, j->deferred, v);
     }
+    free(j->saved);
     for (int i = 0; i < 3; ++i)
         if (j->keep[i]) napi_delete_reference(env, j->keep[i]);
     if (j->result) napi_delete_reference(env, j->result);
@@ -417,6 +453,51 @@ static napi_value build(napi_env env, napi_callback_info info) {
     return queue(env, j, argv[0], "browservec.build");
 }
 
+/* saveSection(idx) -> Promise<Uint8Array>: the index section of a snapshot
+ * (codes, scales, IVF state). */
+static napi_value save_section(napi_env env, napi_callback_info info) {
+    ARGS(1);
+    index_handle *h = get_index(env, argv[0]);
+    if (!h) {
+        napi_throw_type_error(env, NULL, "saveSection(idx)");
+        return NULL;
+    }
+    job *j = new_job(env, OP_SAVE, h);
+    if (!j) {
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    return queue(env, j, argv[0], "browservec.saveSection");
+}
+
+/* loadSection(idx, Float32Array rows, count, Uint8Array section) -> Promise<void>:
+ * fills an empty index from a snapshot's rows and its index section. */
+static napi_value load_section(napi_env env, napi_callback_info info) {
+    ARGS(4);
+    index_handle *h = get_index(env, argv[0]);
+    size_t n = 0, nb = 0;
+    const float *data = (const float *)get_typed(env, argv[1], napi_float32_array, &n);
+    uint32_t count = 0;
+    const void *sec = get_typed(env, argv[3], napi_uint8_array, &nb);
+    if (!h || (!data && n) || !get_u32(env, argv[2], &count) || !sec) {
+        napi_throw_type_error(env, NULL, "loadSection(idx, Float32Array, count, Uint8Array)");
+        return NULL;
+    }
+    if (n != (size_t)count * h->dim) return length_error(env, (size_t)count * h->dim, n);
+    job *j = new_job(env, OP_LOAD, h);
+    if (!j || !keep(env, j, 0, argv[1]) || !keep(env, j, 1, argv[3])) {
+        free(j);
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    j->data = data;
+    j->n_floats = n;
+    j->count = count;
+    j->section = sec;
+    j->section_size = nb;
+    return queue(env, j, argv[0], "browservec.loadSection");
+}
+
 /* query(idx, Float32Array q, k) / queryMasked(idx, q, k, Uint32Array mask) -> Promise<result> */
 static napi_value query_common(napi_env env, napi_callback_info info, int masked) {
     size_t argc = 4;
@@ -565,6 +646,7 @@ static napi_value init(napi_env env, napi_value exports) {
         {"query", query},              {"queryMasked", query_masked},   {"queryBatch", query_batch},
         {"search", search},            {"rerank", rerank},              {"setNprobe", set_nprobe},
         {"stats", stats},              {"lastError", last_error},
+        {"saveSection", save_section}, {"loadSection", load_section},
     };
     for (size_t i = 0; i < sizeof fns / sizeof fns[0]; ++i) {
         napi_value f;

@@ -17,8 +17,10 @@
 //     of query(), which re-ranks and honours a per-query nprobe;
 //   - setNprobe / nlist / nprobe / tunedRecall / trainMode on IVF kinds,
 //     ingestMode on quantized kinds, chunkCount everywhere.
-// search() (approximate top-fetch + exact re-rank in one device call) and
-// rerankExact() are extras a caller may use explicitly.
+// search() (approximate top-fetch + exact re-rank in one device call),
+// rerankExact() and saveSection() / loadSection() (a snapshot section that
+// skips re-encoding and re-training on load) are extras a caller may use
+// explicitly.
 const path = require('path');
 
 const native = require(path.join(__dirname, '..', 'lib', 'browservec_napi.node'));
@@ -114,6 +116,17 @@ class HipIndex {
   rerankExact(q, candidates, k) {
     const rows = Uint32Array.from(candidates.map(function (h) { return h.row; }));
     return native.rerank(this.handle, f32(q), rows, k).then((res) => toHits(res, 0, k));
+  }
+  // Snapshot index section (codes, scales, IVF state): a load from the
+  // snapshot's rows plus this section skips re-encoding and re-training
+  // (the reference re-derives them, src/index.ts:673-700).
+  saveSection() {
+    return native.saveSection(this.handle);
+  }
+  // Fills this empty index; the descriptor must match the saved index.
+  loadSection(data, count, section) {
+    return native.loadSection(this.handle, f32(data), count,
+      section instanceof Uint8Array ? section : new Uint8Array(section));
   }
   get chunkCount() {
     return native.stats(this.handle).chunkCount;

@@ -233,6 +233,22 @@ int bv_index_build(bv_index *idx);
  * padded_dim for quantized kinds, dim for fp32), list offsets (nlist+1) and
  * list rows (rows, ascending within a list).  Any pointer may be null. */
 int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *list_off, uint32_t *list_rows);
+
+/* Index section for snapshots (src/persist/format.ts:1-22, whose v2 HNSW
+ * graph section is the precedent; src/index.ts:673-700 re-encodes and
+ * re-trains on load instead): the codes and scales of quantized kinds and the
+ * IVF state (reservoir rows and ids, centroids, CSR lists, tuned nprobe).
+ * The snapshot's fp32 rows stay where the reference keeps them.
+ * bv_index_save_section writes *size bytes to buf when cap >= *size; with
+ * buf == NULL or a smaller cap it only reports *size. */
+int bv_index_save_section(bv_index *idx, void *buf, uint64_t cap, uint64_t *size);
+/* Fills an empty index from the snapshot's rows (count*dim prepared floats,
+ * as append takes them) and a saved section, without encoding or training.
+ * The index must have been created with the descriptor the section was saved
+ * under (BV_E_INVALID otherwise).  Appends after a load continue exactly as
+ * on the saved index. */
+int bv_index_load_section(bv_index *idx, const float *data, uint64_t n_floats, uint64_t count, const void *section,
+                          uint64_t bytes);
 /* pickProbes' scores (src/index/ivfquant.ts:495-509: the f64 4-way strided
  * dot of the rotated query with every centroid, stored as f32) for nq
  * queries: scores[nq][nlist].  Batches of 8 or more run the batched probe

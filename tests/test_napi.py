@@ -36,7 +36,8 @@ def test_addon_exports_the_seam():
     r = run_node(f"""
 const m = require({json.dumps(MODULE)});
 const has = (C) => ['size', 'append', 'query', 'queryMasked', 'queryBatch', 'setNprobe', 'destroy', 'search',
-  'rerankExact', 'chunkCount', 'nlist', 'nprobe', 'tunedRecall', 'trainMode', 'ingestMode', 'build']
+  'rerankExact', 'chunkCount', 'nlist', 'nprobe', 'tunedRecall', 'trainMode', 'ingestMode', 'build',
+  'saveSection', 'loadSection']
   .filter((k) => k in C.prototype);
 console.log(JSON.stringify({{abi: m.abiVersion, native: Object.keys(m.native),
   flat: has(m.HipFlatIndex), quant: has(m.HipQuantIndex), ivf: has(m.HipIvfIndex),
@@ -45,14 +46,15 @@ console.log(JSON.stringify({{abi: m.abiVersion, native: Object.keys(m.native),
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout.strip().splitlines()[-1])
     assert out["abi"] == 1
-    common = {"size", "append", "query", "destroy", "search", "rerankExact", "chunkCount"}
+    common = {"size", "append", "query", "destroy", "search", "rerankExact", "chunkCount", "saveSection",
+              "loadSection"}
     assert set(out["flat"]) == common | {"queryMasked", "queryBatch"}
     assert set(out["quant"]) == common | {"queryMasked", "ingestMode"}
     ivf = common | {"setNprobe", "nlist", "nprobe", "tunedRecall", "trainMode", "build"}
     assert set(out["ivf"]) == ivf
     assert set(out["ivfquant"]) == ivf | {"ingestMode"}
     for fn in ("openDevice", "debugInject", "createIndex", "append", "build", "query", "queryMasked", "queryBatch",
-               "search", "rerank"):
+               "search", "rerank", "saveSection", "loadSection"):
         assert fn in out["native"], fn
 
 
@@ -106,6 +108,16 @@ const dim = %(dim)d, n = %(n)d, nq = %(nq)d;
   for (let i = 0; i < nq; i++) out.ivf.push(await ivf.query(qs.subarray(i * dim, (i + 1) * dim), 10));
   out.trainAfter = ivf.trainMode;
   out.ivfStats = [ivf.nlist, ivf.nprobe];
+  // a snapshot's index section: the loaded index answers as the saved one
+  const sec = await ivf.saveSection();
+  out.sectionIsBytes = sec instanceof Uint8Array && sec.length > 0;
+  const ivf2 = m.buildIndex(ctx, dim, 'cosine', 8, {}, {nlist: 16, iters: 3, nprobe: 4});
+  await ivf2.loadSection(rows, n, sec);
+  out.loadedTrain = ivf2.trainMode;
+  out.ivfLoaded = [];
+  for (let i = 0; i < nq; i++) out.ivfLoaded.push(await ivf2.query(qs.subarray(i * dim, (i + 1) * dim), 10));
+  try { await ivf2.loadSection(rows, n, sec); } catch (e) { out.loadTwice = [e.code, e.message]; }
+  ivf2.destroy();
   try { m.buildIndex(ctx, dim, 'l2', 0, {}, {}); } catch (e) { out.ivfL2 = e.message; }
   // a destroy while a call is in flight: the call still completes
   const q2 = quant.query(qs.subarray(0, dim), 5);
@@ -147,6 +159,9 @@ def test_node_results_equal_python_binding(tmp_path):
     assert out["lost"] is True
     assert out["lostErr"] == ["BV_E_DEVICE_LOST", "GPU device lost; re-create the store"]
     assert out["sizeAfterLost"] == n
+    assert out["sectionIsBytes"] and out["loadedTrain"] == "device"
+    assert out["ivfLoaded"] == out["ivf"]
+    assert out["loadTwice"] == ["BV_E_STATE", "a section loads into an empty index"]
 
     ctx = DeviceContext(0)
     try:
