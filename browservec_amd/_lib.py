@@ -54,6 +54,7 @@ class IndexDesc(ctypes.Structure):
         ("ivf_seed", ctypes.c_uint32),
         ("has_ivf_seed", ctypes.c_uint32),
         ("target_recall", ctypes.c_float),
+        ("ivf_incremental", ctypes.c_uint32),
     ]
 
 

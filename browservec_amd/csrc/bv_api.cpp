@@ -10,6 +10,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -180,8 +181,10 @@ struct bv_index {
     DevBuf tune_q, tune_rot, tune_rows, tune_scores, tune_n;
     DevBuf ivf_qrot;                          // probe-space queries of an IVF query
     uint64_t built_rows = ~0ull;              // rows covered by the current lists
+    bool retrain_due = false;                 // incremental appends since the last full build
     uint32_t nlist = 0;
     DevBuf centroids, list_off, list_rows;
+    DevBuf list_off2, list_rows2;             // incremental appends: the extended lists, swapped in
     std::vector<uint32_t> list_sizes_desc;    // host: list sizes, largest first
     DevBuf ivf_idx, ivf_idx2, ivf_slot, ivf_assign, ivf_hist, ivf_base, ivf_totals, ivf_toff, ivf_trows;
     DevBuf probe_scores, probes, cand_tot, cand_off;
@@ -285,9 +288,12 @@ static void rotator_signs(uint32_t dim, uint32_t seed, uint32_t rounds, std::vec
 
 extern "C" int bv_index_create(bv_device *dev, const bv_index_desc *desc, bv_index **out) {
     if (!dev || !desc || !out) return fail(BV_E_INVALID, "null argument");
-    if (desc->size < sizeof(bv_index_desc)) return fail(BV_E_INVALID, "bv_index_desc.size too small");
+    // a desc from before ivf_incremental (72 bytes) reads that field as 0
+    const size_t given = desc->size;
+    if (given < offsetof(bv_index_desc, ivf_incremental)) return fail(BV_E_INVALID, "bv_index_desc.size too small");
     if (dev->lost) return fail(BV_E_DEVICE_LOST, "GPU device lost; re-create the store");
-    bv_index_desc d = *desc;
+    bv_index_desc d{};
+    std::memcpy(&d, desc, std::min(given, sizeof(bv_index_desc)));
     if (d.dim == 0) return fail(BV_E_INVALID, "dimension must be a positive integer, got %u", d.dim);
     if (d.metric > BV_METRIC_L2) return fail(BV_E_INVALID, "unknown metric %u", d.metric);
     if (d.kind > BV_KIND_IVFQUANT) return fail(BV_E_INVALID, "unknown index kind %u", d.kind);
@@ -462,7 +468,64 @@ static void ivf_commit(bv_index *idx, uint64_t base, const ReservoirPlan &pl) {
     if (idx->sample_row.size() < idx->sample_filled) idx->sample_row.resize(idx->sample_filled);
     for (uint64_t i = 0; i < pl.slots.size(); ++i)
         if (pl.slots[i] >= 0) idx->sample_row[(uint32_t)pl.slots[i]] = base + i;
-    idx->built_rows = ~0ull;  // lists are stale after any append (ivfquant.ts:462)
+    // lists are stale after any append (ivfquant.ts:462), unless the append
+    // extends them (incremental mode, lists current before it)
+    if (!(idx->d.ivf_incremental && idx->built_rows == base && idx->nlist)) idx->built_rows = ~0ull;
+}
+
+// Incremental append: rows [base, base + count) assigned to the current
+// centroids with the build's final-assignment arithmetic, then merged into
+// the lists (each list: its rows, then the new ones, ascending).  The lists
+// equal those a final assignment over every row with these centroids gives.
+static int ivf_extend_lists(bv_index *idx, uint64_t base, uint64_t count) {
+    const uint32_t nlist = idx->nlist;
+    hipStream_t s = idx->stream;
+    const uint32_t nblk = ivf_list_blocks(count);
+    HIPX(idx->dev, idx->ivf_assign.ensure(count * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_hist.ensure((size_t)std::max(nblk, 1u) * nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_base.ensure((size_t)std::max(nblk, 1u) * nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_totals.ensure((size_t)nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_toff.ensure(((size_t)nlist + 1) * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_trows.ensure(count * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->list_off2.ensure(((size_t)nlist + 1) * 4, 0, s), "lists");
+    HIPX(idx->dev, idx->list_rows2.ensure((base + count) * 4, 0, s), "lists");
+    IvfAssignArgs fa{};
+    fa.n = count;
+    fa.dim = idx->sample_dim;
+    fa.centroids = idx->centroids.as<float>();
+    fa.cen_stride = idx->sample_dim;
+    fa.nlist = nlist;
+    fa.out = idx->ivf_assign.as<uint32_t>();
+    if (idx->quant) {
+        fa.codes = idx->codes.as<uint32_t>() + base * idx->words_per_row;
+        fa.words_per_row = idx->words_per_row;
+        fa.scales = idx->scales.as<float>() + base;
+    } else {
+        fa.rows = idx->raw.as<float>() + base * idx->dim;
+        fa.row_stride = idx->dim;
+    }
+    HIPX(idx->dev, ivf_launch_assign(fa, idx->quant ? (int)idx->d.bits : 0, s), "assign kernel");
+    HIPX(idx->dev, ivf_launch_lists(fa.out, count, nlist, idx->ivf_hist.as<uint32_t>(), idx->ivf_base.as<uint32_t>(),
+                                    idx->ivf_totals.as<uint32_t>(), idx->ivf_toff.as<uint32_t>(),
+                                    idx->ivf_trows.as<uint32_t>(), s),
+         "list kernels");
+    HIPX(idx->dev,
+         ivf_launch_merge_lists(idx->list_off.as<uint32_t>(), idx->list_rows.as<uint32_t>(),
+                                idx->ivf_toff.as<uint32_t>(), idx->ivf_trows.as<uint32_t>(), (uint32_t)base, nlist,
+                                idx->list_off2.as<uint32_t>(), idx->list_rows2.as<uint32_t>(), s),
+         "list merge kernel");
+    std::swap(idx->list_off.p, idx->list_off2.p);
+    std::swap(idx->list_off.cap, idx->list_off2.cap);
+    std::swap(idx->list_rows.p, idx->list_rows2.p);
+    std::swap(idx->list_rows.cap, idx->list_rows2.cap);
+    std::vector<uint32_t> off(nlist + 1);
+    HIPX(idx->dev, hipMemcpyAsync(off.data(), idx->list_off.p, (nlist + 1) * 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "list merge");
+    for (uint32_t c = 0; c < nlist; ++c) idx->list_sizes_desc[c] = off[c + 1] - off[c];
+    std::sort(idx->list_sizes_desc.begin(), idx->list_sizes_desc.end(), std::greater<uint32_t>());
+    idx->built_rows = base + count;
+    idx->retrain_due = true;
+    return BV_OK;
 }
 
 // fp32 IVF: the sampled rows themselves go to their slots.
@@ -562,6 +625,7 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
              launch_row_sqnorms(idx->raw.as<float>() + base * idx->dim, count, idx->dim, idx->rsq.as<float>() + base,
                                 idx->rsq_max.as<uint32_t>(), idx->stream),
              "norm kernel");
+    const bool extend = idx->ivf && idx->built_rows == base && idx->nlist && idx->d.ivf_incremental;
     if (idx->quant) {
         int rc = encode_range(idx, base, count, idx->ivf ? idx->ivf_slot.as<int32_t>() : nullptr);
         if (rc) return rc;
@@ -572,6 +636,10 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
                  "norm kernel");
     } else if (idx->ivf) {
         int rc = ivf_sample_raw(idx, base, plan.slots);
+        if (rc) return rc;
+    }
+    if (extend) {
+        int rc = ivf_extend_lists(idx, base, count);
         if (rc) return rc;
     }
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "append");
@@ -839,6 +907,7 @@ static int ivf_build(bv_index *idx) {
     std::sort(idx->list_sizes_desc.begin(), idx->list_sizes_desc.end(), std::greater<uint32_t>());
     idx->nlist = nlist;
     idx->built_rows = rows;
+    idx->retrain_due = false;
     int rc = ivf_tune(idx, fa.out);
     if (rc) return rc;
     idx->build_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
@@ -2116,7 +2185,7 @@ extern "C" int bv_index_build(bv_index *idx) {
     if (rc) return rc;
     if (!idx->ivf) return BV_OK;
     if (idx->rows == 0) return fail(BV_E_STATE, "IVF build needs rows");
-    if (idx->built_rows == idx->rows) return BV_OK;
+    if (idx->built_rows == idx->rows && !idx->retrain_due) return BV_OK;
     return ivf_build(idx);
 }
 
@@ -2177,7 +2246,7 @@ namespace {
 constexpr uint32_t SECTION_MAGIC = 0x58495642u;  // "BVIX"
 constexpr uint32_t SECTION_VERSION = 1;
 struct SectionHeader {
-    uint32_t magic, version, header_bytes, reserved;
+    uint32_t magic, version, header_bytes, ivf_incremental;
     uint32_t kind, dim, metric, bits, scorer, seed, rounds;
     uint32_t nlist_desc, sample_size, train_size, iters, ivf_seed, has_ivf_seed;
     float target_recall;
@@ -2188,7 +2257,7 @@ struct SectionHeader {
     uint64_t sample_filled, sample_seen;
     uint32_t sample_rng, tuned_nprobe;
     float tuned_recall;
-    uint32_t pad;
+    uint32_t retrain_due;
 };
 static_assert(sizeof(SectionHeader) % 8 == 0, "section header alignment");
 
@@ -2199,6 +2268,7 @@ SectionHeader section_header(const bv_index *idx) {
     h.magic = SECTION_MAGIC;
     h.version = SECTION_VERSION;
     h.header_bytes = sizeof(SectionHeader);
+    h.ivf_incremental = idx->d.ivf_incremental;
     h.kind = idx->d.kind;
     h.dim = idx->d.dim;
     h.metric = idx->d.metric;
@@ -2226,6 +2296,7 @@ SectionHeader section_header(const bv_index *idx) {
     h.sample_rng = idx->sample_rng;
     h.tuned_nprobe = idx->tuned_nprobe;
     h.tuned_recall = idx->tuned_recall;
+    h.retrain_due = idx->retrain_due ? 1u : 0u;
     return h;
 }
 
@@ -2321,6 +2392,7 @@ extern "C" int bv_index_load_section(bv_index *idx, const float *data, uint64_t 
         h.scorer != mine.scorer || h.seed != mine.seed || h.rounds != mine.rounds || h.nlist_desc != mine.nlist_desc ||
         h.sample_size != mine.sample_size || h.train_size != mine.train_size || h.iters != mine.iters ||
         h.ivf_seed != mine.ivf_seed || h.has_ivf_seed != mine.has_ivf_seed || h.P != mine.P ||
+        h.ivf_incremental != mine.ivf_incremental ||
         h.words_per_row != mine.words_per_row || h.sample_cap != mine.sample_cap || h.sample_dim != mine.sample_dim ||
         std::memcmp(&h.target_recall, &mine.target_recall, 4) != 0)
         return fail(BV_E_INVALID, "the index section was saved from an index with a different configuration");
@@ -2415,6 +2487,7 @@ extern "C" int bv_index_load_section(bv_index *idx, const float *data, uint64_t 
             for (uint32_t c = 0; c < h.nlist; ++c) idx->list_sizes_desc[c] = off[c + 1] - off[c];
             std::sort(idx->list_sizes_desc.begin(), idx->list_sizes_desc.end(), std::greater<uint32_t>());
             idx->built_rows = h.built_rows;
+            idx->retrain_due = h.retrain_due != 0;
         }
     }
     HIPX(idx->dev, hipStreamSynchronize(s), "load");
@@ -2428,7 +2501,9 @@ extern "C" int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *li
     int rc = check_live(idx);
     if (rc) return rc;
     if (!idx->ivf) return fail(BV_E_STATE, "not an IVF index");
-    if (idx->built_rows != idx->rows) return fail(BV_E_STATE, "IVF lists are not built (bv_index_build)");
+    if (idx->rows == 0) return fail(BV_E_STATE, "IVF lists need rows");
+    rc = ensure_built(idx);  // the lists a query would probe now
+    if (rc) return rc;
     if (centroids)
         HIPX(idx->dev, hipMemcpy(centroids, idx->centroids.p, (size_t)idx->nlist * idx->sample_dim * 4,
                                  hipMemcpyDeviceToHost), "download");

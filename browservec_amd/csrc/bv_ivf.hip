@@ -556,6 +556,34 @@ hipError_t ivf_launch_lists(const uint32_t *assign, uint64_t n, uint32_t nlist, 
     return hipGetLastError();
 }
 
+namespace {
+// One workgroup per list: the list's old rows, then its appended rows
+// (shifted by add_base), at old_off[c] + add_off[c].
+__global__ __launch_bounds__(256) void ivf_merge_lists(const uint32_t *old_off, const uint32_t *old_rows,
+                                                        const uint32_t *add_off, const uint32_t *add_rows,
+                                                        uint32_t add_base, uint32_t nlist, uint32_t *new_off,
+                                                        uint32_t *new_rows) {
+    const uint32_t c = blockIdx.x;
+    const uint32_t o0 = old_off[c], o1 = old_off[c + 1], a0 = add_off[c], a1 = add_off[c + 1];
+    const uint32_t dst = o0 + a0;
+    if (threadIdx.x == 0) {
+        new_off[c] = dst;
+        if (c == nlist - 1) new_off[nlist] = o1 + a1;
+    }
+    for (uint32_t i = threadIdx.x; i < o1 - o0; i += 256) new_rows[dst + i] = old_rows[o0 + i];
+    for (uint32_t i = threadIdx.x; i < a1 - a0; i += 256) new_rows[dst + (o1 - o0) + i] = add_base + add_rows[a0 + i];
+}
+}  // namespace
+
+hipError_t ivf_launch_merge_lists(const uint32_t *old_off, const uint32_t *old_rows, const uint32_t *add_off,
+                                  const uint32_t *add_rows, uint32_t add_base, uint32_t nlist, uint32_t *new_off,
+                                  uint32_t *new_rows, hipStream_t s) {
+    if (nlist == 0 || nlist > IVF_MAX_NLIST) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(ivf_merge_lists, dim3(nlist), dim3(256), 0, s, old_off, old_rows, add_off, add_rows, add_base,
+                       nlist, new_off, new_rows);
+    return hipGetLastError();
+}
+
 hipError_t ivf_launch_means(const float *sample, uint32_t stride, uint32_t dim, const uint32_t *offset,
                             const uint32_t *list_rows, uint32_t nlist, float *centroids, uint32_t cen_stride,
                             hipStream_t s) {

@@ -188,6 +188,11 @@ uint32_t ivf_list_blocks(uint64_t n);
 // hist/base: ivf_list_blocks(n) x nlist; totals: nlist; offset: nlist+1; rows_out: n.
 hipError_t ivf_launch_lists(const uint32_t *assign, uint64_t n, uint32_t nlist, uint32_t *hist, uint32_t *base,
                             uint32_t *totals, uint32_t *offset, uint32_t *rows_out, hipStream_t s);
+// Lists extended by an append: for each list, its rows (old_off / old_rows),
+// then the appended ones (add_off / add_rows, ids relative to add_base).
+hipError_t ivf_launch_merge_lists(const uint32_t *old_off, const uint32_t *old_rows, const uint32_t *add_off,
+                                  const uint32_t *add_rows, uint32_t add_base, uint32_t nlist, uint32_t *new_off,
+                                  uint32_t *new_rows, hipStream_t s);
 hipError_t ivf_launch_means(const float *sample, uint32_t stride, uint32_t dim, const uint32_t *offset,
                             const uint32_t *list_rows, uint32_t nlist, float *centroids, uint32_t cen_stride,
                             hipStream_t s);

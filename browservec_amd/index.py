@@ -112,6 +112,7 @@ class NativeIndex:
             d.has_ivf_seed = 1
         if ivf.get("targetRecall") is not None:
             d.target_recall = float(ivf["targetRecall"])
+        d.ivf_incremental = 1 if ivf.get("incremental") else 0
         h = ctypes.c_void_p()
         L.check(self.lib.bv_index_create(ctx.handle, ctypes.byref(d), ctypes.byref(h)))
         self.handle = h
@@ -325,8 +326,9 @@ class IVFIndex(NativeIndex):
         return "device" if self.stats()["nlist"] else "pending"
 
     def export_ivf(self):
-        """(centroids [nlist, D], list offsets [nlist+1], list rows [rows])."""
-        self.build()
+        """(centroids [nlist, D], list offsets [nlist+1], list rows [rows]):
+        the lists a query would probe now."""
+        L.check(self.lib.bv_index_export_ivf(self.handle, None, None, None))  # builds stale lists
         st = self.stats()
         nlist = st["nlist"]
         D = st["padded_dim"] if self.bits else self.dim

@@ -368,6 +368,7 @@ static napi_value create_index(napi_env env, napi_callback_info info) {
     d.has_ivf_seed = field_u32(env, argv[1], "hasIvfSeed", 0);
     d.ivf_seed = field_u32(env, argv[1], "ivfSeed", 0);
     d.target_recall = (float)field_f64(env, argv[1], "targetRecall", -1.0);
+    d.ivf_incremental = field_u32(env, argv[1], "incremental", 0);
     bv_index *idx = NULL;
     int rc = bv_index_create((bv_device *)get_ptr(env, argv[0]), &d, &idx);
     if (rc) return throw_bv(env, rc);

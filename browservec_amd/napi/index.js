@@ -93,6 +93,7 @@ class HipIndex {
       hasIvfSeed: ivf && ivf.seed !== undefined ? 1 : 0,
       ivfSeed: ivf && ivf.seed !== undefined ? ivf.seed >>> 0 : 0,
       targetRecall: ivf && ivf.targetRecall !== undefined ? ivf.targetRecall : -1,
+      incremental: ivf && ivf.incremental ? 1 : 0,
     });
   }
   get size() {

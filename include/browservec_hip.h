@@ -70,7 +70,8 @@ typedef struct bv_index bv_index;
  * fields (src/types.ts:116-128, src/index/ivf.ts:29-49).  Zero means "the
  * reference default" for every optional field. */
 typedef struct bv_index_desc {
-    uint32_t size;          /* sizeof(bv_index_desc)                                 */
+    uint32_t size;          /* sizeof(bv_index_desc); 72 (no ivf_incremental) is read
+                             * with ivf_incremental = 0                               */
     uint32_t kind;          /* BV_KIND_*                                             */
     uint32_t dim;           /* vector dimension (> 0)                                */
     uint32_t metric;        /* BV_METRIC_*                                           */
@@ -88,6 +89,10 @@ typedef struct bv_index_desc {
     uint32_t ivf_seed;      /* IVF seed; has_ivf_seed=0 -> reference default         */
     uint32_t has_ivf_seed;
     float target_recall;    /* IVF: < 0 -> unset                                     */
+    uint32_t ivf_incremental; /* IVF: 1 -> appends after a build assign the new rows
+                               * to the current centroids and extend the lists; 0 ->
+                               * the reference's rebuild on the next query
+                               * (src/index/ivfquant.ts:462)                          */
 } bv_index_desc;
 
 /* Stats (the index-derived fields of `Stats`, src/types.ts:253-300, and
@@ -227,11 +232,16 @@ int bv_index_export_rotated_query(bv_index *idx, const float *q, float *rotated)
 /* IVFIndex / IVFQuantIndex build (src/index/ivf.ts:191-259,
  * src/index/ivfquant.ts:248-312): k-means on the reservoir sample, final
  * assignment, CSR lists.  Queries build on demand after appends, as the
- * reference does; this entry builds now. */
+ * reference does; this entry builds now.  With desc.ivf_incremental, appends
+ * after a build extend the lists instead (the new rows assigned to the
+ * current centroids); this entry then retrains over the reservoir and
+ * reassigns every row, giving the lists the reference would build. */
 int bv_index_build(bv_index *idx);
 /* The built IVF state for parity checks: centroids (nlist x D floats, D =
  * padded_dim for quantized kinds, dim for fp32), list offsets (nlist+1) and
- * list rows (rows, ascending within a list).  Any pointer may be null. */
+ * list rows (rows, ascending within a list).  Any pointer may be null.
+ * Stale lists are built first, as a query would; lists extended by
+ * incremental appends are exported as they stand. */
 int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *list_off, uint32_t *list_rows);
 
 /* Index section for snapshots (src/persist/format.ts:1-22, whose v2 HNSW

@@ -58,7 +58,19 @@ def test_no_device_error_path_is_clean():
 def test_struct_layouts_match_header():
     from browservec_amd import _lib
 
-    assert ctypes.sizeof(_lib.IndexDesc) == 18 * 4
+    import re
+    from pathlib import Path
+
+    header = (Path(__file__).resolve().parents[1] / "include" / "browservec_hip.h").read_text()
+    for struct, cls in (("bv_index_desc", _lib.IndexDesc), ("bv_index_stats", _lib.IndexStats)):
+        body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), header, re.S).group(1)
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+        fields = re.findall(r"(\w+)\s+(\w+);", body)
+        assert [n for _, n in fields] == [n for n, _ in cls._fields_], struct
+        ctype = {"uint32_t": ctypes.c_uint32, "uint64_t": ctypes.c_uint64, "float": ctypes.c_float,
+                 "double": ctypes.c_double}
+        assert [ctype[t] for t, _ in fields] == [t for _, t in cls._fields_], struct
+    assert ctypes.sizeof(_lib.IndexDesc) == 19 * 4
     # IndexStats: u64 + 7*u32 + f32 + 3*f64 + 2*u64
     assert ctypes.sizeof(_lib.IndexStats) == 8 + 8 * 4 + 3 * 8 + 2 * 8
 

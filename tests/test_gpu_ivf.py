@@ -357,3 +357,58 @@ def test_ivf_lazy_build_inside_a_query(ctx):
     assert np.array_equal(d_sc.cpu().numpy().view(np.uint32), want_scores.view(np.uint32))
     for idx in (ref_idx, a, b, c):
         idx.destroy()
+
+
+@pytest.mark.parametrize("bits", [8, 0])
+def test_ivf_incremental_append(ctx, bits):
+    """Incremental mode (src/index/ivfquant.ts:216-233,462 rebuilds after
+    every append instead): rows appended after a build are assigned to the
+    current centroids with the final-assignment arithmetic and extend the
+    lists, centroids unchanged; an explicit build then retrains over the
+    reservoir and equals the reference-mode index's lists."""
+    from browservec_amd import IVFIndex, IVFQuantIndex
+
+    dim, n0, n1 = 64, 4000, 1500
+    ivf = {"nlist": 16, "iters": 3, "nprobe": 4, "sampleSize": 2048}
+    say("ivf incremental", bits)
+    data = clustered(n0 + n1, dim, 24, 0.1, seed=77 + bits)
+    make = (lambda o: IVFQuantIndex(ctx, dim, bits=bits, ivf=o)) if bits else (lambda o: IVFIndex(ctx, dim, ivf=o))
+    inc = make(dict(ivf, incremental=True))
+    ref = make(ivf)
+    for x in (inc, ref):
+        x.append(data[:n0], n0)
+        x.build()
+    cen0, off0, rows0 = inc.export_ivf()
+    inc.append(data[n0:], n1)
+    ref.append(data[n0:], n1)
+    cen1, off1, rows1 = inc.export_ivf()  # no rebuild: the lists were extended
+    assert np.array_equal(cen1.view(np.uint32), cen0.view(np.uint32))
+    old = np.empty(n0, np.int64)
+    for c in range(off0.size - 1):
+        old[rows0[off0[c]:off0[c + 1]]] = c
+    if bits:
+        words, scales = idx_codes(inc)
+        new = o.assign_quant(words[n0:], scales[n0:], cen0.shape[1], bits, cen0)
+        V = dequant_f32(words[n0:], scales[n0:], bits, cen0.shape[1]).astype(np.float64)
+    else:
+        new = o.assign_f32(data[n0:], cen0)
+        V = data[n0:].astype(np.float64)
+    got = np.empty(n0 + n1, np.int64)
+    for c in range(off1.size - 1):
+        seg = rows1[off1[c]:off1[c + 1]]
+        assert np.all(np.diff(seg.astype(np.int64)) > 0), c  # rows ascending within a list
+        got[seg] = c
+    assert np.array_equal(got[:n0], old)  # old rows keep their lists
+    for r in np.nonzero(got[n0:] != new)[0]:  # new rows: the oracle's assignment, up to near-ties
+        s = V[r] @ cen0.astype(np.float64).T
+        assert abs(s[got[n0 + r]] - s[new[r]]) <= 1e-5 * np.abs(V[r]).sum(), r
+    q = data[[10, n0 + 20]]
+    for qq in q:  # queries run on the extended lists without a rebuild
+        assert [h.row for h in inc.query(qq, 10)] and inc.stats()["nlist"] == 16
+    inc.build()  # retrain: the reference's lists
+    for a, b in zip(inc.export_ivf(), ref.export_ivf()):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for qq in q:
+        assert [(h.row, h.score) for h in inc.query(qq, 10)] == [(h.row, h.score) for h in ref.query(qq, 10)]
+    inc.destroy()
+    ref.destroy()

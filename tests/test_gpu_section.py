@@ -40,14 +40,16 @@ def make(ctx, kind, dim):
     if kind == "quant1":
         return QuantIndex(ctx, dim, bits=1)
     if kind == "ivfquant":
-        return IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 16, "iters": 3, "nprobe": 4, "sample_size": 2048})
+        return IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 16, "iters": 3, "nprobe": 4, "sampleSize": 1024})
+    if kind == "ivfinc":  # incremental lists: appends after the load extend them as on the saved index
+        return IVFQuantIndex(ctx, dim, bits=4, ivf={"nlist": 10, "iters": 2, "nprobe": 3, "incremental": True})
     if kind == "ivf":
         return IVFIndex(ctx, dim, ivf={"nlist": 12, "iters": 2, "nprobe": 3})
     return FlatIndex(ctx, dim, "dot")
 
 
 @pytest.mark.parametrize("kind,dim,n", [("quant8", 100, 20000), ("quant1", 200, 3000), ("ivfquant", 64, 6000),
-                                        ("ivf", 48, 5000), ("flat", 96, 20000)])
+                                        ("ivfinc", 80, 4000), ("ivf", 48, 5000), ("flat", 96, 20000)])
 def test_section_round_trip(ctx, kind, dim, n):
     say("section", kind, dim, n)
     data = clustered(n + 700, dim, 30, 0.1, seed=dim + n)
@@ -60,7 +62,7 @@ def test_section_round_trip(ctx, kind, dim, n):
     b = make(ctx, kind, dim)
     b.load_section(data[:n], n, sec)
     assert b.size == n
-    if kind.startswith("quant") or kind == "ivfquant":
+    if kind.startswith("quant") or kind in ("ivfquant", "ivfinc"):
         wa, sa = a.export_codes()
         wb, sb = b.export_codes()
         assert np.array_equal(wa, wb) and np.array_equal(sa.view(np.uint32), sb.view(np.uint32))
@@ -74,6 +76,9 @@ def test_section_round_trip(ctx, kind, dim, n):
     a.append(data[n:], 700)
     b.append(data[n:], 700)
     same_answers(a, b, qs, 50, 10)
+    if kind.startswith("ivf"):
+        for x, y in zip(a.export_ivf(), b.export_ivf()):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
     a.destroy()
     b.destroy()
 
