@@ -44,45 +44,6 @@ def normalize_in_place(v: np.ndarray) -> np.ndarray:
     return v
 
 
-def dot_row(row: np.ndarray, q: np.ndarray) -> float:
-    """Store.dotRow (src/store/store.ts:114-130): 4 strided f64 accumulators."""
-    dim = row.shape[0]
-    vec = dim & ~3
-    prod = row[:vec].astype(np.float64) * q[:vec].astype(np.float64)
-    if vec:
-        acc4 = np.cumsum(prod.reshape(-1, 4), axis=0)[-1]
-        acc = ((acc4[0] + acc4[1]) + acc4[2]) + acc4[3]
-    else:
-        acc = 0.0
-    for i in range(vec, dim):
-        acc += float(row[i]) * float(q[i])
-    return float(acc)
-
-
-def l2_row(row: np.ndarray, q: np.ndarray) -> float:
-    """Store.l2Row (src/store/store.ts:137-160)."""
-    dim = row.shape[0]
-    vec = dim & ~3
-    d = row[:vec].astype(np.float64) - q[:vec].astype(np.float64)
-    if vec:
-        acc4 = np.cumsum((d * d).reshape(-1, 4), axis=0)[-1]
-        acc = ((acc4[0] + acc4[1]) + acc4[2]) + acc4[3]
-    else:
-        acc = 0.0
-    for i in range(vec, dim):
-        e = float(row[i]) - float(q[i])
-        acc += e * e
-    return -float(acc)
-
-
-def top_k(scores: np.ndarray, k: int) -> list[FlatHit]:
-    """Host top-k in canonical order (score desc, row asc), the order the
-    device returns; used for the small exact filtered scan."""
-    s = np.asarray(scores, dtype=np.float32) + np.float32(0.0)
-    order = np.lexsort((np.arange(s.size), -s.astype(np.float64)))[: max(k, 0)]
-    return [FlatHit(int(i), float(s[i])) for i in order]
-
-
 @dataclass
 class RowEntry:
     id: str
@@ -355,14 +316,16 @@ class BrowserVec:
         return out
 
     def _query_rows_exact(self, q: np.ndarray, rows: list[int], k: int) -> list[dict]:
-        """queryRowsExact (src/index.ts:445-464): host f64 scores of the
-        matching rows, then top-k."""
-        fn = l2_row if self.store.metric == "l2" else dot_row
-        scores = np.array([fn(self.store.raw[r], q) for r in rows], dtype=np.float32)
-        self.last_query_gpu_ms = 0.0
+        """queryRowsExact (src/index.ts:445-464): the matching rows' exact
+        Store.dotRow / Store.l2Row scores and their top k, computed on the
+        device over the index's stored rows."""
+        t0 = time.perf_counter()
+        hits = self.index.query_rows(q, np.asarray(rows, dtype=np.uint32), k)
+        self.last_query_ms = (time.perf_counter() - t0) * 1e3
+        self.last_query_gpu_ms = self.index.stats()["last_query_gpu_ms"]
         out = []
-        for h in top_k(scores, k):
-            e = self.store.by_row[rows[h.row]]
+        for h in hits:
+            e = self.store.by_row[h.row]
             r = {"id": e.id, "score": h.score}
             if e.metadata is not None:
                 r["metadata"] = e.metadata

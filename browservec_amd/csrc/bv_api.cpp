@@ -162,6 +162,8 @@ struct bv_index {
     DevBuf mq_qsq, mq_slack, mq_rows;         // exact fp32 batches: query norms, slack, surviving rows
     DevBuf cnorm, mq_rq, mq_up, mq_kept;       // flat int8 level-one batches: row code norms, query bounds, upper bounds, kept counts
     DevBuf mq_bk, mq_bu, mq_bc;               // level-one batches: per-workgroup buckets (lower keys, upper bounds, lengths)
+    DevBuf sel_keys, sel_sorted, sel_tmp;     // selection by sort: keys, sorted keys, hipCUB scratch
+    DevBuf sel_list, sel_popc, sel_off, sel_misc;  // listed rows; mask word counts and offsets; flag + count
     HostBuf h_cnt;
     HostBuf h_rows, h_scores, h_n, h_flag;
 
@@ -1762,8 +1764,9 @@ static int host_query(bv_index *idx, const float *q, uint32_t nq, uint32_t kprim
 }
 
 // Dense-score fallback for fetches beyond the fused top-k's capacity.
-static int host_query_dense(bv_index *idx, const float *q, uint32_t nq, uint32_t k, const uint32_t *mask,
-                            uint64_t mask_words, uint32_t *rows, float *scores, uint32_t *n_out);
+static int dense_topk(bv_index *idx, const float *q, uint32_t k, const uint32_t *mask, uint64_t mask_words,
+                      uint32_t *rows, float *scores, uint32_t *n_out);
+static int sorted_topk(bv_index *idx, uint64_t n_keys, uint32_t k, uint32_t *rows, float *scores, uint32_t *n_out);
 
 extern "C" int bv_index_query(bv_index *idx, const float *q, uint32_t k, uint32_t *rows, float *scores,
                               uint32_t *n_out) {
@@ -1773,7 +1776,7 @@ extern "C" int bv_index_query(bv_index *idx, const float *q, uint32_t k, uint32_
     if (rc) return rc;
     if (!q || !n_out || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
     const uint32_t kk = (uint32_t)std::min<uint64_t>(k, idx->rows);
-    if (kk > (uint32_t)MAX_KPRIME) return host_query_dense(idx, q, 1, k, nullptr, 0, rows, scores, n_out);
+    if (kk > (uint32_t)MAX_KPRIME) return dense_topk(idx, q, k, nullptr, 0, rows, scores, n_out);
     return host_query(idx, q, 1, kk, kk, false, nullptr, 0, rows, scores, n_out);
 }
 
@@ -1789,7 +1792,7 @@ extern "C" int bv_index_query_masked(bv_index *idx, const float *q, uint32_t k, 
         return fail(BV_E_INVALID, "mask has %llu words, need %llu for %llu rows", (unsigned long long)n_words,
                     (unsigned long long)need, (unsigned long long)idx->rows);
     const uint32_t kk = (uint32_t)std::min<uint64_t>(k, idx->rows);
-    if (kk > (uint32_t)MAX_KPRIME) return host_query_dense(idx, q, 1, k, mask_words, n_words, rows, scores, n_out);
+    if (kk > (uint32_t)MAX_KPRIME) return dense_topk(idx, q, k, mask_words, n_words, rows, scores, n_out);
     return host_query(idx, q, 1, kk, kk, false, mask_words, n_words, rows, scores, n_out);
 }
 
@@ -1803,11 +1806,9 @@ extern "C" int bv_index_query_batch(bv_index *idx, const float *queries, uint32_
     if (!queries || !n_out || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
     const uint32_t kk = (uint32_t)std::min<uint64_t>(k, idx->rows);
     if (kk > (uint32_t)MAX_KPRIME) {
-        std::vector<uint32_t> r(kk);
-        std::vector<float> s(kk);
         for (uint32_t i = 0; i < nq; i++) {
-            rc = host_query_dense(idx, queries + (size_t)i * idx->dim, 1, k, nullptr, 0, rows + (size_t)i * k,
-                                  scores + (size_t)i * k, n_out + i);
+            rc = dense_topk(idx, queries + (size_t)i * idx->dim, k, nullptr, 0, rows + (size_t)i * k,
+                            scores + (size_t)i * k, n_out + i);
             if (rc) return rc;
         }
         return BV_OK;
@@ -2024,18 +2025,125 @@ extern "C" int bv_index_rerank(bv_index *idx, const float *q, const uint32_t *ca
     return BV_OK;
 }
 
-// Dense scores of one query for every row (the scan's score for each row).
-static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uint64_t mask_words, float *out) {
+// Exact scores of the n_list rows at idx->sel_list against q (Store.dotRow /
+// Store.l2Row order), then their top k by a device sort.
+static int exact_list_topk(bv_index *idx, const float *q, uint64_t n_list, uint32_t k, uint32_t *rows, float *scores,
+                           uint32_t *n_out) {
+    hipStream_t s = idx->stream;
+    const size_t qb = (size_t)idx->dim * 4;
+    HIPX(idx->dev, idx->qin.ensure(qb, 0, s), "query buffer");
+    HIPX(idx->dev, hipMemcpyAsync(idx->qin.p, q, qb, hipMemcpyHostToDevice, s), "upload");
+    HIPX(idx->dev, idx->sel_keys.ensure(n_list * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->sel_misc.ensure(8, 0, s), "scratch");
+    HIPX(idx->dev, launch_zero(idx->sel_misc.p, 4, s), "scratch clear");
+    HIPX(idx->dev, sel_exact_row_keys(idx->raw.as<float>(), idx->rows, idx->dim, idx->d.metric == BV_METRIC_L2,
+                                      idx->qin.as<float>(), idx->sel_list.as<uint32_t>(), n_list,
+                                      idx->sel_keys.as<uint64_t>(), idx->sel_misc.as<uint32_t>(), s),
+         "exact row kernel");
+    uint32_t bad = 0;
+    HIPX(idx->dev, hipMemcpyAsync(&bad, idx->sel_misc.p, 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "exact rows");
+    if (bad) return fail(BV_E_INVALID, "a listed row is out of range (the index holds %llu rows)",
+                         (unsigned long long)idx->rows);
+    return sorted_topk(idx, n_list, k, rows, scores, n_out);
+}
+
+static int rows_prologue(bv_index *idx, const float *q, uint32_t k, uint32_t *rows, float *scores, uint32_t *n_out) {
+    if (!q || !n_out || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
+    if (!idx->raw.p && idx->rows) return fail(BV_E_STATE, "exact row scores need the fp32 rows on the device");
+    if ((size_t)idx->dim * 4 > 96 * 1024) return fail(BV_E_UNSUPPORTED, "dimension %u above 24576", idx->dim);
+    return BV_OK;
+}
+
+extern "C" int bv_index_query_rows(bv_index *idx, const float *q, const uint32_t *list, uint64_t n_list, uint32_t k,
+                                   uint32_t *rows, float *scores, uint32_t *n_out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
+    int rc = check_live(idx);
+    if (rc) return rc;
+    rc = rows_prologue(idx, q, k, rows, scores, n_out);
+    if (rc) return rc;
+    if (n_list && !list) return fail(BV_E_INVALID, "null argument");
+    if (n_list == 0 || k == 0) {
+        *n_out = 0;
+        return BV_OK;
+    }
+    HIPX(idx->dev, idx->sel_list.ensure(n_list * 4, 0, idx->stream), "scratch");
+    HIPX(idx->dev, hipMemcpyAsync(idx->sel_list.p, list, n_list * 4, hipMemcpyHostToDevice, idx->stream), "upload");
+    return exact_list_topk(idx, q, n_list, k, rows, scores, n_out);
+}
+
+extern "C" int bv_index_query_rows_masked(bv_index *idx, const float *q, const uint32_t *mask_words, uint64_t n_words,
+                                          uint32_t k, uint32_t *rows, float *scores, uint32_t *n_out) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
+    int rc = check_live(idx);
+    if (rc) return rc;
+    rc = rows_prologue(idx, q, k, rows, scores, n_out);
+    if (rc) return rc;
+    if (n_words && !mask_words) return fail(BV_E_INVALID, "null argument");
+    const uint64_t words = std::min<uint64_t>(n_words, (idx->rows + 31) / 32);  // bits past the rows are ignored
+    if (words == 0 || k == 0) {
+        *n_out = 0;
+        return BV_OK;
+    }
+    hipStream_t s = idx->stream;
+    HIPX(idx->dev, idx->mask.ensure(words * 4, 0, s), "mask buffer");
+    HIPX(idx->dev, hipMemcpyAsync(idx->mask.p, mask_words, words * 4, hipMemcpyHostToDevice, s), "upload");
+    HIPX(idx->dev, idx->sel_popc.ensure(words * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->sel_off.ensure(words * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->sel_misc.ensure(8, 0, s), "scratch");
+    HIPX(idx->dev, sel_mask_counts(idx->mask.as<uint32_t>(), words, idx->rows, idx->sel_popc.as<uint32_t>(), s),
+         "mask count kernel");
+    size_t tb = 0;
+    HIPX(idx->dev, sel_exclusive_scan(nullptr, tb, nullptr, nullptr, words, s), "scan sizing");
+    HIPX(idx->dev, idx->sel_tmp.ensure(std::max<size_t>(tb, 256), 0, s), "scratch");
+    tb = idx->sel_tmp.cap;
+    HIPX(idx->dev, sel_exclusive_scan(idx->sel_tmp.p, tb, idx->sel_popc.as<uint32_t>(), idx->sel_off.as<uint32_t>(),
+                                      words, s),
+         "scan");
+    // the list can hold every row: sized before its length is known
+    HIPX(idx->dev, idx->sel_list.ensure(words * 32 * 4, 0, s), "scratch");
+    HIPX(idx->dev, sel_mask_rows(idx->mask.as<uint32_t>(), words, idx->rows, idx->sel_popc.as<uint32_t>(),
+                                 idx->sel_off.as<uint32_t>(), idx->sel_list.as<uint32_t>(),
+                                 idx->sel_misc.as<uint32_t>() + 1, s),
+         "mask row kernel");
+    uint32_t n_list = 0;
+    HIPX(idx->dev, hipMemcpyAsync(&n_list, idx->sel_misc.as<uint32_t>() + 1, 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "mask rows");
+    if (n_list == 0) {
+        *n_out = 0;
+        return BV_OK;
+    }
+    return exact_list_topk(idx, q, n_list, k, rows, scores, n_out);
+}
+
+// Dense scores of one query for every row (the scan's score for each row),
+// or with `probed` on an IVF index, for each candidate of its probed lists
+// (idx->cand[0, *n_scored), in gather order).
+static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uint64_t mask_words, float *out,
+                        bool probed = false, uint64_t *n_scored = nullptr) {
     const size_t qb = (size_t)idx->dim * 4;
     HIPX(idx->dev, idx->qin.ensure(qb, 0, idx->stream), "query buffer");
     HIPX(idx->dev, hipMemcpyAsync(idx->qin.p, q, qb, hipMemcpyHostToDevice, idx->stream), "upload");
-    HIPX(idx->dev, idx->dense.ensure(idx->rows * 4, 0, idx->stream), "scratch");
+    uint64_t n = idx->rows;
+    if (probed) {
+        uint64_t per = 0;
+        int rc = ivf_candidates(idx, idx->qin.as<float>(), 1, &per);
+        if (rc) return rc;
+        uint64_t off[2] = {0, 0};
+        HIPX(idx->dev, hipMemcpyAsync(off, idx->cand_off.p, 16, hipMemcpyDeviceToHost, idx->stream), "download");
+        HIPX(idx->dev, hipStreamSynchronize(idx->stream), "candidates");
+        n = off[1] - off[0];
+    }
+    if (n_scored) *n_scored = n;
+    HIPX(idx->dev, idx->dense.ensure(std::max<uint64_t>(n, 1) * 4, 0, idx->stream), "scratch");
     const void *qscan = nullptr;
     uint64_t qstride = 0;
     const bool in_kernel = idx->quant && scan_prep_supported(idx->codec, idx->units, idx->P);
     int rc = in_kernel ? BV_OK : prepare_queries(idx, idx->qin.as<float>(), 1, &qscan, &qstride);
     if (rc) return rc;
-    const uint32_t grid = grid_for(idx, idx->rows);
+    const uint32_t grid = grid_for(idx, std::max<uint64_t>(n, 1));
     const uint32_t *d_mask = nullptr;
     if (mask) {
         HIPX(idx->dev, idx->mask.ensure(mask_words * 4, 0, idx->stream), "mask buffer");
@@ -2062,43 +2170,86 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     }
     a.mask = d_mask;
     a.mask_bits = mask_words * 32;
-    a.n = idx->rows;
+    a.n = n;
+    if (probed) {
+        a.cand = idx->cand.as<uint32_t>();
+        a.cand_off = idx->cand_off.as<uint64_t>();
+    }
     a.kprime = 1;
     a.grid = grid;
     a.dense_out = idx->dense.as<float>();
+    if (n == 0) return BV_OK;
     HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, 1, idx->stream), "scan kernel");
+    if (!out) return BV_OK;  // the scores stay in idx->dense
     HIPX(idx->dev, hipMemcpyAsync(out, idx->dense.p, idx->rows * 4, hipMemcpyDeviceToHost, idx->stream), "download");
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "dense scores");
     return BV_OK;
 }
 
-static int host_query_dense(bv_index *idx, const float *q, uint32_t nq, uint32_t k, const uint32_t *mask,
-                            uint64_t mask_words, uint32_t *rows, float *scores, uint32_t *n_out) {
-    if (idx->ivf) return fail(BV_E_UNSUPPORTED, "IVF queries serve k <= %d", MAX_KPRIME);
-    std::vector<float> s(idx->rows);
-    for (uint32_t i = 0; i < nq; i++) {
-        int rc = dense_scores(idx, q + (size_t)i * idx->dim, nullptr, 0, s.data());
-        if (rc) return rc;
-        std::vector<uint32_t> ids;
-        ids.reserve(idx->rows);
-        for (uint64_t r = 0; r < idx->rows; r++) {
-            if (mask && !((mask[r >> 5] >> (r & 31)) & 1u)) continue;
-            ids.push_back((uint32_t)r);
-        }
-        const size_t kk = std::min<size_t>(k, ids.size());
-        auto better = [&](uint32_t a, uint32_t b) {
-            float sa = s[a] + 0.0f, sb = s[b] + 0.0f;
-            return sa > sb || (sa == sb && a < b);
-        };
-        std::partial_sort(ids.begin(), ids.begin() + kk, ids.end(), better);
-        for (size_t j = 0; j < kk; j++) {
-            rows[(size_t)i * k + j] = ids[j];
-            scores[(size_t)i * k + j] = s[ids[j]] + 0.0f;
-        }
-        n_out[i] = (uint32_t)kk;
+// Top min(k, n_keys) of the keys in idx->sel_keys by a descending device
+// sort: the canonical order (score desc, row asc); empty keys (0) are not
+// returned.  Serves any k (flat.ts:217-239 takes any k).
+static int sorted_topk(bv_index *idx, uint64_t n_keys, uint32_t k, uint32_t *rows, float *scores, uint32_t *n_out) {
+    hipStream_t s = idx->stream;
+    const uint32_t kk = (uint32_t)std::min<uint64_t>(k, n_keys);
+    if (kk == 0) {
+        *n_out = 0;
+        return BV_OK;
     }
-    (void)mask_words;
+    if (n_keys > 0x7fffffffull) return fail(BV_E_UNSUPPORTED, "selection over more than 2^31 - 1 rows");
+    size_t tb = 0;
+    HIPX(idx->dev, sel_sort_desc(nullptr, tb, nullptr, nullptr, n_keys, s), "sort sizing");
+    HIPX(idx->dev, idx->sel_tmp.ensure(std::max<size_t>(tb, 256), 0, s), "scratch");
+    HIPX(idx->dev, idx->sel_sorted.ensure(n_keys * 8, 0, s), "scratch");
+    tb = idx->sel_tmp.cap;
+    HIPX(idx->dev, sel_sort_desc(idx->sel_tmp.p, tb, idx->sel_keys.as<uint64_t>(), idx->sel_sorted.as<uint64_t>(),
+                                 n_keys, s),
+         "sort");
+    HIPX(idx->dev, idx->out_rows.ensure((size_t)kk * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->out_scores.ensure((size_t)kk * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->out_n.ensure(4, 0, s), "scratch");
+    HIPX(idx->dev, sel_keys_to_hits(idx->sel_sorted.as<uint64_t>(), kk, idx->out_rows.as<uint32_t>(),
+                                    idx->out_scores.as<float>(), idx->out_n.as<uint32_t>(), s),
+         "hits kernel");
+    uint32_t n = 0;
+    HIPX(idx->dev, hipMemcpyAsync(&n, idx->out_n.p, 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipMemcpyAsync(rows, idx->out_rows.p, (size_t)kk * 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipMemcpyAsync(scores, idx->out_scores.p, (size_t)kk * 4, hipMemcpyDeviceToHost, s), "download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "selection");
+    *n_out = n;
     return BV_OK;
+}
+
+// Queries with k above the fused top-k's MAX_KPRIME: the dense scores of
+// every row (IVF: of every candidate of the probed lists), then the top k by
+// a device sort.
+static int dense_topk(bv_index *idx, const float *q, uint32_t k, const uint32_t *mask, uint64_t mask_words,
+                      uint32_t *rows, float *scores, uint32_t *n_out) {
+    int rc = ensure_built(idx);
+    if (rc) return rc;
+    if (idx->ivf) {
+        if (mask) return fail(BV_E_UNSUPPORTED, "IVF indexes take no score mask");
+        uint64_t n = 0;
+        rc = dense_scores(idx, q, nullptr, 0, nullptr, true, &n);
+        if (rc) return rc;
+        HIPX(idx->dev, idx->sel_keys.ensure(std::max<uint64_t>(n, 1) * 8, 0, idx->stream), "scratch");
+        HIPX(idx->dev, sel_list_keys(idx->dense.as<float>(), idx->cand.as<uint32_t>(), n,
+                                     idx->sel_keys.as<uint64_t>(), idx->stream),
+             "key kernel");
+        return sorted_topk(idx, n, k, rows, scores, n_out);
+    }
+    rc = dense_scores(idx, q, nullptr, 0, nullptr);
+    if (rc) return rc;
+    const uint32_t *d_mask = nullptr;
+    if (mask) {
+        HIPX(idx->dev, idx->mask.ensure(mask_words * 4, 0, idx->stream), "mask buffer");
+        HIPX(idx->dev, hipMemcpyAsync(idx->mask.p, mask, mask_words * 4, hipMemcpyHostToDevice, idx->stream), "upload");
+        d_mask = idx->mask.as<uint32_t>();
+    }
+    HIPX(idx->dev, idx->sel_keys.ensure(idx->rows * 8, 0, idx->stream), "scratch");
+    HIPX(idx->dev, sel_dense_keys(idx->dense.as<float>(), idx->rows, d_mask, idx->sel_keys.as<uint64_t>(), idx->stream),
+         "key kernel");
+    return sorted_topk(idx, idx->rows, k, rows, scores, n_out);
 }
 
 // ------------------------------------------------------------ stats/exports

@@ -363,4 +363,27 @@ size_t scan_query_lds(int codec, uint32_t P);
 // True when the scan for this codec / row layout transforms fp32 queries itself (ScanArgs::qraw).
 bool scan_prep_supported(int codec, uint32_t units, uint32_t P);
 
+// ---- selection for any k; exact scan of listed rows (bv_select.hip) ---------
+// Keys (make_key) of scores[0, n); rows whose mask bit is clear get key 0.
+hipError_t sel_dense_keys(const float *scores, uint64_t n, const uint32_t *mask, uint64_t *keys, hipStream_t s);
+// Keys of scores[i] for row list[i], i < n.
+hipError_t sel_list_keys(const float *scores, const uint32_t *list, uint64_t n, uint64_t *keys, hipStream_t s);
+// popc[w] = set bits of mask word w below row n.
+hipError_t sel_mask_counts(const uint32_t *mask, uint64_t words, uint64_t n, uint32_t *popc, hipStream_t s);
+// hipCUB exclusive sum (tmp == nullptr: only sizes tmp_bytes).
+hipError_t sel_exclusive_scan(void *tmp, size_t &tmp_bytes, const uint32_t *in, uint32_t *out, uint64_t n,
+                              hipStream_t s);
+// The rows whose mask bit is set, ascending, at list[off[w] ...]; *list_n = their number.
+hipError_t sel_mask_rows(const uint32_t *mask, uint64_t words, uint64_t n, const uint32_t *popc, const uint32_t *off,
+                         uint32_t *list, uint32_t *list_n, hipStream_t s);
+// Key of each listed row's exact score (Store.dotRow, or Store.l2Row when l2)
+// against q; a listed row >= n sets *bad and gets key 0.
+hipError_t sel_exact_row_keys(const float *raw, uint64_t n, uint32_t dim, bool l2, const float *q,
+                              const uint32_t *list, uint64_t n_list, uint64_t *keys, uint32_t *bad, hipStream_t s);
+// hipCUB descending radix sort of n keys (tmp == nullptr: only sizes tmp_bytes).
+hipError_t sel_sort_desc(void *tmp, size_t &tmp_bytes, const uint64_t *in, uint64_t *out, uint64_t n, hipStream_t s);
+// (row, score) of the first k sorted keys; *n_out = how many are not empty.
+hipError_t sel_keys_to_hits(const uint64_t *sorted, uint32_t k, uint32_t *rows, float *scores, uint32_t *n_out,
+                            hipStream_t s);
+
 } // namespace bvk

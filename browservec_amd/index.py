@@ -148,6 +148,31 @@ class NativeIndex:
                                                _ptr(scores), ctypes.byref(n)))
         return [FlatHit(int(rows[i]), float(scores[i])) for i in range(n.value)]
 
+    def query_rows(self, q, rows, k: int) -> list[FlatHit]:
+        """queryRowsExact (src/index.ts:445-464) on the device: the exact
+        scores of the listed rows (Store.dotRow, or Store.l2Row under l2) and
+        their top k, as (row, score)."""
+        q = _f32(q).reshape(-1)
+        _check_len(q, self.dim)
+        lst = np.ascontiguousarray(rows, dtype=np.uint32).reshape(-1)
+        return self._rows_call(self.lib.bv_index_query_rows, q, lst, k)
+
+    def query_rows_masked(self, q, k: int, mask_words) -> list[FlatHit]:
+        """query_rows over the rows whose mask bit is set; the row list is
+        built on the device."""
+        q = _f32(q).reshape(-1)
+        _check_len(q, self.dim)
+        m = np.ascontiguousarray(mask_words, dtype=np.uint32).reshape(-1)
+        return self._rows_call(self.lib.bv_index_query_rows_masked, q, m, k)
+
+    def _rows_call(self, fn, q, arr, k):
+        out_rows = np.empty(max(k, 1), np.uint32)
+        scores = np.empty(max(k, 1), np.float32)
+        n = ctypes.c_uint32()
+        L.check(fn(self.handle, _ptr(q), _ptr(arr) if arr.size else None, arr.size, int(k), _ptr(out_rows),
+                   _ptr(scores), ctypes.byref(n)))
+        return [FlatHit(int(out_rows[i]), float(scores[i])) for i in range(n.value)]
+
     def query_batch(self, packed, n: int, k: int) -> list[list[FlatHit]]:
         packed = _f32(packed).reshape(-1)
         _check_len(packed, int(n) * self.dim)

@@ -111,7 +111,8 @@ static napi_value length_error(napi_env env, size_t want, size_t got) {
 
 /* ---- asynchronous device calls --------------------------------------------- */
 typedef enum {
-    OP_APPEND, OP_QUERY, OP_QUERY_MASKED, OP_QUERY_BATCH, OP_SEARCH, OP_RERANK, OP_BUILD, OP_SAVE, OP_LOAD
+    OP_APPEND, OP_QUERY, OP_QUERY_MASKED, OP_QUERY_BATCH, OP_SEARCH, OP_RERANK, OP_BUILD, OP_SAVE, OP_LOAD,
+    OP_ROWS, OP_ROWS_MASKED
 } op_kind;
 
 typedef struct {
@@ -152,6 +153,12 @@ static void job_execute(napi_env env, void *data) {
         break;
     case OP_RERANK:
         j->rc = bv_index_rerank(j->idx, j->data, j->aux, (uint32_t)j->n_aux, j->k, j->rows, j->scores, j->counts);
+        break;
+    case OP_ROWS:
+        j->rc = bv_index_query_rows(j->idx, j->data, j->aux, j->n_aux, j->k, j->rows, j->scores, j->counts);
+        break;
+    case OP_ROWS_MASKED:
+        j->rc = bv_index_query_rows_masked(j->idx, j->data, j->aux, j->n_aux, j->k, j->rows, j->scores, j->counts);
         break;
     case OP_BUILD: j->rc = bv_index_build(j->idx); break;
     case OP_SAVE: {
@@ -589,6 +596,37 @@ static napi_value rerank(napi_env env, napi_callback_info info) {
     return queue(env, j, argv[0], "browservec.rerank");
 }
 
+/* queryRows(idx, Float32Array q, Uint32Array rows, k) and
+ * queryRowsMasked(idx, Float32Array q, Uint32Array maskWords, k) -> Promise<result>:
+ * queryRowsExact's exact scores of the listed (or masked-in) rows and their top k */
+static napi_value rows_common(napi_env env, napi_callback_info info, int masked) {
+    ARGS(4);
+    size_t qn = 0, an = 0;
+    index_handle *h = get_index(env, argv[0]);
+    const float *q = (const float *)get_typed(env, argv[1], napi_float32_array, &qn);
+    const uint32_t *aux = (const uint32_t *)get_typed(env, argv[2], napi_uint32_array, &an);
+    uint32_t k = 0;
+    if (!h || !q || !aux || !get_u32(env, argv[3], &k)) {
+        napi_throw_type_error(env, NULL, masked ? "queryRowsMasked(idx, Float32Array, Uint32Array, k)"
+                                                : "queryRows(idx, Float32Array, Uint32Array, k)");
+        return NULL;
+    }
+    if (qn != h->dim) return length_error(env, h->dim, qn);
+    job *j = new_job(env, masked ? OP_ROWS_MASKED : OP_ROWS, h);
+    if (!j || !keep(env, j, 0, argv[1]) || !keep(env, j, 1, argv[2]) || !job_result(env, j, 1, k)) {
+        free(j);
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    j->data = q;
+    j->aux = aux;
+    j->n_aux = an;
+    j->k = k;
+    return queue(env, j, argv[0], masked ? "browservec.queryRowsMasked" : "browservec.queryRows");
+}
+static napi_value query_rows(napi_env env, napi_callback_info info) { return rows_common(env, info, 0); }
+static napi_value query_rows_masked(napi_env env, napi_callback_info info) { return rows_common(env, info, 1); }
+
 static napi_value set_nprobe(napi_env env, napi_callback_info info) {
     ARGS(2);
     index_handle *h = get_index(env, argv[0]);
@@ -646,6 +684,7 @@ static napi_value init(napi_env env, napi_value exports) {
         {"size", index_size},          {"append", append},              {"build", build},
         {"query", query},              {"queryMasked", query_masked},   {"queryBatch", query_batch},
         {"search", search},            {"rerank", rerank},              {"setNprobe", set_nprobe},
+        {"queryRows", query_rows},     {"queryRowsMasked", query_rows_masked},
         {"stats", stats},              {"lastError", last_error},
         {"saveSection", save_section}, {"loadSection", load_section},
     };

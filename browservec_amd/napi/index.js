@@ -18,9 +18,10 @@
 //   - setNprobe / nlist / nprobe / tunedRecall / trainMode on IVF kinds,
 //     ingestMode on quantized kinds, chunkCount everywhere.
 // search() (approximate top-fetch + exact re-rank in one device call),
-// rerankExact() and saveSection() / loadSection() (a snapshot section that
-// skips re-encoding and re-training on load) are extras a caller may use
-// explicitly.
+// rerankExact(), queryRowsExact() / queryRowsMasked() (BrowserVec's exact
+// filtered scan, src/index.ts:445-464, on the device rows) and
+// saveSection() / loadSection() (a snapshot section that skips re-encoding
+// and re-training on load) are extras a caller may use explicitly.
 const path = require('path');
 
 const native = require(path.join(__dirname, '..', 'lib', 'browservec_napi.node'));
@@ -117,6 +118,19 @@ class HipIndex {
   rerankExact(q, candidates, k) {
     const rows = Uint32Array.from(candidates.map(function (h) { return h.row; }));
     return native.rerank(this.handle, f32(q), rows, k).then((res) => toHits(res, 0, k));
+  }
+  // queryRowsExact (src/index.ts:445-464): Store.dotRow / Store.l2Row of
+  // each listed row, bit for bit, and their top k as {row, score} (rows in
+  // the index's numbering, ties ordered by row).
+  queryRowsExact(q, rows, k) {
+    const r = rows instanceof Uint32Array ? rows : Uint32Array.from(rows);
+    return native.queryRows(this.handle, f32(q), r, k).then((res) => toHits(res, 0, k));
+  }
+  // The same over the rows whose mask bit is set (the row list is built on
+  // the device): a selective filter of any size.
+  queryRowsMasked(q, k, maskWords) {
+    const m = maskWords instanceof Uint32Array ? maskWords : Uint32Array.from(maskWords);
+    return native.queryRowsMasked(this.handle, f32(q), m, k).then((res) => toHits(res, 0, k));
   }
   // Snapshot index section (codes, scales, IVF state): a load from the
   // snapshot's rows plus this section skips re-encoding and re-training

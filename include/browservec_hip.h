@@ -152,7 +152,9 @@ int bv_index_append(bv_index *idx, const float *data, uint64_t n_floats, uint64_
 /* ---- queries ---------------------------------------------------------------- */
 /* VectorIndex.query (flat.ts:38): top-k of one query.  Flat kinds are exact;
  * quantized kinds return the approximate top-k by code score (the caller
- * re-ranks, as BrowserVec.query does).  *n_out = min(k, rows). */
+ * re-ranks, as BrowserVec.query does).  *n_out = min(k, rows).  Any k on
+ * flat kinds (above 1024: every row's score, then a device sort); IVF
+ * kinds serve k <= 1024. */
 int bv_index_query(bv_index *idx, const float *q, uint32_t k, uint32_t *rows, float *scores, uint32_t *n_out);
 
 /* queryMasked (flat.ts:128-130, quant.ts:174-176): rows whose bit (LSB-first,
@@ -177,6 +179,22 @@ int bv_index_set_nprobe(bv_index *idx, uint32_t nprobe);
  * quantized kinds keep them). */
 int bv_index_rerank(bv_index *idx, const float *q, const uint32_t *cand, uint32_t n_cand, uint32_t k,
                     uint32_t *rows, float *scores, uint32_t *n_out);
+
+/* BrowserVec.queryRowsExact (src/index.ts:445-464): the exact score of each
+ * listed row against q -- Store.dotRow (store.ts:114-130), or Store.l2Row
+ * (store.ts:137-160) on an l2 index, in their f64 order, stored as f32 --
+ * and the top k of them, ordered (score desc, row asc).  Any k and any
+ * number of rows; a row >= size fails with BV_E_INVALID.  The reference
+ * runs this on the host for filters that match few rows (and for selective
+ * filters on IVF indexes); here it runs on the stored device rows. */
+int bv_index_query_rows(bv_index *idx, const float *q, const uint32_t *list, uint64_t n_list, uint32_t k,
+                        uint32_t *rows, float *scores, uint32_t *n_out);
+/* bv_index_query_rows over the rows whose bit is set in mask_words (the
+ * queryMasked layout, scoreMask.ts:23-98: bit r & 31 of word r >> 5; bits at
+ * or past size are ignored, a short mask leaves the remaining rows out).  The
+ * row list is built on the device from the mask. */
+int bv_index_query_rows_masked(bv_index *idx, const float *q, const uint32_t *mask_words, uint64_t n_words,
+                               uint32_t k, uint32_t *rows, float *scores, uint32_t *n_out);
 
 /* BrowserVec.query's quantized path in one device round trip (index.ts:
  * 402-421): approximate top-`fetch`, then exact re-rank to top-`k`.  With

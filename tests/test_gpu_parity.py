@@ -360,6 +360,11 @@ def test_browservec_api(ctx):
         assert res[0]["id"] not in [r["id"] for r in res2] and len(res2) == 10
         filt = db.query(q, k=5, filter=lambda m: m is not None and m["even"])
         assert all(int(r["id"][1:]) % 2 == 0 for r in filt) and len(filt) == 5
+        # 499 matching rows take queryRowsExact: exact dotRow scores, top 5
+        even = np.array([i for i in range(0, 1000, 2) if f"v{i}" != res[0]["id"]], np.uint32)
+        wr, ws = o.topk_canonical(exact[even], 5, even)
+        assert [int(r["id"][1:]) for r in filt] == wr.tolist()
+        assert [r["score"] for r in filt] == ws.tolist()
         st = db.stats()
         assert st["count"] == 999 and st["deleted"] == 1
         db.destroy()

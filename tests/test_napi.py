@@ -37,7 +37,7 @@ def test_addon_exports_the_seam():
 const m = require({json.dumps(MODULE)});
 const has = (C) => ['size', 'append', 'query', 'queryMasked', 'queryBatch', 'setNprobe', 'destroy', 'search',
   'rerankExact', 'chunkCount', 'nlist', 'nprobe', 'tunedRecall', 'trainMode', 'ingestMode', 'build',
-  'saveSection', 'loadSection']
+  'saveSection', 'loadSection', 'queryRowsExact', 'queryRowsMasked']
   .filter((k) => k in C.prototype);
 console.log(JSON.stringify({{abi: m.abiVersion, native: Object.keys(m.native),
   flat: has(m.HipFlatIndex), quant: has(m.HipQuantIndex), ivf: has(m.HipIvfIndex),
@@ -47,14 +47,14 @@ console.log(JSON.stringify({{abi: m.abiVersion, native: Object.keys(m.native),
     out = json.loads(r.stdout.strip().splitlines()[-1])
     assert out["abi"] == 1
     common = {"size", "append", "query", "destroy", "search", "rerankExact", "chunkCount", "saveSection",
-              "loadSection"}
+              "loadSection", "queryRowsExact", "queryRowsMasked"}
     assert set(out["flat"]) == common | {"queryMasked", "queryBatch"}
     assert set(out["quant"]) == common | {"queryMasked", "ingestMode"}
     ivf = common | {"setNprobe", "nlist", "nprobe", "tunedRecall", "trainMode", "build"}
     assert set(out["ivf"]) == ivf
     assert set(out["ivfquant"]) == ivf | {"ingestMode"}
     for fn in ("openDevice", "debugInject", "createIndex", "append", "build", "query", "queryMasked", "queryBatch",
-               "search", "rerank", "saveSection", "loadSection"):
+               "search", "rerank", "saveSection", "loadSection", "queryRows", "queryRowsMasked"):
         assert fn in out["native"], fn
 
 
@@ -101,6 +101,9 @@ const dim = %(dim)d, n = %(n)d, nq = %(nq)d;
   out.approx = await quant.query(qs.subarray(0, dim), 40);
   out.search = await quant.search(qs, nq, 40, 10);
   out.rerank = await quant.rerankExact(qs.subarray(0, dim), out.approx, 10);
+  out.rows = await quant.queryRowsExact(qs.subarray(0, dim), [5, 17, 2000, 40, 999, 2999], 4);
+  out.rowsMasked = await flat.queryRowsMasked(qs.subarray(dim, 2 * dim), 6, new Uint32Array([0xf0f0f0f0, 0x1, 0x80000000]));
+  try { await quant.queryRowsExact(qs.subarray(0, dim), [1, n], 2); } catch (e) { out.rowsBad = [e.code, e.message]; }
   const ivf = m.buildIndex(ctx, dim, 'cosine', 8, {}, {nlist: 16, iters: 3, nprobe: 4});
   await ivf.append(rows, n);
   out.trainBefore = ivf.trainMode;
@@ -185,6 +188,9 @@ def test_node_results_equal_python_binding(tmp_path):
             assert [h["row"] for h in out["search"][i]] == rows[i, :cnt[i]].tolist()
             assert np.array_equal(np.float32([h["score"] for h in out["search"][i]]), scores[i, :cnt[i]])
         same(out["rerank"], quant.rerank(q[0], [h.row for h in py_approx], 10))
+        same(out["rows"], quant.query_rows(q[0], [5, 17, 2000, 40, 999, 2999], 4))
+        same(out["rowsMasked"], flat.query_rows_masked(q[1], 6, np.array([0xF0F0F0F0, 1, 0x80000000], np.uint32)))
+        assert out["rowsBad"] == ["BV_E_INVALID", f"a listed row is out of range (the index holds {n} rows)"]
         ivf = IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 16, "iters": 3, "nprobe": 4})
         ivf.append(x, n)
         for i in range(nq):
