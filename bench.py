@@ -541,6 +541,24 @@ def main():
     flat.destroy()
     idx.destroy()
 
+    # ---- host append: 262,144 rows from pageable host memory (staged through
+    # pinned buffers, encode overlapped) and from a pinned source -----------------
+    log("host append")
+    nh = min(262_144, args.rows)
+    xh_part = x[:nh].cpu().numpy()
+    xh_pin = x[:nh].cpu().pin_memory()
+    append_gbs = {}
+    for label, src in (("pageable", xh_part), ("pinned", xh_pin.numpy())):
+        best = 0.0
+        for _ in range(3):
+            ai = QuantIndex(ctx, args.dim, bits=args.bits)
+            t = time.perf_counter()
+            ai.append(src, nh)
+            best = max(best, nh * args.dim * 4 / (time.perf_counter() - t) / 1e9)
+            ai.destroy()
+        append_gbs[label] = round(best, 1)
+    del xh_part, xh_pin
+
     # ---- CPU baseline -------------------------------------------------------------
     cpu = None
     if not args.no_cpu_baseline:
@@ -611,6 +629,8 @@ def main():
         "latency_ms_sync_p50": round(lat_p50, 4),
         "fp32_flat_cosine_batch_qps": round(flat_qps, 1),
         "build_s": round(build_s, 3),
+        "append_host_gbs": dict(append_gbs, rows=nh, what="QuantIndex.append of fp32 rows from host memory, "
+                                                          "upload + rotate + quantize, best of 3"),
         "device": info["name"],
         "hbm_copy_gbs": round(copy_bandwidth(torch), 1),  # measured 1 GiB device copy, read + write
         "stream_read_gbs": ceiling,

@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <thread>
 #include <string>
 #include <vector>
 
@@ -166,6 +167,10 @@ struct bv_index {
     DevBuf sel_list, sel_popc, sel_off, sel_misc;  // listed rows; mask word counts and offsets; flag + count
     HostBuf h_cnt;
     HostBuf h_rows, h_scores, h_n, h_flag;
+    // host appends: rows staged through two pinned buffers on a copy stream
+    hipStream_t copy_stream = nullptr;
+    hipEvent_t up_ev[2] = {nullptr, nullptr};
+    HostBuf up_ring[2];
 
     uint32_t nprobe_override = 0;
 
@@ -404,6 +409,10 @@ extern "C" int bv_index_destroy(bv_index *idx) {
     }
     if (idx->ev0) (void)hipEventDestroy(idx->ev0);
     if (idx->ev1) (void)hipEventDestroy(idx->ev1);
+    if (idx->copy_stream) (void)hipStreamSynchronize(idx->copy_stream);
+    for (hipEvent_t e : idx->up_ev)
+        if (e) (void)hipEventDestroy(e);
+    if (idx->copy_stream) (void)hipStreamDestroy(idx->copy_stream);
     if (idx->stream) (void)hipStreamDestroy(idx->stream);
     delete idx;
     return BV_OK;
@@ -580,6 +589,67 @@ static int encode_range(bv_index *idx, uint64_t first, uint64_t count, const int
     return BV_OK;
 }
 
+// Host appends larger than one staging chunk go through two pinned buffers:
+// while chunk i's rows travel to the device on the copy stream, the host
+// copies chunk i + 1 into the other buffer (several threads), and the index
+// stream encodes chunk i - 1 once its copy has landed.  A pageable source
+// otherwise crosses PCIe at about half the rate of a pinned one.
+constexpr size_t UPLOAD_CHUNK = 64ull << 20;
+constexpr unsigned UPLOAD_THREADS = 8;
+
+static int staging_ready(bv_index *idx) {
+    if (!idx->copy_stream)
+        HIPX(idx->dev, hipStreamCreateWithFlags(&idx->copy_stream, hipStreamNonBlocking), "copy stream");
+    for (hipEvent_t &e : idx->up_ev)
+        if (!e) HIPX(idx->dev, hipEventCreateWithFlags(&e, hipEventDisableTiming), "copy event");
+    for (HostBuf &b : idx->up_ring) HIPX(idx->dev, b.ensure(UPLOAD_CHUNK), "pinned staging buffer");
+    return BV_OK;
+}
+
+static void parallel_copy(void *dst, const void *src, size_t bytes) {
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const unsigned nt = (unsigned)std::min<size_t>(std::min(UPLOAD_THREADS, hw), std::max<size_t>(1, bytes >> 22));
+    if (nt <= 1) {
+        std::memcpy(dst, src, bytes);
+        return;
+    }
+    const size_t part = (bytes / nt + 63) & ~size_t(63);
+    std::vector<std::thread> th;
+    th.reserve(nt);
+    for (unsigned t = 0; t < nt; ++t) {
+        const size_t o = (size_t)t * part;
+        if (o >= bytes) break;
+        const size_t len = std::min(part, bytes - o);
+        th.emplace_back([=] { std::memcpy((char *)dst + o, (const char *)src + o, len); });
+    }
+    for (auto &x : th) x.join();
+}
+
+// A source the caller already pinned (hipHostMalloc) is copied directly.
+static bool host_pinned(const void *p) {
+    hipPointerAttribute_t at{};
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+        (void)hipGetLastError();  // pageable memory: clear the lookup's error
+        return false;
+    }
+    return at.type == hipMemoryTypeHost;
+}
+
+// Chunk rows [r0, r0 + m) from host `src` into idx->raw through staging
+// buffer b; the index stream waits for the copy.
+static int stage_rows(bv_index *idx, const float *src, uint64_t r0, uint64_t m, int b) {
+    const size_t rb = (size_t)idx->dim * 4, bytes = m * rb;
+    HIPX(idx->dev, hipEventSynchronize(idx->up_ev[b]), "staging wait");  // the buffer's last copy has landed
+    parallel_copy(idx->up_ring[b].p, src, bytes);
+    HIPX(idx->dev,
+         hipMemcpyAsync(idx->raw.as<char>() + r0 * rb, idx->up_ring[b].p, bytes, hipMemcpyHostToDevice,
+                        idx->copy_stream),
+         "row upload");
+    HIPX(idx->dev, hipEventRecord(idx->up_ev[b], idx->copy_stream), "copy event");
+    HIPX(idx->dev, hipStreamWaitEvent(idx->stream, idx->up_ev[b], 0), "copy wait");
+    return BV_OK;
+}
+
 // Append: every allocation happens first, so a failure (or an injected one)
 // leaves the index exactly as it was; then the rows are copied, the reservoir
 // plan is committed and the rows are encoded.
@@ -612,31 +682,51 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
             HIPX(idx->dev, idx->ivf_idx2.ensure(std::max<size_t>(taken, 1) * 4, 0, idx->stream), "scratch");
         }
     }
-    HIPX(idx->dev,
-         hipMemcpyAsync(idx->raw.as<char>() + base * rb, data, count * rb,
-                        device_src ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, idx->stream),
-         "row upload");
+    const bool staged = !device_src && count * rb > UPLOAD_CHUNK && !host_pinned(data);
+    if (staged) {
+        int rc = staging_ready(idx);
+        if (rc) return rc;
+    } else {
+        HIPX(idx->dev,
+             hipMemcpyAsync(idx->raw.as<char>() + base * rb, data, count * rb,
+                            device_src ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, idx->stream),
+             "row upload");
+    }
     if (idx->ivf) {
         HIPX(idx->dev,
              hipMemcpyAsync(idx->ivf_slot.p, plan.slots.data(), count * 4, hipMemcpyHostToDevice, idx->stream),
              "upload");
-        ivf_commit(idx, base, plan);
     }
-    if (norms)
-        HIPX(idx->dev,
-             launch_row_sqnorms(idx->raw.as<float>() + base * idx->dim, count, idx->dim, idx->rsq.as<float>() + base,
-                                idx->rsq_max.as<uint32_t>(), idx->stream),
-             "norm kernel");
     const bool extend = idx->ivf && idx->built_rows == base && idx->nlist && idx->d.ivf_incremental;
-    if (idx->quant) {
-        int rc = encode_range(idx, base, count, idx->ivf ? idx->ivf_slot.as<int32_t>() : nullptr);
-        if (rc) return rc;
-        if (code_norms)
+    // the rows in chunks (one chunk unless staged): upload, norms, encode
+    const uint64_t crow = staged ? std::max<uint64_t>(1, UPLOAD_CHUNK / rb) : count;
+    for (uint64_t off = 0, i = 0; off < count; off += crow, ++i) {
+        const uint64_t m = std::min(crow, count - off), r0 = base + off;
+        if (staged) {
+            int rc = stage_rows(idx, data + off * idx->dim, r0, m, (int)(i & 1));
+            if (rc) {  // rows copied so far are not counted: the index keeps its size
+                (void)hipStreamSynchronize(idx->copy_stream);
+                (void)hipStreamSynchronize(idx->stream);
+                return rc;
+            }
+        }
+        if (norms)
             HIPX(idx->dev,
-                 launch_row_code_norms(idx->codes.as<uint32_t>() + base * idx->words_per_row, count,
-                                       idx->words_per_row, idx->cnorm.as<float>() + base, idx->stream),
+                 launch_row_sqnorms(idx->raw.as<float>() + r0 * idx->dim, m, idx->dim, idx->rsq.as<float>() + r0,
+                                    idx->rsq_max.as<uint32_t>(), idx->stream),
                  "norm kernel");
-    } else if (idx->ivf) {
+        if (idx->quant) {
+            int rc = encode_range(idx, r0, m, idx->ivf ? idx->ivf_slot.as<int32_t>() + off : nullptr);
+            if (rc) return rc;
+            if (code_norms)
+                HIPX(idx->dev,
+                     launch_row_code_norms(idx->codes.as<uint32_t>() + r0 * idx->words_per_row, m,
+                                           idx->words_per_row, idx->cnorm.as<float>() + r0, idx->stream),
+                     "norm kernel");
+        }
+    }
+    if (idx->ivf) ivf_commit(idx, base, plan);
+    if (!idx->quant && idx->ivf) {
         int rc = ivf_sample_raw(idx, base, plan.slots);
         if (rc) return rc;
     }
