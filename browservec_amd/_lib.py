@@ -101,6 +101,7 @@ SIGNATURES = {
     "bv_index_set_nprobe": [vp, u32],
     "bv_index_rerank": [vp, vp, vp, u32, u32, vp, vp, vp],
     "bv_index_query_rows": [vp, vp, vp, u64, u32, vp, vp, vp],
+    "bv_index_set_query_streams": [vp, u32],
     "bv_index_query_rows_masked": [vp, vp, vp, u64, u32, vp, vp, vp],
     "bv_index_search": [vp, vp, u32, u32, u32, vp, vp, vp],
     "bv_index_search_device": [vp, vp, u32, u32, u32, vp, vp, vp],

@@ -199,6 +199,17 @@ struct bv_index {
     double last_query_ms = 0, last_query_gpu_ms = 0;
     uint64_t last_scanned = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    // a second query stream (bv_index_set_query_streams): consecutive fused
+    // queries alternate between the index stream and this one, each with its
+    // own scan scratch, so one query's tail overlaps the next one's scan
+    struct ScanLane {
+        hipStream_t stream = nullptr;
+        hipEvent_t done = nullptr;
+        DevBuf qstate, wmax, cand_keys, merged, merged_n;
+    } lane2;
+    uint32_t query_streams = 1, next_lane = 0;
+    bool lane2_pending = false;               // lane2 has queries the index stream has not joined
+    hipEvent_t ev_mut = nullptr;              // recorded after work that changes the index's buffers
 
     // kernel timing
     bool timing = false;
@@ -409,6 +420,10 @@ extern "C" int bv_index_destroy(bv_index *idx) {
     }
     if (idx->ev0) (void)hipEventDestroy(idx->ev0);
     if (idx->ev1) (void)hipEventDestroy(idx->ev1);
+    if (idx->lane2.stream) (void)hipStreamSynchronize(idx->lane2.stream);
+    if (idx->lane2.done) (void)hipEventDestroy(idx->lane2.done);
+    if (idx->lane2.stream) (void)hipStreamDestroy(idx->lane2.stream);
+    if (idx->ev_mut) (void)hipEventDestroy(idx->ev_mut);
     if (idx->copy_stream) (void)hipStreamSynchronize(idx->copy_stream);
     for (hipEvent_t e : idx->up_ev)
         if (e) (void)hipEventDestroy(e);
@@ -589,6 +604,9 @@ static int encode_range(bv_index *idx, uint64_t first, uint64_t count, const int
     return BV_OK;
 }
 
+static int lanes_join(bv_index *idx);
+static int lanes_mark(bv_index *idx);
+
 // Host appends larger than one staging chunk go through two pinned buffers:
 // while chunk i's rows travel to the device on the copy stream, the host
 // copies chunk i + 1 into the other buffer (several threads), and the index
@@ -656,6 +674,8 @@ static int stage_rows(bv_index *idx, const float *src, uint64_t r0, uint64_t m, 
 static int append_common(bv_index *idx, const float *data, bool device_src, uint64_t count) {
     const uint64_t base = idx->rows, total = base + count;
     const size_t rb = (size_t)idx->dim * 4;
+    int jrc = lanes_join(idx);  // buffers may be reallocated below
+    if (jrc) return jrc;
     if (idx->dev->inject_append_oom) {
         idx->dev->inject_append_oom = false;
         return fail(BV_E_OOM, "row buffer: out of device memory");
@@ -736,7 +756,7 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
     }
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "append");
     idx->rows = total;
-    return BV_OK;
+    return lanes_mark(idx);
 }
 
 extern "C" int bv_index_append(bv_index *idx, const float *data, uint64_t n_floats, uint64_t count) {
@@ -771,7 +791,8 @@ extern "C" int bv_index_append_device(bv_index *idx, const float *d_data, uint64
 // (by its codes for quantized kinds) and the CSR lists are built on the
 // device.
 static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
-                     const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores, uint32_t *d_n);
+                     const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores, uint32_t *d_n,
+                     bool may_alternate = false);
 
 // nprobe auto-tune for targetRecall (src/index/ivfTune.ts:31-42,
 // ivfquant.ts:322-344, ivf.ts:269-291), after a build, when no nprobe is
@@ -1128,30 +1149,49 @@ static void scan_bind(const ScanLayout &L, char *base, uint32_t rr_dim, ScanArgs
     a.merged_n = (uint32_t *)(base + L.merged_n);
 }
 
-static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kprime, uint32_t rr_dim, ScanArgs &a) {
+static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kprime, uint32_t rr_dim, ScanArgs &a,
+                        bv_index::ScanLane *lane = nullptr) {
     const ScanLayout L = scan_layout(nq, grid, kprime);
+    DevBuf &qstate = lane ? lane->qstate : idx->qstate, &wmax = lane ? lane->wmax : idx->wmax;
+    DevBuf &cand_keys = lane ? lane->cand_keys : idx->cand_keys, &merged = lane ? lane->merged : idx->merged;
+    DevBuf &merged_n = lane ? lane->merged_n : idx->merged_n;
+    hipStream_t s = lane ? lane->stream : idx->stream;
     {
-        const size_t old = idx->qstate.cap;
-        HIPX(idx->dev, idx->qstate.ensure((size_t)nq * sizeof(QState), 0, idx->stream), "scratch");
-        if (idx->qstate.cap != old)
-            HIPX(idx->dev, hipMemsetAsync(idx->qstate.p, 0, idx->qstate.cap, idx->stream), "scratch");
+        const size_t old = qstate.cap;
+        HIPX(idx->dev, qstate.ensure((size_t)nq * sizeof(QState), 0, s), "scratch");
+        if (qstate.cap != old) HIPX(idx->dev, hipMemsetAsync(qstate.p, 0, qstate.cap, s), "scratch");
     }
     {
-        const size_t old = idx->wmax.cap;
-        HIPX(idx->dev, idx->wmax.ensure(L.cand_keys - L.wmax, 0, idx->stream), "scratch");
-        if (idx->wmax.cap != old) HIPX(idx->dev, hipMemsetAsync(idx->wmax.p, 0, idx->wmax.cap, idx->stream), "scratch");
+        const size_t old = wmax.cap;
+        HIPX(idx->dev, wmax.ensure(L.cand_keys - L.wmax, 0, s), "scratch");
+        if (wmax.cap != old) HIPX(idx->dev, hipMemsetAsync(wmax.p, 0, wmax.cap, s), "scratch");
     }
-    HIPX(idx->dev, idx->cand_keys.ensure((size_t)nq * L.cap * 16, 0, idx->stream), "scratch");
-    HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, idx->stream), "scratch");
-    HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, idx->stream), "scratch");
-    a.qs = idx->qstate.as<QState>();
-    a.wmax = idx->wmax.as<uint64_t>();
-    a.cand_keys = idx->cand_keys.as<uint64_t>();
+    HIPX(idx->dev, cand_keys.ensure((size_t)nq * L.cap * 16, 0, s), "scratch");
+    HIPX(idx->dev, merged.ensure((size_t)nq * kprime * 8, 0, s), "scratch");
+    HIPX(idx->dev, merged_n.ensure((size_t)nq * 4, 0, s), "scratch");
+    a.qs = qstate.as<QState>();
+    a.wmax = wmax.as<uint64_t>();
+    a.cand_keys = cand_keys.as<uint64_t>();
     a.cand_cap = L.cap;
     a.wcap = L.wcap;
     a.wstride = L.wcap + ((rr_dim & ~3u) + 1) / 2 * 2;  // list + re-rank staging (doubles)
-    a.merged = idx->merged.as<uint64_t>();
-    a.merged_n = idx->merged_n.as<uint32_t>();
+    a.merged = merged.as<uint64_t>();
+    a.merged_n = merged_n.as<uint32_t>();
+    return BV_OK;
+}
+
+// Work that changes the index's buffers first waits for the second query
+// stream's queries (host wait: a buffer may be freed right after), and is
+// followed by ev_mut, which the second stream waits on before its next query.
+static int lanes_join(bv_index *idx) {
+    if (!idx->lane2_pending) return BV_OK;
+    HIPX(idx->dev, hipStreamSynchronize(idx->lane2.stream), "query stream");
+    idx->lane2_pending = false;
+    return BV_OK;
+}
+static int lanes_mark(bv_index *idx) {
+    if (!idx->lane2.stream) return BV_OK;
+    HIPX(idx->dev, hipEventRecord(idx->ev_mut, idx->stream), "event");
     return BV_OK;
 }
 
@@ -1229,7 +1269,7 @@ static int prepare_queries(bv_index *idx, const float *d_q, uint32_t nq, const v
     return BV_OK;
 }
 
-static void timing_begin(bv_index *idx) {
+static void timing_begin(bv_index *idx, hipStream_t s = nullptr) {
     if (!idx->timing) return;
     if (idx->tev_used == idx->tev.size()) {
         hipEvent_t a, b;
@@ -1237,16 +1277,17 @@ static void timing_begin(bv_index *idx) {
         if (hipEventCreate(&b) != hipSuccess) return;
         idx->tev.push_back({a, b});
     }
-    (void)hipEventRecord(idx->tev[idx->tev_used].first, idx->stream);
+    (void)hipEventRecord(idx->tev[idx->tev_used].first, s ? s : idx->stream);
 }
-static void timing_end(bv_index *idx) {
+static void timing_end(bv_index *idx, hipStream_t s = nullptr) {
     if (!idx->timing || idx->tev_used >= idx->tev.size()) return;
-    (void)hipEventRecord(idx->tev[idx->tev_used].second, idx->stream);
+    (void)hipEventRecord(idx->tev[idx->tev_used].second, s ? s : idx->stream);
     idx->tev_used++;
 }
 static void timing_collect(bv_index *idx) {
     if (idx->tev_used == 0) return;
     (void)hipStreamSynchronize(idx->stream);
+    if (idx->lane2.stream) (void)hipStreamSynchronize(idx->lane2.stream);
     for (size_t i = 0; i < idx->tev_used; i++) {
         float ms = 0;
         if (hipEventElapsedTime(&ms, idx->tev[i].first, idx->tev[i].second) == hipSuccess) idx->scan_ms += ms;
@@ -1287,9 +1328,23 @@ static void scan_common(const bv_index *idx, const float *d_q, uint64_t n, uint3
 // The fused single-launch scan (one query per grid row): query transform,
 // scan, top-kprime and exact re-rank.
 static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
-                     const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
+                     const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores, uint32_t *d_n,
+                     bool may_alternate) {
     ScanArgs a{};
     int rc = BV_OK;
+    // with two query streams, every other call runs on the second one (its
+    // own scan scratch; flat indexes whose scan needs no shared query buffer)
+    bv_index::ScanLane *lane = nullptr;
+    hipStream_t s = idx->stream;
+    if (may_alternate && idx->query_streams == 2 && !idx->ivf &&
+        (!idx->quant || scan_prep_supported(idx->codec, idx->units, idx->P))) {
+        if (idx->next_lane == 1) {
+            lane = &idx->lane2;
+            s = lane->stream;
+            HIPX(idx->dev, hipStreamWaitEvent(s, idx->ev_mut, 0), "event wait");
+        }
+        idx->next_lane ^= 1u;
+    }
     if (idx->quant && scan_prep_supported(idx->codec, idx->units, idx->P)) {
         // the scan kernel rotates and transforms the fp32 queries itself
         a.qraw = d_q;
@@ -1312,12 +1367,16 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
         a.cand_off = idx->cand_off.as<uint64_t>();
     }
     const uint32_t grid = grid_for(idx, std::max<uint64_t>(n, 1));
-    rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a);
+    rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a, lane);
     if (rc) return rc;
     scan_common(idx, d_q, n, grid, kprime, k_out, rerank, d_mask, mask_bits, d_rows, d_scores, d_n, a);
-    timing_begin(idx);
-    HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, idx->stream), "scan kernel");
-    timing_end(idx);
+    timing_begin(idx, s);
+    HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, s), "scan kernel");
+    timing_end(idx, s);
+    if (lane) {
+        HIPX(idx->dev, hipEventRecord(lane->done, s), "event");
+        idx->lane2_pending = true;
+    }
     idx->last_scanned = n * nq;
     return BV_OK;
 }
@@ -1788,9 +1847,13 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
 //   outputs   : device arrays [nq][k_out], [nq]
 static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                         const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores,
-                        uint32_t *d_n) {
-    if (mq_eligible(idx, nq, d_mask)) return run_batched(idx, d_q, nq, kprime, k_out, rerank, d_rows, d_scores, d_n);
-    return run_fused(idx, d_q, nq, kprime, k_out, rerank, d_mask, mask_bits, d_rows, d_scores, d_n);
+                        uint32_t *d_n, bool may_alternate = false) {
+    if (mq_eligible(idx, nq, d_mask)) {
+        int rc = lanes_join(idx);  // the batch path shares the index stream's scratch and outputs
+        if (rc) return rc;
+        return run_batched(idx, d_q, nq, kprime, k_out, rerank, d_rows, d_scores, d_n);
+    }
+    return run_fused(idx, d_q, nq, kprime, k_out, rerank, d_mask, mask_bits, d_rows, d_scores, d_n, may_alternate);
 }
 
 // Queries per device call for query batches: the matrix-core path takes
@@ -1973,7 +2036,26 @@ extern "C" int bv_index_search_device(bv_index *idx, const float *d_queries, uin
         return fail(BV_E_UNSUPPORTED, "fetch %u exceeds the fused top-k limit %d", fe, MAX_KPRIME);
     rc = ensure_built(idx);
     if (rc) return rc;
-    return run_pipeline(idx, d_queries, nq, fe ? fe : kk, kk, fe != 0, nullptr, 0, d_rows, d_scores, d_n_out);
+    return run_pipeline(idx, d_queries, nq, fe ? fe : kk, kk, fe != 0, nullptr, 0, d_rows, d_scores, d_n_out, true);
+}
+
+extern "C" int bv_index_set_query_streams(bv_index *idx, uint32_t n) {
+    if (!idx) return fail(BV_E_INVALID, "null index");
+    std::lock_guard<std::recursive_mutex> lock(idx->mu);
+    int rc = check_live(idx);
+    if (rc) return rc;
+    if (n != 1 && n != 2) return fail(BV_E_INVALID, "query streams must be 1 or 2, got %u", n);
+    if (n == 2 && !idx->lane2.stream) {
+        HIPX(idx->dev, hipStreamCreateWithFlags(&idx->lane2.stream, hipStreamNonBlocking), "query stream");
+        HIPX(idx->dev, hipEventCreateWithFlags(&idx->lane2.done, hipEventDisableTiming), "event");
+        HIPX(idx->dev, hipEventCreateWithFlags(&idx->ev_mut, hipEventDisableTiming), "event");
+        HIPX(idx->dev, hipEventRecord(idx->ev_mut, idx->stream), "event");
+    }
+    rc = lanes_join(idx);
+    if (rc) return rc;
+    idx->query_streams = n;
+    idx->next_lane = 0;
+    return BV_OK;
 }
 
 // bv_index_search_device without any device allocation: the fused scan on
@@ -2032,6 +2114,8 @@ extern "C" int bv_index_sync(bv_index *idx) {
     int rc = check_live(idx);
     if (rc) return rc;
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "sync");
+    rc = lanes_join(idx);
+    if (rc) return rc;
     return BV_OK;
 }
 
@@ -2733,7 +2817,7 @@ extern "C" int bv_index_load_section(bv_index *idx, const float *data, uint64_t 
     }
     HIPX(idx->dev, hipStreamSynchronize(s), "load");
     idx->rows = count;
-    return BV_OK;
+    return lanes_mark(idx);
 }
 
 extern "C" int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *list_off, uint32_t *list_rows) {

@@ -1070,8 +1070,8 @@ __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
             above += excl;
             rem -= excl;
             lo = G;
-            const uint64_t top = G + ((1ull << shift) - 1);
-            hi = top < hi ? top : hi;
+            const uint64_t w = (1ull << shift) - 1;  // the bin's last key, without wrapping past 2^64
+            hi = hi - G > w ? G + w : hi;
         }
     }
     if (tid == 0) s_cnt = 0;

@@ -285,6 +285,11 @@ class NativeIndex:
     def sync(self) -> None:
         L.check(self.lib.bv_index_sync(self.handle))
 
+    def set_query_streams(self, n: int) -> None:
+        """1 or 2 streams for search_device's single queries (2: consecutive
+        calls overlap; each call in flight needs its own outputs)."""
+        L.check(self.lib.bv_index_set_query_streams(self.handle, int(n)))
+
     def stream_ptr(self) -> int:
         s = ctypes.c_void_p()
         L.check(self.lib.bv_index_stream(self.handle, ctypes.byref(s)))

@@ -210,6 +210,16 @@ int bv_index_search(bv_index *idx, const float *queries, uint32_t nq, uint32_t f
  * and wait once for the batch (one overflow flag per query is read back). */
 int bv_index_search_device(bv_index *idx, const float *d_queries, uint32_t nq, uint32_t fetch, uint32_t k,
                            uint32_t *d_rows, float *d_scores, uint32_t *d_n_out);
+
+/* Query streams for bv_index_search_device (no counterpart in the
+ * reference; for callers that keep several single queries in flight):
+ * n = 2 lets consecutive fused calls (flat indexes, fewer than 8 queries per
+ * call, no IVF) alternate between the index's stream and a second stream,
+ * each with its own scan scratch, so one query's final selection overlaps
+ * the next query's scan.  Two calls in flight may then run at once: each
+ * needs its own output buffers.  bv_index_sync waits for both streams;
+ * appends wait for queries still running.  n = 1 (default): one stream. */
+int bv_index_set_query_streams(bv_index *idx, uint32_t n);
 /* bv_index_search_device for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  It has no counterpart in the reference.  Every query runs the

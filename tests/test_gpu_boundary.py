@@ -77,3 +77,54 @@ def test_failed_append_leaves_the_index_unchanged():
     a.destroy()
     b.destroy()
     ctx.destroy()
+
+
+@pytest.mark.parametrize("kind", ["quant8", "flat"])
+def test_two_query_streams_equal_one(kind):
+    """bv_index_set_query_streams(2): consecutive search_device calls
+    alternate between two streams and overlap; every call's rows and score
+    bits equal the one-stream answers, an append between calls waits for
+    the queries in flight and the next queries see the new rows."""
+    need_gpu()
+    import torch
+    from browservec_amd import DeviceContext, FlatIndex, QuantIndex
+
+    dim, n, nq = 256, 60000, 24
+    say("two query streams", kind)
+    ctx = DeviceContext(0)
+    data = gaussian(n, dim, 91)
+    idx = QuantIndex(ctx, dim, bits=8) if kind == "quant8" else FlatIndex(ctx, dim, "cosine")
+    idx.append(data[:n], n)
+    q = torch.from_numpy(gaussian(nq, dim, 92)).cuda()
+    fetch = 40 if kind == "quant8" else 0
+
+    def run(streams):
+        idx.set_query_streams(streams)
+        rows = torch.zeros(nq, 10, dtype=torch.int32, device="cuda")
+        sc = torch.zeros(nq, 10, dtype=torch.float32, device="cuda")
+        cnt = torch.zeros(nq, dtype=torch.int32, device="cuda")
+        for i in range(nq):  # one query per call, each with its own outputs
+            idx.search_device(q[i].data_ptr(), 1, fetch, 10, rows[i].data_ptr(), sc[i].data_ptr(), cnt[i].data_ptr())
+        idx.sync()
+        return rows.cpu().numpy(), sc.cpu().numpy(), cnt.cpu().numpy()
+
+    r1, s1, c1 = run(1)
+    r2, s2, c2 = run(2)
+    assert np.array_equal(r1, r2) and np.array_equal(s1.view(np.uint32), s2.view(np.uint32)) and np.array_equal(c1, c2)
+    # an append while queries are in flight on both streams
+    rows = torch.zeros(4, 10, dtype=torch.int32, device="cuda")
+    sc = torch.zeros(4, 10, dtype=torch.float32, device="cuda")
+    cnt = torch.zeros(4, dtype=torch.int32, device="cuda")
+    for i in range(2):
+        idx.search_device(q[i].data_ptr(), 1, fetch, 10, rows[i].data_ptr(), sc[i].data_ptr(), cnt[i].data_ptr())
+    near = np.repeat(q[2:3].cpu().numpy(), 3000, axis=0)  # copies of query 2
+    idx.append(near, 3000)
+    for i in range(2, 4):
+        idx.search_device(q[i].data_ptr(), 1, fetch, 10, rows[i].data_ptr(), sc[i].data_ptr(), cnt[i].data_ptr())
+    idx.sync()
+    got = rows.cpu().numpy()
+    assert np.array_equal(got[:2], r1[:2])
+    assert (got[2] >= n).all()  # the appended copies of query 2 win its top 10
+    idx.set_query_streams(1)
+    idx.destroy()
+    ctx.destroy()
