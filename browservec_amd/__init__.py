@@ -7,7 +7,7 @@ This package is the host side: ctypes binding, ``VectorIndex`` classes and the
 """
 
 from .browservec import BrowserVec, Store, normalize_in_place  # noqa: F401
-from .index import DeviceContext, FlatHit, FlatIndex, IVFIndex, IVFQuantIndex, QuantIndex  # noqa: F401
+from .index import DeviceContext, FlatHit, FlatIndex, GraphSearcher, IVFIndex, IVFQuantIndex, QuantIndex  # noqa: F401
 
-__all__ = ["BrowserVec", "Store", "normalize_in_place", "DeviceContext", "FlatHit", "FlatIndex", "QuantIndex",
+__all__ = ["BrowserVec", "Store", "normalize_in_place", "DeviceContext", "FlatHit", "FlatIndex", "GraphSearcher", "QuantIndex",
            "IVFIndex", "IVFQuantIndex"]

@@ -102,6 +102,12 @@ SIGNATURES = {
     "bv_index_rerank": [vp, vp, vp, u32, u32, vp, vp, vp],
     "bv_index_query_rows": [vp, vp, vp, u64, u32, vp, vp, vp],
     "bv_index_set_query_streams": [vp, u32],
+    "bv_graph_create": [vp, u32, u32, u32, vp],
+    "bv_graph_destroy": [vp],
+    "bv_graph_append": [vp, vp, u64, u64],
+    "bv_graph_upload": [vp, vp, u64],
+    "bv_graph_search": [vp, vp, u32, u32, u32, u32, vp, vp, vp],
+    "bv_graph_search_beams": [vp, vp, u32, vp, u32, u32, u32, vp, vp],
     "bv_index_query_rows_masked": [vp, vp, vp, u64, u32, vp, vp, vp],
     "bv_index_search": [vp, vp, u32, u32, u32, vp, vp, vp],
     "bv_index_search_device": [vp, vp, u32, u32, u32, vp, vp, vp],

@@ -2840,3 +2840,198 @@ extern "C" int bv_index_export_ivf(bv_index *idx, float *centroids, uint32_t *li
              "download");
     return BV_OK;
 }
+
+
+// ------------------------------------------------------------ graph search
+// HNSWGpuSearcher (src/index/hnswGpu.ts:28-244): the corpus rows and the
+// layer-0 adjacency the host's HNSW build hands over, and the beam search of
+// a batch of queries in one launch (one wave per query).
+struct bv_graph {
+    mutable std::mutex mu;
+    bv_device *dev = nullptr;
+    hipStream_t stream = nullptr;
+    uint32_t dim = 0, metric = 0, degree = 0;
+    uint64_t corpus_rows = 0, graph_rows = 0;
+    DevBuf corpus, graph, queries, entries, out_rows, out_scores, out_n, beam_d, beam_i;
+};
+
+namespace {
+int graph_live(bv_graph *g) {
+    if (!g) return fail(BV_E_INVALID, "null graph searcher");
+    if (g->dev->lost) return fail(BV_E_DEVICE_LOST, "GPU device lost; re-create the store");
+    hipError_t e = hipSetDevice(g->dev->ordinal);
+    if (e != hipSuccess) return hip_fail(g->dev, e, "hipSetDevice");
+    return BV_OK;
+}
+
+// The searcher's seeds (hnswGpu.ts:142-150): the HNSW entry, then up to
+// seven rows spread evenly over the adjacency's rows.
+uint32_t graph_seeds(uint32_t entry, uint64_t rows, uint32_t *out) {
+    uint32_t e = 0;
+    out[e++] = entry;
+    const uint64_t extra = std::min<uint64_t>(7, rows);
+    for (uint64_t i = 0; i < extra; i++)
+        out[e++] = (uint32_t)((uint64_t)std::floor((double)(i + 1) * (double)rows / (double)(extra + 1)) % rows);
+    return e;
+}
+
+int graph_run(bv_graph *g, const float *queries, uint32_t nq, const uint32_t *entries, uint32_t n_entries,
+              uint32_t ef_active, uint32_t iter_cap, uint32_t k, uint32_t stride, bool beams) {
+    hipStream_t s = g->stream;
+    const size_t qb = (size_t)nq * g->dim * 4;
+    HIPX(g->dev, g->queries.ensure(qb, 0, s), "query buffer");
+    HIPX(g->dev, hipMemcpyAsync(g->queries.p, queries, qb, hipMemcpyHostToDevice, s), "upload");
+    HIPX(g->dev, g->entries.ensure(std::max<size_t>(n_entries, 1) * 4, 0, s), "scratch");
+    if (n_entries)
+        HIPX(g->dev, hipMemcpyAsync(g->entries.p, entries, (size_t)n_entries * 4, hipMemcpyHostToDevice, s), "upload");
+    GraphArgs a{};
+    a.corpus = g->corpus.as<float>();
+    a.dim = g->dim;
+    a.corpus_rows = g->corpus_rows;
+    a.graph = g->graph.as<uint32_t>();
+    a.K = g->degree;
+    a.graph_rows = g->graph_rows;
+    a.queries = g->queries.as<float>();
+    a.entries = g->entries.as<uint32_t>();
+    a.n_entries = n_entries;
+    a.efA = ef_active;
+    a.iter_cap = iter_cap;
+    if (beams) {
+        HIPX(g->dev, g->beam_d.ensure((size_t)nq * GRAPH_EF_CAP * 4, 0, s), "scratch");
+        HIPX(g->dev, g->beam_i.ensure((size_t)nq * GRAPH_EF_CAP * 4, 0, s), "scratch");
+        a.beam_dist = g->beam_d.as<float>();
+        a.beam_id = g->beam_i.as<uint32_t>();
+    } else {
+        HIPX(g->dev, g->out_rows.ensure((size_t)nq * std::max(stride, 1u) * 4, 0, s), "scratch");
+        HIPX(g->dev, g->out_scores.ensure((size_t)nq * std::max(stride, 1u) * 4, 0, s), "scratch");
+        HIPX(g->dev, g->out_n.ensure((size_t)nq * 4, 0, s), "scratch");
+        a.k = k;
+        a.out_stride = stride;
+        a.out_rows = g->out_rows.as<uint32_t>();
+        a.out_scores = g->out_scores.as<float>();
+        a.out_n = g->out_n.as<uint32_t>();
+    }
+    HIPX(g->dev, launch_graph_beam(a, nq, g->metric == BV_METRIC_L2, s), "graph search kernel");
+    return BV_OK;
+}
+}  // namespace
+
+extern "C" int bv_graph_create(bv_device *dev, uint32_t dim, uint32_t metric, uint32_t degree, bv_graph **out) {
+    if (!dev || !out) return fail(BV_E_INVALID, "null argument");
+    if (dev->lost) return fail(BV_E_DEVICE_LOST, "GPU device lost; re-create the store");
+    if (dim == 0) return fail(BV_E_INVALID, "dimension must be a positive integer, got %u", dim);
+    if ((size_t)dim * 4 > 64 * 1024) return fail(BV_E_UNSUPPORTED, "graph search supports dimension <= 16384");
+    if (metric > BV_METRIC_L2) return fail(BV_E_INVALID, "unknown metric %u", metric);
+    if (degree == 0 || degree > 64)
+        return fail(BV_E_UNSUPPORTED, "GPU graph search supports degree \xe2\x89\xa4 64 (M \xe2\x89\xa4 32), got %u", degree);
+    hipError_t e = hipSetDevice(dev->ordinal);
+    if (e != hipSuccess) return hip_fail(dev, e, "hipSetDevice");
+    bv_graph *g = new bv_graph();
+    g->dev = dev;
+    g->dim = dim;
+    g->metric = metric;
+    g->degree = degree;
+    e = hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete g;
+        return hip_fail(dev, e, "hipStreamCreate");
+    }
+    *out = g;
+    return BV_OK;
+}
+
+extern "C" int bv_graph_destroy(bv_graph *g) {
+    if (!g) return BV_OK;
+    (void)hipSetDevice(g->dev->ordinal);
+    if (g->stream) {
+        (void)hipStreamSynchronize(g->stream);
+        (void)hipStreamDestroy(g->stream);
+    }
+    delete g;
+    return BV_OK;
+}
+
+extern "C" int bv_graph_append(bv_graph *g, const float *data, uint64_t n_floats, uint64_t count) {
+    if (!g) return fail(BV_E_INVALID, "null graph searcher");
+    std::lock_guard<std::mutex> lock(g->mu);
+    int rc = graph_live(g);
+    if (rc) return rc;
+    if (n_floats != count * g->dim)
+        return fail(BV_E_INVALID, "expected %llu floats, got %llu", (unsigned long long)(count * g->dim),
+                    (unsigned long long)n_floats);
+    if (count == 0) return BV_OK;
+    if (!data) return fail(BV_E_INVALID, "data is null");
+    if (g->corpus_rows + count > 0xfffffffeull) return fail(BV_E_INVALID, "row count exceeds 2^32-2");
+    const size_t rb = (size_t)g->dim * 4;
+    HIPX(g->dev, g->corpus.ensure((g->corpus_rows + count) * rb, g->corpus_rows * rb, g->stream), "corpus buffer");
+    HIPX(g->dev, hipMemcpyAsync(g->corpus.as<char>() + g->corpus_rows * rb, data, count * rb, hipMemcpyHostToDevice,
+                                g->stream),
+         "row upload");
+    HIPX(g->dev, hipStreamSynchronize(g->stream), "append");
+    g->corpus_rows += count;
+    return BV_OK;
+}
+
+extern "C" int bv_graph_upload(bv_graph *g, const uint32_t *links, uint64_t rows) {
+    if (!g) return fail(BV_E_INVALID, "null graph searcher");
+    std::lock_guard<std::mutex> lock(g->mu);
+    int rc = graph_live(g);
+    if (rc) return rc;
+    if (rows && !links) return fail(BV_E_INVALID, "links is null");
+    if (rows > 0xfffffffeull) return fail(BV_E_INVALID, "row count exceeds 2^32-2");
+    const size_t b = rows * g->degree * 4;
+    HIPX(g->dev, g->graph.ensure(std::max<size_t>(b, 4), 0, g->stream), "graph buffer");
+    if (b) HIPX(g->dev, hipMemcpyAsync(g->graph.p, links, b, hipMemcpyHostToDevice, g->stream), "upload");
+    HIPX(g->dev, hipStreamSynchronize(g->stream), "graph upload");
+    g->graph_rows = rows;
+    return BV_OK;
+}
+
+extern "C" int bv_graph_search(bv_graph *g, const float *queries, uint32_t nq, uint32_t k, uint32_t ef,
+                               uint32_t entry, uint32_t *rows, float *scores, uint32_t *n_out) {
+    if (!g) return fail(BV_E_INVALID, "null graph searcher");
+    std::lock_guard<std::mutex> lock(g->mu);
+    int rc = graph_live(g);
+    if (rc) return rc;
+    if (nq == 0) return BV_OK;
+    if (!queries || !n_out || (k && (!rows || !scores))) return fail(BV_E_INVALID, "null argument");
+    if (g->corpus_rows == 0 || g->graph_rows == 0)
+        return fail(BV_E_STATE, "graph search needs corpus rows and an uploaded adjacency");
+    const uint32_t efA = std::min(std::max(ef, k), GRAPH_EF_CAP);
+    const uint32_t kk = std::min(k, efA);
+    if (kk == 0) {
+        for (uint32_t i = 0; i < nq; i++) n_out[i] = 0;
+        return BV_OK;
+    }
+    uint32_t seeds[8];
+    const uint32_t ns = graph_seeds(entry, g->graph_rows, seeds);
+    rc = graph_run(g, queries, nq, seeds, ns, efA, efA, kk, k, false);
+    if (rc) return rc;
+    HIPX(g->dev, hipMemcpyAsync(rows, g->out_rows.p, (size_t)nq * k * 4, hipMemcpyDeviceToHost, g->stream), "download");
+    HIPX(g->dev, hipMemcpyAsync(scores, g->out_scores.p, (size_t)nq * k * 4, hipMemcpyDeviceToHost, g->stream),
+         "download");
+    HIPX(g->dev, hipMemcpyAsync(n_out, g->out_n.p, (size_t)nq * 4, hipMemcpyDeviceToHost, g->stream), "download");
+    HIPX(g->dev, hipStreamSynchronize(g->stream), "graph search");
+    return BV_OK;
+}
+
+extern "C" int bv_graph_search_beams(bv_graph *g, const float *queries, uint32_t nq, const uint32_t *entries,
+                                     uint32_t n_entries, uint32_t ef, uint32_t iter_cap, float *beam_dist,
+                                     uint32_t *beam_id) {
+    if (!g) return fail(BV_E_INVALID, "null graph searcher");
+    std::lock_guard<std::mutex> lock(g->mu);
+    int rc = graph_live(g);
+    if (rc) return rc;
+    if (nq == 0) return BV_OK;
+    if (!queries || !beam_dist || !beam_id || (n_entries && !entries)) return fail(BV_E_INVALID, "null argument");
+    if (g->corpus_rows == 0 || g->graph_rows == 0)
+        return fail(BV_E_STATE, "graph search needs corpus rows and an uploaded adjacency");
+    if (ef == 0 || ef > GRAPH_EF_CAP) return fail(BV_E_INVALID, "ef must be 1..%u, got %u", GRAPH_EF_CAP, ef);
+    rc = graph_run(g, queries, nq, entries, std::min(n_entries, 64u), ef, iter_cap, 0, 0, true);
+    if (rc) return rc;
+    const size_t b = (size_t)nq * GRAPH_EF_CAP * 4;
+    HIPX(g->dev, hipMemcpyAsync(beam_dist, g->beam_d.p, b, hipMemcpyDeviceToHost, g->stream), "download");
+    HIPX(g->dev, hipMemcpyAsync(beam_id, g->beam_i.p, b, hipMemcpyDeviceToHost, g->stream), "download");
+    HIPX(g->dev, hipStreamSynchronize(g->stream), "graph search");
+    return BV_OK;
+}

@@ -363,6 +363,30 @@ size_t scan_query_lds(int codec, uint32_t P);
 // True when the scan for this codec / row layout transforms fp32 queries itself (ScanArgs::qraw).
 bool scan_prep_supported(int codec, uint32_t units, uint32_t P);
 
+// ---- graph beam search (bv_graph.hip) ---------------------------------------
+constexpr uint32_t GRAPH_EF_CAP = 256;  // beam slots (src/engine/wgsl/graphSearch.ts:32)
+struct GraphArgs {
+    const float *corpus;      // corpus_rows x dim, prepared rows
+    uint32_t dim;
+    uint64_t corpus_rows;
+    const uint32_t *graph;    // graph_rows x K, 0xffffffff = empty slot
+    uint32_t K;
+    uint64_t graph_rows;
+    const float *queries;     // nq x dim
+    const uint32_t *entries;  // seed rows
+    uint32_t n_entries;
+    uint32_t efA;             // beam width <= GRAPH_EF_CAP
+    uint32_t iter_cap;        // expansions at most
+    uint32_t k;               // hits per query <= GRAPH_EF_CAP
+    uint32_t out_stride;      // out_rows / out_scores entries per query (>= k)
+    float *beam_dist;         // optional: [nq][GRAPH_EF_CAP] raw beam
+    uint32_t *beam_id;
+    uint32_t *out_rows;       // optional: [nq][k] deduped, sorted hits
+    float *out_scores;
+    uint32_t *out_n;          // [nq]
+};
+hipError_t launch_graph_beam(const GraphArgs &a, uint32_t nq, bool l2, hipStream_t s);
+
 // ---- selection for any k; exact scan of listed rows (bv_select.hip) ---------
 // Keys (make_key) of scores[0, n); rows whose mask bit is clear get key 0.
 hipError_t sel_dense_keys(const float *scores, uint64_t n, const uint32_t *mask, uint64_t *keys, hipStream_t s);

@@ -395,3 +395,62 @@ class IVFQuantIndex(IVFIndex):
     @property
     def ingest_mode(self) -> str:
         return "device" if self.size else "pending"
+
+
+class GraphSearcher:
+    """HNSWGpuSearcher (src/index/hnswGpu.ts:28-244): corpus rows and the
+    layer-0 adjacency on the device, beam search of query batches
+    (src/engine/wgsl/graphSearch.ts), one wave per query."""
+
+    EF_CAP = 256
+    EMPTY = 0xFFFFFFFF
+
+    def __init__(self, ctx, dim, metric="cosine", degree=32):
+        self.lib = ctx.lib
+        self.dim = int(dim)
+        self.degree = int(degree)
+        h = ctypes.c_void_p()
+        L.check(self.lib.bv_graph_create(ctx.handle, self.dim, L.METRICS[metric], self.degree, ctypes.byref(h)))
+        self.handle = h
+
+    def append(self, data, count: int) -> None:
+        data = _f32(data).reshape(-1)
+        L.check(self.lib.bv_graph_append(self.handle, _ptr(data), data.size, int(count)))
+
+    def upload_graph(self, links, rows: int) -> None:
+        links = np.ascontiguousarray(links, dtype=np.uint32).reshape(-1)
+        if links.size < int(rows) * self.degree:
+            raise ValueError(f"expected {int(rows) * self.degree} links, got {links.size}")
+        L.check(self.lib.bv_graph_upload(self.handle, _ptr(links) if links.size else None, int(rows)))
+
+    def search(self, queries, n: int, k: int, ef: int, entry: int) -> list[list[FlatHit]]:
+        qs = _f32(queries).reshape(-1)
+        _check_len(qs, int(n) * self.dim)
+        rows = np.empty((max(n, 1), max(k, 1)), np.uint32)
+        scores = np.empty((max(n, 1), max(k, 1)), np.float32)
+        cnt = np.zeros(max(n, 1), np.uint32)
+        L.check(self.lib.bv_graph_search(self.handle, _ptr(qs), int(n), int(k), int(ef), int(entry) & 0xFFFFFFFF,
+                                         _ptr(rows), _ptr(scores), _ptr(cnt)))
+        return [[FlatHit(int(rows[i, j]), float(scores[i, j])) for j in range(cnt[i])] for i in range(n)]
+
+    def search_beams(self, queries, entries, ef: int, iter_cap: int):
+        """Raw beams for parity: (dist [nq, 256], id [nq, 256])."""
+        qs = _f32(queries).reshape(-1, self.dim)
+        e = np.ascontiguousarray(entries, dtype=np.uint32).reshape(-1)
+        nq = qs.shape[0]
+        dist = np.empty((nq, self.EF_CAP), np.float32)
+        ids = np.empty((nq, self.EF_CAP), np.uint32)
+        L.check(self.lib.bv_graph_search_beams(self.handle, _ptr(qs), nq, _ptr(e), e.size, int(ef), int(iter_cap),
+                                               _ptr(dist), _ptr(ids)))
+        return dist, ids
+
+    def destroy(self) -> None:
+        if getattr(self, "handle", None):
+            self.lib.bv_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass

@@ -64,6 +64,7 @@ extern "C" {
 
 typedef struct bv_device bv_device;
 typedef struct bv_index bv_index;
+typedef struct bv_graph bv_graph;
 
 /* Index description: buildIndex's arguments (dim, metric, quantBits, quant,
  * ann, chunkRows; src/index.ts:105-113) with the QuantConfig and IVFParams
@@ -292,6 +293,34 @@ int bv_index_load_section(bv_index *idx, const float *data, uint64_t n_floats, u
  * queries: scores[nq][nlist].  Batches of 8 or more run the batched probe
  * kernel, fewer the single-query one; both give the same bits. */
 int bv_index_export_probe_scores(bv_index *idx, const float *queries, uint32_t nq, float *scores);
+
+/* ---- graph search (HNSW layer 0) ------------------------------------------ */
+/* HNSWGpuSearcher (src/index/hnswGpu.ts:28-244): the host's HNSW build keeps
+ * the graph; this object holds the corpus rows and the flat layer-0
+ * adjacency on the device and beam-searches query batches
+ * (src/engine/wgsl/graphSearch.ts:62-259), one wave per query.  degree is
+ * the adjacency's fixed out-degree (2M), at most 64; metric BV_METRIC_* (the
+ * rows and queries arrive prepared, as for an index). */
+int bv_graph_create(bv_device *dev, uint32_t dim, uint32_t metric, uint32_t degree, bv_graph **out);
+int bv_graph_destroy(bv_graph *g);
+/* HNSWGpuSearcher.append (hnswGpu.ts:83-109): mirror appended rows. */
+int bv_graph_append(bv_graph *g, const float *data, uint64_t n_floats, uint64_t count);
+/* HNSWGpuSearcher.uploadGraph (hnswGpu.ts:112-126): the layer-0 adjacency,
+ * rows x degree row ids, 0xffffffff for an empty slot.  Rows past the
+ * adjacency have no neighbours; ids at or past the corpus rows are skipped. */
+int bv_graph_upload(bv_graph *g, const uint32_t *links, uint64_t rows);
+/* HNSWGpuSearcher.search (hnswGpu.ts:134-206): beam width
+ * min(max(ef, k), 256), as many expansions, seeds = entry plus up to seven
+ * rows spread over the adjacency; per query the beam's ids deduped, sorted
+ * by score (-distance: dot for dot / cosine, -squared distance for l2) with
+ * ties in beam order, the first k: rows / scores [nq][k], n_out[nq]. */
+int bv_graph_search(bv_graph *g, const float *queries, uint32_t nq, uint32_t k, uint32_t ef, uint32_t entry,
+                    uint32_t *rows, float *scores, uint32_t *n_out);
+/* Parity export: the raw beams ([nq][256] distances and ids, unsorted, empty
+ * slots 3.4e38 / 0xffffffff) for explicit seeds, beam width and expansion
+ * cap. */
+int bv_graph_search_beams(bv_graph *g, const float *queries, uint32_t nq, const uint32_t *entries,
+                          uint32_t n_entries, uint32_t ef, uint32_t iter_cap, float *beam_dist, uint32_t *beam_id);
 
 #ifdef __cplusplus
 }

@@ -935,3 +935,203 @@ EXPORT uint32_t bvo_pick_tune_queries(uint32_t filled, uint32_t want, uint32_t *
     for (uint32_t i = 0; i < n; i++) out[i] = (uint32_t)floor(((double)i * (double)filled) / (double)n);
     return n;
 }
+
+/* ------------------------------------------------------------------------ */
+/* f4. Graph beam search over a flat fixed-degree adjacency                  */
+/* (src/engine/wgsl/graphSearch.ts:62-259) and the searcher's seeds, dedup   */
+/* and top-k (src/index/hnswGpu.ts:134-206).  Where the shader lets lanes    */
+/* race (the visited-set inserts of one staged batch) they are taken in lane */
+/* order; its reductions are restated in its own order: each lane keeps the  */
+/* first strict best of slots t, t+WG, ..., then a halving tree with strict  */
+/* compares.  Distances are f32, element order, multiply and add each        */
+/* rounded (the shader's `acc = acc + c * q`; WGSL leaves fusing to the      */
+/* compiler -- parity unpinned against a fusing backend).                    */
+/* ------------------------------------------------------------------------ */
+#define G_EF 256u
+#define G_WG 64u
+#define G_HASH 2048u
+#define G_PROBES 16u
+#define G_INF 3.4e38f
+#define G_EMPTY 0xffffffffu
+
+static float g_dist(const float *row, const float *q, uint32_t dim, int l2) {
+    float acc = 0.0f;
+    for (uint32_t i = 0; i < dim; i++) {
+        if (l2) {
+            const float d = row[i] - q[i];
+            acc = acc + d * d;
+        } else {
+            acc = acc + row[i] * q[i];
+        }
+    }
+    return l2 ? acc : -acc;
+}
+
+/* markVisited (graphSearch.ts:112-128): 1 when id was already seen. */
+static int g_mark(uint32_t *vis, uint32_t id) {
+    uint32_t h = (id * 2654435761u) & (G_HASH - 1u);
+    for (uint32_t p = 0; p < G_PROBES; p++) {
+        const uint32_t cur = vis[h];
+        if (cur == id + 1u) return 1;
+        if (cur == 0u) {
+            vis[h] = id + 1u;
+            return 0;
+        }
+        h = (h + 1u) & (G_HASH - 1u);
+    }
+    return 0; /* shed: reported unseen, not recorded */
+}
+
+/* The shader's argmin (unexpanded slots) / argmax (all active slots). */
+static uint32_t g_arg(const float *val, const uint32_t *expd, uint32_t efA, int want_max, float *best_out) {
+    float rv[G_WG];
+    uint32_t ri[G_WG];
+    for (uint32_t t = 0; t < G_WG; t++) {
+        float best = want_max ? -G_INF : G_INF;
+        uint32_t bi = 0;
+        for (uint32_t s = t; s < efA; s += G_WG) {
+            if (want_max) {
+                if (val[s] > best) {
+                    best = val[s];
+                    bi = s;
+                }
+            } else if (expd[s] == 0u && val[s] < best) {
+                best = val[s];
+                bi = s;
+            }
+        }
+        rv[t] = best;
+        ri[t] = bi;
+    }
+    for (uint32_t stride = G_WG >> 1; stride; stride >>= 1)
+        for (uint32_t t = 0; t < stride; t++)
+            if (want_max ? rv[t + stride] > rv[t] : rv[t + stride] < rv[t]) {
+                rv[t] = rv[t + stride];
+                ri[t] = ri[t + stride];
+            }
+    *best_out = rv[0];
+    return ri[0];
+}
+
+/* foldStaged (graphSearch.ts:133-165). */
+static void g_fold(float *cd, uint32_t *ci, uint32_t *ce, uint32_t efA, const float *sd, const uint32_t *si,
+                   uint32_t count) {
+    for (uint32_t j = 0; j < count; j++) {
+        float worst;
+        const uint32_t slot = g_arg(cd, ce, efA, 1, &worst);
+        if (sd[j] < worst) {
+            cd[slot] = sd[j];
+            ci[slot] = si[j];
+            ce[slot] = 0u;
+        }
+    }
+}
+
+/* The beam of each query after the search: G_EF (dist, id) slots per query.
+ * The adjacency covers graph_rows rows of a corpus of corpus_rows rows; a
+ * node past graph_rows has no neighbours and an id at or past corpus_rows
+ * is skipped like an empty slot (the shader relies on WebGPU's robust
+ * buffer access for those). */
+EXPORT void bvo_graph_search(const float *corpus, uint32_t dim, int l2, const uint32_t *graph, uint32_t K,
+                             uint32_t graph_rows, uint32_t corpus_rows, const float *queries, uint32_t nq,
+                             const uint32_t *entries, uint32_t n_entries, uint32_t ef, uint32_t iter_cap,
+                             float *out_dist, uint32_t *out_id) {
+    const uint32_t efA = ef < G_EF ? ef : G_EF;
+    const uint32_t ne = n_entries < G_WG ? n_entries : G_WG;
+    uint32_t *vis = (uint32_t *)malloc(G_HASH * sizeof(uint32_t));
+    float cd[G_EF], sd[G_WG];
+    uint32_t ci[G_EF], ce[G_EF], si[G_WG];
+    for (uint32_t q = 0; q < nq; q++) {
+        const float *qv = queries + (size_t)q * dim;
+        memset(vis, 0, G_HASH * sizeof(uint32_t));
+        for (uint32_t s = 0; s < G_EF; s++) {
+            cd[s] = G_INF;
+            ci[s] = G_EMPTY;
+            ce[s] = 1u;
+        }
+        for (uint32_t t = 0; t < ne; t++) {
+            const uint32_t e = entries[t];
+            sd[t] = G_INF;
+            si[t] = G_EMPTY;
+            if (e < corpus_rows && !g_mark(vis, e)) {
+                sd[t] = g_dist(corpus + (size_t)e * dim, qv, dim, l2);
+                si[t] = e;
+            }
+        }
+        g_fold(cd, ci, ce, efA, sd, si, ne);
+        for (uint32_t iter = 0; iter < iter_cap; iter++) {
+            float best;
+            const uint32_t slot = g_arg(cd, ce, efA, 0, &best);
+            if (best >= G_INF) break;
+            ce[slot] = 1u;
+            const uint32_t node = ci[slot];
+            for (uint32_t t = 0; t < K; t++) {
+                sd[t] = G_INF;
+                si[t] = G_EMPTY;
+                const uint32_t nb = node < graph_rows ? graph[(size_t)node * K + t] : G_EMPTY;
+                if (nb < corpus_rows && !g_mark(vis, nb)) {
+                    sd[t] = g_dist(corpus + (size_t)nb * dim, qv, dim, l2);
+                    si[t] = nb;
+                }
+            }
+            g_fold(cd, ci, ce, efA, sd, si, K);
+        }
+        memcpy(out_dist + (size_t)q * G_EF, cd, sizeof(cd));
+        memcpy(out_id + (size_t)q * G_EF, ci, sizeof(ci));
+    }
+    free(vis);
+}
+
+/* HNSWGpuSearcher.search's seeds (hnswGpu.ts:142-150): the entry, then up to
+ * seven rows spread evenly over the graph's rows.  Returns the count. */
+EXPORT uint32_t bvo_graph_entries(uint32_t entry, uint32_t graph_rows, uint32_t *out) {
+    uint32_t e = 0;
+    out[e++] = entry;
+    const uint32_t extra = graph_rows < 7u ? graph_rows : 7u;
+    for (uint32_t i = 0; i < extra; i++)
+        out[e++] = (uint32_t)(floor(((double)(i + 1) * (double)graph_rows) / (double)(extra + 1)) ) % graph_rows;
+    return e;
+}
+
+/* The readback's dedup and top-k (hnswGpu.ts:191-203): live slots in slot
+ * order, first occurrence of an id kept, score = -dist, stable sort by score
+ * descending, first k.  Returns the count. */
+EXPORT uint32_t bvo_graph_hits(const float *dist, const uint32_t *id, uint32_t efA, uint32_t k, uint32_t *rows,
+                               float *scores) {
+    uint32_t n = 0;
+    uint32_t hr[G_EF];
+    float hs[G_EF];
+    for (uint32_t s = 0; s < efA && s < G_EF; s++) {
+        const uint32_t r = id[s];
+        if (r == G_EMPTY) continue;
+        int dup = 0;
+        for (uint32_t j = 0; j < n; j++)
+            if (hr[j] == r) {
+                dup = 1;
+                break;
+            }
+        if (dup) continue;
+        hr[n] = r;
+        hs[n] = -dist[s];
+        n++;
+    }
+    /* stable insertion sort, descending */
+    for (uint32_t i = 1; i < n; i++) {
+        const uint32_t r = hr[i];
+        const float v = hs[i];
+        uint32_t j = i;
+        while (j > 0 && hs[j - 1] < v) {
+            hs[j] = hs[j - 1];
+            hr[j] = hr[j - 1];
+            j--;
+        }
+        hs[j] = v;
+        hr[j] = r;
+    }
+    const uint32_t m = n < k ? n : k;
+    for (uint32_t i = 0; i < m; i++) {
+        rows[i] = hr[i];
+        scores[i] = hs[i];
+    }
+    return m;
+}

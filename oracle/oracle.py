@@ -50,6 +50,14 @@ assign_f32 (order 1)         brute-force argmax; the AVX2 path equals the
                              scalar fmaf chain (order 2), ties included
 choose_nprobe / pick_tune    ivfTune.test.ts tables
 probe_scores                 long double brute force within 1 ulp f32
+graph_search / graph_hits    a connected graph searched with ef >= its rows
+                             returns the brute-force top-k of the same f32
+                             element-order distances (every row visited);
+                             dedup keeps the first slot of an id; seeds
+                             (graph_entries) against hand-computed rows;
+                             the shader's lane races and reduction tie order
+                             are restated in one fixed order: parity unpinned
+                             beyond tie-free cases
 ===========================  =================================================
 """
 
@@ -137,6 +145,11 @@ def _load() -> ctypes.CDLL:
         "bvo_build_csr": (None, [u32p, ctypes.c_uint64, ctypes.c_uint32, i32p, i32p]),
         "bvo_choose_nprobe": (ctypes.c_uint32, [u32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double, f64p]),
         "bvo_pick_tune_queries": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32, u32p]),
+        "bvo_graph_search": (None, [f32p, ctypes.c_uint32, ctypes.c_int, u32p, ctypes.c_uint32, ctypes.c_uint32,
+                                    ctypes.c_uint32, f32p, ctypes.c_uint32, u32p, ctypes.c_uint32, ctypes.c_uint32,
+                                    ctypes.c_uint32, f32p, u32p]),
+        "bvo_graph_entries": (ctypes.c_uint32, [ctypes.c_uint32, ctypes.c_uint32, u32p]),
+        "bvo_graph_hits": (ctypes.c_uint32, [f32p, u32p, ctypes.c_uint32, ctypes.c_uint32, u32p, f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -488,3 +501,41 @@ class Reservoir:
     def slot(self) -> int:
         return int(_lib.bvo_reservoir_slot(self.cap, ctypes.byref(self.filled), ctypes.byref(self.seen),
                                            ctypes.byref(self.rng)))
+
+
+# ------------------------------------------------------------- graph search
+GRAPH_EF = 256
+GRAPH_EMPTY = 0xFFFFFFFF
+
+
+def graph_entries(entry: int, graph_rows: int) -> np.ndarray:
+    """HNSWGpuSearcher.search's seed rows (src/index/hnswGpu.ts:142-150)."""
+    out = np.empty(8, np.uint32)
+    n = _lib.bvo_graph_entries(int(entry) & 0xFFFFFFFF, int(graph_rows), _p(out, u32p))
+    return out[:n].copy()
+
+
+def graph_search(corpus, graph, queries, entries, ef: int, iter_cap: int, l2: bool = False):
+    """The beam-search shader (src/engine/wgsl/graphSearch.ts:62-259), lanes in
+    lane order: (dist [nq, 256], id [nq, 256]) beams.  graph: [graph_rows, K]
+    adjacency over the first graph_rows rows of corpus."""
+    corpus, queries = _f32(corpus), _f32(np.atleast_2d(queries))
+    graph, entries = _u32(graph), _u32(entries)
+    nq, dim = queries.shape
+    K = graph.shape[1]
+    dist = np.empty((nq, GRAPH_EF), np.float32)
+    ids = np.empty((nq, GRAPH_EF), np.uint32)
+    _lib.bvo_graph_search(_p(corpus, f32p), dim, 1 if l2 else 0, _p(graph, u32p), K, graph.shape[0],
+                          corpus.shape[0], _p(queries, f32p), nq, _p(entries, u32p), entries.size, int(ef),
+                          int(iter_cap), _p(dist, f32p), _p(ids, u32p))
+    return dist, ids
+
+
+def graph_hits(dist, ids, ef_active: int, k: int):
+    """The searcher's dedup + stable sort + top-k of one beam
+    (src/index/hnswGpu.ts:191-203): (rows, scores)."""
+    dist, ids = _f32(dist), _u32(ids)
+    rows = np.empty(max(k, 1), np.uint32)
+    scores = np.empty(max(k, 1), np.float32)
+    n = _lib.bvo_graph_hits(_p(dist, f32p), _p(ids, u32p), int(ef_active), int(k), _p(rows, u32p), _p(scores, f32p))
+    return rows[:n].copy(), scores[:n].copy()

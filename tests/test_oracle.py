@@ -496,3 +496,57 @@ def test_reservoir_is_a_uniform_sample():
     p = cap / n
     sd = np.sqrt(p * (1 - p) / trials)
     assert np.all(np.abs(held / trials - p) <= 5 * sd), held / trials
+
+
+def _knn_graph(x, K, metric):
+    """Fixed-degree kNN adjacency by brute force (f64 scores), self excluded."""
+    if metric == "l2":
+        s = -((x[:, None, :].astype(np.float64) - x[None, :, :]) ** 2).sum(-1)
+    else:
+        s = x.astype(np.float64) @ x.astype(np.float64).T
+    np.fill_diagonal(s, -np.inf)
+    g = np.argsort(-s, axis=1, kind="stable")[:, :K].astype(np.uint32)
+    g[:, -1] = (np.arange(x.shape[0]) + 1) % x.shape[0]  # a ring: every row reachable
+    return g
+
+
+@pytest.mark.parametrize("metric", ["dot", "l2"])
+def test_graph_search_visits_everything_when_ef_covers_the_graph(metric):
+    """With ef at least the row count (and an iteration cap that high) the
+    beam expands every reachable row, so the searcher's hits are the
+    brute-force top-k of the shader's own distance arithmetic: f32, element
+    order, each product and sum rounded (graphSearch.ts:101-109)."""
+    rng = np.random.default_rng(3)
+    n, dim, K = 200, 12, 8
+    x = rng.standard_normal((n, dim)).astype(np.float32)
+    g = _knn_graph(x, K, metric)
+    q = rng.standard_normal((4, dim)).astype(np.float32)
+    e = o.graph_entries(7, n)
+    dist, ids = o.graph_search(x, g, q, e, 256, 256, l2=(metric == "l2"))
+    for i in range(4):
+        if metric == "l2":
+            d = (x - q[i]).astype(np.float32)
+            brute = np.cumsum(d * d, axis=1, dtype=np.float32)[:, -1]
+            score = -brute
+        else:
+            score = np.cumsum(x * q[i], axis=1, dtype=np.float32)[:, -1]
+        live = ids[i][ids[i] != o.GRAPH_EMPTY]
+        assert live.size == np.unique(live).size  # the visited set keeps ids unique here
+        rows, sc = o.graph_hits(dist[i], ids[i], 256, 10)
+        want_r, want_s = o.topk_canonical(score, 10)
+        assert np.array_equal(sc.view(np.uint32), want_s.view(np.uint32))
+        assert set(rows.tolist()) == set(want_r.tolist())
+
+
+def test_graph_entries_and_hits_known_answers():
+    # seeds: the entry, then floor((i + 1) * rows / (extra + 1)) % rows
+    assert o.graph_entries(0, 500).tolist() == [0, 62, 125, 187, 250, 312, 375, 437]
+    assert o.graph_entries(3, 4).tolist() == [3, 0, 1, 2, 3]
+    assert o.graph_entries(0, 1).tolist() == [0, 0]
+    # dedup keeps an id's first slot; ties keep slot order; k cuts
+    dist = np.full(256, 3.4e38, np.float32)
+    ids = np.full(256, o.GRAPH_EMPTY, np.uint32)
+    dist[:5] = [-1.0, -3.0, -1.0, -2.0, -3.0]
+    ids[:5] = [10, 11, 12, 11, 13]
+    rows, sc = o.graph_hits(dist, ids, 256, 3)
+    assert rows.tolist() == [11, 13, 10] and sc.tolist() == [3.0, 3.0, 1.0]
