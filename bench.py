@@ -23,6 +23,8 @@ throughput, roofline, recall and CPU baseline:
   c4  4,000,000 x 1024 int4 and 1-bit (asym, Hamming), fetch 200 -> 10
   c5  4,000,000 x 768 IVF int8, 4096 lists, 20 iterations, nprobe 32,
       1024 queries, fetch 40 -> 10
+  graph  HNSW layer-0 beam search, 200,000 x 768, degree 32, ef 64, 1024
+      queries
 """
 
 from __future__ import annotations
@@ -369,6 +371,83 @@ def bench_c5(ctx, torch, budget_s):
             "nlist": st["nlist"], "nprobe": nprobe, "cpu_baseline": cpu}
 
 
+def bench_graph(ctx, torch, budget_s):
+    """HNSW layer-0 beam search (HNSWGpuSearcher, src/index/hnswGpu.ts; the
+    shader of src/engine/wgsl/graphSearch.ts): 200,000 x 768 cosine rows, a
+    degree-32 adjacency (each row's 16 nearest others by the exact flat scan
+    and 16 random rows), 1024 queries, ef 128, k 10."""
+    from browservec_amd import FlatIndex, GraphSearcher
+
+    n, dim, K, nq, ef, k = 200_000, 768, 32, 1024, 128, 10
+    near = 16  # nearest neighbours per row; the other slots are random long links
+    # tight clusters (per-coordinate sigma 0.02: noise norm 0.55 against unit
+    # centres), queries = rows + 0.01 noise: neighbourhoods a graph walk can
+    # follow, unlike the near-isotropic mixtures of the scan workloads
+    x, q = make_data(n, dim, 1024, 0.02, nq, 0.01, 0xB5EC0006)
+    t0 = time.perf_counter()
+    flat = FlatIndex(ctx, dim, "cosine")
+    flat.append_device(x.data_ptr(), n)
+    nb = torch.empty(n, K + 1, dtype=torch.int32, device="cuda")
+    sc = torch.empty(n, K + 1, dtype=torch.float32, device="cuda")
+    cn = torch.empty(n, dtype=torch.int32, device="cuda")
+    for s0 in range(0, n, 1024):
+        m = min(1024, n - s0)
+        flat.search_device(x[s0:s0 + m].data_ptr(), m, 0, K + 1, nb[s0:].data_ptr(), sc[s0:].data_ptr(),
+                           cn[s0:].data_ptr())
+    flat.sync()
+    nbh = nb.cpu().numpy().astype(np.int64)
+    self_col = nbh == np.arange(n)[:, None]
+    keep = ~self_col
+    keep[self_col.sum(axis=1) == 0, K] = False  # no self hit: drop the last
+    links = nbh[keep].reshape(n, K).astype(np.uint32)
+    # a navigable small world: the nearest rows plus random long-range links
+    # (a pure kNN graph of a clustered corpus splits into per-cluster islands)
+    rng = np.random.default_rng(6)
+    links[:, near:] = rng.integers(0, n, size=(n, K - near), dtype=np.uint32)
+    adj_s = time.perf_counter() - t0
+    xh = x.cpu().numpy()
+    gs = GraphSearcher(ctx, dim, "cosine", K)
+    gs.append(xh, n)
+    gs.upload_graph(links, n)
+    qh = q.cpu().numpy()
+    gs.search(qh, nq, k, ef, 0)  # warmup
+    reps = 5
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        hits = gs.search(qh, nq, k, ef, 0)
+    bq = reps * nq / (time.perf_counter() - t0)
+    lat = []
+    for i in range(32):
+        t0 = time.perf_counter()
+        gs.search(qh[i:i + 1], 1, k, ef, 0)
+        lat.append((time.perf_counter() - t0) * 1e3)
+    rows_g = np.array([[h.row for h in hs] + [-1] * (k - len(hs)) for hs in hits])
+    recall = recall_vs_flat(ctx, x, q, rows_g, k, torch)
+    flat.destroy()
+    gs.destroy()
+    cpu = None
+    if budget_s > 0:
+        from oracle import oracle as o
+
+        e = o.graph_entries(0, n)
+        t0 = time.perf_counter()
+        done = 0
+        while done < nq and (done < 4 or time.perf_counter() - t0 < budget_s):
+            o.graph_search(xh, links, qh[done:done + 4], e, ef, ef)
+            done += 4
+        el = time.perf_counter() - t0
+        cpu = {"value": round(done / el, 2), "unit": "queries/s", "cores": 1, "kind": "port",
+               "sample": f"{done} queries through the oracle's single-thread restatement of the beam search "
+                         f"(same graph, ef {ef}), {el:.1f} s"}
+    del x, q, xh
+    free(torch)
+    return {"workload": f"{n}x{dim} cosine rows (1024 clusters, sigma 0.02), degree-{K} layer-0 adjacency ({near} exact nearest + "
+                        f"{K - near} random links), "
+                        f"{nq} queries, ef {ef}, k {k}, one wave per query",
+            "batch1024_qps": round(bq, 1), "batch1_ms_p50": round(float(np.median(lat)), 3),
+            "recall_at_10": round(recall, 4), "adjacency_build_s": round(adj_s, 2), "cpu_baseline": cpu}
+
+
 def stream_ceiling(torch, nbytes=1 << 30, reps=20):
     """Read-only streaming kernel (libbv_bench.so) over nbytes: plain and
     nontemporal 16-byte loads, grid-stride or contiguous chunks per
@@ -429,15 +508,15 @@ def main():
     ap.add_argument("--bits", type=int, default=8)
     ap.add_argument("--batch-steps", type=int, default=8, help="timed batch-256 steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--configs", default="c1,c2,c4,c5",
-                    help="extra workloads carried under 'configs' (comma list of c1,c2,c4,c5; '' for none)")
+    ap.add_argument("--configs", default="c1,c2,c4,c5,graph",
+                    help="extra workloads carried under 'configs' (comma list of c1,c2,c4,c5,graph; '' for none)")
     ap.add_argument("--profile-only", action="store_true", help="build + a short timed loop (for rocprofv3)")
     ap.add_argument("--profile-batch", action="store_true",
                     help="build + timed batch-256 searches on the matrix-core path (for rocprofv3)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--stream-ceiling", action="store_true", help="only time the read-only streaming kernel")
-    ap.add_argument("--config", default=None, choices=["c1", "c2", "c4", "c5"],
+    ap.add_argument("--config", default=None, choices=["c1", "c2", "c4", "c5", "graph"],
                     help="run one extra workload alone and print its object (for rocprofv3)")
     args = ap.parse_args()
 
@@ -468,7 +547,8 @@ def main():
     budget = 0.0 if args.no_cpu_baseline else 6.0
     if args.config:
         fn = {"c1": lambda: bench_c1(ctx, torch), "c2": lambda: bench_c2(ctx, torch, budget),
-              "c4": lambda: bench_c4(ctx, torch, budget), "c5": lambda: bench_c5(ctx, torch, budget)}[args.config]
+              "c4": lambda: bench_c4(ctx, torch, budget), "c5": lambda: bench_c5(ctx, torch, budget),
+              "graph": lambda: bench_graph(ctx, torch, budget)}[args.config]
         print(json.dumps({args.config: fn(), "device": info["name"]}))
         ctx.destroy()
         return
@@ -597,6 +677,8 @@ def main():
             configs["c4_int4_1bit_4Mx1024"] = bench_c4(ctx, torch, budget)
         elif name == "c5":
             configs["c5_ivf_int8_4Mx768"] = bench_c5(ctx, torch, budget)
+        elif name == "graph":
+            configs["hnsw_layer0_beam_200kx768"] = bench_graph(ctx, torch, budget)
     log("streaming ceiling")
     ceiling = stream_ceiling(torch)
 

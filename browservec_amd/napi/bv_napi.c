@@ -51,6 +51,7 @@ static napi_value throw_bv(napi_env env, int rc) {
  * the last call's completion destroys the index (all on the main thread). */
 typedef struct {
     bv_index *idx;
+    bv_graph *graph; /* a graph searcher's handle has graph set and idx NULL */
     uint32_t dim;
     uint32_t pending;
     int dead;
@@ -67,6 +68,11 @@ static void *get_ptr(napi_env env, napi_value v) {
 static index_handle *get_index(napi_env env, napi_value v) {
     index_handle *h = (index_handle *)get_ptr(env, v);
     return h && h->idx && !h->dead ? h : NULL;
+}
+
+static index_handle *get_graph(napi_env env, napi_value v) {
+    index_handle *h = (index_handle *)get_ptr(env, v);
+    return h && h->graph && !h->dead ? h : NULL;
 }
 
 static int get_u32(napi_env env, napi_value v, uint32_t *out) {
@@ -112,7 +118,7 @@ static napi_value length_error(napi_env env, size_t want, size_t got) {
 /* ---- asynchronous device calls --------------------------------------------- */
 typedef enum {
     OP_APPEND, OP_QUERY, OP_QUERY_MASKED, OP_QUERY_BATCH, OP_SEARCH, OP_RERANK, OP_BUILD, OP_SAVE, OP_LOAD,
-    OP_ROWS, OP_ROWS_MASKED
+    OP_ROWS, OP_ROWS_MASKED, OP_GRAPH_SEARCH
 } op_kind;
 
 typedef struct {
@@ -159,6 +165,10 @@ static void job_execute(napi_env env, void *data) {
         break;
     case OP_ROWS_MASKED:
         j->rc = bv_index_query_rows_masked(j->idx, j->data, j->aux, j->n_aux, j->k, j->rows, j->scores, j->counts);
+        break;
+    case OP_GRAPH_SEARCH:
+        j->rc = bv_graph_search(j->h->graph, j->data, j->nq, j->k, j->fetch, (uint32_t)j->count, j->rows, j->scores,
+                                j->counts);
         break;
     case OP_BUILD: j->rc = bv_index_build(j->idx); break;
     case OP_SAVE: {
@@ -224,6 +234,10 @@ static void job_complete(napi_env env, napi_status status, void *data) {
     if (--h->pending == 0 && h->dead && h->idx) {
         bv_index_destroy(h->idx);
         h->idx = NULL;
+    }
+    if (h->pending == 0 && h->dead && h->graph) {
+        bv_graph_destroy(h->graph);
+        h->graph = NULL;
     }
 }
 
@@ -627,6 +641,102 @@ static napi_value rows_common(napi_env env, napi_callback_info info, int masked)
 static napi_value query_rows(napi_env env, napi_callback_info info) { return rows_common(env, info, 0); }
 static napi_value query_rows_masked(napi_env env, napi_callback_info info) { return rows_common(env, info, 1); }
 
+/* ---- graph search (HNSWGpuSearcher) --------------------------------------- */
+/* graphCreate(device, {dim, metric, degree}) -> external */
+static napi_value graph_create(napi_env env, napi_callback_info info) {
+    ARGS(2);
+    bv_device *dev = (bv_device *)get_ptr(env, argv[0]);
+    const uint32_t dim = field_u32(env, argv[1], "dim", 0);
+    const uint32_t metric = field_u32(env, argv[1], "metric", BV_METRIC_COSINE);
+    const uint32_t degree = field_u32(env, argv[1], "degree", 0);
+    bv_graph *g = NULL;
+    int rc = bv_graph_create(dev, dim, metric, degree, &g);
+    if (rc) return throw_bv(env, rc);
+    index_handle *h = (index_handle *)calloc(1, sizeof(index_handle));
+    if (!h) {
+        bv_graph_destroy(g);
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    h->graph = g;
+    h->dim = dim;
+    napi_value out;
+    CALL(env, napi_create_external(env, h, NULL, NULL, &out));
+    return out;
+}
+
+/* graphAppend(g, Float32Array rows, count) (synchronous, as the reference's) */
+static napi_value graph_append(napi_env env, napi_callback_info info) {
+    ARGS(3);
+    size_t n = 0;
+    index_handle *h = get_graph(env, argv[0]);
+    const float *d = (const float *)get_typed(env, argv[1], napi_float32_array, &n);
+    uint32_t count = 0;
+    if (!h || !d || !get_u32(env, argv[2], &count)) {
+        napi_throw_type_error(env, NULL, "graphAppend(g, Float32Array, count)");
+        return NULL;
+    }
+    int rc = bv_graph_append(h->graph, d, n, count);
+    if (rc) return throw_bv(env, rc);
+    return NULL;
+}
+
+/* graphUpload(g, Uint32Array links, rows) */
+static napi_value graph_upload(napi_env env, napi_callback_info info) {
+    ARGS(3);
+    size_t n = 0;
+    index_handle *h = get_graph(env, argv[0]);
+    const uint32_t *l = (const uint32_t *)get_typed(env, argv[1], napi_uint32_array, &n);
+    uint32_t rows = 0;
+    if (!h || !l || !get_u32(env, argv[2], &rows)) {
+        napi_throw_type_error(env, NULL, "graphUpload(g, Uint32Array, rows)");
+        return NULL;
+    }
+    int rc = bv_graph_upload(h->graph, l, rows);
+    if (rc) return throw_bv(env, rc);
+    return NULL;
+}
+
+/* graphSearch(g, Float32Array queries, n, k, ef, entry) -> Promise<result> */
+static napi_value graph_search(napi_env env, napi_callback_info info) {
+    ARGS(6);
+    size_t qn = 0;
+    index_handle *h = get_graph(env, argv[0]);
+    const float *q = (const float *)get_typed(env, argv[1], napi_float32_array, &qn);
+    uint32_t n = 0, k = 0, ef = 0, entry = 0;
+    if (!h || !q || !get_u32(env, argv[2], &n) || !get_u32(env, argv[3], &k) || !get_u32(env, argv[4], &ef) ||
+        !get_u32(env, argv[5], &entry)) {
+        napi_throw_type_error(env, NULL, "graphSearch(g, Float32Array, n, k, ef, entry)");
+        return NULL;
+    }
+    if (qn < (size_t)n * h->dim) return length_error(env, (size_t)n * h->dim, qn);
+    job *j = (job *)calloc(1, sizeof(job));
+    if (!j || !keep(env, j, 0, argv[1]) || !job_result(env, j, n, k)) {
+        free(j);
+        napi_throw_error(env, NULL, "out of host memory");
+        return NULL;
+    }
+    j->op = OP_GRAPH_SEARCH;
+    j->h = h;
+    j->data = q;
+    j->nq = n;
+    j->k = k;
+    j->fetch = ef;
+    j->count = entry;
+    return queue(env, j, argv[0], "browservec.graphSearch");
+}
+
+static napi_value graph_destroy(napi_env env, napi_callback_info info) {
+    ARGS(1);
+    index_handle *h = get_graph(env, argv[0]);
+    if (!h) return NULL;
+    h->dead = 1;
+    if (h->pending) return NULL;  /* the search in flight destroys it */
+    bv_graph_destroy(h->graph);
+    h->graph = NULL;
+    return NULL;
+}
+
 static napi_value set_nprobe(napi_env env, napi_callback_info info) {
     ARGS(2);
     index_handle *h = get_index(env, argv[0]);
@@ -685,6 +795,8 @@ static napi_value init(napi_env env, napi_value exports) {
         {"query", query},              {"queryMasked", query_masked},   {"queryBatch", query_batch},
         {"search", search},            {"rerank", rerank},              {"setNprobe", set_nprobe},
         {"queryRows", query_rows},     {"queryRowsMasked", query_rows_masked},
+        {"graphCreate", graph_create}, {"graphAppend", graph_append},    {"graphUpload", graph_upload},
+        {"graphSearch", graph_search}, {"graphDestroy", graph_destroy},
         {"stats", stats},              {"lastError", last_error},
         {"saveSection", save_section}, {"loadSection", load_section},
     };

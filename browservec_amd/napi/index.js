@@ -252,7 +252,44 @@ function buildIndex(ctx, dim, metric, quantBits, quant, ann, chunkRows) {
   throw new Error(`quantBits ${bits} not supported (ships 0, 1, 4, 8)`);
 }
 
+// HNSWGpuSearcher (src/index/hnswGpu.ts:28-244) on the device: the HNSW
+// index (its CPU graph build) hands over corpus rows and the layer-0
+// adjacency; search() beam-searches a query batch in one launch.
+class HipGraphSearcher {
+  constructor(ctx, dim, metric, degree) {
+    this.dim = dim;
+    this.degree = degree;
+    this.handle = native.graphCreate(ctx.handle, { dim, metric: METRIC[metric], degree });
+    this.rows = 0;
+    this.graphRows = 0;
+  }
+  get maxRows() {
+    return 0xfffffffe;
+  }
+  append(data, count) {
+    native.graphAppend(this.handle, f32(data), count);
+    this.rows += count;
+  }
+  uploadGraph(links, rows) {
+    native.graphUpload(this.handle, links instanceof Uint32Array ? links : Uint32Array.from(links), rows);
+    this.graphRows = rows;
+  }
+  get uploadedRows() {
+    return this.graphRows;
+  }
+  search(queries, nQ, k, ef, entry) {
+    return native.graphSearch(this.handle, f32(queries), nQ, k, ef, entry >>> 0).then((res) => batchHits(res, nQ, k));
+  }
+  destroy() {
+    if (this.handle !== null) {
+      native.graphDestroy(this.handle);
+      this.handle = null;
+    }
+  }
+}
+
 module.exports = {
-  HipDeviceContext, HipIndex, HipFlatIndex, HipQuantIndex, HipIvfIndex, HipIvfQuantIndex, buildIndex,
+  HipDeviceContext, HipIndex, HipFlatIndex, HipQuantIndex, HipIvfIndex, HipIvfQuantIndex, HipGraphSearcher,
+  buildIndex,
   native, abiVersion: native.abiVersion,
 };

@@ -54,7 +54,8 @@ console.log(JSON.stringify({{abi: m.abiVersion, native: Object.keys(m.native),
     assert set(out["ivf"]) == ivf
     assert set(out["ivfquant"]) == ivf | {"ingestMode"}
     for fn in ("openDevice", "debugInject", "createIndex", "append", "build", "query", "queryMasked", "queryBatch",
-               "search", "rerank", "saveSection", "loadSection", "queryRows", "queryRowsMasked"):
+               "search", "rerank", "saveSection", "loadSection", "queryRows", "queryRowsMasked", "graphCreate",
+               "graphAppend", "graphUpload", "graphSearch", "graphDestroy"):
         assert fn in out["native"], fn
 
 
@@ -122,6 +123,15 @@ const dim = %(dim)d, n = %(n)d, nq = %(nq)d;
   try { await ivf2.loadSection(rows, n, sec); } catch (e) { out.loadTwice = [e.code, e.message]; }
   ivf2.destroy();
   try { m.buildIndex(ctx, dim, 'l2', 0, {}, {}); } catch (e) { out.ivfL2 = e.message; }
+  // the graph searcher: a ring adjacency of degree 4 over the rows
+  const gsr = new m.HipGraphSearcher(ctx, dim, 'cosine', 4);
+  gsr.append(rows, n);
+  const links = new Uint32Array(n * 4);
+  for (let r = 0; r < n; r++) for (let j = 0; j < 4; j++) links[r * 4 + j] = (r + j + 1) %% n;
+  gsr.uploadGraph(links, n);
+  out.graph = await gsr.search(qs, nq, 5, 32, 0);
+  try { new m.HipGraphSearcher(ctx, dim, 'cosine', 65); } catch (e) { out.graphDegree = [e.code, e.message]; }
+  gsr.destroy();
   // a destroy while a call is in flight: the call still completes
   const q2 = quant.query(qs.subarray(0, dim), 5);
   quant.destroy();
@@ -197,6 +207,16 @@ def test_node_results_equal_python_binding(tmp_path):
             same(out["ivf"][i], ivf.query(q[i], 10))
         assert out["ivfStats"] == [16, 4]
         assert out["ivfL2"] == "IVF supports metric cosine/dot only (l2 is later work)"
+        from browservec_amd import GraphSearcher
+
+        gs = GraphSearcher(ctx, dim, "cosine", 4)
+        gs.append(x, n)
+        gs.upload_graph(np.array([[(r + j + 1) % n for j in range(4)] for r in range(n)], np.uint32), n)
+        py_graph = gs.search(q, nq, 5, 32, 0)
+        for i in range(nq):
+            same(out["graph"][i], py_graph[i])
+        assert out["graphDegree"][0] == "BV_E_UNSUPPORTED" and "degree" in out["graphDegree"][1]
+        gs.destroy()
         ivf.destroy()
         flat.destroy()
         quant.destroy()
