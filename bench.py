@@ -410,18 +410,18 @@ def bench_graph(ctx, torch, budget_s):
     gs.append(xh, n)
     gs.upload_graph(links, n)
     qh = q.cpu().numpy()
-    gs.search(qh, nq, k, ef, 0)  # warmup
+    gs.search_arrays(qh, nq, k, ef, 0)  # warmup
     reps = 5
     t0 = time.perf_counter()
     for _ in range(reps):
-        hits = gs.search(qh, nq, k, ef, 0)
+        rows_g, _, cnt_g = gs.search_arrays(qh, nq, k, ef, 0)
     bq = reps * nq / (time.perf_counter() - t0)
     lat = []
     for i in range(32):
         t0 = time.perf_counter()
-        gs.search(qh[i:i + 1], 1, k, ef, 0)
+        gs.search_arrays(qh[i:i + 1], 1, k, ef, 0)
         lat.append((time.perf_counter() - t0) * 1e3)
-    rows_g = np.array([[h.row for h in hs] + [-1] * (k - len(hs)) for hs in hits])
+    rows_g = np.where(np.arange(k)[None, :] < cnt_g[:, None], rows_g.astype(np.int64), -1)
     recall = recall_vs_flat(ctx, x, q, rows_g, k, torch)
     flat.destroy()
     gs.destroy()

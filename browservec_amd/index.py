@@ -423,7 +423,8 @@ class GraphSearcher:
             raise ValueError(f"expected {int(rows) * self.degree} links, got {links.size}")
         L.check(self.lib.bv_graph_upload(self.handle, _ptr(links) if links.size else None, int(rows)))
 
-    def search(self, queries, n: int, k: int, ef: int, entry: int) -> list[list[FlatHit]]:
+    def search_arrays(self, queries, n: int, k: int, ef: int, entry: int):
+        """search() as arrays: rows [n, k], scores [n, k], counts [n]."""
         qs = _f32(queries).reshape(-1)
         _check_len(qs, int(n) * self.dim)
         rows = np.empty((max(n, 1), max(k, 1)), np.uint32)
@@ -431,6 +432,10 @@ class GraphSearcher:
         cnt = np.zeros(max(n, 1), np.uint32)
         L.check(self.lib.bv_graph_search(self.handle, _ptr(qs), int(n), int(k), int(ef), int(entry) & 0xFFFFFFFF,
                                          _ptr(rows), _ptr(scores), _ptr(cnt)))
+        return rows, scores, cnt
+
+    def search(self, queries, n: int, k: int, ef: int, entry: int) -> list[list[FlatHit]]:
+        rows, scores, cnt = self.search_arrays(queries, n, k, ef, entry)
         return [[FlatHit(int(rows[i, j]), float(scores[i, j])) for j in range(cnt[i])] for i in range(n)]
 
     def search_beams(self, queries, entries, ef: int, iter_cap: int):
