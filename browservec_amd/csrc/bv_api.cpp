@@ -164,6 +164,8 @@ struct bv_index {
     DevBuf cnorm, mq_rq, mq_up, mq_kept;       // flat int8 level-one batches: row code norms, query bounds, upper bounds, kept counts
     DevBuf mq_bk, mq_bu, mq_bc;               // level-one batches: per-workgroup buckets (lower keys, upper bounds, lengths)
     DevBuf sel_keys, sel_sorted, sel_tmp;     // selection by sort: keys, sorted keys, hipCUB scratch
+    DevBuf pm_codes, pm_ones, pm_cn, pm_qbits; // Hamming batches: +1/-1 int8 rows, unit scales, norms, query bits
+    uint64_t pm_rows = 0;                      // rows expanded into pm_codes
     DevBuf sel_list, sel_popc, sel_off, sel_misc;  // listed rows; mask word counts and offsets; flag + count
     HostBuf h_cnt;
     HostBuf h_rows, h_scores, h_n, h_flag;
@@ -1399,7 +1401,10 @@ static bool mq_eligible(const bv_index *idx, uint32_t nq, const uint32_t *d_mask
         return (idx->codec == C_F32DOT || idx->codec == C_F32L2) && mq_f32_supported(idx->dim) &&
                idx->rows > MQ_SAMPLE;
     const uint32_t u16 = idx->P / 16;  // 16-code units per row
-    return (idx->codec == C_Q8 || idx->codec == C_Q4) && u16 >= 2 && (u16 % 2) == 0 && u16 / 2 <= MQ_MAX_STEPS;
+    const bool shape = u16 >= 2 && (u16 % 2) == 0 && u16 / 2 <= MQ_MAX_STEPS;
+    // Hamming: the first-level pass over +1 / -1 rows, above the sample size
+    if (idx->codec == C_HAM) return shape && idx->rows > MQ_SAMPLE;
+    return (idx->codec == C_Q8 || idx->codec == C_Q4) && shape;
 }
 
 // Rotated queries split into three int8 levels in the 16-code unit layout
@@ -1566,11 +1571,67 @@ static int run_batched_f32(bv_index *idx, const float *d_q, uint32_t nq, uint32_
 // single query's are.
 // A query whose kept rows overflow their buffer runs the fused scan over
 // every row.
+// The codes the first-level pass reads: the index's int8 codes, or for a
+// Hamming index the +1 / -1 expansion of its 1-bit codes (unit scales), whose
+// int8 dots are the Hamming similarities.
+struct Q8Source {
+    const uint32_t *codes;
+    uint32_t W;
+    const float *scales, *cn;
+};
+
+// Hamming batches: the +1 / -1 rows (kept up to date with appends) and the
+// queries' 1-bit codes as level one of the packed levels.
+static int prepare_pm(bv_index *idx, const float *d_q, uint32_t nq, const unsigned char **qlev, uint64_t *qstride,
+                      Q8Source *src) {
+    hipStream_t s = idx->stream;
+    const uint32_t P = idx->P, W1 = idx->words_per_row;
+    if (idx->pm_rows < idx->rows) {
+        const uint64_t n0 = idx->pm_rows, n = idx->rows;
+        HIPX(idx->dev, idx->pm_codes.ensure(n * P, n0 * P, s), "expanded code buffer");
+        HIPX(idx->dev, idx->pm_ones.ensure(n * 4, n0 * 4, s), "scale buffer");
+        HIPX(idx->dev, idx->pm_cn.ensure(n * 4, n0 * 4, s), "norm buffer");
+        HIPX(idx->dev,
+             launch_expand_pm(idx->codes.as<uint32_t>() + n0 * W1, (n - n0) * W1,
+                              idx->pm_codes.as<uint32_t>() + n0 * (P / 4), s),
+             "expand kernel");
+        HIPX(idx->dev, launch_fill_f32(idx->pm_ones.as<float>() + n0, n - n0, 1.0f, s), "fill kernel");
+        HIPX(idx->dev,
+             launch_row_code_norms(idx->pm_codes.as<uint32_t>() + n0 * (P / 4), n - n0, P / 4,
+                                   idx->pm_cn.as<float>() + n0, s),
+             "norm kernel");
+        idx->pm_rows = n;
+    }
+    const size_t st = level_stride(C_Q8, P);
+    HIPX(idx->dev, idx->pm_qbits.ensure((size_t)nq * W1 * 4, 0, s), "query buffer");
+    HIPX(idx->dev, idx->qscale.ensure((size_t)nq * 4, 0, s), "query buffer");
+    HIPX(idx->dev, idx->qscan.ensure((size_t)nq * st, 0, s), "query buffer");
+    EncodeArgs e{};
+    e.src = d_q;
+    e.rows = nq;
+    e.dim = idx->dim;
+    e.P = P;
+    e.signs = idx->signs.as<float>();
+    e.rounds = idx->d.rounds;
+    e.bits = 1;  // the queries' bits, as the single-query Hamming scan takes them
+    e.codes = idx->pm_qbits.as<uint32_t>();
+    e.scales = idx->qscale.as<float>();
+    HIPX(idx->dev, launch_encode(e, s), "query encode kernel");
+    HIPX(idx->dev, launch_pm_levels(idx->pm_qbits.as<uint32_t>(), nq, P, idx->qscan.as<unsigned char>(), st, s),
+         "query levels kernel");
+    *qlev = idx->qscan.as<unsigned char>();
+    *qstride = st;
+    *src = Q8Source{idx->pm_codes.as<uint32_t>(), P / 4, idx->pm_ones.as<float>(), idx->pm_cn.as<float>()};
+    return BV_OK;
+}
+
 static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out,
                           bool rerank, uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
     const unsigned char *qlev = nullptr;
     uint64_t qstride = 0;
-    int rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride);
+    Q8Source src{idx->codes.as<uint32_t>(), idx->words_per_row, idx->scales.as<float>(), idx->cnorm.as<float>()};
+    int rc = idx->codec == C_HAM ? prepare_pm(idx, d_q, nq, &qlev, &qstride, &src)
+                                 : prepare_levels16(idx, d_q, nq, &qlev, &qstride);
     if (rc) return rc;
     const uint64_t N = idx->rows, S = MQ_SAMPLE;  // N > S (mq_eligible)
     // rows kept per query: those within the bounds' width of the sample's
@@ -1606,10 +1667,10 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
                            idx->mq_cnt.as<uint32_t>(), (uint32_t)S, s),
          "query bound kernel");
     Mq1Args m{};
-    m.codes = idx->codes.as<uint32_t>();
-    m.scales = idx->scales.as<float>();
-    m.cn = idx->cnorm.as<float>();
-    m.W = idx->words_per_row;
+    m.codes = src.codes;
+    m.scales = src.scales;
+    m.cn = src.cn;
+    m.W = src.W;
     m.units = units16;
     m.qlev = qlev;
     m.qstride = qstride;
@@ -1649,9 +1710,9 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
         if (rn == 0) break;
         m.n = rn;
         m.row_base = r0;
-        m.codes = idx->codes.as<uint32_t>() + r0 * idx->words_per_row;
-        m.scales = idx->scales.as<float>() + r0;
-        m.cn = idx->cnorm.as<float>() + r0;
+        m.codes = src.codes + r0 * src.W;
+        m.scales = src.scales + r0;
+        m.cn = src.cn + r0;
         m.cand = idx->mq_bk.as<uint64_t>();
         HIPX(idx->dev, launch_mq1_scan(m, s), "batched scan kernel");
         HIPX(idx->dev,
@@ -1666,8 +1727,8 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
             sa.tau_max = false;
         }
     }
-    m.codes = idx->codes.as<uint32_t>();
-    m.scales = idx->scales.as<float>();
+    m.codes = src.codes;
+    m.scales = src.scales;
     m.cand = idx->mq_cand.as<uint64_t>();
     m.up_out = idx->mq_up.as<uint32_t>();
     m.cnt = idx->mq_cnt.as<uint32_t>();
@@ -1734,7 +1795,7 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
 static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                        uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
     if (!idx->quant) return run_batched_f32(idx, d_q, nq, kprime, k_out, d_rows, d_scores, d_n);
-    if (idx->codec == C_Q8 && idx->rows > MQ_SAMPLE)
+    if ((idx->codec == C_Q8 || idx->codec == C_HAM) && idx->rows > MQ_SAMPLE)
         return run_batched_q8(idx, d_q, nq, kprime, k_out, rerank, d_rows, d_scores, d_n);
     const unsigned char *qscan = (const unsigned char *)d_q;  // fp32 rows: the queries as they are
     uint64_t qstride = (uint64_t)idx->dim * 4;

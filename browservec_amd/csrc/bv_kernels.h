@@ -363,6 +363,15 @@ size_t scan_query_lds(int codec, uint32_t P);
 // True when the scan for this codec / row layout transforms fp32 queries itself (ScanArgs::qraw).
 bool scan_prep_supported(int codec, uint32_t units, uint32_t P);
 
+// ---- Hamming batches on the int8 first-level path (bv_mq.hip) ---------------
+// 1-bit codes (words 32-bit words) as +1 / -1 int8 codes (8 words out per word in).
+hipError_t launch_expand_pm(const uint32_t *bits, uint64_t words, uint32_t *out, hipStream_t s);
+// Queries' 1-bit codes (P / 32 words each) as packed levels: level one +1 / -1,
+// the other levels zero, tail scales (1, 0, 0).
+hipError_t launch_pm_levels(const uint32_t *qbits, uint32_t nq, uint32_t P, unsigned char *qlev, uint64_t stride,
+                            hipStream_t s);
+hipError_t launch_fill_f32(float *p, uint64_t n, float v, hipStream_t s);
+
 // ---- graph beam search (bv_graph.hip) ---------------------------------------
 constexpr uint32_t GRAPH_EF_CAP = 256;  // beam slots (src/engine/wgsl/graphSearch.ts:32)
 struct GraphArgs {

@@ -1403,6 +1403,85 @@ hipError_t launch_mq1_keep(const uint64_t *cand, const uint32_t *up, const uint3
     return hipGetLastError();
 }
 
+namespace {
+// 1-bit codes (bit j of word g = code 32g + j) as int8 +1 / -1 codes (byte
+// j of word g = code 4g + j): the int8 dot of two such rows is
+// P - 2 * popcount(a ^ b), the Hamming similarity.
+__device__ __forceinline__ uint32_t pm_word(uint32_t bits4) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w |= (((bits4 >> j) & 1u) ? 0x01u : 0xffu) << (8 * j);
+    return w;
+}
+
+__global__ __launch_bounds__(256) void expand_pm(const uint32_t *bits, uint64_t words, uint32_t *out) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += stride) {
+        const uint32_t b = bits[i];
+        uint4 lo, hi;
+        lo.x = pm_word(b), lo.y = pm_word(b >> 4), lo.z = pm_word(b >> 8), lo.w = pm_word(b >> 12);
+        hi.x = pm_word(b >> 16), hi.y = pm_word(b >> 20), hi.z = pm_word(b >> 24), hi.w = pm_word(b >> 28);
+        ((uint4 *)out)[2 * i] = lo;
+        ((uint4 *)out)[2 * i + 1] = hi;
+    }
+}
+
+// A query's 1-bit code as the batched scan's packed levels: level one the
+// +1 / -1 bytes, levels two and three zero, scales (1, 0, 0).
+__global__ __launch_bounds__(64) void pm_levels(const uint32_t *qbits, uint32_t P, unsigned char *qlev,
+                                                uint64_t stride) {
+    const uint32_t q = blockIdx.x, units = P / 16;
+    const uint32_t *b = qbits + (uint64_t)q * (P / 32);
+    unsigned char *dst = qlev + (uint64_t)q * stride;
+    for (uint32_t u = threadIdx.x; u < units; u += 64) {
+        const uint32_t half = (b[u >> 1] >> (16 * (u & 1))) & 0xffffu;
+        uint4 l1;
+        l1.x = pm_word(half), l1.y = pm_word(half >> 4), l1.z = pm_word(half >> 8), l1.w = pm_word(half >> 12);
+        uint4 *o = (uint4 *)(dst + (uint64_t)u * 48);
+        o[0] = l1;
+        o[1] = make_uint4(0, 0, 0, 0);
+        o[2] = make_uint4(0, 0, 0, 0);
+    }
+    if (threadIdx.x == 0) {
+        QLevelTail *t = (QLevelTail *)(dst + (uint64_t)units * 48);
+        t->s[0] = 1.0;
+        t->s[1] = 0.0;
+        t->s[2] = 0.0;
+        t->sum[0] = t->sum[1] = t->sum[2] = 0;
+        t->pad = 0;
+    }
+}
+
+__global__ __launch_bounds__(256) void fill_f32(float *p, uint64_t n, float v) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+}  // namespace
+
+hipError_t launch_expand_pm(const uint32_t *bits, uint64_t words, uint32_t *out, hipStream_t s) {
+    if (words == 0) return hipSuccess;
+    uint64_t blocks = (words + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(expand_pm, dim3((uint32_t)blocks), dim3(256), 0, s, bits, words, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_pm_levels(const uint32_t *qbits, uint32_t nq, uint32_t P, unsigned char *qlev, uint64_t stride,
+                            hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    if (P % 32 || stride < (uint64_t)P / 16 * 48 + sizeof(QLevelTail)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(pm_levels, dim3(nq), dim3(64), 0, s, qbits, P, qlev, stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_f32(float *p, uint64_t n, float v, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    uint64_t blocks = (n + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(fill_f32, dim3((uint32_t)blocks), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
+}
+
 hipError_t launch_row_code_norms(const uint32_t *codes, uint64_t n, uint32_t W, float *cn, hipStream_t s) {
     if (n == 0) return hipSuccess;
     uint64_t blocks = (n + 3) / 4;

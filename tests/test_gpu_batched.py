@@ -252,3 +252,32 @@ def test_batched_tiny_corpus(ctx, n):
         for h in batch[i]:
             assert abs(h.score - float(exact[h.row])) <= 1e-5 * float(np.linalg.norm(data[h.row])) + 1e-7
     flat.destroy()
+
+
+@pytest.mark.parametrize("dim,n,nq", [(256, 40000, 33), (1024, 30000, 300), (128, 20000, 9)])
+def test_batched_hamming_equals_singles(ctx, dim, n, nq):
+    """Hamming batches run the int8 first-level pass over the +1 / -1
+    expansion of the 1-bit codes: the int8 dot of two +1 / -1 rows is
+    P - 2 * popcount(a ^ b), so the keys are the single-query scan's exact
+    Hamming similarities; rows and scores equal the same queries run alone,
+    with and without the re-rank, across appends (the expansion follows
+    them), with duplicate rows tying."""
+    from browservec_amd import QuantIndex
+
+    say("batched hamming", dim, n, nq)
+    data = clustered(n, dim, 40, 0.1, seed=dim + 3)
+    data[n // 2:n // 2 + 200] = data[:200]  # ties: identical codes
+    idx = QuantIndex(ctx, dim, bits=1, scorer="hamming")
+    idx.append(data[:n - 2000], n - 2000)
+    qs = data[np.arange(nq) * (n // nq)] + gaussian(nq, dim, 4, normalize=False) * 0.05
+    qs = np.stack([o.normalize(q) for q in qs]).astype(np.float32)
+    singles_equal(idx, qs, 200, 10)
+    idx.append(data[n - 2000:], 2000)
+    rows, scores, cnt = singles_equal(idx, qs, 0, 50)
+    # the scores are Hamming similarities of the codes: integers in [-P, P]
+    P = idx.padded_dim
+    assert np.all(scores[:, :1] == np.round(scores[:, :1])) and np.all(np.abs(scores[:, 0]) <= P)
+    batch = idx.query_batch(qs, nq, 20)
+    for i in range(nq):
+        assert batch[i] == idx.query(qs[i], 20), i
+    idx.destroy()
