@@ -166,6 +166,7 @@ struct bv_index {
     DevBuf sel_keys, sel_sorted, sel_tmp;     // selection by sort: keys, sorted keys, hipCUB scratch
     DevBuf pm_codes, pm_ones, pm_cn, pm_qbits; // Hamming batches: +1/-1 int8 rows, unit scales, norms, query bits
     uint64_t pm_rows = 0;                      // rows expanded into pm_codes
+    DevBuf ivb_base, ivb_pcount, ivb_poff, ivb_fill, ivb_pq, ivb_pbase, ivb_tmp;  // list-major IVF batches
     DevBuf sel_list, sel_popc, sel_off, sel_misc;  // listed rows; mask word counts and offsets; flag + count
     HostBuf h_cnt;
     HostBuf h_rows, h_scores, h_n, h_flag;
@@ -1906,9 +1907,126 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
 //   k_out     : results per query
 //   rerank    : re-rank the kprime candidates with f64 dotRow
 //   outputs   : device arrays [nq][k_out], [nq]
+// IVF int8 batches, list-major: the probes of every query, then every
+// probed list read once for all the queries probing it (its rows' keys
+// written at their candidate positions, the single-query scan's keys), then
+// each query's top-kprime and the exact re-rank, as the fused scan does
+// query by query (ivfquant.ts:459-527).
+constexpr uint32_t IVF_BATCH_MIN_Q = 8;
+
+static bool ivf_batch_eligible(const bv_index *idx, uint32_t nq, const uint32_t *d_mask) {
+    if (!idx->ivf || idx->codec != C_Q8 || d_mask || nq < IVF_BATCH_MIN_Q || idx->rows == 0 || !idx->nlist)
+        return false;
+    const uint32_t u16 = idx->P / 16;
+    return u16 >= 2 && u16 <= 64 && (u16 & (u16 - 1)) == 0;
+}
+
+static int run_ivf_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out,
+                           bool rerank, uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
+    hipStream_t s = idx->stream;
+    const unsigned char *qlev = nullptr;
+    uint64_t qstride = 0;
+    int rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride);  // also leaves the rotated queries in qrot
+    if (rc) return rc;
+    const uint32_t nprobe = ivf_resolve_nprobe(idx), nlist = idx->nlist;
+    uint64_t cap = 0;  // the most candidates a query can have: its nprobe largest lists
+    for (uint32_t i = 0; i < nprobe && i < idx->list_sizes_desc.size(); ++i) cap += idx->list_sizes_desc[i];
+    cap = std::max<uint64_t>(cap, 1);
+    const uint64_t npairs = (uint64_t)nq * nprobe;
+    if (npairs > 0xffffffffull || cap > 0xffffffffull) return fail(BV_E_UNSUPPORTED, "IVF batch too large");
+    HIPX(idx->dev, idx->probe_scores.ensure((size_t)nq * nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->probes.ensure(npairs * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->cand_tot.ensure((size_t)nq * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivb_base.ensure(npairs * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivb_pq.ensure(npairs * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivb_pbase.ensure(npairs * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivb_pcount.ensure((size_t)nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivb_poff.ensure((size_t)nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivb_fill.ensure((size_t)nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_cand.ensure((size_t)nq * cap * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_cnt.ensure((size_t)nq * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, s), "scratch");
+    size_t tb = 0;
+    HIPX(idx->dev, sel_exclusive_scan(nullptr, tb, nullptr, nullptr, nlist, s), "scan sizing");
+    HIPX(idx->dev, idx->ivb_tmp.ensure(std::max<size_t>(tb, 256), 0, s), "scratch");
+    tb = idx->ivb_tmp.cap;
+
+    timing_begin(idx);
+    IvfProbeArgs pa{};
+    pa.centroids = idx->centroids.as<float>();
+    pa.nlist = nlist;
+    pa.P = idx->sample_dim;
+    pa.qrot = idx->qrot.as<float>();
+    pa.scores = idx->probe_scores.as<float>();
+    pa.nprobe = nprobe;
+    pa.probes = idx->probes.as<uint32_t>();
+    pa.offset = idx->list_off.as<uint32_t>();
+    pa.totals = idx->cand_tot.as<uint64_t>();
+    HIPX(idx->dev, ivf_launch_probes(pa, nq, s), "probe kernels");
+    HIPX(idx->dev, launch_zero(idx->ivb_pcount.p, (size_t)nlist * 4, s), "scratch clear");
+    HIPX(idx->dev, launch_zero(idx->ivb_fill.p, (size_t)nlist * 4, s), "scratch clear");
+    HIPX(idx->dev,
+         launch_ivf_pairs(idx->probes.as<uint32_t>(), nq, nprobe, idx->list_off.as<uint32_t>(),
+                          idx->ivb_base.as<uint32_t>(), idx->mq_cnt.as<uint32_t>(), idx->ivb_pcount.as<uint32_t>(), s),
+         "pair kernel");
+    HIPX(idx->dev,
+         sel_exclusive_scan(idx->ivb_tmp.p, tb, idx->ivb_pcount.as<uint32_t>(), idx->ivb_poff.as<uint32_t>(), nlist, s),
+         "pair scan");
+    HIPX(idx->dev,
+         launch_ivf_pair_scatter(idx->probes.as<uint32_t>(), idx->ivb_base.as<uint32_t>(), (uint32_t)npairs, nprobe,
+                                 idx->ivb_poff.as<uint32_t>(), idx->ivb_fill.as<uint32_t>(),
+                                 idx->ivb_pq.as<uint32_t>(), idx->ivb_pbase.as<uint32_t>(), s),
+         "pair scatter kernel");
+    HIPX(idx->dev,
+         launch_ivf_list_scan(idx->codes.as<uint32_t>(), idx->words_per_row, idx->scales.as<float>(),
+                              idx->list_off.as<uint32_t>(), idx->list_rows.as<uint32_t>(), nlist,
+                              idx->ivb_poff.as<uint32_t>(), idx->ivb_pcount.as<uint32_t>(), idx->ivb_pq.as<uint32_t>(),
+                              idx->ivb_pbase.as<uint32_t>(), qlev, qstride, idx->P / 16,
+                              idx->mq_cand.as<uint64_t>(), cap, s),
+         "list scan kernel");
+    MqSelArgs fa{};
+    fa.cand = idx->mq_cand.as<uint64_t>();
+    fa.cnt = idx->mq_cnt.as<uint32_t>();
+    fa.cap = cap;
+    fa.kk = kprime;
+    fa.merged = idx->merged.as<uint64_t>();
+    fa.merged_n = idx->merged_n.as<uint32_t>();
+    if (!rerank) {
+        fa.k_out = k_out;
+        fa.out_rows = d_rows;
+        fa.out_scores = d_scores;
+        fa.out_n = d_n;
+    }
+    HIPX(idx->dev, launch_mq_select(fa, nq, s), "batched select kernel");
+    if (rerank) {
+        MqRerankArgs r{};
+        r.rows = idx->raw.as<float>();
+        r.dim = idx->dim;
+        r.q = d_q;
+        r.q_stride = idx->dim;
+        r.merged = idx->merged.as<uint64_t>();
+        r.merged_n = idx->merged_n.as<uint32_t>();
+        r.kprime = kprime;
+        r.k_out = k_out;
+        r.out_rows = d_rows;
+        r.out_scores = d_scores;
+        r.out_n = d_n;
+        HIPX(idx->dev, launch_mq_rerank(r, nq, s), "rerank kernel");
+    }
+    timing_end(idx);
+    idx->last_scanned = 0;
+    return BV_OK;
+}
+
 static int run_pipeline(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                         const uint32_t *d_mask, uint64_t mask_bits, uint32_t *d_rows, float *d_scores,
                         uint32_t *d_n, bool may_alternate = false) {
+    if (ivf_batch_eligible(idx, nq, d_mask)) {
+        int rc = lanes_join(idx);
+        if (rc) return rc;
+        return run_ivf_batched(idx, d_q, nq, kprime, k_out, rerank, d_rows, d_scores, d_n);
+    }
     if (mq_eligible(idx, nq, d_mask)) {
         int rc = lanes_join(idx);  // the batch path shares the index stream's scratch and outputs
         if (rc) return rc;

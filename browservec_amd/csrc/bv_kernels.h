@@ -363,6 +363,24 @@ size_t scan_query_lds(int codec, uint32_t P);
 // True when the scan for this codec / row layout transforms fp32 queries itself (ScanArgs::qraw).
 bool scan_prep_supported(int codec, uint32_t units, uint32_t P);
 
+// ---- list-major IVF int8 batches (bv_mq.hip) ---------------------------------
+// base[q][j]: where probe j's rows start among query q's candidates; cnt[q]:
+// its candidate count; pair_count[c] += queries probing list c (zeroed first).
+hipError_t launch_ivf_pairs(const uint32_t *probes, uint32_t nq, uint32_t nprobe, const uint32_t *list_off,
+                            uint32_t *base, uint32_t *cnt, uint32_t *pair_count, hipStream_t s);
+// The (query, base) pairs grouped by list (pair_off: exclusive scan of
+// pair_count; fill zeroed first).
+hipError_t launch_ivf_pair_scatter(const uint32_t *probes, const uint32_t *base, uint32_t npairs, uint32_t nprobe,
+                                   const uint32_t *pair_off, uint32_t *fill, uint32_t *pair_q, uint32_t *pair_base,
+                                   hipStream_t s);
+// Every probed list's rows scored once for all its queries: the single-query
+// scan's key at cand[q * cap + base + i].
+hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, const float *scales, const uint32_t *list_off,
+                                const uint32_t *list_rows, uint32_t nlist, const uint32_t *pair_off,
+                                const uint32_t *pair_count, const uint32_t *pair_q, const uint32_t *pair_base,
+                                const unsigned char *qlev, uint64_t qstride, uint32_t units16, uint64_t *cand,
+                                uint64_t cap, hipStream_t s);
+
 // ---- Hamming batches on the int8 first-level path (bv_mq.hip) ---------------
 // 1-bit codes (words 32-bit words) as +1 / -1 int8 codes (8 words out per word in).
 hipError_t launch_expand_pm(const uint32_t *bits, uint64_t words, uint32_t *out, hipStream_t s);

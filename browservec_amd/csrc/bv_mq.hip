@@ -1365,6 +1365,152 @@ __global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, const f
 
 }  // namespace
 
+namespace {
+// ---- list-major IVF batches (int8) -------------------------------------------
+// Each query's candidates are its probed lists' rows in probe order, then
+// list order (gatherCandidates); base[q][j] is where probe j's rows start.
+// One thread per query; pair_count[c] counts the queries probing list c.
+__global__ __launch_bounds__(256) void ivf_pair_bases(const uint32_t *probes, uint32_t nq, uint32_t nprobe,
+                                                      const uint32_t *list_off, uint32_t *base, uint32_t *cnt,
+                                                      uint32_t *pair_count) {
+    const uint32_t q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= nq) return;
+    uint32_t run = 0;
+    for (uint32_t j = 0; j < nprobe; ++j) {
+        const uint32_t c = probes[(uint64_t)q * nprobe + j];
+        base[(uint64_t)q * nprobe + j] = run;
+        run += list_off[c + 1] - list_off[c];
+        atomicAdd(&pair_count[c], 1u);
+    }
+    cnt[q] = run;
+}
+
+// The (query, base) pairs grouped by list: pair_off = exclusive scan of
+// pair_count; fill[c] starts at zero.
+__global__ __launch_bounds__(256) void ivf_pair_scatter(const uint32_t *probes, const uint32_t *base, uint32_t npairs,
+                                                        uint32_t nprobe, const uint32_t *pair_off, uint32_t *fill,
+                                                        uint32_t *pair_q, uint32_t *pair_base) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= npairs) return;
+    const uint32_t c = probes[i];
+    const uint32_t slot = pair_off[c] + atomicAdd(&fill[c], 1u);
+    pair_q[slot] = i / nprobe;
+    pair_base[slot] = base[i];
+}
+
+// One workgroup per list: its rows read once for every query probing it,
+// IVF_QC queries at a time; 16 lanes per row, the single-query scan's key
+// (the three levels' exact int32 dots, combined in f64) written at the
+// row's candidate position of each query.
+constexpr int IVF_QC = 8;
+template <int UNITS>
+__global__ __launch_bounds__(1024) void ivf_list_scan(const uint32_t *codes, const float *scales,
+                                                      const uint32_t *list_off, const uint32_t *list_rows,
+                                                      const uint32_t *pair_off, const uint32_t *pair_count,
+                                                      const uint32_t *pair_q, const uint32_t *pair_base,
+                                                      const unsigned char *qlev, uint64_t qstride, uint64_t *cand,
+                                                      uint64_t cap) {
+    constexpr int PER = UNITS < 16 ? 1 : UNITS / 16;
+    constexpr uint32_t W = UNITS * 4;
+    __shared__ v4i ql[IVF_QC][UNITS * 3];
+    __shared__ double qs[IVF_QC][3];
+    __shared__ uint32_t qid[IVF_QC], qbase[IVF_QC];
+    const uint32_t c = blockIdx.x, tid = threadIdx.x;
+    const uint32_t np = pair_count[c], p0 = pair_off[c];
+    const uint32_t r0 = list_off[c], nrows = list_off[c + 1] - r0;
+    if (np == 0 || nrows == 0) return;
+    const int l16 = tid & 15;
+    for (uint32_t pc = 0; pc < np; pc += IVF_QC) {
+        const uint32_t m = np - pc < (uint32_t)IVF_QC ? np - pc : (uint32_t)IVF_QC;
+        __syncthreads();  // the previous chunk is done with the query levels
+        for (uint32_t i = tid; i < m * UNITS * 3; i += 1024) {
+            const uint32_t k = i / (UNITS * 3), u = i % (UNITS * 3);
+            const uint32_t q = pair_q[p0 + pc + k];
+            ql[k][u] = ((const v4i *)(qlev + (uint64_t)q * qstride))[u];
+        }
+        if (tid < m) {
+            const uint32_t q = pair_q[p0 + pc + tid];
+            const QLevelTail *t = (const QLevelTail *)(qlev + (uint64_t)q * qstride + (uint64_t)UNITS * 48);
+            qs[tid][0] = t->s[0];
+            qs[tid][1] = t->s[1];
+            qs[tid][2] = t->s[2];
+            qid[tid] = q;
+            qbase[tid] = pair_base[p0 + pc + tid];
+        }
+        __syncthreads();
+        for (uint32_t i = tid >> 4; i < nrows; i += 64) {
+            const uint32_t row = list_rows[r0 + i];
+            const v4i *x = (const v4i *)(codes + (uint64_t)row * W);
+            v4i cx[PER];
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int u = l16 + 16 * j;
+                cx[j] = u < UNITS ? x[u] : v4i{};
+            }
+            const float sc = scales[row];
+            for (uint32_t k = 0; k < m; ++k) {
+                int a0 = 0, a1 = 0, a2 = 0;
+#pragma unroll
+                for (int j = 0; j < PER; ++j) {
+                    const int u = l16 + 16 * j;
+                    if (u >= UNITS) continue;
+                    const v4i q0 = ql[k][3 * u], q1 = ql[k][3 * u + 1], q2 = ql[k][3 * u + 2];
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        a0 = __builtin_amdgcn_sdot4(cx[j][w], q0[w], a0, false);
+                        a1 = __builtin_amdgcn_sdot4(cx[j][w], q1[w], a1, false);
+                        a2 = __builtin_amdgcn_sdot4(cx[j][w], q2[w], a2, false);
+                    }
+                }
+                a0 = row16_sum(a0), a1 = row16_sum(a1), a2 = row16_sum(a2);
+                if (l16 == 0)
+                    cand[(uint64_t)qid[k] * cap + qbase[k] + i] = q_key(qs[k][0], qs[k][1], qs[k][2], a0, a1, a2, sc, row);
+            }
+        }
+    }
+}
+}  // namespace
+
+hipError_t launch_ivf_pairs(const uint32_t *probes, uint32_t nq, uint32_t nprobe, const uint32_t *list_off,
+                            uint32_t *base, uint32_t *cnt, uint32_t *pair_count, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    hipLaunchKernelGGL(ivf_pair_bases, dim3((nq + 255) / 256), dim3(256), 0, s, probes, nq, nprobe, list_off, base, cnt,
+                       pair_count);
+    return hipGetLastError();
+}
+
+hipError_t launch_ivf_pair_scatter(const uint32_t *probes, const uint32_t *base, uint32_t npairs, uint32_t nprobe,
+                                   const uint32_t *pair_off, uint32_t *fill, uint32_t *pair_q, uint32_t *pair_base,
+                                   hipStream_t s) {
+    if (npairs == 0) return hipSuccess;
+    hipLaunchKernelGGL(ivf_pair_scatter, dim3((npairs + 255) / 256), dim3(256), 0, s, probes, base, npairs, nprobe,
+                       pair_off, fill, pair_q, pair_base);
+    return hipGetLastError();
+}
+
+hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, const float *scales, const uint32_t *list_off,
+                                const uint32_t *list_rows, uint32_t nlist, const uint32_t *pair_off,
+                                const uint32_t *pair_count, const uint32_t *pair_q, const uint32_t *pair_base,
+                                const unsigned char *qlev, uint64_t qstride, uint32_t units16, uint64_t *cand,
+                                uint64_t cap, hipStream_t s) {
+    if (nlist == 0) return hipSuccess;
+    if (W != units16 * 4) return hipErrorInvalidValue;
+#define BV_LS_CASE(U)                                                                                             \
+    case U: hipLaunchKernelGGL(ivf_list_scan<U>, dim3(nlist), dim3(1024), 0, s, codes, scales, list_off, list_rows, \
+                               pair_off, pair_count, pair_q, pair_base, qlev, qstride, cand, cap); break;
+    switch (units16) {
+        BV_LS_CASE(2)
+        BV_LS_CASE(4)
+        BV_LS_CASE(8)
+        BV_LS_CASE(16)
+        BV_LS_CASE(32)
+        BV_LS_CASE(64)
+    default: return hipErrorInvalidValue;
+    }
+#undef BV_LS_CASE
+    return hipGetLastError();
+}
+
 hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scales, const unsigned char *qlev,
                             uint64_t qstride, uint32_t units16, const uint32_t *rows, const uint32_t *kept,
                             uint64_t cap, uint64_t *keys, uint32_t nq, hipStream_t s) {

@@ -412,3 +412,33 @@ def test_ivf_incremental_append(ctx, bits):
         assert [(h.row, h.score) for h in inc.query(qq, 10)] == [(h.row, h.score) for h in ref.query(qq, 10)]
     inc.destroy()
     ref.destroy()
+
+
+@pytest.mark.parametrize("dim,n,nq,ivf", [(96, 12000, 40, {"nlist": 32, "iters": 3, "nprobe": 5}),
+                                          (768, 20000, 300, {"nlist": 64, "iters": 2, "nprobe": 9}),
+                                          (64, 3000, 9, {"nlist": 16, "iters": 2, "nprobe": 16})])
+def test_ivf_int8_batches_list_major_equal_singles(ctx, dim, n, nq, ivf):
+    """IVF int8 batches read every probed list once for all the queries
+    probing it (list-major) and write each row's single-query key at its
+    candidate position: rows and score bits equal the same queries run one at
+    a time, with and without the re-rank, also with every list probed."""
+    from browservec_amd import IVFQuantIndex
+
+    say("ivf list-major batch", dim, n, nq)
+    data = clustered(n, dim, 48, 0.1, seed=dim + nq)
+    idx = IVFQuantIndex(ctx, dim, bits=8, ivf=ivf)
+    idx.append(data, n)
+    qs = data[np.arange(nq) * (n // nq)] + gaussian(nq, dim, 11, normalize=False) * 0.05
+    qs = np.stack([o.normalize(q) for q in qs]).astype(np.float32)
+    for fetch, k in ((40, 10), (0, 25)):
+        rows, scores, cnt = idx.search(qs, fetch, k)
+        for i in range(nq):
+            r1, s1, c1 = idx.search(qs[i:i + 1], fetch, k)
+            assert cnt[i] == c1[0], i
+            assert np.array_equal(rows[i, :cnt[i]], r1[0, :c1[0]]), i
+            assert np.array_equal(scores[i, :cnt[i]].view(np.uint32), s1[0, :c1[0]].view(np.uint32)), i
+    m = min(16, nq)
+    batch = idx.query_batch(qs[:m], m, 30)
+    for i in range(m):
+        assert batch[i] == idx.query(qs[i], 30), i
+    idx.destroy()
