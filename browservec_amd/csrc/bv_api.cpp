@@ -167,6 +167,7 @@ struct bv_index {
     DevBuf pm_codes, pm_ones, pm_cn, pm_qbits; // Hamming batches: +1/-1 int8 rows, unit scales, norms, query bits
     uint64_t pm_rows = 0;                      // rows expanded into pm_codes
     DevBuf ivb_base, ivb_pcount, ivb_poff, ivb_fill, ivb_pq, ivb_pbase, ivb_tmp;  // list-major IVF batches
+    DevBuf ivb_chunks, ivb_choff;             // list-major IVF batches: work items per list, their offsets
     DevBuf sel_list, sel_popc, sel_off, sel_misc;  // listed rows; mask word counts and offsets; flag + count
     HostBuf h_cnt;
     HostBuf h_rows, h_scores, h_n, h_flag;
@@ -1943,6 +1944,8 @@ static int run_ivf_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_
     HIPX(idx->dev, idx->ivb_pcount.ensure((size_t)nlist * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->ivb_poff.ensure((size_t)nlist * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->ivb_fill.ensure((size_t)nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivb_chunks.ensure((size_t)nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivb_choff.ensure((size_t)nlist * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->mq_cand.ensure((size_t)nq * cap * 8, 0, s), "scratch");
     HIPX(idx->dev, idx->mq_cnt.ensure((size_t)nq * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, s), "scratch");
@@ -1978,12 +1981,17 @@ static int run_ivf_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_
                                  idx->ivb_poff.as<uint32_t>(), idx->ivb_fill.as<uint32_t>(),
                                  idx->ivb_pq.as<uint32_t>(), idx->ivb_pbase.as<uint32_t>(), s),
          "pair scatter kernel");
+    HIPX(idx->dev, launch_ivf_chunk_counts(idx->ivb_pcount.as<uint32_t>(), nlist, idx->ivb_chunks.as<uint32_t>(), s),
+         "chunk kernel");
+    HIPX(idx->dev,
+         sel_exclusive_scan(idx->ivb_tmp.p, tb, idx->ivb_chunks.as<uint32_t>(), idx->ivb_choff.as<uint32_t>(), nlist, s),
+         "chunk scan");
     HIPX(idx->dev,
          launch_ivf_list_scan(idx->codes.as<uint32_t>(), idx->words_per_row, idx->scales.as<float>(),
                               idx->list_off.as<uint32_t>(), idx->list_rows.as<uint32_t>(), nlist,
-                              idx->ivb_poff.as<uint32_t>(), idx->ivb_pcount.as<uint32_t>(), idx->ivb_pq.as<uint32_t>(),
-                              idx->ivb_pbase.as<uint32_t>(), qlev, qstride, idx->P / 16,
-                              idx->mq_cand.as<uint64_t>(), cap, s),
+                              idx->ivb_choff.as<uint32_t>(), (uint32_t)npairs, idx->ivb_poff.as<uint32_t>(),
+                              idx->ivb_pcount.as<uint32_t>(), idx->ivb_pq.as<uint32_t>(), idx->ivb_pbase.as<uint32_t>(),
+                              qlev, qstride, idx->P / 16, idx->mq_cand.as<uint64_t>(), cap, s),
          "list scan kernel");
     MqSelArgs fa{};
     fa.cand = idx->mq_cand.as<uint64_t>();

@@ -1403,9 +1403,19 @@ __global__ __launch_bounds__(256) void ivf_pair_scatter(const uint32_t *probes, 
 // (the three levels' exact int32 dots, combined in f64) written at the
 // row's candidate position of each query.
 constexpr int IVF_QC = 8;
+// chunks[c] = the list's work items (IVF_QC queries each).
+__global__ __launch_bounds__(256) void ivf_chunk_counts(const uint32_t *pair_count, uint32_t nlist, uint32_t *chunks) {
+    const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+    if (c < nlist) chunks[c] = (pair_count[c] + IVF_QC - 1) / IVF_QC;
+}
+
+// One workgroup per work item: a list and up to IVF_QC of the queries
+// probing it (chunk_off = exclusive scan of the lists' item counts), so a
+// list probed by many queries spreads over many workgroups.
 template <int UNITS>
 __global__ __launch_bounds__(1024) void ivf_list_scan(const uint32_t *codes, const float *scales,
                                                       const uint32_t *list_off, const uint32_t *list_rows,
+                                                      uint32_t nlist, const uint32_t *chunk_off,
                                                       const uint32_t *pair_off, const uint32_t *pair_count,
                                                       const uint32_t *pair_q, const uint32_t *pair_base,
                                                       const unsigned char *qlev, uint64_t qstride, uint64_t *cand,
@@ -1415,14 +1425,22 @@ __global__ __launch_bounds__(1024) void ivf_list_scan(const uint32_t *codes, con
     __shared__ v4i ql[IVF_QC][UNITS * 3];
     __shared__ double qs[IVF_QC][3];
     __shared__ uint32_t qid[IVF_QC], qbase[IVF_QC];
-    const uint32_t c = blockIdx.x, tid = threadIdx.x;
+    const uint32_t item = blockIdx.x, tid = threadIdx.x;
+    // the list: the last c with chunk_off[c] <= item
+    uint32_t lo = 0, hi = nlist;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) / 2;
+        if (chunk_off[mid] <= item) lo = mid;
+        else hi = mid;
+    }
+    const uint32_t c = lo;
     const uint32_t np = pair_count[c], p0 = pair_off[c];
+    const uint32_t pc = (item - chunk_off[c]) * IVF_QC;
     const uint32_t r0 = list_off[c], nrows = list_off[c + 1] - r0;
-    if (np == 0 || nrows == 0) return;
+    if (chunk_off[c] > item || pc >= np || nrows == 0) return;  // past the last item
     const int l16 = tid & 15;
-    for (uint32_t pc = 0; pc < np; pc += IVF_QC) {
+    {
         const uint32_t m = np - pc < (uint32_t)IVF_QC ? np - pc : (uint32_t)IVF_QC;
-        __syncthreads();  // the previous chunk is done with the query levels
         for (uint32_t i = tid; i < m * UNITS * 3; i += 1024) {
             const uint32_t k = i / (UNITS * 3), u = i % (UNITS * 3);
             const uint32_t q = pair_q[p0 + pc + k];
@@ -1488,16 +1506,26 @@ hipError_t launch_ivf_pair_scatter(const uint32_t *probes, const uint32_t *base,
     return hipGetLastError();
 }
 
-hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, const float *scales, const uint32_t *list_off,
-                                const uint32_t *list_rows, uint32_t nlist, const uint32_t *pair_off,
-                                const uint32_t *pair_count, const uint32_t *pair_q, const uint32_t *pair_base,
-                                const unsigned char *qlev, uint64_t qstride, uint32_t units16, uint64_t *cand,
-                                uint64_t cap, hipStream_t s) {
+hipError_t launch_ivf_chunk_counts(const uint32_t *pair_count, uint32_t nlist, uint32_t *chunks, hipStream_t s) {
     if (nlist == 0) return hipSuccess;
+    hipLaunchKernelGGL(ivf_chunk_counts, dim3((nlist + 255) / 256), dim3(256), 0, s, pair_count, nlist, chunks);
+    return hipGetLastError();
+}
+
+hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, const float *scales, const uint32_t *list_off,
+                                const uint32_t *list_rows, uint32_t nlist, const uint32_t *chunk_off, uint32_t npairs,
+                                const uint32_t *pair_off, const uint32_t *pair_count, const uint32_t *pair_q,
+                                const uint32_t *pair_base, const unsigned char *qlev, uint64_t qstride,
+                                uint32_t units16, uint64_t *cand, uint64_t cap, hipStream_t s) {
+    if (nlist == 0 || npairs == 0) return hipSuccess;
     if (W != units16 * 4) return hipErrorInvalidValue;
-#define BV_LS_CASE(U)                                                                                             \
-    case U: hipLaunchKernelGGL(ivf_list_scan<U>, dim3(nlist), dim3(1024), 0, s, codes, scales, list_off, list_rows, \
-                               pair_off, pair_count, pair_q, pair_base, qlev, qstride, cand, cap); break;
+    // work items: at most ceil(npairs / IVF_QC) + nlist (one partial chunk per list)
+    const uint64_t items = ((uint64_t)npairs + IVF_QC - 1) / IVF_QC + nlist;
+    if (items > 0x7fffffffull) return hipErrorInvalidValue;
+#define BV_LS_CASE(U)                                                                                               \
+    case U: hipLaunchKernelGGL(ivf_list_scan<U>, dim3((uint32_t)items), dim3(1024), 0, s, codes, scales, list_off,   \
+                               list_rows, nlist, chunk_off, pair_off, pair_count, pair_q, pair_base, qlev, qstride, \
+                               cand, cap); break;
     switch (units16) {
         BV_LS_CASE(2)
         BV_LS_CASE(4)
