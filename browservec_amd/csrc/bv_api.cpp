@@ -638,12 +638,18 @@ static void parallel_copy(void *dst, const void *src, size_t bytes) {
     const size_t part = (bytes / nt + 63) & ~size_t(63);
     std::vector<std::thread> th;
     th.reserve(nt);
-    for (unsigned t = 0; t < nt; ++t) {
-        const size_t o = (size_t)t * part;
-        if (o >= bytes) break;
-        const size_t len = std::min(part, bytes - o);
-        th.emplace_back([=] { std::memcpy((char *)dst + o, (const char *)src + o, len); });
+    size_t done = 0;  // bytes handed to threads; the rest is copied here
+    try {
+        for (unsigned t = 0; t < nt; ++t) {
+            const size_t o = (size_t)t * part;
+            if (o >= bytes) break;
+            const size_t len = std::min(part, bytes - o);
+            th.emplace_back([=] { std::memcpy((char *)dst + o, (const char *)src + o, len); });
+            done = o + len;
+        }
+    } catch (...) {  // no thread to be had: this thread copies what is left
     }
+    if (done < bytes) std::memcpy((char *)dst + done, (const char *)src + done, bytes - done);
     for (auto &x : th) x.join();
 }
 
