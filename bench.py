@@ -298,14 +298,21 @@ def bench_c4(ctx, torch, budget_s):
         b1, kus = kernel_timed_b1(idx, q, nq, 300, fetch, k, torch)
         b256 = qps(idx, q, nq, nq, 3, 1, fetch, k, torch)
         rows_q = device_rows(idx, q, fetch, k, torch)
+        # control: the same codes with the widest fetch the device serves; if
+        # recall rises with the fetch, the loss at fetch 200 is the codec's
+        # ranking, not the scan's
+        rows_wide = device_rows(idx, q, 1024, k, torch) if bits == 1 else None
         rb = dim * bits // 8
         res[name] = {"batch1_qps": round(b1, 1), "batch256_qps": round(b256, 1),
                      "roofline_b1": hbm_roof(n * (rb + 4) + fetch * dim * 4, kus),
-                     "encode_s": round(enc_s, 3), "rows_q": rows_q}
+                     "encode_s": round(enc_s, 3), "rows_q": rows_q, "rows_wide": rows_wide}
         idx.destroy()
         free(torch)
     for key in res:
         res[key]["recall_at_10"] = round(recall_vs_flat(ctx, x, q, res[key].pop("rows_q"), k, torch), 4)
+        wide = res[key].pop("rows_wide")
+        if wide is not None:
+            res[key]["recall_at_10_fetch_1024"] = round(recall_vs_flat(ctx, x, q, wide, k, torch), 4)
     cpu = None
     if budget_s > 0:
         cpu = cpu_entry(x.cpu().numpy(), q[:16].cpu().numpy(), "cosine", budget_s,
