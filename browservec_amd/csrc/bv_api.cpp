@@ -1914,7 +1914,7 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
 //   k_out     : results per query
 //   rerank    : re-rank the kprime candidates with f64 dotRow
 //   outputs   : device arrays [nq][k_out], [nq]
-// IVF int8 batches, list-major: the probes of every query, then every
+// IVF int8 / int4 batches, list-major: the probes of every query, then every
 // probed list read once for all the queries probing it (its rows' keys
 // written at their candidate positions, the single-query scan's keys), then
 // each query's top-kprime and the exact re-rank, as the fused scan does
@@ -1922,7 +1922,8 @@ static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kp
 constexpr uint32_t IVF_BATCH_MIN_Q = 8;
 
 static bool ivf_batch_eligible(const bv_index *idx, uint32_t nq, const uint32_t *d_mask) {
-    if (!idx->ivf || idx->codec != C_Q8 || d_mask || nq < IVF_BATCH_MIN_Q || idx->rows == 0 || !idx->nlist)
+    if (!idx->ivf || (idx->codec != C_Q8 && idx->codec != C_Q4) || d_mask || nq < IVF_BATCH_MIN_Q || idx->rows == 0 ||
+        !idx->nlist)
         return false;
     const uint32_t u16 = idx->P / 16;
     return u16 >= 2 && u16 <= 64 && (u16 & (u16 - 1)) == 0;
@@ -1993,7 +1994,8 @@ static int run_ivf_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_
          sel_exclusive_scan(idx->ivb_tmp.p, tb, idx->ivb_chunks.as<uint32_t>(), idx->ivb_choff.as<uint32_t>(), nlist, s),
          "chunk scan");
     HIPX(idx->dev,
-         launch_ivf_list_scan(idx->codes.as<uint32_t>(), idx->words_per_row, idx->scales.as<float>(),
+         launch_ivf_list_scan(idx->codes.as<uint32_t>(), idx->words_per_row, idx->codec == C_Q4 ? 4u : 8u,
+                              idx->scales.as<float>(), idx->codec == C_Q4 ? 1.0f / 7.0f : 1.0f,
                               idx->list_off.as<uint32_t>(), idx->list_rows.as<uint32_t>(), nlist,
                               idx->ivb_choff.as<uint32_t>(), (uint32_t)npairs, idx->ivb_poff.as<uint32_t>(),
                               idx->ivb_pcount.as<uint32_t>(), idx->ivb_pq.as<uint32_t>(), idx->ivb_pbase.as<uint32_t>(),

@@ -377,11 +377,14 @@ hipError_t launch_ivf_pair_scatter(const uint32_t *probes, const uint32_t *base,
 hipError_t launch_ivf_chunk_counts(const uint32_t *pair_count, uint32_t nlist, uint32_t *chunks, hipStream_t s);
 // Every probed list's rows scored once per work item (chunk_off: exclusive
 // scan of chunks): the single-query scan's key at cand[q * cap + base + i].
-hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, const float *scales, const uint32_t *list_off,
-                                const uint32_t *list_rows, uint32_t nlist, const uint32_t *chunk_off, uint32_t npairs,
-                                const uint32_t *pair_off, const uint32_t *pair_count, const uint32_t *pair_q,
-                                const uint32_t *pair_base, const unsigned char *qlev, uint64_t qstride,
-                                uint32_t units16, uint64_t *cand, uint64_t cap, hipStream_t s);
+// bits 8 (int8 codes) or 4 (int4 codes and the int4 level layout; keys as
+// the batched int4 scan forms them); scales times scale_mul (1/7 for int4).
+hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, uint32_t bits, const float *scales,
+                                float scale_mul, const uint32_t *list_off, const uint32_t *list_rows, uint32_t nlist,
+                                const uint32_t *chunk_off, uint32_t npairs, const uint32_t *pair_off,
+                                const uint32_t *pair_count, const uint32_t *pair_q, const uint32_t *pair_base,
+                                const unsigned char *qlev, uint64_t qstride, uint32_t units16, uint64_t *cand,
+                                uint64_t cap, hipStream_t s);
 
 // ---- Hamming batches on the int8 first-level path (bv_mq.hip) ---------------
 // 1-bit codes (words 32-bit words) as +1 / -1 int8 codes (8 words out per word in).

@@ -1412,8 +1412,8 @@ __global__ __launch_bounds__(256) void ivf_chunk_counts(const uint32_t *pair_cou
 // One workgroup per work item: a list and up to IVF_QC of the queries
 // probing it (chunk_off = exclusive scan of the lists' item counts), so a
 // list probed by many queries spreads over many workgroups.
-template <int UNITS>
-__global__ __launch_bounds__(1024) void ivf_list_scan(const uint32_t *codes, const float *scales,
+template <int UNITS, int BITS>
+__global__ __launch_bounds__(1024) void ivf_list_scan(const uint32_t *codes, const float *scales, float scale_mul,
                                                       const uint32_t *list_off, const uint32_t *list_rows,
                                                       uint32_t nlist, const uint32_t *chunk_off,
                                                       const uint32_t *pair_off, const uint32_t *pair_count,
@@ -1421,9 +1421,10 @@ __global__ __launch_bounds__(1024) void ivf_list_scan(const uint32_t *codes, con
                                                       const unsigned char *qlev, uint64_t qstride, uint64_t *cand,
                                                       uint64_t cap) {
     constexpr int PER = UNITS < 16 ? 1 : UNITS / 16;
-    constexpr uint32_t W = UNITS * 4;
+    constexpr uint32_t W = UNITS * BITS / 2;  // words per row: 16 codes per unit
     __shared__ v4i ql[IVF_QC][UNITS * 3];
     __shared__ double qs[IVF_QC][3];
+    __shared__ int32_t qc[IVF_QC][3];  // int4: 8 x the level's byte sum (the n ^ 8 offset of the codes)
     __shared__ uint32_t qid[IVF_QC], qbase[IVF_QC];
     const uint32_t item = blockIdx.x, tid = threadIdx.x;
     // the list: the last c with chunk_off[c] <= item
@@ -1452,20 +1453,24 @@ __global__ __launch_bounds__(1024) void ivf_list_scan(const uint32_t *codes, con
             qs[tid][0] = t->s[0];
             qs[tid][1] = t->s[1];
             qs[tid][2] = t->s[2];
+            for (int l = 0; l < 3; ++l) qc[tid][l] = BITS == 4 ? 8 * t->sum[l] : 0;
             qid[tid] = q;
             qbase[tid] = pair_base[p0 + pc + tid];
         }
         __syncthreads();
         for (uint32_t i = tid >> 4; i < nrows; i += 64) {
             const uint32_t row = list_rows[r0 + i];
-            const v4i *x = (const v4i *)(codes + (uint64_t)row * W);
             v4i cx[PER];
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
                 const int u = l16 + 16 * j;
-                cx[j] = u < UNITS ? x[u] : v4i{};
+                if (BITS == 8) {
+                    cx[j] = u < UNITS ? ((const v4i *)(codes + (uint64_t)row * W))[u] : v4i{};
+                } else {
+                    cx[j] = u < UNITS ? unpack_q4(((const uint2 *)(codes + (uint64_t)row * W))[u]) : v4i{};
+                }
             }
-            const float sc = scales[row];
+            const float sc = scales[row] * scale_mul;
             for (uint32_t k = 0; k < m; ++k) {
                 int a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
@@ -1482,7 +1487,9 @@ __global__ __launch_bounds__(1024) void ivf_list_scan(const uint32_t *codes, con
                 }
                 a0 = row16_sum(a0), a1 = row16_sum(a1), a2 = row16_sum(a2);
                 if (l16 == 0)
-                    cand[(uint64_t)qid[k] * cap + qbase[k] + i] = q_key(qs[k][0], qs[k][1], qs[k][2], a0, a1, a2, sc, row);
+                    cand[(uint64_t)qid[k] * cap + qbase[k] + i] =
+                        q_key(qs[k][0], qs[k][1], qs[k][2], dq<BITS>(a0, qc[k][0]), dq<BITS>(a1, qc[k][1]),
+                              dq<BITS>(a2, qc[k][2]), sc, row);
             }
         }
     }
@@ -1512,20 +1519,28 @@ hipError_t launch_ivf_chunk_counts(const uint32_t *pair_count, uint32_t nlist, u
     return hipGetLastError();
 }
 
-hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, const float *scales, const uint32_t *list_off,
-                                const uint32_t *list_rows, uint32_t nlist, const uint32_t *chunk_off, uint32_t npairs,
-                                const uint32_t *pair_off, const uint32_t *pair_count, const uint32_t *pair_q,
-                                const uint32_t *pair_base, const unsigned char *qlev, uint64_t qstride,
-                                uint32_t units16, uint64_t *cand, uint64_t cap, hipStream_t s) {
+hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, uint32_t bits, const float *scales,
+                                float scale_mul, const uint32_t *list_off, const uint32_t *list_rows, uint32_t nlist,
+                                const uint32_t *chunk_off, uint32_t npairs, const uint32_t *pair_off,
+                                const uint32_t *pair_count, const uint32_t *pair_q, const uint32_t *pair_base,
+                                const unsigned char *qlev, uint64_t qstride, uint32_t units16, uint64_t *cand,
+                                uint64_t cap, hipStream_t s) {
     if (nlist == 0 || npairs == 0) return hipSuccess;
-    if (W != units16 * 4) return hipErrorInvalidValue;
+    if ((bits != 8 && bits != 4) || W != units16 * bits / 2) return hipErrorInvalidValue;
     // work items: at most ceil(npairs / IVF_QC) + nlist (one partial chunk per list)
     const uint64_t items = ((uint64_t)npairs + IVF_QC - 1) / IVF_QC + nlist;
     if (items > 0x7fffffffull) return hipErrorInvalidValue;
-#define BV_LS_CASE(U)                                                                                               \
-    case U: hipLaunchKernelGGL(ivf_list_scan<U>, dim3((uint32_t)items), dim3(1024), 0, s, codes, scales, list_off,   \
-                               list_rows, nlist, chunk_off, pair_off, pair_count, pair_q, pair_base, qlev, qstride, \
-                               cand, cap); break;
+#define BV_LS_CASE(U)                                                                                             \
+    case U:                                                                                                        \
+        if (bits == 8)                                                                                             \
+            hipLaunchKernelGGL((ivf_list_scan<U, 8>), dim3((uint32_t)items), dim3(1024), 0, s, codes, scales,     \
+                               scale_mul, list_off, list_rows, nlist, chunk_off, pair_off, pair_count, pair_q,    \
+                               pair_base, qlev, qstride, cand, cap);                                              \
+        else                                                                                                       \
+            hipLaunchKernelGGL((ivf_list_scan<U, 4>), dim3((uint32_t)items), dim3(1024), 0, s, codes, scales,     \
+                               scale_mul, list_off, list_rows, nlist, chunk_off, pair_off, pair_count, pair_q,    \
+                               pair_base, qlev, qstride, cand, cap);                                              \
+        break;
     switch (units16) {
         BV_LS_CASE(2)
         BV_LS_CASE(4)

@@ -417,16 +417,17 @@ def test_ivf_incremental_append(ctx, bits):
 @pytest.mark.parametrize("dim,n,nq,ivf", [(96, 12000, 40, {"nlist": 32, "iters": 3, "nprobe": 5}),
                                           (768, 20000, 300, {"nlist": 64, "iters": 2, "nprobe": 9}),
                                           (64, 3000, 9, {"nlist": 16, "iters": 2, "nprobe": 16})])
-def test_ivf_int8_batches_list_major_equal_singles(ctx, dim, n, nq, ivf):
-    """IVF int8 batches read every probed list once for all the queries
+@pytest.mark.parametrize("bits", [8, 4])
+def test_ivf_batches_list_major_equal_singles(ctx, dim, n, nq, ivf, bits):
+    """IVF int8 and int4 batches read every probed list once for all the queries
     probing it (list-major) and write each row's single-query key at its
     candidate position: rows and score bits equal the same queries run one at
     a time, with and without the re-rank, also with every list probed."""
     from browservec_amd import IVFQuantIndex
 
-    say("ivf list-major batch", dim, n, nq)
+    say("ivf list-major batch", bits, dim, n, nq)
     data = clustered(n, dim, 48, 0.1, seed=dim + nq)
-    idx = IVFQuantIndex(ctx, dim, bits=8, ivf=ivf)
+    idx = IVFQuantIndex(ctx, dim, bits=bits, ivf=ivf)
     idx.append(data, n)
     qs = data[np.arange(nq) * (n // nq)] + gaussian(nq, dim, 11, normalize=False) * 0.05
     qs = np.stack([o.normalize(q) for q in qs]).astype(np.float32)
