@@ -315,13 +315,16 @@ __global__ __launch_bounds__(64) void ivf_probe_scores(IvfProbeArgs a) {
     }
 }
 
-// Query batches: eight queries per 256-thread workgroup (64 centroids x four
-// lanes), each centroid load feeding eight chains in the same element order
-// as ivf_probe_scores, so the scores are identical.  The queries sit in LDS
-// as f64, element 4j+m of query q at (4q+m)*(P/4+1)+j (the +1 keeps the four
-// chains' reads in distinct banks).  P a multiple of 128, at most 1024.
+// Query batches: eight queries per 256-thread workgroup, CT centroids per
+// four lanes (64 x CT centroids per workgroup), each centroid load feeding
+// eight chains and each query element read from LDS feeding CT chains, in
+// the same element order as ivf_probe_scores, so the scores are identical.
+// The queries sit in LDS as f64, element 4j+m of query q at
+// (4q+m)*(P/4+1)+j (the +1 keeps the four chains' reads in distinct banks).
+// P a multiple of 128, at most 1024.
 constexpr uint32_t PROBE_QB = 8;
 constexpr uint32_t PROBE_QB_MAX_DIM = 1024;
+template <int CT>
 __global__ __launch_bounds__(256) void ivf_probe_scores_qb(IvfProbeArgs a, uint32_t nq) {
     extern __shared__ double qd[];
     const uint32_t tid = threadIdx.x, g = tid >> 2, m = tid & 3, q0 = blockIdx.y * PROBE_QB;
@@ -333,31 +336,47 @@ __global__ __launch_bounds__(256) void ivf_probe_scores_qb(IvfProbeArgs a, uint3
         for (uint32_t e = tid; e < P; e += 256) qd[(qq * 4 + (e & 3)) * S + (e >> 2)] = (double)rq[e];
     }
     __syncthreads();
-    const uint32_t c = blockIdx.x * 64 + g;
-    const float *cen = a.centroids + (uint64_t)(c < a.nlist ? c : 0) * P;
-    double acc[PROBE_QB];
+    const float *cen[CT];
+    bool live[CT];
 #pragma unroll
-    for (uint32_t qq = 0; qq < PROBE_QB; ++qq) acc[qq] = 0.0;
-    if (c < a.nlist) {
-        for (uint32_t i = m; i < P; i += 128) {  // elements i + 4u, u < 32, all below P
-            float cv[32];
+    for (int j = 0; j < CT; ++j) {
+        const uint32_t c = blockIdx.x * 64 * CT + 64 * j + g;
+        live[j] = c < a.nlist;
+        cen[j] = a.centroids + (uint64_t)(live[j] ? c : 0) * P;
+    }
+    double acc[CT][PROBE_QB];
 #pragma unroll
-            for (int u = 0; u < 32; ++u) cv[u] = cen[i + 4 * u];
-            const double *qm = qd + m * S + (i >> 2);
+    for (int j = 0; j < CT; ++j)
 #pragma unroll
-            for (int u = 0; u < 32; ++u) {
-                const double cd = (double)cv[u];
+        for (uint32_t qq = 0; qq < PROBE_QB; ++qq) acc[j][qq] = 0.0;
+    constexpr int U = CT == 1 ? 32 : 16;  // elements i + 4u, u < U, per round trip
+    for (uint32_t i = m; i < P; i += 4 * U) {  // P a multiple of 128: every element below P
+        float cv[CT][U];
 #pragma unroll
-                for (uint32_t qq = 0; qq < PROBE_QB; ++qq) acc[qq] = fma(cd, qm[qq * 4 * S + u], acc[qq]);
+        for (int j = 0; j < CT; ++j)
+#pragma unroll
+            for (int u = 0; u < U; ++u) cv[j][u] = cen[j][i + 4 * u];
+        const double *qm = qd + m * S + (i >> 2);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (uint32_t qq = 0; qq < PROBE_QB; ++qq) {
+                const double qv = qm[qq * 4 * S + u];
+#pragma unroll
+                for (int j = 0; j < CT; ++j) acc[j][qq] = fma((double)cv[j][u], qv, acc[j][qq]);
             }
         }
     }
 #pragma unroll
-    for (uint32_t qq = 0; qq < PROBE_QB; ++qq) {
-        const double a1 = __shfl_down(acc[qq], 1, 4), a2 = __shfl_down(acc[qq], 2, 4),
-                     a3 = __shfl_down(acc[qq], 3, 4);
-        if (m == 0 && c < a.nlist && qq < nqb)
-            a.scores[(uint64_t)(q0 + qq) * a.nlist + c] = (float)(((acc[qq] + a1) + a2) + a3);
+    for (int j = 0; j < CT; ++j) {
+        const uint32_t c = blockIdx.x * 64 * CT + 64 * j + g;
+#pragma unroll
+        for (uint32_t qq = 0; qq < PROBE_QB; ++qq) {
+            const double a1 = __shfl_down(acc[j][qq], 1, 4), a2 = __shfl_down(acc[j][qq], 2, 4),
+                         a3 = __shfl_down(acc[j][qq], 3, 4);
+            if (m == 0 && live[j] && qq < nqb)
+                a.scores[(uint64_t)(q0 + qq) * a.nlist + c] = (float)(((acc[j][qq] + a1) + a2) + a3);
+        }
     }
 }
 
@@ -596,9 +615,13 @@ hipError_t ivf_launch_means(const float *sample, uint32_t stride, uint32_t dim, 
 hipError_t ivf_launch_probes(const IvfProbeArgs &a, uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
     if (a.nlist > IVF_MAX_NLIST || a.nprobe > IVF_MAX_NPROBE || a.P > PROBE_MAX_DIM) return hipErrorInvalidValue;
-    if (nq >= PROBE_QB && a.P % 128 == 0 && a.P <= PROBE_QB_MAX_DIM)
-        hipLaunchKernelGGL(ivf_probe_scores_qb, dim3((a.nlist + 63) / 64, (nq + PROBE_QB - 1) / PROBE_QB), dim3(256),
-                           (size_t)PROBE_QB * 4 * (a.P / 4 + 1) * 8, s, a, nq);
+    const size_t qb_lds = (size_t)PROBE_QB * 4 * (a.P / 4 + 1) * 8;
+    if (nq >= PROBE_QB && a.P % 128 == 0 && a.P <= PROBE_QB_MAX_DIM && a.nlist >= 1024)
+        hipLaunchKernelGGL(ivf_probe_scores_qb<4>, dim3((a.nlist + 255) / 256, (nq + PROBE_QB - 1) / PROBE_QB),
+                           dim3(256), qb_lds, s, a, nq);
+    else if (nq >= PROBE_QB && a.P % 128 == 0 && a.P <= PROBE_QB_MAX_DIM)
+        hipLaunchKernelGGL(ivf_probe_scores_qb<1>, dim3((a.nlist + 63) / 64, (nq + PROBE_QB - 1) / PROBE_QB), dim3(256),
+                           qb_lds, s, a, nq);
     else
         hipLaunchKernelGGL(ivf_probe_scores, dim3((a.nlist + 15) / 16, nq), dim3(64), (size_t)a.P * 4, s, a);
     hipLaunchKernelGGL(ivf_probe_select, dim3(nq), dim3(256), ((size_t)a.nlist * 2 + 16) * 8, s, a);

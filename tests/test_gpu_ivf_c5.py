@@ -68,6 +68,9 @@ def test_ivf_4096_lists_p1024_matches_oracle(ctx):
     # pickProbes' scores: the 300-query batch (eight-query probe tiles) equals
     # single queries bit for bit, and both equal the oracle's f64 strided dot
     ps = idx.export_probe_scores(qs)
+    # calls of fewer than eight queries take the one-query kernel
+    ps1 = np.concatenate([idx.export_probe_scores(qs[s:s + 7]) for s in range(0, nq, 7)])
+    assert np.array_equal(ps.view(np.uint32), ps1.view(np.uint32))
     rq = np.stack([o.rotate(q, dim)[0] for q in qs])
     for i in (0, 1, 7, 8, 150, nq - 1):
         assert np.array_equal(ps[i].view(np.uint32), idx.export_probe_scores(qs[i:i + 1])[0].view(np.uint32)), i
