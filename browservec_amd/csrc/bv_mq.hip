@@ -1398,10 +1398,10 @@ __global__ __launch_bounds__(256) void ivf_pair_scatter(const uint32_t *probes, 
     pair_base[slot] = base[i];
 }
 
-// One workgroup per list: its rows read once for every query probing it,
-// IVF_QC queries at a time; 16 lanes per row, the single-query scan's key
-// (the three levels' exact int32 dots, combined in f64) written at the
-// row's candidate position of each query.
+// List-major IVF batches: each list's rows read once for every IVF_QC
+// queries probing it, the single-query scan's key (the three levels' exact
+// int32 dots, combined in f64) written at the row's candidate position of
+// each query.
 constexpr int IVF_QC = 8;
 // chunks[c] = the list's work items (IVF_QC queries each).
 __global__ __launch_bounds__(256) void ivf_chunk_counts(const uint32_t *pair_count, uint32_t nlist, uint32_t *chunks) {
@@ -1411,87 +1411,97 @@ __global__ __launch_bounds__(256) void ivf_chunk_counts(const uint32_t *pair_cou
 
 // One workgroup per work item: a list and up to IVF_QC of the queries
 // probing it (chunk_off = exclusive scan of the lists' item counts), so a
-// list probed by many queries spreads over many workgroups.
+// list probed by many queries spreads over many workgroups.  The work runs
+// on v_mfma_i32_32x32x32_i8: four waves per workgroup,
+// each taking 32-row tiles of the list.  B holds 24 columns, level l of
+// query k at column 8l + k (columns 24-31 and missing queries are zero),
+// staged in LDS by 16-byte unit so lane (c, h) reads column c at unit
+// 2 * step + h; A is row c of the tile at the same unit (int4 rows unpacked
+// to n ^ 8 bytes).  The int32 dots are exact; the three level dots of a
+// (row, query) meet in a per-wave LDS tile and q_key combines them in f64,
+// giving the single-query scan's key.
 template <int UNITS, int BITS>
-__global__ __launch_bounds__(1024) void ivf_list_scan(const uint32_t *codes, const float *scales, float scale_mul,
-                                                      const uint32_t *list_off, const uint32_t *list_rows,
-                                                      uint32_t nlist, const uint32_t *chunk_off,
-                                                      const uint32_t *pair_off, const uint32_t *pair_count,
-                                                      const uint32_t *pair_q, const uint32_t *pair_base,
-                                                      const unsigned char *qlev, uint64_t qstride, uint64_t *cand,
-                                                      uint64_t cap) {
-    constexpr int PER = UNITS < 16 ? 1 : UNITS / 16;
-    constexpr uint32_t W = UNITS * BITS / 2;  // words per row: 16 codes per unit
-    __shared__ v4i ql[IVF_QC][UNITS * 3];
+__global__ __launch_bounds__(256) void ivf_list_mfma(const uint32_t *codes, const float *scales, float scale_mul,
+                                                     const uint32_t *list_off, const uint32_t *list_rows,
+                                                     uint32_t nlist, const uint32_t *chunk_off,
+                                                     const uint32_t *pair_off, const uint32_t *pair_count,
+                                                     const uint32_t *pair_q, const uint32_t *pair_base,
+                                                     const unsigned char *qlev, uint64_t qstride, uint64_t *cand,
+                                                     uint64_t cap) {
+    static_assert(IVF_QC == 8 && UNITS % 2 == 0, "24 columns: three levels of eight queries");
+    constexpr int S = UNITS / 2;                 // K steps of 32 codes
+    constexpr uint32_t W = UNITS * BITS / 2;     // words per row
+    __shared__ v4i bq[S][2][32];
+    __shared__ int32_t stg[4][32][25];           // per wave: 32 rows x 24 columns (+1)
     __shared__ double qs[IVF_QC][3];
-    __shared__ int32_t qc[IVF_QC][3];  // int4: 8 x the level's byte sum (the n ^ 8 offset of the codes)
+    __shared__ int32_t qc[IVF_QC][3];
     __shared__ uint32_t qid[IVF_QC], qbase[IVF_QC];
     const uint32_t item = blockIdx.x, tid = threadIdx.x;
-    // the list: the last c with chunk_off[c] <= item
-    uint32_t lo = 0, hi = nlist;
+    uint32_t lo = 0, hi = nlist;  // the list: the last c with chunk_off[c] <= item
     while (hi - lo > 1) {
         const uint32_t mid = (lo + hi) / 2;
         if (chunk_off[mid] <= item) lo = mid;
         else hi = mid;
     }
-    const uint32_t c = lo;
-    const uint32_t np = pair_count[c], p0 = pair_off[c];
-    const uint32_t pc = (item - chunk_off[c]) * IVF_QC;
-    const uint32_t r0 = list_off[c], nrows = list_off[c + 1] - r0;
-    if (chunk_off[c] > item || pc >= np || nrows == 0) return;  // past the last item
-    const int l16 = tid & 15;
-    {
-        const uint32_t m = np - pc < (uint32_t)IVF_QC ? np - pc : (uint32_t)IVF_QC;
-        for (uint32_t i = tid; i < m * UNITS * 3; i += 1024) {
-            const uint32_t k = i / (UNITS * 3), u = i % (UNITS * 3);
-            const uint32_t q = pair_q[p0 + pc + k];
-            ql[k][u] = ((const v4i *)(qlev + (uint64_t)q * qstride))[u];
+    const uint32_t li = lo;
+    const uint32_t np = pair_count[li], p0 = pair_off[li];
+    const uint32_t pc = (item - chunk_off[li]) * IVF_QC;
+    const uint32_t r0 = list_off[li], nrows = list_off[li + 1] - r0;
+    if (chunk_off[li] > item || pc >= np || nrows == 0) return;  // past the last item
+    const uint32_t m = np - pc < (uint32_t)IVF_QC ? np - pc : (uint32_t)IVF_QC;
+    for (uint32_t i = tid; i < (uint32_t)UNITS * 32; i += 256) {
+        const uint32_t u = i / 32, col = i % 32, k = col % 8, l = col / 8;
+        v4i v{};
+        if (l < 3 && k < m) v = ((const v4i *)(qlev + (uint64_t)pair_q[p0 + pc + k] * qstride))[3 * u + l];
+        bq[u / 2][u % 2][col] = v;
+    }
+    if (tid < m) {
+        const uint32_t q = pair_q[p0 + pc + tid];
+        const QLevelTail *t = (const QLevelTail *)(qlev + (uint64_t)q * qstride + (uint64_t)UNITS * 48);
+        for (int l = 0; l < 3; ++l) {
+            qs[tid][l] = t->s[l];
+            qc[tid][l] = BITS == 4 ? 8 * t->sum[l] : 0;
         }
-        if (tid < m) {
-            const uint32_t q = pair_q[p0 + pc + tid];
-            const QLevelTail *t = (const QLevelTail *)(qlev + (uint64_t)q * qstride + (uint64_t)UNITS * 48);
-            qs[tid][0] = t->s[0];
-            qs[tid][1] = t->s[1];
-            qs[tid][2] = t->s[2];
-            for (int l = 0; l < 3; ++l) qc[tid][l] = BITS == 4 ? 8 * t->sum[l] : 0;
-            qid[tid] = q;
-            qbase[tid] = pair_base[p0 + pc + tid];
-        }
-        __syncthreads();
-        for (uint32_t i = tid >> 4; i < nrows; i += 64) {
-            const uint32_t row = list_rows[r0 + i];
-            v4i cx[PER];
+        qid[tid] = q;
+        qbase[tid] = pair_base[p0 + pc + tid];
+    }
+    __syncthreads();
+    const uint32_t wave = tid >> 6, lane = tid & 63, c = lane & 31, h = lane >> 5;
+    const uint32_t tiles = (nrows + 31) / 32;
+    for (uint32_t t = wave; t < tiles; t += 4) {
+        const uint32_t ri = t * 32 + c;
+        const uint64_t row = list_rows[r0 + (ri < nrows ? ri : nrows - 1)];  // past the end: a valid row, dropped
+        v4i A[S];
 #pragma unroll
-            for (int j = 0; j < PER; ++j) {
-                const int u = l16 + 16 * j;
-                if (BITS == 8) {
-                    cx[j] = u < UNITS ? ((const v4i *)(codes + (uint64_t)row * W))[u] : v4i{};
-                } else {
-                    cx[j] = u < UNITS ? unpack_q4(((const uint2 *)(codes + (uint64_t)row * W))[u]) : v4i{};
-                }
+        for (int st = 0; st < S; ++st) {
+            const uint32_t u = 2 * st + h;
+            if constexpr (BITS == 8) A[st] = ((const v4i *)(codes + row * W))[u];
+            else A[st] = unpack_q4(((const uint2 *)(codes + row * W))[u]);
+        }
+        v16i acc = v16i{};
+#pragma unroll
+        for (int st = 0; st < S; ++st) acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[st], bq[st][h][c], acc, 0, 0, 0);
+        if (c < 24) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) stg[wave][8 * (r >> 2) + 4 * h + (r & 3)][c] = acc[r];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t p = lane + 64 * j, rr = p % 32, k = p / 32;
+            const uint32_t i = t * 32 + rr;
+            if (k < m && i < nrows) {
+                const uint32_t rw = list_rows[r0 + i];
+                const float sc = scales[rw] * scale_mul;
+                cand[(uint64_t)qid[k] * cap + qbase[k] + i] =
+                    q_key(qs[k][0], qs[k][1], qs[k][2], dq<BITS>(stg[wave][rr][k], qc[k][0]),
+                          dq<BITS>(stg[wave][rr][8 + k], qc[k][1]), dq<BITS>(stg[wave][rr][16 + k], qc[k][2]), sc,
+                          rw);
             }
-            const float sc = scales[row] * scale_mul;
-            for (uint32_t k = 0; k < m; ++k) {
-                int a0 = 0, a1 = 0, a2 = 0;
-#pragma unroll
-                for (int j = 0; j < PER; ++j) {
-                    const int u = l16 + 16 * j;
-                    if (u >= UNITS) continue;
-                    const v4i q0 = ql[k][3 * u], q1 = ql[k][3 * u + 1], q2 = ql[k][3 * u + 2];
-#pragma unroll
-                    for (int w = 0; w < 4; ++w) {
-                        a0 = __builtin_amdgcn_sdot4(cx[j][w], q0[w], a0, false);
-                        a1 = __builtin_amdgcn_sdot4(cx[j][w], q1[w], a1, false);
-                        a2 = __builtin_amdgcn_sdot4(cx[j][w], q2[w], a2, false);
-                    }
-                }
-                a0 = row16_sum(a0), a1 = row16_sum(a1), a2 = row16_sum(a2);
-                if (l16 == 0)
-                    cand[(uint64_t)qid[k] * cap + qbase[k] + i] =
-                        q_key(qs[k][0], qs[k][1], qs[k][2], dq<BITS>(a0, qc[k][0]), dq<BITS>(a1, qc[k][1]),
-                              dq<BITS>(a2, qc[k][2]), sc, row);
-            }
         }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     }
 }
 }  // namespace
@@ -1533,11 +1543,11 @@ hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, uint32_t bits
 #define BV_LS_CASE(U)                                                                                             \
     case U:                                                                                                        \
         if (bits == 8)                                                                                             \
-            hipLaunchKernelGGL((ivf_list_scan<U, 8>), dim3((uint32_t)items), dim3(1024), 0, s, codes, scales,     \
+            hipLaunchKernelGGL((ivf_list_mfma<U, 8>), dim3((uint32_t)items), dim3(256), 0, s, codes, scales,      \
                                scale_mul, list_off, list_rows, nlist, chunk_off, pair_off, pair_count, pair_q,    \
                                pair_base, qlev, qstride, cand, cap);                                              \
         else                                                                                                       \
-            hipLaunchKernelGGL((ivf_list_scan<U, 4>), dim3((uint32_t)items), dim3(1024), 0, s, codes, scales,     \
+            hipLaunchKernelGGL((ivf_list_mfma<U, 4>), dim3((uint32_t)items), dim3(256), 0, s, codes, scales,      \
                                scale_mul, list_off, list_rows, nlist, chunk_off, pair_off, pair_count, pair_q,    \
                                pair_base, qlev, qstride, cand, cap);                                              \
         break;

@@ -1946,7 +1946,6 @@ __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
     const uint32_t nslots = a.grid * (SCAN_WG / 64);
     const uint64_t *wm = a.wmax + (uint64_t)qi * nslots;
     const uint32_t kp = a.kprime;
-    const uint32_t ng = a.grid < (uint32_t)NGROUP ? a.grid : (uint32_t)NGROUP;
     const uint32_t cap = kp <= (uint32_t)SCAN_WG ? (uint32_t)SCAN_WG : (uint32_t)SCAN_CAP;
     const int tid = threadIdx.x, lane = tid & 63;
     uint64_t th = 0;
