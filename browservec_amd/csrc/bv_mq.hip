@@ -1412,7 +1412,7 @@ __global__ __launch_bounds__(256) void ivf_chunk_counts(const uint32_t *pair_cou
 // One workgroup per work item: a list and up to IVF_QC of the queries
 // probing it (chunk_off = exclusive scan of the lists' item counts), so a
 // list probed by many queries spreads over many workgroups.  The work runs
-// on v_mfma_i32_32x32x32_i8: four waves per workgroup,
+// on v_mfma_i32_32x32x32_i8: IVF_LM_WAVES waves per workgroup,
 // each taking 32-row tiles of the list.  B holds 24 columns, level l of
 // query k at column 8l + k (columns 24-31 and missing queries are zero),
 // staged in LDS by 16-byte unit so lane (c, h) reads column c at unit
@@ -1420,8 +1420,9 @@ __global__ __launch_bounds__(256) void ivf_chunk_counts(const uint32_t *pair_cou
 // to n ^ 8 bytes).  The int32 dots are exact; the three level dots of a
 // (row, query) meet in a per-wave LDS tile and q_key combines them in f64,
 // giving the single-query scan's key.
+constexpr uint32_t IVF_LM_WAVES = 4;  // eight measured slower for int8 rows (1.58 ms against 1.35 ms at 4M x 768)
 template <int UNITS, int BITS>
-__global__ __launch_bounds__(256) void ivf_list_mfma(const uint32_t *codes, const float *scales, float scale_mul,
+__global__ __launch_bounds__(IVF_LM_WAVES * 64) void ivf_list_mfma(const uint32_t *codes, const float *scales, float scale_mul,
                                                      const uint32_t *list_off, const uint32_t *list_rows,
                                                      uint32_t nlist, const uint32_t *chunk_off,
                                                      const uint32_t *pair_off, const uint32_t *pair_count,
@@ -1432,7 +1433,7 @@ __global__ __launch_bounds__(256) void ivf_list_mfma(const uint32_t *codes, cons
     constexpr int S = UNITS / 2;                 // K steps of 32 codes
     constexpr uint32_t W = UNITS * BITS / 2;     // words per row
     __shared__ v4i bq[S][2][32];
-    __shared__ int32_t stg[4][32][25];           // per wave: 32 rows x 24 columns (+1)
+    __shared__ int32_t stg[IVF_LM_WAVES][32][25];  // per wave: 32 rows x 24 columns (+1)
     __shared__ double qs[IVF_QC][3];
     __shared__ int32_t qc[IVF_QC][3];
     __shared__ uint32_t qid[IVF_QC], qbase[IVF_QC];
@@ -1449,7 +1450,7 @@ __global__ __launch_bounds__(256) void ivf_list_mfma(const uint32_t *codes, cons
     const uint32_t r0 = list_off[li], nrows = list_off[li + 1] - r0;
     if (chunk_off[li] > item || pc >= np || nrows == 0) return;  // past the last item
     const uint32_t m = np - pc < (uint32_t)IVF_QC ? np - pc : (uint32_t)IVF_QC;
-    for (uint32_t i = tid; i < (uint32_t)UNITS * 32; i += 256) {
+    for (uint32_t i = tid; i < (uint32_t)UNITS * 32; i += IVF_LM_WAVES * 64) {
         const uint32_t u = i / 32, col = i % 32, k = col % 8, l = col / 8;
         v4i v{};
         if (l < 3 && k < m) v = ((const v4i *)(qlev + (uint64_t)pair_q[p0 + pc + k] * qstride))[3 * u + l];
@@ -1468,7 +1469,7 @@ __global__ __launch_bounds__(256) void ivf_list_mfma(const uint32_t *codes, cons
     __syncthreads();
     const uint32_t wave = tid >> 6, lane = tid & 63, c = lane & 31, h = lane >> 5;
     const uint32_t tiles = (nrows + 31) / 32;
-    for (uint32_t t = wave; t < tiles; t += 4) {
+    for (uint32_t t = wave; t < tiles; t += IVF_LM_WAVES) {
         const uint32_t ri = t * 32 + c;
         const uint64_t row = list_rows[r0 + (ri < nrows ? ri : nrows - 1)];  // past the end: a valid row, dropped
         v4i A[S];
@@ -1543,11 +1544,11 @@ hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, uint32_t bits
 #define BV_LS_CASE(U)                                                                                             \
     case U:                                                                                                        \
         if (bits == 8)                                                                                             \
-            hipLaunchKernelGGL((ivf_list_mfma<U, 8>), dim3((uint32_t)items), dim3(256), 0, s, codes, scales,      \
+            hipLaunchKernelGGL((ivf_list_mfma<U, 8>), dim3((uint32_t)items), dim3(IVF_LM_WAVES * 64), 0, s, codes, scales, \
                                scale_mul, list_off, list_rows, nlist, chunk_off, pair_off, pair_count, pair_q,    \
                                pair_base, qlev, qstride, cand, cap);                                              \
         else                                                                                                       \
-            hipLaunchKernelGGL((ivf_list_mfma<U, 4>), dim3((uint32_t)items), dim3(256), 0, s, codes, scales,      \
+            hipLaunchKernelGGL((ivf_list_mfma<U, 4>), dim3((uint32_t)items), dim3(IVF_LM_WAVES * 64), 0, s, codes, scales, \
                                scale_mul, list_off, list_rows, nlist, chunk_off, pair_off, pair_count, pair_q,    \
                                pair_base, qlev, qstride, cand, cap);                                              \
         break;
