@@ -1333,6 +1333,8 @@ static void scan_common(const bv_index *idx, const float *d_q, uint64_t n, uint3
         a.rr_q = d_q;
         a.rr_q_stride = idx->dim;
     }
+    // few rows per wave (IVF lists, small corpora): the short tail
+    a.short_tail = n < SHORT_TAIL_ROWS * grid * (SCAN_WG / 64);
 }
 
 // The fused single-launch scan (one query per grid row): query transform,

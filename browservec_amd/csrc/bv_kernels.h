@@ -97,7 +97,15 @@ struct ScanArgs {
     uint32_t *out_rows;       // [nq][k_out]
     float *out_scores;
     uint32_t *out_n;          // [nq]
+    uint32_t short_tail;      // few rows per wave: every pass polls the shared bound, the flush takes
+                              // a fresh read of it, and the final gather is bounded by the wave maxima
 };
+
+// Rows per wave below which a scan takes the short tail (a wave then scans
+// too few steps for the threshold helper's bound to reach it through the
+// usual polling, so a flush by the wave's own bound would carry, and
+// exactly re-score, most of its rows).
+constexpr uint64_t SHORT_TAIL_ROWS = 256;
 
 struct EncodeArgs {
     const float *src;         // rows x dim

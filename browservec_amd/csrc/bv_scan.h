@@ -842,45 +842,44 @@ template <int E> struct RotIn {
     float s[2][E];
 };
 
+// Every load is unconditional, of a clamped address (rounds >= 1, and the
+// sign table has rounds x P entries): a load under a condition makes the
+// compiler wait for it (and, the load counter draining in order, for every
+// older load) where the two paths join, instead of where the value is first
+// used.  The values are masked at first use, in rotate_apply.
 template <int E>
 __device__ __forceinline__ void rotate_load(const float *src, uint32_t dim, uint32_t P, const float *signs,
                                             uint32_t rounds, RotIn<E> &in, int lane) {
-    const uint32_t lanes_used = P / E;
     const uint32_t e0 = lane * E;
-    const bool active = (uint32_t)lane < lanes_used;
 #pragma unroll
     for (int t = 0; t < E; ++t) {
         const uint32_t e = e0 + t;
-        in.x[t] = (active && e < dim) ? src[e] : 0.0f;
+        in.x[t] = src[e < dim ? e : dim - 1];
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
+        const uint32_t rr = (uint32_t)r < rounds ? (uint32_t)r : 0u;
 #pragma unroll
-        for (int t = 0; t < E; ++t) in.s[r][t] = (active && (uint32_t)r < rounds) ? signs[(size_t)r * P + e0 + t] : 0.0f;
+        for (int t = 0; t < E; ++t) {
+            const uint32_t e = e0 + t;
+            in.s[r][t] = signs[(size_t)rr * P + (e < P ? e : P - 1)];
+        }
     }
 }
 
+// The rounds: the first two from the signs loaded up front, any further ones
+// (never by default) from a load of their own, in a loop of their own so that
+// no wait for it lands on the common path.
 template <int E>
-__device__ __forceinline__ void rotate_apply(RotIn<E> &in, uint32_t P, const float *signs, uint32_t rounds,
-                                             float (&x)[E], int lane) {
+__device__ __forceinline__ void rotate_apply(RotIn<E> &in, uint32_t dim, uint32_t P, const float *signs,
+                                             uint32_t rounds, float (&x)[E], int lane) {
 #pragma clang fp contract(off)
     const uint32_t lanes_used = P / E;
     const uint32_t e0 = lane * E;
     const bool active = (uint32_t)lane < lanes_used;
 #pragma unroll
-    for (int t = 0; t < E; ++t) x[t] = in.x[t];
-    for (uint32_t r = 0; r < rounds; ++r) {
-        float sg[E];
-        if (r == 0) {
-#pragma unroll
-            for (int t = 0; t < E; ++t) sg[t] = in.s[0][t];
-        } else if (r == 1) {
-#pragma unroll
-            for (int t = 0; t < E; ++t) sg[t] = in.s[1][t];
-        } else {
-#pragma unroll
-            for (int t = 0; t < E; ++t) sg[t] = signs[(size_t)r * P + e0 + t];
-        }
+    for (int t = 0; t < E; ++t) x[t] = (active && e0 + t < dim) ? in.x[t] : 0.0f;
+    auto one_round = [&](const float (&sg)[E]) {
 #pragma unroll
         for (int t = 0; t < E; ++t) x[t] = active ? x[t] * sg[t] : 0.0f;
 #pragma unroll
@@ -906,6 +905,17 @@ __device__ __forceinline__ void rotate_apply(RotIn<E> &in, uint32_t P, const flo
                 }
             }
         }
+    };
+    one_round(in.s[0]);
+    if (rounds > 1) one_round(in.s[1]);
+    for (uint32_t r = 2; r < rounds; ++r) {
+        float sg[E];
+#pragma unroll
+        for (int t = 0; t < E; ++t) {
+            const uint32_t e = e0 + t;
+            sg[t] = signs[(size_t)r * P + (e < P ? e : P - 1)];
+        }
+        one_round(sg);
     }
 }
 
@@ -914,7 +924,7 @@ __device__ __forceinline__ void rotate_wave(const float *src, uint32_t dim, uint
                                             uint32_t rounds, float (&x)[E], int lane) {
     RotIn<E> in;
     rotate_load<E>(src, dim, P, signs, rounds, in, lane);
-    rotate_apply<E>(in, P, signs, rounds, x, lane);
+    rotate_apply<E>(in, dim, P, signs, rounds, x, lane);
 }
 
 // quantizeRow8 / quantizeRow4 / quantizeRow1 of a rotated row held by the
@@ -1294,7 +1304,7 @@ template <int C, int E>
 __device__ __forceinline__ void prep_query_e(const ScanArgs &a, RotIn<E> &in, unsigned char *lds, int lane) {
     const uint32_t P = a.padded_dim;
     float x[E];
-    rotate_apply<E>(in, P, a.signs, a.rounds, x, lane);
+    rotate_apply<E>(in, a.qdim, P, a.signs, a.rounds, x, lane);
     const size_t lay = query_layout_bytes(C, P);
     if constexpr (C == C_Q8 || C == C_Q4) {
         levels_wave<E>(x, P, C, (signed char *)(lds + lay), lds, lane);
@@ -1347,16 +1357,19 @@ template <int EP> struct RotInWG {
 
 __host__ __device__ inline size_t prep_wg_xs_offset(size_t lay) { return (lay + 15) & ~(size_t)15; }
 
+// (unconditional loads of clamped addresses, as in rotate_load; the query
+// is masked by the dimension at first use in prep_query_wg)
 template <int EP>
 __device__ __forceinline__ void rotate_load_wg(const float *src, uint32_t dim, uint32_t P, const float *signs,
                                                uint32_t rounds, RotInWG<EP> &in, int tid) {
     const uint32_t e0 = (uint32_t)tid * EP;  // quarter of wave w starts at w*64*EP = (tid - lane)*EP
 #pragma unroll
-    for (int t = 0; t < EP; ++t) in.x[t] = e0 + t < dim ? src[e0 + t] : 0.0f;
+    for (int t = 0; t < EP; ++t) in.x[t] = src[e0 + t < dim ? e0 + t : dim - 1];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
+        const uint32_t rr = (uint32_t)r < rounds ? (uint32_t)r : 0u;
 #pragma unroll
-        for (int t = 0; t < EP; ++t) in.s[r][t] = (uint32_t)r < rounds ? signs[(size_t)r * P + e0 + t] : 0.0f;
+        for (int t = 0; t < EP; ++t) in.s[r][t] = signs[(size_t)rr * P + e0 + t];
     }
 }
 
@@ -1370,19 +1383,10 @@ __device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in
     float *xs = (float *)(lds + prep_wg_xs_offset(lay));
     float x[EP];
 #pragma unroll
-    for (int t = 0; t < EP; ++t) x[t] = in.x[t];
-    for (uint32_t r = 0; r < a.rounds; ++r) {
-        float sg[EP];
-        if (r == 0) {
-#pragma unroll
-            for (int t = 0; t < EP; ++t) sg[t] = in.s[0][t];
-        } else if (r == 1) {
-#pragma unroll
-            for (int t = 0; t < EP; ++t) sg[t] = in.s[1][t];
-        } else {
-#pragma unroll
-            for (int t = 0; t < EP; ++t) sg[t] = a.signs[(size_t)r * P + e0 + t];
-        }
+    for (int t = 0; t < EP; ++t) x[t] = e0 + t < a.qdim ? in.x[t] : 0.0f;
+    // the rounds, as in rotate_apply: the first two from the signs loaded up
+    // front, further ones in a loop of their own
+    auto one_round = [&](const float (&sg)[EP]) {
 #pragma unroll
         for (int t = 0; t < EP; ++t) x[t] = x[t] * sg[t];
 #pragma unroll
@@ -1413,6 +1417,14 @@ __device__ __forceinline__ void prep_query_wg(const ScanArgs &a, RotInWG<EP> &in
 #pragma unroll
         for (int t = 0; t < EP; ++t) x[t] = xs[e0 + t];
         __syncthreads();  // xs is rewritten by the next round
+    };
+    one_round(in.s[0]);
+    if (a.rounds > 1) one_round(in.s[1]);
+    for (uint32_t r = 2; r < a.rounds; ++r) {
+        float sg[EP];
+#pragma unroll
+        for (int t = 0; t < EP; ++t) sg[t] = a.signs[(size_t)r * P + e0 + t];
+        one_round(sg);
     }
     if constexpr (C == C_Q1A) {
         float *f = (float *)lds;
@@ -1632,8 +1644,8 @@ __device__ __forceinline__ uint64_t exact_key_lanes4(const float *x, const doubl
 
 // ------------------------------------------------------------ scan + top-k --
 constexpr uint32_t TAU_POLL = 4;     // step pairs between reads of the shared bound
-constexpr uint32_t STATIC_PCT = 80;  // share of the grabs assigned statically
-constexpr uint32_t DSTEPS = 4;       // steps per dynamically assigned chunk
+constexpr uint32_t STATIC_PCT = 70;  // share of the grabs assigned statically
+constexpr uint32_t DSTEPS = 6;       // steps per dynamically assigned chunk
 
 // A unit slot past the end of a row (layouts whose lanes overhang the row)
 // must contribute nothing: zero query values do that for the dot-style codecs;
@@ -1734,6 +1746,9 @@ __device__ __forceinline__ void load_step(const ScanArgs &a, const ScanRegs<C, U
     const uint32_t myrow = base + (uint32_t)(xrow<U, LPR>(lane) * G + slot);
     const uint32_t myrc = myrow < lim ? myrow : lim - 1;
     S.grow = IDX ? cand[myrc] : (uint32_t)myrc;
+    // (a runtime condition: the unconditional form for the scaled codecs,
+    // which lets the compiler schedule the load among the code loads,
+    // measured 3.4 us slower per 1M-row int8 query)
     S.scale = a.scales ? load_stream(a.scales + S.grow) : 1.0f;
 }
 
@@ -1989,7 +2004,7 @@ __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
 // helper.  At the end every wave flushes its keys at or above the freshest
 // bound to a global array; the last workgroup to finish selects the best
 // kprime of the flushes.  Dynamic LDS: max(sizeof(TopkLds), 4 * wcap * 8).
-template <int C, int LPR, int UPL, bool IDX>
+template <int C, int LPR, int UPL, bool IDX, bool PREP>
 __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     using CD = Codec<C>;
     using QT = typename CD::QT;
@@ -2151,12 +2166,11 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     using PW = PrepWG<C, LPR, UPL>;
     RotIn<(PS::ok && !PW::ok) ? PS::E : 1> rin;
     RotInWG<PW::EP> rinw;
-    const bool prep = PS::ok && a.qraw != nullptr;
     const float *qsrc = a.qraw + (uint64_t)qi * a.qdim;
-    if constexpr (PW::ok) {
-        if (prep) rotate_load_wg<PW::EP>(qsrc, a.qdim, a.padded_dim, a.signs, a.rounds, rinw, tid);
-    } else if constexpr (PS::ok) {
-        if (prep && wave == 0) rotate_load<PS::E>(qsrc, a.qdim, a.padded_dim, a.signs, a.rounds, rin, lane);
+    if constexpr (PREP && PW::ok) {
+        rotate_load_wg<PW::EP>(qsrc, a.qdim, a.padded_dim, a.signs, a.rounds, rinw, tid);
+    } else if constexpr (PREP && PS::ok) {
+        if (wave == 0) rotate_load<PS::E>(qsrc, a.qdim, a.padded_dim, a.signs, a.rounds, rin, lane);
     }
     // The first two steps' code loads need no query: both go out before the
     // query transform, so the memory system stays busy while it runs.  Every
@@ -2181,12 +2195,12 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         }
         R.fin.load((const char *)qb + (uint64_t)a.units * CD::QN * sizeof(QT), a.padded_dim);
     };
-    if (!prep) read_query((const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride));
+    if constexpr (!PREP) read_query((const QT *)((const char *)a.q + (uint64_t)qi * a.q_stride));
     if constexpr (C == C_Q1P) {
         // the exact re-score table, in LDS behind everything else (built by
         // the query transform, or here from the prepared fp32 query)
         R.qf = (const float *)(scan_smem + a.qf_off);
-        if (!prep) {
+        if constexpr (!PREP) {
             const float *src = (const float *)((const char *)a.q + (uint64_t)qi * a.q_stride + q1p_f_off(a.padded_dim));
             q1p_lut_build(src, a.padded_dim, (float *)(scan_smem + a.qf_off), (uint32_t)tid, SCAN_WG);
             __syncthreads();
@@ -2198,6 +2212,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     // with its row loads.
     constexpr int RQ = 16;
     const uint32_t rvec = a.rr_dim & ~3u;
+    const bool stail = a.short_tail != 0;
     const bool stage_q = a.rr_src != nullptr && rvec <= 64 * RQ;
     float rqv[RQ];
     if (stage_q) {
@@ -2208,29 +2223,63 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             rqv[k] = rq[i < rvec ? i : rvec - 1];  // (clamped: every lane loads)
         }
     }
-    const bool any = n > 0;
-    bool ha = any && next_step(ab, al);
-    if (PIPE && any) load_step<C, LPR, UPL, IDX>(a, R, cand, ha ? ab : 0, ha ? al : 1, A, lane);
-    bool hb = PIPE && ha && next_step(bb, bl);
-    if (PIPE && any) load_step<C, LPR, UPL, IDX>(a, R, cand, hb ? bb : 0, hb ? bl : 1, B, lane);
-
-    if (prep) {
-        if constexpr (PW::ok) {
-            prep_query_wg<C, PW::EP>(a, rinw, scan_smem, tid);
-        } else if constexpr (PS::ok) {
-            if (wave == 0) prep_query_e<C, PS::E>(a, rin, scan_smem, lane);
+    // The query transform and the re-rank query's staging, after the first
+    // two steps' loads are issued.  The code is repeated on three paths
+    // (straight-line first steps, the general first steps, no rows) rather
+    // than placed after their join: at a join of paths that issued
+    // different loads the compiler waits for every load in flight, which
+    // would make the transform wait for both steps' codes.
+    auto prologue = [&]() {
+        if constexpr (PREP) {
+            if constexpr (PW::ok) {
+                prep_query_wg<C, PW::EP>(a, rinw, scan_smem, tid);
+            } else if constexpr (PS::ok) {
+                if (wave == 0) prep_query_e<C, PS::E>(a, rin, scan_smem, lane);
+            }
+            __syncthreads();
+            read_query((const QT *)scan_smem);
+            __syncthreads();  // the LDS holding it becomes the waves' lists
         }
-        __syncthreads();
-        read_query((const QT *)scan_smem);
-        __syncthreads();  // the LDS holding it becomes the waves' lists
-    }
-    if (stage_q) {
-        double *qd = (double *)(wk + wcap);
+        if (stage_q) {
+            double *qd = (double *)(wk + wcap);
 #pragma unroll
-        for (int k = 0; k < RQ; ++k) {
-            const uint32_t i = (uint32_t)lane + 64u * k;
-            if (i < rvec) qd[i] = (double)rqv[k];
+            for (int k = 0; k < RQ; ++k) {
+                const uint32_t i = (uint32_t)lane + 64u * k;
+                // (the empty asm keeps the conversion, and the wait for the
+                // load, here: hoisted to the load it would wait before the
+                // first code load is issued)
+                float r = rqv[k];
+                asm volatile("" : "+v"(r));
+                if (i < rvec) qd[i] = (double)r;
+            }
         }
+    };
+    bool ha = false, hb = false;
+    static_assert(SH::GRAB_STEPS == 2, "the straight-line first steps are one grab's two steps");
+    if (PIPE && sgrabs > 0) {
+        // the workgroup's first static grab is full: the wave's first two
+        // steps are its two steps in that grab (next_step's state moves on
+        // to the second grab)
+        const uint32_t r0 = blockIdx.x * SH::GRAB_ROWS;
+        ab = r0 + wofs;
+        al = r0 + SH::GRAB_ROWS;
+        bb = ab + wstep;
+        bl = al;
+        gi = 1;
+        ha = hb = true;
+        load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
+        load_step<C, LPR, UPL, IDX>(a, R, cand, bb, bl, B, lane);
+        __builtin_amdgcn_sched_barrier(0);  // every load issued before the transform's first use of the query
+        prologue();
+    } else if (n > 0) {
+        ha = next_step(ab, al);
+        if (PIPE) load_step<C, LPR, UPL, IDX>(a, R, cand, ha ? ab : 0, ha ? al : 1, A, lane);
+        hb = PIPE && ha && next_step(bb, bl);
+        if (PIPE) load_step<C, LPR, UPL, IDX>(a, R, cand, hb ? bb : 0, hb ? bl : 1, B, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        prologue();
+    } else {
+        prologue();
     }
     uint64_t gt = 0;      // what the previous pass read: the shared bound when it polled
     bool polled = false;
@@ -2253,7 +2302,8 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             publish_wave_max(wslot, lmax);
             // (the bit-plane scan polls every pass until a bound exists: its
             // rows go through the exact re-score until then)
-            polled = (C == C_Q1P && tau == 0) || (pi + (uint32_t)wave) % TAU_POLL == 0;
+            // (a short scan polls every pass: its waves run only a few)
+            polled = stail || (C == C_Q1P && tau == 0) || (pi + (uint32_t)wave) % TAU_POLL == 0;
             gt = __hip_atomic_load(polled ? (const uint64_t *)&qs->tau : (const uint64_t *)wslot, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             const bool nb = na && next_step(bb, bl);
@@ -2294,6 +2344,10 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             const uint64_t ugt = uniform_u64(gt);
             tau = ugt > tau ? ugt : tau;
         }
+    }
+    if (stail) {  // a short scan flushes by a fresh read: the helper's bound has had the whole scan to form
+        const uint64_t g = load_tau(qs);
+        tau = g > tau ? g : tau;
     }
     wc = wave_filter(wk, wc, tau, lane);
     // Flushed entries are (scan key, exact key) pairs; with re-ranking on,
@@ -2391,6 +2445,37 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     __syncthreads();
     const uint32_t total = L.ovl[32 + ng];
     constexpr uint32_t CHUNK = SCAN_CAP / 2;
+    if (stail && total > CHUNK) {
+        // A short scan whose flushes overflow the one-pass gather (the
+        // helper's bound formed late): the gather is bounded first by the
+        // kp-th best wave maximum.  The maxima of distinct waves are distinct
+        // rows' keys, so kp rows score at least that much and it is at most
+        // the kp-th best key.  Every wave published the maximum over all its
+        // rows before its workgroup took a ticket.
+        const uint32_t nslots = a.grid * (SCAN_WG / 64);
+        const uint64_t *wm = a.wmax + (uint64_t)qi * nslots;
+        for (uint32_t i0 = 0; i0 < nslots; i0 += 8 * SCAN_WG) {
+            uint64_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t i = i0 + j * SCAN_WG + tid;
+                v[j] = i < nslots ? load_shared(&wm[i]) : 0ull;
+            }
+            // (beyond SCAN_CAP maxima are dropped: the kp-th best of a
+            // subset is a valid bound too)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) wave_append(L.keys, &L.cnt, SCAN_CAP, v[j] != 0, v[j], lane);
+        }
+        __syncthreads();
+        const uint32_t nm = L.cnt < (uint32_t)SCAN_CAP ? L.cnt : (uint32_t)SCAN_CAP;
+        if (nm > kp) {
+            const uint32_t m0 = select_topk(L, nm, kp);
+            if (tid == 0 && L.keys[m0 - 1] > L.tau) L.tau = L.keys[m0 - 1];
+        }
+        __syncthreads();
+        if (tid == 0) L.cnt = 0;
+        __syncthreads();
+    }
     if (a.rr_src && total <= CHUNK) {
         // Re-rank, common case: one pass gathers the (scan key, exact key)
         // pairs at or above the bound; the fetch is the best kp scan keys,
@@ -2633,10 +2718,19 @@ hipError_t go(const ScanArgs &a, uint32_t nq, hipStream_t s) {
         lds += q1p_lut_bytes(a.padded_dim);
     }
     if (lds > 160 * 1024) return hipErrorInvalidValue;
-    if (a.cand)
-        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, true>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, b);
-    else
-        hipLaunchKernelGGL((scan_topk<C, LPR, UPL, false>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, b);
+
+    constexpr bool PP = PrepShape<C, LPR, UPL>::ok;  // layouts that can transform the query themselves
+    if (a.cand) {
+        if (PP && a.qraw)
+            hipLaunchKernelGGL((scan_topk<C, LPR, UPL, true, PP>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, b);
+        else
+            hipLaunchKernelGGL((scan_topk<C, LPR, UPL, true, false>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, b);
+    } else {
+        if (PP && a.qraw)
+            hipLaunchKernelGGL((scan_topk<C, LPR, UPL, false, PP>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, b);
+        else
+            hipLaunchKernelGGL((scan_topk<C, LPR, UPL, false, false>), dim3(a.grid + 1, nq), dim3(SCAN_WG), lds, s, b);
+    }
     return hipGetLastError();
 }
 
