@@ -40,6 +40,7 @@ struct bv_device {
     hipDeviceProp_t prop{};
     bool lost = false;
     bool inject_append_oom = false;  // bv_debug_inject: fail the next append's allocation
+    bool inject_append_late = false; // bv_debug_inject: fail the next append after its rows are encoded
     void *scratch = nullptr;         // this GPU's copy of the no-allocation scratch array
 };
 
@@ -198,6 +199,7 @@ struct bv_index {
     DevBuf list_off2, list_rows2;             // incremental appends: the extended lists, swapped in
     std::vector<uint32_t> list_sizes_desc;    // host: list sizes, largest first
     DevBuf ivf_idx, ivf_idx2, ivf_slot, ivf_assign, ivf_hist, ivf_base, ivf_totals, ivf_toff, ivf_trows;
+    DevBuf ivf_pend;  // an append's sampled rows (rotated), scattered into `sample` once nothing can fail
     DevBuf probe_scores, probes, cand_tot, cand_off;
     double build_ms = 0;
     double last_query_ms = 0, last_query_gpu_ms = 0;
@@ -262,6 +264,7 @@ extern "C" int bv_debug_inject(bv_device *dev, int what) {
     switch (what) {
     case BV_INJECT_LOST: dev->lost = true; return BV_OK;
     case BV_INJECT_APPEND_OOM: dev->inject_append_oom = true; return BV_OK;
+    case BV_INJECT_APPEND_LATE: dev->inject_append_late = true; return BV_OK;
     default: return fail(BV_E_INVALID, "unknown injection %d", what);
     }
 }
@@ -491,7 +494,7 @@ static void ivf_plan(const bv_index *idx, uint64_t count, ReservoirPlan &pl) {
     }
 }
 
-static void ivf_commit(bv_index *idx, uint64_t base, const ReservoirPlan &pl) {
+static void ivf_commit(bv_index *idx, uint64_t base, const ReservoirPlan &pl, bool extended) {
     idx->sample_filled = pl.filled;
     idx->sample_seen = pl.seen;
     idx->sample_rng = pl.rng;
@@ -499,15 +502,17 @@ static void ivf_commit(bv_index *idx, uint64_t base, const ReservoirPlan &pl) {
     for (uint64_t i = 0; i < pl.slots.size(); ++i)
         if (pl.slots[i] >= 0) idx->sample_row[(uint32_t)pl.slots[i]] = base + i;
     // lists are stale after any append (ivfquant.ts:462), unless the append
-    // extends them (incremental mode, lists current before it)
-    if (!(idx->d.ivf_incremental && idx->built_rows == base && idx->nlist)) idx->built_rows = ~0ull;
+    // extended them (incremental mode, lists current before it)
+    if (!extended) idx->built_rows = ~0ull;
 }
 
 // Incremental append: rows [base, base + count) assigned to the current
 // centroids with the build's final-assignment arithmetic, then merged into
 // the lists (each list: its rows, then the new ones, ascending).  The lists
 // equal those a final assignment over every row with these centroids gives.
-static int ivf_extend_lists(bv_index *idx, uint64_t base, uint64_t count) {
+// The buffers ivf_extend_lists uses, allocated before an append changes
+// anything.
+static int ivf_extend_reserve(bv_index *idx, uint64_t base, uint64_t count) {
     const uint32_t nlist = idx->nlist;
     hipStream_t s = idx->stream;
     const uint32_t nblk = ivf_list_blocks(count);
@@ -519,6 +524,14 @@ static int ivf_extend_lists(bv_index *idx, uint64_t base, uint64_t count) {
     HIPX(idx->dev, idx->ivf_trows.ensure(count * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->list_off2.ensure(((size_t)nlist + 1) * 4, 0, s), "lists");
     HIPX(idx->dev, idx->list_rows2.ensure((base + count) * 4, 0, s), "lists");
+    return BV_OK;
+}
+
+// Runs on the buffers ivf_extend_reserve allocated; the new lists are built
+// in the second buffers and swapped in at the end.
+static int ivf_extend_lists(bv_index *idx, uint64_t base, uint64_t count) {
+    const uint32_t nlist = idx->nlist;
+    hipStream_t s = idx->stream;
     IvfAssignArgs fa{};
     fa.n = count;
     fa.dim = idx->sample_dim;
@@ -555,56 +568,6 @@ static int ivf_extend_lists(bv_index *idx, uint64_t base, uint64_t count) {
     std::sort(idx->list_sizes_desc.begin(), idx->list_sizes_desc.end(), std::greater<uint32_t>());
     idx->built_rows = base + count;
     idx->retrain_due = true;
-    return BV_OK;
-}
-
-// fp32 IVF: the sampled rows themselves go to their slots.
-static int ivf_sample_raw(bv_index *idx, uint64_t base, const std::vector<int32_t> &slots) {
-    std::vector<uint32_t> src, dst;
-    for (size_t i = 0; i < slots.size(); ++i)
-        if (slots[i] >= 0) {
-            src.push_back((uint32_t)(base + i));
-            dst.push_back((uint32_t)slots[i]);
-        }
-    if (src.empty()) return BV_OK;
-    HIPX(idx->dev, idx->ivf_idx.ensure(src.size() * 4, 0, idx->stream), "scratch");
-    HIPX(idx->dev, idx->ivf_idx2.ensure(dst.size() * 4, 0, idx->stream), "scratch");
-    HIPX(idx->dev, hipMemcpyAsync(idx->ivf_idx.p, src.data(), src.size() * 4, hipMemcpyHostToDevice, idx->stream),
-         "upload");
-    HIPX(idx->dev, hipMemcpyAsync(idx->ivf_idx2.p, dst.data(), dst.size() * 4, hipMemcpyHostToDevice, idx->stream),
-         "upload");
-    IvfCopyArgs c{};
-    c.src = idx->raw.as<float>();
-    c.src_stride = idx->dim;
-    c.src_idx = idx->ivf_idx.as<uint32_t>();
-    c.dst = idx->sample.as<float>();
-    c.dst_stride = idx->sample_dim;
-    c.dst_idx = idx->ivf_idx2.as<uint32_t>();
-    c.n = (uint32_t)src.size();
-    c.dim = idx->dim;
-    HIPX(idx->dev, ivf_launch_copy_rows(c, idx->stream), "sample copy");
-    HIPX(idx->dev, hipStreamSynchronize(idx->stream), "sample copy");
-    return BV_OK;
-}
-
-// Rotate+quantize rows [first, first+count) from the device row buffer.
-static int encode_range(bv_index *idx, uint64_t first, uint64_t count, const int32_t *d_sample_slot = nullptr) {
-    EncodeArgs a{};
-    a.src = idx->raw.as<float>() + first * idx->dim;
-    a.rows = count;
-    a.dim = idx->dim;
-    a.P = idx->P;
-    a.signs = idx->signs.as<float>();
-    a.rounds = idx->d.rounds;
-    a.bits = idx->d.bits;
-    a.codes = idx->codes.as<uint32_t>() + first * idx->words_per_row;
-    a.scales = idx->scales.as<float>() + first;
-    a.slow_rows = idx->slow.as<uint32_t>();
-    if (d_sample_slot) {
-        a.sample_slot = d_sample_slot;
-        a.sample = idx->sample.as<float>();
-    }
-    HIPX(idx->dev, launch_encode(a, idx->stream), "encode kernel");
     return BV_OK;
 }
 
@@ -679,8 +642,13 @@ static int stage_rows(bv_index *idx, const float *src, uint64_t r0, uint64_t m, 
 }
 
 // Append: every allocation happens first, so a failure (or an injected one)
-// leaves the index exactly as it was; then the rows are copied, the reservoir
-// plan is committed and the rows are encoded.
+// leaves the index exactly as it was; then the rows are copied and encoded
+// into space past the index's rows.  The rows an IVF reservoir samples go to
+// a staging buffer, not to their slots, so a failure at any point before the
+// commit (a later staged chunk, an injected late failure) leaves the sample,
+// the reservoir state and the lists as they were; the commit scatters the
+// sampled rows, extends the lists (incremental mode) and advances the
+// reservoir.
 static int append_common(bv_index *idx, const float *data, bool device_src, uint64_t count) {
     const uint64_t base = idx->rows, total = base + count;
     const size_t rb = (size_t)idx->dim * 4;
@@ -691,7 +659,20 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
         return fail(BV_E_OOM, "row buffer: out of device memory");
     }
     ReservoirPlan plan;
-    if (idx->ivf) ivf_plan(idx, count, plan);
+    std::vector<int32_t> pend_slot;         // per appended row: its staging row, or -1
+    std::vector<uint32_t> src_row, dst_slot;  // the scatter: staging (or raw) row -> reservoir slot
+    if (idx->ivf) {
+        ivf_plan(idx, count, plan);
+        pend_slot.assign(count, -1);
+        for (uint64_t i = 0; i < count; ++i)
+            if (plan.slots[i] >= 0) {
+                pend_slot[i] = (int32_t)dst_slot.size();
+                src_row.push_back(idx->quant ? (uint32_t)dst_slot.size() : (uint32_t)(base + i));
+                dst_slot.push_back((uint32_t)plan.slots[i]);
+            }
+    }
+    const size_t taken = dst_slot.size();
+    const bool extend = idx->ivf && idx->built_rows == base && idx->nlist && idx->d.ivf_incremental;
     HIPX(idx->dev, idx->raw.ensure(total * rb, base * rb, idx->stream), "row buffer");
     if (idx->quant) {
         HIPX(idx->dev, idx->codes.ensure(total * idx->row_bytes, base * idx->row_bytes, idx->stream), "code buffer");
@@ -705,11 +686,14 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
         HIPX(idx->dev, idx->sample.ensure(plan.filled * (size_t)idx->sample_dim * 4, idx->sample.cap, idx->stream),
              "sample buffer");
         HIPX(idx->dev, idx->ivf_slot.ensure(count * 4, 0, idx->stream), "scratch");
-        if (!idx->quant) {  // fp32 kinds copy the sampled rows by index lists
-            size_t taken = 0;
-            for (int32_t s : plan.slots) taken += s >= 0;
-            HIPX(idx->dev, idx->ivf_idx.ensure(std::max<size_t>(taken, 1) * 4, 0, idx->stream), "scratch");
-            HIPX(idx->dev, idx->ivf_idx2.ensure(std::max<size_t>(taken, 1) * 4, 0, idx->stream), "scratch");
+        HIPX(idx->dev, idx->ivf_idx.ensure(std::max<size_t>(taken, 1) * 4, 0, idx->stream), "scratch");
+        HIPX(idx->dev, idx->ivf_idx2.ensure(std::max<size_t>(taken, 1) * 4, 0, idx->stream), "scratch");
+        if (idx->quant)
+            HIPX(idx->dev, idx->ivf_pend.ensure(std::max<size_t>(taken, 1) * idx->sample_dim * 4, 0, idx->stream),
+                 "sample staging buffer");
+        if (extend) {
+            int rc = ivf_extend_reserve(idx, base, count);
+            if (rc) return rc;
         }
     }
     const bool staged = !device_src && count * rb > UPLOAD_CHUNK && !host_pinned(data);
@@ -724,11 +708,18 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
     }
     if (idx->ivf) {
         HIPX(idx->dev,
-             hipMemcpyAsync(idx->ivf_slot.p, plan.slots.data(), count * 4, hipMemcpyHostToDevice, idx->stream),
+             hipMemcpyAsync(idx->ivf_slot.p, pend_slot.data(), count * 4, hipMemcpyHostToDevice, idx->stream),
              "upload");
+        if (taken) {
+            HIPX(idx->dev, hipMemcpyAsync(idx->ivf_idx.p, src_row.data(), taken * 4, hipMemcpyHostToDevice, idx->stream),
+                 "upload");
+            HIPX(idx->dev,
+                 hipMemcpyAsync(idx->ivf_idx2.p, dst_slot.data(), taken * 4, hipMemcpyHostToDevice, idx->stream),
+                 "upload");
+        }
     }
-    const bool extend = idx->ivf && idx->built_rows == base && idx->nlist && idx->d.ivf_incremental;
     // the rows in chunks (one chunk unless staged): upload, norms, encode
+    // (sampled rows' rotations into the staging buffer)
     const uint64_t crow = staged ? std::max<uint64_t>(1, UPLOAD_CHUNK / rb) : count;
     for (uint64_t off = 0, i = 0; off < count; off += crow, ++i) {
         const uint64_t m = std::min(crow, count - off), r0 = base + off;
@@ -746,8 +737,22 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
                                     idx->rsq_max.as<uint32_t>(), idx->stream),
                  "norm kernel");
         if (idx->quant) {
-            int rc = encode_range(idx, r0, m, idx->ivf ? idx->ivf_slot.as<int32_t>() + off : nullptr);
-            if (rc) return rc;
+            EncodeArgs e{};
+            e.src = idx->raw.as<float>() + r0 * idx->dim;
+            e.rows = m;
+            e.dim = idx->dim;
+            e.P = idx->P;
+            e.signs = idx->signs.as<float>();
+            e.rounds = idx->d.rounds;
+            e.bits = idx->d.bits;
+            e.codes = idx->codes.as<uint32_t>() + r0 * idx->words_per_row;
+            e.scales = idx->scales.as<float>() + r0;
+            e.slow_rows = idx->slow.as<uint32_t>();
+            if (idx->ivf) {
+                e.sample_slot = idx->ivf_slot.as<int32_t>() + off;
+                e.sample = idx->ivf_pend.as<float>();
+            }
+            HIPX(idx->dev, launch_encode(e, idx->stream), "encode kernel");
             if (code_norms)
                 HIPX(idx->dev,
                      launch_row_code_norms(idx->codes.as<uint32_t>() + r0 * idx->words_per_row, m,
@@ -755,15 +760,29 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
                      "norm kernel");
         }
     }
-    if (idx->ivf) ivf_commit(idx, base, plan);
-    if (!idx->quant && idx->ivf) {
-        int rc = ivf_sample_raw(idx, base, plan.slots);
-        if (rc) return rc;
+    if (idx->dev->inject_append_late) {  // (tests: a failure after the rows are encoded)
+        idx->dev->inject_append_late = false;
+        (void)hipStreamSynchronize(idx->stream);
+        return fail(BV_E_HIP, "append: injected failure after the rows were encoded");
+    }
+    // commit: sampled rows to their reservoir slots, lists, reservoir state
+    if (taken) {
+        IvfCopyArgs c{};
+        c.src = idx->quant ? idx->ivf_pend.as<float>() : idx->raw.as<float>();
+        c.src_stride = idx->quant ? idx->sample_dim : idx->dim;
+        c.src_idx = idx->ivf_idx.as<uint32_t>();
+        c.dst = idx->sample.as<float>();
+        c.dst_stride = idx->sample_dim;
+        c.dst_idx = idx->ivf_idx2.as<uint32_t>();
+        c.n = (uint32_t)taken;
+        c.dim = idx->quant ? idx->sample_dim : idx->dim;
+        HIPX(idx->dev, ivf_launch_copy_rows(c, idx->stream), "sample copy");
     }
     if (extend) {
         int rc = ivf_extend_lists(idx, base, count);
         if (rc) return rc;
     }
+    if (idx->ivf) ivf_commit(idx, base, plan, extend);
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "append");
     idx->rows = total;
     return lanes_mark(idx);

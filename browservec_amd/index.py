@@ -63,9 +63,11 @@ class DeviceContext:
         return {"name": name.value.decode(), "cu_count": cu.value, "hbm_bytes": hbm.value}
 
     def debug_inject(self, what: str) -> None:
-        """Force the device-lost state ('lost') or a failed allocation on the
-        next append ('append_oom') from the host; no device work happens."""
-        L.check(self.lib.bv_debug_inject(self.handle, {"lost": 1, "append_oom": 2}[what]))
+        """Force the device-lost state ('lost'), a failed allocation on the
+        next append ('append_oom') or a failure of the next append after its
+        rows are encoded ('append_late') from the host; no device work is made
+        to fail."""
+        L.check(self.lib.bv_debug_inject(self.handle, {"lost": 1, "append_oom": 2, "append_late": 3}[what]))
 
     def destroy(self) -> None:
         if self.handle:

@@ -133,6 +133,8 @@ int bv_device_is_lost(const bv_device *dev, int *lost);
  * conditions without touching the GPU. */
 #define BV_INJECT_LOST 1       /* mark the device lost: every later call fails with BV_E_DEVICE_LOST */
 #define BV_INJECT_APPEND_OOM 2 /* the next append fails as if a device allocation failed; the index is unchanged */
+#define BV_INJECT_APPEND_LATE 3 /* the next append fails after its rows are uploaded and encoded, before its
+                                 * reservoir sample and lists are committed; the index is unchanged */
 int bv_debug_inject(bv_device *dev, int what);
 /* Device name, compute-unit count and HBM size. */
 int bv_device_info(const bv_device *dev, char *name, uint32_t name_len, uint32_t *cu_count, uint64_t *hbm_bytes);
@@ -164,9 +166,10 @@ int bv_index_query_masked(bv_index *idx, const float *q, uint32_t k, const uint3
                           uint64_t n_words, uint32_t *rows, float *scores, uint32_t *n_out);
 
 /* queryBatch (src/index.ts:499-501): nq queries (nq*dim floats); results
- * row-major [nq][k], n_out[nq].  Equal to looping bv_index_query (8 or more
- * queries on a flat fp32 dot/cosine index run on the matrix cores and agree
- * with single queries to fp32 rounding: rows may differ at near-ties). */
+ * row-major [nq][k], n_out[nq].  Equal to looping bv_index_query: rows and
+ * score bits (8 or more queries on a flat fp32 or int8 / int4 index run on
+ * the matrix cores as a prefilter; the rows it keeps are scored with the
+ * single-query arithmetic). */
 int bv_index_query_batch(bv_index *idx, const float *queries, uint32_t nq, uint32_t k, uint32_t *rows,
                          float *scores, uint32_t *n_out);
 

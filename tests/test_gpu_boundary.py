@@ -6,7 +6,9 @@
     (src/index/flat.ts:137) and the row count stays as it was;
   * a failed append allocation (src/index/quant.ts:129-140 appends are
     all-or-nothing): the index, its reservoir included, is unchanged, and a
-    retried append gives the same index as if the failure never happened."""
+    retried append gives the same index as if the failure never happened;
+  * an append that fails after its rows were encoded: the reservoir sample
+    and the incrementally extended IVF lists are unchanged too."""
 
 import numpy as np
 import pytest
@@ -127,4 +129,55 @@ def test_two_query_streams_equal_one(kind):
     assert (got[2] >= n).all()  # the appended copies of query 2 win its top 10
     idx.set_query_streams(1)
     idx.destroy()
+    ctx.destroy()
+
+
+@pytest.mark.parametrize("bits", [8, 0])
+def test_late_append_failure_leaves_sample_and_lists_unchanged(bits):
+    """An append that fails after its rows were uploaded and encoded (a host
+    append staged through pinned buffers in two chunks, failing after both)
+    leaves the IVF reservoir's slots and state and the incrementally
+    extended lists as they were: the index still answers from its old lists,
+    and after the retried append both its extended lists and a rebuild from
+    its reservoir equal those of an index whose append never failed."""
+    need_gpu()
+    from browservec_amd import DeviceContext, IVFIndex, IVFQuantIndex
+    from browservec_amd import _lib as L
+
+    say("inject append late", bits)
+    ctx = DeviceContext(0)
+    dim, n0, n1 = 96, 3000, 200_000  # 200,000 x 96 fp32 = 73 MiB: two staged chunks
+    ivf = {"nlist": 24, "iters": 3, "sampleSize": 1024, "incremental": True}
+    data = clustered(n0 + n1, dim, 40, 0.1, seed=62)
+
+    def make():
+        return IVFQuantIndex(ctx, dim, bits=bits, ivf=ivf) if bits else IVFIndex(ctx, dim, ivf=ivf)
+
+    a = make()
+    a.append(data[:n0], n0)
+    a.build()  # lists current: the next append extends them
+    cen0, off0, rows0 = a.export_ivf()
+    hits0 = [h.row for h in a.query(data[7], 10)]
+    ctx.debug_inject("append_late")
+    with pytest.raises(L.BVError) as e:
+        a.append(data[n0:], n1)
+    assert e.value.code == L.BV_E_HIP and a.size == n0
+    cen1, off1, rows1 = a.export_ivf()
+    assert np.array_equal(cen0.view(np.uint32), cen1.view(np.uint32))
+    assert np.array_equal(off0, off1) and np.array_equal(rows0, rows1)
+    assert [h.row for h in a.query(data[7], 10)] == hits0
+    a.append(data[n0:], n1)  # the retry succeeds
+    b = make()
+    b.append(data[:n0], n0)
+    b.build()
+    b.append(data[n0:], n1)
+    for stage in ("extended lists", "rebuild from the reservoir"):
+        ca, oa, ra = a.export_ivf()
+        cb, ob, rb = b.export_ivf()
+        assert np.array_equal(ca.view(np.uint32), cb.view(np.uint32)), stage
+        assert np.array_equal(oa, ob) and np.array_equal(ra, rb), stage
+        a.build()
+        b.build()
+    a.destroy()
+    b.destroy()
     ctx.destroy()
