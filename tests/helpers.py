@@ -95,3 +95,50 @@ def assert_topk_near(got_rows, ref_scores, k, tol_abs, what=""):
     for r in got ^ want:
         assert abs(float(ref_scores[r]) - kth) <= tol_abs, (
             f"{what}: row {r} differs (score {ref_scores[r]}, k-th {kth})")
+
+
+def fetch_window(approx, ids, fetch: int, tol: float):
+    """The oracle pipeline's fetch (src/index.ts:414-418): the top-`fetch`
+    rows by approximate score, ties by row.  Returns (sure, maybe): `sure`
+    holds the rows whose approximate score exceeds the fetch-th score by more
+    than tol (every scan whose scores are within tol / 2 of the oracle's
+    fetches them), `maybe` the rows within tol of it (a fetch-boundary
+    near-tie: such a scan may or may not fetch them).  Every other row is
+    fetched by no such scan."""
+    approx = np.asarray(approx, np.float64)
+    ids = np.asarray(ids, np.int64)
+    nf = min(fetch, ids.size)
+    order = np.lexsort((ids, -approx))
+    kth = approx[order[nf - 1]]
+    sure = ids[approx > kth + tol]
+    maybe = ids[np.abs(approx - kth) <= tol]
+    return sure, maybe
+
+
+def assert_fetch_rerank(got_rows, got_scores, approx, ids, exact_fn, fetch: int, k: int, tol: float, what=""):
+    """A fetch -> exact re-rank -> top-k answer equals the oracle pipeline's
+    (top-`fetch` by approximate score, exact re-rank, canonical top-k by
+    exact score and row), allowing only fetch-boundary near-ties: rows whose
+    approximate score is within tol of the fetch-th may be in or out of the
+    fetch.  exact_fn(rows) gives the oracle's exact f32 scores.  Fails on a
+    wrong order, a row outside the fetch window, a score that is not the
+    exact score, or a fetched row that beats the last row returned."""
+    got_rows = [int(r) for r in got_rows]
+    sure, maybe = fetch_window(approx, ids, fetch, tol)
+    nf = min(fetch, np.asarray(ids).size)
+    assert len(got_rows) == min(k, nf), f"{what}: {len(got_rows)} rows, want {min(k, nf)}"
+    assert len(set(got_rows)) == len(got_rows), f"{what}: duplicate rows"
+    allowed = set(sure.tolist()) | set(maybe.tolist())
+    out = [r for r in got_rows if r not in allowed]
+    assert not out, f"{what}: rows {out} are outside the oracle's fetch window"
+    ex = exact_fn(np.array(got_rows, np.uint32))
+    got_scores = np.asarray(got_scores, np.float32)
+    assert np.array_equal(got_scores.view(np.uint32), ex.view(np.uint32)), f"{what}: scores are not the exact scores"
+    keys = [(float(s), -r) for s, r in zip(ex, got_rows)]
+    assert keys == sorted(keys, reverse=True), f"{what}: rows not in (score desc, row asc) order"
+    rest = np.array(sorted(set(sure.tolist()) - set(got_rows)), np.uint32)
+    if rest.size and len(got_rows) == k:
+        er = exact_fn(rest)
+        last = keys[-1]
+        beat = [int(r) for r, s in zip(rest, er) if (float(s), -int(r)) > last]
+        assert not beat, f"{what}: fetched rows {beat[:5]} beat the last row returned"

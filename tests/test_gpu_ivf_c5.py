@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as o
-from tests.helpers import clustered, gaussian, need_gpu, say
+from tests.helpers import REL_TOL, assert_fetch_rerank, clustered, gaussian, need_gpu, say
 from tests.test_gpu_ivf import dequant_f32, reference_build
 
 pytestmark = pytest.mark.gpu
@@ -85,14 +85,30 @@ def test_ivf_4096_lists_p1024_matches_oracle(ctx):
         assert want.size <= 1024
         assert cnt[i] == want.size and set(rows[i, :cnt[i]].tolist()) == set(want.tolist()), i
 
-    # the P = 1024 indexed scan, fetch 40 -> exact re-rank to 10
+    # the P = 1024 indexed scan, fetch 40 -> exact re-rank to 10: every query
+    # of the batch (list-major path) and a few one at a time (fused scan, the
+    # short tail) equal the oracle pipeline over the probed lists: top 40 by
+    # code score, exact re-rank, canonical top 10, up to fetch-boundary
+    # near-ties
+    words = np.empty((n, idx.words_per_row), np.uint32)
+    scales = np.empty(n, np.float32)
+    for s0 in range(0, n, 10000):
+        w, sc = idx.export_codes(s0, min(10000, n - s0))
+        words[s0:s0 + w.shape[0]], scales[s0:s0 + w.shape[0]] = w, sc
     rows, scores, cnt = device_search(idx, qs, 40, 10)
-    for i in (0, 99, nq - 1):
+    singles = {i: device_search(idx, qs[i:i + 1], 40, 10) for i in (0, 99, nq - 1)}
+    for i in range(nq):
         probes, _ = o.topk_canonical(ps[i], 32)
         cand = np.concatenate([lrows[off[c]:off[c + 1]] for c in probes]).astype(np.uint32)
-        assert cnt[i] == 10 and set(rows[i].tolist()) <= set(cand.tolist()), i
-        exact = o.rerank_scores(data, qs[i], rows[i])
-        assert np.array_equal(scores[i].view(np.uint32), exact.view(np.uint32)), i
+        approx = o.scan_quant(words, scales, rq[i], 8, cand=cand)
+        tol = 2 * REL_TOL * float(scales[cand].max()) * float(np.abs(rq[i].astype(np.float64)).sum())
+        assert cnt[i] == 10, i
+        ex = lambda rr, q=qs[i]: o.rerank_scores(data, q, rr)  # noqa: E731
+        assert_fetch_rerank(rows[i], scores[i], approx, cand, ex, 40, 10, tol, what=f"batch query {i}")
+        if i in singles:
+            r1, s1, c1 = singles[i]
+            assert c1[0] == 10
+            assert_fetch_rerank(r1[0], s1[0], approx, cand, ex, 40, 10, tol, what=f"single query {i}")
     idx.destroy()
 
 
