@@ -340,20 +340,38 @@ class BrowserVec:
         return self.index.rerank(q, [h.row for h in candidates], k)
 
     def query_batch(self, queries, k: int = 10, **opts) -> list[list[dict]]:
-        """queryBatch (src/index.ts:473-517).  The index's own batch is used
-        where the reference seam would offer one: a flat fp32 index, whose
-        batch returns exactly the single-query results.  Quantized and IVF
-        indexes (and filtered batches) loop query(), which re-ranks and
-        honours a per-query nprobe, as the reference's fallback loop does."""
+        """queryBatch (src/index.ts:473-517), with one more branch than the
+        reference's.  A flat fp32 index answers with its own batch (the
+        reference's `'queryBatch' in this.index` branch); a quantized or IVF
+        index whose seam offers search() answers the whole batch in one
+        device call with query()'s kEff / fetch / re-rank rules
+        (src/index.ts:402-421) and a one-batch nprobe override, so each
+        query's results equal query()'s; filtered batches, and fetches
+        beyond the fused top-k, loop query() as the reference's fallback
+        does."""
         if len(queries) == 0:
             return []
-        if type(self.index) is not FlatIndex or opts.get("filter") is not None:
+        rerank = opts.get("rerank")
+        nprobe = opts.get("nprobe")
+        flat = type(self.index) is FlatIndex
+        quant = self.quant_bits > 0 and hasattr(self.index, "search")
+        total = self.index.size
+        deleted = self.store.deleted_count
+        k_eff = min(total, k + deleted)
+        do_rerank = rerank if rerank is not None else self.rerank_factor > 1
+        fetch = min(total, max(k_eff, k_eff * self.rerank_factor)) if do_rerank else k_eff
+        if opts.get("filter") is not None or not (flat or quant) or (quant and (fetch > 1024 or k_eff == 0)):
             return [self.query(q, k=k, **opts) for q in queries]
         packed = np.stack([self._prep_query(q) for q in queries])
-        deleted = self.store.deleted_count
-        k_eff = min(self.index.size, k + deleted)
+        if nprobe is not None and hasattr(self.index, "set_nprobe"):
+            self.index.set_nprobe(nprobe)  # consumed by the one batch call, as each query() consumes its own
         t0 = time.perf_counter()
-        batch = self.index.query_batch(packed, len(queries), k_eff)
+        if flat:
+            batch = self.index.query_batch(packed, len(queries), k_eff)
+        else:
+            rows, scores, cnt = self.index.search(packed, fetch if do_rerank else 0, k_eff)
+            batch = [[FlatHit(int(rows[i, j]), float(scores[i, j])) for j in range(cnt[i])]
+                     for i in range(len(queries))]
         self.last_query_ms = (time.perf_counter() - t0) * 1e3
         self.last_query_gpu_ms = self.index.stats()["last_query_gpu_ms"]
         out = []

@@ -13,8 +13,11 @@
 //   - queryMasked on flat and quantized indexes only (IVF filters go through
 //     BrowserVec's exact scan or over-fetch, as in the reference);
 //   - queryBatch on flat fp32 indexes only, whose batches return exactly the
-//     single-query results; quantized and IVF batches stay BrowserVec's loop
-//     of query(), which re-ranks and honours a per-query nprobe;
+//     single-query results (an addition: the reference's WebGPU FlatIndex
+//     has no queryBatch; its queryBatch is HNSW's, hnsw.ts:166); quantized
+//     and IVF batches go through search() in one call, with query()'s
+//     re-rank and nprobe rules, in the branch the integration adds to
+//     BrowserVec.queryBatch (a queryBatch member would skip the re-rank);
 //   - setNprobe / nlist / nprobe / tunedRecall / trainMode on IVF kinds,
 //     ingestMode on quantized kinds, chunkCount everywhere.
 // search() (approximate top-fetch + exact re-rank in one device call),

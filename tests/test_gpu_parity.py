@@ -453,3 +453,50 @@ def test_int8_1m_rows_fetch_rerank_matches_oracle(ctx):
                             fetch, k, tol, what=f"1M query {i}")
     idx.destroy()
 
+
+@pytest.mark.parametrize("kind", ["int8", "ivf_int8", "int4_no_rerank"])
+def test_browservec_query_batch_takes_one_batched_search(ctx, kind):
+    """BrowserVec.queryBatch on a quantized or IVF store answers the batch
+    with one device search() call, not a loop of query(), and returns per
+    query exactly what query() returns (ids, order and score bits), with
+    tombstones skipped and an nprobe option applied to the whole batch
+    (src/index.ts:402-421, 473-517)."""
+    from browservec_amd import BrowserVec
+
+    say("queryBatch batched", kind)
+    dim, n, nq = 96, 6000, 40
+    data = clustered(n, dim, 40, 0.1, seed=171)
+    if kind == "ivf_int8":
+        db = BrowserVec.create(dimension=dim, quantBits=8, ann={"type": "ivf", "nlist": 24, "iters": 3, "nprobe": 4})
+    else:
+        db = BrowserVec.create(dimension=dim, quantBits=8 if kind == "int8" else 4)
+    db.add_vectors([f"v{i}" for i in range(n)], data)
+    qs = data[np.random.default_rng(172).integers(0, n, nq)] + 0.05 * gaussian(nq, dim, 173, normalize=False)
+    db.delete("v17")
+    opts = {"rerank": False} if kind == "int4_no_rerank" else {}
+    if kind == "ivf_int8":
+        opts["nprobe"] = 6
+    calls = {"search": 0, "query": 0}
+    search, query = db.index.search, db.query
+
+    def counted_search(*a, **kw):
+        calls["search"] += 1
+        return search(*a, **kw)
+
+    def counted_query(*a, **kw):
+        calls["query"] += 1
+        return query(*a, **kw)
+
+    db.index.search, db.query = counted_search, counted_query
+    batch = db.query_batch(list(qs), k=10, **opts)
+    assert calls == {"search": 1, "query": 0}, calls
+    db.index.search, db.query = search, query
+    if kind == "ivf_int8":
+        assert db.index.stats()["nprobe"] == 4  # the override was consumed by the batch
+    for i in range(nq):
+        single = db.query(qs[i], k=10, **opts)
+        assert len(single) == 10 and "v17" not in [r["id"] for r in single]
+        assert [r["id"] for r in batch[i]] == [r["id"] for r in single], i
+        assert (np.array([r["score"] for r in batch[i]], np.float32).view(np.uint32).tolist() ==
+                np.array([r["score"] for r in single], np.float32).view(np.uint32).tolist()), i
+    db.destroy()

@@ -222,3 +222,98 @@ def test_node_results_equal_python_binding(tmp_path):
         quant.destroy()
     finally:
         ctx.destroy()
+
+
+NODE_QUERY_BATCH = """
+const fs = require('fs');
+const m = require(%(module)s);
+function f32(p) { const b = fs.readFileSync(p); return new Float32Array(b.buffer, b.byteOffset, b.length / 4); }
+const rows = f32(%(rows)s), qs = f32(%(queries)s);
+const dim = %(dim)d, n = %(n)d, nq = %(nq)d;
+const RERANK_FACTOR = 4;  // BrowserVec's default for int8 / int4 (src/index.ts:236-250)
+// The tombstone skip and stop-at-k of BrowserVec.query / queryBatch (src/index.ts:424-435, 505-515).
+function post(hits, k, deleted) {
+  const out = [];
+  for (const h of hits) {
+    if (deleted.has(h.row)) continue;
+    out.push({row: h.row, score: h.score});
+    if (out.length === k) break;
+  }
+  return out;
+}
+// BrowserVec.query's quantized path with the one-call search (src/index.ts:402-421).
+async function queryOne(index, q, k, opts, deleted) {
+  const total = index.size;
+  const kEff = Math.min(total, k + deleted.size);
+  const doRerank = opts.rerank !== undefined ? opts.rerank : RERANK_FACTOR > 1;
+  const fetch = doRerank ? Math.min(total, Math.max(kEff, kEff * RERANK_FACTOR)) : kEff;
+  if (opts.nprobe !== undefined && 'setNprobe' in index) index.setNprobe(opts.nprobe);
+  const batch = await index.search(q, 1, doRerank ? fetch : 0, kEff);
+  return post(batch[0], k, deleted);
+}
+// The queryBatch branch the integration adds (src/index.ts:473-517): one search() call.
+async function queryBatch(index, packed, count, k, opts, deleted) {
+  const total = index.size;
+  const kEff = Math.min(total, k + deleted.size);
+  const doRerank = opts.rerank !== undefined ? opts.rerank : RERANK_FACTOR > 1;
+  const fetch = doRerank ? Math.min(total, Math.max(kEff, kEff * RERANK_FACTOR)) : kEff;
+  if (kEff === 0 || fetch > 1024) throw new Error('falls back to the query() loop');
+  if (opts.nprobe !== undefined && 'setNprobe' in index) index.setNprobe(opts.nprobe);
+  const batch = await index.search(packed, count, doRerank ? fetch : 0, kEff);
+  return batch.map((hits) => post(hits, k, deleted));
+}
+(async () => {
+  const ctx = new m.HipDeviceContext(0);
+  const out = {};
+  const cases = [['int8', 8, null, {}], ['ivf_int8', 8, {nlist: 24, iters: 3, nprobe: 4}, {nprobe: 6}],
+                 ['int4_no_rerank', 4, null, {rerank: false}]];
+  for (const [name, bits, ann, opts] of cases) {
+    const index = ann ? m.buildIndex(ctx, dim, 'cosine', bits, {}, ann) : m.buildIndex(ctx, dim, 'cosine', bits, {});
+    await index.append(rows, n);
+    const deleted = new Set([17]);
+    let calls = 0;
+    const search = index.search.bind(index);
+    index.search = (...a) => { calls += 1; return search(...a); };
+    const batch = await queryBatch(index, qs, nq, 10, opts, deleted);
+    const batchCalls = calls;
+    const singles = [];
+    for (let i = 0; i < nq; i++) singles.push(await queryOne(index, qs.subarray(i * dim, (i + 1) * dim), 10, opts, deleted));
+    out[name] = {batch: batch, singles: singles, batchCalls: batchCalls, nprobeAfter: ann ? index.nprobe : null};
+    index.destroy();
+  }
+  ctx.destroy();
+  console.log(JSON.stringify(out));
+})().catch((e) => { console.error(e.code, e.message); process.exit(3); });
+"""
+
+
+@pytest.mark.gpu
+def test_node_query_batch_branch_takes_one_search(tmp_path):
+    """The queryBatch branch INTEGRATION.md adds to BrowserVec, run in node
+    over the addon: a quantized or IVF store's batch is one search() call,
+    and every query's rows, order and score bits equal query()'s one-call
+    search with the same kEff / fetch / re-rank / nprobe rules and the same
+    tombstone skip (src/index.ts:402-436, 473-517)."""
+    need_gpu()
+    dim, n, nq = 96, 6000, 24
+    say("napi queryBatch", dim, n, nq)
+    x = clustered(n, dim, 40, 0.1, seed=181)
+    q = x[np.random.default_rng(182).integers(0, n, nq)] + 0.05 * gaussian(nq, dim, seed=183, normalize=False)
+    q = q.astype(np.float32)
+    (tmp_path / "rows.f32").write_bytes(x.tobytes())
+    (tmp_path / "q.f32").write_bytes(q.tobytes())
+    r = run_node(NODE_QUERY_BATCH % {"module": json.dumps(MODULE), "rows": json.dumps(str(tmp_path / "rows.f32")),
+                                     "queries": json.dumps(str(tmp_path / "q.f32")), "dim": dim, "n": n,
+                                     "nq": nq})
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    for name in ("int8", "ivf_int8", "int4_no_rerank"):
+        res = out[name]
+        assert res["batchCalls"] == 1, name
+        for i in range(nq):
+            b, s = res["batch"][i], res["singles"][i]
+            assert len(b) == 10 and 17 not in [h["row"] for h in b], (name, i)
+            assert [h["row"] for h in b] == [h["row"] for h in s], (name, i)
+            assert (np.float32([h["score"] for h in b]).view(np.uint32).tolist() ==
+                    np.float32([h["score"] for h in s]).view(np.uint32).tolist()), (name, i)
+    assert out["ivf_int8"]["nprobeAfter"] == 4  # the override was consumed by one call
