@@ -200,6 +200,7 @@ struct bv_index {
     std::vector<uint32_t> list_sizes_desc;    // host: list sizes, largest first
     DevBuf ivf_idx, ivf_idx2, ivf_slot, ivf_assign, ivf_hist, ivf_base, ivf_totals, ivf_toff, ivf_trows;
     DevBuf ivf_pend;  // an append's sampled rows (rotated), scattered into `sample` once nothing can fail
+    DevBuf ivf_keys;  // the split assignment's per-row keys
     DevBuf probe_scores, probes, cand_tot, cand_off;
     double build_ms = 0;
     double last_query_ms = 0, last_query_gpu_ms = 0;
@@ -517,6 +518,7 @@ static int ivf_extend_reserve(bv_index *idx, uint64_t base, uint64_t count) {
     hipStream_t s = idx->stream;
     const uint32_t nblk = ivf_list_blocks(count);
     HIPX(idx->dev, idx->ivf_assign.ensure(count * 4, 0, s), "scratch");
+    if (ivf_assign_split(count)) HIPX(idx->dev, idx->ivf_keys.ensure(count * 8, 0, s), "scratch");
     HIPX(idx->dev, idx->ivf_hist.ensure((size_t)std::max(nblk, 1u) * nlist * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->ivf_base.ensure((size_t)std::max(nblk, 1u) * nlist * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->ivf_totals.ensure((size_t)nlist * 4, 0, s), "scratch");
@@ -539,6 +541,7 @@ static int ivf_extend_lists(bv_index *idx, uint64_t base, uint64_t count) {
     fa.cen_stride = idx->sample_dim;
     fa.nlist = nlist;
     fa.out = idx->ivf_assign.as<uint32_t>();
+    fa.keys = idx->ivf_keys.as<uint64_t>();
     if (idx->quant) {
         fa.codes = idx->codes.as<uint32_t>() + base * idx->words_per_row;
         fa.words_per_row = idx->words_per_row;
@@ -996,6 +999,10 @@ static int ivf_build(bv_index *idx) {
     ta.cen_stride = D;
     ta.nlist = nlist;
     ta.out = idx->ivf_assign.as<uint32_t>();
+    if (ivf_assign_split(train) || ivf_assign_split(rows)) {
+        HIPX(idx->dev, idx->ivf_keys.ensure((size_t)std::max<uint64_t>(train, rows) * 8, 0, s), "scratch");
+        ta.keys = idx->ivf_keys.as<uint64_t>();
+    }
     std::vector<uint32_t> toff(nlist + 1);
     for (uint32_t it = 0; it < iters; ++it) {
         HIPX(idx->dev, ivf_launch_assign(ta, 0, s), "assign kernel");
@@ -1354,6 +1361,8 @@ static void scan_common(const bv_index *idx, const float *d_q, uint64_t n, uint3
     }
     // few rows per wave (IVF lists, small corpora): the short tail
     a.short_tail = n < SHORT_TAIL_ROWS * grid * (SCAN_WG / 64);
+    a.static_pct = a.short_tail ? SHORT_STATIC_PCT : LONG_STATIC_PCT;
+    a.dsteps = a.short_tail ? SHORT_DSTEPS : LONG_DSTEPS;
 }
 
 // The fused single-launch scan (one query per grid row): query transform,

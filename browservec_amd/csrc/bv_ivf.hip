@@ -64,6 +64,11 @@ __global__ __launch_bounds__(256) void ivf_normalize_rows(float *m, uint32_t row
 // each, fp32 fused multiply-add over the dimension in order), argmax per row
 // with the lowest centroid index winning ties.  The row loader dequantizes
 // codes exactly as the reference's assign kernels do before the product.
+// SPLIT: workgroup (x, y) takes row tile x against centroid tile y only and
+// folds its rows' best (score, ~centroid) keys into a.keys with a 64-bit
+// atomic maximum; the keys are unique, so the maximum over the tiles is the
+// fold of the one-workgroup form, whatever the order.  ivf_assign_finish
+// turns the keys into centroids.
 constexpr int AT = 128;  // rows and centroids per tile
 constexpr int AK = 8;    // dimension chunk per LDS stage
 
@@ -96,7 +101,7 @@ template <> struct RowLoader<1> {  // sign bits as +-1 (the scale multiplies the
     }
 };
 
-template <int BITS>
+template <int BITS, bool SPLIT>
 __global__ __launch_bounds__(256) void ivf_assign(IvfAssignArgs a) {
     __shared__ float As[AK][AT + 4];
     __shared__ float Bs[AK][AT + 4];
@@ -105,7 +110,8 @@ __global__ __launch_bounds__(256) void ivf_assign(IvfAssignArgs a) {
     uint64_t best[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) best[i] = 0;
-    for (uint32_t c0 = 0; c0 < a.nlist; c0 += AT) {
+    const uint32_t cbeg = SPLIT ? blockIdx.y * AT : 0u, cend = SPLIT ? cbeg + AT : a.nlist;
+    for (uint32_t c0 = cbeg; c0 < cend && c0 < a.nlist; c0 += AT) {
         float acc[8][8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -166,8 +172,21 @@ __global__ __launch_bounds__(256) void ivf_assign(IvfAssignArgs a) {
             b = o > b ? o : b;
         }
         const uint64_t r = r0 + ty + 16 * i;
-        if (tx == 0 && r < a.n) a.out[r] = 0xffffffffu - (uint32_t)b;
+        if (tx == 0 && r < a.n) {
+            if constexpr (SPLIT) atomicMax((unsigned long long *)&a.keys[r], (unsigned long long)b);
+            else a.out[r] = 0xffffffffu - (uint32_t)b;
+        }
     }
+}
+
+__global__ __launch_bounds__(256) void ivf_assign_keys_zero(uint64_t *keys, uint64_t n) {
+    const uint64_t r = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r < n) keys[r] = 0;
+}
+
+__global__ __launch_bounds__(256) void ivf_assign_finish(const uint64_t *keys, uint64_t n, uint32_t *out) {
+    const uint64_t r = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r < n) out[r] = 0xffffffffu - (uint32_t)keys[r];
 }
 
 // ----------------------------------------------------------------- lists --
@@ -549,16 +568,28 @@ hipError_t ivf_launch_normalize(float *m, uint32_t rows, uint32_t dim, uint32_t 
     return hipGetLastError();
 }
 
-hipError_t ivf_launch_assign(const IvfAssignArgs &a, int bits, hipStream_t s) {
-    if (a.n == 0) return hipSuccess;
-    const dim3 grid((uint32_t)((a.n + AT - 1) / AT));
+template <bool SPLIT>
+static hipError_t assign_bits(const IvfAssignArgs &a, int bits, dim3 grid, hipStream_t s) {
     switch (bits) {
-    case 0: hipLaunchKernelGGL(ivf_assign<0>, grid, dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL(ivf_assign<8>, grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(ivf_assign<4>, grid, dim3(256), 0, s, a); break;
-    case 1: hipLaunchKernelGGL(ivf_assign<1>, grid, dim3(256), 0, s, a); break;
+    case 0: hipLaunchKernelGGL((ivf_assign<0, SPLIT>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((ivf_assign<8, SPLIT>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((ivf_assign<4, SPLIT>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((ivf_assign<1, SPLIT>), grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t ivf_launch_assign(const IvfAssignArgs &a, int bits, hipStream_t s) {
+    if (a.n == 0) return hipSuccess;
+    const uint32_t tiles = (uint32_t)((a.n + AT - 1) / AT);
+    if (!ivf_assign_split(a.n)) return assign_bits<false>(a, bits, dim3(tiles), s);
+    if (!a.keys) return hipErrorInvalidValue;
+    const uint32_t flat = (uint32_t)((a.n + 255) / 256);
+    hipLaunchKernelGGL(ivf_assign_keys_zero, dim3(flat), dim3(256), 0, s, a.keys, a.n);
+    hipError_t e = assign_bits<true>(a, bits, dim3(tiles, (a.nlist + AT - 1) / AT), s);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(ivf_assign_finish, dim3(flat), dim3(256), 0, s, a.keys, a.n, a.out);
     return hipGetLastError();
 }
 

@@ -99,6 +99,8 @@ struct ScanArgs {
     uint32_t *out_n;          // [nq]
     uint32_t short_tail;      // few rows per wave: every pass polls the shared bound, the flush takes
                               // a fresh read of it, and the final gather is bounded by the wave maxima
+    uint32_t static_pct;      // share (%) of the row grabs assigned statically (0: the kernel's default)
+    uint32_t dsteps;          // wave steps per dynamic ticket (0: the kernel's default)
 };
 
 // Rows per wave below which a scan takes the short tail (a wave then scans
@@ -106,6 +108,11 @@ struct ScanArgs {
 // usual polling, so a flush by the wave's own bound would carry, and
 // exactly re-score, most of its rows).
 constexpr uint64_t SHORT_TAIL_ROWS = 256;
+// The static / dynamic split of a long scan and of a short one (a short
+// scan's dynamic share is handed out in finer chunks: a wave scans only a
+// few steps in all).
+constexpr uint32_t LONG_STATIC_PCT = 70, LONG_DSTEPS = 6;
+constexpr uint32_t SHORT_STATIC_PCT = 80, SHORT_DSTEPS = 1;
 
 struct EncodeArgs {
     const float *src;         // rows x dim
@@ -175,7 +182,13 @@ struct IvfAssignArgs {
     uint32_t cen_stride;
     uint32_t nlist;
     uint32_t *out;            // [n] nearest centroid
+    uint64_t *keys;           // [n] scratch of the split form (row tiles x centroid tiles), or null
 };
+// Row tiles below which the assignment splits the centroids over workgroups
+// too (a workgroup per row tile and centroid tile, joined by a per-row
+// atomic maximum) so that the grid fills the device.
+constexpr uint64_t IVF_ASSIGN_SPLIT_TILES = 1024;
+inline bool ivf_assign_split(uint64_t n) { return (n + 127) / 128 < IVF_ASSIGN_SPLIT_TILES; }
 
 struct IvfProbeArgs {
     const float *centroids;   // nlist x P

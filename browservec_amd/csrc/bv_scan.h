@@ -1644,6 +1644,9 @@ __device__ __forceinline__ uint64_t exact_key_lanes4(const float *x, const doubl
 
 // ------------------------------------------------------------ scan + top-k --
 constexpr uint32_t TAU_POLL = 4;     // step pairs between reads of the shared bound
+// The split between statically assigned grabs and dynamic tickets comes
+// with each launch (ScanArgs::static_pct / dsteps, chosen by the host for
+// long and short scans); zero takes these.
 constexpr uint32_t STATIC_PCT = 70;  // share of the grabs assigned statically
 constexpr uint32_t DSTEPS = 6;       // steps per dynamically assigned chunk
 
@@ -2069,7 +2072,9 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     // workgroups (older waves win memory arbitration) and XCDs.
     const uint32_t wofs = (uint32_t)wave * SH::RPS, wstep = (uint32_t)SH::WAVES * SH::RPS;
     const uint32_t ngrabs = (n + SH::GRAB_ROWS - 1) / SH::GRAB_ROWS;
-    const uint32_t sgrabs = (uint32_t)((uint64_t)ngrabs * STATIC_PCT / 100 / a.grid);  // full static grabs per workgroup
+    const uint32_t spct = a.static_pct ? a.static_pct : STATIC_PCT;
+    const uint32_t dsteps = a.dsteps ? a.dsteps : DSTEPS;
+    const uint32_t sgrabs = (uint32_t)((uint64_t)ngrabs * spct / 100 / a.grid);  // full static grabs per workgroup
     uint32_t d0 = sgrabs * a.grid * SH::GRAB_ROWS;
     if (d0 > n) d0 = n;
     const uint32_t nsd = (n - d0 + SH::RPS - 1) / SH::RPS;  // dynamic steps
@@ -2080,10 +2085,10 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         const uint32_t lo = r * per;
         return lo >= nsd ? 0 : (nsd - lo < per ? nsd - lo : per);
     };
-    auto big_chunks = [&](uint32_t ls) -> uint32_t { return ls / DSTEPS; };
+    auto big_chunks = [&](uint32_t ls) -> uint32_t { return ls / dsteps; };
     auto slice_tickets = [&](uint32_t r) -> uint32_t {
         const uint32_t ls = slice_steps(r), nb = big_chunks(ls);
-        return nb + (ls - nb * DSTEPS);
+        return nb + (ls - nb * dsteps);
     };
     uint32_t gi = 0;
     uint32_t sub = 0, ds = 0, dlen = 0, slice = (blockIdx.x * SH::WAVES + wave) % ng, pend = 0;
@@ -2103,11 +2108,11 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
                 t = __builtin_amdgcn_readfirstlane(v);
             }
             const uint32_t ls = slice_steps(slice), nb = big_chunks(ls);
-            if (t < nb + (ls - nb * DSTEPS)) {
+            if (t < nb + (ls - nb * dsteps)) {
                 if (lane == 0) pend = atomicAdd(&qs->dyn[slice * CL], 1u);  // next ticket in flight
                 has_pend = true;
-                const uint32_t st = t < nb ? t * DSTEPS : nb * DSTEPS + (t - nb);
-                dlen = t < nb ? DSTEPS : 1;
+                const uint32_t st = t < nb ? t * dsteps : nb * dsteps + (t - nb);
+                dlen = t < nb ? dsteps : 1;
                 c0 = d0 + (slice * per + st) * SH::RPS;
                 const uint32_t e = c0 + dlen * SH::RPS;
                 clim = e < n ? e : n;
