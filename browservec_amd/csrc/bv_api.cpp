@@ -1440,17 +1440,18 @@ static bool mq_eligible(const bv_index *idx, uint32_t nq, const uint32_t *d_mask
                idx->rows > MQ_SAMPLE;
     const uint32_t u16 = idx->P / 16;  // 16-code units per row
     const bool shape = u16 >= 2 && (u16 % 2) == 0 && u16 / 2 <= MQ_MAX_STEPS;
-    // Hamming: the first-level pass over +1 / -1 rows, above the sample size
-    if (idx->codec == C_HAM) return shape && idx->rows > MQ_SAMPLE;
+    // Hamming and 1-bit asymmetric: the first-level pass over +1 / -1 rows,
+    // above the sample size
+    if (idx->codec == C_HAM || idx->codec == C_Q1P || idx->codec == C_Q1A) return shape && idx->rows > MQ_SAMPLE;
     return (idx->codec == C_Q8 || idx->codec == C_Q4) && shape;
 }
 
 // Rotated queries split into three int8 levels in the 16-code unit layout
 // the batched scan reads (int4 indexes: levels without the 1/127 scale).
 static int prepare_levels16(bv_index *idx, const float *d_q, uint32_t nq, const unsigned char **qlev,
-                            uint64_t *qstride) {
+                            uint64_t *qstride, int layout = -1) {
     const uint32_t P = idx->P;
-    const int layout = idx->codec == C_Q4 ? C_Q4M : C_Q8;
+    if (layout < 0) layout = idx->codec == C_Q4 ? C_Q4M : C_Q8;
     const size_t st = level_stride(layout, P);
     HIPX(idx->dev, idx->qrot.ensure((size_t)nq * P * 4, 0, idx->stream), "query buffer");
     HIPX(idx->dev, idx->qscan.ensure((size_t)nq * st, 0, idx->stream), "query buffer");
@@ -1620,8 +1621,10 @@ struct Q8Source {
 
 // Hamming batches: the +1 / -1 rows (kept up to date with appends) and the
 // queries' 1-bit codes as level one of the packed levels.
-static int prepare_pm(bv_index *idx, const float *d_q, uint32_t nq, const unsigned char **qlev, uint64_t *qstride,
-                      Q8Source *src) {
+// The +1 / -1 expansion of a 1-bit index's codes (1 byte per code), kept
+// current with the index's rows, with unit row scales and the rows' code
+// norms.
+static int ensure_pm_rows(bv_index *idx) {
     hipStream_t s = idx->stream;
     const uint32_t P = idx->P, W1 = idx->words_per_row;
     if (idx->pm_rows < idx->rows) {
@@ -1640,6 +1643,15 @@ static int prepare_pm(bv_index *idx, const float *d_q, uint32_t nq, const unsign
              "norm kernel");
         idx->pm_rows = n;
     }
+    return BV_OK;
+}
+
+static int prepare_pm(bv_index *idx, const float *d_q, uint32_t nq, const unsigned char **qlev, uint64_t *qstride,
+                      Q8Source *src) {
+    hipStream_t s = idx->stream;
+    const uint32_t P = idx->P, W1 = idx->words_per_row;
+    int rc = ensure_pm_rows(idx);
+    if (rc) return rc;
     const size_t st = level_stride(C_Q8, P);
     HIPX(idx->dev, idx->pm_qbits.ensure((size_t)nq * W1 * 4, 0, s), "query buffer");
     HIPX(idx->dev, idx->qscale.ensure((size_t)nq * 4, 0, s), "query buffer");
@@ -1663,13 +1675,77 @@ static int prepare_pm(bv_index *idx, const float *d_q, uint32_t nq, const unsign
     return BV_OK;
 }
 
+// The last step of a batch whose prefilter kept, per query, a superset of
+// the rows that can reach its top kprime (mq_rows, counts in mq_kept, cap
+// apart; a query whose joined list overflowed, mq_cnt[q] > cap, kept none):
+// the fused scan in indexed mode over the kept rows computes their
+// single-query keys, selects and re-ranks, so every query returns what it
+// returns alone.  Overflowed queries are re-run alone over every row.
+static int finish_batched_indexed(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out,
+                                  bool rerank, uint64_t cap, uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
+    hipStream_t s = idx->stream;
+    uint32_t *h = (uint32_t *)idx->h_cnt.p;  // [nq] kept, then [nq] joined counts
+    HIPX(idx->dev, hipMemcpyAsync(h, idx->mq_kept.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s), "count download");
+    HIPX(idx->dev, hipMemcpyAsync(h + nq, idx->mq_cnt.p, (size_t)nq * 4, hipMemcpyDeviceToHost, s), "count download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "batched scan");
+    std::vector<uint32_t> kept(h, h + nq), joined(h + nq, h + 2 * (size_t)nq);
+    uint64_t most = 1;
+    for (uint32_t i = 0; i < nq; i++) most = std::max<uint64_t>(most, std::min<uint64_t>(kept[i], cap));
+    ScanArgs a{};
+    const uint32_t grid = grid_for(idx, most);
+    int rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a);
+    if (rc) return rc;
+    if (scan_prep_supported(idx->codec, idx->units, idx->P)) {  // the scan transforms the fp32 queries itself
+        a.qraw = d_q;
+        a.qdim = idx->dim;
+        a.signs = idx->signs.as<float>();
+        a.rounds = idx->d.rounds;
+    } else {
+        const void *qscan = nullptr;
+        uint64_t qstride = 0;
+        rc = prepare_queries(idx, d_q, nq, &qscan, &qstride);
+        if (rc) return rc;
+        a.q = qscan;
+        a.q_stride = qstride;
+    }
+    scan_common(idx, d_q, most, grid, kprime, k_out, rerank, nullptr, 0, d_rows, d_scores, d_n, a);
+    a.cand = idx->mq_rows.as<uint32_t>();
+    a.cand_n = idx->mq_kept.as<uint32_t>();
+    a.cand_stride = cap;
+    HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, s), "scan kernel");
+    timing_end(idx);
+    uint64_t scanned = (idx->rows + MQ_SAMPLE) * nq;
+    for (uint32_t i = 0; i < nq; i++) scanned += std::min<uint64_t>(kept[i], cap);
+    idx->last_scanned = scanned;
+    for (uint32_t i = 0; i < nq; i++) {
+        if (joined[i] <= cap) continue;
+        rc = run_fused(idx, d_q + (size_t)i * idx->dim, 1, kprime, k_out, rerank, nullptr, 0,
+                       d_rows + (size_t)i * k_out, d_scores + (size_t)i * k_out, d_n + i);
+        if (rc) return rc;
+    }
+    return BV_OK;
+}
+
 static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out,
                           bool rerank, uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
     const unsigned char *qlev = nullptr;
     uint64_t qstride = 0;
     Q8Source src{idx->codes.as<uint32_t>(), idx->words_per_row, idx->scales.as<float>(), idx->cnorm.as<float>()};
-    int rc = idx->codec == C_HAM ? prepare_pm(idx, d_q, nq, &qlev, &qstride, &src)
-                                 : prepare_levels16(idx, d_q, nq, &qlev, &qstride);
+    // 1-bit asymmetric: the pass over the +1 / -1 expansion with the rotated
+    // query's int8 level one (levels without the 1/127), the rows' own
+    // scales and row term 1 (mq1_qconst_l1); the kept rows are re-scored by
+    // the fused scan in indexed mode, which gives them the single-query keys
+    const bool asym1 = idx->codec == C_Q1P || idx->codec == C_Q1A;
+    int rc = BV_OK;
+    if (idx->codec == C_HAM) {
+        rc = prepare_pm(idx, d_q, nq, &qlev, &qstride, &src);
+    } else if (asym1) {
+        rc = ensure_pm_rows(idx);
+        if (!rc) rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride, C_Q4M);
+        src = Q8Source{idx->pm_codes.as<uint32_t>(), idx->P / 4, idx->scales.as<float>(), idx->pm_ones.as<float>()};
+    } else {
+        rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride);
+    }
     if (rc) return rc;
     const uint64_t N = idx->rows, S = MQ_SAMPLE;  // N > S (mq_eligible)
     // rows kept per query: those within the bounds' width of the sample's
@@ -1693,17 +1769,23 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     HIPX(idx->dev, idx->mq_kept.ensure((size_t)nq * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->mq_tau.ensure((size_t)nq * 8, 0, s), "scratch");
     HIPX(idx->dev, idx->mq_rq.ensure((size_t)nq * 4, 0, s), "scratch");
-    HIPX(idx->dev, idx->h_cnt.ensure((size_t)nq * 4), "pinned buffer");
+    HIPX(idx->dev, idx->h_cnt.ensure((size_t)nq * 8), "pinned buffer");
     HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, s), "scratch");
     HIPX(idx->dev, idx->merged_n.ensure((size_t)nq * 4, 0, s), "scratch");
     const uint32_t units16 = idx->P / 16;
 
     timing_begin(idx);
     // the query bounds, and the sample pass's key count per query
-    HIPX(idx->dev,
-         launch_mq1_qconst(qlev, qstride, units16, units16 * 48, nq, idx->mq_rq.as<float>(),
-                           idx->mq_cnt.as<uint32_t>(), (uint32_t)S, s),
-         "query bound kernel");
+    if (asym1)
+        HIPX(idx->dev,
+             launch_mq1_qconst_l1(idx->qrot.as<float>(), idx->P, qlev, qstride, units16 * 48, nq,
+                                  idx->mq_rq.as<float>(), idx->mq_cnt.as<uint32_t>(), (uint32_t)S, s),
+             "query bound kernel");
+    else
+        HIPX(idx->dev,
+             launch_mq1_qconst(qlev, qstride, units16, units16 * 48, nq, idx->mq_rq.as<float>(),
+                               idx->mq_cnt.as<uint32_t>(), (uint32_t)S, s),
+             "query bound kernel");
     Mq1Args m{};
     m.codes = src.codes;
     m.scales = src.scales;
@@ -1778,6 +1860,7 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
          launch_mq1_keep(m.cand, m.up_out, m.cnt, cap, idx->mq_tau.as<uint64_t>(), idx->mq_rows.as<uint32_t>(),
                          idx->mq_kept.as<uint32_t>(), nq, s),
          "batched keep kernel");
+    if (asym1) return finish_batched_indexed(idx, d_q, nq, kprime, k_out, rerank, cap, d_rows, d_scores, d_n);
     // exact keys of those rows, the best kprime of them, and the re-rank
     HIPX(idx->dev,
          launch_mq1_exact(m.codes, m.W, m.scales, qlev, qstride, units16, idx->mq_rows.as<uint32_t>(),
@@ -1833,7 +1916,8 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
 static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                        uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
     if (!idx->quant) return run_batched_f32(idx, d_q, nq, kprime, k_out, d_rows, d_scores, d_n);
-    if ((idx->codec == C_Q8 || idx->codec == C_HAM) && idx->rows > MQ_SAMPLE)
+    if ((idx->codec == C_Q8 || idx->codec == C_HAM || idx->codec == C_Q1P || idx->codec == C_Q1A) &&
+        idx->rows > MQ_SAMPLE)
         return run_batched_q8(idx, d_q, nq, kprime, k_out, rerank, d_rows, d_scores, d_n);
     const unsigned char *qscan = (const unsigned char *)d_q;  // fp32 rows: the queries as they are
     uint64_t qstride = (uint64_t)idx->dim * 4;

@@ -358,6 +358,11 @@ hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scal
 hipError_t launch_row_code_norms(const uint32_t *codes, uint64_t n, uint32_t W, float *cn, hipStream_t s);
 hipError_t launch_mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32_t units, uint32_t tail_off,
                              uint32_t nq, float *rq, uint32_t *cnt, uint32_t cnt_value, hipStream_t s);
+// The 1-bit asymmetric batch's query term (row term 1): |x - s1 q1|_1 plus
+// the f32 summation slack, rounded up; x the rotated queries (nq x P).
+hipError_t launch_mq1_qconst_l1(const float *qrot, uint32_t P, const unsigned char *qlev, uint64_t qstride,
+                                uint32_t tail_off, uint32_t nq, float *rq, uint32_t *cnt, uint32_t cnt_value,
+                                hipStream_t s);
 hipError_t launch_mq1_scan(const Mq1Args &a, hipStream_t s);
 hipError_t launch_mq_scan(const MqArgs &a, hipStream_t s);
 // fp32 rows (dot / cosine): a.codes = the rows, a.W = dim, a.units = dim / 8,

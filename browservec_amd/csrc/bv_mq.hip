@@ -1270,6 +1270,45 @@ __global__ __launch_bounds__(64) void mq1_qconst(const unsigned char *qlev, uint
     }
 }
 
+// The 1-bit asymmetric batch's query term, with the row term 1: the
+// single-query score is f32(f32 sum_i (bit_i ? x_i : -x_i) * scale), x the
+// rotated query.  With x = s1 q1 + r (q1 the query's int8 level one, s1 its
+// step), sum_i sign_i x_i = s1 D + sum_i sign_i r_i, D the level-one dot
+// with the +1 / -1 row, and |sum_i sign_i r_i| <= |r|_1.  The f32 sum in
+// order differs from the exact one by at most (P - 1) 2^-24 |x|_1; rq adds
+// twice that to |r|_1, then 2^-18 of the whole, rounded up to f32 (the
+// bound's f32 arithmetic and the final product are covered by the bound's
+// own 2^-20 |s1 D| and by the 2^-18).  Level bytes: the C_Q4M unit layout
+// (level one at bytes [48u, 48u + 16) of unit u, step s[0] undivided).
+__global__ __launch_bounds__(64) void mq1_qconst_l1(const float *qrot, uint32_t P, const unsigned char *qlev,
+                                                    uint64_t qstride, uint32_t tail_off, float *rq, uint32_t *cnt,
+                                                    uint32_t cnt_value) {
+    const int lane = threadIdx.x;
+    const float *x = qrot + (uint64_t)blockIdx.x * P;
+    const unsigned char *src = qlev + (uint64_t)blockIdx.x * qstride;
+    const QLevelTail *t = (const QLevelTail *)(src + tail_off);
+    const double s1 = t->s[0];
+    double r = 0.0, ax = 0.0;
+    for (uint32_t i = lane; i < P; i += 64) {
+        const double xi = (double)x[i];
+        const double q1 = (double)(int8_t)src[(uint64_t)(i >> 4) * 48 + (i & 15)];
+        r += fabs(fma(-s1, q1, xi));
+        ax += fabs(xi);
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        r += __shfl_xor(r, o);
+        ax += __shfl_xor(ax, o);
+    }
+    if (lane == 0) {
+        const double v = (r + 2.0 * (double)P * 0x1p-24 * ax) * (1.0 + 0x1p-18);
+        float f = (float)v;
+        if ((double)f < v) f = next_up(f);
+        rq[blockIdx.x] = f;
+        if (cnt) cnt[blockIdx.x] = cnt_value;
+    }
+}
+
 // One workgroup per query: the kept rows whose upper bound reaches tau[q]
 // (the kk-th best lower-bound key among them, so every row of the exact
 // top kk is among these).
@@ -1694,6 +1733,14 @@ hipError_t launch_mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32
                              uint32_t nq, float *rq, uint32_t *cnt, uint32_t cnt_value, hipStream_t s) {
     if (nq == 0) return hipSuccess;
     hipLaunchKernelGGL(mq1_qconst, dim3(nq), dim3(64), 0, s, qlev, qstride, units, tail_off, rq, cnt, cnt_value);
+    return hipGetLastError();
+}
+
+hipError_t launch_mq1_qconst_l1(const float *qrot, uint32_t P, const unsigned char *qlev, uint64_t qstride,
+                                uint32_t tail_off, uint32_t nq, float *rq, uint32_t *cnt, uint32_t cnt_value,
+                                hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    hipLaunchKernelGGL(mq1_qconst_l1, dim3(nq), dim3(64), 0, s, qrot, P, qlev, qstride, tail_off, rq, cnt, cnt_value);
     return hipGetLastError();
 }
 

@@ -281,3 +281,38 @@ def test_batched_hamming_equals_singles(ctx, dim, n, nq):
     for i in range(nq):
         assert batch[i] == idx.query(qs[i], 20), i
     idx.destroy()
+
+
+@pytest.mark.parametrize("dim,n,nq", [(1024, 40000, 64), (256, 30000, 33), (100, 20000, 9)])
+def test_batched_1bit_asym_equals_singles(ctx, dim, n, nq):
+    """1-bit asymmetric batches (the reference's distanceQ1 scorer) run the
+    int8 first-level pass over the +1 / -1 expansion with the rotated query's
+    int8 level one: the score scale * sum_i (bit_i ? x_i : -x_i) lies within
+    scale * (|x - s1 q1|_1 + the f32 summation slack) of scale * s1 * D, D
+    the level-one dot; the rows that can still reach a query's fetch are
+    re-scored by the fused scan in indexed mode.  Rows and score bits equal
+    the same queries run alone, with and without the re-rank, across appends
+    (the expansion follows them), with duplicate rows tying."""
+    from browservec_amd import QuantIndex
+
+    say("batched 1-bit asym", dim, n, nq)
+    data = clustered(n, dim, 40, 0.1, seed=dim + 5)
+    data[n // 2:n // 2 + 200] = data[:200]  # ties: identical codes and scales
+    idx = QuantIndex(ctx, dim, bits=1)
+    idx.append(data[:n - 2000], n - 2000)
+    qs = data[np.arange(nq) * (n // nq)] + gaussian(nq, dim, 6, normalize=False) * 0.05
+    qs = np.stack([o.normalize(q) for q in qs]).astype(np.float32)
+    singles_equal(idx, qs, 200, 10)
+    idx.append(data[n - 2000:], 2000)
+    rows, scores, cnt = singles_equal(idx, qs, 0, 50)
+    # the approximate scores are the oracle's distanceQ1 scores of those rows
+    words, sc = idx.export_codes()
+    for i in (0, nq - 1):
+        q_rot = o.rotate(qs[i], dim)[0]
+        want = o.scan_quant(words, sc, q_rot, 1, cand=rows[i, :cnt[i]].astype(np.uint32))
+        mag = np.abs(sc[rows[i, :cnt[i]]].astype(np.float64)) * float(np.abs(q_rot.astype(np.float64)).sum())
+        assert np.all(np.abs(scores[i, :cnt[i]].astype(np.float64) - want) <= 1e-5 * mag + 1e-30), i
+    batch = idx.query_batch(qs, nq, 20)
+    for i in range(nq):
+        assert batch[i] == idx.query(qs[i], 20), i
+    idx.destroy()
