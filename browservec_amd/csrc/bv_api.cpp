@@ -1621,9 +1621,10 @@ struct Q8Source {
 
 // Hamming batches: the +1 / -1 rows (kept up to date with appends) and the
 // queries' 1-bit codes as level one of the packed levels.
-// The +1 / -1 expansion of a 1-bit index's codes (1 byte per code), kept
-// current with the index's rows, with unit row scales and the rows' code
-// norms.
+// The codes of a 1-bit or int4 index as int8 bytes (1 byte per code), kept
+// current with the index's rows, for the first-level pass: 1-bit codes as
+// +1 / -1 with unit row multipliers, int4 codes as their signed values with
+// the multipliers f32(scale * f32(1/7)); and the rows' code norms.
 static int ensure_pm_rows(bv_index *idx) {
     hipStream_t s = idx->stream;
     const uint32_t P = idx->P, W1 = idx->words_per_row;
@@ -1632,11 +1633,21 @@ static int ensure_pm_rows(bv_index *idx) {
         HIPX(idx->dev, idx->pm_codes.ensure(n * P, n0 * P, s), "expanded code buffer");
         HIPX(idx->dev, idx->pm_ones.ensure(n * 4, n0 * 4, s), "scale buffer");
         HIPX(idx->dev, idx->pm_cn.ensure(n * 4, n0 * 4, s), "norm buffer");
-        HIPX(idx->dev,
-             launch_expand_pm(idx->codes.as<uint32_t>() + n0 * W1, (n - n0) * W1,
-                              idx->pm_codes.as<uint32_t>() + n0 * (P / 4), s),
-             "expand kernel");
-        HIPX(idx->dev, launch_fill_f32(idx->pm_ones.as<float>() + n0, n - n0, 1.0f, s), "fill kernel");
+        if (idx->codec == C_Q4) {
+            HIPX(idx->dev,
+                 launch_expand_q4(idx->codes.as<uint32_t>() + n0 * W1, (n - n0) * W1,
+                                  idx->pm_codes.as<uint32_t>() + n0 * (P / 4), s),
+                 "expand kernel");
+            HIPX(idx->dev,
+                 launch_scale_mul(idx->scales.as<float>() + n0, n - n0, 1.0f / 7.0f, idx->pm_ones.as<float>() + n0, s),
+                 "scale kernel");
+        } else {
+            HIPX(idx->dev,
+                 launch_expand_pm(idx->codes.as<uint32_t>() + n0 * W1, (n - n0) * W1,
+                                  idx->pm_codes.as<uint32_t>() + n0 * (P / 4), s),
+                 "expand kernel");
+            HIPX(idx->dev, launch_fill_f32(idx->pm_ones.as<float>() + n0, n - n0, 1.0f, s), "fill kernel");
+        }
         HIPX(idx->dev,
              launch_row_code_norms(idx->pm_codes.as<uint32_t>() + n0 * (P / 4), n - n0, P / 4,
                                    idx->pm_cn.as<float>() + n0, s),
@@ -1743,6 +1754,13 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
         rc = ensure_pm_rows(idx);
         if (!rc) rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride, C_Q4M);
         src = Q8Source{idx->pm_codes.as<uint32_t>(), idx->P / 4, idx->scales.as<float>(), idx->pm_ones.as<float>()};
+    } else if (idx->codec == C_Q4) {
+        // int4: the pass over the codes' signed bytes with the query's int8
+        // levels without the 1/127 (C_Q4M), the rows' multipliers
+        // f32(scale / 7) and code norms; re-scored like the 1-bit batch
+        rc = ensure_pm_rows(idx);
+        if (!rc) rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride, C_Q4M);
+        src = Q8Source{idx->pm_codes.as<uint32_t>(), idx->P / 4, idx->pm_ones.as<float>(), idx->pm_cn.as<float>()};
     } else {
         rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride);
     }
@@ -1860,7 +1878,8 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
          launch_mq1_keep(m.cand, m.up_out, m.cnt, cap, idx->mq_tau.as<uint64_t>(), idx->mq_rows.as<uint32_t>(),
                          idx->mq_kept.as<uint32_t>(), nq, s),
          "batched keep kernel");
-    if (asym1) return finish_batched_indexed(idx, d_q, nq, kprime, k_out, rerank, cap, d_rows, d_scores, d_n);
+    if (asym1 || idx->codec == C_Q4)
+        return finish_batched_indexed(idx, d_q, nq, kprime, k_out, rerank, cap, d_rows, d_scores, d_n);
     // exact keys of those rows, the best kprime of them, and the re-rank
     HIPX(idx->dev,
          launch_mq1_exact(m.codes, m.W, m.scales, qlev, qstride, units16, idx->mq_rows.as<uint32_t>(),
@@ -1916,7 +1935,8 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
 static int run_batched(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kprime, uint32_t k_out, bool rerank,
                        uint32_t *d_rows, float *d_scores, uint32_t *d_n) {
     if (!idx->quant) return run_batched_f32(idx, d_q, nq, kprime, k_out, d_rows, d_scores, d_n);
-    if ((idx->codec == C_Q8 || idx->codec == C_HAM || idx->codec == C_Q1P || idx->codec == C_Q1A) &&
+    if ((idx->codec == C_Q8 || idx->codec == C_Q4 || idx->codec == C_HAM || idx->codec == C_Q1P ||
+         idx->codec == C_Q1A) &&
         idx->rows > MQ_SAMPLE)
         return run_batched_q8(idx, d_q, nq, kprime, k_out, rerank, d_rows, d_scores, d_n);
     const unsigned char *qscan = (const unsigned char *)d_q;  // fp32 rows: the queries as they are

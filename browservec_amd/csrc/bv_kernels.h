@@ -415,6 +415,10 @@ hipError_t launch_ivf_list_scan(const uint32_t *codes, uint32_t W, uint32_t bits
 // ---- Hamming batches on the int8 first-level path (bv_mq.hip) ---------------
 // 1-bit codes (words 32-bit words) as +1 / -1 int8 codes (8 words out per word in).
 hipError_t launch_expand_pm(const uint32_t *bits, uint64_t words, uint32_t *out, hipStream_t s);
+// int4 codes (words of 8 nibbles) as signed bytes, one per code; and
+// dst[i] = f32(src[i] * mul).
+hipError_t launch_expand_q4(const uint32_t *nib, uint64_t words, uint32_t *out, hipStream_t s);
+hipError_t launch_scale_mul(const float *src, uint64_t n, float mul, float *dst, hipStream_t s);
 // Queries' 1-bit codes (P / 32 words each) as packed levels: level one +1 / -1,
 // the other levels zero, tail scales (1, 0, 0).
 hipError_t launch_pm_levels(const uint32_t *qbits, uint32_t nq, uint32_t P, unsigned char *qlev, uint64_t stride,

@@ -1665,6 +1665,29 @@ __global__ __launch_bounds__(256) void expand_pm(const uint32_t *bits, uint64_t 
     }
 }
 
+// int4 codes as signed bytes, one per code (nibble j of word g -> byte
+// 8g + j, value n - 16 (n >> 3)), for the first-level pass of int4 batches;
+// and the rows' score multipliers f32(scale * f32(1/7)), as the
+// single-query scan forms them.
+__global__ __launch_bounds__(256) void expand_q4(const uint32_t *nib, uint64_t words, uint32_t *out) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += stride) {
+        const uint32_t w = nib[i];
+        uint32_t b[2] = {0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int32_t n = (int32_t)((w >> (4 * j)) & 0xfu);
+            b[j >> 2] |= ((uint32_t)(n - 16 * (n >> 3)) & 0xffu) << (8 * (j & 3));
+        }
+        ((uint2 *)out)[i] = make_uint2(b[0], b[1]);
+    }
+}
+
+__global__ __launch_bounds__(256) void scale_mul_f32(const float *src, uint64_t n, float mul, float *dst) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) dst[i] = src[i] * mul;
+}
+
 // A query's 1-bit code as the batched scan's packed levels: level one the
 // +1 / -1 bytes, levels two and three zero, scales (1, 0, 0).
 __global__ __launch_bounds__(64) void pm_levels(const uint32_t *qbits, uint32_t P, unsigned char *qlev,
@@ -1696,6 +1719,20 @@ __global__ __launch_bounds__(256) void fill_f32(float *p, uint64_t n, float v) {
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) p[i] = v;
 }
 }  // namespace
+
+hipError_t launch_expand_q4(const uint32_t *nib, uint64_t words, uint32_t *out, hipStream_t s) {
+    if (words == 0) return hipSuccess;
+    const uint64_t blocks = std::min<uint64_t>((words + 255) / 256, 65536);
+    hipLaunchKernelGGL(expand_q4, dim3((uint32_t)blocks), dim3(256), 0, s, nib, words, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_scale_mul(const float *src, uint64_t n, float mul, float *dst, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(scale_mul_f32, dim3((uint32_t)blocks), dim3(256), 0, s, src, n, mul, dst);
+    return hipGetLastError();
+}
 
 hipError_t launch_expand_pm(const uint32_t *bits, uint64_t words, uint32_t *out, hipStream_t s) {
     if (words == 0) return hipSuccess;
