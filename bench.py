@@ -52,9 +52,10 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def make_data(n, dim, nclusters, sigma, nq, qsigma, seed):
+def make_data(n, dim, nclusters, sigma, nq, qsigma, seed, with_source=False):
     """Gaussian mixture (unit-norm centres + sigma N(0,1), rows normalized)
-    and noisy corpus rows as queries, generated on the device."""
+    and noisy corpus rows as queries, generated on the device (with_source:
+    also each query's source row)."""
     import torch
 
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -71,7 +72,15 @@ def make_data(n, dim, nclusters, sigma, nq, qsigma, seed):
     q = x[pick] + qsigma * torch.randn(nq, dim, generator=g, device="cuda")
     q /= q.norm(dim=1, keepdim=True)
     torch.cuda.synchronize()
+    if with_source:
+        return x.contiguous(), q.contiguous(), pick.cpu().numpy()
     return x.contiguous(), q.contiguous()
+
+
+def recall_at_1_source(rows_got, source):
+    """The share of queries whose first result is the corpus row the query
+    was drawn from (a control that needs no ground-truth scan)."""
+    return float(np.mean(rows_got[:, 0].astype(np.int64) == source.astype(np.int64)))
 
 
 def timed_search(idx, d_q, nq_total, batch, steps, warmup, fetch, k, torch, outs=1):
@@ -287,7 +296,7 @@ def bench_c4(ctx, torch, budget_s):
     from browservec_amd import QuantIndex
 
     n, dim, nq, fetch, k = 4_000_000, 1024, 256, 200, 10
-    x, q = make_data(n, dim, 1024, 0.1, nq, 0.05, 0xB5EC0004)
+    x, q, src_rows = make_data(n, dim, 1024, 0.1, nq, 0.05, 0xB5EC0004, with_source=True)
     res = {}
     for name, bits, scorer in (("int4", 4, "asym"), ("1bit_asym", 1, "asym"), ("1bit_hamming", 1, "hamming")):
         idx = QuantIndex(ctx, dim, bits=bits, scorer=scorer)
@@ -305,7 +314,8 @@ def bench_c4(ctx, torch, budget_s):
         rb = dim * bits // 8
         res[name] = {"batch1_qps": round(b1, 1), "batch256_qps": round(b256, 1),
                      "roofline_b1": hbm_roof(n * (rb + 4) + fetch * dim * 4, kus),
-                     "encode_s": round(enc_s, 3), "rows_q": rows_q, "rows_wide": rows_wide}
+                     "encode_s": round(enc_s, 3), "rows_q": rows_q, "rows_wide": rows_wide,
+                     "recall_at_1_source_row": round(recall_at_1_source(rows_q, src_rows), 4)}
         idx.destroy()
         free(torch)
     for key in res:
@@ -329,7 +339,7 @@ def bench_c5(ctx, torch, budget_s):
     from browservec_amd import IVFQuantIndex
 
     n, dim, nq, fetch, k, nprobe = 4_000_000, 768, 1024, 40, 10, 32
-    x, q = make_data(n, dim, 4096, 0.15, nq, 0.05, 0xB5EC0005)
+    x, q, src_rows = make_data(n, dim, 4096, 0.15, nq, 0.05, 0xB5EC0005, with_source=True)
     idx = IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 4096, "iters": 20, "nprobe": nprobe})
     t0 = time.perf_counter()
     idx.append_device(x.data_ptr(), n)
@@ -360,6 +370,21 @@ def bench_c5(ctx, torch, budget_s):
         rows_all.append(r)
     recall_all = recall_vs_flat(ctx, x, q[:64].contiguous(), np.concatenate(rows_all), k, torch)
     idx.destroy()
+    # control: the same lists trained on every row (sampleSize = trainSize =
+    # N, the reservoir holding all rows): if recall stays low, the loss is the
+    # workload's (noise norm ~4 per row against unit centres), not the
+    # 16,384-row training sample's
+    full = IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 4096, "iters": 20, "nprobe": nprobe, "sampleSize": n,
+                                                "trainSize": n})
+    full.append_device(x.data_ptr(), n)
+    full.sync()
+    t0 = time.perf_counter()
+    full.build()
+    build_full_s = time.perf_counter() - t0
+    rows_full = device_rows(full, q, fetch, k, torch, chunk=nq)
+    recall_full = recall_vs_flat(ctx, x, q, rows_full, k, torch)
+    full.destroy()
+    free(torch)
     cpu = None
     if budget_s > 0:
         cpu = cpu_entry(x.cpu().numpy(), q[:16].cpu().numpy(), "cosine", budget_s,
@@ -374,6 +399,11 @@ def bench_c5(ctx, torch, budget_s):
             "roofline_b1_list_scan": dict(hbm_roof(list_bytes + fetch * dim * 4, kus),
                                           avg_scanned_rows=round(scanned, 1)),
             "recall_at_10": round(recall, 4), "recall_at_10_all_lists_64q": round(recall_all, 4),
+            "recall_at_1_source_row": round(recall_at_1_source(rows_q, src_rows), 4),
+            "control_train_on_all_rows": {"sampleSize": n, "trainSize": n, "build_s": round(build_full_s, 3),
+                                          "recall_at_10": round(recall_full, 4),
+                                          "recall_at_1_source_row": round(recall_at_1_source(rows_full, src_rows),
+                                                                          4)},
             "build_s": round(build_s, 3), "build_ms_device": round(st["build_ms"], 1), "encode_s": round(enc_s, 3),
             "nlist": st["nlist"], "nprobe": nprobe, "cpu_baseline": cpu}
 
@@ -562,7 +592,7 @@ def main():
 
     seed = 0xB5EC0001
     log("generating data", args.rows, args.dim)
-    x, q = make_data(args.rows, args.dim, 1024, 0.1, args.queries, 0.05, seed)
+    x, q, src_rows = make_data(args.rows, args.dim, 1024, 0.1, args.queries, 0.05, seed, with_source=True)
 
     log("building int8 index")
     t0 = time.perf_counter()
@@ -734,6 +764,7 @@ def main():
                                "codes_read_gbs": round(args.rows * (row_bytes + 4) * qps_b256 / nb / 1e9, 1),
                                "trace_source": "profiles/mq1_scan_q8_1Mx768_b256.md"},
         "recall_at_10": round(recall, 4),
+        "recall_at_1_source_row": round(recall_at_1_source(rows_q, src_rows), 4),
         "end_to_end_hbm_frac_b1": round(algo_bytes_q * qps_b1 / (HBM_PEAK_GBS * 1e9), 4),
         "end_to_end_hbm_frac_b1_one_stream": round(algo_bytes_q * qps_b1_serial / (HBM_PEAK_GBS * 1e9), 4),
         "latency_ms_sync_p50": round(lat_p50, 4),

@@ -788,6 +788,7 @@ static int append_common(bv_index *idx, const float *data, bool device_src, uint
     if (idx->ivf) ivf_commit(idx, base, plan, extend);
     HIPX(idx->dev, hipStreamSynchronize(idx->stream), "append");
     idx->rows = total;
+    if (idx->ivf_pend.cap > (64ull << 20)) idx->ivf_pend.release();  // a large staging buffer is not kept
     return lanes_mark(idx);
 }
 
