@@ -72,22 +72,22 @@ __global__ __launch_bounds__(256) void ivf_normalize_rows(float *m, uint32_t row
 constexpr int AT = 128;  // rows and centroids per tile
 constexpr int AK = 8;    // dimension chunk per LDS stage
 
+// dq8: for int8 codes, max(f32(b / 127), -1) of every byte b (the
+// correctly rounded quotient, as the per-element division gives it), in LDS.
 template <int BITS> struct RowLoader;
 template <> struct RowLoader<0> {  // fp32 rows
-    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i) {
+    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i, const float *) {
         return a.rows[r * a.row_stride + i];
     }
 };
 template <> struct RowLoader<8> {  // unpack4x8snorm(b) * scale
-    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i) {
+    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i, const float *dq8) {
         const uint32_t w = a.codes[r * a.words_per_row + (i >> 2)];
-        const int8_t b = (int8_t)((w >> (8 * (i & 3))) & 0xffu);
-        const float u = fmaxf((float)b / 127.0f, -1.0f);
-        return u * a.scales[r];
+        return dq8[(w >> (8 * (i & 3))) & 0xffu] * a.scales[r];
     }
 };
 template <> struct RowLoader<4> {  // signed nibble * (scale * f32(1/7))
-    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i) {
+    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i, const float *) {
         const uint32_t w = a.codes[r * a.words_per_row + (i >> 3)];
         const int32_t n = (int32_t)((w >> (4 * (i & 7))) & 0xfu);
         const float inv7 = a.scales[r] * (1.0f / 7.0f);
@@ -95,7 +95,7 @@ template <> struct RowLoader<4> {  // signed nibble * (scale * f32(1/7))
     }
 };
 template <> struct RowLoader<1> {  // sign bits as +-1 (the scale multiplies the sum)
-    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i) {
+    static __device__ __forceinline__ float get(const IvfAssignArgs &a, uint64_t r, uint32_t i, const float *) {
         const uint32_t w = a.codes[r * a.words_per_row + (i >> 5)];
         return ((w >> (i & 31)) & 1u) ? 1.0f : -1.0f;
     }
@@ -105,8 +105,13 @@ template <int BITS, bool SPLIT>
 __global__ __launch_bounds__(256) void ivf_assign(IvfAssignArgs a) {
     __shared__ float As[AK][AT + 4];
     __shared__ float Bs[AK][AT + 4];
+    __shared__ float dq8[BITS == 8 ? 256 : 1];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     const uint64_t r0 = (uint64_t)blockIdx.x * AT;
+    if constexpr (BITS == 8) {
+        dq8[tid] = fmaxf((float)(int8_t)(uint8_t)tid / 127.0f, -1.0f);
+        __syncthreads();
+    }
     uint64_t best[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) best[i] = 0;
@@ -125,7 +130,7 @@ __global__ __launch_bounds__(256) void ivf_assign(IvfAssignArgs a) {
                 const int kk = e % AK, rr = e / AK;  // consecutive lanes read consecutive elements of a row
                 const uint32_t k = k0 + kk;
                 const uint64_t r = r0 + rr;
-                As[kk][rr] = (r < a.n && k < a.dim) ? RowLoader<BITS>::get(a, r, k) : 0.0f;
+                As[kk][rr] = (r < a.n && k < a.dim) ? RowLoader<BITS>::get(a, r, k, dq8) : 0.0f;
                 const uint32_t c = c0 + rr;
                 Bs[kk][rr] = (c < a.nlist && k < a.dim) ? a.centroids[(uint64_t)c * a.cen_stride + k] : 0.0f;
             }
