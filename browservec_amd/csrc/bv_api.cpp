@@ -1758,7 +1758,9 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     } else if (idx->codec == C_Q4) {
         // int4: the pass over the codes' signed bytes with the query's int8
         // levels without the 1/127 (C_Q4M), the rows' multipliers
-        // f32(scale / 7) and code norms; re-scored like the 1-bit batch
+        // f32(scale * f32(1/7)) and code norms.  The exact step below then
+        // forms the single-query int4 key: the byte dots are the nibble dots
+        // the int4 scan recovers, combined with the same level steps.
         rc = ensure_pm_rows(idx);
         if (!rc) rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride, C_Q4M);
         src = Q8Source{idx->pm_codes.as<uint32_t>(), idx->P / 4, idx->pm_ones.as<float>(), idx->pm_cn.as<float>()};
@@ -1879,8 +1881,7 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
          launch_mq1_keep(m.cand, m.up_out, m.cnt, cap, idx->mq_tau.as<uint64_t>(), idx->mq_rows.as<uint32_t>(),
                          idx->mq_kept.as<uint32_t>(), nq, s),
          "batched keep kernel");
-    if (asym1 || idx->codec == C_Q4)
-        return finish_batched_indexed(idx, d_q, nq, kprime, k_out, rerank, cap, d_rows, d_scores, d_n);
+    if (asym1) return finish_batched_indexed(idx, d_q, nq, kprime, k_out, rerank, cap, d_rows, d_scores, d_n);
     // exact keys of those rows, the best kprime of them, and the re-rank
     HIPX(idx->dev,
          launch_mq1_exact(m.codes, m.W, m.scales, qlev, qstride, units16, idx->mq_rows.as<uint32_t>(),
