@@ -211,12 +211,13 @@ struct bv_index {
     // own scan scratch, so one query's tail overlaps the next one's scan
     struct ScanLane {
         hipStream_t stream = nullptr;
-        hipEvent_t done = nullptr;
         DevBuf qstate, wmax, cand_keys, merged, merged_n;
+        uint64_t mut_seen = 0;                // the ev_mut record this stream last waited on
     } lane2;
     uint32_t query_streams = 1, next_lane = 0;
     bool lane2_pending = false;               // lane2 has queries the index stream has not joined
     hipEvent_t ev_mut = nullptr;              // recorded after work that changes the index's buffers
+    uint64_t mut_gen = 0;                     // counts the ev_mut records
 
     // kernel timing
     bool timing = false;
@@ -429,7 +430,6 @@ extern "C" int bv_index_destroy(bv_index *idx) {
     if (idx->ev0) (void)hipEventDestroy(idx->ev0);
     if (idx->ev1) (void)hipEventDestroy(idx->ev1);
     if (idx->lane2.stream) (void)hipStreamSynchronize(idx->lane2.stream);
-    if (idx->lane2.done) (void)hipEventDestroy(idx->lane2.done);
     if (idx->lane2.stream) (void)hipStreamDestroy(idx->lane2.stream);
     if (idx->ev_mut) (void)hipEventDestroy(idx->ev_mut);
     if (idx->copy_stream) (void)hipStreamSynchronize(idx->copy_stream);
@@ -1229,6 +1229,7 @@ static int lanes_join(bv_index *idx) {
 static int lanes_mark(bv_index *idx) {
     if (!idx->lane2.stream) return BV_OK;
     HIPX(idx->dev, hipEventRecord(idx->ev_mut, idx->stream), "event");
+    idx->mut_gen++;
     return BV_OK;
 }
 
@@ -1309,9 +1310,14 @@ static int prepare_queries(bv_index *idx, const float *d_q, uint32_t nq, const v
 static void timing_begin(bv_index *idx, hipStream_t s = nullptr) {
     if (!idx->timing) return;
     if (idx->tev_used == idx->tev.size()) {
+        // Timing-only events: no system-scope fence at the record (its L2
+        // write-back would stall the next launch and show up in the timing).
         hipEvent_t a, b;
-        if (hipEventCreate(&a) != hipSuccess) return;
-        if (hipEventCreate(&b) != hipSuccess) return;
+        if (hipEventCreateWithFlags(&a, hipEventDisableSystemFence) != hipSuccess) return;
+        if (hipEventCreateWithFlags(&b, hipEventDisableSystemFence) != hipSuccess) {
+            (void)hipEventDestroy(a);
+            return;
+        }
         idx->tev.push_back({a, b});
     }
     (void)hipEventRecord(idx->tev[idx->tev_used].first, s ? s : idx->stream);
@@ -1382,7 +1388,11 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
         if (idx->next_lane == 1) {
             lane = &idx->lane2;
             s = lane->stream;
-            HIPX(idx->dev, hipStreamWaitEvent(s, idx->ev_mut, 0), "event wait");
+            // (the stream is in order: one wait covers every later query on it)
+            if (lane->mut_seen != idx->mut_gen) {
+                HIPX(idx->dev, hipStreamWaitEvent(s, idx->ev_mut, 0), "event wait");
+                lane->mut_seen = idx->mut_gen;
+            }
         }
         idx->next_lane ^= 1u;
     }
@@ -1414,10 +1424,7 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
     timing_begin(idx, s);
     HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, s), "scan kernel");
     timing_end(idx, s);
-    if (lane) {
-        HIPX(idx->dev, hipEventRecord(lane->done, s), "event");
-        idx->lane2_pending = true;
-    }
+    if (lane) idx->lane2_pending = true;
     idx->last_scanned = n * nq;
     return BV_OK;
 }
@@ -2378,9 +2385,9 @@ extern "C" int bv_index_set_query_streams(bv_index *idx, uint32_t n) {
     if (n != 1 && n != 2) return fail(BV_E_INVALID, "query streams must be 1 or 2, got %u", n);
     if (n == 2 && !idx->lane2.stream) {
         HIPX(idx->dev, hipStreamCreateWithFlags(&idx->lane2.stream, hipStreamNonBlocking), "query stream");
-        HIPX(idx->dev, hipEventCreateWithFlags(&idx->lane2.done, hipEventDisableTiming), "event");
         HIPX(idx->dev, hipEventCreateWithFlags(&idx->ev_mut, hipEventDisableTiming), "event");
         HIPX(idx->dev, hipEventRecord(idx->ev_mut, idx->stream), "event");
+        idx->mut_gen++;
     }
     rc = lanes_join(idx);
     if (rc) return rc;
