@@ -406,7 +406,8 @@ def bench_c5(ctx, torch, budget_s):
                                           "recall_at_10": round(recall_full, 4),
                                           "recall_at_1_source_row": round(recall_at_1_source(rows_full, src_rows),
                                                                           4)},
-            "build_s": round(build_s, 3), "build_ms_device": round(st["build_ms"], 1), "encode_s": round(enc_s, 3),
+            "build_s": round(build_s, 3), "build_ms_device": round(st["build_ms"], 1),
+            "build_final_assign_exact_rows": int(st["build_exact_rows"]), "encode_s": round(enc_s, 3),
             "nlist": st["nlist"], "nprobe": nprobe, "cpu_baseline": cpu}
 
 

@@ -74,6 +74,7 @@ class IndexStats(ctypes.Structure):
         ("build_ms", ctypes.c_double),
         ("device_bytes", ctypes.c_uint64),
         ("last_scanned_rows", ctypes.c_uint64),
+        ("build_exact_rows", ctypes.c_uint64),
     ]
 
 

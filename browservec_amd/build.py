@@ -22,7 +22,7 @@ ARCH = os.environ.get("BV_OFFLOAD_ARCH", "gfx950")
 SCAN_CODECS = ["f32dot", "f32l2", "q8", "q4", "q1a", "q1p", "ham", "i8s", "f32dot_s", "f32l2_s"]
 SOURCES = (["bv_kernels.hip"] + [f"bv_scan_{c}.hip" for c in SCAN_CODECS] +
            ["bv_ivf.hip", "bv_mq.hip", "bv_select.hip", "bv_graph.hip", "bv_api.cpp"])
-HEADERS = ["bv_kernels.h", "bv_device.h", "bv_scan.h"]
+HEADERS = ["bv_kernels.h", "bv_device.h", "bv_scan.h", "bv_mfma.h"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -201,6 +201,9 @@ struct bv_index {
     DevBuf ivf_idx, ivf_idx2, ivf_slot, ivf_assign, ivf_hist, ivf_base, ivf_totals, ivf_toff, ivf_trows;
     DevBuf ivf_pend;  // an append's sampled rows (rotated), scattered into `sample` once nothing can fail
     DevBuf ivf_keys;  // the split assignment's per-row keys
+    DevBuf ivf_lev, ivf_ls, ivf_mwords, ivf_queue;  // the matrix-core assignment's scratch
+    uint64_t ivf_exact_rows = 0;              // rows the last assignment gave the exact arithmetic alone
+    uint64_t build_exact_rows = 0;            // the same, for the last build's final assignment
     DevBuf probe_scores, probes, cand_tot, cand_off;
     double build_ms = 0;
     double last_query_ms = 0, last_query_gpu_ms = 0;
@@ -507,6 +510,50 @@ static void ivf_commit(bv_index *idx, uint64_t base, const ReservoirPlan &pl, bo
     if (!extended) idx->built_rows = ~0ull;
 }
 
+// The matrix-core assignment of int8 codes (the final pass of a build and
+// incremental appends): its scratch for n rows and nlist centroids, taken
+// before anything is assigned.
+static int ivf_assign_reserve(bv_index *idx, uint64_t n, uint32_t nlist) {
+    const int bits = idx->quant ? (int)idx->d.bits : 0;
+    const uint32_t P = idx->sample_dim;
+    if (!ivf_assign_mfma_ok(bits, P, nlist) || n == 0) return BV_OK;
+    hipStream_t s = idx->stream;
+    const size_t pad = ivf_mfma_nlist_pad(nlist);
+    HIPX(idx->dev, idx->ivf_lev.ensure(pad * 2 * P, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_ls.ensure(pad * 2 * 4, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_mwords.ensure(8, 0, s), "scratch");
+    HIPX(idx->dev, idx->ivf_queue.ensure((size_t)ivf_mfma_qcap(n) * sizeof(IvfRecheck), 0, s), "scratch");
+    HIPX(idx->dev, idx->h_cnt.ensure(8), "pinned buffer");
+    return BV_OK;
+}
+
+// The assignment of fa.n rows to the centroids (fa.out): int8 codes of a
+// padded dimension the matrix pass takes go through it and the exact
+// re-check of the rows it leaves open (same result as ivf_assign<8>), every
+// other kind through ivf_assign.  Waits for the device.
+static int ivf_assign_rows(bv_index *idx, const IvfAssignArgs &fa, int bits) {
+    hipStream_t s = idx->stream;
+    idx->ivf_exact_rows = fa.n;
+    if (!ivf_assign_mfma_ok(bits, fa.dim, fa.nlist) || fa.n == 0) {
+        HIPX(idx->dev, ivf_launch_assign(fa, bits, s), "assign kernel");
+        return BV_OK;
+    }
+    IvfMfmaScratch m{idx->ivf_lev.as<int8_t>(), idx->ivf_ls.as<float>(), idx->ivf_mwords.as<uint32_t>(),
+                     idx->ivf_queue.as<IvfRecheck>(), ivf_mfma_qcap(fa.n)};
+    HIPX(idx->dev, ivf_launch_assign_mfma(fa, m, s), "assign kernel");
+    uint32_t *h = (uint32_t *)idx->h_cnt.p;
+    HIPX(idx->dev, hipMemcpyAsync(h, m.words + 1, 4, hipMemcpyDeviceToHost, s), "count download");
+    HIPX(idx->dev, hipStreamSynchronize(s), "assign kernel");
+    const uint32_t queued = h[0];
+    if (queued > m.qcap) {  // more open rows than the queue holds: every row exactly
+        HIPX(idx->dev, ivf_launch_assign(fa, bits, s), "assign kernel");
+        return BV_OK;
+    }
+    HIPX(idx->dev, ivf_launch_assign_recheck(fa, m, queued, s), "assign kernel");
+    idx->ivf_exact_rows = queued;
+    return BV_OK;
+}
+
 // Incremental append: rows [base, base + count) assigned to the current
 // centroids with the build's final-assignment arithmetic, then merged into
 // the lists (each list: its rows, then the new ones, ascending).  The lists
@@ -519,6 +566,8 @@ static int ivf_extend_reserve(bv_index *idx, uint64_t base, uint64_t count) {
     const uint32_t nblk = ivf_list_blocks(count);
     HIPX(idx->dev, idx->ivf_assign.ensure(count * 4, 0, s), "scratch");
     if (ivf_assign_split(count)) HIPX(idx->dev, idx->ivf_keys.ensure(count * 8, 0, s), "scratch");
+    int rc = ivf_assign_reserve(idx, count, nlist);
+    if (rc) return rc;
     HIPX(idx->dev, idx->ivf_hist.ensure((size_t)std::max(nblk, 1u) * nlist * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->ivf_base.ensure((size_t)std::max(nblk, 1u) * nlist * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->ivf_totals.ensure((size_t)nlist * 4, 0, s), "scratch");
@@ -550,7 +599,8 @@ static int ivf_extend_lists(bv_index *idx, uint64_t base, uint64_t count) {
         fa.rows = idx->raw.as<float>() + base * idx->dim;
         fa.row_stride = idx->dim;
     }
-    HIPX(idx->dev, ivf_launch_assign(fa, idx->quant ? (int)idx->d.bits : 0, s), "assign kernel");
+    int rc = ivf_assign_rows(idx, fa, idx->quant ? (int)idx->d.bits : 0);
+    if (rc) return rc;
     HIPX(idx->dev, ivf_launch_lists(fa.out, count, nlist, idx->ivf_hist.as<uint32_t>(), idx->ivf_base.as<uint32_t>(),
                                     idx->ivf_totals.as<uint32_t>(), idx->ivf_toff.as<uint32_t>(),
                                     idx->ivf_trows.as<uint32_t>(), s),
@@ -1042,7 +1092,12 @@ static int ivf_build(bv_index *idx) {
         fa.rows = idx->raw.as<float>();
         fa.row_stride = idx->dim;
     }
-    HIPX(idx->dev, ivf_launch_assign(fa, idx->quant ? (int)idx->d.bits : 0, s), "assign kernel");
+    {
+        int rc = ivf_assign_reserve(idx, rows, nlist);
+        if (!rc) rc = ivf_assign_rows(idx, fa, idx->quant ? (int)idx->d.bits : 0);
+        if (rc) return rc;
+        idx->build_exact_rows = idx->ivf_exact_rows;
+    }
     HIPX(idx->dev, idx->list_off.ensure(((size_t)nlist + 1) * 4, 0, s), "lists");
     HIPX(idx->dev, idx->list_rows.ensure(std::max<uint64_t>(rows, 1) * 4, 0, s), "lists");
     HIPX(idx->dev, ivf_launch_lists(fa.out, rows, nlist, idx->ivf_hist.as<uint32_t>(), idx->ivf_base.as<uint32_t>(),
@@ -2785,6 +2840,7 @@ extern "C" int bv_index_get_stats(bv_index *idx, bv_index_stats *out) {
         out->nprobe = ivf_resolve_nprobe(idx);
         idx->nprobe_override = saved;
         out->build_ms = idx->build_ms;
+        out->build_exact_rows = idx->build_exact_rows;
         out->tuned_recall = idx->tuned_recall;
     }
     out->last_query_ms = idx->last_query_ms;

@@ -17,6 +17,7 @@
 //                        gatherCandidates (ivfquant.ts:513-527): the probed
 //                        lists concatenated in probe order
 #include "bv_kernels.h"
+#include "bv_mfma.h"
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -595,6 +596,384 @@ hipError_t ivf_launch_assign(const IvfAssignArgs &a, int bits, hipStream_t s) {
     hipError_t e = assign_bits<true>(a, bits, dim3(tiles, (a.nlist + AT - 1) / AT), s);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(ivf_assign_finish, dim3(flat), dim3(256), 0, s, a.keys, a.n, a.out);
+    return hipGetLastError();
+}
+
+// ------------------------------------------- assign on the matrix cores --
+// The assignment of int8 codes (every row of a build, the rows of an
+// incremental append) on v_mfma_i32_32x32x32_i8, with ivf_assign's exact
+// arithmetic kept for the rows whose winner the matrix pass cannot decide.
+//
+// ivf_cen_levels splits each centroid into two int8 levels,
+// c = s1 q1 + s2 q2 + e (s1 = max|c| / 127, s2 = max|c - s1 q1| / 127, e
+// exact in f64).  For a row with codes b and scale sc > 0 the exact score
+// s(c) is the fmaf chain over x_k = f32(f32(b_k / 127) sc) and c_k, and
+// v(c) = s1 (b.q1) + s2 (b.q2) with exact int32 dots.  With u = 2^-24:
+//   |s(c) - (sc / 127) v(c)| <= (sc / 127) |b| (|e_c| + (gamma_P + 3u) |c|)
+// (the chain's P roundings, the two roundings of each x_k, Cauchy-Schwarz on
+// the level residual), and the pass's f32 value of v is within 4u |b| |c| of
+// v.  So with M = max over centroids of |e_c| + (gamma_P + 7u) |c|, the
+// exact winner's f32 v is within W = 2 |b| M of the row's largest: a row
+// with one centroid in that window is decided.  The others go to the queue:
+// rows with several centroids in the window (their candidates), and rows
+// whose window may hold more than a lane keeps, whose scale is not a
+// positive finite number, or with a byte -128 (decoded as -1, outside the
+// levels' arithmetic), for which every centroid is re-scored.
+
+// Each lane keeps its row's best IVF_MQ_KEEP values over its half of the
+// centroids.
+constexpr int IVF_MQ_KEEP = 4;
+constexpr int IVF_MA_WAVES = 8;                  // waves per workgroup, 32 rows each
+constexpr int IVF_MA_ROWS = IVF_MA_WAVES * 32;
+
+namespace {
+
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ double wave_max_d(double v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v = fmax(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t b) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t x = ((uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)(b >> 32), o) << 32) |
+                           (uint32_t)__shfl_xor((int)(uint32_t)b, o);
+        b = x > b ? x : b;
+    }
+    return b;
+}
+
+// One wave per centroid (c < nlist rounded up to 32; the padding centroids
+// get zero levels): the two int8 levels (lev[c][0..1][P]), their scales
+// (ls[c][0..1]) and the bound term m_c, folded into words[0] with an atomic
+// maximum of its f32 bits (a non-finite centroid makes it +inf: every row is
+// then re-scored exactly).  P is a multiple of 64, at most 1024.
+__global__ __launch_bounds__(64) void ivf_cen_levels(const float *cen, uint32_t stride, uint32_t nlist, uint32_t P,
+                                                      int8_t *lev, float *ls, uint32_t *words) {
+    const uint32_t c = blockIdx.x, lane = threadIdx.x;
+    int8_t *q1 = lev + (uint64_t)c * 2 * P, *q2 = q1 + P;
+    if (c >= nlist) {
+        for (uint32_t i = lane; i < P; i += 64) q1[i] = q2[i] = 0;
+        if (lane == 0) ls[2 * c] = ls[2 * c + 1] = 0.0f;
+        return;
+    }
+    const uint32_t per = P / 64;
+    const float *v = cen + (uint64_t)c * stride;
+    float x[16];
+    bool finite = true;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        x[j] = (uint32_t)j < per ? v[lane + 64 * j] : 0.0f;
+        finite = finite && (fabsf(x[j]) < __builtin_inff());
+    }
+    float m1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) m1 = fmaxf(m1, fabsf(x[j]));
+    m1 = wave_max_f(m1);
+    const float s1 = m1 / 127.0f;
+    double r1[16];
+    double m2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        float q = s1 > 0.0f ? rintf(x[j] / s1) : 0.0f;
+        q = fminf(fmaxf(q, -127.0f), 127.0f);
+        if ((uint32_t)j < per) q1[lane + 64 * j] = (int8_t)(int)q;
+        r1[j] = (double)x[j] - (double)s1 * (double)q;  // exact: at most 32 significant bits
+        m2 = fmax(m2, fabs(r1[j]));
+    }
+    m2 = wave_max_d(m2);
+    const float s2 = (float)(m2 / 127.0);
+    double ee = 0.0, cc = 0.0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        double q = s2 > 0.0f ? rint(r1[j] / (double)s2) : 0.0;
+        q = fmin(fmax(q, -127.0), 127.0);
+        if ((uint32_t)j < per) q2[lane + 64 * j] = (int8_t)(int)q;
+        const double e = r1[j] - (double)s2 * q;  // exact
+        ee = fma(e, e, ee);
+        cc = fma((double)x[j], (double)x[j], cc);
+    }
+    ee = wave_sum_d(ee);
+    cc = wave_sum_d(cc);
+    const bool all_finite = __all(finite) && s2 == s2;
+    if (lane == 0) {
+        ls[2 * c] = s1;
+        ls[2 * c + 1] = s2;
+        const double u = 0x1p-24, gamma = (double)P * u / (1.0 - (double)P * u);
+        // (the sums' and square roots' own rounding: well inside 1e-12)
+        const double m = (sqrt(ee) + (gamma + 7.0 * u) * sqrt(cc)) * (1.0 + 1e-12);
+        const float mf = all_finite ? (float)(m * (1.0 + 0x1p-20)) : __builtin_inff();  // rounded up
+        atomicMax(&words[0], __float_as_uint(mf));
+    }
+}
+
+__global__ __launch_bounds__(64) void ivf_mfma_words_zero(uint32_t *words) {
+    if (threadIdx.x < 2) words[threadIdx.x] = 0;
+}
+
+// The matrix pass: a workgroup of IVF_MA_WAVES waves takes 256 rows; each
+// wave holds its 32 rows' codes in registers (lane l: row l % 32, units
+// 2 st + l / 32 -- the B operand of K step st) for the whole launch, and the
+// centroids' levels stream through four LDS buffers in half tiles (32
+// centroids, one level), three in flight while one is multiplied.  The
+// output of a 32 x 32 MFMA gives lane (h, c) the 16 centroids 8 (r / 4) +
+// 4 h + r % 4 of its row c.
+template <int S>
+__global__ __launch_bounds__(IVF_MA_WAVES * 64) void ivf_assign_mfma(IvfAssignArgs a, IvfMfmaScratch m,
+                                                                      uint32_t tiles) {
+    constexpr uint32_t U = 2 * S;                    // 16-byte units per centroid level
+    constexpr uint32_t RS = U + 1;                   // LDS stride in units (one unit of padding)
+    constexpr uint32_t PER = 32 / IVF_MA_WAVES;      // centroid rows each wave loads per half tile
+    __shared__ v4i tb0[32 * RS], tb1[32 * RS], tb2[32 * RS], tb3[32 * RS];
+    __shared__ __attribute__((aligned(16))) float sb0[32], sb1[32], sb2[32], sb3[32];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane >> 5, c = lane & 31;
+    const uint64_t row = (uint64_t)blockIdx.x * IVF_MA_ROWS + (uint64_t)wave * 32 + c;
+    const uint64_t rowc = row < a.n ? row : a.n - 1;
+    const v4i *rsrc = (const v4i *)(a.codes + rowc * a.words_per_row);
+    v4i br[S];
+#pragma unroll
+    for (int st = 0; st < S; ++st) br[st] = rsrc[2 * st + h];
+    const uint32_t nh = 2 * tiles;
+
+    auto load_half = [&](uint32_t j, v4i *tl, float *sb) {
+        const uint32_t t = j >> 1, l = j & 1;
+        const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+        const uint32_t lb = lds_addr(&tl[wv * PER * RS]);
+        if ((uint32_t)lane < U) {
+#pragma unroll
+            for (uint32_t jj = 0; jj < PER; ++jj) {
+                const uint64_t cen = (uint64_t)t * 32 + wv * PER + jj;
+                lds_dma16((const v4i *)(m.lev + (cen * 2 + l) * (uint64_t)(U * 16)) + lane, lb + jj * RS * 16);
+            }
+        }
+        if (wv == 0 && lane < 32) lds_dma4(m.ls + ((uint64_t)t * 32 + lane) * 2 + l, lds_addr(sb));
+    };
+
+    float p[16];                 // the current tile's level-one terms s1 * D1
+    float tv[IVF_MQ_KEEP];       // the lane's best values, descending, and their centroids
+    uint32_t ti[IVF_MQ_KEEP];
+#pragma unroll
+    for (int i = 0; i < IVF_MQ_KEEP; ++i) tv[i] = -__builtin_inff(), ti[i] = 0xffffffffu;
+    auto run_half = [&](uint32_t j, const v4i *tl, const float *sb, v4i *ntl, float *nsb) {
+        // this wave's loads of half j have landed (those of j + 1 and j + 2,
+        // issued after them, may still run: vmcnt counts in issue order)
+        const uint32_t after = (nh - 1 - j) < 2 ? (nh - 1 - j) : 2;
+        if (wave == 0) {
+            if (after == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (PER + 1)));
+            else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER + 1));
+            else __builtin_amdgcn_s_waitcnt(0);
+        } else {
+            if (after == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER));
+            else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER));
+            else __builtin_amdgcn_s_waitcnt(0);
+        }
+        // every wave's loads of half j have landed and every wave is done with
+        // half j - 1's buffer, which half j + 3 now takes (the barrier waits
+        // for this wave's LDS reads only; the memory clobber keeps every
+        // access on its side)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (j + 3 < nh) load_half(j + 3, ntl, nsb);
+        v16i e2[2] = {v16i{}, v16i{}};
+        const v4i *A0 = tl + c * RS + h;
+        constexpr int PF = S < 4 ? S : 4;
+        v4i ar[PF];
+#pragma unroll
+        for (int st = 0; st < PF; ++st) ar[st] = A0[2 * st];
+#pragma unroll
+        for (int st = 0; st < S; ++st) {
+            const v4i x = ar[st % PF];
+            if (st + PF < S) ar[st % PF] = A0[2 * (st + PF)];
+            e2[st & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x, br[st], e2[st & 1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const v16i d = e2[0] + e2[1];
+        // the lane's centroids come in runs of four: one 16-byte LDS read per run
+        float sv[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const float4 s4 = *(const float4 *)&sb[8 * g + 4 * h];
+            sv[4 * g] = s4.x, sv[4 * g + 1] = s4.y, sv[4 * g + 2] = s4.z, sv[4 * g + 3] = s4.w;
+        }
+        if ((j & 1) == 0) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = sv[r] * (float)d[r];
+            return;
+        }
+        const uint32_t c0 = (j >> 1) * 32;
+        const bool full_tile = c0 + 32 <= a.nlist;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float v = fmaf(sv[r], (float)d[r], p[r]);
+            const uint32_t ci = c0 + 8 * (r >> 2) + 4 * (uint32_t)h + (r & 3);
+            if (v > tv[IVF_MQ_KEEP - 1] && (full_tile || ci < a.nlist)) {
+                // insertion into the descending list
+                float nv = v;
+                uint32_t ni = ci;
+#pragma unroll
+                for (int i = 0; i < IVF_MQ_KEEP; ++i) {
+                    const bool sw = nv > tv[i];
+                    const float ov = tv[i];
+                    const uint32_t oi = ti[i];
+                    tv[i] = sw ? nv : ov;
+                    ti[i] = sw ? ni : oi;
+                    nv = sw ? ov : nv;
+                    ni = sw ? oi : ni;
+                }
+            }
+        }
+    };
+
+    load_half(0, tb0, sb0);
+    if (nh > 1) load_half(1, tb1, sb1);
+    if (nh > 2) load_half(2, tb2, sb2);
+    for (uint32_t j = 0; j < nh; j += 4) {
+        run_half(j, tb0, sb0, tb3, sb3);
+        if (j + 1 >= nh) break;
+        run_half(j + 1, tb1, sb1, tb0, sb0);
+        if (j + 2 >= nh) break;
+        run_half(j + 2, tb2, sb2, tb1, sb1);
+        if (j + 3 >= nh) break;
+        run_half(j + 3, tb3, sb3, tb2, sb2);
+    }
+
+    // the row's |b|^2 and any byte -128 (this lane's half of the codes)
+    int nb2 = 0;
+    uint32_t m128 = 0;
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t x = (uint32_t)br[st][w];
+            nb2 = __builtin_amdgcn_sdot4(br[st][w], br[st][w], nb2, false);
+            const uint32_t y = x ^ 0x80808080u;  // a byte 0x80 becomes zero
+            m128 |= (y - 0x01010101u) & ~y & 0x80808080u;
+        }
+    nb2 += __shfl_xor(nb2, 32);
+    const bool bad = (m128 | (uint32_t)__shfl_xor((int)m128, 32)) != 0;
+    float pv[IVF_MQ_KEEP];
+    uint32_t pi[IVF_MQ_KEEP];
+#pragma unroll
+    for (int i = 0; i < IVF_MQ_KEEP; ++i) {
+        pv[i] = __shfl_xor(tv[i], 32);
+        pi[i] = (uint32_t)__shfl_xor((int)ti[i], 32);
+    }
+    if (h != 0 || row >= a.n) return;
+    const float sc = a.scales[row];
+    const double vmax = fmax((double)tv[0], (double)pv[0]);
+    const double W = 2.0 * sqrt((double)nb2) * (1.0 + 1e-12) * (double)__uint_as_float(m.words[0]);
+    const double thr = vmax - W;
+    bool all = bad || !(sc > 0.0f) || !(sc < __builtin_inff()) || !(thr > -__builtin_inf()) ||
+               (double)tv[IVF_MQ_KEEP - 1] >= thr || (double)pv[IVF_MQ_KEEP - 1] >= thr;
+    uint32_t cand[2 * IVF_MQ_KEEP - 2];
+    uint32_t nc = 0;
+#pragma unroll
+    for (int i = 0; i < IVF_MQ_KEEP - 1; ++i) {
+        if ((double)tv[i] >= thr) cand[nc++] = ti[i];
+        if ((double)pv[i] >= thr) cand[nc++] = pi[i];
+    }
+    if (!all && nc == 1) {
+        a.out[row] = cand[0];
+        return;
+    }
+    const uint32_t slot = atomicAdd(&m.words[1], 1u);
+    if (slot >= m.qcap) return;  // the caller sees the count and assigns every row exactly
+    IvfRecheck e;
+    e.row = (uint32_t)row;
+    e.n = (all || nc == 0) ? IVF_RECHECK_ALL : nc;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) e.c[i] = (uint32_t)i < nc ? cand[i] : 0u;
+    m.queue[slot] = e;
+}
+
+// The queued rows, one wave each: ivf_assign<8>'s arithmetic (the row's
+// values x_k = f32(f32(b_k / 127) * scale), staged in LDS, and an fmaf chain
+// over k in order per centroid), over the row's candidates or every
+// centroid, the lowest centroid winning ties.
+constexpr int IVF_RC_WAVES = 4;
+__global__ __launch_bounds__(IVF_RC_WAVES * 64) void ivf_assign_recheck(IvfAssignArgs a, IvfMfmaScratch m,
+                                                                         uint32_t entries) {
+    __shared__ __attribute__((aligned(16))) float xs[IVF_RC_WAVES][1024];
+    __shared__ float dq8[256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    dq8[threadIdx.x] = fmaxf((float)(int8_t)(uint8_t)threadIdx.x / 127.0f, -1.0f);
+    __syncthreads();
+    const uint32_t P = a.dim;
+    float *x = xs[wave];
+    for (uint32_t e = blockIdx.x * IVF_RC_WAVES + wave; e < entries; e += gridDim.x * IVF_RC_WAVES) {
+        const IvfRecheck *q = m.queue + e;
+        const uint64_t r = q->row;
+        const uint32_t qn = q->n;
+        const float sc = a.scales[r];
+        const uint32_t *w = a.codes + r * a.words_per_row;
+        for (uint32_t k = lane; k < P; k += 64) x[k] = dq8[(w[k >> 2] >> (8 * (k & 3))) & 0xffu] * sc;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const uint32_t cnt = qn == IVF_RECHECK_ALL ? a.nlist : qn;
+        uint64_t best = 0;
+        for (uint32_t j = lane; j < cnt; j += 64) {
+            const uint32_t ci = qn == IVF_RECHECK_ALL ? j : q->c[j];
+            const float4 *cv = (const float4 *)(a.centroids + (uint64_t)ci * a.cen_stride);
+            float acc = 0.0f;
+            for (uint32_t k4 = 0; k4 < P / 4; ++k4) {
+                const float4 cc = cv[k4];
+                const float4 xx = *(const float4 *)&x[4 * k4];
+                acc = fmaf(xx.x, cc.x, acc);
+                acc = fmaf(xx.y, cc.y, acc);
+                acc = fmaf(xx.z, cc.z, acc);
+                acc = fmaf(xx.w, cc.w, acc);
+            }
+            const uint64_t key = idx_key(acc, ci);
+            best = key > best ? key : best;
+        }
+        best = wave_max_u64(best);
+        if (lane == 0) a.out[r] = 0xffffffffu - (uint32_t)best;
+        // every lane is done with x before the next entry overwrites it
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+}  // namespace
+
+hipError_t ivf_launch_assign_mfma(const IvfAssignArgs &a, const IvfMfmaScratch &m, hipStream_t s) {
+    if (!ivf_assign_mfma_ok(8, a.dim, a.nlist) || a.cen_stride % 4 != 0 || a.words_per_row != a.dim / 4)
+        return hipErrorInvalidValue;
+    const uint32_t pad = ivf_mfma_nlist_pad(a.nlist);
+    hipLaunchKernelGGL(ivf_mfma_words_zero, dim3(1), dim3(64), 0, s, m.words);
+    hipLaunchKernelGGL(ivf_cen_levels, dim3(pad), dim3(64), 0, s, a.centroids, a.cen_stride, a.nlist, a.dim, m.lev,
+                       m.ls, m.words);
+    if (a.n == 0) return hipGetLastError();
+    const dim3 grid((uint32_t)((a.n + IVF_MA_ROWS - 1) / IVF_MA_ROWS)), block(IVF_MA_WAVES * 64);
+    const uint32_t tiles = pad / 32;
+    switch (a.dim) {
+    case 128: hipLaunchKernelGGL(ivf_assign_mfma<4>, grid, block, 0, s, a, m, tiles); break;
+    case 256: hipLaunchKernelGGL(ivf_assign_mfma<8>, grid, block, 0, s, a, m, tiles); break;
+    case 512: hipLaunchKernelGGL(ivf_assign_mfma<16>, grid, block, 0, s, a, m, tiles); break;
+    case 1024: hipLaunchKernelGGL(ivf_assign_mfma<32>, grid, block, 0, s, a, m, tiles); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t ivf_launch_assign_recheck(const IvfAssignArgs &a, const IvfMfmaScratch &m, uint32_t entries,
+                                     hipStream_t s) {
+    if (entries == 0) return hipSuccess;
+    if (entries > m.qcap || a.dim > 1024 || a.dim % 4 != 0 || a.cen_stride % 4 != 0) return hipErrorInvalidValue;
+    const uint32_t wgs = std::min<uint32_t>((entries + IVF_RC_WAVES - 1) / IVF_RC_WAVES, 4096);
+    hipLaunchKernelGGL(ivf_assign_recheck, dim3(wgs), dim3(IVF_RC_WAVES * 64), 0, s, a, m, entries);
     return hipGetLastError();
 }
 

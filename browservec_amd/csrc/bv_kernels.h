@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 namespace bvk {
 
 // Code layouts the scan understands.
@@ -205,6 +207,36 @@ struct IvfProbeArgs {
 hipError_t ivf_launch_copy_rows(const IvfCopyArgs &a, hipStream_t s);
 hipError_t ivf_launch_normalize(float *m, uint32_t rows, uint32_t dim, uint32_t stride, hipStream_t s);
 hipError_t ivf_launch_assign(const IvfAssignArgs &a, int bits, hipStream_t s);
+
+// The assignment of int8 codes on the matrix cores: a pass that decides
+// every row whose nearest centroid is clear by a proven margin and queues
+// the others, then the exact arithmetic of ivf_assign for the queued rows.
+// Scratch: the centroids' two int8 levels (nlist rounded up to 32, x 2 x P
+// bytes) and scales (x 2 floats), a bound word and a queue count (two
+// words), and the queue (qcap entries).
+struct IvfRecheck {
+    uint32_t row;
+    uint32_t n;               // candidates in c, or IVF_RECHECK_ALL: every centroid
+    uint32_t c[6];
+};
+constexpr uint32_t IVF_RECHECK_ALL = 0xffffffffu;
+struct IvfMfmaScratch {
+    int8_t *lev;
+    float *ls;
+    uint32_t *words;          // [0] bound (f32 bits), [1] queue count
+    IvfRecheck *queue;
+    uint32_t qcap;
+};
+inline bool ivf_assign_mfma_ok(int bits, uint32_t P, uint32_t nlist) {
+    return bits == 8 && (P == 128 || P == 256 || P == 512 || P == 1024) && nlist >= 1 && nlist <= IVF_MAX_NLIST;
+}
+inline uint32_t ivf_mfma_nlist_pad(uint32_t nlist) { return (nlist + 31) & ~31u; }
+inline uint32_t ivf_mfma_qcap(uint64_t n) { return (uint32_t)std::max<uint64_t>(65536, std::min<uint64_t>(n, (n + 3) / 4)); }
+// levels, then the pass (out[r] for the decided rows, the queue for the rest)
+hipError_t ivf_launch_assign_mfma(const IvfAssignArgs &a, const IvfMfmaScratch &m, hipStream_t s);
+// the exact assignment of the first `entries` queued rows
+hipError_t ivf_launch_assign_recheck(const IvfAssignArgs &a, const IvfMfmaScratch &m, uint32_t entries,
+                                     hipStream_t s);
 uint32_t ivf_list_blocks(uint64_t n);
 // hist/base: ivf_list_blocks(n) x nlist; totals: nlist; offset: nlist+1; rows_out: n.
 hipError_t ivf_launch_lists(const uint32_t *assign, uint64_t n, uint32_t nlist, uint32_t *hist, uint32_t *base,

@@ -771,6 +771,7 @@ static napi_value stats(napi_env env, napi_callback_info info) {
     NUM("nlist", st.nlist);
     NUM("nprobe", st.nprobe);
     NUM("buildMs", st.build_ms);
+    NUM("buildExactRows", st.build_exact_rows);
     NUM("tunedRecall", st.tuned_recall);
 #undef NUM
     return obj;

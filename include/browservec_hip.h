@@ -113,6 +113,9 @@ typedef struct bv_index_stats {
     double build_ms;          /* last IVF build                                       */
     uint64_t device_bytes;    /* HBM held by the index                                */
     uint64_t last_scanned_rows;
+    uint64_t build_exact_rows;  /* last IVF build's final assignment: rows assigned by
+                                 * the exact fp32 arithmetic alone (all of them, or
+                                 * those the int8 matrix pass left open)            */
 } bv_index_stats;
 
 /* ---- errors / version ---------------------------------------------------- */

@@ -71,8 +71,8 @@ def test_struct_layouts_match_header():
                  "double": ctypes.c_double}
         assert [ctype[t] for t, _ in fields] == [t for _, t in cls._fields_], struct
     assert ctypes.sizeof(_lib.IndexDesc) == 19 * 4
-    # IndexStats: u64 + 7*u32 + f32 + 3*f64 + 2*u64
-    assert ctypes.sizeof(_lib.IndexStats) == 8 + 8 * 4 + 3 * 8 + 2 * 8
+    # IndexStats: u64 + 7*u32 + f32 + 3*f64 + 3*u64
+    assert ctypes.sizeof(_lib.IndexStats) == 8 + 8 * 4 + 3 * 8 + 3 * 8
 
 
 def test_query_lengths_are_checked_before_the_library():

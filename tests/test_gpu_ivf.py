@@ -95,6 +95,8 @@ def test_ivf_build_matches_oracle(ctx, bits, dim, ivf):
     say("ivf build", bits, dim, ivf)
     n = 6000
     data = clustered(n, dim, 40, 0.08, seed=90 + bits)
+    data[11] = 0.0  # a zero row (int8: scale 0, which the matrix-core assignment leaves to the exact one)
+    data[12] = data[4000]  # a duplicate row
     idx = IVFQuantIndex(ctx, dim, bits=bits, ivf=ivf) if bits else IVFIndex(ctx, dim, ivf=ivf)
     idx.append(data[:2500], 2500)  # two appends: the reservoir carries over
     idx.append(data[2500:], n - 2500)
@@ -115,6 +117,10 @@ def test_ivf_build_matches_oracle(ctx, bits, dim, ivf):
             assert abs(s[ref_assign[r]] - s[ref["final"][r]]) <= 1e-5 * np.abs(V[r]).sum(), r
     st = idx.stats()
     assert st["nlist"] == ref["nlist"] and st["nprobe"] == max(1, int(np.floor(ref["nlist"] * 0.05 + 0.5)))
+    if bits == 8:  # the final assignment ran on the matrix cores: it decided most rows itself
+        assert 1 <= st["build_exact_rows"] < n // 2, st["build_exact_rows"]
+    else:
+        assert st["build_exact_rows"] == n
     idx.destroy()
 
 
