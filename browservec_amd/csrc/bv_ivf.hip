@@ -60,6 +60,34 @@ __global__ __launch_bounds__(256) void ivf_normalize_rows(float *m, uint32_t row
     for (uint32_t i = 0; i < dim; ++i) v[i] = (float)((double)v[i] * inv);
 }
 
+// The same with one wave per row: the row staged in LDS with coalesced
+// loads, lane 0's sequential f64 sum (element order) over it, and the scaled
+// row written by every lane.  The thread-per-row form above waits on one
+// scattered load per element (0.47 ms for 4096 x 1024 centroids).
+// Up to four waves per workgroup, within 64 KB of LDS.
+constexpr uint32_t NRM_MAX_DIM = 16384;
+__global__ __launch_bounds__(256) void ivf_normalize_rows_w(float *m, uint32_t rows, uint32_t dim, uint32_t stride) {
+    extern __shared__ float nbuf[];  // waves x dim
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t r = blockIdx.x * (blockDim.x >> 6) + wave;
+    if (r >= rows) return;  // wave-uniform; the kernel has no workgroup barrier
+    float *v = m + (uint64_t)r * stride;
+    float *b = nbuf + (size_t)wave * dim;
+    for (uint32_t i = lane; i < dim; i += 64) b[i] = v[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    double sum = 0.0;
+    if (lane == 0) {
+#pragma unroll 16
+        for (uint32_t i = 0; i < dim; ++i) sum = fma((double)b[i], (double)b[i], sum);
+    }
+    sum = __shfl(sum, 0);
+    const double sq = sqrt(sum);
+    const double inv = 1.0 / (sq != 0.0 ? sq : 1.0);
+    for (uint32_t i = lane; i < dim; i += 64) v[i] = (float)((double)b[i] * inv);
+}
+
 // ---------------------------------------------------------------- assign --
 // Rows x centroids product in 128 x 128 tiles (256 threads, 8 x 8 outputs
 // each, fp32 fused multiply-add over the dimension in order), argmax per row
@@ -570,7 +598,12 @@ hipError_t ivf_launch_copy_rows(const IvfCopyArgs &a, hipStream_t s) {
 
 hipError_t ivf_launch_normalize(float *m, uint32_t rows, uint32_t dim, uint32_t stride, hipStream_t s) {
     if (rows == 0) return hipSuccess;
-    hipLaunchKernelGGL(ivf_normalize_rows, dim3((rows + 255) / 256), dim3(256), 0, s, m, rows, dim, stride);
+    if (dim >= 1 && dim <= NRM_MAX_DIM) {
+        const uint32_t waves = std::max<uint32_t>(1, std::min<uint32_t>(4, NRM_MAX_DIM / dim));
+        hipLaunchKernelGGL(ivf_normalize_rows_w, dim3((rows + waves - 1) / waves), dim3(waves * 64),
+                           (size_t)waves * dim * 4, s, m, rows, dim, stride);
+    } else
+        hipLaunchKernelGGL(ivf_normalize_rows, dim3((rows + 255) / 256), dim3(256), 0, s, m, rows, dim, stride);
     return hipGetLastError();
 }
 
