@@ -1193,10 +1193,24 @@ static int ivf_candidates(bv_index *idx, const float *d_q, uint32_t nq, uint64_t
 // Scanning workgroups per query: at least 256 rows each, and at most
 // 2 * CUs - 1 so that the scanning workgroups plus the threshold helper fit
 // the device at two workgroups per CU whatever the kernel's register count.
-static uint32_t grid_for(const bv_index *idx, uint64_t n) {
+// The fused scan's grid for n rows: one workgroup per 256 rows, at most as
+// many as the device holds at once next to the threshold helper (two per
+// CU, or one when a workgroup's LDS -- the per-wave lists, which grow with
+// the fetch -- leaves room for one only).  The helper is the grid's last
+// workgroup: with more workgroups than fit, it would start only after the
+// others, the scan would run without its bound, and every wave would flush
+// and exactly re-score all of its rows (measured 27 ms instead of 0.2 ms at
+// fetch 1024 over 1M rows).
+static uint32_t grid_for(const bv_index *idx, uint64_t n, uint32_t kprime, uint32_t rr_dim) {
     uint64_t g = (n + 255) / 256;
     const int cus = idx->dev->prop.multiProcessorCount > 0 ? idx->dev->prop.multiProcessorCount : 128;
-    uint64_t cap = 2 * (uint64_t)cus - 1;
+    const size_t lds_cu = idx->dev->prop.maxSharedMemoryPerMultiProcessor > 0
+                              ? (size_t)idx->dev->prop.maxSharedMemoryPerMultiProcessor
+                              : (size_t)160 * 1024;
+    const uint32_t wstride = scan_wcap(kprime) + ((rr_dim & ~3u) + 1) / 2 * 2;
+    const size_t lds = scan_lds_bytes(idx->codec, idx->P, wstride);
+    const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(2, lds_cu / std::max<size_t>(lds, 1)));
+    uint64_t cap = per_cu * (uint64_t)cus - 1;
     if (cap > (uint64_t)SCAN_GRID) cap = SCAN_GRID;
     if (g > cap) g = cap;
     if (g < 1) g = 1;
@@ -1211,6 +1225,7 @@ struct ScanLayout {
     size_t qstate, wmax, cand_keys, merged, merged_n, total;
     uint64_t cap;  // pairs per query
     uint32_t wcap;
+    uint32_t pub_m;  // wave maxima published per wave
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1221,9 +1236,10 @@ static ScanLayout scan_layout(uint32_t nq, uint32_t grid, uint32_t kprime) {
     const uint64_t ng = grid < (uint32_t)NGROUP ? grid : (uint32_t)NGROUP;
     L.wcap = scan_wcap(kprime);
     L.cap = ng * ((grid + ng - 1) / ng) * (SCAN_WG / 64) * L.wcap;
+    L.pub_m = scan_pub_m(kprime, grid);
     L.qstate = 0;
     L.wmax = align256(L.qstate + (size_t)nq * sizeof(QState));
-    L.cand_keys = align256(L.wmax + (size_t)nq * slots * 8);
+    L.cand_keys = align256(L.wmax + (size_t)nq * slots * L.pub_m * 8);
     L.merged = align256(L.cand_keys + (size_t)nq * L.cap * 16);
     L.merged_n = align256(L.merged + (size_t)nq * kprime * 8);
     L.total = align256(L.merged_n + (size_t)nq * 4);
@@ -1233,6 +1249,7 @@ static ScanLayout scan_layout(uint32_t nq, uint32_t grid, uint32_t kprime) {
 static void scan_bind(const ScanLayout &L, char *base, uint32_t rr_dim, ScanArgs &a) {
     a.qs = (QState *)(base + L.qstate);
     a.wmax = (uint64_t *)(base + L.wmax);
+    a.pub_m = L.pub_m;
     a.cand_keys = (uint64_t *)(base + L.cand_keys);
     a.cand_cap = L.cap;
     a.wcap = L.wcap;
@@ -1263,6 +1280,7 @@ static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kpri
     HIPX(idx->dev, merged_n.ensure((size_t)nq * 4, 0, s), "scratch");
     a.qs = qstate.as<QState>();
     a.wmax = wmax.as<uint64_t>();
+    a.pub_m = L.pub_m;
     a.cand_keys = cand_keys.as<uint64_t>();
     a.cand_cap = L.cap;
     a.wcap = L.wcap;
@@ -1472,7 +1490,7 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
         a.cand = idx->cand.as<uint32_t>();
         a.cand_off = idx->cand_off.as<uint64_t>();
     }
-    const uint32_t grid = grid_for(idx, std::max<uint64_t>(n, 1));
+    const uint32_t grid = grid_for(idx, std::max<uint64_t>(n, 1), kprime, rerank ? idx->dim : 0);
     rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a, lane);
     if (rc) return rc;
     scan_common(idx, d_q, n, grid, kprime, k_out, rerank, d_mask, mask_bits, d_rows, d_scores, d_n, a);
@@ -1620,7 +1638,7 @@ static int run_batched_f32(bv_index *idx, const float *d_q, uint32_t nq, uint32_
     for (uint32_t i = 0; i < nq; i++) most = std::max<uint64_t>(most, std::min<uint64_t>(cnt[i], cap));
     // exact re-score of the kept rows: the fused scan in indexed mode
     ScanArgs a{};
-    const uint32_t grid = grid_for(idx, most);
+    const uint32_t grid = grid_for(idx, most, kprime, 0);
     int rc = scan_scratch(idx, nq, grid, kprime, 0, a);
     if (rc) return rc;
     a.codes = idx->raw.p;
@@ -1766,7 +1784,7 @@ static int finish_batched_indexed(bv_index *idx, const float *d_q, uint32_t nq, 
     uint64_t most = 1;
     for (uint32_t i = 0; i < nq; i++) most = std::max<uint64_t>(most, std::min<uint64_t>(kept[i], cap));
     ScanArgs a{};
-    const uint32_t grid = grid_for(idx, most);
+    const uint32_t grid = grid_for(idx, most, kprime, rerank ? idx->dim : 0);
     int rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a);
     if (rc) return rc;
     if (scan_prep_supported(idx->codec, idx->units, idx->P)) {  // the scan transforms the fp32 queries itself
@@ -2477,7 +2495,7 @@ extern "C" int bv_index_search_device_noalloc(bv_index *idx, const float *d_quer
         return fail(BV_E_UNSUPPORTED, "fetch %u exceeds the fused top-k limit %d", fe, MAX_KPRIME);
     const uint32_t kprime = fe ? fe : kk;
     const bool rerank = fe != 0;
-    const uint32_t grid = grid_for(idx, idx->rows);
+    const uint32_t grid = grid_for(idx, idx->rows, kprime, rerank ? idx->dim : 0);
     const ScanLayout L = scan_layout(nq, grid, kprime);
     if (L.total > (size_t)BV_NOALLOC_SCRATCH_BYTES)
         return fail(BV_E_INVALID, "%u queries with fetch %u need %zu bytes of scratch; the limit is %zu", nq, kprime,
@@ -2710,7 +2728,7 @@ static int dense_scores(bv_index *idx, const float *q, const uint32_t *mask, uin
     const bool in_kernel = idx->quant && scan_prep_supported(idx->codec, idx->units, idx->P);
     int rc = in_kernel ? BV_OK : prepare_queries(idx, idx->qin.as<float>(), 1, &qscan, &qstride);
     if (rc) return rc;
-    const uint32_t grid = grid_for(idx, std::max<uint64_t>(n, 1));
+    const uint32_t grid = grid_for(idx, std::max<uint64_t>(n, 1), 1, 0);
     const uint32_t *d_mask = nullptr;
     if (mask) {
         HIPX(idx->dev, idx->mask.ensure(mask_words * 4, 0, idx->stream), "mask buffer");

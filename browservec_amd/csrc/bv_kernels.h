@@ -35,6 +35,15 @@ constexpr int MAX_KPRIME = 1024;  // largest fetch the fused top-k serves
 constexpr int MAX_GRID = 1024;    // workgroups per query (bound of the wave-maxima scratch)
 constexpr int SCAN_GRID = 512;    // scanning workgroups per query for large row counts
 
+// Wave maxima published per wave when a query's fetch exceeds half the
+// number of waves: the threshold helper's bound, the kprime-th best of the
+// published keys, needs at least kprime of them (each the key of a distinct
+// row), and then forms from the waves' few best rows instead of their one.
+constexpr uint32_t SCAN_PUB_MANY = 4;
+inline uint32_t scan_pub_m(uint32_t kprime, uint32_t grid) {
+    return 2ull * kprime > (uint64_t)grid * (SCAN_WG / 64) ? SCAN_PUB_MANY : 1u;
+}
+
 // Per-wave candidate list capacity of the fused scan for a fetch of kp:
 // twice kp plus room for one grab, at least 256 keys, a multiple of 64.
 inline uint32_t scan_wcap(uint32_t kp) {
@@ -85,7 +94,9 @@ struct ScanArgs {
     uint32_t qf_off;          // C_Q1P: LDS byte offset of the fp32 query (set at launch)
     uint32_t grid;            // scanning workgroups per query (one more runs the threshold helper)
     QState *qs;               // [nq]
-    uint64_t *wmax;           // [nq][grid*4] per-wave running maxima (zero on entry and exit)
+    uint64_t *wmax;           // [nq][grid*4*pub_m] per-wave running maxima (zero on entry and exit)
+    uint32_t pub_m;           // maxima each wave publishes: 1 (its maximum), or SCAN_PUB_MANY (the
+                              // largest lane maxima) when the fetch is large next to the waves
     uint64_t *cand_keys;      // [nq][cand_cap][2] flushed (scan key, exact key) pairs
     uint64_t cand_cap;        // pairs per query: min(grid,NGROUP) regions of ceil(grid/NGROUP)*4*wcap
     uint64_t *merged;         // [nq][kprime] merged keys, descending
@@ -418,6 +429,9 @@ hipError_t launch_levels(const LevelArgs &a, uint32_t nq, hipStream_t s);
 hipError_t launch_q1p_layout(const LevelArgs &a, uint32_t nq, hipStream_t s);
 size_t level_stride(int codec, uint32_t P);
 size_t scan_query_lds(int codec, uint32_t P);
+// The fused scan's LDS per workgroup (at most: with the in-kernel query
+// transform) for per-wave list stride wstride.
+size_t scan_lds_bytes(int codec, uint32_t P, uint32_t wstride);
 // True when the scan for this codec / row layout transforms fp32 queries itself (ScanArgs::qraw).
 bool scan_prep_supported(int codec, uint32_t units, uint32_t P);
 

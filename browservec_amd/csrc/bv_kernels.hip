@@ -184,6 +184,14 @@ bool scan_prep_supported(int codec, uint32_t units, uint32_t P) {
     return P == full && P >= 64 && P / 64 <= 16;
 }
 size_t scan_query_lds(int codec, uint32_t P) { return query_prep_lds(codec, P); }
+size_t scan_lds_bytes(int codec, uint32_t P, uint32_t wstride) {
+    size_t lds = (size_t)(SCAN_WG / 64) * wstride * sizeof(uint64_t);
+    if (lds < sizeof(TopkLds)) lds = sizeof(TopkLds);
+    const size_t prep = (query_prep_lds(codec, P) + 15) & ~(size_t)15;
+    if (lds < prep) lds = prep;
+    if (codec == C_Q1P) lds = ((lds + 15) & ~(size_t)15) + q1p_lut_bytes(P);
+    return lds;
+}
 
 hipError_t launch_rerank(const RerankArgs &a, uint32_t nq, hipStream_t s) {
     const size_t lds = sizeof(double) * (size_t)(a.dim & ~3u) + 16;

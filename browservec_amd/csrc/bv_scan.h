@@ -1910,9 +1910,22 @@ __device__ __forceinline__ void compute_step(const ScanArgs &a, const ScanRegs<C
 
 // Publishes the wave's running maximum to wmax[slot] on every call, from
 // every lane (one line, one value): the scan loop issues the same memory
-// operations whatever the data, so that its waits stay exact.
-__device__ __forceinline__ void publish_wave_max(uint64_t *wslot, uint64_t lmax) {
-    __hip_atomic_store(wslot, wave_max_u64(lmax), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// operations whatever the data, so that its waits stay exact.  With m > 1
+// (a fetch large next to the number of waves) the m largest lane maxima go
+// to m slots: the lanes hold disjoint rows, so they are distinct rows' keys.
+__device__ __forceinline__ void publish_wave_max(uint64_t *wslot, uint64_t lmax, uint32_t m, int lane) {
+    if (m == 1) {
+        __hip_atomic_store(wslot, wave_max_u64(lmax), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    uint64_t v = lmax;
+#pragma unroll
+    for (uint32_t j = 0; j < SCAN_PUB_MANY; ++j) {
+        const uint64_t mx = wave_max_u64(v);
+        __hip_atomic_store(wslot + j, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t hit = __ballot(v == mx);  // (mx is some lane's value: hit is not empty)
+        if ((uint64_t)lane == (uint64_t)(__ffsll((unsigned long long)hit) - 1)) v = 0;
+    }
 }
 
 // Cross-workgroup hand-off without cache-wide maintenance: data goes through
@@ -1940,8 +1953,9 @@ __device__ __forceinline__ uint64_t load_tau(const QState *qs) {
 // the final selection and the helper finishes last).
 __device__ void reset_query(const ScanArgs &a, uint32_t qi) {
     QState *qs = a.qs + qi;
-    uint64_t *wm = a.wmax + (uint64_t)qi * a.grid * (SCAN_WG / 64);
-    for (uint32_t i = threadIdx.x; i < a.grid * (SCAN_WG / 64); i += blockDim.x) wm[i] = 0;
+    const uint32_t nw = a.grid * (SCAN_WG / 64) * a.pub_m;
+    uint64_t *wm = a.wmax + (uint64_t)qi * nw;
+    for (uint32_t i = threadIdx.x; i < nw; i += blockDim.x) wm[i] = 0;
     for (uint32_t r = threadIdx.x; r < (uint32_t)NGROUP; r += blockDim.x) {
         qs->cc[r * CL] = 0;
         qs->dyn[r * CL] = 0;
@@ -1961,7 +1975,7 @@ __device__ void reset_query(const ScanArgs &a, uint32_t qi) {
 // has finished.
 __device__ void threshold_helper(const ScanArgs &a, uint32_t qi, TopkLds &L) {
     QState *qs = a.qs + qi;
-    const uint32_t nslots = a.grid * (SCAN_WG / 64);
+    const uint32_t nslots = a.grid * (SCAN_WG / 64) * a.pub_m;
     const uint64_t *wm = a.wmax + (uint64_t)qi * nslots;
     const uint32_t kp = a.kprime;
     const uint32_t cap = kp <= (uint32_t)SCAN_WG ? (uint32_t)SCAN_WG : (uint32_t)SCAN_CAP;
@@ -2048,7 +2062,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         cand = a.cand + (uint64_t)qi * a.cand_stride;
         n = a.cand_n[qi] < a.cand_stride ? a.cand_n[qi] : (uint32_t)a.cand_stride;
     }
-    uint64_t *wslot = a.wmax + ((uint64_t)qi * a.grid + blockIdx.x) * SH::WAVES + wave;
+    uint64_t *wslot = a.wmax + (((uint64_t)qi * a.grid + blockIdx.x) * SH::WAVES + wave) * a.pub_m;
     uint64_t lmax = 0;
 
     const uint32_t wcap = a.wcap;
@@ -2304,7 +2318,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             // shared bound every TAU_POLL passes (waves staggered; it is one
             // line that every wave of the grid reads) or else the wave's own
             // slot
-            publish_wave_max(wslot, lmax);
+            publish_wave_max(wslot, lmax, a.pub_m, lane);
             // (the bit-plane scan polls every pass until a bound exists: its
             // rows go through the exact re-score until then)
             // (a short scan polls every pass: its waves run only a few)
@@ -2325,7 +2339,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
             } else {
                 ha = false;
             }
-            publish_wave_max(wslot, lmax);
+            publish_wave_max(wslot, lmax, a.pub_m, lane);
             const uint64_t g = uniform_u64(__hip_atomic_load(&qs->tau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
             tau = g > tau ? g : tau;
         }
@@ -2457,7 +2471,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
         // rows' keys, so kp rows score at least that much and it is at most
         // the kp-th best key.  Every wave published the maximum over all its
         // rows before its workgroup took a ticket.
-        const uint32_t nslots = a.grid * (SCAN_WG / 64);
+        const uint32_t nslots = a.grid * (SCAN_WG / 64) * a.pub_m;
         const uint64_t *wm = a.wmax + (uint64_t)qi * nslots;
         for (uint32_t i0 = 0; i0 < nslots; i0 += 8 * SCAN_WG) {
             uint64_t v[8];

@@ -417,7 +417,8 @@ def test_int8_1m_rows_fetch_rerank_matches_oracle(ctx):
     dynamic share of the rows is handed out by tickets.  Single queries equal
     the oracle pipeline (top 100 by code score, exact re-rank, canonical top
     10) up to fetch-boundary near-ties; an eight-query batch (matrix-core
-    path) equals the single queries bit for bit."""
+    path) equals the single queries bit for bit.  The same at fetch 1024 and
+    k 32, where the scan's grid and bound take their large-fetch forms."""
     from browservec_amd import QuantIndex
 
     n, dim, fetch, k = 1_000_000, 768, 100, 10
@@ -451,6 +452,23 @@ def test_int8_1m_rows_fetch_rerank_matches_oracle(ctx):
         r1, s1, _ = singles[i]
         assert_fetch_rerank(r1[0], s1[0], approx, np.arange(n), lambda rr, q=qs[i]: o.rerank_scores(data, q, rr),
                             fetch, k, tol, what=f"1M query {i}")
+        if i < 2:
+            # fetch 1024, k 32: the per-wave lists leave room for one workgroup
+            # per CU (a smaller grid) and the waves publish their four best
+            # lane maxima, so the threshold helper still forms its bound
+            say("1M x 768 int8: fetch 1024, query", i)
+            rw, sw, cw = idx.search(qs[i:i + 1], 1024, 32)
+            assert cw[0] == 32
+            assert_fetch_rerank(rw[0], sw[0], approx, np.arange(n),
+                                lambda rr, q=qs[i]: o.rerank_scores(data, q, rr), 1024, 32, tol,
+                                what=f"1M query {i} fetch 1024")
+    say("1M x 768 int8: batch of 8, fetch 1024")
+    wide = [idx.search(qs[i:i + 1], 1024, 32) for i in range(8)]
+    br, bs, bc = idx.search(qs, 1024, 32)
+    for i in range(8):
+        r1, s1, c1 = wide[i]
+        assert bc[i] == c1[0] == 32
+        assert np.array_equal(br[i], r1[0]) and np.array_equal(bs[i].view(np.uint32), s1[0].view(np.uint32)), i
     idx.destroy()
 
 
