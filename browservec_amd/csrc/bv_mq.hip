@@ -954,9 +954,13 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_f32(MqArgs a) {
 // One workgroup per query.  The kk-th best key is found by binning the
 // keys over their actual range (2048 bins of a power-of-two width, so keys
 // concentrated in a few score octaves still spread over many bins) and
-// narrowing into the bin that holds it until the keys at or above that
-// bin's lower edge fit SEL_CAP; those are gathered and sorted.  Keys are
-// unique, so exactly kk keys are at or above the kk-th.
+// narrowing into the bin that holds it.  When the best kk keys are wanted in
+// order, the narrowing stops once the keys at or above that bin's lower edge
+// fit the smallest sort that holds twice kk (at least 256, at most
+// SEL_CAP); those are gathered and sorted.  When only the bound is wanted,
+// it goes on until the kk-th key is alone in its bin, and one more pass
+// picks it out (no sort).  Keys are unique, so exactly kk keys are at or
+// above the kk-th.
 constexpr int SEL_THREADS = 1024;
 constexpr int SEL_BINS = 2048;
 constexpr int SEL_CAP = 4096;
@@ -972,7 +976,11 @@ __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
     const uint32_t n = (uint64_t)total < a.cap ? total : (uint32_t)a.cap;
     const uint64_t *keys = a.cand + (uint64_t)q * a.cap;
     const uint32_t kk = a.kk < n ? a.kk : n;
+    const bool sorted = a.merged != nullptr || a.out_rows != nullptr;
+    uint32_t lim = 256;
+    while (lim < 2 * kk && lim < (uint32_t)SEL_CAP) lim <<= 1;
     uint64_t G = 0;  // keys >= G are gathered
+    uint64_t Gend = ~0ull;  // the last key of the kk-th's bin
     if (n > kk) {
         uint64_t lo = ~0ull, hi = 0;
         for (uint32_t i = tid; i < n; i += SEL_THREADS) {
@@ -1039,13 +1047,34 @@ __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
             const uint32_t bin = s_bin, excl = s_excl, cb = s_cnt;
             __syncthreads();
             G = lo + ((uint64_t)bin << shift);
-            if (above + excl + cb <= (uint32_t)SEL_CAP || shift == 0) break;
+            const uint64_t w = (1ull << shift) - 1;  // the bin's last key, without wrapping past 2^64
+            Gend = hi - G > w ? G + w : hi;
+            if ((sorted ? above + excl + cb <= lim : cb <= 1) || shift == 0) break;
             above += excl;
             rem -= excl;
             lo = G;
-            const uint64_t w = (1ull << shift) - 1;  // the bin's last key, without wrapping past 2^64
-            hi = hi - G > w ? G + w : hi;
+            hi = Gend;
         }
+    }
+    if (!sorted) {
+        // the bound alone: the kk-th key is the one key in [G, Gend]
+        if (tid == 0) s_cnt = 0;
+        __syncthreads();
+        if (n > kk)
+            for (uint32_t i = tid; i < n; i += SEL_THREADS) {
+                const uint64_t k = keys[i];
+                if (k >= G && k <= Gend) red[0][0] = k;  // (exactly one such key)
+            }
+        __syncthreads();
+        if (tid == 0) {
+            if (a.tau) {
+                const uint64_t t = n > kk ? red[0][0] : 0ull;
+                a.tau[q] = a.tau_max && a.tau[q] > t ? a.tau[q] : t;
+            }
+            if (a.merged_n) a.merged_n[q] = kk;
+            if (a.overflow) a.overflow[q] = (uint64_t)total > a.cap ? 1u : 0u;
+        }
+        return;
     }
     if (tid == 0) s_cnt = 0;
     __syncthreads();
