@@ -1514,11 +1514,20 @@ __global__ __launch_bounds__(IVF_LM_WAVES * 64) void ivf_list_mfma(const uint32_
         const uint32_t ri = t * 32 + c;
         const uint64_t row = list_rows[r0 + (ri < nrows ? ri : nrows - 1)];  // past the end: a valid row, dropped
         v4i A[S];
+        if constexpr (BITS == 8) {
+            // every load of the tile is issued before the first MFMA (left to
+            // itself the compiler places each load next to its MFMA and the
+            // wave waits on memory once per K step)
 #pragma unroll
-        for (int st = 0; st < S; ++st) {
-            const uint32_t u = 2 * st + h;
-            if constexpr (BITS == 8) A[st] = ((const v4i *)(codes + row * W))[u];
-            else A[st] = unpack_q4(((const uint2 *)(codes + row * W))[u]);
+            for (int st = 0; st < S; ++st) A[st] = ((const v4i *)(codes + row * W))[2 * st + h];
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            uint2 raw[S];
+#pragma unroll
+            for (int st = 0; st < S; ++st) raw[st] = ((const uint2 *)(codes + row * W))[2 * st + h];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int st = 0; st < S; ++st) A[st] = unpack_q4(raw[st]);
         }
         v16i acc = v16i{};
 #pragma unroll
