@@ -1368,39 +1368,52 @@ __global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, const f
     const uint32_t *rq = rows + (uint64_t)q * cap;
     uint64_t *out = keys + (uint64_t)q * cap;
     const int l16 = tid & 15;
-    // the 16 lanes of a DPP row take one row; two rows per step in flight
-    for (uint32_t i = tid >> 4; i < n; i += 128) {
-        const uint32_t i2 = i + 64 < n ? i + 64 : i;
-        const uint32_t ra = rq[i], rb = rq[i2];
-        const v4i *xa = (const v4i *)(codes + (uint64_t)ra * W), *xb = (const v4i *)(codes + (uint64_t)rb * W);
-        v4i ca[PER], cb[PER];
+    // the 16 lanes of a DPP row take one row; four rows per step in flight
+    // (rows i, i + 64, i + 128, i + 192; a slot past the end repeats row i
+    // and is not written)
+    constexpr int R = 4;
+    for (uint32_t i = tid >> 4; i < n; i += 64 * R) {
+        uint32_t rr[R];
+        const v4i *x[R];
 #pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            const int u = l16 + 16 * j;
-            ca[j] = u < UNITS ? xa[u] : v4i{};
-            cb[j] = u < UNITS ? xb[u] : v4i{};
+        for (int k = 0; k < R; ++k) {
+            const uint32_t ik = i + 64 * k < n ? i + 64 * k : i;
+            rr[k] = rq[ik];
+            x[k] = (const v4i *)(codes + (uint64_t)rr[k] * W);
         }
-        const float sa = scales[ra], sb = scales[rb];
-        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+        v4i cr[R][PER];
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int u = l16 + 16 * j;
+                cr[k][j] = u < UNITS ? x[k][u] : v4i{};
+            }
+        float sc[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k) sc[k] = scales[rr[k]];
+        int d[R][3];
+#pragma unroll
+        for (int k = 0; k < R; ++k) d[k][0] = d[k][1] = d[k][2] = 0;
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             const int u = l16 + 16 * j;
             if (u >= UNITS) continue;
             const v4i q0 = ql[3 * u], q1 = ql[3 * u + 1], q2 = ql[3 * u + 2];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                a0 = __builtin_amdgcn_sdot4(ca[j][w], q0[w], a0, false);
-                a1 = __builtin_amdgcn_sdot4(ca[j][w], q1[w], a1, false);
-                a2 = __builtin_amdgcn_sdot4(ca[j][w], q2[w], a2, false);
-                b0 = __builtin_amdgcn_sdot4(cb[j][w], q0[w], b0, false);
-                b1 = __builtin_amdgcn_sdot4(cb[j][w], q1[w], b1, false);
-                b2 = __builtin_amdgcn_sdot4(cb[j][w], q2[w], b2, false);
-            }
+            for (int w = 0; w < 4; ++w)
+#pragma unroll
+                for (int k = 0; k < R; ++k) {
+                    d[k][0] = __builtin_amdgcn_sdot4(cr[k][j][w], q0[w], d[k][0], false);
+                    d[k][1] = __builtin_amdgcn_sdot4(cr[k][j][w], q1[w], d[k][1], false);
+                    d[k][2] = __builtin_amdgcn_sdot4(cr[k][j][w], q2[w], d[k][2], false);
+                }
         }
-        a0 = row16_sum(a0), a1 = row16_sum(a1), a2 = row16_sum(a2);
-        b0 = row16_sum(b0), b1 = row16_sum(b1), b2 = row16_sum(b2);
-        if (l16 == 0) out[i] = q_key(s0, s1, s2, a0, a1, a2, sa, ra);
-        if (l16 == 1 && i2 != i) out[i2] = q_key(s0, s1, s2, b0, b1, b2, sb, rb);
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            d[k][0] = row16_sum(d[k][0]), d[k][1] = row16_sum(d[k][1]), d[k][2] = row16_sum(d[k][2]);
+            if (l16 == k && i + 64 * k < n) out[i + 64 * k] = q_key(s0, s1, s2, d[k][0], d[k][1], d[k][2], sc[k], rr[k]);
+        }
     }
 }
 
