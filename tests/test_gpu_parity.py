@@ -518,3 +518,46 @@ def test_browservec_query_batch_takes_one_batched_search(ctx, kind):
         assert (np.array([r["score"] for r in batch[i]], np.float32).view(np.uint32).tolist() ==
                 np.array([r["score"] for r in single], np.float32).view(np.uint32).tolist()), i
     db.destroy()
+
+
+def test_1bit_asym_large_fetch_matches_oracle(ctx):
+    """600,000 x 1024 1-bit asymmetric codes, fetch 1024 -> exact re-rank ->
+    top 32 (the reference's re-rank factor 32 at k 32): the bit-plane scan's
+    lists and re-score table leave LDS for one workgroup per CU, so the grid
+    shrinks to what the device holds and each wave publishes its four best
+    lane maxima.  Single queries equal the oracle pipeline (top 1024 by the
+    dequantized product, exact re-rank, canonical top 32) up to
+    fetch-boundary near-ties, as does fetch 320 (k 10); a batch equals the
+    single queries bit for bit."""
+    from browservec_amd import QuantIndex
+
+    n, dim = 600_000, 1024
+    say("600k x 1024 1-bit asym: data")
+    data = _mixture_1m(n, dim, 1024, 0.1, 0xB5EC0201)
+    idx = QuantIndex(ctx, dim, bits=1, scorer="asym")
+    idx.append(data, n)
+    words, scales = idx.export_codes()
+    rng = np.random.default_rng(0xB5EC0202)
+    pick = rng.integers(0, n, 8)
+    qs = data[pick] + 0.05 * rng.standard_normal((8, dim), dtype=np.float32)
+    qs = np.stack([o.normalize(q) for q in qs]).astype(np.float32)
+    for fetch, k in ((1024, 32), (320, 10)):
+        singles = [idx.search(qs[i:i + 1], fetch, k) for i in range(8)]
+        say("600k x 1024 1-bit asym: batch of 8, fetch", fetch)
+        br, bs, bc = idx.search(qs, fetch, k)
+        for i in range(8):
+            r1, s1, c1 = singles[i]
+            assert bc[i] == c1[0] == k
+            assert np.array_equal(br[i], r1[0]) and np.array_equal(bs[i].view(np.uint32), s1[0].view(np.uint32)), i
+        for i in range(2):
+            say("600k x 1024 1-bit asym: oracle query", i, "fetch", fetch)
+            rq = o.rotate(qs[i], dim)[0]
+            approx = o.scan_quant(words, scales, rq, 1)
+            # every 1-bit code dequantizes to +-1: sum_i |deq_i q_i| * scale
+            tol = 2 * REL_TOL * float(np.abs(scales.astype(np.float64)).max()) * float(
+                np.abs(rq.astype(np.float64)).sum())
+            r1, s1, _ = singles[i]
+            assert_fetch_rerank(r1[0], s1[0], approx, np.arange(n),
+                                lambda rr, q=qs[i]: o.rerank_scores(data, q, rr), fetch, k, tol,
+                                what=f"1-bit query {i} fetch {fetch}")
+    idx.destroy()
