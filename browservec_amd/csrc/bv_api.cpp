@@ -159,7 +159,7 @@ struct bv_index {
     DevBuf rr_keys, rr_tickets;
     DevBuf out_rows, out_scores, out_n;
     DevBuf cand, cand_n, dense;
-    DevBuf mq_cand, mq_cnt, mq_tau, mq_flag;  // batched matrix-core scans
+    DevBuf mq_cand, mq_cnt, mq_tau, mq_tau2, mq_flag;  // batched matrix-core scans
     DevBuf rsq, rsq_max;                      // flat fp32: squared row norms and their maximum (float bits)
     DevBuf mq_qsq, mq_slack, mq_rows;         // exact fp32 batches: query norms, slack, surviving rows
     DevBuf cnorm, mq_rq, mq_up, mq_kept;       // flat int8 level-one batches: row code norms, query bounds, upper bounds, kept counts
@@ -1869,6 +1869,7 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     HIPX(idx->dev, idx->mq_cnt.ensure((size_t)nq * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->mq_kept.ensure((size_t)nq * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->mq_tau.ensure((size_t)nq * 8, 0, s), "scratch");
+    HIPX(idx->dev, idx->mq_tau2.ensure((size_t)nq * 8, 0, s), "scratch");
     HIPX(idx->dev, idx->mq_rq.ensure((size_t)nq * 4, 0, s), "scratch");
     HIPX(idx->dev, idx->h_cnt.ensure((size_t)nq * 8), "pinned buffer");
     HIPX(idx->dev, idx->merged.ensure((size_t)nq * kprime * 8, 0, s), "scratch");
@@ -1914,6 +1915,18 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     sa.kk = kprime;
     sa.tau = idx->mq_tau.as<uint64_t>();
     HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+    // each bound is then raised to the smallest exact key of the kprime rows
+    // that reach it (the kprime-th best exact key of all rows is at least
+    // that), which narrows the rows the passes keep.  The 1-bit asymmetric
+    // keys come from the fused scan, not from these level dots, and Hamming
+    // bounds are exact already (one level, no residual).
+    const bool exact_tau = !asym1 && idx->codec != C_HAM && kprime <= MQ1_TAU_KK;
+    auto tighten = [&](const uint64_t *cand, uint64_t ccap, const uint64_t *tsel) {
+        return launch_mq1_tau_exact(src.codes, src.W, src.scales, qlev, qstride, units16, cand,
+                                    idx->mq_cnt.as<uint32_t>(), ccap, kprime, tsel, idx->mq_tau.as<uint64_t>(),
+                                    nq, s);
+    };
+    if (exact_tau) HIPX(idx->dev, tighten(m.cand, S, idx->mq_tau.as<uint64_t>()), "batched bound kernel");
     // the pass over every row keeps the rows whose upper bound reaches the
     // bound, into the workgroups' buckets, then one list per query.  It runs
     // in two parts: the first eighth of the rows, whose kept rows' kprime-th
@@ -1943,9 +1956,16 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
              "batched compact kernel");
         if (part == 0) {  // the tighter bound
             sa.cap = cap;
-            sa.tau_max = true;
-            HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
-            sa.tau_max = false;
+            if (exact_tau) {
+                sa.tau = idx->mq_tau2.as<uint64_t>();
+                HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+                HIPX(idx->dev, tighten(idx->mq_cand.as<uint64_t>(), cap, sa.tau), "batched bound kernel");
+                sa.tau = idx->mq_tau.as<uint64_t>();
+            } else {
+                sa.tau_max = true;
+                HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+                sa.tau_max = false;
+            }
         }
     }
     m.codes = src.codes;
@@ -1953,10 +1973,16 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     m.cand = idx->mq_cand.as<uint64_t>();
     m.up_out = idx->mq_up.as<uint32_t>();
     m.cnt = idx->mq_cnt.as<uint32_t>();
-    // the kprime-th best lower bound among the kept rows, and the rows whose
-    // upper bound reaches it
+    // the kprime-th best lower bound among the kept rows (raised as above),
+    // and the rows whose upper bound reaches it
     sa.cap = cap;
-    HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+    if (exact_tau) {
+        sa.tau = idx->mq_tau2.as<uint64_t>();
+        HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+        HIPX(idx->dev, tighten(m.cand, cap, sa.tau), "batched bound kernel");
+    } else {
+        HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+    }
     HIPX(idx->dev,
          launch_mq1_keep(m.cand, m.up_out, m.cnt, cap, idx->mq_tau.as<uint64_t>(), idx->mq_rows.as<uint32_t>(),
                          idx->mq_kept.as<uint32_t>(), nq, s),

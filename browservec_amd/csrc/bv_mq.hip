@@ -1336,11 +1336,6 @@ __global__ __launch_bounds__(1024) void mq1_keep(const uint64_t *cand, const uin
     if (threadIdx.x == 0) kept[q] = s_n;
 }
 
-// One workgroup per query: the exact key of every kept row, with the
-// single-query scan's arithmetic (three exact int32 level dots, f64
-// combine, row scale), into keys[q][i].  Sixteen lanes per row, four rows
-// per wave at a time: each load instruction reads 256 contiguous bytes of
-// four rows.
 // Sum over the 16 lanes of a DPP row, in every lane of the row.
 __device__ __forceinline__ int row16_sum(int x) {
     x += __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false);  // row_ror:8
@@ -1350,27 +1345,21 @@ __device__ __forceinline__ int row16_sum(int x) {
     return x;
 }
 
-template <int UNITS>
-__global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, const float *scales,
-                                                   const unsigned char *qlev, uint64_t qstride,
-                                                   const uint32_t *rows, const uint32_t *kept, uint64_t cap,
-                                                   uint64_t *keys) {
+// The exact keys of rows row_at(0 .. n-1) of one query (levels in ql,
+// steps s0..s2) with the single-query scan's arithmetic (three exact int32
+// level dots, f64 combine, row scale), each handed to emit(i, key) by one
+// lane of the row's 16-lane group.  Sixteen lanes per row, four rows per
+// group in flight (rows i, i + 64, i + 128, i + 192 of a 1024-thread
+// workgroup; a slot past the end repeats row i and is not emitted): each
+// load instruction reads 256 contiguous bytes of four rows.
+template <int UNITS, class RowAt, class Emit>
+__device__ __forceinline__ void mq1_exact_rows(const uint32_t *codes, const float *scales, const v4i *ql,
+                                               double s0, double s1, double s2, uint32_t n, RowAt row_at,
+                                               Emit emit) {
     constexpr int PER = UNITS < 16 ? 1 : UNITS / 16;  // units per lane (lanes >= UNITS idle when UNITS < 16)
     constexpr uint32_t W = UNITS * 4;
-    __shared__ v4i ql[UNITS * 3];  // the query's packed levels: unit u, level l at 3u + l
-    const uint32_t q = blockIdx.x, tid = threadIdx.x;
-    const unsigned char *src = qlev + (uint64_t)q * qstride;
-    for (uint32_t i = tid; i < UNITS * 3; i += 1024) ql[i] = ((const v4i *)src)[i];
-    const QLevelTail *t = (const QLevelTail *)(src + (uint64_t)UNITS * 48);
-    const double s0 = t->s[0], s1 = t->s[1], s2 = t->s[2];
-    __syncthreads();
-    const uint32_t n = kept[q];
-    const uint32_t *rq = rows + (uint64_t)q * cap;
-    uint64_t *out = keys + (uint64_t)q * cap;
+    const uint32_t tid = threadIdx.x;
     const int l16 = tid & 15;
-    // the 16 lanes of a DPP row take one row; four rows per step in flight
-    // (rows i, i + 64, i + 128, i + 192; a slot past the end repeats row i
-    // and is not written)
     constexpr int R = 4;
     for (uint32_t i = tid >> 4; i < n; i += 64 * R) {
         uint32_t rr[R];
@@ -1378,7 +1367,7 @@ __global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, const f
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             const uint32_t ik = i + 64 * k < n ? i + 64 * k : i;
-            rr[k] = rq[ik];
+            rr[k] = row_at(ik);
             x[k] = (const v4i *)(codes + (uint64_t)rr[k] * W);
         }
         v4i cr[R][PER];
@@ -1412,8 +1401,80 @@ __global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, const f
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             d[k][0] = row16_sum(d[k][0]), d[k][1] = row16_sum(d[k][1]), d[k][2] = row16_sum(d[k][2]);
-            if (l16 == k && i + 64 * k < n) out[i + 64 * k] = q_key(s0, s1, s2, d[k][0], d[k][1], d[k][2], sc[k], rr[k]);
+            if (l16 == k && i + 64 * k < n) emit(i + 64 * k, q_key(s0, s1, s2, d[k][0], d[k][1], d[k][2], sc[k], rr[k]));
         }
+    }
+}
+
+// One workgroup per query: the exact key of every kept row into keys[q][i].
+template <int UNITS>
+__global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, const float *scales,
+                                                   const unsigned char *qlev, uint64_t qstride,
+                                                   const uint32_t *rows, const uint32_t *kept, uint64_t cap,
+                                                   uint64_t *keys) {
+    __shared__ v4i ql[UNITS * 3];  // the query's packed levels: unit u, level l at 3u + l
+    const uint32_t q = blockIdx.x, tid = threadIdx.x;
+    const unsigned char *src = qlev + (uint64_t)q * qstride;
+    for (uint32_t i = tid; i < UNITS * 3; i += 1024) ql[i] = ((const v4i *)src)[i];
+    const QLevelTail *t = (const QLevelTail *)(src + (uint64_t)UNITS * 48);
+    const double s0 = t->s[0], s1 = t->s[1], s2 = t->s[2];
+    __syncthreads();
+    const uint32_t *rq = rows + (uint64_t)q * cap;
+    uint64_t *out = keys + (uint64_t)q * cap;
+    mq1_exact_rows<UNITS>(codes, scales, ql, s0, s1, s2, kept[q], [&](uint32_t i) { return rq[i]; },
+                          [&](uint32_t i, uint64_t key) { out[i] = key; });
+}
+
+// A tighter bound from exact keys, one workgroup per query: the kk keys of
+// cand[q][0, min(cnt[q], cap)) at or above tsel[q] (that list's kk-th best
+// key, so exactly kk of them: keys are unique) name kk distinct rows; the
+// smallest of their exact keys is at most the kk-th best exact key of all
+// rows, so tau[q] = max(tau[q], that key) is still a bound that every row
+// of the exact top kk reaches, and it is at least tsel[q] when cand holds
+// lower-bound keys.  Lists shorter than kk leave tau[q] as it is.
+template <int UNITS>
+__global__ __launch_bounds__(1024) void mq1_tau_exact(const uint32_t *codes, const float *scales,
+                                                       const unsigned char *qlev, uint64_t qstride,
+                                                       const uint64_t *cand, const uint32_t *cnt, uint64_t cap,
+                                                       uint32_t kk, const uint64_t *tsel, uint64_t *tau) {
+    __shared__ v4i ql[UNITS * 3];
+    __shared__ uint32_t srow[MQ1_TAU_KK];
+    __shared__ uint64_t wmin[16];
+    __shared__ uint32_t s_n;
+    const uint32_t q = blockIdx.x, tid = threadIdx.x;
+    const uint32_t n = (uint64_t)cnt[q] < cap ? cnt[q] : (uint32_t)cap;
+    if (kk == 0 || kk > (uint32_t)MQ1_TAU_KK || n < kk) return;
+    const unsigned char *src = qlev + (uint64_t)q * qstride;
+    for (uint32_t i = tid; i < UNITS * 3; i += 1024) ql[i] = ((const v4i *)src)[i];
+    const QLevelTail *t = (const QLevelTail *)(src + (uint64_t)UNITS * 48);
+    const double s0 = t->s[0], s1 = t->s[1], s2 = t->s[2];
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    const uint64_t ts = tsel[q];
+    const uint64_t *keys = cand + (uint64_t)q * cap;
+    for (uint32_t i = tid; i < n; i += 1024) {
+        const uint64_t k = keys[i];
+        if (k >= ts) {
+            const uint32_t p = atomicAdd(&s_n, 1u);
+            if (p < kk) srow[p] = key_row(k);
+        }
+    }
+    __syncthreads();
+    if (s_n != kk) return;  // (not reached: exactly kk keys are at or above the kk-th)
+    uint64_t m = ~0ull;
+    mq1_exact_rows<UNITS>(codes, scales, ql, s0, s1, s2, kk, [&](uint32_t i) { return srow[i]; },
+                          [&](uint32_t, uint64_t key) { m = key < m ? key : m; });
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t v = __shfl_xor(m, o);
+        m = v < m ? v : m;
+    }
+    if ((tid & 63) == 0) wmin[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; ++w) m = wmin[w] < m ? wmin[w] : m;
+        m = wmin[0] < m ? wmin[0] : m;
+        tau[q] = tau[q] > m ? tau[q] : m;
     }
 }
 
@@ -1646,6 +1707,28 @@ hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scal
     default: return hipErrorInvalidValue;
     }
 #undef BV_EX_CASE
+    return hipGetLastError();
+}
+
+hipError_t launch_mq1_tau_exact(const uint32_t *codes, uint32_t W, const float *scales,
+                                const unsigned char *qlev, uint64_t qstride, uint32_t units16,
+                                const uint64_t *cand, const uint32_t *cnt, uint64_t cap, uint32_t kk,
+                                const uint64_t *tsel, uint64_t *tau, uint32_t nq, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+    if (W != units16 * 4 || kk > (uint32_t)MQ1_TAU_KK) return hipErrorInvalidValue;
+#define BV_TE_CASE(U)                                                                                          \
+    case U: hipLaunchKernelGGL(mq1_tau_exact<U>, dim3(nq), dim3(1024), 0, s, codes, scales, qlev, qstride, \
+                               cand, cnt, cap, kk, tsel, tau); break;
+    switch (units16) {
+        BV_TE_CASE(2)
+        BV_TE_CASE(4)
+        BV_TE_CASE(8)
+        BV_TE_CASE(16)
+        BV_TE_CASE(32)
+        BV_TE_CASE(64)
+    default: return hipErrorInvalidValue;
+    }
+#undef BV_TE_CASE
     return hipGetLastError();
 }
 
