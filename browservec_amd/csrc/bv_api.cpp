@@ -1825,8 +1825,9 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     Q8Source src{idx->codes.as<uint32_t>(), idx->words_per_row, idx->scales.as<float>(), idx->cnorm.as<float>()};
     // 1-bit asymmetric: the pass over the +1 / -1 expansion with the rotated
     // query's int8 level one (levels without the 1/127), the rows' own
-    // scales and row term 1 (mq1_qconst_l1); the kept rows are re-scored by
-    // the fused scan in indexed mode, which gives them the single-query keys
+    // scales and row term 1 (mq1_qconst_l1); the kept rows get the
+    // single-query keys from q1p_exact_rows (bit-plane codes), or from the
+    // fused scan in indexed mode (C_Q1A)
     const bool asym1 = idx->codec == C_Q1P || idx->codec == C_Q1A;
     int rc = BV_OK;
     if (idx->codec == C_HAM) {
@@ -1917,11 +1918,27 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
     // each bound is then raised to the smallest exact key of the kprime rows
     // that reach it (the kprime-th best exact key of all rows is at least
-    // that), which narrows the rows the passes keep.  The 1-bit asymmetric
-    // keys come from the fused scan, not from these level dots, and Hamming
-    // bounds are exact already (one level, no residual).
-    const bool exact_tau = !asym1 && idx->codec != C_HAM && kprime <= MQ1_TAU_KK;
+    // that), which narrows the rows the passes keep.  Hamming bounds are
+    // exact already (one level, no residual); the 1-bit asymmetric keys
+    // without bit planes (C_Q1A) are left to the fused scan.
+    const bool q1p = idx->codec == C_Q1P;
+    const bool exact_tau = (!asym1 || q1p) && idx->codec != C_HAM && kprime <= MQ1_TAU_KK;
+    // the bit-plane scan's exact keys come from its re-score table over the
+    // rotated queries and its own codes
+    Q1pRowsArgs qa{};
+    qa.codes = idx->codes.p;
+    qa.row_bytes = idx->row_bytes;
+    qa.units = idx->units;
+    qa.P = idx->P;
+    qa.scales = idx->scales.as<float>();
+    qa.scale_mul = 1.0f;
+    qa.qrot = idx->qrot.as<float>();
     auto tighten = [&](const uint64_t *cand, uint64_t ccap, const uint64_t *tsel) {
+        if (q1p) {
+            qa.cap = ccap;
+            return launch_q1p_tau_exact(qa, cand, idx->mq_cnt.as<uint32_t>(), kprime, tsel,
+                                        idx->mq_tau.as<uint64_t>(), nq, s);
+        }
         return launch_mq1_tau_exact(src.codes, src.W, src.scales, qlev, qstride, units16, cand,
                                     idx->mq_cnt.as<uint32_t>(), ccap, kprime, tsel, idx->mq_tau.as<uint64_t>(),
                                     nq, s);
@@ -1987,12 +2004,21 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
          launch_mq1_keep(m.cand, m.up_out, m.cnt, cap, idx->mq_tau.as<uint64_t>(), idx->mq_rows.as<uint32_t>(),
                          idx->mq_kept.as<uint32_t>(), nq, s),
          "batched keep kernel");
-    if (asym1) return finish_batched_indexed(idx, d_q, nq, kprime, k_out, rerank, cap, d_rows, d_scores, d_n);
+    if (asym1 && idx->codec != C_Q1P)
+        return finish_batched_indexed(idx, d_q, nq, kprime, k_out, rerank, cap, d_rows, d_scores, d_n);
     // exact keys of those rows, the best kprime of them, and the re-rank
-    HIPX(idx->dev,
-         launch_mq1_exact(m.codes, m.W, m.scales, qlev, qstride, units16, idx->mq_rows.as<uint32_t>(),
-                          idx->mq_kept.as<uint32_t>(), cap, m.cand, nq, s),
-         "batched exact kernel");
+    if (asym1) {
+        qa.rows = idx->mq_rows.as<uint32_t>();
+        qa.kept = idx->mq_kept.as<uint32_t>();
+        qa.cap = cap;
+        qa.keys = m.cand;
+        HIPX(idx->dev, launch_q1p_exact_rows(qa, nq, 8, s), "batched exact kernel");
+    } else {
+        HIPX(idx->dev,
+             launch_mq1_exact(m.codes, m.W, m.scales, qlev, qstride, units16, idx->mq_rows.as<uint32_t>(),
+                              idx->mq_kept.as<uint32_t>(), cap, m.cand, nq, s),
+             "batched exact kernel");
+    }
     MqSelArgs fa{};
     fa.cand = m.cand;
     fa.cnt = idx->mq_kept.as<uint32_t>();

@@ -116,6 +116,30 @@ struct ScanArgs {
     uint32_t dsteps;          // wave steps per dynamic ticket (0: the kernel's default)
 };
 
+// Exact keys of listed rows of a 1-bit asymmetric (C_Q1P) index, one grid
+// row per query (q1p_exact_rows).
+struct Q1pRowsArgs {
+    const void *codes;        // N rows of row_bytes
+    uint64_t row_bytes;
+    uint32_t units;           // 128-code units per row
+    uint32_t P;               // padded dimension
+    const float *scales;      // per-row scale
+    float scale_mul;
+    const float *qrot;        // nq x P rotated fp32 queries
+    const uint32_t *rows;     // [nq][cap] row ids
+    const uint32_t *kept;     // [nq] listed rows (at most cap used)
+    uint64_t cap;
+    uint64_t *keys;           // [nq][cap] exact scan keys
+};
+// Launches q1p_exact_rows in the fused scan's layout for a.units, with gx
+// workgroups per query.
+hipError_t launch_q1p_exact_rows(const Q1pRowsArgs &a, uint32_t nq, uint32_t gx, hipStream_t s);
+// The 1-bit asymmetric form of launch_mq1_tau_exact: lower-bound keys in
+// cand[q][0, min(cnt[q], a.cap)), the kk-th best in tsel[q]; tau[q] raised
+// to the smallest exact key of those kk rows (a.rows, a.kept, a.keys unused).
+hipError_t launch_q1p_tau_exact(const Q1pRowsArgs &a, const uint64_t *cand, const uint32_t *cnt, uint32_t kk,
+                                const uint64_t *tsel, uint64_t *tau, uint32_t nq, hipStream_t s);
+
 // Rows per wave below which a scan takes the short tail (a wave then scans
 // too few steps for the threshold helper's bound to reach it through the
 // usual polling, so a flush by the wave's own bound would carry, and

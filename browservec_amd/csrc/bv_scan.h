@@ -1805,6 +1805,25 @@ __device__ __forceinline__ float float_below(float x) {
     return __uint_as_float((b & 0x80000000u) ? b + 1 : b - 1);
 }
 
+// A lane's part of a row's exact 1-bit asymmetric sum: its units' 32 nibble
+// entries of the re-score table (q1p_lut_build) each, added in order.
+template <int LPR, int UPL>
+__device__ __forceinline__ float q1p_exact_partial(const ScanRegs<C_Q1P, UPL> &R, const uint4 (&d)[UPL], int pl) {
+    float e = 0.0f;
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+        if (!R.uok[t]) continue;
+        const float *lt = R.qf + (size_t)(pl + LPR * t) * Q1P_LUT_UNIT;
+        const uint32_t w[4] = {d[t].x, d[t].y, d[t].z, d[t].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) e += lt[(k * 8 + c) * 16 + ((w[k] >> (4 * c)) & 15u)];
+        }
+    }
+    return e;
+}
+
 // C_Q1P: every row is scored through the levels' bit planes, exact integers
 // T1, T2 = sums of Q1, Q2 over the row's set code bits.  A row group in
 // which some row's bound on its exact score reaches the wave's bound is
@@ -1868,23 +1887,11 @@ __device__ __forceinline__ void compute_step_q1p(const ScanArgs &a, const ScanRe
         float ex[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float e = 0.0f;
             if (__ballot(need && xr == u) == 0) {
-                ex[u] = e;
+                ex[u] = 0.0f;
                 continue;
             }
-#pragma unroll
-            for (int t = 0; t < UPL; ++t) {
-                if (!R.uok[t]) continue;
-                const float *lt = R.qf + (size_t)(pl + LPR * t) * Q1P_LUT_UNIT;
-                const uint32_t w[4] = {S.d[u][t].x, S.d[u][t].y, S.d[u][t].z, S.d[u][t].w};
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-#pragma unroll
-                    for (int c = 0; c < 8; ++c) e += lt[(d * 8 + c) * 16 + ((w[d] >> (4 * c)) & 15u)];
-                }
-            }
-            ex[u] = e;
+            ex[u] = q1p_exact_partial<LPR, UPL>(R, S.d[u], pl);
         }
         const float tot = xreduce<U, LPR>(ex, lane);
         if (need) {
@@ -2683,6 +2690,124 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     if (tid == 0) L.last = atomicAdd(&qs->fin, 1u) == 1;
     __syncthreads();
     if (L.last) reset_query(a, qi);
+}
+
+// Exact keys of listed rows for the 1-bit asymmetric batch: rows[q][0,
+// min(kept[q], cap)) of query q (grid row y), each row's key computed as
+// compute_step_q1p computes it (the same layout, table, partial sums,
+// reduction and row scale), into keys[q][i].  The re-score table is built
+// from the rotated fp32 query qrot[q] in LDS; grid column x takes every
+// gridDim.x-th wave step of the list.
+template <int LPR, int UPL>
+__global__ __launch_bounds__(SCAN_WG) void q1p_exact_rows(Q1pRowsArgs a) {
+    using SH = ScanShape<C_Q1P, LPR, UPL>;
+    constexpr int U = SH::U, G = SH::G;
+    extern __shared__ __align__(16) unsigned char q1p_smem[];
+    float *lut = (float *)q1p_smem;
+    const uint32_t q = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    q1p_lut_build(a.qrot + (uint64_t)q * a.P, a.P, lut, (uint32_t)tid, SCAN_WG);
+    __syncthreads();
+    ScanRegs<C_Q1P, UPL> R{};
+    const int pl = lane % LPR;
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+        const uint32_t unit = pl + LPR * t;
+        R.uok[t] = unit < a.units;
+        R.ucl[t] = R.uok[t] ? unit : a.units - 1;
+    }
+    R.qf = lut;
+    ScanArgs sa{};
+    sa.codes = a.codes;
+    sa.row_bytes = a.row_bytes;
+    sa.scales = a.scales;
+    const uint32_t n = a.kept[q] < a.cap ? a.kept[q] : (uint32_t)a.cap;
+    const uint32_t *cand = a.rows + (uint64_t)q * a.cap;
+    uint64_t *out = a.keys + (uint64_t)q * a.cap;
+    const uint32_t stride = gridDim.x * (uint32_t)SH::WAVES * SH::RPS;
+    for (uint32_t base = (blockIdx.x * SH::WAVES + (uint32_t)wave) * SH::RPS; base < n; base += stride) {
+        StepData<C_Q1P, LPR, UPL> S;
+        load_step<C_Q1P, LPR, UPL, true>(sa, R, cand, base, n, S, lane);
+        float ex[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) ex[u] = q1p_exact_partial<LPR, UPL>(R, S.d[u], pl);
+        const float tot = xreduce<U, LPR>(ex, lane);
+        const uint32_t myrow = base + (uint32_t)(xrow<U, LPR>(lane) * G + lane / LPR);
+        if (xrep<U, LPR>(lane) && myrow < n) out[myrow] = make_key(ord_f32(tot * (S.scale * a.scale_mul)), S.grow);
+    }
+}
+
+// The 1-bit asymmetric counterpart of mq1_tau_exact (one workgroup per
+// query): the kk keys of cand[q][0, min(cnt[q], cap)) at or above tsel[q]
+// name kk distinct rows; tau[q] = max(tau[q], the smallest of their exact
+// keys, computed as q1p_exact_rows computes them).  Lists shorter than kk
+// leave tau[q] as it is.
+template <int LPR, int UPL>
+__global__ __launch_bounds__(SCAN_WG) void q1p_tau_exact(Q1pRowsArgs a, const uint64_t *cand, const uint32_t *cnt,
+                                                          uint32_t kk, const uint64_t *tsel, uint64_t *tau) {
+    using SH = ScanShape<C_Q1P, LPR, UPL>;
+    constexpr int U = SH::U, G = SH::G;
+    extern __shared__ __align__(16) unsigned char q1p_smem[];
+    float *lut = (float *)q1p_smem;
+    uint32_t *srow = (uint32_t *)(q1p_smem + q1p_lut_bytes(a.P));
+    __shared__ uint32_t s_n;
+    __shared__ uint64_t wmin[SH::WAVES];
+    const uint32_t q = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t n = cnt[q] < a.cap ? cnt[q] : (uint32_t)a.cap;
+    if (kk == 0 || kk > MQ1_TAU_KK || n < kk) return;
+    q1p_lut_build(a.qrot + (uint64_t)q * a.P, a.P, lut, (uint32_t)tid, SCAN_WG);
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    const uint64_t ts = tsel[q];
+    const uint64_t *keys = cand + (uint64_t)q * a.cap;
+    for (uint32_t i = (uint32_t)tid; i < n; i += SCAN_WG) {
+        const uint64_t k = keys[i];
+        if (k >= ts) {
+            const uint32_t p = atomicAdd(&s_n, 1u);
+            if (p < kk) srow[p] = key_row(k);
+        }
+    }
+    __syncthreads();
+    if (s_n != kk) return;  // (not reached: exactly kk keys are at or above the kk-th)
+    ScanRegs<C_Q1P, UPL> R{};
+    const int pl = lane % LPR;
+#pragma unroll
+    for (int t = 0; t < UPL; ++t) {
+        const uint32_t unit = pl + LPR * t;
+        R.uok[t] = unit < a.units;
+        R.ucl[t] = R.uok[t] ? unit : a.units - 1;
+    }
+    R.qf = lut;
+    ScanArgs sa{};
+    sa.codes = a.codes;
+    sa.row_bytes = a.row_bytes;
+    sa.scales = a.scales;
+    uint64_t m = ~0ull;
+    for (uint32_t base = (uint32_t)wave * SH::RPS; base < kk; base += (uint32_t)SH::WAVES * SH::RPS) {
+        StepData<C_Q1P, LPR, UPL> S;
+        load_step<C_Q1P, LPR, UPL, true>(sa, R, srow, base, kk, S, lane);
+        float ex[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) ex[u] = q1p_exact_partial<LPR, UPL>(R, S.d[u], pl);
+        const float tot = xreduce<U, LPR>(ex, lane);
+        const uint32_t myrow = base + (uint32_t)(xrow<U, LPR>(lane) * G + lane / LPR);
+        if (xrep<U, LPR>(lane) && myrow < kk) {
+            const uint64_t key = make_key(ord_f32(tot * (S.scale * a.scale_mul)), S.grow);
+            m = key < m ? key : m;
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t v = __shfl_xor(m, o);
+        m = v < m ? v : m;
+    }
+    if (lane == 0) wmin[wave] = m;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 0; w < SH::WAVES; ++w) m = wmin[w] < m ? wmin[w] : m;
+        tau[q] = tau[q] > m ? tau[q] : m;
+    }
 }
 
 // -------------------------------------------------- layouts and dispatch --
