@@ -1915,14 +1915,13 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     sa.cap = S;
     sa.kk = kprime;
     sa.tau = idx->mq_tau.as<uint64_t>();
-    HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
     // each bound is then raised to the smallest exact key of the kprime rows
     // that reach it (the kprime-th best exact key of all rows is at least
     // that), which narrows the rows the passes keep.  Hamming bounds are
     // exact already (one level, no residual); the 1-bit asymmetric keys
     // without bit planes (C_Q1A) are left to the fused scan.
     const bool q1p = idx->codec == C_Q1P;
-    const bool exact_tau = (!asym1 || q1p) && idx->codec != C_HAM && kprime <= MQ1_TAU_KK;
+    const bool exact_tau = (!asym1 || q1p) && idx->codec != C_HAM && kprime <= 2048;
     // the bit-plane scan's exact keys come from its re-score table over the
     // rotated queries and its own codes
     Q1pRowsArgs qa{};
@@ -1933,17 +1932,31 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     qa.scales = idx->scales.as<float>();
     qa.scale_mul = 1.0f;
     qa.qrot = idx->qrot.as<float>();
-    auto tighten = [&](const uint64_t *cand, uint64_t ccap, const uint64_t *tsel) {
-        if (q1p) {
-            qa.cap = ccap;
-            return launch_q1p_tau_exact(qa, cand, idx->mq_cnt.as<uint32_t>(), kprime, tsel,
+    // the select writes the list's kprime best lower-bound keys, in order, to
+    // merged (free until the final select), and their exact keys raise tau
+    auto tighten = [&]() {
+        if (q1p)
+            return launch_q1p_tau_exact(qa, idx->merged.as<uint64_t>(), idx->merged_n.as<uint32_t>(), kprime,
                                         idx->mq_tau.as<uint64_t>(), nq, s);
-        }
-        return launch_mq1_tau_exact(src.codes, src.W, src.scales, qlev, qstride, units16, cand,
-                                    idx->mq_cnt.as<uint32_t>(), ccap, kprime, tsel, idx->mq_tau.as<uint64_t>(),
-                                    nq, s);
+        return launch_mq1_tau_exact(src.codes, src.W, src.scales, qlev, qstride, units16, idx->merged.as<uint64_t>(),
+                                    idx->merged_n.as<uint32_t>(), kprime, idx->mq_tau.as<uint64_t>(), nq, s);
     };
-    if (exact_tau) HIPX(idx->dev, tighten(m.cand, S, idx->mq_tau.as<uint64_t>()), "batched bound kernel");
+    auto select_bound = [&](uint64_t ccap, uint64_t *tau_out) {
+        sa.cap = ccap;
+        sa.tau = tau_out;
+        sa.merged = idx->merged.as<uint64_t>();
+        sa.merged_n = idx->merged_n.as<uint32_t>();
+        const hipError_t e = launch_mq_select(sa, nq, s);
+        sa.merged = nullptr;
+        sa.merged_n = nullptr;
+        return e;
+    };
+    if (exact_tau) {
+        HIPX(idx->dev, select_bound(S, idx->mq_tau.as<uint64_t>()), "batched select kernel");
+        HIPX(idx->dev, tighten(), "batched bound kernel");
+    } else {
+        HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
+    }
     // the pass over every row keeps the rows whose upper bound reaches the
     // bound, into the workgroups' buckets, then one list per query.  It runs
     // in two parts: the first eighth of the rows, whose kept rows' kprime-th
@@ -1974,9 +1987,8 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
         if (part == 0) {  // the tighter bound
             sa.cap = cap;
             if (exact_tau) {
-                sa.tau = idx->mq_tau2.as<uint64_t>();
-                HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
-                HIPX(idx->dev, tighten(idx->mq_cand.as<uint64_t>(), cap, sa.tau), "batched bound kernel");
+                HIPX(idx->dev, select_bound(cap, idx->mq_tau2.as<uint64_t>()), "batched select kernel");
+                HIPX(idx->dev, tighten(), "batched bound kernel");
                 sa.tau = idx->mq_tau.as<uint64_t>();
             } else {
                 sa.tau_max = true;
@@ -1994,9 +2006,8 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     // and the rows whose upper bound reaches it
     sa.cap = cap;
     if (exact_tau) {
-        sa.tau = idx->mq_tau2.as<uint64_t>();
-        HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
-        HIPX(idx->dev, tighten(m.cand, cap, sa.tau), "batched bound kernel");
+        HIPX(idx->dev, select_bound(cap, idx->mq_tau2.as<uint64_t>()), "batched select kernel");
+        HIPX(idx->dev, tighten(), "batched bound kernel");
     } else {
         HIPX(idx->dev, launch_mq_select(sa, nq, s), "batched select kernel");
     }

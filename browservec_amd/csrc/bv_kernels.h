@@ -134,11 +134,10 @@ struct Q1pRowsArgs {
 // Launches q1p_exact_rows in the fused scan's layout for a.units, with gx
 // workgroups per query.
 hipError_t launch_q1p_exact_rows(const Q1pRowsArgs &a, uint32_t nq, uint32_t gx, hipStream_t s);
-// The 1-bit asymmetric form of launch_mq1_tau_exact: lower-bound keys in
-// cand[q][0, min(cnt[q], a.cap)), the kk-th best in tsel[q]; tau[q] raised
-// to the smallest exact key of those kk rows (a.rows, a.kept, a.keys unused).
-hipError_t launch_q1p_tau_exact(const Q1pRowsArgs &a, const uint64_t *cand, const uint32_t *cnt, uint32_t kk,
-                                const uint64_t *tsel, uint64_t *tau, uint32_t nq, hipStream_t s);
+// The 1-bit asymmetric form of launch_mq1_tau_exact (a.rows, a.kept, a.cap
+// and a.keys unused).  kk <= 4096.
+hipError_t launch_q1p_tau_exact(const Q1pRowsArgs &a, const uint64_t *merged, const uint32_t *merged_n, uint32_t kk,
+                                uint64_t *tau, uint32_t nq, hipStream_t s);
 
 // Rows per wave below which a scan takes the short tail (a wave then scans
 // too few steps for the threshold helper's bound to reach it through the
@@ -422,14 +421,13 @@ hipError_t launch_mq1_keep(const uint64_t *cand, const uint32_t *up, const uint3
 hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scales, const unsigned char *qlev,
                             uint64_t qstride, uint32_t units16, const uint32_t *rows, const uint32_t *kept,
                             uint64_t cap, uint64_t *keys, uint32_t nq, hipStream_t s);
-// Per query: tau[q] = max(tau[q], the smallest exact key of the kk rows
-// whose keys in cand[q][0, min(cnt[q], cap)) reach tsel[q], that list's
-// kk-th best key); lists shorter than kk are left alone.  kk <= MQ1_TAU_KK.
-constexpr uint32_t MQ1_TAU_KK = 4096;
+// Per query: tau[q] = max(tau[q], the smallest exact key of the rows of
+// merged[q][0, kk), a list's kk best lower-bound keys (mq_select's sorted
+// output); nothing when merged_n[q] < kk.
 hipError_t launch_mq1_tau_exact(const uint32_t *codes, uint32_t W, const float *scales,
                                 const unsigned char *qlev, uint64_t qstride, uint32_t units16,
-                                const uint64_t *cand, const uint32_t *cnt, uint64_t cap, uint32_t kk,
-                                const uint64_t *tsel, uint64_t *tau, uint32_t nq, hipStream_t s);
+                                const uint64_t *merged, const uint32_t *merged_n, uint32_t kk, uint64_t *tau,
+                                uint32_t nq, hipStream_t s);
 hipError_t launch_row_code_norms(const uint32_t *codes, uint64_t n, uint32_t W, float *cn, hipStream_t s);
 hipError_t launch_mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32_t units, uint32_t tail_off,
                              uint32_t nq, float *rq, uint32_t *cnt, uint32_t cnt_value, hipStream_t s);

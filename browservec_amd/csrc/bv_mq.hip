@@ -1425,44 +1425,30 @@ __global__ __launch_bounds__(1024) void mq1_exact(const uint32_t *codes, const f
                           [&](uint32_t i, uint64_t key) { out[i] = key; });
 }
 
-// A tighter bound from exact keys, one workgroup per query: the kk keys of
-// cand[q][0, min(cnt[q], cap)) at or above tsel[q] (that list's kk-th best
-// key, so exactly kk of them: keys are unique) name kk distinct rows; the
-// smallest of their exact keys is at most the kk-th best exact key of all
-// rows, so tau[q] = max(tau[q], that key) is still a bound that every row
-// of the exact top kk reaches, and it is at least tsel[q] when cand holds
-// lower-bound keys.  Lists shorter than kk leave tau[q] as it is.
+// A tighter bound from exact keys, one workgroup per query: merged[q][0,
+// kk) holds the kk best lower-bound keys of a list (mq_select's sorted
+// output), so they name kk distinct rows; the smallest of their exact keys
+// is at most the kk-th best exact key of all rows, so tau[q] = max(tau[q],
+// that key) is still a bound that every row of the exact top kk reaches, and
+// it is at least the list's kk-th lower-bound key.  A list shorter than kk
+// (merged_n[q] < kk) leaves tau[q] as it is.
 template <int UNITS>
 __global__ __launch_bounds__(1024) void mq1_tau_exact(const uint32_t *codes, const float *scales,
                                                        const unsigned char *qlev, uint64_t qstride,
-                                                       const uint64_t *cand, const uint32_t *cnt, uint64_t cap,
-                                                       uint32_t kk, const uint64_t *tsel, uint64_t *tau) {
+                                                       const uint64_t *merged, const uint32_t *merged_n, uint32_t kk,
+                                                       uint64_t *tau) {
     __shared__ v4i ql[UNITS * 3];
-    __shared__ uint32_t srow[MQ1_TAU_KK];
     __shared__ uint64_t wmin[16];
-    __shared__ uint32_t s_n;
     const uint32_t q = blockIdx.x, tid = threadIdx.x;
-    const uint32_t n = (uint64_t)cnt[q] < cap ? cnt[q] : (uint32_t)cap;
-    if (kk == 0 || kk > (uint32_t)MQ1_TAU_KK || n < kk) return;
+    if (kk == 0 || merged_n[q] < kk) return;
     const unsigned char *src = qlev + (uint64_t)q * qstride;
     for (uint32_t i = tid; i < UNITS * 3; i += 1024) ql[i] = ((const v4i *)src)[i];
     const QLevelTail *t = (const QLevelTail *)(src + (uint64_t)UNITS * 48);
     const double s0 = t->s[0], s1 = t->s[1], s2 = t->s[2];
-    if (tid == 0) s_n = 0;
     __syncthreads();
-    const uint64_t ts = tsel[q];
-    const uint64_t *keys = cand + (uint64_t)q * cap;
-    for (uint32_t i = tid; i < n; i += 1024) {
-        const uint64_t k = keys[i];
-        if (k >= ts) {
-            const uint32_t p = atomicAdd(&s_n, 1u);
-            if (p < kk) srow[p] = key_row(k);
-        }
-    }
-    __syncthreads();
-    if (s_n != kk) return;  // (not reached: exactly kk keys are at or above the kk-th)
+    const uint64_t *mk = merged + (uint64_t)q * kk;
     uint64_t m = ~0ull;
-    mq1_exact_rows<UNITS>(codes, scales, ql, s0, s1, s2, kk, [&](uint32_t i) { return srow[i]; },
+    mq1_exact_rows<UNITS>(codes, scales, ql, s0, s1, s2, kk, [&](uint32_t i) { return key_row(mk[i]); },
                           [&](uint32_t, uint64_t key) { m = key < m ? key : m; });
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -1472,8 +1458,7 @@ __global__ __launch_bounds__(1024) void mq1_tau_exact(const uint32_t *codes, con
     if ((tid & 63) == 0) wmin[tid >> 6] = m;
     __syncthreads();
     if (tid == 0) {
-        for (int w = 1; w < 16; ++w) m = wmin[w] < m ? wmin[w] : m;
-        m = wmin[0] < m ? wmin[0] : m;
+        for (int w = 0; w < 16; ++w) m = wmin[w] < m ? wmin[w] : m;
         tau[q] = tau[q] > m ? tau[q] : m;
     }
 }
@@ -1712,13 +1697,13 @@ hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scal
 
 hipError_t launch_mq1_tau_exact(const uint32_t *codes, uint32_t W, const float *scales,
                                 const unsigned char *qlev, uint64_t qstride, uint32_t units16,
-                                const uint64_t *cand, const uint32_t *cnt, uint64_t cap, uint32_t kk,
-                                const uint64_t *tsel, uint64_t *tau, uint32_t nq, hipStream_t s) {
+                                const uint64_t *merged, const uint32_t *merged_n, uint32_t kk, uint64_t *tau,
+                                uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
-    if (W != units16 * 4 || kk > (uint32_t)MQ1_TAU_KK) return hipErrorInvalidValue;
+    if (W != units16 * 4) return hipErrorInvalidValue;
 #define BV_TE_CASE(U)                                                                                          \
     case U: hipLaunchKernelGGL(mq1_tau_exact<U>, dim3(nq), dim3(1024), 0, s, codes, scales, qlev, qstride, \
-                               cand, cnt, cap, kk, tsel, tau); break;
+                               merged, merged_n, kk, tau); break;
     switch (units16) {
         BV_TE_CASE(2)
         BV_TE_CASE(4)

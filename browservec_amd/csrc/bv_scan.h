@@ -2738,38 +2738,25 @@ __global__ __launch_bounds__(SCAN_WG) void q1p_exact_rows(Q1pRowsArgs a) {
 }
 
 // The 1-bit asymmetric counterpart of mq1_tau_exact (one workgroup per
-// query): the kk keys of cand[q][0, min(cnt[q], cap)) at or above tsel[q]
-// name kk distinct rows; tau[q] = max(tau[q], the smallest of their exact
-// keys, computed as q1p_exact_rows computes them).  Lists shorter than kk
-// leave tau[q] as it is.
+// query): tau[q] = max(tau[q], the smallest exact key, computed as
+// q1p_exact_rows computes it, of the rows of merged[q][0, kk)); nothing when
+// merged_n[q] < kk.
 template <int LPR, int UPL>
-__global__ __launch_bounds__(SCAN_WG) void q1p_tau_exact(Q1pRowsArgs a, const uint64_t *cand, const uint32_t *cnt,
-                                                          uint32_t kk, const uint64_t *tsel, uint64_t *tau) {
+__global__ __launch_bounds__(SCAN_WG) void q1p_tau_exact(Q1pRowsArgs a, const uint64_t *merged,
+                                                          const uint32_t *merged_n, uint32_t kk, uint64_t *tau) {
     using SH = ScanShape<C_Q1P, LPR, UPL>;
     constexpr int U = SH::U, G = SH::G;
     extern __shared__ __align__(16) unsigned char q1p_smem[];
     float *lut = (float *)q1p_smem;
     uint32_t *srow = (uint32_t *)(q1p_smem + q1p_lut_bytes(a.P));
-    __shared__ uint32_t s_n;
     __shared__ uint64_t wmin[SH::WAVES];
     const uint32_t q = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t n = cnt[q] < a.cap ? cnt[q] : (uint32_t)a.cap;
-    if (kk == 0 || kk > MQ1_TAU_KK || n < kk) return;
+    if (kk == 0 || merged_n[q] < kk) return;
     q1p_lut_build(a.qrot + (uint64_t)q * a.P, a.P, lut, (uint32_t)tid, SCAN_WG);
-    if (tid == 0) s_n = 0;
+    const uint64_t *mk = merged + (uint64_t)q * kk;
+    for (uint32_t i = (uint32_t)tid; i < kk; i += SCAN_WG) srow[i] = key_row(mk[i]);
     __syncthreads();
-    const uint64_t ts = tsel[q];
-    const uint64_t *keys = cand + (uint64_t)q * a.cap;
-    for (uint32_t i = (uint32_t)tid; i < n; i += SCAN_WG) {
-        const uint64_t k = keys[i];
-        if (k >= ts) {
-            const uint32_t p = atomicAdd(&s_n, 1u);
-            if (p < kk) srow[p] = key_row(k);
-        }
-    }
-    __syncthreads();
-    if (s_n != kk) return;  // (not reached: exactly kk keys are at or above the kk-th)
     ScanRegs<C_Q1P, UPL> R{};
     const int pl = lane % LPR;
 #pragma unroll

@@ -16,33 +16,33 @@ hipError_t exact_rows(const Q1pRowsArgs &a, uint32_t nq, uint32_t gx, hipStream_
     return hipGetLastError();
 }
 template <int LPR, int UPL>
-hipError_t tau_exact(const Q1pRowsArgs &a, const uint64_t *cand, const uint32_t *cnt, uint32_t kk,
-                     const uint64_t *tsel, uint64_t *tau, uint32_t nq, hipStream_t s) {
-    const size_t lds = q1p_lut_bytes(a.P) + (size_t)MQ1_TAU_KK * 4;
-    if (lds > 160 * 1024 || a.units == 0 || a.P != a.units * 128 || kk > MQ1_TAU_KK) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((q1p_tau_exact<LPR, UPL>), dim3(1, nq), dim3(SCAN_WG), lds, s, a, cand, cnt, kk, tsel, tau);
+hipError_t tau_exact(const Q1pRowsArgs &a, const uint64_t *merged, const uint32_t *merged_n, uint32_t kk,
+                     uint64_t *tau, uint32_t nq, hipStream_t s) {
+    const size_t lds = q1p_lut_bytes(a.P) + (size_t)kk * 4;
+    if (lds > 160 * 1024 || a.units == 0 || a.P != a.units * 128 || kk > 4096) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((q1p_tau_exact<LPR, UPL>), dim3(1, nq), dim3(SCAN_WG), lds, s, a, merged, merged_n, kk, tau);
     return hipGetLastError();
 }
 }  // namespace
 
-hipError_t launch_q1p_tau_exact(const Q1pRowsArgs &a, const uint64_t *cand, const uint32_t *cnt, uint32_t kk,
-                                const uint64_t *tsel, uint64_t *tau, uint32_t nq, hipStream_t s) {
+hipError_t launch_q1p_tau_exact(const Q1pRowsArgs &a, const uint64_t *merged, const uint32_t *merged_n, uint32_t kk,
+                                uint64_t *tau, uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
     Layout L;
     if (nq > 65535 || !pick_layout(a.units, L)) return hipErrorInvalidValue;
     if (L.lpr == 64) {
         switch (L.upl) {
-        case 1: return tau_exact<64, 1>(a, cand, cnt, kk, tsel, tau, nq, s);
-        case 2: return tau_exact<64, 2>(a, cand, cnt, kk, tsel, tau, nq, s);
+        case 1: return tau_exact<64, 1>(a, merged, merged_n, kk, tau, nq, s);
+        case 2: return tau_exact<64, 2>(a, merged, merged_n, kk, tau, nq, s);
         default: return hipErrorInvalidValue;
         }
     }
     if (L.upl != 1) return hipErrorInvalidValue;
     switch (L.lpr) {
-    case 4: return tau_exact<4, 1>(a, cand, cnt, kk, tsel, tau, nq, s);
-    case 8: return tau_exact<8, 1>(a, cand, cnt, kk, tsel, tau, nq, s);
-    case 16: return tau_exact<16, 1>(a, cand, cnt, kk, tsel, tau, nq, s);
-    case 32: return tau_exact<32, 1>(a, cand, cnt, kk, tsel, tau, nq, s);
+    case 4: return tau_exact<4, 1>(a, merged, merged_n, kk, tau, nq, s);
+    case 8: return tau_exact<8, 1>(a, merged, merged_n, kk, tau, nq, s);
+    case 16: return tau_exact<16, 1>(a, merged, merged_n, kk, tau, nq, s);
+    case 32: return tau_exact<32, 1>(a, merged, merged_n, kk, tau, nq, s);
     default: return hipErrorInvalidValue;
     }
 }
