@@ -29,20 +29,10 @@ hipError_t launch_q1p_tau_exact(const Q1pRowsArgs &a, const uint64_t *merged, co
                                 uint64_t *tau, uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
     Layout L;
-    if (nq > 65535 || !pick_layout(a.units, L)) return hipErrorInvalidValue;
-    if (L.lpr == 64) {
-        switch (L.upl) {
-        case 1: return tau_exact<64, 1>(a, merged, merged_n, kk, tau, nq, s);
-        case 2: return tau_exact<64, 2>(a, merged, merged_n, kk, tau, nq, s);
-        default: return hipErrorInvalidValue;
-        }
-    }
-    if (L.upl != 1) return hipErrorInvalidValue;
-    switch (L.lpr) {
+    if (nq > 65535 || !pick_layout(a.units, L) || L.upl != 1) return hipErrorInvalidValue;
+    switch (L.lpr) {  // the batch path's dimensions (P <= 1024)
     case 4: return tau_exact<4, 1>(a, merged, merged_n, kk, tau, nq, s);
     case 8: return tau_exact<8, 1>(a, merged, merged_n, kk, tau, nq, s);
-    case 16: return tau_exact<16, 1>(a, merged, merged_n, kk, tau, nq, s);
-    case 32: return tau_exact<32, 1>(a, merged, merged_n, kk, tau, nq, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -50,21 +40,10 @@ hipError_t launch_q1p_tau_exact(const Q1pRowsArgs &a, const uint64_t *merged, co
 hipError_t launch_q1p_exact_rows(const Q1pRowsArgs &a, uint32_t nq, uint32_t gx, hipStream_t s) {
     if (nq == 0) return hipSuccess;
     Layout L;
-    if (gx == 0 || nq > 65535 || !pick_layout(a.units, L)) return hipErrorInvalidValue;
-    const int lpr = L.lpr, upl = L.upl;  // the fused scan's layout, so the sums run in its order
-    if (lpr == 64) {
-        switch (upl) {
-        case 1: return exact_rows<64, 1>(a, nq, gx, s);
-        case 2: return exact_rows<64, 2>(a, nq, gx, s);
-        default: return hipErrorInvalidValue;
-        }
-    }
-    if (upl != 1) return hipErrorInvalidValue;
-    switch (lpr) {
+    if (gx == 0 || nq > 65535 || !pick_layout(a.units, L) || L.upl != 1) return hipErrorInvalidValue;
+    switch (L.lpr) {  // the fused scan's layout, so the sums run in its order (P <= 1024)
     case 4: return exact_rows<4, 1>(a, nq, gx, s);
     case 8: return exact_rows<8, 1>(a, nq, gx, s);
-    case 16: return exact_rows<16, 1>(a, nq, gx, s);
-    case 32: return exact_rows<32, 1>(a, nq, gx, s);
     default: return hipErrorInvalidValue;
     }
 }

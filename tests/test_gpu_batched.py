@@ -289,10 +289,12 @@ def test_batched_1bit_asym_equals_singles(ctx, dim, n, nq):
     int8 first-level pass over the +1 / -1 expansion with the rotated query's
     int8 level one: the score scale * sum_i (bit_i ? x_i : -x_i) lies within
     scale * (|x - s1 q1|_1 + the f32 summation slack) of scale * s1 * D, D
-    the level-one dot; the rows that can still reach a query's fetch are
-    re-scored by the fused scan in indexed mode.  Rows and score bits equal
-    the same queries run alone, with and without the re-rank, across appends
-    (the expansion follows them), with duplicate rows tying."""
+    the level-one dot; the rows that can still reach a query's fetch get
+    their exact keys from q1p_exact_rows, in the single-query scan's own
+    layout (4 and 8 lanes per row at these dimensions).  Rows and score
+    bits equal the same queries run alone, with and without the re-rank,
+    across appends (the expansion follows them), with duplicate rows
+    tying."""
     from browservec_amd import QuantIndex
 
     say("batched 1-bit asym", dim, n, nq)
