@@ -814,7 +814,7 @@ __device__ uint32_t wave_count_ge(const uint64_t *wk, uint32_t wc, uint64_t t, i
 __device__ uint64_t wave_bound(const uint64_t *wk, uint32_t wc, uint64_t lo, uint32_t kp, uint32_t target, int lane) {
     uint64_t mx = 0;
     for (uint32_t j = lane; j < wc; j += 64) mx = wk[j] > mx ? wk[j] : mx;
-    uint64_t hi = wave_max_u64(mx) + 1;  // nothing at or above hi
+    uint64_t hi = uniform_u64(wave_max_u64(mx)) + 1;  // nothing at or above hi
     while (hi - lo > 1) {
         const uint64_t mid = lo + ((hi - lo) >> 1);
         const uint32_t c = wave_count_ge(wk, wc, mid, lane);
@@ -2038,7 +2038,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
 
     const uint32_t qi = blockIdx.y;
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     QState *qs = a.qs + qi;
     const uint32_t kp = a.kprime;
 
@@ -2119,15 +2119,10 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     // false when every slice is exhausted
     auto take_chunk = [&]() -> bool {
         for (;;) {
-            uint32_t t;
-            if (has_pend) {
-                t = __builtin_amdgcn_readfirstlane(pend);
-                has_pend = false;
-            } else {
-                uint32_t v = 0;
-                if (lane == 0) v = atomicAdd(&qs->dyn[slice * CL], 1u);
-                t = __builtin_amdgcn_readfirstlane(v);
-            }
+            uint32_t v = pend;
+            if (!has_pend && lane == 0) v = atomicAdd(&qs->dyn[slice * CL], 1u);
+            has_pend = false;
+            const uint32_t t = __builtin_amdgcn_readfirstlane(v);
             const uint32_t ls = slice_steps(slice), nb = big_chunks(ls);
             if (t < nb + (ls - nb * dsteps)) {
                 if (lane == 0) pend = atomicAdd(&qs->dyn[slice * CL], 1u);  // next ticket in flight
@@ -2147,7 +2142,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
                 const uint64_t L = slice_tickets((uint32_t)lane);
                 rem = c < L ? L - c : 0;
             }
-            const uint64_t best = wave_max_u64((rem << 32) | (uint32_t)lane);
+            const uint64_t best = uniform_u64(wave_max_u64((rem << 32) | (uint32_t)lane));
             if ((best >> 32) == 0) return false;
             slice = (uint32_t)best;
         }
@@ -2310,6 +2305,24 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
     uint64_t gt = 0;      // what the previous pass read: the shared bound when it polled
     bool polled = false;
     for (uint32_t pi = 0; ha; ++pi) {
+        // the loop state is wave-uniform: restated so the compiler keeps it
+        // (and the stepping branches) scalar
+        ab = __builtin_amdgcn_readfirstlane(ab);
+        al = __builtin_amdgcn_readfirstlane(al);
+        bb = __builtin_amdgcn_readfirstlane(bb);
+        bl = __builtin_amdgcn_readfirstlane(bl);
+        gi = __builtin_amdgcn_readfirstlane(gi);
+        sub = __builtin_amdgcn_readfirstlane(sub);
+        ds = __builtin_amdgcn_readfirstlane(ds);
+        dlen = __builtin_amdgcn_readfirstlane(dlen);
+        c0 = __builtin_amdgcn_readfirstlane(c0);
+        clim = __builtin_amdgcn_readfirstlane(clim);
+        slice = __builtin_amdgcn_readfirstlane(slice);
+        wc = __builtin_amdgcn_readfirstlane(wc);
+        hb = __builtin_amdgcn_readfirstlane((int)hb) != 0;
+        dynamic = __builtin_amdgcn_readfirstlane((int)dynamic) != 0;
+        has_pend = __builtin_amdgcn_readfirstlane((int)has_pend) != 0;
+        tau = uniform_u64(tau);
         if constexpr (PIPE) {
             // steps alternate between A and B; the other buffer's loads are
             // in flight while one is scored
@@ -2334,7 +2347,7 @@ __global__ __launch_bounds__(SCAN_WG) void scan_topk(ScanArgs a) {
                                    __HIP_MEMORY_SCOPE_AGENT);
             const bool nb = na && next_step(bb, bl);
             load_step<C, LPR, UPL, IDX>(a, R, cand, nb ? bb : 0, nb ? bl : 1, B, lane);
-            ha = na;
+                        ha = na;
             hb = nb;
         } else {
             load_step<C, LPR, UPL, IDX>(a, R, cand, ab, al, A, lane);
