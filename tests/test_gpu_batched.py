@@ -135,6 +135,29 @@ def test_batched_overflow_falls_back(ctx):
     idx.destroy()
 
 
+@pytest.mark.parametrize("scorer", ["asym", "hamming"])
+def test_batched_1bit_overflow_falls_back(ctx, scorer):
+    """The overflow case of test_batched_overflow_falls_back on 1-bit codes:
+    the sampled rows score low, every unsampled row can reach the bound,
+    the kept lists overflow and those queries run alone (for the asymmetric
+    scorer after the exact bound raises), still equal to single queries."""
+    from browservec_amd import QuantIndex
+
+    dim, n, nq = 128, 40000, 8
+    say("batched 1-bit overflow", scorer)
+    rng = np.random.default_rng(15)
+    qs = np.abs(gaussian(nq, dim, 41))
+    qs /= np.linalg.norm(qs, axis=1, keepdims=True)
+    data = -np.abs(gaussian(n, dim, 42))
+    odd = np.arange(1, n, 2)
+    near = np.abs(qs[odd % nq] + rng.standard_normal((odd.size, dim)).astype(np.float32) * 0.01)
+    data[odd] = near / np.linalg.norm(near, axis=1, keepdims=True)
+    idx = QuantIndex(ctx, dim, bits=1, scorer=scorer)
+    idx.append(data.astype(np.float32), n)
+    singles_equal(idx, qs.astype(np.float32), 100, 10)
+    idx.destroy()
+
+
 def f32_singles_equal(idx, qs, k):
     """queryBatch rows and score bits equal query() of each vector."""
     nq = qs.shape[0]
