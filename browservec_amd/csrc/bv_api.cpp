@@ -1932,6 +1932,7 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     qa.scales = idx->scales.as<float>();
     qa.scale_mul = 1.0f;
     qa.qrot = idx->qrot.as<float>();
+    qa.nrows = idx->rows;
     // the select writes the list's kprime best lower-bound keys, in order, to
     // merged (free until the final select), and their exact keys raise tau
     auto tighten = [&]() {
@@ -1939,7 +1940,8 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
             return launch_q1p_tau_exact(qa, idx->merged.as<uint64_t>(), idx->merged_n.as<uint32_t>(), kprime,
                                         idx->mq_tau.as<uint64_t>(), nq, s);
         return launch_mq1_tau_exact(src.codes, src.W, src.scales, qlev, qstride, units16, idx->merged.as<uint64_t>(),
-                                    idx->merged_n.as<uint32_t>(), kprime, idx->mq_tau.as<uint64_t>(), nq, s);
+                                    idx->merged_n.as<uint32_t>(), kprime, idx->rows, idx->mq_tau.as<uint64_t>(), nq,
+                                    s);
     };
     auto select_bound = [&](uint64_t ccap, uint64_t *tau_out) {
         sa.cap = ccap;

@@ -130,6 +130,7 @@ struct Q1pRowsArgs {
     const uint32_t *kept;     // [nq] listed rows (at most cap used)
     uint64_t cap;
     uint64_t *keys;           // [nq][cap] exact scan keys
+    uint64_t nrows;           // rows of the index (listed rows are below it)
 };
 // Launches q1p_exact_rows in the fused scan's layout for a.units, with gx
 // workgroups per query.
@@ -423,11 +424,11 @@ hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scal
                             uint64_t cap, uint64_t *keys, uint32_t nq, hipStream_t s);
 // Per query: tau[q] = max(tau[q], the smallest exact key of the rows of
 // merged[q][0, kk), a list's kk best lower-bound keys (mq_select's sorted
-// output); nothing when merged_n[q] < kk.
+// output); nothing when merged_n[q] < kk or a row is not below nrows.
 hipError_t launch_mq1_tau_exact(const uint32_t *codes, uint32_t W, const float *scales,
                                 const unsigned char *qlev, uint64_t qstride, uint32_t units16,
-                                const uint64_t *merged, const uint32_t *merged_n, uint32_t kk, uint64_t *tau,
-                                uint32_t nq, hipStream_t s);
+                                const uint64_t *merged, const uint32_t *merged_n, uint32_t kk, uint64_t nrows,
+                                uint64_t *tau, uint32_t nq, hipStream_t s);
 hipError_t launch_row_code_norms(const uint32_t *codes, uint64_t n, uint32_t W, float *cn, hipStream_t s);
 hipError_t launch_mq1_qconst(const unsigned char *qlev, uint64_t qstride, uint32_t units, uint32_t tail_off,
                              uint32_t nq, float *rq, uint32_t *cnt, uint32_t cnt_value, hipStream_t s);

@@ -964,6 +964,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan_f32(MqArgs a) {
 constexpr int SEL_THREADS = 1024;
 constexpr int SEL_BINS = 2048;
 constexpr int SEL_CAP = 4096;
+constexpr int SEL_KPT = 16;  // keys per thread held in registers (lists up to 16,384 keys)
 
 __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
     __shared__ uint32_t hist[SEL_BINS];
@@ -973,21 +974,52 @@ __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
     const uint32_t q = blockIdx.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const uint32_t total = a.cnt[q];
+    if (total == 0xffffffffu) {
+        // a list marked incomplete (mq1_compact): its entries were never
+        // written, so nothing is selected from it and its bound is left as
+        // it was; the query runs alone afterwards
+        if (tid == 0) {
+            if (a.merged_n) a.merged_n[q] = 0;
+            if (a.overflow) a.overflow[q] = 1u;
+            if (a.out_n) a.out_n[q] = 0;
+        }
+        return;
+    }
     const uint32_t n = (uint64_t)total < a.cap ? total : (uint32_t)a.cap;
     const uint64_t *keys = a.cand + (uint64_t)q * a.cap;
     const uint32_t kk = a.kk < n ? a.kk : n;
     const bool sorted = a.merged != nullptr || a.out_rows != nullptr;
+    // lists of at most SEL_KPT keys per thread are read once into registers
+    // and every pass below runs over those; longer lists re-read memory
+    const bool cached = n <= (uint32_t)(SEL_THREADS * SEL_KPT);
+    uint64_t kr[SEL_KPT];
+    if (cached) {
+#pragma unroll
+        for (int j = 0; j < SEL_KPT; ++j) {
+            const uint32_t i = tid + (uint32_t)j * SEL_THREADS;
+            kr[j] = i < n ? keys[i] : 0ull;
+        }
+    }
+    // f(key) for every key of the list
+    auto each = [&](auto f) {
+        if (cached) {
+#pragma unroll
+            for (int j = 0; j < SEL_KPT; ++j)
+                if (tid + (uint32_t)j * SEL_THREADS < n) f(kr[j]);
+        } else {
+            for (uint32_t i = tid; i < n; i += SEL_THREADS) f(keys[i]);
+        }
+    };
     uint32_t lim = 256;
     while (lim < 2 * kk && lim < (uint32_t)SEL_CAP) lim <<= 1;
     uint64_t G = 0;  // keys >= G are gathered
     uint64_t Gend = ~0ull;  // the last key of the kk-th's bin
     if (n > kk) {
         uint64_t lo = ~0ull, hi = 0;
-        for (uint32_t i = tid; i < n; i += SEL_THREADS) {
-            const uint64_t k = keys[i];
+        each([&](uint64_t k) {
             lo = k < lo ? k : lo;
             hi = k > hi ? k : hi;
-        }
+        });
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const uint64_t l2 = __shfl_xor(lo, o), h2 = __shfl_xor(hi, o);
@@ -1011,10 +1043,9 @@ __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
             const int shift = (span >> 11) ? 64 - __clzll((long long)(span >> 11)) : 0;  // (span >> shift) < 2048
             for (uint32_t i = tid; i < SEL_BINS; i += SEL_THREADS) hist[i] = 0;
             __syncthreads();
-            for (uint32_t i = tid; i < n; i += SEL_THREADS) {
-                const uint64_t k = keys[i];
+            each([&](uint64_t k) {
                 if (k >= lo && k <= hi) atomicAdd(&hist[(uint32_t)((k - lo) >> shift)], 1u);
-            }
+            });
             __syncthreads();
             if (wave == 0) {
                 // lane l holds bins 2047 - 32l - j (j < 32): counts from the top
@@ -1061,10 +1092,9 @@ __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
         if (tid == 0) s_cnt = 0;
         __syncthreads();
         if (n > kk)
-            for (uint32_t i = tid; i < n; i += SEL_THREADS) {
-                const uint64_t k = keys[i];
+            each([&](uint64_t k) {
                 if (k >= G && k <= Gend) red[0][0] = k;  // (exactly one such key)
-            }
+            });
         __syncthreads();
         if (tid == 0) {
             if (a.tau) {
@@ -1078,13 +1108,12 @@ __global__ __launch_bounds__(SEL_THREADS) void mq_select(MqSelArgs a) {
     }
     if (tid == 0) s_cnt = 0;
     __syncthreads();
-    for (uint32_t i = tid; i < n; i += SEL_THREADS) {
-        const uint64_t k = keys[i];
+    each([&](uint64_t k) {
         if (k >= G && k != 0) {
             const uint32_t p = atomicAdd(&s_cnt, 1u);
             if (p < (uint32_t)SEL_CAP) sel[p] = k;
         }
-    }
+    });
     __syncthreads();
     const uint32_t got = s_cnt < (uint32_t)SEL_CAP ? s_cnt : (uint32_t)SEL_CAP;
     uint32_t npow = 2;
@@ -1436,17 +1465,21 @@ template <int UNITS>
 __global__ __launch_bounds__(1024) void mq1_tau_exact(const uint32_t *codes, const float *scales,
                                                        const unsigned char *qlev, uint64_t qstride,
                                                        const uint64_t *merged, const uint32_t *merged_n, uint32_t kk,
-                                                       uint64_t *tau) {
+                                                       uint64_t nrows, uint64_t *tau) {
     __shared__ v4i ql[UNITS * 3];
     __shared__ uint64_t wmin[16];
     const uint32_t q = blockIdx.x, tid = threadIdx.x;
     if (kk == 0 || merged_n[q] < kk) return;
+    const uint64_t *mk = merged + (uint64_t)q * kk;
+    // (every row must be one of the index's: a list that is not is left alone)
+    int bad = 0;
+    for (uint32_t i = tid; i < kk; i += 1024) bad |= key_row(mk[i]) >= nrows;
+    if (__syncthreads_or(bad)) return;
     const unsigned char *src = qlev + (uint64_t)q * qstride;
     for (uint32_t i = tid; i < UNITS * 3; i += 1024) ql[i] = ((const v4i *)src)[i];
     const QLevelTail *t = (const QLevelTail *)(src + (uint64_t)UNITS * 48);
     const double s0 = t->s[0], s1 = t->s[1], s2 = t->s[2];
     __syncthreads();
-    const uint64_t *mk = merged + (uint64_t)q * kk;
     uint64_t m = ~0ull;
     mq1_exact_rows<UNITS>(codes, scales, ql, s0, s1, s2, kk, [&](uint32_t i) { return key_row(mk[i]); },
                           [&](uint32_t, uint64_t key) { m = key < m ? key : m; });
@@ -1697,13 +1730,13 @@ hipError_t launch_mq1_exact(const uint32_t *codes, uint32_t W, const float *scal
 
 hipError_t launch_mq1_tau_exact(const uint32_t *codes, uint32_t W, const float *scales,
                                 const unsigned char *qlev, uint64_t qstride, uint32_t units16,
-                                const uint64_t *merged, const uint32_t *merged_n, uint32_t kk, uint64_t *tau,
-                                uint32_t nq, hipStream_t s) {
+                                const uint64_t *merged, const uint32_t *merged_n, uint32_t kk, uint64_t nrows,
+                                uint64_t *tau, uint32_t nq, hipStream_t s) {
     if (nq == 0) return hipSuccess;
     if (W != units16 * 4) return hipErrorInvalidValue;
 #define BV_TE_CASE(U)                                                                                          \
     case U: hipLaunchKernelGGL(mq1_tau_exact<U>, dim3(nq), dim3(1024), 0, s, codes, scales, qlev, qstride, \
-                               merged, merged_n, kk, tau); break;
+                               merged, merged_n, kk, nrows, tau); break;
     switch (units16) {
         BV_TE_CASE(2)
         BV_TE_CASE(4)

@@ -2768,8 +2768,14 @@ __global__ __launch_bounds__(SCAN_WG) void q1p_tau_exact(Q1pRowsArgs a, const ui
     if (kk == 0 || merged_n[q] < kk) return;
     q1p_lut_build(a.qrot + (uint64_t)q * a.P, a.P, lut, (uint32_t)tid, SCAN_WG);
     const uint64_t *mk = merged + (uint64_t)q * kk;
-    for (uint32_t i = (uint32_t)tid; i < kk; i += SCAN_WG) srow[i] = key_row(mk[i]);
-    __syncthreads();
+    int bad = 0;
+    for (uint32_t i = (uint32_t)tid; i < kk; i += SCAN_WG) {
+        const uint32_t r = key_row(mk[i]);
+        bad |= r >= a.nrows;
+        srow[i] = r;
+    }
+    // (every row must be one of the index's: a list that is not is left alone)
+    if (__syncthreads_or(bad)) return;
     ScanRegs<C_Q1P, UPL> R{};
     const int pl = lane % LPR;
 #pragma unroll
