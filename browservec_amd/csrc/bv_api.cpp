@@ -1739,11 +1739,13 @@ static int ensure_pm_rows(bv_index *idx) {
 }
 
 static int prepare_pm(bv_index *idx, const float *d_q, uint32_t nq, const unsigned char **qlev, uint64_t *qstride,
-                      Q8Source *src) {
+                      Q8Source *src, bool widen_rows = true) {
     hipStream_t s = idx->stream;
     const uint32_t P = idx->P, W1 = idx->words_per_row;
-    int rc = ensure_pm_rows(idx);
-    if (rc) return rc;
+    if (widen_rows) {
+        const int rc = ensure_pm_rows(idx);
+        if (rc) return rc;
+    }
     const size_t st = level_stride(C_Q8, P);
     HIPX(idx->dev, idx->pm_qbits.ensure((size_t)nq * W1 * 4, 0, s), "query buffer");
     HIPX(idx->dev, idx->qscale.ensure((size_t)nq * 4, 0, s), "query buffer");
@@ -1763,7 +1765,7 @@ static int prepare_pm(bv_index *idx, const float *d_q, uint32_t nq, const unsign
          "query levels kernel");
     *qlev = idx->qscan.as<unsigned char>();
     *qstride = st;
-    *src = Q8Source{idx->pm_codes.as<uint32_t>(), P / 4, idx->pm_ones.as<float>(), idx->pm_cn.as<float>()};
+    if (widen_rows) *src = Q8Source{idx->pm_codes.as<uint32_t>(), P / 4, idx->pm_ones.as<float>(), idx->pm_cn.as<float>()};
     return BV_OK;
 }
 
@@ -1829,8 +1831,24 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     // single-query keys from q1p_exact_rows (bit-plane codes), or from the
     // fused scan in indexed mode (C_Q1A)
     const bool asym1 = idx->codec == C_Q1P || idx->codec == C_Q1A;
+    // Hamming and bit-plane 1-bit codes of 128 to 1024 codes per row: the
+    // pass reads the bits and widens them to +1 / -1 bytes in LDS
+    // (mq1_scan_bits), so the index keeps no widened copy; every such row has
+    // the code norm sqrt(P) (Hamming, rounded up as row_code_norms rounds) or
+    // the row term 1 (asymmetric)
+    const bool bits1 = (idx->codec == C_HAM || idx->codec == C_Q1P) && idx->P >= 128 && idx->P <= 1024;
+    float cn_const = 1.0f;
     int rc = BV_OK;
-    if (idx->codec == C_HAM) {
+    if (bits1 && idx->codec == C_HAM) {
+        rc = prepare_pm(idx, d_q, nq, &qlev, &qstride, &src, false);
+        src = Q8Source{idx->codes.as<uint32_t>(), idx->words_per_row, nullptr, nullptr};
+        const double v = std::sqrt((double)idx->P);
+        cn_const = (float)v;
+        if ((double)cn_const < v) cn_const = std::nextafter(cn_const, INFINITY);
+    } else if (bits1) {
+        rc = prepare_levels16(idx, d_q, nq, &qlev, &qstride, C_Q4M);
+        src = Q8Source{idx->codes.as<uint32_t>(), idx->words_per_row, idx->scales.as<float>(), nullptr};
+    } else if (idx->codec == C_HAM) {
         rc = prepare_pm(idx, d_q, nq, &qlev, &qstride, &src);
     } else if (asym1) {
         rc = ensure_pm_rows(idx);
@@ -1894,6 +1912,8 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     m.scales = src.scales;
     m.cn = src.cn;
     m.W = src.W;
+    m.cn_const = cn_const;
+    auto scan = [&]() { return bits1 ? launch_mq1_scan_bits(m, s) : launch_mq1_scan(m, s); };
     m.units = units16;
     m.qlev = qlev;
     m.qstride = qstride;
@@ -1908,7 +1928,7 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
     m.row_step = N / S;
     m.cand = idx->mq_cand.as<uint64_t>();
     m.cap = S;
-    HIPX(idx->dev, launch_mq1_scan(m, s), "batched scan kernel");
+    HIPX(idx->dev, scan(), "batched scan kernel");
     MqSelArgs sa{};
     sa.cand = m.cand;
     sa.cnt = idx->mq_cnt.as<uint32_t>();
@@ -1977,10 +1997,10 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
         m.n = rn;
         m.row_base = r0;
         m.codes = src.codes + r0 * src.W;
-        m.scales = src.scales + r0;
-        m.cn = src.cn + r0;
+        m.scales = src.scales ? src.scales + r0 : nullptr;
+        m.cn = src.cn ? src.cn + r0 : nullptr;
         m.cand = idx->mq_bk.as<uint64_t>();
-        HIPX(idx->dev, launch_mq1_scan(m, s), "batched scan kernel");
+        HIPX(idx->dev, scan(), "batched scan kernel");
         HIPX(idx->dev,
              launch_mq1_compact(idx->mq_bk.as<uint64_t>(), idx->mq_bu.as<uint32_t>(), idx->mq_bc.as<uint32_t>(),
                                 nwg, capw, cap, idx->mq_cand.as<uint64_t>(), idx->mq_up.as<uint32_t>(),
@@ -2026,6 +2046,11 @@ static int run_batched_q8(bv_index *idx, const float *d_q, uint32_t nq, uint32_t
         qa.cap = cap;
         qa.keys = m.cand;
         HIPX(idx->dev, launch_q1p_exact_rows(qa, nq, 8, s), "batched exact kernel");
+    } else if (bits1) {  // Hamming over the bits
+        HIPX(idx->dev,
+             launch_ham_exact(src.codes, src.W, idx->pm_qbits.as<uint32_t>(), qlev, qstride, units16 * 48,
+                              idx->mq_rows.as<uint32_t>(), idx->mq_kept.as<uint32_t>(), cap, m.cand, nq, s),
+             "batched exact kernel");
     } else {
         HIPX(idx->dev,
              launch_mq1_exact(m.codes, m.W, m.scales, qlev, qstride, units16, idx->mq_rows.as<uint32_t>(),

@@ -405,7 +405,18 @@ struct Mq1Args {
     uint32_t *cnt;            // threshold: [nq][nwg] bucket lengths (0xffffffff: overflowed)
     uint64_t cap;
     uint32_t capw;            // threshold: entries per bucket
+    float cn_const;           // mq1_scan_bits: every row's code norm (cn unused)
 };
+// mq1_scan over 1-bit codes (codes: W = units / 2 words of 32 bits per
+// row) widened to +1 / -1 bytes in LDS; scales may be null (1); every row's
+// code norm is cn_const.  16-code units per row: 8 to 64.
+hipError_t launch_mq1_scan_bits(const Mq1Args &a, hipStream_t s);
+// Hamming exact keys of rows[q][0, min(kept[q], cap)) over 1-bit codes (W
+// words per row, 4 to 32) and the queries' bits (W words each), into
+// keys[q][...]: the keys mq1_exact gives over the widened codes.
+hipError_t launch_ham_exact(const uint32_t *codes, uint32_t W, const uint32_t *qbits, const unsigned char *qlev,
+                            uint64_t qstride, uint32_t tail_off, const uint32_t *rows, const uint32_t *kept,
+                            uint64_t cap, uint64_t *keys, uint32_t nq, hipStream_t s);
 // Per query: its buckets joined into lk / uo [nq][cap] (after the list's
 // cnt[q] entries when append is set) and the length in cnt[q] (0xffffffff
 // when a bucket overflowed or the total exceeds cap).

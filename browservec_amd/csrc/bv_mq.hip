@@ -669,6 +669,178 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan(Mq1Args a) {
     }
 }
 
+// The first-level pass over 1-bit codes: mq1_scan over the +1 / -1 bytes of
+// each row (bit set: +1, clear: -1), with the rows read as bits (P/8 bytes)
+// and widened in LDS, so neither HBM nor the index holds the bytes.  The
+// loader waves bring each tile's bits into a four-deep ring (one
+// global_load_lds per wave and tile) three tiles ahead; at tile k every
+// wave widens tile k + 1 into the other of two byte tiles (a 256-entry
+// table of 8 codes per bit byte) while the matrix cores read tile k.  The
+// rows' scales come with the bits (none: 1), and their code norms are the
+// constant a.cn_const (every +1 / -1 row has the same norm).  The keys,
+// bounds, staging and buckets are mq1_scan's.
+template <int S>
+__global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan_bits(Mq1Args a) {
+    constexpr uint32_t U = 2 * S;     // 16-byte units per widened row (8 <= U <= 64)
+    constexpr uint32_t RS = U + 1;    // LDS row stride of the byte tiles in units
+    constexpr uint32_t UB = U / 8;    // 16-byte units per row of bits
+    constexpr uint32_t PER_WAVE = MQ1_ROWS / MQ1_LOADERS;
+    constexpr uint32_t LN = PER_WAVE * UB;  // lanes of a loader wave's one load per tile
+    static_assert(S >= 4 && LN <= 64, "1-bit rows of 128 to 1024 codes");
+    __shared__ v4i tb[2][MQ1_ROWS * RS];
+    __shared__ v4i bb[4][MQ1_ROWS * UB];
+    __shared__ __align__(16) float scr[4][MQ1_ROWS];
+    __shared__ __align__(16) float ones[MQ1_ROWS];
+    __shared__ __align__(16) float cnc[MQ1_ROWS];
+    __shared__ uint2 lut[256];
+    __shared__ Mq1Stage stage;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = lane >> 5, c = lane & 31;
+    const uint64_t ntiles = (a.n + MQ1_ROWS - 1) / MQ1_ROWS;
+    const uint32_t qb = blockIdx.x % a.qblocks;
+    const uint32_t wg = blockIdx.x / a.qblocks;
+    const bool loader = wave < MQ1_LOADERS;
+    const bool thr = a.tau != nullptr;
+    const bool scaled = a.scales != nullptr;
+    for (uint32_t i = threadIdx.x; i < 2 * MQ_WAVES * 64; i += MQ_WAVES * 64)
+        stage.ln[i / (MQ_WAVES * 64)][(i / 64) % MQ_WAVES][i % 64] = 0;
+    if (threadIdx.x < MQ1_QB) stage.qovf[threadIdx.x] = 0;
+    if (threadIdx.x < 256) {  // codes 8j .. 8j + 7 of a bit byte, as two words of +1 / -1 bytes
+        const uint32_t b = threadIdx.x;
+        uint2 e;
+        e.x = 0;
+        e.y = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            e.x |= (((b >> j) & 1u) ? 0x01u : 0xffu) << (8 * j);
+            e.y |= (((b >> (4 + j)) & 1u) ? 0x01u : 0xffu) << (8 * j);
+        }
+        lut[b] = e;
+    }
+    if (threadIdx.x < MQ1_ROWS) {
+        ones[threadIdx.x] = 1.0f;
+        cnc[threadIdx.x] = a.cn_const;
+    }
+    uint32_t blen = 0;
+    bool bovf = false;
+    const uint64_t mine = wg < ntiles ? (ntiles - wg + a.nwg - 1) / a.nwg : 0;
+
+    const uint32_t qlocal = (uint32_t)wave * 32 + c;
+    const uint32_t q = qb * MQ1_QB + qlocal;
+    const bool wave_live = qb * MQ1_QB + (uint32_t)wave * 32 < a.nq;
+    const uint32_t qc = q < a.nq ? q : a.nq - 1;
+    const unsigned char *qsrc = a.qlev + (uint64_t)qc * a.qstride;
+    v4i qreg[S];
+#pragma unroll
+    for (int st = 0; st < S; ++st) qreg[st] = *(const v4i *)(qsrc + (uint64_t)(2 * st + h) * 48);
+    const QLevelTail *qt = (const QLevelTail *)(qsrc + a.tail_off);
+    const float s0f = (float)qt->s[0];
+    const float rq = a.rq[qc];
+    const uint64_t tau = thr ? a.tau[qc] : 0ull;
+    const float tau_score = tau ? f32_from_ord((uint32_t)(tau >> 32)) : -__builtin_inff();
+
+    // tile k's bits into ring slot k & 3 by the loader waves (lane i of wave
+    // w: row w * PER_WAVE + i / UB, unit i % UB, so the tile's rows sit
+    // back to back), and its scales by wave 0
+    auto load_bits = [&](uint64_t k) {
+        const uint64_t t = wg + k * a.nwg;
+        const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+        const uint32_t lb = lds_addr(&bb[k & 3][wv * LN]);
+        if ((uint32_t)lane < LN) {
+            uint64_t li = t * MQ1_ROWS + wv * PER_WAVE + (uint32_t)lane / UB;
+            if (li >= a.n) li = a.n - 1;  // rows past the end load a valid row; their results are dropped
+            lds_dma16((const v4i *)(a.codes + li * a.row_step * a.W) + (uint32_t)lane % UB, lb);
+        }
+        if (scaled && wv == 0 && lane < MQ1_ROWS) {
+            uint64_t li = t * MQ1_ROWS + (uint32_t)lane;
+            if (li >= a.n) li = a.n - 1;
+            lds_dma4(a.scales + li * a.row_step, lds_addr(&scr[k & 3][0]));
+        }
+    };
+    // tile k's bits into byte tile k & 1: unit u of row r (codes 16u ..
+    // 16u + 15) from the row's 16-bit half-word u
+    auto widen = [&](uint64_t k) {
+        const uint16_t *src = (const uint16_t *)&bb[k & 3][0];
+        v4i *dst = &tb[k & 1][0];
+        for (uint32_t i = threadIdx.x; i < MQ1_ROWS * U; i += MQ_WAVES * 64) {
+            const uint32_t r = i / U, u = i % U;
+            const uint32_t b16 = src[r * (UB * 8) + u];
+            const uint2 lo = lut[b16 & 255u], hi = lut[b16 >> 8];
+            dst[r * RS + u] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+        }
+    };
+    // this loader wave's loads of tile j have landed, with those of the
+    // tiles after it (at most `after` of them) still running; the dense pass
+    // writes keys, so it waits for all
+    auto wait_tile = [&](uint64_t after) {
+        if (loader && thr) {
+            if (wave == 0 && scaled) {  // two loads per tile
+                if (after >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(4));
+                else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));
+                else __builtin_amdgcn_s_waitcnt(0);
+            } else {
+                if (after >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));
+                else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(1));
+                else __builtin_amdgcn_s_waitcnt(0);
+            }
+        } else if (loader || !thr) {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+    };
+
+    if (loader) {
+        if (mine > 0) load_bits(0);
+        if (mine > 1) load_bits(1);
+        if (mine > 2) load_bits(2);
+    }
+    if (mine > 0) {
+        wait_tile(mine - 1 < 2 ? mine - 1 : 2);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        widen(0);
+    }
+    for (uint64_t k = 0; k < mine; ++k) {
+        // tile k + 1's bits have landed (every loader wave waited for its
+        // own), tile k is widened, and every wave is done with tile k - 1
+        if (k + 1 < mine) wait_tile(mine - 2 - k < 1 ? mine - 2 - k : 1);
+        else wait_tile(0);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (loader) {
+            if (k + 3 < mine) load_bits(k + 3);
+        } else if (thr) {
+            mq1_flush(a, qb, wg, stage, (int)((k + 1) & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+        }
+        if (k + 1 < mine) widen(k + 1);
+        if (wave_live) {
+            const v4i *tl = &tb[k & 1][0];
+            const float *sc = scaled ? &scr[k & 3][0] : ones;
+            v16i acc2[2] = {v16i{}, v16i{}};
+            const v4i *A0 = tl + c * RS + h;
+            constexpr int PF = S < 4 ? S : 4;
+            v4i ar[PF];
+#pragma unroll
+            for (int st = 0; st < PF; ++st) ar[st] = A0[2 * st];
+#pragma unroll
+            for (int st = 0; st < S; ++st) {
+                const v4i x = ar[st % PF];
+                if (st + PF < S) ar[st % PF] = A0[2 * (st + PF)];
+                acc2[st & 1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x, qreg[st], acc2[st & 1], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const v16i acc = acc2[0] + acc2[1];
+            mq1_epilogue(a, acc, (wg + k * a.nwg) * MQ1_ROWS, q, qlocal, h, s0f, rq, tau_score, sc, cnc, stage,
+                         (int)(k & 1));
+        }
+    }
+    if (thr) {
+        __syncthreads();
+        if (!loader) {
+            if (mine) mq1_flush(a, qb, wg, stage, (int)((mine - 1) & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+            const uint32_t ql = (uint32_t)(wave - MQ1_LOADERS) * 64 + lane, qq = qb * MQ1_QB + ql;
+            if (qq < a.nq) a.cnt[(uint64_t)qq * a.nwg + wg] = bovf || stage.qovf[ql] ? 0xffffffffu : blen;
+        }
+    }
+}
+
 // One workgroup per query: the workgroups' buckets of the query joined into
 // one list (bucket order; appended after the list's cnt[q] entries when
 // append is set), and its length; a query with an overflowed bucket or more
@@ -1496,6 +1668,38 @@ __global__ __launch_bounds__(1024) void mq1_tau_exact(const uint32_t *codes, con
     }
 }
 
+// Hamming batches on 1-bit codes: the exact key of every kept row (one
+// workgroup per query, a row per thread), d = P - 2 * popcount(code ^
+// query bits), the +1 / -1 dot that mq1_exact gives over the widened codes,
+// combined by q_key with the query's level steps and row scale 1.
+template <int W>
+__global__ __launch_bounds__(1024) void ham_exact(const uint32_t *codes, const uint32_t *qbits,
+                                                  const unsigned char *qlev, uint64_t qstride, uint32_t tail_off,
+                                                  const uint32_t *rows, const uint32_t *kept, uint64_t cap,
+                                                  uint64_t *keys) {
+    __shared__ uint32_t qw[W];
+    const uint32_t q = blockIdx.x, tid = threadIdx.x;
+    if (tid < (uint32_t)W) qw[tid] = qbits[(uint64_t)q * W + tid];
+    const QLevelTail *t = (const QLevelTail *)(qlev + (uint64_t)q * qstride + tail_off);
+    const double s0 = t->s[0], s1 = t->s[1], s2 = t->s[2];
+    __syncthreads();
+    const uint32_t n = kept[q] < cap ? kept[q] : (uint32_t)cap;
+    const uint32_t *rq = rows + (uint64_t)q * cap;
+    uint64_t *out = keys + (uint64_t)q * cap;
+    for (uint32_t i = tid; i < n; i += 1024) {
+        const uint32_t row = rq[i];
+        const uint4 *x = (const uint4 *)(codes + (uint64_t)row * W);
+        int pc = 0;
+#pragma unroll
+        for (int j = 0; j < W / 4; ++j) {
+            const uint4 v = x[j];
+            pc += __popc(v.x ^ qw[4 * j]) + __popc(v.y ^ qw[4 * j + 1]) + __popc(v.z ^ qw[4 * j + 2]) +
+                  __popc(v.w ^ qw[4 * j + 3]);
+        }
+        out[i] = q_key(s0, s1, s2, 32 * W - 2 * pc, 0, 0, 1.0f, row);
+    }
+}
+
 }  // namespace
 
 namespace {
@@ -1747,6 +1951,44 @@ hipError_t launch_mq1_tau_exact(const uint32_t *codes, uint32_t W, const float *
     default: return hipErrorInvalidValue;
     }
 #undef BV_TE_CASE
+    return hipGetLastError();
+}
+
+hipError_t launch_mq1_scan_bits(const Mq1Args &a, hipStream_t s) {
+    if (a.n == 0 || a.nq == 0) return hipSuccess;
+    const uint32_t steps = a.units >> 1;
+    if ((a.units & 1u) || steps < 4 || steps > 32 || (steps & (steps - 1)) || a.qblocks == 0 || a.groups == 0 ||
+        (uint64_t)a.qblocks * MQ1_QB < a.nq || a.W * 2u != a.units || !a.cand ||
+        (a.tau && (!a.up_out || !a.cnt || a.capw == 0)) || a.nwg != a.groups || !(a.cn_const >= 0.0f))
+        return hipErrorInvalidValue;
+    const uint64_t blocks = (uint64_t)a.groups * a.qblocks;
+    if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
+    const dim3 g((uint32_t)blocks), wg(MQ_WAVES * 64);
+    switch (steps) {
+    case 4: hipLaunchKernelGGL((mq1_scan_bits<4>), g, wg, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((mq1_scan_bits<8>), g, wg, 0, s, a); break;
+    case 16: hipLaunchKernelGGL((mq1_scan_bits<16>), g, wg, 0, s, a); break;
+    case 32: hipLaunchKernelGGL((mq1_scan_bits<32>), g, wg, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_ham_exact(const uint32_t *codes, uint32_t W, const uint32_t *qbits, const unsigned char *qlev,
+                            uint64_t qstride, uint32_t tail_off, const uint32_t *rows, const uint32_t *kept,
+                            uint64_t cap, uint64_t *keys, uint32_t nq, hipStream_t s) {
+    if (nq == 0) return hipSuccess;
+#define BV_HE_CASE(WW)                                                                                         \
+    case WW: hipLaunchKernelGGL(ham_exact<WW>, dim3(nq), dim3(1024), 0, s, codes, qbits, qlev, qstride, tail_off, \
+                                rows, kept, cap, keys); break;
+    switch (W) {
+        BV_HE_CASE(4)
+        BV_HE_CASE(8)
+        BV_HE_CASE(16)
+        BV_HE_CASE(32)
+    default: return hipErrorInvalidValue;
+    }
+#undef BV_HE_CASE
     return hipGetLastError();
 }
 
