@@ -323,6 +323,51 @@ __device__ __forceinline__ void mq1_epilogue(const Mq1Args &a, const v16i &acc, 
     }
 }
 
+// 1 when a (row, query) upper bound can reach the query's bound (NaN: 1),
+// as in mq1_epilogue.
+__device__ __forceinline__ uint32_t mq1_reach(int32_t d, float s0f, float nr_rq, float scale, float tau_score) {
+    return !(mq1_upper(d, s0f, nr_rq, scale) < tau_score) ? 1u : 0u;
+}
+
+// The staging half of mq1_epilogue for a tile whose reach bits p are formed
+// (bit r: the lane's row 8(r/4) + 4h + r%4): the same slots and entries,
+// each entry's scale and code norm read again from the tile's LDS.
+__device__ __forceinline__ void mq1_stage(const Mq1Args &a, uint32_t p, const v16i &acc, uint64_t t0, uint32_t q,
+                                          uint32_t qlocal, int h, float s0f, float rq, const float *sc,
+                                          const float *cn, Mq1Stage &st, int sb) {
+    // (the wave index as a scalar: the staging addresses stay in SGPRs)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    auto row_of = [&](uint32_t r) { return 8 * (r >> 2) + 4 * (uint32_t)h + (r & 3); };
+    if (t0 + MQ1_ROWS > a.n) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (t0 + row_of(r) >= a.n) p &= ~(1u << r);
+    }
+    if (q >= a.nq) p = 0;
+    const uint32_t mine = __popc(p);
+    const uint32_t incl = wave_incl_scan(mine);
+    st.lo[sb][wave][lane] = (uint16_t)(incl - mine);
+    st.ln[sb][wave][lane] = (uint16_t)mine;
+    if (!__builtin_amdgcn_readlane((int)incl, 63)) return;
+    uint32_t pos = incl - mine;
+    for (uint32_t m = p; m; m &= m - 1, ++pos) {
+        if (pos >= (uint32_t)MQ1_STAGE) {
+            st.qovf[qlocal] = 1;  // the query's list can no longer be complete: it falls back
+            break;
+        }
+        const uint32_t bit = __builtin_ctz(m);
+        int32_t d = 0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if ((uint32_t)k == bit) d = acc[k];
+        const uint32_t rr = row_of(bit);
+        const float s_ = sc[rr], b_ = cn[rr] * rq;
+        const float lo = mq1_lower(d, s0f, b_, s_), up = mq1_upper(d, s0f, b_, s_);
+        st.lk[sb][wave][pos] = make_key(lo == lo ? ord_f32(lo) : 0u, (uint32_t)(a.row_base + (t0 + rr) * a.row_step));
+        st.uo[sb][wave][pos] = up == up ? ord_f32(up) : 0xffffffffu;
+    }
+}
+
 // Staged entries of buffer fb into this workgroup's bucket of each query.
 // Lane l of flushing wave f owns query f*64 + l of the block: its entries
 // were staged by wave (f*64 + l) / 32, lanes c and c + 32 (c = l % 32), and
@@ -519,7 +564,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq_scan(MqArgs a) {
 // writes lower-bound keys (whose kk-th best per query is a valid bound: kk
 // rows have exact keys at or above it), and the pass over every row keeps
 // the rows whose upper bound reaches it.
-template <int S>
+template <int S, bool THR>
 __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan(Mq1Args a) {
     constexpr uint32_t U = 2 * S;     // 16-byte units per row (<= 64)
     constexpr uint32_t RS = U + 1;    // LDS row stride in units: one unit of padding
@@ -537,7 +582,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan(Mq1Args a) {
     const uint32_t qb = blockIdx.x % a.qblocks;
     const uint32_t wg = blockIdx.x / a.qblocks;  // a.nwg workgroups per query block
     const bool loader = wave < MQ1_LOADERS;
-    const bool thr = a.tau != nullptr;
+    constexpr bool thr = THR;  // (the launch picks THR from a.tau)
     for (uint32_t i = threadIdx.x; i < 2 * MQ_WAVES * 64; i += MQ_WAVES * 64)
         stage.ln[i / (MQ_WAVES * 64)][(i / 64) % MQ_WAVES][i % 64] = 0;
     if (threadIdx.x < MQ1_QB) stage.qovf[threadIdx.x] = 0;
@@ -645,27 +690,178 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan(Mq1Args a) {
         }
     };
 
+    if constexpr (!THR) {
+        if (loader) {
+            if (mine > 0) load_tile(0, tb0, sc0, cs0);
+            if (mine > 1) load_tile(1, tb1, sc1, cs1);
+            if (mine > 2) load_tile(2, tb2, sc2, cs2);
+        }
+        for (uint64_t k = 0; k < mine; k += 4) {
+            run_tile(k, tb0, sc0, cs0, tb3, sc3, cs3);
+            if (k + 1 >= mine) break;
+            run_tile(k + 1, tb1, sc1, cs1, tb0, sc0, cs0);
+            if (k + 2 >= mine) break;
+            run_tile(k + 2, tb2, sc2, cs2, tb1, sc1, cs1);
+            if (k + 3 >= mine) break;
+            run_tile(k + 3, tb3, sc3, cs3, tb2, sc2, cs2);
+        }
+        return;
+    }
+
+    // ---- the threshold pass: each tile's bounds are formed while the matrix
+    // cores multiply the next tile ----
+    // Tile k's level-one dots stay in registers (pacc) until tile k + 1's
+    // K loop, which tests them against the bound between its MFMAs (the VALU
+    // issues while the matrix cores run), then stages the rows that can
+    // reach it.  Tile k's scales and code norms are therefore read during
+    // tile k + 1: they come one tile behind its codes (the scales of tile
+    // j + 2 and the codes of tile j + 3 are issued at tile j), so their
+    // buffer is overwritten only after the barrier that follows that read.
+    // Staged entries of tile k are moved to the buckets at tile k + 2.
+    auto load_codes = [&](uint64_t k, v4i *tl) {
+        const uint64_t t = wg + k * a.nwg;
+        const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+        const uint32_t lb = lds_addr(&tl[wv * PER_WAVE * RS]);
+        if ((uint32_t)lane < U) {
+#pragma unroll
+            for (uint32_t j = 0; j < PER_WAVE; ++j) {
+                uint64_t li = t * MQ1_ROWS + wv * PER_WAVE + j;
+                if (li >= a.n) li = a.n - 1;  // rows past the end load a valid row; their results are dropped
+                lds_dma16((const v4i *)(a.codes + li * a.row_step * a.W) + lane, lb + j * RS * 16);
+            }
+        }
+    };
+    auto load_scales = [&](uint64_t k, float *sc, float *cs) {
+        if (wave == 0 && lane < MQ1_ROWS) {
+            uint64_t li = (wg + k * a.nwg) * MQ1_ROWS + (uint32_t)lane;
+            if (li >= a.n) li = a.n - 1;
+            lds_dma4(a.scales + li * a.row_step, lds_addr(sc));
+            lds_dma4(a.cn + li * a.row_step, lds_addr(cs));
+        }
+    };
+    v16i pacc = v16i{};  // the previous tile's level-one dots
+    // tile k's matrix work from tl, with tile k - 1's bounds from its dots
+    // and (psc, pcs); issues tile k + 3's codes into ntl and tile k + 2's
+    // scales into (nsc, ncs)
+    auto run_tile2 = [&](uint64_t k, const v4i *tl, const float *psc, const float *pcs, v4i *ntl, float *nsc,
+                         float *ncs) {
+        // tile k's codes and tile k - 1's scales have landed: both were
+        // issued at tile k - 3 (or before the loop, in the same order);
+        // the loads of tiles k - 2 and k - 1 may still run (vmcnt counts in
+        // issue order): codes of k + 1 and k + 2, scales of k and k + 1
+        if (loader) {
+            const uint64_t left = mine - 1 - k;
+            if (wave == 0) {
+                if (left >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER_WAVE + 4));
+                else if (left == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE + 4));
+                else __builtin_amdgcn_s_waitcnt(vmcnt_imm(2));
+            } else {
+                if (left >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER_WAVE));
+                else if (left == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER_WAVE));
+                else __builtin_amdgcn_s_waitcnt(0);
+            }
+        }
+        // (as in run_tile: this wave's LDS operations, then the barrier)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        // The flushing waves move staged entries first; the loader waves
+        // multiply first (the matrix cores are theirs alone meanwhile) and
+        // issue their loads after the K loop, while the flushing waves
+        // multiply: issued at the barrier, the four loader waves' 32 KB of
+        // loads kept them out of the K loop for ~1,100 cycles.
+        if (!loader) mq1_flush(a, qb, wg, stage, (int)(k & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+        auto issue_loads = [&]() {
+            if (loader) {
+                if (k + 3 < mine) load_codes(k + 3, ntl);
+                if (k + 2 < mine) load_scales(k + 2, nsc, ncs);
+            }
+        };
+        if (!wave_live) issue_loads();
+        if (wave_live) {
+            v16i acc = v16i{};  // one chain: back-to-back MFMAs of one shape forward their sums
+            const v4i *A0 = tl + c * RS + h;
+            constexpr int PF = S < 4 ? S : 4;
+            v4i ar[PF];
+#pragma unroll
+            for (int st = 0; st < PF; ++st) ar[st] = A0[2 * st];
+            // element r of the lane's rows of tile k - 1 is row
+            // 8(r/4) + 4h + r%4; its scale and norm are read one element ahead
+            const float *psh = psc + 4 * h, *pnh = pcs + 4 * h;
+            float sv = psh[0], nv = pnh[0];
+            uint32_t p = 0;
+#pragma unroll
+            for (int st = 0; st < S; ++st) {
+                const v4i x = ar[st % PF];
+                if (st + PF < S) ar[st % PF] = A0[2 * (st + PF)];
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(x, qreg[st], acc, 0, 0, 0);
+                // tile k - 1's elements [16 st / S, 16 (st + 1) / S) (tile 0
+                // tests zero dots against a buffer not yet written: unused)
+#pragma unroll
+                for (int r = 16 * st / S; r < 16 * (st + 1) / S; ++r) {
+                    float svn = 0.0f, nvn = 0.0f;
+                    if (r < 15) {
+                        const int rn = 8 * ((r + 1) >> 2) + ((r + 1) & 3);
+                        svn = psh[rn];
+                        nvn = pnh[rn];
+                    }
+                    p |= mq1_reach(pacc[r], s0f, nv * rq, sv, tau_score) << r;
+                    // (here, between the MFMAs: not sunk to the staging below)
+                    asm volatile("" : "+v"(p));
+                    sv = svn;
+                    nv = nvn;
+                }
+                __builtin_amdgcn_sched_barrier(0);  // keep each step's read PF steps ahead
+            }
+            issue_loads();
+            if (k > 0)
+                mq1_stage(a, p, pacc, (wg + (k - 1) * a.nwg) * MQ1_ROWS, q, qlocal, h, s0f, rq, psc, pcs, stage,
+                          (int)((k - 1) & 1));
+            pacc = acc;
+        }
+    };
+
+    // before the loop, the loads of tiles -3, -2, -1 in the loop's pattern:
+    // codes of 0, 1, 2 and scales of 0, 1
     if (loader) {
-        if (mine > 0) load_tile(0, tb0, sc0, cs0);
-        if (mine > 1) load_tile(1, tb1, sc1, cs1);
-        if (mine > 2) load_tile(2, tb2, sc2, cs2);
+        if (mine > 0) load_codes(0, tb0);
+        if (mine > 1) load_codes(1, tb1);
+        if (mine > 0) load_scales(0, sc0, cs0);
+        if (mine > 2) load_codes(2, tb2);
+        if (mine > 1) load_scales(1, sc1, cs1);
     }
     for (uint64_t k = 0; k < mine; k += 4) {
-        run_tile(k, tb0, sc0, cs0, tb3, sc3, cs3);
+        run_tile2(k, tb0, sc3, cs3, tb3, sc2, cs2);
         if (k + 1 >= mine) break;
-        run_tile(k + 1, tb1, sc1, cs1, tb0, sc0, cs0);
+        run_tile2(k + 1, tb1, sc0, cs0, tb0, sc3, cs3);
         if (k + 2 >= mine) break;
-        run_tile(k + 2, tb2, sc2, cs2, tb1, sc1, cs1);
+        run_tile2(k + 2, tb2, sc1, cs1, tb1, sc0, cs0);
         if (k + 3 >= mine) break;
-        run_tile(k + 3, tb3, sc3, cs3, tb2, sc2, cs2);
+        run_tile2(k + 3, tb3, sc2, cs2, tb2, sc1, cs1);
     }
-    if (thr) {  // the last tile's staged entries, then this workgroup's bucket lengths
-        __syncthreads();
-        if (!loader) {
-            if (mine) mq1_flush(a, qb, wg, stage, (int)((mine - 1) & 1), wave - MQ1_LOADERS, lane, blen, bovf);
-            const uint32_t ql = (uint32_t)(wave - MQ1_LOADERS) * 64 + lane, qq = qb * MQ1_QB + ql;
-            if (qq < a.nq) a.cnt[(uint64_t)qq * a.nwg + wg] = bovf || stage.qovf[ql] ? 0xffffffffu : blen;
+    // the last tile's bounds (its scales have landed after the wait), the
+    // staged entries of the last two tiles, then this workgroup's bucket
+    // lengths
+    if (loader) __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (!loader && mine >= 2)
+        mq1_flush(a, qb, wg, stage, (int)((mine - 2) & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+    if (wave_live && mine > 0) {
+        const uint32_t lbuf = (uint32_t)((mine - 1) & 3);
+        const float *lsc = lbuf == 0 ? sc0 : lbuf == 1 ? sc1 : lbuf == 2 ? sc2 : sc3;
+        const float *lcs = lbuf == 0 ? cs0 : lbuf == 1 ? cs1 : lbuf == 2 ? cs2 : cs3;
+        uint32_t p = 0;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t rr = 8 * (r >> 2) + 4 * (uint32_t)h + (r & 3);
+            p |= mq1_reach(pacc[r], s0f, lcs[rr] * rq, lsc[rr], tau_score) << r;
         }
+        mq1_stage(a, p, pacc, (wg + (mine - 1) * a.nwg) * MQ1_ROWS, q, qlocal, h, s0f, rq, lsc, lcs, stage,
+                  (int)((mine - 1) & 1));
+    }
+    __syncthreads();
+    if (!loader) {
+        if (mine) mq1_flush(a, qb, wg, stage, (int)((mine - 1) & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+        const uint32_t ql = (uint32_t)(wave - MQ1_LOADERS) * 64 + lane, qq = qb * MQ1_QB + ql;
+        if (qq < a.nq) a.cnt[(uint64_t)qq * a.nwg + wg] = bovf || stage.qovf[ql] ? 0xffffffffu : blen;
     }
 }
 
@@ -2158,8 +2354,11 @@ hipError_t launch_mq1_scan(const Mq1Args &a, hipStream_t s) {
     const uint64_t blocks = (uint64_t)a.groups * a.qblocks;
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
     const dim3 g((uint32_t)blocks), wg(MQ_WAVES * 64);
-#define BV_MQ1_CASE(ST)                                             \
-    case ST: hipLaunchKernelGGL((mq1_scan<ST>), g, wg, 0, s, a); break;
+#define BV_MQ1_CASE(ST)                                                      \
+    case ST:                                                                 \
+        if (a.tau) hipLaunchKernelGGL((mq1_scan<ST, true>), g, wg, 0, s, a);  \
+        else hipLaunchKernelGGL((mq1_scan<ST, false>), g, wg, 0, s, a);       \
+        break;
     switch (steps) {
         BV_MQ1_CASE(1)
         BV_MQ1_CASE(2)
