@@ -377,20 +377,19 @@ __device__ __forceinline__ void mq1_flush(const Mq1Args &a, uint32_t qb, uint32_
                                           int f, int lane, uint32_t &len, bool &ovf) {
     const uint32_t ql = (uint32_t)f * 64 + lane, w = ql / 32, c = ql % 32;
     const uint64_t bucket = ((uint64_t)(qb * MQ1_QB + ql) * a.nwg + wg) * a.capw;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        const uint32_t off = st.lo[fb][w][c + 32 * hh], n = st.ln[fb][w][c + 32 * hh];
-        for (uint32_t j = 0; j < n; ++j) {
-            const uint32_t i = off + j;
-            if (i >= (uint32_t)MQ1_STAGE) break;  // not staged (the query is marked)
-            if (len < a.capw) {
-                a.cand[bucket + len] = st.lk[fb][w][i];
-                a.up_out[bucket + len] = st.uo[fb][w][i];
-            } else {
-                ovf = true;
-            }
-            ++len;
+    // the entries of lanes c and c + 32, in that order, in one loop
+    const uint32_t off0 = st.lo[fb][w][c], n0 = st.ln[fb][w][c];
+    const uint32_t off1 = st.lo[fb][w][c + 32], n1 = st.ln[fb][w][c + 32];
+    for (uint32_t j = 0; j < n0 + n1; ++j) {
+        const uint32_t i = j < n0 ? off0 + j : off1 + (j - n0);
+        if (i >= (uint32_t)MQ1_STAGE) continue;  // not staged (the query is marked)
+        if (len < a.capw) {
+            a.cand[bucket + len] = st.lk[fb][w][i];
+            a.up_out[bucket + len] = st.uo[fb][w][i];
+        } else {
+            ovf = true;
         }
+        ++len;
     }
 }
 
