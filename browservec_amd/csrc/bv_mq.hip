@@ -874,7 +874,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan(Mq1Args a) {
 // rows' scales come with the bits (none: 1), and their code norms are the
 // constant a.cn_const (every +1 / -1 row has the same norm).  The keys,
 // bounds, staging and buckets are mq1_scan's.
-template <int S>
+template <int S, bool THR>
 __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan_bits(Mq1Args a) {
     constexpr uint32_t U = 2 * S;     // 16-byte units per widened row (8 <= U <= 64)
     constexpr uint32_t RS = U + 1;    // LDS row stride of the byte tiles in units
@@ -884,7 +884,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan_bits(Mq1Args a) {
     static_assert(S >= 4 && LN <= 64, "1-bit rows of 128 to 1024 codes");
     __shared__ v4i tb[2][MQ1_ROWS * RS];
     __shared__ v4i bb[4][MQ1_ROWS * UB];
-    __shared__ __align__(16) float scr[4][MQ1_ROWS];
+    __shared__ __align__(16) float scr[8][MQ1_ROWS];  // (8 deep: the threshold pass reads a tile's scales one tile late)
     __shared__ __align__(16) float ones[MQ1_ROWS];
     __shared__ __align__(16) float cnc[MQ1_ROWS];
     __shared__ uint2 lut[256];
@@ -895,7 +895,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan_bits(Mq1Args a) {
     const uint32_t qb = blockIdx.x % a.qblocks;
     const uint32_t wg = blockIdx.x / a.qblocks;
     const bool loader = wave < MQ1_LOADERS;
-    const bool thr = a.tau != nullptr;
+    constexpr bool thr = THR;  // (the launch picks THR from a.tau)
     const bool scaled = a.scales != nullptr;
     for (uint32_t i = threadIdx.x; i < 2 * MQ_WAVES * 64; i += MQ_WAVES * 64)
         stage.ln[i / (MQ_WAVES * 64)][(i / 64) % MQ_WAVES][i % 64] = 0;
@@ -949,7 +949,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan_bits(Mq1Args a) {
         if (scaled && wv == 0 && lane < MQ1_ROWS) {
             uint64_t li = t * MQ1_ROWS + (uint32_t)lane;
             if (li >= a.n) li = a.n - 1;
-            lds_dma4(a.scales + li * a.row_step, lds_addr(&scr[k & 3][0]));
+            lds_dma4(a.scales + li * a.row_step, lds_addr(&scr[k & 7][0]));
         }
     };
     // tile k's bits into byte tile k & 1: unit u of row r (codes 16u ..
@@ -993,6 +993,87 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan_bits(Mq1Args a) {
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         widen(0);
     }
+    if constexpr (THR) {
+        // The threshold pass as in mq1_scan: tile k - 1's bounds are tested
+        // between tile k's MFMAs (its dots in pacc, its scales still in
+        // their ring slot: eight deep, four tiles ahead of the loads), its
+        // reaching rows staged after them and moved to the buckets at tile
+        // k + 1; the loader waves multiply first and issue their loads
+        // after the K loop, while the flushing waves multiply.
+        v16i pacc = v16i{};
+        for (uint64_t k = 0; k < mine; ++k) {
+            if (k + 1 < mine) wait_tile(mine - 2 - k < 1 ? mine - 2 - k : 1);
+            else wait_tile(0);
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (!loader) mq1_flush(a, qb, wg, stage, (int)(k & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+            if (k + 1 < mine) widen(k + 1);
+            const float *psc = scaled ? &scr[(k - 1) & 7][0] : ones;  // tile k - 1's (unused at k = 0)
+            if (!wave_live) {
+                if (loader && k + 3 < mine) load_bits(k + 3);
+                continue;
+            }
+            const v4i *tl = &tb[k & 1][0];
+            v16i acc = v16i{};
+            const v4i *A0 = tl + c * RS + h;
+            constexpr int PF = S < 4 ? S : 4;
+            v4i ar[PF];
+#pragma unroll
+            for (int st = 0; st < PF; ++st) ar[st] = A0[2 * st];
+            const float *psh = psc + 4 * h, *pnh = cnc + 4 * h;
+            float sv = psh[0], nv = pnh[0];
+            uint32_t p = 0;
+#pragma unroll
+            for (int st = 0; st < S; ++st) {
+                const v4i x = ar[st % PF];
+                if (st + PF < S) ar[st % PF] = A0[2 * (st + PF)];
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(x, qreg[st], acc, 0, 0, 0);
+                constexpr int EPS = S >= 16 ? 1 : 16 / S, SPE = S >= 16 ? S / 16 : 1;
+#pragma unroll
+                for (int e = 0; e < (st % SPE == SPE - 1 ? EPS : 0); ++e) {
+                    const int r = st / SPE * EPS + e;
+                    float svn = 0.0f, nvn = 0.0f;
+                    if (r < 15) {
+                        const int rn = 8 * ((r + 1) >> 2) + ((r + 1) & 3);
+                        svn = psh[rn];
+                        nvn = pnh[rn];
+                    }
+                    p |= mq1_reach(pacc[r], s0f, nv * rq, sv, tau_score) << r;
+                    asm volatile("" : "+v"(p));  // (between the MFMAs: not sunk to the staging below)
+                    sv = svn;
+                    nv = nvn;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (loader && k + 3 < mine) load_bits(k + 3);
+            if (k > 0)
+                mq1_stage(a, p, pacc, (wg + (k - 1) * a.nwg) * MQ1_ROWS, q, qlocal, h, s0f, rq, psc, cnc, stage,
+                          (int)((k - 1) & 1));
+            pacc = acc;
+        }
+        // the last tile's bounds, the staged entries of the last two tiles,
+        // then this workgroup's bucket lengths
+        __syncthreads();
+        if (!loader && mine >= 2)
+            mq1_flush(a, qb, wg, stage, (int)((mine - 2) & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+        if (wave_live && mine > 0) {
+            const float *lsc = scaled ? &scr[(mine - 1) & 7][0] : ones;
+            uint32_t p = 0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const uint32_t rr = 8 * (r >> 2) + 4 * (uint32_t)h + (r & 3);
+                p |= mq1_reach(pacc[r], s0f, cnc[rr] * rq, lsc[rr], tau_score) << r;
+            }
+            mq1_stage(a, p, pacc, (wg + (mine - 1) * a.nwg) * MQ1_ROWS, q, qlocal, h, s0f, rq, lsc, cnc, stage,
+                      (int)((mine - 1) & 1));
+        }
+        __syncthreads();
+        if (!loader) {
+            if (mine) mq1_flush(a, qb, wg, stage, (int)((mine - 1) & 1), wave - MQ1_LOADERS, lane, blen, bovf);
+            const uint32_t ql = (uint32_t)(wave - MQ1_LOADERS) * 64 + lane, qq = qb * MQ1_QB + ql;
+            if (qq < a.nq) a.cnt[(uint64_t)qq * a.nwg + wg] = bovf || stage.qovf[ql] ? 0xffffffffu : blen;
+        }
+        return;
+    }
     for (uint64_t k = 0; k < mine; ++k) {
         // tile k + 1's bits have landed (every loader wave waited for its
         // own), tile k is widened, and every wave is done with tile k - 1
@@ -1007,7 +1088,7 @@ __global__ __launch_bounds__(MQ_WAVES * 64) void mq1_scan_bits(Mq1Args a) {
         if (k + 1 < mine) widen(k + 1);
         if (wave_live) {
             const v4i *tl = &tb[k & 1][0];
-            const float *sc = scaled ? &scr[k & 3][0] : ones;
+            const float *sc = scaled ? &scr[k & 7][0] : ones;
             v16i acc2[2] = {v16i{}, v16i{}};
             const v4i *A0 = tl + c * RS + h;
             constexpr int PF = S < 4 ? S : 4;
@@ -2160,10 +2241,22 @@ hipError_t launch_mq1_scan_bits(const Mq1Args &a, hipStream_t s) {
     if (blocks > 0x7fffffffull) return hipErrorInvalidValue;
     const dim3 g((uint32_t)blocks), wg(MQ_WAVES * 64);
     switch (steps) {
-    case 4: hipLaunchKernelGGL((mq1_scan_bits<4>), g, wg, 0, s, a); break;
-    case 8: hipLaunchKernelGGL((mq1_scan_bits<8>), g, wg, 0, s, a); break;
-    case 16: hipLaunchKernelGGL((mq1_scan_bits<16>), g, wg, 0, s, a); break;
-    case 32: hipLaunchKernelGGL((mq1_scan_bits<32>), g, wg, 0, s, a); break;
+    case 4:
+        if (a.tau) hipLaunchKernelGGL((mq1_scan_bits<4, true>), g, wg, 0, s, a);
+        else hipLaunchKernelGGL((mq1_scan_bits<4, false>), g, wg, 0, s, a);
+        break;
+    case 8:
+        if (a.tau) hipLaunchKernelGGL((mq1_scan_bits<8, true>), g, wg, 0, s, a);
+        else hipLaunchKernelGGL((mq1_scan_bits<8, false>), g, wg, 0, s, a);
+        break;
+    case 16:
+        if (a.tau) hipLaunchKernelGGL((mq1_scan_bits<16, true>), g, wg, 0, s, a);
+        else hipLaunchKernelGGL((mq1_scan_bits<16, false>), g, wg, 0, s, a);
+        break;
+    case 32:
+        if (a.tau) hipLaunchKernelGGL((mq1_scan_bits<32, true>), g, wg, 0, s, a);
+        else hipLaunchKernelGGL((mq1_scan_bits<32, false>), g, wg, 0, s, a);
+        break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
