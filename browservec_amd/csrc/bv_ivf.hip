@@ -447,7 +447,7 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
     __shared__ uint32_t cnt_s[4];
     __shared__ uint64_t tot_s[4];
     __shared__ uint32_t nsel;
-    __shared__ uint64_t s_bound;
+    __shared__ uint64_t s_bound, smp_b1;
     const uint32_t qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *sc = a.scores + (uint64_t)qi * a.nlist;
 #pragma unroll 8
@@ -461,6 +461,10 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
     uint64_t lo = 0, hi = ~0ull;  // count(>= lo) >= np > count(>= hi) (hi unreachable)
     bool bisect = np < a.nlist;
     if (bisect && a.nlist >= 512 && np <= 64) {
+        // Bounds from a strided sample of 256 keys: the sample of rank
+        // np - 1 has at least np keys at or above it (about stride * np);
+        // the one of rank k1 about 4 np, which keeps the all-pairs ranking
+        // below small, and fewer than np only rarely (then the first).
         const uint32_t stride = a.nlist / 256;
         smp[tid] = pk[tid * stride];
         __syncthreads();
@@ -468,21 +472,29 @@ __global__ __launch_bounds__(256) void ivf_probe_select(IvfProbeArgs a) {
         uint32_t r = 0;
 #pragma unroll 16
         for (uint32_t j = 0; j < 256; ++j) r += smp[j] > mine ? 1u : 0u;
+        uint32_t k1 = (4 * np + stride - 1) / stride;
+        k1 = k1 > 0 ? k1 - 1 : 0;
+        if (k1 > np - 1) k1 = np - 1;
         if (r == np - 1) s_bound = mine;
+        if (r == k1) smp_b1 = mine;
         __syncthreads();
-        const uint64_t bound = s_bound;
-        uint32_t c = 0;
+        for (int pass = 0; pass < 2; ++pass) {
+            const uint64_t bound = pass == 0 ? smp_b1 : s_bound;
+            uint32_t c = 0;
 #pragma unroll 8
-        for (uint32_t j = tid; j < a.nlist; j += 256) c += pk[j] >= bound ? 1u : 0u;
+            for (uint32_t j = tid; j < a.nlist; j += 256) c += pk[j] >= bound ? 1u : 0u;
 #pragma unroll
-        for (int s = 1; s < 64; s <<= 1) c += __shfl_xor(c, s);
-        if (lane == 0) cnt_s[wave] = c;
-        __syncthreads();
-        const uint32_t tot = cnt_s[0] + cnt_s[1] + cnt_s[2] + cnt_s[3];
-        __syncthreads();
-        if (tot <= PROBE_RANK_CAP) {
-            lo = bound;  // rank the tot >= np keys at or above the bound below
-            bisect = false;
+            for (int s = 1; s < 64; s <<= 1) c += __shfl_xor(c, s);
+            if (lane == 0) cnt_s[wave] = c;
+            __syncthreads();
+            const uint32_t tot = cnt_s[0] + cnt_s[1] + cnt_s[2] + cnt_s[3];
+            __syncthreads();
+            if (tot >= np && tot <= PROBE_RANK_CAP) {
+                lo = bound;  // rank the tot >= np keys at or above the bound below
+                bisect = false;
+                break;
+            }
+            if (k1 == np - 1) break;  // (the same bound twice)
         }
     }
     if (bisect) {
