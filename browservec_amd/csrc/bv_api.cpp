@@ -1458,6 +1458,7 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
     hipStream_t s = idx->stream;
     if (may_alternate && idx->query_streams == 2 && !idx->ivf &&
         (!idx->quant || scan_prep_supported(idx->codec, idx->units, idx->P))) {
+        a.lean = 1;  // (both queries' scans: their workgroups share CUs)
         if (idx->next_lane == 1) {
             lane = &idx->lane2;
             s = lane->stream;

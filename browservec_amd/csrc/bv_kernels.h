@@ -114,6 +114,7 @@ struct ScanArgs {
                               // a fresh read of it, and the final gather is bounded by the wave maxima
     uint32_t static_pct;      // share (%) of the row grabs assigned statically (0: the kernel's default)
     uint32_t dsteps;          // wave steps per dynamic ticket (0: the kernel's default)
+    uint32_t lean;            // 1: the register-lean build of the int8 transform scan (two queries in flight)
 };
 
 // Exact keys of listed rows of a 1-bit asymmetric (C_Q1P) index, one grid

@@ -81,7 +81,7 @@ def test_failed_append_leaves_the_index_unchanged():
     ctx.destroy()
 
 
-@pytest.mark.parametrize("kind", ["quant8", "flat"])
+@pytest.mark.parametrize("kind", ["quant8", "quant8_768", "flat"])
 def test_two_query_streams_equal_one(kind):
     """bv_index_set_query_streams(2): consecutive search_device calls
     alternate between two streams and overlap; every call's rows and score
@@ -91,14 +91,16 @@ def test_two_query_streams_equal_one(kind):
     import torch
     from browservec_amd import DeviceContext, FlatIndex, QuantIndex
 
-    dim, n, nq = 256, 60000, 24
+    # (two streams run the register-lean build of the int8 scan: 768
+    # dimensions is the 1024-code layout of the 1M x 768 workload)
+    dim, n, nq = (768 if kind == "quant8_768" else 256), 60000, 24
     say("two query streams", kind)
     ctx = DeviceContext(0)
     data = gaussian(n, dim, 91)
-    idx = QuantIndex(ctx, dim, bits=8) if kind == "quant8" else FlatIndex(ctx, dim, "cosine")
+    idx = QuantIndex(ctx, dim, bits=8) if kind.startswith("quant8") else FlatIndex(ctx, dim, "cosine")
     idx.append(data[:n], n)
     q = torch.from_numpy(gaussian(nq, dim, 92)).cuda()
-    fetch = 40 if kind == "quant8" else 0
+    fetch = 40 if kind.startswith("quant8") else 0
 
     def run(streams):
         idx.set_query_streams(streams)
