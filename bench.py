@@ -743,7 +743,8 @@ def main():
                                f"re-rank -> top-{args.k}, batch 1",
                    "batch1_mode": "one query per search_device call; two calls in flight on two streams "
                                   "(bv_index_set_query_streams(2)), so one query's final selection overlaps the "
-                                  "next query's scan",
+                                  "next query's scan; two-stream calls run the register-lean build of the scan "
+                                  "(scan_topk_lean), the roofline's kernel is the default build on one stream",
                    "rows": args.rows, "dim": args.dim, "padded_dim": P, "bits": args.bits, "fetch": args.fetch,
                    "k": args.k, "queries": args.queries, "rotation_seed": "0x9e3779b9", "data_seed": hex(seed)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
