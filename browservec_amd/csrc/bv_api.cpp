@@ -215,6 +215,7 @@ struct bv_index {
     struct ScanLane {
         hipStream_t stream = nullptr;
         DevBuf qstate, wmax, cand_keys, merged, merged_n;
+        DevBuf ivf_qrot, probe_scores, probes, cand, cand_tot, cand_off;  // an IVF query's probes and candidates
         uint64_t mut_seen = 0;                // the ev_mut record this stream last waited on
     } lane2;
     uint32_t query_streams = 1, next_lane = 0;
@@ -1124,7 +1125,12 @@ static int ivf_build(bv_index *idx) {
 // scratch or output pointer: the build grows and reuses buffers.
 static int ensure_built(bv_index *idx) {
     if (!idx->ivf || idx->rows == 0 || idx->built_rows == idx->rows) return BV_OK;
-    return ivf_build(idx);
+    // (the build rewrites the lists that queries on the second stream read)
+    int rc = lanes_join(idx);
+    if (rc) return rc;
+    rc = ivf_build(idx);
+    if (rc) return rc;
+    return lanes_mark(idx);
 }
 
 // nprobe for the next query (ivfquant.ts:159-162, 487-491): the per-query
@@ -1142,14 +1148,19 @@ static uint32_t ivf_resolve_nprobe(bv_index *idx) {
 
 // Probes + gathered candidate lists for nq device queries (original space).
 // Returns the per-query candidate bound used to size the scan.
-static int ivf_candidates(bv_index *idx, const float *d_q, uint32_t nq, uint64_t *max_per_query) {
+// (on the second query stream, `lane`: its own buffers and stream)
+static int ivf_candidates(bv_index *idx, const float *d_q, uint32_t nq, uint64_t *max_per_query,
+                          bv_index::ScanLane *lane = nullptr) {
     // every query entry point builds before it takes any buffer pointer
     if (idx->built_rows != idx->rows) return fail(BV_E_STATE, "IVF lists are stale");
-    hipStream_t s = idx->stream;
+    hipStream_t s = lane ? lane->stream : idx->stream;
+    DevBuf &b_qrot = lane ? lane->ivf_qrot : idx->ivf_qrot, &b_scores = lane ? lane->probe_scores : idx->probe_scores;
+    DevBuf &b_probes = lane ? lane->probes : idx->probes, &b_cand = lane ? lane->cand : idx->cand;
+    DevBuf &b_tot = lane ? lane->cand_tot : idx->cand_tot, &b_off = lane ? lane->cand_off : idx->cand_off;
     const uint32_t nprobe = ivf_resolve_nprobe(idx);
     const float *qrot = d_q;
     if (idx->quant) {  // pickProbes scores the rotated query
-        HIPX(idx->dev, idx->ivf_qrot.ensure((size_t)nq * idx->P * 4, 0, s), "query buffer");
+        HIPX(idx->dev, b_qrot.ensure((size_t)nq * idx->P * 4, 0, s), "query buffer");
         EncodeArgs e{};
         e.src = d_q;
         e.rows = nq;
@@ -1158,32 +1169,32 @@ static int ivf_candidates(bv_index *idx, const float *d_q, uint32_t nq, uint64_t
         e.signs = idx->signs.as<float>();
         e.rounds = idx->d.rounds;
         e.bits = 0;
-        e.rotated = idx->ivf_qrot.as<float>();
+        e.rotated = b_qrot.as<float>();
         HIPX(idx->dev, launch_encode(e, s), "query rotate kernel");
-        qrot = idx->ivf_qrot.as<float>();
+        qrot = b_qrot.as<float>();
     }
-    HIPX(idx->dev, idx->probe_scores.ensure((size_t)nq * idx->nlist * 4, 0, s), "scratch");
-    HIPX(idx->dev, idx->probes.ensure((size_t)nq * nprobe * 4, 0, s), "scratch");
+    HIPX(idx->dev, b_scores.ensure((size_t)nq * idx->nlist * 4, 0, s), "scratch");
+    HIPX(idx->dev, b_probes.ensure((size_t)nq * nprobe * 4, 0, s), "scratch");
     IvfProbeArgs pa{};
     pa.centroids = idx->centroids.as<float>();
     pa.nlist = idx->nlist;
     pa.P = idx->sample_dim;
     pa.qrot = qrot;
-    pa.scores = idx->probe_scores.as<float>();
+    pa.scores = b_scores.as<float>();
     pa.nprobe = nprobe;
-    pa.probes = idx->probes.as<uint32_t>();
+    pa.probes = b_probes.as<uint32_t>();
     uint64_t per = 0;
     for (uint32_t i = 0; i < nprobe && i < idx->list_sizes_desc.size(); ++i) per += idx->list_sizes_desc[i];
-    HIPX(idx->dev, idx->cand.ensure(std::max<uint64_t>(per * nq, 1) * 4, 0, s), "scratch");
-    HIPX(idx->dev, idx->cand_tot.ensure((size_t)nq * 8, 0, s), "scratch");
-    HIPX(idx->dev, idx->cand_off.ensure(((size_t)nq + 1) * 8, 0, s), "scratch");
+    HIPX(idx->dev, b_cand.ensure(std::max<uint64_t>(per * nq, 1) * 4, 0, s), "scratch");
+    HIPX(idx->dev, b_tot.ensure((size_t)nq * 8, 0, s), "scratch");
+    HIPX(idx->dev, b_off.ensure(((size_t)nq + 1) * 8, 0, s), "scratch");
     pa.offset = idx->list_off.as<uint32_t>();
-    pa.totals = idx->cand_tot.as<uint64_t>();
-    pa.cand_off = idx->cand_off.as<uint64_t>();
+    pa.totals = b_tot.as<uint64_t>();
+    pa.cand_off = b_off.as<uint64_t>();
     HIPX(idx->dev, ivf_launch_probes(pa, nq, s), "probe kernels");
-    HIPX(idx->dev, ivf_launch_gather(idx->probes.as<uint32_t>(), nq, nprobe, idx->list_off.as<uint32_t>(),
-                                     idx->list_rows.as<uint32_t>(), idx->cand_tot.as<uint64_t>(),
-                                     idx->cand_off.as<uint64_t>(), idx->cand.as<uint32_t>(), s),
+    HIPX(idx->dev, ivf_launch_gather(b_probes.as<uint32_t>(), nq, nprobe, idx->list_off.as<uint32_t>(),
+                                     idx->list_rows.as<uint32_t>(), b_tot.as<uint64_t>(),
+                                     b_off.as<uint64_t>(), b_cand.as<uint32_t>(), s),
          "gather kernels");
     *max_per_query = per;
     return BV_OK;
@@ -1456,7 +1467,7 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
     // own scan scratch; flat indexes whose scan needs no shared query buffer)
     bv_index::ScanLane *lane = nullptr;
     hipStream_t s = idx->stream;
-    if (may_alternate && idx->query_streams == 2 && !idx->ivf &&
+    if (may_alternate && idx->query_streams == 2 &&
         (!idx->quant || scan_prep_supported(idx->codec, idx->units, idx->P))) {
         a.lean = 1;  // (both queries' scans: their workgroups share CUs)
         if (idx->next_lane == 1) {
@@ -1486,10 +1497,10 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
     }
     uint64_t n = idx->rows;
     if (idx->ivf) {  // scan only the probed lists: indexed mode with per-query candidate ranges
-        rc = ivf_candidates(idx, d_q, nq, &n);
+        rc = ivf_candidates(idx, d_q, nq, &n, lane);
         if (rc) return rc;
-        a.cand = idx->cand.as<uint32_t>();
-        a.cand_off = idx->cand_off.as<uint64_t>();
+        a.cand = (lane ? lane->cand : idx->cand).as<uint32_t>();
+        a.cand_off = (lane ? lane->cand_off : idx->cand_off).as<uint64_t>();
     }
     const uint32_t grid = grid_for(idx, std::max<uint64_t>(n, 1), kprime, rerank ? idx->dim : 0);
     rc = scan_scratch(idx, nq, grid, kprime, rerank ? idx->dim : 0, a, lane);

@@ -81,7 +81,7 @@ def test_failed_append_leaves_the_index_unchanged():
     ctx.destroy()
 
 
-@pytest.mark.parametrize("kind", ["quant8", "quant8_768", "flat"])
+@pytest.mark.parametrize("kind", ["quant8", "quant8_768", "flat", "ivf8"])
 def test_two_query_streams_equal_one(kind):
     """bv_index_set_query_streams(2): consecutive search_device calls
     alternate between two streams and overlap; every call's rows and score
@@ -89,7 +89,7 @@ def test_two_query_streams_equal_one(kind):
     the queries in flight and the next queries see the new rows."""
     need_gpu()
     import torch
-    from browservec_amd import DeviceContext, FlatIndex, QuantIndex
+    from browservec_amd import DeviceContext, FlatIndex, IVFQuantIndex, QuantIndex
 
     # (two streams run the register-lean build of the int8 scan: 768
     # dimensions is the 1024-code layout of the 1M x 768 workload)
@@ -97,10 +97,13 @@ def test_two_query_streams_equal_one(kind):
     say("two query streams", kind)
     ctx = DeviceContext(0)
     data = gaussian(n, dim, 91)
-    idx = QuantIndex(ctx, dim, bits=8) if kind.startswith("quant8") else FlatIndex(ctx, dim, "cosine")
+    if kind == "ivf8":  # (each stream has its own probe and candidate buffers)
+        idx = IVFQuantIndex(ctx, dim, bits=8, ivf={"nlist": 64, "nprobe": 8})
+    else:
+        idx = QuantIndex(ctx, dim, bits=8) if kind.startswith("quant8") else FlatIndex(ctx, dim, "cosine")
     idx.append(data[:n], n)
     q = torch.from_numpy(gaussian(nq, dim, 92)).cuda()
-    fetch = 40 if kind.startswith("quant8") else 0
+    fetch = 40 if kind != "flat" else 0
 
     def run(streams):
         idx.set_query_streams(streams)
