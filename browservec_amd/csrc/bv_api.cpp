@@ -135,6 +135,10 @@ struct HostBuf {
 };
 
 // ------------------------------------------------------------------ index
+// query streams a caller may keep single queries in flight on
+// (bv_index_set_query_streams)
+constexpr int MAX_QUERY_STREAMS = 4;
+
 struct bv_index {
     // Calls on one index are serialized (the Node binding runs them on worker
     // threads); the reference awaits them one at a time per store.
@@ -209,17 +213,17 @@ struct bv_index {
     double last_query_ms = 0, last_query_gpu_ms = 0;
     uint64_t last_scanned = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    // a second query stream (bv_index_set_query_streams): consecutive fused
-    // queries alternate between the index stream and this one, each with its
-    // own scan scratch, so one query's tail overlaps the next one's scan
+    // further query streams (bv_index_set_query_streams): consecutive fused
+    // queries take the index stream and these in turn, each with its own
+    // scan scratch, so one query's tail overlaps the next one's scan
     struct ScanLane {
         hipStream_t stream = nullptr;
         DevBuf qstate, wmax, cand_keys, merged, merged_n;
         DevBuf ivf_qrot, probe_scores, probes, cand, cand_tot, cand_off;  // an IVF query's probes and candidates
         uint64_t mut_seen = 0;                // the ev_mut record this stream last waited on
-    } lane2;
+    } lanes[MAX_QUERY_STREAMS - 1];
     uint32_t query_streams = 1, next_lane = 0;
-    bool lane2_pending = false;               // lane2 has queries the index stream has not joined
+    uint32_t lanes_pending = 0;               // bit i: lanes[i] has queries the index stream has not joined
     hipEvent_t ev_mut = nullptr;              // recorded after work that changes the index's buffers
     uint64_t mut_gen = 0;                     // counts the ev_mut records
 
@@ -433,8 +437,10 @@ extern "C" int bv_index_destroy(bv_index *idx) {
     }
     if (idx->ev0) (void)hipEventDestroy(idx->ev0);
     if (idx->ev1) (void)hipEventDestroy(idx->ev1);
-    if (idx->lane2.stream) (void)hipStreamSynchronize(idx->lane2.stream);
-    if (idx->lane2.stream) (void)hipStreamDestroy(idx->lane2.stream);
+    for (auto &l : idx->lanes) {
+        if (l.stream) (void)hipStreamSynchronize(l.stream);
+        if (l.stream) (void)hipStreamDestroy(l.stream);
+    }
     if (idx->ev_mut) (void)hipEventDestroy(idx->ev_mut);
     if (idx->copy_stream) (void)hipStreamSynchronize(idx->copy_stream);
     for (hipEvent_t e : idx->up_ev)
@@ -1305,13 +1311,13 @@ static int scan_scratch(bv_index *idx, uint32_t nq, uint32_t grid, uint32_t kpri
 // stream's queries (host wait: a buffer may be freed right after), and is
 // followed by ev_mut, which the second stream waits on before its next query.
 static int lanes_join(bv_index *idx) {
-    if (!idx->lane2_pending) return BV_OK;
-    HIPX(idx->dev, hipStreamSynchronize(idx->lane2.stream), "query stream");
-    idx->lane2_pending = false;
+    for (uint32_t i = 0; i < MAX_QUERY_STREAMS - 1; ++i)
+        if (idx->lanes_pending & (1u << i)) HIPX(idx->dev, hipStreamSynchronize(idx->lanes[i].stream), "query stream");
+    idx->lanes_pending = 0;
     return BV_OK;
 }
 static int lanes_mark(bv_index *idx) {
-    if (!idx->lane2.stream) return BV_OK;
+    if (!idx->lanes[0].stream) return BV_OK;
     HIPX(idx->dev, hipEventRecord(idx->ev_mut, idx->stream), "event");
     idx->mut_gen++;
     return BV_OK;
@@ -1414,7 +1420,8 @@ static void timing_end(bv_index *idx, hipStream_t s = nullptr) {
 static void timing_collect(bv_index *idx) {
     if (idx->tev_used == 0) return;
     (void)hipStreamSynchronize(idx->stream);
-    if (idx->lane2.stream) (void)hipStreamSynchronize(idx->lane2.stream);
+    for (auto &l : idx->lanes)
+        if (l.stream) (void)hipStreamSynchronize(l.stream);
     for (size_t i = 0; i < idx->tev_used; i++) {
         float ms = 0;
         if (hipEventElapsedTime(&ms, idx->tev[i].first, idx->tev[i].second) == hipSuccess) idx->scan_ms += ms;
@@ -1467,11 +1474,13 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
     // own scan scratch; flat indexes whose scan needs no shared query buffer)
     bv_index::ScanLane *lane = nullptr;
     hipStream_t s = idx->stream;
-    if (may_alternate && idx->query_streams == 2 &&
+    if (may_alternate && idx->query_streams >= 2 &&
         (!idx->quant || scan_prep_supported(idx->codec, idx->units, idx->P))) {
         a.lean = 1;  // (both queries' scans: their workgroups share CUs)
-        if (idx->next_lane == 1) {
-            lane = &idx->lane2;
+        const uint32_t li = idx->next_lane;
+        idx->next_lane = (li + 1) % idx->query_streams;
+        if (li > 0) {
+            lane = &idx->lanes[li - 1];
             s = lane->stream;
             // (the stream is in order: one wait covers every later query on it)
             if (lane->mut_seen != idx->mut_gen) {
@@ -1479,7 +1488,6 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
                 lane->mut_seen = idx->mut_gen;
             }
         }
-        idx->next_lane ^= 1u;
     }
     if (idx->quant && scan_prep_supported(idx->codec, idx->units, idx->P)) {
         // the scan kernel rotates and transforms the fp32 queries itself
@@ -1509,7 +1517,7 @@ static int run_fused(bv_index *idx, const float *d_q, uint32_t nq, uint32_t kpri
     timing_begin(idx, s);
     HIPX(idx->dev, launch_scan(idx->codec, idx->units, a, nq, s), "scan kernel");
     timing_end(idx, s);
-    if (lane) idx->lane2_pending = true;
+    if (lane) idx->lanes_pending |= 1u << (uint32_t)(lane - idx->lanes);
     idx->last_scanned = n * nq;
     return BV_OK;
 }
@@ -2557,13 +2565,18 @@ extern "C" int bv_index_set_query_streams(bv_index *idx, uint32_t n) {
     std::lock_guard<std::recursive_mutex> lock(idx->mu);
     int rc = check_live(idx);
     if (rc) return rc;
-    if (n != 1 && n != 2) return fail(BV_E_INVALID, "query streams must be 1 or 2, got %u", n);
-    if (n == 2 && !idx->lane2.stream) {
-        HIPX(idx->dev, hipStreamCreateWithFlags(&idx->lane2.stream, hipStreamNonBlocking), "query stream");
+    if (n < 1 || n > (uint32_t)MAX_QUERY_STREAMS)
+        return fail(BV_E_INVALID, "query streams must be 1 to %d, got %u", MAX_QUERY_STREAMS, n);
+    if (n >= 2 && !idx->ev_mut) {
         HIPX(idx->dev, hipEventCreateWithFlags(&idx->ev_mut, hipEventDisableTiming), "event");
         HIPX(idx->dev, hipEventRecord(idx->ev_mut, idx->stream), "event");
         idx->mut_gen++;
     }
+    for (uint32_t i = 0; i + 1 < n; ++i)
+        if (!idx->lanes[i].stream) {
+            HIPX(idx->dev, hipStreamCreateWithFlags(&idx->lanes[i].stream, hipStreamNonBlocking), "query stream");
+            idx->lanes[i].mut_seen = 0;  // (waits on ev_mut before its first query)
+        }
     rc = lanes_join(idx);
     if (rc) return rc;
     idx->query_streams = n;

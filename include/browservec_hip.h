@@ -220,12 +220,13 @@ int bv_index_search_device(bv_index *idx, const float *d_queries, uint32_t nq, u
 
 /* Query streams for bv_index_search_device (no counterpart in the
  * reference; for callers that keep several single queries in flight):
- * n = 2 lets consecutive fused calls (fewer than 8 queries per call, no
- * mask) alternate between the index's stream and a second stream, each with
- * its own scan scratch (IVF indexes: also its own probe and candidate
- * buffers), so one query's final selection overlaps the next query's scan.  Two calls in flight may then run at once: each
- * needs its own output buffers.  bv_index_sync waits for both streams;
- * appends wait for queries still running.  n = 1 (default): one stream. */
+ * n = 2 to 4 lets consecutive fused calls (fewer than 8 queries per call,
+ * no mask) take the index's stream and n - 1 further streams in turn, each
+ * with its own scan scratch (IVF indexes: also its own probe and candidate
+ * buffers), so one query's final selection overlaps the next query's scan.
+ * Calls in flight may then run at once: each needs its own output buffers.
+ * bv_index_sync waits for every stream; appends wait for queries still
+ * running.  n = 1 (default): one stream. */
 int bv_index_set_query_streams(bv_index *idx, uint32_t n);
 /* bv_index_search_device for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
