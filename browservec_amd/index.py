@@ -288,8 +288,9 @@ class NativeIndex:
         L.check(self.lib.bv_index_sync(self.handle))
 
     def set_query_streams(self, n: int) -> None:
-        """1 or 2 streams for search_device's single queries (2: consecutive
-        calls overlap; each call in flight needs its own outputs)."""
+        """1 to 4 streams for search_device's single queries (2 or more:
+        consecutive calls take the streams in turn and overlap; each call in
+        flight needs its own outputs)."""
         L.check(self.lib.bv_index_set_query_streams(self.handle, int(n)))
 
     def stream_ptr(self) -> int:
