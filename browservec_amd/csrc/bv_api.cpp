@@ -1228,6 +1228,11 @@ static uint32_t grid_for(const bv_index *idx, uint64_t n, uint32_t kprime, uint3
     const size_t lds = scan_lds_bytes(idx->codec, idx->P, wstride);
     const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(2, lds_cu / std::max<size_t>(lds, 1)));
     uint64_t cap = per_cu * (uint64_t)cus - 1;
+    // several query streams on a flat int8 index run the register-lean scan
+    // (three workgroups per CU): each query's grid is sized so that every
+    // stream's grid and threshold helper are resident at once
+    if (idx->query_streams >= 2 && idx->codec == C_Q8 && !idx->ivf && lds * 3 <= lds_cu)
+        cap = std::min<uint64_t>(cap, 3ull * (uint64_t)cus / idx->query_streams - 1);
     if (cap > (uint64_t)SCAN_GRID) cap = SCAN_GRID;
     if (g > cap) g = cap;
     if (g < 1) g = 1;
